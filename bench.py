@@ -1,0 +1,400 @@
+"""Benchmark of the MI355X quantized linear layer (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--quick]
+
+Prints ONE JSON line. The headline (``value``) is the benchmark metric's
+GEMV half on configuration 1, the Q4_0 transformer MLP pair at batch 1: one
+step is x -> gate and up GEMVs (Q4, 6144 x 2048, activation quantizer fused)
+-> SiLU(gate) * up -> down GEMV (Q4, 2048 x 6144), all on the GPU with inputs
+resident in HBM. ``value`` = algorithmic bytes per step (weights at the GGUF
+Q4_0 size of 18 B per 32, x read and y written as fp32) x K / time. Weight
+copies rotate through >= 512 MB so the 256 MB Infinity Cache cannot serve
+them (HBM-cold). The other configurations (Q8 GEMV, LM head + argmax,
+prefill GEMM, BF16 -> Q8 + vision pair, the M = 1..64 sweep) are reported
+under ``configs``; the prefill GEMM gives the metric's TOPS half.
+
+``roofline`` is for the dominant kernel of the headline step (the Q4 GEMV):
+algorithmic bytes per launch / its mean launch time from HIP events on the
+stream it runs on. ``traffic`` comes from rocprofv3 FETCH_SIZE / WRITE_SIZE
+runs committed under profiles/ (null when absent). ``cpu_baseline`` times the
+reference's own CPU kernels (oracle/_ref, built from src/c/lab_native.c) on
+this host over a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
+I8_PEAK_TOPS = 5000.0       # MI355X dense int8 MFMA, TOPS
+METRIC = "Q4_0/Q8_0 GEMV GB/s (% HBM peak) @batch 1; prefill GEMM TOPS (% i8 MFMA peak)"
+ROTATE_BYTES = 600 << 20    # distinct weight bytes cycled per config (> 2 x MALL)
+
+
+def q4_bytes(rows, cols):
+    return rows * cols // 32 * 18
+
+
+def q8_bytes(rows, cols):
+    return rows * cols // 32 * 34
+
+
+def copies_for(nbytes):
+    return max(2, -(-ROTATE_BYTES // nbytes))
+
+
+class Timer:
+    """Events on torch's current stream, which the launchers enqueue on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time(self, fn, steps, warmup):
+        torch = self.torch
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            fn(i)
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps  # ms per step
+
+    def kernel_means(self, launches, steps):
+        """Mean duration of each launch in a step: events between launches."""
+        torch = self.torch
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)]
+              for _ in range(steps)]
+        torch.cuda.synchronize()
+        for s in range(steps):
+            ev[s][0].record()
+            for k, fn in enumerate(launches):
+                fn(s)
+                ev[s][k + 1].record()
+        torch.cuda.synchronize()
+        return [float(np.mean([ev[s][k].elapsed_time(ev[s][k + 1]) for s in range(steps)]))
+                for k in range(len(launches))]
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+# ------------------------------------------------------------------ configs
+
+def bench_c1(torch, D, synth, timer, steps, warmup):
+    (gq, gs), (uq, us), (dq, ds), x = synth.config1()
+    per_set = 2 * q4_bytes(6144, 2048) + q4_bytes(2048, 6144)
+    copies = copies_for(per_set)
+    sets = []
+    for c in range(copies):
+        sets.append(tuple(dev(torch, a) for a in (gq, gs, uq, us, dq, ds)))
+    xd = dev(torch, x)
+    g = torch.empty(6144, device="cuda")
+    u = torch.empty(6144, device="cuda")
+    y = torch.empty(2048, device="cuda")
+
+    def gate(i):
+        s = sets[i % copies]
+        D.gemv_q4(s[0], s[1], xd, g, 6144, 2048, 1)
+
+    def up(i):
+        s = sets[i % copies]
+        D.gemv_q4(s[2], s[3], xd, u, 6144, 2048, 1)
+
+    def glue(i):
+        D.swiglu(g, u)
+
+    def down(i):
+        s = sets[i % copies]
+        D.gemv_q4(s[4], s[5], g, y, 2048, 6144, 1)
+
+    def step(i):
+        gate(i)
+        up(i)
+        glue(i)
+        down(i)
+
+    ms = timer.time(step, steps, warmup)
+    algo = per_set + (2048 * 4) * 2 + 6144 * 4 + 2 * 6144 * 4 + 2048 * 4
+    means = timer.kernel_means([gate, up, glue, down], min(steps, 200))
+    gemv_ms = (means[0] + means[1] + means[3]) / 3
+    gemv_bytes = q4_bytes(6144, 2048) + 2048 * 4 + 6144 * 4  # gate/up/down move the same
+    resident = timer.time(lambda i: step(0), steps, warmup)
+    return {
+        "ms_per_step": ms, "bytes_per_step": algo, "gbps": algo / ms / 1e6,
+        "weight_copies": copies, "kernel_ms": {"gemv_q4_gate": means[0], "gemv_q4_up": means[1],
+                                               "swiglu": means[2], "gemv_q4_down": means[3]},
+        "gemv_mean_ms": gemv_ms, "gemv_bytes_per_launch": gemv_bytes,
+        "gemv_gbps": gemv_bytes / gemv_ms / 1e6,
+        "resident_gbps": algo / resident / 1e6,
+    }
+
+
+def bench_c0(torch, D, synth, timer, steps, warmup):
+    qs, sc, x = synth.config0()
+    nbytes = q8_bytes(3072, 1024)
+    copies = copies_for(nbytes)
+    ws = [(dev(torch, qs), dev(torch, sc)) for _ in range(copies)]
+    xd = dev(torch, x)
+    y = torch.empty(3072, device="cuda")
+
+    def step(i):
+        q, s = ws[i % copies]
+        D.gemv_q8(q, s, xd, y, 3072, 1024, 1)
+
+    ms = timer.time(step, steps, warmup)
+    algo = nbytes + 1024 * 4 + 3072 * 4
+    resident = timer.time(lambda i: step(0), steps, warmup)
+    return {"ms": ms, "gbps": algo / ms / 1e6, "frac_hbm": algo / ms / 1e6 / HBM_PEAK_GBS,
+            "resident_gbps": algo / resident / 1e6, "weight_copies": copies}
+
+
+def bench_c2(torch, D, synth, timer, steps, warmup):
+    qs, sc, x = synth.config2()
+    copies = 2
+    ws = [(dev(torch, qs), dev(torch, sc)) for _ in range(copies)]
+    del qs, sc
+    xd = dev(torch, x)
+    y = torch.empty(151936, device="cuda")
+    out = torch.empty(1, dtype=torch.int64, device="cuda")
+    wsp = D.argmax_workspace(151936)
+
+    def gemv(i):
+        q, s = ws[i % copies]
+        D.gemv_q8(q, s, xd, y, 151936, 2048, 1)
+
+    def amax(i):
+        D.argmax(y, out, wsp)
+
+    def step(i):
+        gemv(i)
+        amax(i)
+
+    n = max(10, steps // 4)
+    ms = timer.time(step, n, max(2, warmup // 4))
+    algo = q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4
+    means = timer.kernel_means([gemv, amax], n)
+    gemv_algo = q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4
+    return {"ms": ms, "gbps": algo / ms / 1e6, "frac_hbm": algo / ms / 1e6 / HBM_PEAK_GBS,
+            "gemv_ms": means[0], "argmax_ms": means[1],
+            "gemv_gbps": gemv_algo / means[0] / 1e6,
+            "gemv_frac_hbm": gemv_algo / means[0] / 1e6 / HBM_PEAK_GBS, "weight_copies": copies}
+
+
+def bench_c3(torch, D, synth, timer, steps, warmup):
+    qs, sc, xs = synth.config3()
+    M, N, K = 512, 6144, 2048
+    copies = 8
+    ws = [(dev(torch, qs), dev(torch, sc)) for _ in range(copies)]
+    xd = dev(torch, xs)
+    xq = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    xsc = torch.empty((M, K // 32), dtype=torch.float32, device="cuda")
+    y = torch.empty((M, N), device="cuda")
+
+    def quant(i):
+        D.quantize_q8(xd, xq, xsc, M, K, K)
+
+    def gemm(i):
+        q, s = ws[i % copies]
+        D.gemm_q4(q, s, xq, xsc, y, N, K, M)
+
+    n = max(10, steps // 4)
+    ms = timer.time(lambda i: (quant(i), gemm(i)), n, max(2, warmup // 4))
+    means = timer.kernel_means([quant, gemm], n)
+    ops = 2 * M * N * K
+    out = {"ms": ms, "tops": ops / ms / 1e9, "gemm_ms": means[1], "quantize_ms": means[0],
+           "gemm_tops": ops / means[1] / 1e9,
+           "gemm_frac_i8": ops / means[1] / 1e9 / I8_PEAK_TOPS}
+    # M = 1..64 sweep: GEMV (exact order) up to 4 tokens, GEMM beyond.
+    sweep = {}
+    for m in (1, 2, 4, 8, 16, 32, 64):
+        xm = xd[:m].contiguous()
+        ym = torch.empty((m, N), device="cuda")
+        if m <= 4:
+            fn = lambda i, xm=xm, ym=ym, m=m: D.gemv_q4(ws[i % copies][0], ws[i % copies][1],  # noqa: E731
+                                                        xm, ym, N, K, m)
+        else:
+            xqm = torch.empty((m, K), dtype=torch.int8, device="cuda")
+            xsm = torch.empty((m, K // 32), device="cuda")
+
+            def fn(i, xm=xm, ym=ym, m=m, xqm=xqm, xsm=xsm):
+                D.quantize_q8(xm, xqm, xsm, m, K, K)
+                D.gemm_q4(ws[i % copies][0], ws[i % copies][1], xqm, xsm, ym, N, K, m)
+        t = timer.time(fn, n, 3)
+        nbytes = q4_bytes(N, K) + m * K * 4 + m * N * 4
+        sweep[str(m)] = {"ms": t, "gbps": nbytes / t / 1e6, "tops": 2 * m * N * K / t / 1e9,
+                         "kernel": "gemv_q4" if m <= 4 else "quantize+gemm_q4"}
+    out["sweep_m"] = sweep
+    return out
+
+
+def bench_c4(torch, D, synth, timer, steps, warmup):
+    fc1, fc2, x = synth.config4()
+    M = 1024
+    w1 = dev(torch, fc1)
+    w2 = dev(torch, fc2)
+    q1 = torch.zeros((4320, 1152), dtype=torch.int8, device="cuda")  # 16 zero rows of padding
+    s1 = torch.zeros((4320, 36), device="cuda")
+    q2 = torch.empty((1152, 4320), dtype=torch.int8, device="cuda")
+    s2 = torch.empty((1152, 135), device="cuda")
+    xd = dev(torch, x)
+    xq = torch.empty((M, 4320), dtype=torch.int8, device="cuda")
+    xs = torch.empty((M, 135), device="cuda")
+    h = torch.empty((M, 4320), device="cuda")
+    y = torch.empty((M, 1152), device="cuda")
+
+    def quant_w(i):
+        D.quantize_q8_bf16(w1, q1, s1, 4304, 1152, 1152)
+        D.quantize_q8_bf16(w2, q2, s2, 1152, 4304, 4320)
+
+    def fc1_(i):
+        D.quantize_q8(xd, xq, xs, M, 1152, 1152)
+        D.gemm_q8(q1, s1, xq, xs, h, 4320, 1152, M)
+
+    def gelu_(i):
+        D.gelu(h)
+
+    def fc2_(i):
+        D.quantize_q8(h, xq, xs, M, 4320, 4320)
+        D.gemm_q8(q2, s2, xq, xs, y, 1152, 4320, M)
+
+    n = max(10, steps // 4)
+    quant_w(0)
+    means = timer.kernel_means([quant_w, fc1_, gelu_, fc2_], n)
+    qbytes = (4304 * 1152 * 2 + 4320 * 1152 + 4320 * 36 * 4) + (1152 * 4304 * 2 + 1152 * 4320 + 1152 * 135 * 4)
+    ops = 2 * M * 4304 * 1152
+    return {"quantize_weights_ms": means[0], "quantize_weights_gbps": qbytes / means[0] / 1e6,
+            "fc1_ms": means[1], "fc1_tops": ops / means[1] / 1e9, "gelu_ms": means[2],
+            "fc2_ms": means[3], "fc2_tops": ops / means[3] / 1e9,
+            "pair_tops": 2 * ops / (means[1] + means[2] + means[3]) / 1e9}
+
+
+# ------------------------------------------------------------------ CPU
+
+def cpu_baseline(synth, seconds):
+    """The reference's CPU kernels on this host: lab_gemm_q4 mode 1 (with its
+    single-threaded input quantization) for the config-1 MLP, the glue as
+    the CPU engine does it, weight copies rotated like the GPU run."""
+    from oracle import oracle as O
+    O.build()
+    kind = "reference" if O.reference_available() else "port"
+    lib = O.Reference() if kind == "reference" else O.get()
+    glue = O.get()
+    threads = min(16, len(os.sched_getaffinity(0)))
+    (gq, gs), (uq, us), (dq, ds), x = synth.config1()
+    per_set = 2 * q4_bytes(6144, 2048) + q4_bytes(2048, 6144)
+    copies = copies_for(per_set)
+    sets = [tuple(a.copy() for a in (gq, gs, uq, us, dq, ds)) for _ in range(copies)]
+
+    def step(i):
+        s = sets[i % copies]
+        g = lib.gemm_q4(s[0], s[1], x, 1, threads=threads, mode=1)
+        u = lib.gemm_q4(s[2], s[3], x, 1, threads=threads, mode=1)
+        h = glue.silu_mul(g, u)
+        return lib.gemm_q4(s[4], s[5], h, 1, threads=threads, mode=1)
+
+    for i in range(2):
+        step(i)
+    n, t0 = 0, time.perf_counter()
+    while n < 10 or time.perf_counter() - t0 < seconds:
+        step(n)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    algo = per_set + (2048 * 4) * 2 + 6144 * 4 + 2 * 6144 * 4 + 2048 * 4
+    return {"value": algo / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"{n} config-1 MLP steps ({dt * 1e3:.3f} ms each) over {copies} rotated "
+                      f"weight copies, lab_gemm_q4 mode 1 x3 + SiLU glue, {threads} OpenMP threads",
+            "ms_per_step": dt * 1e3}
+
+
+def traffic_from_profiles():
+    path = os.path.join(ROOT, "profiles", "traffic_gemv_q4_c1.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--quick", action="store_true", help="headline config only")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the quantized linear layer runs on one MI355X; see DESIGN.md for sharding)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from dianoia_amd import device as D
+    from dianoia_amd import synth
+    if not torch.cuda.is_available():
+        print("bench.py needs the GPU", file=sys.stderr)
+        sys.exit(1)
+    timer = Timer(torch)
+    print(f"bench: config 1 (steps={args.steps}, warmup={args.warmup})", file=sys.stderr, flush=True)
+    c1 = bench_c1(torch, D, synth, timer, args.steps, args.warmup)
+    configs = {"c1_q4_mlp": c1}
+    if not args.quick:
+        for name, fn in (("c0_q8_gemv", bench_c0), ("c2_q8_lmhead_argmax", bench_c2),
+                         ("c3_q4_prefill_gemm", bench_c3), ("c4_vision_bf16_pair", bench_c4)):
+            print(f"bench: {name}", file=sys.stderr, flush=True)
+            configs[name] = fn(torch, D, synth, timer, args.steps, args.warmup)
+            torch.cuda.empty_cache()
+    cpu = None
+    if not args.no_cpu:
+        print("bench: cpu baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(synth, args.cpu_seconds)
+
+    achieved = c1["gemv_gbps"]
+    line = {
+        "metric": METRIC,
+        "value": round(c1["gbps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c1["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded PCG64: Q4 nibbles uniform 0..15, fp16 d = |N(0,1)|*0.02, x ~ N(0,1))",
+        "config": {"workload": "c1_q4_mlp_6144x2048_batch1", "batch": 1, "gate_up": [6144, 2048],
+                   "down": [2048, 6144], "weights": "Q4_0", "weight_copies": c1["weight_copies"],
+                   "frac_hbm": round(c1["gbps"] / HBM_PEAK_GBS, 4),
+                   "resident_gbps_mall": round(c1["resident_gbps"], 2)},
+        "roofline": {"bound": "hbm", "kernel": "gemv_q4 (gate/up/down, mean)",
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles(),
+                     "bytes_per_launch": c1["gemv_bytes_per_launch"],
+                     "launch_ms": round(c1["gemv_mean_ms"], 6)},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

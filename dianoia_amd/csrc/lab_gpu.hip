@@ -1,0 +1,595 @@
+// The lab_gpu_* C ABI of the reference (src/vulkan/lab_vulkan.c,
+// src/metal/lab_metal.m), on one MI355X through HIP.
+//
+// Design for a discrete GPU (the reference assumes host-visible coherent
+// buffers, lab_vulkan.c:7-10):
+//
+// * A buffer is an HBM allocation plus a pinned host shadow; the shadow is
+//   what lab_gpu_contents returns. Wrapped weights get no shadow until a
+//   caller asks for their contents.
+// * lab_gpu_enc_* only record commands. lab_gpu_commit runs them in order
+//   on one HIP stream: before a command, the host regions it reads are
+//   uploaded unless an earlier command of this command buffer wrote them
+//   (the host may have rewritten any input since, lab_vulkan.c:664); a
+//   weight buffer is uploaded once, on its first use as weights, and is
+//   immutable afterwards. After the last command, every region a command
+//   wrote is copied back to the shadow. Stream order gives each dispatch
+//   the previous one's writes (the reference's barrier after each
+//   dispatch, lab_vulkan.c:769-787).
+// * Scratch (quantized activations, argmax partials) is internal device
+//   memory: it does not count as a live buffer.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <utility>
+#include <vector>
+
+#include "dnx_kernels.h"
+#include "lab_gpu.h"
+
+#define LOG(...) fprintf(stderr, "lab_gpu: " __VA_ARGS__)
+
+namespace {
+
+constexpr int64_t kMaxBuffers = 4096;
+constexpr int kMaxProfiled = 1024;
+
+// Kernel kinds in the reference's lab_gpu_profile order (lab_vulkan.c:
+// 174-177, names in gpu.dart:545-564), then this library's own.
+enum Kind {
+  kKindGemvQ8, kKindGemmQ8, kKindGemvQ4, kKindGemmQ4, kKindRmsNorm, kKindHeadNormRope,
+  kKindConv, kKindAttention, kKindSwiglu, kKindCopy, kKindQuantize, kKindGemmQ8I8,
+  kKindGemmQ4I8, kKindGemvQ8I8, kKindGemvQ4I8, kKindGemvQ8I8Vec, kKindSteer, kKindAdd,
+  kKindArgmax, kKindQuantizeWeights, kKindGelu, kKinds
+};
+
+struct Buffer {
+  void* host = nullptr;   // pinned shadow (lazily made for wrapped buffers)
+  void* dev = nullptr;
+  int64_t size = 0;
+  bool live = false;
+  bool weights = false;   // HBM copy is authoritative and immutable
+};
+
+enum Op { kOpMatmulQ8, kOpMatmulQ4, kOpSwiglu, kOpQuantize, kOpQuantizeBf16, kOpArgmax, kOpGelu };
+
+struct Cmd {
+  Op op;
+  int64_t a[10];
+};
+
+struct Region {
+  int64_t handle, offset, bytes;
+};
+
+bool gReady = false;
+hipStream_t gStream;
+hipEvent_t gStart, gStop;
+hipEvent_t gProfEvents[kMaxProfiled];
+int gProfKinds[kMaxProfiled];
+int gProfiled = 0;
+bool gProfiling = false;
+double gKindMs[kKinds];
+int64_t gKindCount[kKinds];
+double gLastMs = 0;
+bool gPending = false;
+bool gFailed = false;   // a recorded command was invalid
+std::vector<Cmd> gCmds;
+std::vector<Region> gWritten;
+
+Buffer gBuffers[kMaxBuffers];
+int64_t gBufferCount = 0, gFree[kMaxBuffers], gFreeCount = 0, gLive = 0;
+
+// Quantized-activation scratch for the GEMM path, and argmax partials.
+int8_t* gXq = nullptr;
+float* gXs = nullptr;
+int64_t gXCapacity = 0;  // values
+void* gArgmaxWs = nullptr;
+
+bool valid(int64_t h) { return h >= 0 && h < gBufferCount && gBuffers[h].live; }
+
+bool in_bounds(int64_t h, int64_t offset, int64_t bytes) {
+  return valid(h) && offset >= 0 && bytes >= 0 && offset + bytes <= gBuffers[h].size;
+}
+
+char* dev_at(int64_t h, int64_t offset) { return (char*)gBuffers[h].dev + offset; }
+
+int64_t create(int64_t bytes, bool shadow) {
+  if (!gReady || bytes <= 0) return -1;
+  int64_t handle;
+  if (gFreeCount > 0) {
+    handle = gFree[gFreeCount - 1];
+  } else if (gBufferCount < kMaxBuffers) {
+    handle = gBufferCount;
+  } else {
+    return -1;
+  }
+  Buffer b;
+  if (hipMalloc(&b.dev, (size_t)bytes) != hipSuccess) return -1;
+  if (shadow && hipHostMalloc(&b.host, (size_t)bytes, hipHostMallocDefault) != hipSuccess) {
+    (void)hipFree(b.dev);
+    return -1;
+  }
+  b.size = bytes;
+  b.live = true;
+  gBuffers[handle] = b;
+  if (handle == gBufferCount) {
+    gBufferCount++;
+  } else {
+    gFreeCount--;
+  }
+  gLive++;
+  return handle;
+}
+
+// Uploads the parts of [offset, offset + bytes) of h that no command of
+// this command buffer has written (those are current in HBM already).
+void upload_gaps(int64_t h, int64_t offset, int64_t bytes) {
+  Buffer& b = gBuffers[h];
+  std::vector<std::pair<int64_t, int64_t>> cover;
+  for (const Region& r : gWritten) {
+    if (r.handle == h && offset < r.offset + r.bytes && r.offset < offset + bytes) {
+      cover.push_back({r.offset, r.offset + r.bytes});
+    }
+  }
+  std::sort(cover.begin(), cover.end());
+  int64_t at = offset;
+  const int64_t end = offset + bytes;
+  for (const auto& c : cover) {
+    if (c.first > at) {
+      (void)hipMemcpyAsync(dev_at(h, at), (char*)b.host + at, (size_t)(c.first - at),
+                           hipMemcpyHostToDevice, gStream);
+    }
+    if (c.second > at) at = c.second;
+  }
+  if (at < end) {
+    (void)hipMemcpyAsync(dev_at(h, at), (char*)b.host + at, (size_t)(end - at),
+                         hipMemcpyHostToDevice, gStream);
+  }
+}
+
+// Makes the device copy of [offset, offset + bytes) of h current.
+void read_region(int64_t h, int64_t offset, int64_t bytes) {
+  Buffer& b = gBuffers[h];
+  if (b.weights || b.host == nullptr || bytes <= 0) return;
+  upload_gaps(h, offset, bytes);
+}
+
+// First use of h as weights: its host content goes to HBM once (except what
+// this command buffer already produced there); afterwards HBM is
+// authoritative and the buffer is treated as immutable.
+void use_as_weights(int64_t h) {
+  Buffer& b = gBuffers[h];
+  if (b.weights) return;
+  if (b.host != nullptr) upload_gaps(h, 0, b.size);
+  b.weights = true;
+}
+
+void wrote_region(int64_t h, int64_t offset, int64_t bytes) {
+  gWritten.push_back({h, offset, bytes});
+}
+
+void after_dispatch(int kind) {
+  if (gProfiling && gProfiled < kMaxProfiled) {
+    (void)hipEventRecord(gProfEvents[gProfiled], gStream);
+    gProfKinds[gProfiled++] = kind;
+  }
+}
+
+bool grow_scratch(int64_t values) {
+  if (values <= gXCapacity) return true;
+  const int64_t cap = values > (1 << 20) ? values : (1 << 20);
+  if (gXq) (void)hipFree(gXq);
+  if (gXs) (void)hipFree(gXs);
+  gXq = nullptr;
+  gXs = nullptr;
+  gXCapacity = 0;
+  if (hipMalloc(&gXq, (size_t)cap) != hipSuccess) return false;
+  if (hipMalloc(&gXs, (size_t)(cap / 32) * 4) != hipSuccess) return false;
+  gXCapacity = cap;
+  return true;
+}
+
+bool wait_pending() {
+  if (!gPending) return true;
+  gPending = false;
+  if (hipEventSynchronize(gStop) != hipSuccess) return false;
+  float ms = 0;
+  if (hipEventElapsedTime(&ms, gStart, gStop) == hipSuccess) gLastMs = ms;
+  for (int i = 0; i < gProfiled; i++) {
+    float e = 0;
+    // Each dispatch's share runs from the previous mark to its own, which
+    // includes the uploads it waited for (as the reference's includes its
+    // barrier, lab_vulkan.c:623-629).
+    if (hipEventElapsedTime(&e, i == 0 ? gStart : gProfEvents[i - 1], gProfEvents[i]) ==
+        hipSuccess) {
+      gKindMs[gProfKinds[i]] += e;
+      gKindCount[gProfKinds[i]]++;
+    }
+  }
+  gProfiled = 0;
+  return hipStreamQuery(gStream) == hipSuccess;
+}
+
+void record(Op op, std::initializer_list<int64_t> args) {
+  Cmd c;
+  c.op = op;
+  int i = 0;
+  for (int64_t v : args) c.a[i++] = v;
+  gCmds.push_back(c);
+}
+
+// The matmul of one recorded command: GEMV (bit-exact) for n <= 4, else the
+// activation quantizer and the int8-MFMA GEMM.
+bool run_matmul(const Cmd& c, bool q4) {
+  const int64_t w = c.a[0], qsOff = c.a[1], scOff = c.a[2], x = c.a[3], xOff = c.a[4];
+  const int64_t y = c.a[5], yOff = c.a[6], rows = c.a[7], cols = c.a[8], n = c.a[9];
+  use_as_weights(w);
+  read_region(x, xOff, n * cols * 4);
+  const void* qs = dev_at(w, qsOff);
+  const void* sc = dev_at(w, scOff);
+  const float* xs = (const float*)dev_at(x, xOff);
+  float* ys = (float*)dev_at(y, yOff);
+  int rc;
+  if (n <= 4) {
+    rc = q4 ? dnx_gemv_q4((const uint8_t*)qs, (const uint16_t*)sc, xs, ys, rows, cols, n,
+                          gStream)
+            : dnx_gemv_q8((const int8_t*)qs, (const float*)sc, xs, ys, rows, cols, n, gStream);
+    if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+  } else {
+    rc = dnx_quantize_q8(xs, gXq, gXs, n, cols, cols, gStream);
+    if (rc == DNX_OK) {
+      after_dispatch(kKindQuantize);
+      rc = q4 ? dnx_gemm_q4((const uint8_t*)qs, (const uint16_t*)sc, gXq, gXs, ys, rows, cols, n,
+                            gStream)
+              : dnx_gemm_q8((const int8_t*)qs, (const float*)sc, gXq, gXs, ys, rows, cols, n,
+                            gStream);
+      if (rc == DNX_OK) after_dispatch(q4 ? kKindGemmQ4I8 : kKindGemmQ8I8);
+    }
+  }
+  wrote_region(y, yOff, n * rows * 4);
+  if (rc != DNX_OK) LOG("matmul %s %ldx%ld n=%ld failed (%d)\n", q4 ? "q4" : "q8", (long)rows,
+                        (long)cols, (long)n, rc);
+  return rc == DNX_OK;
+}
+
+bool run(const Cmd& c) {
+  switch (c.op) {
+    case kOpMatmulQ8:
+      return run_matmul(c, false);
+    case kOpMatmulQ4:
+      return run_matmul(c, true);
+    case kOpSwiglu: {
+      const int64_t g = c.a[0], u = c.a[1], count = c.a[2];
+      read_region(g, 0, count * 4);
+      read_region(u, 0, count * 4);
+      const int rc = dnx_swiglu((float*)dev_at(g, 0), (const float*)dev_at(u, 0), count, gStream);
+      after_dispatch(kKindSwiglu);
+      wrote_region(g, 0, count * 4);
+      return rc == DNX_OK;
+    }
+    case kOpQuantize:
+    case kOpQuantizeBf16: {
+      const bool bf16 = c.op == kOpQuantizeBf16;
+      const int64_t src = c.a[0], srcOff = c.a[1], qs = c.a[2], qsOff = c.a[3];
+      const int64_t sc = c.a[4], scOff = c.a[5], rows = c.a[6], cols = c.a[7], pad = c.a[8];
+      read_region(src, srcOff, rows * cols * (bf16 ? 2 : 4));
+      const int rc =
+          bf16 ? dnx_quantize_q8_bf16((const uint16_t*)dev_at(src, srcOff),
+                                      (int8_t*)dev_at(qs, qsOff), (float*)dev_at(sc, scOff), rows,
+                                      cols, pad, gStream)
+               : dnx_quantize_q8((const float*)dev_at(src, srcOff), (int8_t*)dev_at(qs, qsOff),
+                                 (float*)dev_at(sc, scOff), rows, cols, pad, gStream);
+      after_dispatch(kKindQuantizeWeights);
+      wrote_region(qs, qsOff, rows * pad);
+      wrote_region(sc, scOff, rows * (pad / 32) * 4);
+      return rc == DNX_OK;
+    }
+    case kOpArgmax: {
+      const int64_t x = c.a[0], xOff = c.a[1], n = c.a[2], out = c.a[3], outOff = c.a[4];
+      read_region(x, xOff, n * 4);
+      const int rc = dnx_argmax((const float*)dev_at(x, xOff), n, (int64_t*)dev_at(out, outOff),
+                                gArgmaxWs, gStream);
+      after_dispatch(kKindArgmax);
+      wrote_region(out, outOff, 8);
+      return rc == DNX_OK;
+    }
+    case kOpGelu: {
+      const int64_t x = c.a[0], xOff = c.a[1], count = c.a[2];
+      read_region(x, xOff, count * 4);
+      const int rc = dnx_gelu((float*)dev_at(x, xOff), count, gStream);
+      after_dispatch(kKindGelu);
+      wrote_region(x, xOff, count * 4);
+      return rc == DNX_OK;
+    }
+  }
+  return false;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t lab_gpu_init(void) {
+  if (gReady) return 1;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count < 1) {
+    LOG("no HIP device\n");
+    return 0;
+  }
+  if (hipSetDevice(0) != hipSuccess) {
+    LOG("hipSetDevice(0) failed\n");
+    return 0;
+  }
+  // Default priority: streams of other priorities are not used here.
+  if (hipStreamCreateWithFlags(&gStream, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreate(&gStart) != hipSuccess || hipEventCreate(&gStop) != hipSuccess) {
+    LOG("stream or event creation failed\n");
+    return 0;
+  }
+  for (int i = 0; i < kMaxProfiled; i++) {
+    if (hipEventCreate(&gProfEvents[i]) != hipSuccess) {
+      LOG("event creation failed\n");
+      return 0;
+    }
+  }
+  if (hipMalloc(&gArgmaxWs, (size_t)dnx_argmax_workspace_bytes(0)) != hipSuccess) {
+    LOG("scratch allocation failed\n");
+    return 0;
+  }
+  gReady = true;
+  return 1;
+}
+
+int64_t lab_gpu_buffer(int64_t bytes) {
+  const int64_t h = create(bytes, true);
+  if (h < 0) return -1;
+  memset(gBuffers[h].host, 0, (size_t)bytes);
+  if (hipMemset(gBuffers[h].dev, 0, (size_t)bytes) != hipSuccess) {
+    lab_gpu_release(h);
+    return -1;
+  }
+  return h;
+}
+
+int64_t lab_gpu_readback_buffer(int64_t bytes) { return lab_gpu_buffer(bytes); }
+
+int64_t lab_gpu_wrap(void* address, int64_t bytes) {
+  if (address == nullptr) return -1;
+  const int64_t h = create(bytes, false);
+  if (h < 0) return -1;
+  if (hipMemcpy(gBuffers[h].dev, address, (size_t)bytes, hipMemcpyHostToDevice) != hipSuccess) {
+    lab_gpu_release(h);
+    return -1;
+  }
+  gBuffers[h].weights = true;
+  return h;
+}
+
+int64_t lab_gpu_wrap_copies(void) { return 1; }
+
+void* lab_gpu_contents(int64_t handle) {
+  if (!valid(handle)) return nullptr;
+  Buffer& b = gBuffers[handle];
+  if (b.host == nullptr) {
+    // A wrapped buffer: its host view is made on request from HBM.
+    if (!wait_pending()) return nullptr;
+    if (hipHostMalloc(&b.host, (size_t)b.size, hipHostMallocDefault) != hipSuccess) {
+      b.host = nullptr;
+      return nullptr;
+    }
+    if (hipMemcpy(b.host, b.dev, (size_t)b.size, hipMemcpyDeviceToHost) != hipSuccess) {
+      return nullptr;
+    }
+  }
+  return b.host;
+}
+
+double lab_gpu_last_ms(void) { return gLastMs; }
+
+void lab_gpu_release(int64_t handle) {
+  if (!valid(handle)) return;
+  wait_pending();
+  Buffer& b = gBuffers[handle];
+  (void)hipFree(b.dev);
+  if (b.host) (void)hipHostFree(b.host);
+  b = Buffer();
+  gFree[gFreeCount++] = handle;
+  gLive--;
+}
+
+int64_t lab_gpu_live_buffers(void) { return gLive; }
+
+void lab_gpu_begin(void) {
+  wait_pending();
+  gCmds.clear();
+  gFailed = false;
+}
+
+int64_t lab_gpu_commit(int64_t wait) {
+  if (!gReady) return 0;
+  gWritten.clear();
+  gProfiled = 0;
+  bool ok = !gFailed;
+  (void)hipEventRecord(gStart, gStream);
+  for (const Cmd& c : gCmds) ok = run(c) && ok;
+  // Results back to the host views.
+  for (const Region& r : gWritten) {
+    Buffer& b = gBuffers[r.handle];
+    if (b.host != nullptr && r.bytes > 0) {
+      (void)hipMemcpyAsync((char*)b.host + r.offset, dev_at(r.handle, r.offset), (size_t)r.bytes,
+                           hipMemcpyDeviceToHost, gStream);
+    }
+  }
+  if (hipEventRecord(gStop, gStream) != hipSuccess) ok = false;
+  gCmds.clear();
+  gFailed = false;
+  gPending = true;
+  if (!wait) return ok ? 1 : 0;
+  if (!wait_pending()) {
+    LOG("waiting for the GPU failed\n");
+    return 0;
+  }
+  return ok ? 1 : 0;
+}
+
+int64_t lab_gpu_wait(void) {
+  if (!wait_pending()) {
+    LOG("waiting for the GPU failed\n");
+    return 0;
+  }
+  return 1;
+}
+
+static void enc_matmul(Op op, int64_t w, int64_t qsOffset, int64_t scalesOffset, int64_t x,
+                       int64_t xOffset, int64_t y, int64_t yOffset, int64_t rows, int64_t cols,
+                       int64_t n) {
+  const bool q4 = op == kOpMatmulQ4;
+  const int64_t blocks = cols / 32;
+  const bool ok = rows > 0 && cols > 0 && n > 0 && cols % 32 == 0 &&
+                  in_bounds(w, qsOffset, q4 ? rows * cols / 2 : rows * cols) &&
+                  in_bounds(w, scalesOffset, rows * blocks * (q4 ? 2 : 4)) &&
+                  in_bounds(x, xOffset, n * cols * 4) && in_bounds(y, yOffset, n * rows * 4) &&
+                  ((uintptr_t)dev_at(w, qsOffset) % 16) == 0 &&
+                  ((uintptr_t)dev_at(w, scalesOffset) % (q4 ? 2 : 4)) == 0 &&
+                  (xOffset % 4) == 0 && (yOffset % 4) == 0 && (n <= 4 || grow_scratch(n * cols));
+  if (!ok) {
+    LOG("enc_matmul_%s: invalid arguments (rows=%ld cols=%ld n=%ld)\n", q4 ? "q4" : "q8",
+        (long)rows, (long)cols, (long)n);
+    gFailed = true;
+    return;
+  }
+  record(op, {w, qsOffset, scalesOffset, x, xOffset, y, yOffset, rows, cols, n});
+}
+
+void lab_gpu_enc_matmul_q8(int64_t w, int64_t qsOffset, int64_t scalesOffset, int64_t x,
+                           int64_t xOffset, int64_t y, int64_t yOffset, int64_t rows,
+                           int64_t cols, int64_t n) {
+  enc_matmul(kOpMatmulQ8, w, qsOffset, scalesOffset, x, xOffset, y, yOffset, rows, cols, n);
+}
+
+void lab_gpu_enc_matmul_q4(int64_t w, int64_t qsOffset, int64_t scalesOffset, int64_t x,
+                           int64_t xOffset, int64_t y, int64_t yOffset, int64_t rows,
+                           int64_t cols, int64_t n) {
+  enc_matmul(kOpMatmulQ4, w, qsOffset, scalesOffset, x, xOffset, y, yOffset, rows, cols, n);
+}
+
+void lab_gpu_enc_swiglu(int64_t g, int64_t u, int64_t count) {
+  if (count < 0 || !in_bounds(g, 0, count * 4) || !in_bounds(u, 0, count * 4)) {
+    LOG("enc_swiglu: invalid arguments\n");
+    gFailed = true;
+    return;
+  }
+  record(kOpSwiglu, {g, u, count});
+}
+
+static void enc_quantize(Op op, int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                         int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols,
+                         int64_t colsPad) {
+  const int64_t esize = op == kOpQuantizeBf16 ? 2 : 4;
+  const bool ok = rows >= 0 && cols > 0 && colsPad >= cols && colsPad % 32 == 0 &&
+                  in_bounds(src, srcOffset, rows * cols * esize) &&
+                  in_bounds(qs, qsOffset, rows * colsPad) &&
+                  in_bounds(scales, scalesOffset, rows * (colsPad / 32) * 4) &&
+                  srcOffset % esize == 0 && qsOffset % 4 == 0 && scalesOffset % 4 == 0;
+  if (!ok) {
+    LOG("enc_quantize: invalid arguments\n");
+    gFailed = true;
+    return;
+  }
+  record(op, {src, srcOffset, qs, qsOffset, scales, scalesOffset, rows, cols, colsPad});
+}
+
+void lab_gpu_enc_quantize_q8(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                             int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols,
+                             int64_t colsPad) {
+  enc_quantize(kOpQuantize, src, srcOffset, qs, qsOffset, scales, scalesOffset, rows, cols,
+               colsPad);
+}
+
+void lab_gpu_enc_quantize_q8_bf16(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                                  int64_t scales, int64_t scalesOffset, int64_t rows,
+                                  int64_t cols, int64_t colsPad) {
+  enc_quantize(kOpQuantizeBf16, src, srcOffset, qs, qsOffset, scales, scalesOffset, rows, cols,
+               colsPad);
+}
+
+void lab_gpu_enc_argmax(int64_t x, int64_t xOffset, int64_t n, int64_t out, int64_t outOffset) {
+  if (n <= 0 || !in_bounds(x, xOffset, n * 4) || !in_bounds(out, outOffset, 8) ||
+      xOffset % 4 != 0 || outOffset % 8 != 0) {
+    LOG("enc_argmax: invalid arguments\n");
+    gFailed = true;
+    return;
+  }
+  record(kOpArgmax, {x, xOffset, n, out, outOffset});
+}
+
+void lab_gpu_enc_gelu(int64_t x, int64_t xOffset, int64_t count) {
+  if (count < 0 || !in_bounds(x, xOffset, count * 4) || xOffset % 4 != 0) {
+    LOG("enc_gelu: invalid arguments\n");
+    gFailed = true;
+    return;
+  }
+  record(kOpGelu, {x, xOffset, count});
+}
+
+void lab_gpu_set_profiling(int64_t on) { gProfiling = on != 0; }
+
+int64_t lab_gpu_profile(double* ms, int64_t* counts, int64_t kinds) {
+  for (int64_t k = 0; k < kinds && k < kKinds; k++) {
+    ms[k] = gKindMs[k];
+    counts[k] = gKindCount[k];
+    gKindMs[k] = 0;
+    gKindCount[k] = 0;
+  }
+  return kKinds;
+}
+
+void lab_gpu_set_decode_rows(int64_t rows) { (void)rows; }
+int64_t lab_gpu_set_q8_group(int64_t invocations) {
+  (void)invocations;
+  return 0;
+}
+int64_t lab_gpu_set_q8_vector(int64_t on) {
+  (void)on;
+  return 0;
+}
+int64_t lab_gpu_register_q8_head(int64_t w, int64_t qs, int64_t rows, int64_t cols,
+                                 int64_t q4Body) {
+  (void)w; (void)qs; (void)rows; (void)cols; (void)q4Body;
+  return 0;
+}
+
+void lab_gpu_device_name(char* out, int64_t capacity) {
+  if (out == nullptr || capacity <= 0) return;
+  hipDeviceProp_t prop;
+  if (gReady && hipGetDeviceProperties(&prop, 0) == hipSuccess) {
+    snprintf(out, (size_t)capacity, "%s (%s)", prop.name, prop.gcnArchName);
+  } else {
+    snprintf(out, (size_t)capacity, "%s", "");
+  }
+}
+
+int64_t lab_gpu_max_buffer_length(void) {
+  size_t free_b = 0, total = 0;
+  if (!gReady || hipMemGetInfo(&free_b, &total) != hipSuccess) return 0;
+  return (int64_t)total;
+}
+
+// No attention kernel is built here; report the LDS a workgroup may use.
+int64_t lab_gpu_max_shared_memory(void) { return 160 * 1024; }
+
+int64_t lab_gpu_recommended_working_set(void) { return lab_gpu_max_buffer_length(); }
+
+int64_t lab_gpu_thermal_state(void) { return -1; }
+
+int64_t lab_gpu_physical_memory(void) {
+  return (int64_t)sysconf(_SC_PHYS_PAGES) * (int64_t)sysconf(_SC_PAGESIZE);
+}
+
+}  // extern "C"

@@ -1,0 +1,83 @@
+"""The dnx_* device launchers for torch tensors already in HBM.
+
+torch supplies device memory and the stream (plumbing); the computation is
+the library's HIP kernels. Every function enqueues on the current torch
+stream (or ``stream``) and raises on a non-zero return code, before which
+nothing was launched.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _stream(stream=None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("device launchers take CUDA (HIP) tensors")
+    if not t.is_contiguous():
+        raise ValueError("device launchers take contiguous tensors")
+    return t.data_ptr()
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed with code {rc}")
+
+
+def quantize_q8(x: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, rows: int, cols: int,
+                cols_pad: int, stream=None) -> None:
+    _check(_lib.load().dnx_quantize_q8(_ptr(x), _ptr(qs), _ptr(scales), rows, cols, cols_pad,
+                                       _stream(stream)), "dnx_quantize_q8")
+
+
+def quantize_q8_bf16(w: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, rows: int,
+                     cols: int, cols_pad: int, stream=None) -> None:
+    _check(_lib.load().dnx_quantize_q8_bf16(_ptr(w), _ptr(qs), _ptr(scales), rows, cols,
+                                            cols_pad, _stream(stream)), "dnx_quantize_q8_bf16")
+
+
+def gemv_q8(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> None:
+    _check(_lib.load().dnx_gemv_q8(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
+                                   _stream(stream)), "dnx_gemv_q8")
+
+
+def gemv_q4(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> None:
+    _check(_lib.load().dnx_gemv_q4(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
+                                   _stream(stream)), "dnx_gemv_q4")
+
+
+def gemm_q8(qs, scales, xq, xsc, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _check(_lib.load().dnx_gemm_q8(_ptr(qs), _ptr(scales), _ptr(xq), _ptr(xsc), _ptr(y), rows,
+                                   cols, n, _stream(stream)), "dnx_gemm_q8")
+
+
+def gemm_q4(qs, scales, xq, xsc, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _check(_lib.load().dnx_gemm_q4(_ptr(qs), _ptr(scales), _ptr(xq), _ptr(xsc), _ptr(y), rows,
+                                   cols, n, _stream(stream)), "dnx_gemm_q4")
+
+
+def argmax_workspace(n: int, device="cuda") -> torch.Tensor:
+    nbytes = int(_lib.load().dnx_argmax_workspace_bytes(n))
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def argmax(v: torch.Tensor, out: torch.Tensor, workspace: torch.Tensor, stream=None) -> None:
+    _check(_lib.load().dnx_argmax(_ptr(v), v.numel(), _ptr(out), _ptr(workspace),
+                                  _stream(stream)), "dnx_argmax")
+
+
+def swiglu(g: torch.Tensor, u: torch.Tensor, stream=None) -> None:
+    _check(_lib.load().dnx_swiglu(_ptr(g), _ptr(u), g.numel(), _stream(stream)), "dnx_swiglu")
+
+
+def gelu(x: torch.Tensor, stream=None) -> None:
+    _check(_lib.load().dnx_gelu(_ptr(x), x.numel(), _stream(stream)), "dnx_gelu")

@@ -1,0 +1,76 @@
+// Device-pointer launchers of the MI355X (gfx950) quantized-linear kernels.
+//
+// These are the kernels behind the lab_gpu_* drop-in ABI (lab_gpu.h),
+// exported for callers that already hold device memory and a HIP stream
+// (the benchmark, the tests, an engine that keeps activations in HBM). All
+// pointers are device pointers; every call only enqueues work on `stream`
+// and returns DNX_OK or a negative error before anything is launched.
+//
+// Layouts are the reference engine's (lab_native.c:398-405, :893-902):
+//   Q8: qs int8 [rows][cols] row-major, scales fp32 [rows][cols/32]
+//   Q4: qs uint8 [rows][cols/2] (weight k of a block = low nibble of byte k,
+//       weight k+16 = high nibble), scales IEEE fp16 bits [rows][cols/32]
+//   x fp32 [n][cols], y fp32 [n][rows] (ys[t*rows + r], lab_native.c:547-552)
+#pragma once
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* dnx_stream_t;  // a hipStream_t
+
+enum {
+  DNX_OK = 0,
+  DNX_EINVAL = -1,   // shape or argument outside what the kernel supports
+  DNX_ELAUNCH = -2,  // the HIP launch failed
+  DNX_ENOMEM = -3,   // a scratch allocation failed
+};
+
+// lab_quantize_q8 (lab_native.c:407-429) on the GPU, bit-exact: rows x cols
+// fp32 -> int8 [rows][cols_pad] + fp32 scales [rows][cols_pad/32]. cols_pad
+// is a multiple of 32 >= cols; the values past cols are zero padding (the
+// extension that lets K = 4304 run as 4320).
+int dnx_quantize_q8(const float* x, int8_t* qs, float* scales, int64_t rows, int64_t cols,
+                    int64_t cols_pad, dnx_stream_t stream);
+
+// The BF16 load-time weight quantizer: _widenBf16 (safetensors.dart:207-212)
+// then lab_quantize_q8, fused; bit-exact with that CPU pair. Same padding.
+int dnx_quantize_q8_bf16(const uint16_t* w, int8_t* qs, float* scales, int64_t rows,
+                         int64_t cols, int64_t cols_pad, dnx_stream_t stream);
+
+// Decode GEMV, n <= 4 tokens, fp32 x quantized in the kernel's prologue:
+// lab_gemm_q8 / lab_gemm_q4 mode 1 (lab_native.c:553-579, :1059-1080) with
+// the CPU's exact float order, so y is bit-identical to theirs.
+int dnx_gemv_q8(const int8_t* qs, const float* scales, const float* x, float* y, int64_t rows,
+                int64_t cols, int64_t n, dnx_stream_t stream);
+int dnx_gemv_q4(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
+                int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
+
+// Prefill / encoder GEMM on int8 MFMA, any n, inputs already quantized
+// (xq int8 [n][cols], xsc fp32 [n][cols/32], e.g. by dnx_quantize_q8):
+// the per-32-block int32 dots are exact, the per-block scaling is fp32
+// (within 1e-4 relative of the CPU kernels, not bit-identical).
+int dnx_gemm_q8(const int8_t* qs, const float* scales, const int8_t* xq, const float* xsc,
+                float* y, int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
+int dnx_gemm_q4(const uint8_t* qs, const uint16_t* scales, const int8_t* xq, const float* xsc,
+                float* y, int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
+
+// Greedy argmax of v[0..n) (argmaxToken, lib/src/sampler.dart:137-152):
+// the first index of the maximum; a NaN at index 0 wins, other NaNs never.
+// Writes one int64 to *out. workspace: dnx_argmax_workspace_bytes(n) bytes.
+int64_t dnx_argmax_workspace_bytes(int64_t n);
+int dnx_argmax(const float* v, int64_t n, int64_t* out, void* workspace, dnx_stream_t stream);
+
+// g = SiLU(g) * u in place (the glue of lib/src/shard.dart:457-461 and
+// lab_gpu_enc_swiglu), SiLU in double as the Dart glue computes it.
+int dnx_swiglu(float* g, const float* u, int64_t count, dnx_stream_t stream);
+
+// Exact-erf GELU in place with the Abramowitz-Stegun erf in double
+// (lib/src/vision_encoder.dart:260-263, :496-509).
+int dnx_gelu(float* x, int64_t count, dnx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif

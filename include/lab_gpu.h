@@ -1,0 +1,142 @@
+// The reference's GPU C ABI (lab_gpu_*), implemented for one MI355X (gfx950)
+// by libdianoia_amd.so. Dart binds these names with @Native in
+// lib/src/gpu.dart:36-312 of the reference (Atrac613/dianoia); the Vulkan
+// (src/vulkan/lab_vulkan.c) and Metal (src/metal/lab_metal.m) layers export
+// the same signatures. Every handle, offset, size and count is int64_t.
+//
+// Model (as in the reference): one process-wide command buffer. Buffers have
+// a host view (lab_gpu_contents) that the caller writes inputs into and reads
+// outputs from. lab_gpu_enc_* record work; lab_gpu_commit submits it; each
+// recorded dispatch sees every earlier one's writes. On this discrete GPU a
+// buffer is a device allocation plus a pinned host shadow: commit uploads the
+// host regions a dispatch reads (unless an earlier dispatch of the same
+// command buffer wrote them), uploads a weight buffer once on its first use
+// as weights (weights are immutable, as in GpuLinear.upload,
+// gpu.dart:1295-1323), and copies every region a dispatch wrote back to the
+// host before the commit completes.
+//
+// Not re-entrant: one thread drives the GPU layer at a time (gpu.dart:
+// 1277-1278).
+#pragma once
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// lab_gpu_init (lab_vulkan.c:295-296; gpu.dart:36-37): 1 when the GPU is
+// ready, 0 when there is none (logged to stderr). Idempotent.
+int64_t lab_gpu_init(void);
+
+// lab_gpu_buffer (lab_vulkan.c:582-586; gpu.dart:63-64): a zeroed buffer of
+// `bytes`, returning its handle (>= 0) or -1. Handles freed by
+// lab_gpu_release are handed out again first; at most 4096 live.
+int64_t lab_gpu_buffer(int64_t bytes);
+
+// lab_gpu_readback_buffer (lab_vulkan.c:590-594; gpu.dart:66-67): the same,
+// for buffers the host reads after every command buffer (logits).
+int64_t lab_gpu_readback_buffer(int64_t bytes);
+
+// lab_gpu_wrap (lab_vulkan.c:598-602; gpu.dart:69-73): a buffer holding a
+// copy of `bytes` at `address` (the mapped weight cache), placed in HBM now.
+// lab_gpu_wrap_copies (lab_vulkan.c:605; gpu.dart:75-76) returns 1: the
+// wrapped memory may be evicted afterwards.
+int64_t lab_gpu_wrap(void* address, int64_t bytes);
+int64_t lab_gpu_wrap_copies(void);
+
+// lab_gpu_contents (lab_vulkan.c:607; gpu.dart:78-79): the buffer's stable
+// host pointer for its lifetime.
+void* lab_gpu_contents(int64_t handle);
+
+// lab_gpu_release / lab_gpu_live_buffers (lab_vulkan.c:637-652;
+// gpu.dart:81-85): release waits for submitted work, then frees the handle.
+// Internal scratch is not counted as a live buffer.
+void lab_gpu_release(int64_t handle);
+int64_t lab_gpu_live_buffers(void);
+
+// lab_gpu_begin / commit / wait / last_ms (lab_vulkan.c:655-665, 737-767,
+// 610; gpu.dart:111-123). commit(1) blocks until done; commit(0) returns
+// at once and lab_gpu_wait blocks later. Both return 1 on success, 0 on
+// failure (logged); a dispatch recorded with invalid arguments fails its
+// commit. last_ms is the GPU time of the last waited command buffer.
+void lab_gpu_begin(void);
+int64_t lab_gpu_commit(int64_t wait);
+int64_t lab_gpu_wait(void);
+double lab_gpu_last_ms(void);
+
+// lab_gpu_enc_matmul_q8 / _q4 (lab_vulkan.c:877-890; gpu.dart:125-177):
+// Y[n][rows] = X[n][cols] W^T, W inside buffer w at qsOffset / scalesOffset
+// in the engine's Q8 (int8 + fp32 scales) or Q4 (nibbles + fp16 scales)
+// layout, X at x + xOffset (fp32), Y at y + yOffset (fp32). The inputs are
+// quantized to Q8 per block as lab_native.c does (mode 1): for n <= 4 the
+// products are bit-identical to lab_gemm_q8 / lab_gemm_q4 mode 1; for larger
+// n they run on int8 MFMA within 1e-4 relative. qs must be 16-byte aligned.
+void lab_gpu_enc_matmul_q8(int64_t w, int64_t qsOffset, int64_t scalesOffset, int64_t x,
+                           int64_t xOffset, int64_t y, int64_t yOffset, int64_t rows,
+                           int64_t cols, int64_t n);
+void lab_gpu_enc_matmul_q4(int64_t w, int64_t qsOffset, int64_t scalesOffset, int64_t x,
+                           int64_t xOffset, int64_t y, int64_t yOffset, int64_t rows,
+                           int64_t cols, int64_t n);
+
+// lab_gpu_enc_swiglu (lab_vulkan.c:974-978; gpu.dart:179-312): g = SiLU(g)
+// * u over `count` floats from offset 0 of each buffer, SiLU in double as
+// the CPU glue computes it (shard.dart:457-461).
+void lab_gpu_enc_swiglu(int64_t g, int64_t u, int64_t count);
+
+// Load-time Q8 quantization on the GPU. No GPU counterpart in the
+// reference, which quantizes on the CPU: lab_quantize_q8 (lab_native.c:
+// 407-429, bound at native.dart:138-147) for fp32 weights, after
+// SafetensorsFile._widenBf16 (safetensors.dart:207-212) for BF16 ones
+// (vision_encoder.dart:36-66). rows x cols values (fp32, or bf16 bits) at
+// src + srcOffset become int8 [rows][colsPad] at qs + qsOffset and fp32
+// scales [rows][colsPad/32] at scales + scalesOffset, bit-exact with that
+// CPU path. colsPad is a multiple of 32 >= cols; the tail is zero padding
+// (the reference refuses cols % 32 != 0, native.dart:634-636; padding is
+// this library's defined extension).
+void lab_gpu_enc_quantize_q8(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                             int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols,
+                             int64_t colsPad);
+void lab_gpu_enc_quantize_q8_bf16(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                                  int64_t scales, int64_t scalesOffset, int64_t rows,
+                                  int64_t cols, int64_t colsPad);
+
+// Greedy token on the GPU: argmaxToken (sampler.dart:137-152, no
+// suppression) over n floats at x + xOffset, the index written as one int64
+// at out + outOffset. Replaces the logits copy + host argmax of
+// ChatSession.greedyToken (chat_session.dart:267-270, gpu.dart:785-793).
+void lab_gpu_enc_argmax(int64_t x, int64_t xOffset, int64_t n, int64_t out, int64_t outOffset);
+
+// The projector's exact-erf GELU in place over count floats at x + xOffset
+// (vision_encoder.dart:260-263): the glue between the vision encoder's fc1
+// and fc2. No GPU counterpart in the reference (done in Dart there).
+void lab_gpu_enc_gelu(int64_t x, int64_t xOffset, int64_t count);
+
+// lab_gpu_set_profiling / lab_gpu_profile (lab_vulkan.c:720-733;
+// gpu.dart:102-109, 545-564): per-kind GPU ms and dispatch counts since the
+// last call, in the reference's 18-kind order, followed here by three kinds
+// of this library's own (18 argmax, 19 weight quantization, 20 gelu). Copies
+// at most `kinds` entries and returns the number of kinds (21).
+void lab_gpu_set_profiling(int64_t on);
+int64_t lab_gpu_profile(double* ms, int64_t* counts, int64_t kinds);
+
+// Tuning knobs and device queries (lab_vulkan.c:506-530, 670-717;
+// gpu.dart:39-61, 87-100). The decode kernel here has one shape chosen per
+// matrix, so the knobs are accepted and have no effect: set_decode_rows is a
+// no-op, set_q8_group / set_q8_vector / register_q8_head return 0 (not
+// available), as the Metal layer does (lab_metal.m:757-766).
+void lab_gpu_set_decode_rows(int64_t rows);
+int64_t lab_gpu_set_q8_group(int64_t invocations);
+int64_t lab_gpu_set_q8_vector(int64_t on);
+int64_t lab_gpu_register_q8_head(int64_t w, int64_t qs, int64_t rows, int64_t cols,
+                                 int64_t q4Body);
+void lab_gpu_device_name(char* out, int64_t capacity);
+int64_t lab_gpu_max_buffer_length(void);
+int64_t lab_gpu_max_shared_memory(void);
+int64_t lab_gpu_recommended_working_set(void);
+int64_t lab_gpu_thermal_state(void);
+int64_t lab_gpu_physical_memory(void);
+
+#ifdef __cplusplus
+}
+#endif

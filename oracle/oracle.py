@@ -1,0 +1,224 @@
+"""ctypes bindings of the CPU oracle. TEST INFRASTRUCTURE ONLY.
+
+Loads ``oracle/liblab_oracle.so`` (the scalar restatement in lab_oracle.c)
+and, where it was built, ``oracle/_ref/liblab_native.so`` (the reference's
+own ``src/c/lab_native.c``). Only tests/, ``__graft_entry__.smoke()`` and
+bench.py's ``cpu_baseline`` leg may import this module: it is the checker
+and the CPU baseline, never the product path.
+
+Both libraries export the reference's argument order
+(``lab_gemm_q8(qs, scales, xs, xq, xsc, ys, rows, cols, n, threads, mode)``,
+``src/c/lab_native.c:553-555``), so one wrapper class serves both.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liblab_oracle.so")
+REF_SO = os.path.join(HERE, "_ref", "liblab_native.so")
+
+_i64 = ctypes.c_int64
+_p = ctypes.c_void_p
+
+
+def build(force: bool = False) -> None:
+    """Builds liblab_oracle.so (and _ref when the reference is mounted)."""
+    if force or not os.path.exists(ORACLE_SO):
+        subprocess.run(["make", "-C", HERE, "all"], check=True, capture_output=True)
+
+
+def _ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "arrays handed to C must be contiguous"
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+class _Kernels:
+    """The lab_* product and quantizer entry points of one library."""
+
+    def __init__(self, path: str, prefix: str):
+        self.path = path
+        self.lib = ctypes.CDLL(path)
+        self.prefix = prefix
+        for name in ("quantize_q8", "quantize_q4"):
+            f = getattr(self.lib, prefix + name)
+            f.argtypes = [_p, _p, _p, _i64, _i64]
+            f.restype = None
+        for name in ("gemm_q8", "gemm_q4"):
+            f = getattr(self.lib, prefix + name)
+            f.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64]
+            f.restype = None
+
+    def quantize_q8(self, x: np.ndarray):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        rows, cols = x.shape
+        qs = np.zeros((rows, cols), np.int8)
+        scales = np.zeros((rows, cols // 32), np.float32)
+        getattr(self.lib, self.prefix + "quantize_q8")(_ptr(x), _ptr(qs), _ptr(scales), rows, cols)
+        return qs, scales
+
+    def quantize_q4(self, w: np.ndarray):
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        rows, cols = w.shape
+        qs = np.zeros((rows, cols // 2), np.uint8)
+        scales = np.zeros((rows, cols // 32), np.uint16)
+        getattr(self.lib, self.prefix + "quantize_q4")(_ptr(w), _ptr(qs), _ptr(scales), rows, cols)
+        return qs, scales
+
+    def _gemm(self, name, qs, scales, xs, n, threads, mode, rows, cols):
+        xs = np.ascontiguousarray(xs, dtype=np.float32).reshape(n, cols)
+        xq = np.zeros(n * cols, np.int8)
+        xsc = np.zeros(n * cols // 32 + 1, np.float32)
+        ys = np.zeros((n, rows), np.float32)
+        getattr(self.lib, self.prefix + name)(
+            _ptr(qs), _ptr(scales), _ptr(xs), _ptr(xq), _ptr(xsc), _ptr(ys),
+            rows, cols, n, threads, mode)
+        return ys
+
+    def gemm_q8(self, qs, scales, xs, n=None, threads=1, mode=1):
+        qs = np.ascontiguousarray(qs, dtype=np.int8)
+        scales = np.ascontiguousarray(scales, dtype=np.float32)
+        rows, cols = qs.shape
+        n = xs.size // cols if n is None else n
+        return self._gemm("gemm_q8", qs, scales, xs, n, threads, mode, rows, cols)
+
+    def gemm_q4(self, qs, scales, xs, n=None, threads=1, mode=1):
+        qs = np.ascontiguousarray(qs, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint16)
+        rows, cols = qs.shape[0], qs.shape[1] * 2
+        n = xs.size // cols if n is None else n
+        return self._gemm("gemm_q4", qs, scales, xs, n, threads, mode, rows, cols)
+
+
+class Oracle(_Kernels):
+    """The restatement, plus the helpers the reference has no C form of."""
+
+    def __init__(self, path: str = ORACLE_SO):
+        build()
+        super().__init__(path, "orc_")
+        L = self.lib
+        L.orc_half_to_float.argtypes = [ctypes.c_uint16]
+        L.orc_half_to_float.restype = ctypes.c_float
+        L.orc_float_to_half.argtypes = [ctypes.c_float]
+        L.orc_float_to_half.restype = ctypes.c_uint16
+        for name in ("orc_quantize_q8_bf16", "orc_quantize_q8_padded"):
+            getattr(L, name).argtypes = [_p, _p, _p, _i64, _i64, _i64]
+            getattr(L, name).restype = None
+        for name in ("orc_gemm_q8_prequant", "orc_gemm_q4_prequant"):
+            getattr(L, name).argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64]
+            getattr(L, name).restype = None
+        for name in ("orc_block_dots_q8", "orc_block_dots_q4"):
+            getattr(L, name).argtypes = [_p, _p, _p, _i64, _i64, _i64]
+            getattr(L, name).restype = None
+        L.orc_argmax.argtypes = [_p, _i64]
+        L.orc_argmax.restype = _i64
+        L.orc_silu_mul.argtypes = [_p, _p, _i64]
+        L.orc_silu_mul.restype = None
+        L.orc_gelu.argtypes = [_p, _i64]
+        L.orc_gelu.restype = None
+
+    def half_to_float(self, h: int) -> float:
+        return self.lib.orc_half_to_float(h)
+
+    def float_to_half(self, f: float) -> int:
+        return self.lib.orc_float_to_half(f)
+
+    def quantize_q8_padded(self, x: np.ndarray, cols_pad: int):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        rows, cols = x.shape
+        qs = np.zeros((rows, cols_pad), np.int8)
+        scales = np.zeros((rows, cols_pad // 32), np.float32)
+        self.lib.orc_quantize_q8_padded(_ptr(x), _ptr(qs), _ptr(scales), rows, cols, cols_pad)
+        return qs, scales
+
+    def quantize_q8_bf16(self, w: np.ndarray, cols_pad: int | None = None):
+        w = np.ascontiguousarray(w, dtype=np.uint16)
+        rows, cols = w.shape
+        cols_pad = (cols + 31) // 32 * 32 if cols_pad is None else cols_pad
+        qs = np.zeros((rows, cols_pad), np.int8)
+        scales = np.zeros((rows, cols_pad // 32), np.float32)
+        self.lib.orc_quantize_q8_bf16(_ptr(w), _ptr(qs), _ptr(scales), rows, cols, cols_pad)
+        return qs, scales
+
+    def gemm_q8_prequant(self, qs, scales, xq, xsc, threads=8):
+        qs = np.ascontiguousarray(qs, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        rows, cols = qs.shape
+        xq = np.ascontiguousarray(xq, np.int8).reshape(-1, cols)
+        xsc = np.ascontiguousarray(xsc, np.float32).reshape(xq.shape[0], -1)
+        n = xq.shape[0]
+        ys = np.zeros((n, rows), np.float32)
+        self.lib.orc_gemm_q8_prequant(_ptr(qs), _ptr(scales), _ptr(xq), _ptr(xsc), _ptr(ys),
+                                      rows, cols, n, threads)
+        return ys
+
+    def gemm_q4_prequant(self, qs, scales, xq, xsc, threads=8):
+        qs = np.ascontiguousarray(qs, np.uint8)
+        scales = np.ascontiguousarray(scales, np.uint16)
+        rows, cols = qs.shape[0], qs.shape[1] * 2
+        xq = np.ascontiguousarray(xq, np.int8).reshape(-1, cols)
+        xsc = np.ascontiguousarray(xsc, np.float32).reshape(xq.shape[0], -1)
+        n = xq.shape[0]
+        ys = np.zeros((n, rows), np.float32)
+        self.lib.orc_gemm_q4_prequant(_ptr(qs), _ptr(scales), _ptr(xq), _ptr(xsc), _ptr(ys),
+                                      rows, cols, n, threads)
+        return ys
+
+    def block_dots_q8(self, qs, xq):
+        qs = np.ascontiguousarray(qs, np.int8)
+        rows, cols = qs.shape
+        xq = np.ascontiguousarray(xq, np.int8).reshape(-1, cols)
+        d = np.zeros((xq.shape[0], rows, cols // 32), np.int32)
+        self.lib.orc_block_dots_q8(_ptr(qs), _ptr(xq), _ptr(d), rows, cols, xq.shape[0])
+        return d
+
+    def block_dots_q4(self, qs, xq):
+        qs = np.ascontiguousarray(qs, np.uint8)
+        rows, cols = qs.shape[0], qs.shape[1] * 2
+        xq = np.ascontiguousarray(xq, np.int8).reshape(-1, cols)
+        d = np.zeros((xq.shape[0], rows, cols // 32), np.int32)
+        self.lib.orc_block_dots_q4(_ptr(qs), _ptr(xq), _ptr(d), rows, cols, xq.shape[0])
+        return d
+
+    def argmax(self, logits: np.ndarray) -> int:
+        logits = np.ascontiguousarray(logits, np.float32)
+        return int(self.lib.orc_argmax(_ptr(logits), logits.size))
+
+    def silu_mul(self, g: np.ndarray, u: np.ndarray) -> np.ndarray:
+        out = np.array(g, dtype=np.float32, copy=True)
+        u = np.ascontiguousarray(u, np.float32)
+        self.lib.orc_silu_mul(_ptr(out), _ptr(u), out.size)
+        return out
+
+    def gelu(self, x: np.ndarray) -> np.ndarray:
+        out = np.array(x, dtype=np.float32, copy=True)
+        self.lib.orc_gelu(_ptr(out), out.size)
+        return out
+
+
+class Reference(_Kernels):
+    """The reference's lab_native.c, compiled in oracle/_ref by oracle/Makefile."""
+
+    def __init__(self, path: str = REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        super().__init__(path, "lab_")
+
+
+def reference_available() -> bool:
+    return os.path.exists(REF_SO)
+
+
+_oracle: Oracle | None = None
+
+
+def get() -> Oracle:
+    global _oracle
+    if _oracle is None:
+        _oracle = Oracle()
+    return _oracle

@@ -1,0 +1,68 @@
+"""int8-MFMA GEMM: per-block int32 dots exact, fp32 outputs within 1e-4."""
+
+import numpy as np
+import pytest
+import torch
+
+from dianoia_amd import device as D
+from dianoia_amd import synth
+from gpu_util import bits, dev, host, within_tolerance
+
+pytestmark = pytest.mark.gpu
+
+
+def gemm(fmt, qs, sc, xq, xsc, rows, cols, n):
+    y = torch.full((n, rows), float("nan"), dtype=torch.float32, device="cuda")
+    f = D.gemm_q4 if fmt == "q4" else D.gemm_q8
+    f(dev(qs), dev(sc), dev(xq), dev(xsc), y, rows, cols, n)
+    return host(y)
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+@pytest.mark.parametrize("rows,cols,n", [(130, 256, 70), (128, 128, 128), (33, 96, 5)])
+def test_block_dots_are_exact(gpu_ready, orc, fmt, rows, cols, n):
+    """With scale 1 on one block and 0 on the others, y is that block's
+    int32 dot product as a float (exact below 2^24): the MFMA's integer
+    result for every block, compared with brute-force sums."""
+    rng = np.random.default_rng(rows + cols + n)
+    B = cols // 32
+    xq = rng.integers(-127, 128, (n, cols), dtype=np.int8)
+    if fmt == "q8":
+        qs = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+        want = orc.block_dots_q8(qs, xq)
+        one, zero = np.float32(1.0), np.float32(0.0)
+    else:
+        qs = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+        want = orc.block_dots_q4(qs, xq)
+        one, zero = np.uint16(0x3C00), np.uint16(0)
+    for b in range(B):
+        sw = np.full((rows, B), zero)
+        sw[:, b] = one
+        xsc = np.zeros((n, B), np.float32)
+        xsc[:, b] = 1.0
+        y = gemm(fmt, qs, sw, xq, xsc, rows, cols, n)
+        assert np.array_equal(y, want[:, :, b].astype(np.float32)), f"block {b}"
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+@pytest.mark.parametrize("rows,cols,n", [(6144, 2048, 512), (70, 96, 13), (36, 64, 9),
+                                         (128, 128, 40), (4304, 1152, 64), (1152, 4320, 33),
+                                         (257, 2048, 1), (100, 2048, 64)])
+def test_gemm_within_tolerance(gpu_ready, orc, fmt, rows, cols, n):
+    rng = np.random.default_rng(rows * 3 + cols + n)
+    if fmt == "q8":
+        qs, sc = synth.q8_weights(rng, rows, cols)
+    else:
+        qs, sc = synth.q4_weights(rng, rows, cols)
+    xs = synth.activations(rng, n, cols)
+    xq, xsc = orc.quantize_q8(xs)
+    ref = (orc.gemm_q8 if fmt == "q8" else orc.gemm_q4)(qs, sc, xs, n, threads=8, mode=1)
+    y = gemm(fmt, qs, sc, xq, xsc, rows, cols, n)
+    ok, worst_rel, worst_abs = within_tolerance(y, ref)
+    assert ok, (worst_rel, worst_abs)
+
+
+def test_gemm_rejects_unsupported(gpu_ready):
+    z = torch.zeros(4096, device="cuda")
+    with pytest.raises(RuntimeError):
+        D.gemm_q8(z, z, z, z, z, 4, 40, 2)

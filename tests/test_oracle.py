@@ -1,0 +1,205 @@
+"""The CPU oracle pinned against the reference's own kernels (CPU only).
+
+Every function of oracle/lab_oracle.c is checked against:
+* the golden vectors in tests/golden/ (written by the compiled reference
+  src/c/lab_native.c, see make_golden.py);
+* the compiled reference itself (oracle/_ref) on fresh seeded inputs, when
+  that library is present;
+* closed forms: quantizer edge cases, exhaustive fp16 conversions,
+  brute-force integer block dots, argmax ties and NaN, SiLU and GELU
+  identities.
+"""
+
+import glob
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("name", ["edges", "random"])
+def test_quantize_q8_matches_golden(orc, name):
+    d = np.load(os.path.join(GOLDEN, f"quantize_q8_{name}.npz"))
+    qs, sc = orc.quantize_q8(d["x"])
+    assert np.array_equal(qs, d["qs"])
+    assert np.array_equal(bits(sc), bits(d["scales"]))
+
+
+def test_quantize_q4_matches_golden(orc):
+    d = np.load(os.path.join(GOLDEN, "quantize_q4.npz"))
+    qs, sc = orc.quantize_q4(d["x"])
+    assert np.array_equal(qs, d["qs"])
+    assert np.array_equal(sc, d["scales"])
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "gemm_*.npz"))),
+                         ids=lambda p: os.path.basename(p)[:-4])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_gemm_matches_golden(orc, path, mode):
+    d = np.load(path)
+    q4 = os.path.basename(path).startswith("gemm_q4")
+    n = d["xs"].shape[0]
+    f = orc.gemm_q4 if q4 else orc.gemm_q8
+    for threads in (1, 3):
+        y = f(d["qs"], d["scales"], d["xs"], n, threads=threads, mode=mode)
+        assert np.array_equal(bits(y), bits(d[f"y_mode{mode}"]))
+
+
+def test_quantizer_closed_forms(orc):
+    # scale 1 (amax 127): q = round half away from zero, in float.
+    x = np.zeros((1, 32), np.float32)
+    x[0, :7] = [127.0, -127.0, 0.49999997, 2.5, -2.5, 0.5, -0.5]
+    qs, sc = orc.quantize_q8(x)
+    assert sc[0, 0] == 1.0
+    assert list(qs[0, :7]) == [127, -127, 1, 3, -3, 1, -1]
+    # all-zero block: scale 0, q 0
+    qs, sc = orc.quantize_q8(np.zeros((2, 64), np.float32))
+    assert not qs.any() and not sc.any()
+    # scale is amax / 127 correctly rounded; every |q| <= 127
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((64, 128)).astype(np.float32)
+    qs, sc = orc.quantize_q8(x)
+    amax = np.abs(x.reshape(64, 4, 32)).max(axis=2)
+    assert np.array_equal(bits(sc), bits((amax / np.float32(127)).astype(np.float32)))
+    assert np.abs(qs.astype(int)).max() <= 127
+    # dequantized values within half a step of the input
+    deq = qs.reshape(64, 4, 32).astype(np.float64) * sc[..., None]
+    assert np.all(np.abs(deq - x.reshape(64, 4, 32)) <= sc[..., None] * 0.5 * (1 + 1e-6))
+
+
+def test_padded_quantizer_is_the_padded_problem(orc):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 4304)).astype(np.float32)
+    qs, sc = orc.quantize_q8_padded(x, 4320)
+    xp = np.zeros((5, 4320), np.float32)
+    xp[:, :4304] = x
+    qs2, sc2 = orc.quantize_q8(xp)
+    assert np.array_equal(qs, qs2) and np.array_equal(bits(sc), bits(sc2))
+    assert not qs[:, 4304:].any()
+
+
+def test_bf16_quantizer_is_widen_then_quantize(orc):
+    from dianoia_amd.formats import widen_bf16
+    from dianoia_amd.synth import bf16_rne
+    rng = np.random.default_rng(4)
+    w = bf16_rne(rng.standard_normal((7, 1152)).astype(np.float32) * np.float32(0.02))
+    qs, sc = orc.quantize_q8_bf16(w)
+    qs2, sc2 = orc.quantize_q8(widen_bf16(w))
+    assert np.array_equal(qs, qs2) and np.array_equal(bits(sc), bits(sc2))
+
+
+def test_half_conversions_exhaustive(orc):
+    h = np.arange(65536, dtype=np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([orc.half_to_float(int(v)) for v in h], dtype=np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(bits(got)[finite], bits(want)[finite])
+    assert np.all(np.isnan(got[~np.isfinite(want) & np.isnan(want)]))
+    # float -> half round trip and RNE against numpy's conversion
+    f = np.concatenate([want[finite], np.float32([1e-8, 6.1e-5, 65519.0, 65520.0, 1e6, -1e-9])])
+    f = np.concatenate([f, (f * np.float32(1.0009765)).astype(np.float32)])
+    got_h = np.array([orc.float_to_half(float(v)) for v in f], dtype=np.uint16)
+    assert np.array_equal(got_h, f.astype(np.float16).view(np.uint16))
+
+
+def test_block_dots_brute_force(orc):
+    rng = np.random.default_rng(9)
+    qs = rng.integers(-127, 128, (6, 96), dtype=np.int8)
+    xq = rng.integers(-127, 128, (3, 96), dtype=np.int8)
+    d = orc.block_dots_q8(qs, xq)
+    want = np.einsum("rbk,tbk->trb", qs.reshape(6, 3, 32).astype(np.int64),
+                     xq.reshape(3, 3, 32).astype(np.int64))
+    assert np.array_equal(d, want)
+    q4 = rng.integers(0, 256, (6, 48), dtype=np.uint8)
+    w = np.empty((6, 96), np.int64)
+    blocks = q4.reshape(6, 3, 16).astype(np.int64)
+    w.reshape(6, 3, 32)[:, :, :16] = (blocks & 15) - 8
+    w.reshape(6, 3, 32)[:, :, 16:] = (blocks >> 4) - 8
+    d4 = orc.block_dots_q4(q4, xq)
+    assert np.array_equal(d4, np.einsum("rbk,tbk->trb", w.reshape(6, 3, 32),
+                                        xq.reshape(3, 3, 32).astype(np.int64)))
+
+
+def test_mode1_products_against_exact_sums(orc):
+    # y = sum_b s_b * d_b within fp32 rounding of the exact double sum
+    rng = np.random.default_rng(11)
+    w = (rng.random((9, 512)) - 0.5).astype(np.float32)
+    xs = (rng.random((2, 512)) * 2 - 1).astype(np.float32)
+    qs, sc = orc.quantize_q8(w)
+    y = orc.gemm_q8(qs, sc, xs, 2, threads=1, mode=1)
+    xq, xsc = orc.quantize_q8(xs)
+    d = orc.block_dots_q8(qs, xq).astype(np.float64)
+    exact = (d * sc[None].astype(np.float64) * xsc[:, None, :]).sum(axis=2)
+    mag = (np.abs(d) * sc[None] * xsc[:, None, :]).sum(axis=2)
+    assert np.all(np.abs(y - exact) <= 1e-6 * mag + 1e-30)
+
+
+def test_argmax_closed_forms(orc):
+    assert orc.argmax(np.float32([1, 3, 3, 2])) == 1            # first of a tie
+    assert orc.argmax(np.float32([-0.0, 0.0])) == 0             # -0 == +0
+    assert orc.argmax(np.float32([np.nan, 5, 7])) == 0          # NaN at 0 stays
+    assert orc.argmax(np.float32([1, np.nan, 0.5])) == 0        # NaN never wins
+    assert orc.argmax(np.float32([1, np.nan, 4])) == 2
+    assert orc.argmax(np.float32([-np.inf, -1e38])) == 1
+    rng = np.random.default_rng(5)
+    v = rng.standard_normal(100001).astype(np.float32)
+    assert orc.argmax(v) == int(np.argmax(v))
+
+
+def test_silu_glue_closed_forms(orc):
+    rng = np.random.default_rng(12)
+    g = rng.standard_normal(4096).astype(np.float32) * 4
+    u = rng.standard_normal(4096).astype(np.float32)
+    h = orc.silu_mul(g, u)
+    gd = g.astype(np.float64)
+    silu = (gd / (1 + np.exp(-gd))).astype(np.float32)
+    assert np.array_equal(bits(h), bits((silu * u).astype(np.float32)))
+    assert orc.silu_mul(np.float32([0.0]), np.float32([3.0]))[0] == 0.0
+    big = orc.silu_mul(np.float32([30.0]), np.float32([1.0]))[0]
+    assert abs(big - 30.0) < 1e-5
+
+
+def test_gelu_closed_forms(orc):
+    x = np.linspace(-6, 6, 2001).astype(np.float32)
+    y = orc.gelu(x).astype(np.float64)
+    exact = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in x.astype(np.float64)])
+    # A&S 7.1.26 has |error| <= 1.5e-7 in erf
+    assert np.all(np.abs(y - exact) <= 0.5 * np.abs(x) * 1.6e-7 + 6e-8 * np.abs(exact) + 1e-30)
+    assert orc.gelu(np.float32([0.0]))[0] == 0.0
+    # gelu(x) - gelu(-x) = x (erf is odd)
+    assert np.allclose(orc.gelu(x) - orc.gelu(-x), x, atol=2e-6)
+
+
+@pytest.mark.skipif(not O.reference_available(), reason="oracle/_ref not built (no reference)")
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_oracle_matches_compiled_reference(orc, fmt):
+    ref = O.Reference()
+    rng = np.random.default_rng(21)
+    for rows, cols, n in [(37, 2048, 3), (130, 1152, 2), (8, 6144, 1), (64, 4320, 4)]:
+        w = (rng.random((rows, cols), dtype=np.float32) - 0.5).astype(np.float32)
+        xs = rng.standard_normal((n, cols), dtype=np.float32)
+        if fmt == "q8":
+            qs, sc = ref.quantize_q8(w)
+            q2, s2 = orc.quantize_q8(w)
+            assert np.array_equal(qs, q2) and np.array_equal(bits(sc), bits(s2))
+            for mode in (0, 1):
+                a = ref.gemm_q8(qs, sc, xs, n, threads=4, mode=mode)
+                b = orc.gemm_q8(qs, sc, xs, n, threads=2, mode=mode)
+                assert np.array_equal(bits(a), bits(b))
+        else:
+            qs, sc = ref.quantize_q4(w)
+            q2, s2 = orc.quantize_q4(w)
+            assert np.array_equal(qs, q2) and np.array_equal(sc, s2)
+            for mode in (0, 1):
+                a = ref.gemm_q4(qs, sc, xs, n, threads=4, mode=mode)
+                b = orc.gemm_q4(qs, sc, xs, n, threads=2, mode=mode)
+                assert np.array_equal(bits(a), bits(b))
