@@ -221,10 +221,12 @@ class GpuLinear:
         self._finish()
         ys.reshape(-1)[: n * d_m.rows] = y.view(count=n * d_m.rows)
 
-    def gelu_pair(self, fc1: str, fc2: str, xs: np.ndarray, ys: np.ndarray, n: int) -> None:
+    def gelu_pair(self, fc1: str, fc2: str, xs: np.ndarray, ys: np.ndarray, n: int,
+                  intermediate: np.ndarray | None = None) -> None:
         """fc2(GELU(fc1 xs)), the projector's linear_1 -> GELU -> linear_2
         (vision_encoder.dart:252-271) without biases. fc1's rows may carry
-        zero padding up to fc2's padded width."""
+        zero padding up to fc2's padded width. ``intermediate`` receives
+        GELU(fc1 xs) ([n][fc1 rows]) when given."""
         self._check_open()
         a, b = self._matrix(fc1), self._matrix(fc2)
         if a.rows != b.cols:
@@ -242,6 +244,8 @@ class GpuLinear:
         b.encode(self._lib, h.handle, y.handle, 0, n)
         self._finish()
         ys.reshape(-1)[: n * b.rows] = y.view(count=n * b.rows)
+        if intermediate is not None:
+            intermediate.reshape(-1)[: n * a.rows] = h.view(count=n * a.rows)
 
     # ------------------------------------------------------------ lifecycle
 

@@ -167,15 +167,23 @@ def test_config4_vision_pair(gpu, orc):
     assert np.array_equal(g1[:4304], q1) and np.array_equal(bits(h1[:4304]), bits(s1))
     assert not g1[4304:].any() and not h1[4304:].any()
     assert np.array_equal(g2, q2) and np.array_equal(bits(h2), bits(s2))
+    # Stage-wise, as the glue's parity is: each stage's CPU reference takes
+    # the GPU's own input to that stage (a 1-ulp difference upstream can move
+    # a value across a Q8 rounding boundary of the next input quantizer).
     y = np.zeros(1024 * 1152, np.float32)
-    gpu.gelu_pair("fc1", "fc2", x, y, 1024)
-    # stage-wise CPU chain: fc1 (mode 1) -> GELU (double) -> pad -> fc2
-    a = orc.gemm_q8(q1, s1, x, 1024, threads=8, mode=1)
-    h = np.zeros((1024, 4320), np.float32)
-    h[:, :4304] = orc.gelu(a)
-    ref = orc.gemm_q8(q2, s2, h, 1024, threads=8, mode=1)
+    h = np.zeros(1024 * 4320, np.float32)
+    gpu.gelu_pair("fc1", "fc2", x, y, 1024, intermediate=h)
+    h = h.reshape(1024, 4320)
+    a = np.zeros(1024 * 4320, np.float32)
+    gpu.apply("fc1", x, a, 1024)
+    a = a.reshape(1024, 4320)
+    ok, rel, ab = within_tolerance(a[:, :4304], orc.gemm_q8(q1, s1, x, 1024, threads=8, mode=1))
+    assert ok, ("fc1", rel, ab)
+    assert not a[:, 4304:].any()
+    assert np.array_equal(bits(h), bits(orc.gelu(a)))          # GELU stage, bit-exact
+    ref = orc.gemm_q8(q2, s2, h, 1024, threads=8, mode=1)       # fc2 stage
     ok, rel, ab = within_tolerance(y.reshape(1024, 1152), ref)
-    assert ok, (rel, ab)
+    assert ok, ("fc2", rel, ab)
 
 
 def test_profile_and_device_queries(gpu, orc):
@@ -204,7 +212,7 @@ def test_invalid_dispatch_fails_its_commit(gpu_ready):
     h = lib.lab_gpu_buffer(1024)
     try:
         lib.lab_gpu_begin()
-        lib.lab_gpu_enc_matmul_q8(h, 0, 512, h, 0, h, 0, 4, 96, 1)  # out of bounds
+        lib.lab_gpu_enc_matmul_q8(h, 0, 512, h, 0, h, 0, 64, 96, 1)  # qs past the end
         assert lib.lab_gpu_commit(1) == 0
         lib.lab_gpu_begin()
         assert lib.lab_gpu_commit(1) == 1
