@@ -13,9 +13,12 @@ them (HBM-cold). The other configurations (Q8 GEMV, LM head + argmax,
 prefill GEMM, BF16 -> Q8 + vision pair, the M = 1..64 sweep) are reported
 under ``configs``; the prefill GEMM gives the metric's TOPS half.
 
-``roofline`` is for the dominant kernel of the headline step (the Q4 GEMV):
-algorithmic bytes per launch / its mean launch time from HIP events on the
-stream it runs on. ``traffic`` comes from rocprofv3 FETCH_SIZE / WRITE_SIZE
+Timed regions are GPU time: the K steps are captured into one HIP graph and
+its replay is bracketed by HIP events on the launch stream (host-driven
+launches from Python cost more than the kernels; that figure is reported as
+``eager_host_driven_ms_per_step``). ``roofline`` is for the dominant kernel
+of the headline step (the fused gate/up Q4 GEMV): algorithmic bytes per
+launch / its mean launch time. ``traffic`` comes from rocprofv3 FETCH_SIZE / WRITE_SIZE
 runs committed under profiles/ (null when absent). ``cpu_baseline`` times the
 reference's own CPU kernels (oracle/_ref, built from src/c/lab_native.c) on
 this host over a bounded sample of the same workload.
@@ -53,12 +56,46 @@ def copies_for(nbytes):
 
 
 class Timer:
-    """Events on torch's current stream, which the launchers enqueue on."""
+    """Times launches on the GPU, not on the host: the K timed launches are
+    captured once into a HIP graph (torch's capture, on the stream the
+    launchers enqueue on) and the graph's replay is bracketed by HIP events
+    on that stream. Eager launches from Python cost ~7 us of host time each,
+    more than most of these kernels take on the GPU."""
 
     def __init__(self, torch):
         self.torch = torch
 
+    def graph(self, fn, steps):
+        torch = self.torch
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                fn(i)
+        return g
+
     def time(self, fn, steps, warmup):
+        """Mean ms per step over `steps` steps replayed from one graph."""
+        torch = self.torch
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        g = self.graph(fn, steps)
+        g.replay()  # warm replay
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        g.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps
+
+    def kernel_means(self, launches, steps):
+        """Mean duration of each launch kind: a graph of `steps` launches of
+        that kernel alone, replayed between events."""
+        return [self.time(fn, steps, 2) for fn in launches]
+
+    def eager(self, fn, steps, warmup):
+        """Host-driven launches (includes the host's launch cost)."""
         torch = self.torch
         for i in range(warmup):
             fn(i)
@@ -69,22 +106,7 @@ class Timer:
             fn(i)
         stop.record()
         torch.cuda.synchronize()
-        return start.elapsed_time(stop) / steps  # ms per step
-
-    def kernel_means(self, launches, steps):
-        """Mean duration of each launch in a step: events between launches."""
-        torch = self.torch
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)]
-              for _ in range(steps)]
-        torch.cuda.synchronize()
-        for s in range(steps):
-            ev[s][0].record()
-            for k, fn in enumerate(launches):
-                fn(s)
-                ev[s][k + 1].record()
-        torch.cuda.synchronize()
-        return [float(np.mean([ev[s][k].elapsed_time(ev[s][k + 1]) for s in range(steps)]))
-                for k in range(len(launches))]
+        return start.elapsed_time(stop) / steps
 
 
 def dev(torch, a):
@@ -94,6 +116,8 @@ def dev(torch, a):
 # ------------------------------------------------------------------ configs
 
 def bench_c1(torch, D, synth, timer, steps, warmup):
+    """Config 1 as two launches: gate + up + SiLU glue in one pass over x,
+    then the down GEMV (its prologue quantizes h)."""
     (gq, gs), (uq, us), (dq, ds), x = synth.config1()
     per_set = 2 * q4_bytes(6144, 2048) + q4_bytes(2048, 6144)
     copies = copies_for(per_set)
@@ -101,44 +125,48 @@ def bench_c1(torch, D, synth, timer, steps, warmup):
     for c in range(copies):
         sets.append(tuple(dev(torch, a) for a in (gq, gs, uq, us, dq, ds)))
     xd = dev(torch, x)
+    h = torch.empty(6144, device="cuda")
     g = torch.empty(6144, device="cuda")
     u = torch.empty(6144, device="cuda")
     y = torch.empty(2048, device="cuda")
 
-    def gate(i):
+    def gate_up(i):
         s = sets[i % copies]
-        D.gemv_q4(s[0], s[1], xd, g, 6144, 2048, 1)
-
-    def up(i):
-        s = sets[i % copies]
-        D.gemv_q4(s[2], s[3], xd, u, 6144, 2048, 1)
-
-    def glue(i):
-        D.swiglu(g, u)
+        D.gate_up_q4(s[0], s[1], s[2], s[3], xd, h, 6144, 2048, 1)
 
     def down(i):
         s = sets[i % copies]
-        D.gemv_q4(s[4], s[5], g, y, 2048, 6144, 1)
+        D.gemv_q4(s[4], s[5], h, y, 2048, 6144, 1)
 
     def step(i):
-        gate(i)
-        up(i)
-        glue(i)
+        gate_up(i)
         down(i)
 
     ms = timer.time(step, steps, warmup)
     algo = per_set + (2048 * 4) * 2 + 6144 * 4 + 2 * 6144 * 4 + 2048 * 4
-    means = timer.kernel_means([gate, up, glue, down], min(steps, 200))
-    gemv_ms = (means[0] + means[1] + means[3]) / 3
-    gemv_bytes = q4_bytes(6144, 2048) + 2048 * 4 + 6144 * 4  # gate/up/down move the same
+    means = timer.kernel_means([gate_up, down], min(steps, 200))
+    gu_bytes = 2 * q4_bytes(6144, 2048) + 2048 * 4 + 6144 * 4
     resident = timer.time(lambda i: step(0), steps, warmup)
+
+    # The same step unfused (four launches), for comparison.
+    def unfused(i):
+        s = sets[i % copies]
+        D.gemv_q4(s[0], s[1], xd, g, 6144, 2048, 1)
+        D.gemv_q4(s[2], s[3], xd, u, 6144, 2048, 1)
+        D.swiglu(g, u)
+        D.gemv_q4(s[4], s[5], g, y, 2048, 6144, 1)
+
+    unfused_ms = timer.time(unfused, steps, warmup)
+    eager_ms = timer.eager(step, steps, warmup)
     return {
         "ms_per_step": ms, "bytes_per_step": algo, "gbps": algo / ms / 1e6,
-        "weight_copies": copies, "kernel_ms": {"gemv_q4_gate": means[0], "gemv_q4_up": means[1],
-                                               "swiglu": means[2], "gemv_q4_down": means[3]},
-        "gemv_mean_ms": gemv_ms, "gemv_bytes_per_launch": gemv_bytes,
-        "gemv_gbps": gemv_bytes / gemv_ms / 1e6,
+        "weight_copies": copies,
+        "kernel_ms": {"gate_up_silu_q4": means[0], "gemv_q4_down": means[1]},
+        "gate_up_bytes_per_launch": gu_bytes, "gate_up_gbps": gu_bytes / means[0] / 1e6,
+        "down_gbps": (q4_bytes(2048, 6144) + 6144 * 4 + 2048 * 4) / means[1] / 1e6,
         "resident_gbps": algo / resident / 1e6,
+        "unfused_ms_per_step": unfused_ms, "unfused_gbps": algo / unfused_ms / 1e6,
+        "eager_host_driven_ms_per_step": eager_ms,
     }
 
 
@@ -162,6 +190,7 @@ def bench_c0(torch, D, synth, timer, steps, warmup):
 
 
 def bench_c2(torch, D, synth, timer, steps, warmup):
+    """Config 2: the LM-head GEMV with the greedy argmax fused into it."""
     qs, sc, x = synth.config2()
     copies = 2
     ws = [(dev(torch, qs), dev(torch, sc)) for _ in range(copies)]
@@ -169,28 +198,19 @@ def bench_c2(torch, D, synth, timer, steps, warmup):
     xd = dev(torch, x)
     y = torch.empty(151936, device="cuda")
     out = torch.empty(1, dtype=torch.int64, device="cuda")
-    wsp = D.argmax_workspace(151936)
-
-    def gemv(i):
-        q, s = ws[i % copies]
-        D.gemv_q8(q, s, xd, y, 151936, 2048, 1)
-
-    def amax(i):
-        D.argmax(y, out, wsp)
+    wsp = D.gemv_argmax_workspace()
 
     def step(i):
-        gemv(i)
-        amax(i)
+        q, s = ws[i % copies]
+        D.gemv_q8_argmax(q, s, xd, y, out, wsp, 151936, 2048)
 
-    n = max(10, steps // 4)
-    ms = timer.time(step, n, max(2, warmup // 4))
+    n = max(20, steps // 2)
+    ms = timer.time(step, n, max(2, warmup // 2))
     algo = q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4
-    means = timer.kernel_means([gemv, amax], n)
-    gemv_algo = q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4
+    resident = timer.time(lambda i: step(0), n, 2)
     return {"ms": ms, "gbps": algo / ms / 1e6, "frac_hbm": algo / ms / 1e6 / HBM_PEAK_GBS,
-            "gemv_ms": means[0], "argmax_ms": means[1],
-            "gemv_gbps": gemv_algo / means[0] / 1e6,
-            "gemv_frac_hbm": gemv_algo / means[0] / 1e6 / HBM_PEAK_GBS, "weight_copies": copies}
+            "kernel": "gemv_q8 + fused argmax", "weight_copies": copies,
+            "resident_gbps": algo / resident / 1e6}
 
 
 def bench_c3(torch, D, synth, timer, steps, warmup):
@@ -330,6 +350,34 @@ def traffic_from_profiles():
         return None
 
 
+def check_graph_replay(torch, D, synth):
+    """A graph replay gives the same bits as eager launches (checked once,
+    on config 1's step, with eager work and syncs between replays)."""
+    (gq, gs), (uq, us), (dq, ds), x = synth.config1()
+    t = [dev(torch, a) for a in (gq, gs, uq, us, dq, ds)]
+    xd = dev(torch, x)
+    h = torch.empty(6144, device="cuda")
+    y = torch.empty(2048, device="cuda")
+
+    def step(i):
+        D.gate_up_q4(t[0], t[1], t[2], t[3], xd, h, 6144, 2048, 1)
+        D.gemv_q4(t[4], t[5], h, y, 2048, 6144, 1)
+
+    step(0)
+    torch.cuda.synchronize()
+    want = y.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step(0)
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(y, want):
+            raise RuntimeError("graph replay differs from eager launches")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -352,6 +400,7 @@ def main():
         print("bench.py needs the GPU", file=sys.stderr)
         sys.exit(1)
     timer = Timer(torch)
+    check_graph_replay(torch, D, synth)
     print(f"bench: config 1 (steps={args.steps}, warmup={args.warmup})", file=sys.stderr, flush=True)
     c1 = bench_c1(torch, D, synth, timer, args.steps, args.warmup)
     configs = {"c1_q4_mlp": c1}
@@ -366,7 +415,7 @@ def main():
         print("bench: cpu baseline", file=sys.stderr, flush=True)
         cpu = cpu_baseline(synth, args.cpu_seconds)
 
-    achieved = c1["gemv_gbps"]
+    achieved = c1["gate_up_gbps"]
     line = {
         "metric": METRIC,
         "value": round(c1["gbps"], 2),
@@ -384,12 +433,12 @@ def main():
                    "down": [2048, 6144], "weights": "Q4_0", "weight_copies": c1["weight_copies"],
                    "frac_hbm": round(c1["gbps"] / HBM_PEAK_GBS, 4),
                    "resident_gbps_mall": round(c1["resident_gbps"], 2)},
-        "roofline": {"bound": "hbm", "kernel": "gemv_q4 (gate/up/down, mean)",
+        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<Q4> gate+up pair with SiLU glue",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles(),
-                     "bytes_per_launch": c1["gemv_bytes_per_launch"],
-                     "launch_ms": round(c1["gemv_mean_ms"], 6)},
+                     "bytes_per_launch": c1["gate_up_bytes_per_launch"],
+                     "launch_ms": round(c1["kernel_ms"]["gate_up_silu_q4"], 6)},
         "cpu_baseline": cpu,
         "configs": configs,
     }

@@ -72,10 +72,75 @@ DNX_DEV float max4abs(float4 v) {
   return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte load marked non-temporal: weights are streamed once, so they
+// should not displace the inputs other workgroups still reuse.
+DNX_DEV uint4 load_stream16(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Raw buffer loads (gfx9 MUBUF): a 128-bit resource in SGPRs holds a base
+// address and a byte range; a lane whose offset falls outside the range
+// reads zeros without touching memory. That makes bounds checks free and
+// branch-free, so the compiler can count outstanding loads exactly.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ i32x4 dnx_raw_buffer_load_v4i32(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+__device__ int dnx_raw_buffer_load_i32(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.i32");
+__device__ short dnx_raw_buffer_load_i16(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.i16");
+
+constexpr int kBufferFlags = 0x00020000;  // gfx9 resource word 3: 32-bit raw data
+
+// A resource for [base, base + bytes). Every field is made wave-uniform.
+DNX_DEV i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));  // stride 0
+  r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+  r.w = kBufferFlags;
+  return r;
+}
+
+DNX_DEV uint4 buffer_load16(i32x4 rsrc, int offset) {
+  const i32x4 v = dnx_raw_buffer_load_v4i32(rsrc, offset, 0, 0);
+  return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+
+DNX_DEV float4 buffer_load_f4(i32x4 rsrc, int offset) {
+  const i32x4 v = dnx_raw_buffer_load_v4i32(rsrc, offset, 0, 0);
+  return make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z),
+                     __int_as_float(v.w));
+}
+
 DNX_DEV float bf16_to_float(uint16_t p) { return __uint_as_float((uint32_t)p << 16); }
 
 DNX_DEV float half_bits_to_float(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// argmaxToken (lib/src/sampler.dart:137-143): the first index of the
+// maximum. A value becomes an order-preserving key (-0 == +0, NaN below
+// everything) packed with the complemented index, so that one unsigned max
+// picks the largest value and, on a tie, the lowest index.
+DNX_DEV uint64_t argmax_key(float v, uint32_t i) {
+  uint32_t b = __float_as_uint(v);
+  if (v == 0.0f) b = 0;  // -0 ties with +0
+  uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  if (v != v) ord = 0;   // NaN never wins
+  return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - i);
+}
+
+DNX_DEV uint64_t wave_max_u64(uint64_t k) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = __shfl_xor(k, off);
+    k = o > k ? o : k;
+  }
+  return k;
 }
 
 }  // namespace dnx

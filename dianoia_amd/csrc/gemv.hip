@@ -1,0 +1,547 @@
+// Exact-order decode GEMV on gfx950 for the engine's Q8 and Q4 weights.
+//
+// y[t][r] = (W x[t])[r] for n <= 4 tokens, computed in the float order of
+// the reference CPU kernels (dot_q8_sdot lab_native.c:503-512, dot_q4_sdot
+// :1025-1034, lane_sum :209-212): per 32-block, four exact int32 lane sums
+// d_l over bytes {4l..4l+3, 16+4l..19+4l}; s = sw * sx rounded;
+// acc_l = fma(float(d_l), s, acc_l), block after block; y = (acc0 + acc1) +
+// (acc2 + acc3). The logits are therefore bit-identical to lab_gemm_q8 /
+// lab_gemm_q4 mode 1, and so is their greedy argmax.
+//
+// Work decomposition (HBM streaming on 256 CUs):
+// * A workgroup is 4 independent waves. Each wave owns tiles of R weight
+//   rows, taken round-robin over a persistent grid sized to what stays
+//   resident, so each workgroup quantizes x once and then streams.
+// * A tile is read in 1 KB chunks per row (32 Q8 blocks or 64 Q4 blocks):
+//   one wave instruction loads 1 KB of one row with 16-byte lanes. Loads go
+//   through a ring of 16 units (row-chunks; 8 for one-row tiles) per wave:
+//   the next ring slots are refilled as soon as a chunk is turned into lane
+//   sums, so about 16 KB per wave stays in flight while the wave runs its
+//   FMA chains. The first
+//   chunks are requested while the prologue quantizes x, so the two
+//   latencies overlap.
+// * Lane sums (as floats; exact below 2^24) and per-block scales go to the
+//   wave's own LDS; lanes (t, row, l) then run the chunk's FMA chains and a
+//   DPP lane combine gives each row.
+// * Fusions: the gate/up pair of an MLP shares x and finishes with the
+//   SiLU(gate) * up glue (shard.dart:457-461); an LM head can finish with
+//   the greedy argmax (sampler.dart:137-143) reduced across the grid with
+//   64-bit atomics, the last wave to finish writing the token.
+
+#include "common.h"
+#include "dnx_kernels.h"
+
+using namespace dnx;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+// Fused argmax. A rank orders (value, lowest index): the 32-bit value key
+// of argmax_key above 20 bits of complemented row index (rows < 2^20). A
+// workspace word holds an arrival count above a 52-bit rank. Workspace: 32
+// group words 16 words (128 B) apart, then the top word.
+constexpr int kIndexBits = 20;
+constexpr uint64_t kIndexMask = (1ull << kIndexBits) - 1;
+constexpr int kRankBits = 32 + kIndexBits;
+constexpr uint64_t kRankMask = (1ull << kRankBits) - 1;
+constexpr int kArgmaxGroups = 32;
+constexpr int kArgmaxTop = kArgmaxGroups * 16;
+constexpr int kArgmaxMaxGrid = 4096;  // arrivals per word stay below 2^12
+
+DNX_DEV uint64_t argmax_rank(float v, uint32_t row) {
+  const uint64_t key = argmax_key(v, row);  // value order << 32 | ~row
+  uint64_t rank = ((key >> 32) << kIndexBits) | (kIndexMask - row);
+  // A NaN at index 0 is the answer whatever follows (every comparison with
+  // it is false): give it the one rank no value reaches.
+  if (row == 0 && v != v) rank = kRankMask;
+  return rank;
+}
+
+// One arrival at a workspace word: count + 1, rank = max(rank, r). Returns
+// the word after this arrival.
+DNX_DEV uint64_t arrive(unsigned long long* word, uint64_t r) {
+  unsigned long long old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  unsigned long long next;
+  do {
+    const uint64_t best = (old & kRankMask) > r ? (old & kRankMask) : r;
+    next = (((old >> kRankBits) + 1) << kRankBits) | best;
+  } while (!__hip_atomic_compare_exchange_strong(word, &old, next, __ATOMIC_RELAXED,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  return next;
+}
+
+struct GemvParams {
+  const void* qs[2];
+  const void* scales[2];
+  const float* x;              // [n][cols] fp32
+  float* y;                    // [n][rows]; the pair writes SiLU(gate) * up
+  float* y2;                   // pair: the up products too, when not null
+  int rows, cols, n;
+  int tiles;                   // ceil(rows / R)
+  int full;                    // 1: a tile's whole K goes to LDS before its chains run
+  int stride;                  // LDS floats per chain: span of blocks + 4
+  unsigned long long* ws;      // argmax: {key, finished waves}, zero between calls
+  int64_t* amax_out;
+};
+
+// Orders LDS writes and reads among the lanes of one wave (a wave's LDS
+// operations execute in issue order; this keeps the compiler from moving
+// them across).
+DNX_DEV void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// SiLU(g) * u as the CPU glue rounds it: SiLU in double, stored to float,
+// then one float multiply (the exact double product rounded once).
+DNX_DEV float silu_mul(float g, float u) {
+  const double a = (double)g;
+  const float s = (float)(a / (1.0 + exp(-a)));
+  return s * u;
+}
+
+template <bool kQ4, int R, int NT, bool kPair, bool kArgmax>
+__global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
+  constexpr int CB = kQ4 ? 64 : 32;           // blocks per 1 KB chunk of a row
+  constexpr int M = kPair ? 2 : 1;            // matrices sharing x
+  constexpr int RR = R * M;                   // weight rows per tile
+  constexpr int CH = NT * RR * 4;             // chain lanes per tile
+  static_assert(CH <= 64, "a tile's chains must fit one wave");
+  constexpr int G = RR >= 16 ? 1 : RR >= 2 ? 16 / RR : 8;  // chunk groups per ring batch
+  constexpr int Q = RR * G;                   // ring slots (row-chunks in flight)
+
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int cols = p.cols, B = cols / kBlock, n = p.n;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar bookkeeping
+
+  int8_t* sxq = (int8_t*)lds;                              // [NT][cols]
+  float* sxs = (float*)(lds + NT * cols);                  // [NT][B]
+  int* sxsum = (int*)(sxs + ((NT * B + 3) & ~3));          // Q4: [NT][B][4]
+  const int CP = p.stride;  // floats per chain: a chunk (or the whole K) + 4
+  float* sf = (float*)(sxsum + (kQ4 ? NT * B * 4 : 0)) + wave * (NT * RR * 5 * CP);
+  float* ss = sf + NT * RR * 4 * CP;                       // [NT][RR][CP]
+
+  const int chunks = (B + CB - 1) / CB;
+  const int stride = gridDim.x * kWaves;
+  const int tile0 = blockIdx.x * kWaves + wave;
+  const int my_tiles = tile0 < p.tiles ? (p.tiles - 1 - tile0) / stride + 1 : 0;
+  const int groups = my_tiles * chunks;                    // chunk groups of this wave
+  const int lblk = kQ4 ? lane : (lane >> 1);               // lane's block in a chunk
+
+  uint4 raw[Q];
+  uint32_t swb[Q];  // scale bits (fp16 or fp32), converted when used: a
+                    // conversion here would wait for the load at once
+
+  // Requests the RR row-chunks of chunk c of this wave's k-th tile into ring
+  // slots [s0, s0 + RR) with buffer loads bounded by the row: blocks past
+  // the row, rows past the matrix and tiles past this wave's last read as
+  // zeros without a memory access (their results are never stored), so the
+  // issue has no branch.
+  auto issue = [&](const int s0, const int k, const int c) {
+    const int tile = tile0 + k * stride;
+    const int blk = c * CB + lblk;
+#pragma unroll
+    for (int i = 0; i < RR; i++) {
+      const int m = i / R, r = i - (i / R) * R;
+      const int row = tile * R + r;
+      const bool live = k < my_tiles && row < p.rows;
+      if (kQ4) {
+        const i32x4 rq = buffer_rsrc((const uint8_t*)p.qs[m] + (size_t)row * (cols / 2),
+                                     live ? (uint32_t)(cols / 2) : 0u);
+        const i32x4 rs = buffer_rsrc((const uint16_t*)p.scales[m] + (size_t)row * B,
+                                     live ? (uint32_t)(B * 2) : 0u);
+        raw[s0 + i] = buffer_load16(rq, blk * 16);
+        swb[s0 + i] = (uint16_t)dnx_raw_buffer_load_i16(rs, blk * 2, 0, 0);
+      } else {
+        const i32x4 rq = buffer_rsrc((const int8_t*)p.qs[m] + (size_t)row * cols,
+                                     live ? (uint32_t)cols : 0u);
+        const i32x4 rs = buffer_rsrc((const float*)p.scales[m] + (size_t)row * B,
+                                     live ? (uint32_t)(B * 4) : 0u);
+        raw[s0 + i] = buffer_load16(rq, blk * 32 + (lane & 1) * 16);
+        swb[s0 + i] = (uint32_t)dnx_raw_buffer_load_i32(rs, blk * 4, 0, 0);
+      }
+    }
+  };
+  // Next chunk group: the following chunk of the tile, or the next tile.
+  auto advance = [&](int& k, int& c) {
+    if (++c == chunks) {
+      c = 0;
+      ++k;
+    }
+  };
+
+  // Prologue: the n input rows quantized into LDS (lab_quantize_q8, fused).
+  // The first batch of x is requested before the first weight chunks (loads
+  // complete in order, so x must not queue behind the weights), then the
+  // weight ring is filled, then x is quantized while the weights stream.
+  // Rows of tokens t >= n are never stored, so their LDS is left as is.
+  constexpr int PQ = 8;  // x quads per thread per batch
+  const int quads = cols / 4;
+  float4 v[PQ];
+  auto load_x = [&](const int t, const int q0) {
+    const i32x4 rx = buffer_rsrc(p.x + (size_t)t * cols, (uint32_t)cols * 4);
+#pragma unroll
+    for (int j = 0; j < PQ; j++) {
+      const int q = q0 + j * kThreads + tid;  // past the row: zeros, unused
+      v[j] = buffer_load_f4(rx, q * 16);
+    }
+  };
+  load_x(0, 0);
+  int pk = 0, pc = 0;  // position of the next chunk group to request
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    issue(g * RR, pk, pc);
+    advance(pk, pc);
+  }
+  auto quantize_x = [&](const int t, const int q0) {
+#pragma unroll
+    for (int j = 0; j < PQ; j++) {
+      const int q = q0 + j * kThreads + tid;
+      if (q >= quads) break;  // whole 8-lane groups: quads is a multiple of 8
+      const int c = q * 4;
+      const float amax = group8_max(fmaxf(0.0f, max4abs(v[j])));
+      const float scale = q8_scale(amax);
+      const int packed = quant4(v[j], q8_inv(scale));
+      *(int*)(sxq + t * cols + c) = packed;
+      const int jq = q & 7;  // quad within the block
+      if (jq == 0) sxs[t * B + (q >> 3)] = scale;
+      if (kQ4) {
+        // -8 * (sum of the x bytes meeting lane l's low and high nibbles):
+        // quads l and l + 4 of the block, so the nibbles enter sdot as 0..15.
+        const int s = sdot4(packed, 0x01010101, 0);
+        const int other = __builtin_amdgcn_ds_swizzle(s, 0x101F);  // lane ^ 4
+        if (jq < 4) sxsum[(t * B + (q >> 3)) * 4 + jq] = -8 * (s + other);
+      }
+    }
+  };
+  // The first batch straight after the ring is filled (no loop around it,
+  // so waiting for x does not wait for the weights behind it).
+  quantize_x(0, 0);
+  for (int t = 0; t < n; t++) {
+    for (int q0 = t == 0 ? kThreads * PQ : 0; q0 < quads; q0 += kThreads * PQ) {
+      load_x(t, q0);
+      quantize_x(t, q0);
+    }
+  }
+  __syncthreads();  // the only workgroup barrier: x is ready
+
+  float acc = 0.0f;
+  uint64_t best = 0;
+  int ck = 0, cc = 0;  // position of the chunk group being consumed
+  for (int base = 0; base < groups; base += G) {
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      if (base + g >= groups) break;  // uniform across the wave
+      const int tile = tile0 + ck * stride;
+      const int nb = min(CB, B - cc * CB), nb4 = (nb + 3) & ~3;
+      const bool ok = lblk < nb, pad = !ok && lblk < nb4;
+      const int blk = cc * CB + (ok ? lblk : 0);
+      const int at = p.full ? cc * CB + lblk : lblk;  // block slot in this chain's LDS
+      // Row-chunks -> lane sums and block scales in LDS.
+#pragma unroll
+      for (int i = 0; i < RR; i++) {
+        const uint4 w = raw[g * RR + i];
+        const float swi = kQ4 ? half_bits_to_float((uint16_t)swb[g * RR + i])
+                              : __uint_as_float(swb[g * RR + i]);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          float* f = sf + ((t * RR + i) * 4) * CP + at;
+          float* sp = ss + (t * RR + i) * CP + at;
+          if (kQ4) {
+            const int4 xa = *(const int4*)(sxq + t * cols + blk * 32);
+            const int4 xb = *(const int4*)(sxq + t * cols + blk * 32 + 16);
+            const int4 c8 = *(const int4*)(sxsum + (t * B + blk) * 4);
+            const int mk = 0x0f0f0f0f;
+            const int d0 = sdot4(w.x & mk, xa.x, sdot4((w.x >> 4) & mk, xb.x, c8.x));
+            const int d1 = sdot4(w.y & mk, xa.y, sdot4((w.y >> 4) & mk, xb.y, c8.y));
+            const int d2 = sdot4(w.z & mk, xa.z, sdot4((w.z >> 4) & mk, xb.z, c8.z));
+            const int d3 = sdot4(w.w & mk, xa.w, sdot4((w.w >> 4) & mk, xb.w, c8.w));
+            if (ok) {
+              f[0] = (float)d0;
+              f[CP] = (float)d1;
+              f[2 * CP] = (float)d2;
+              f[3 * CP] = (float)d3;
+              *sp = swi * sxs[t * B + blk];
+            } else if (pad) {
+              f[0] = 0.0f;
+              f[CP] = 0.0f;
+              f[2 * CP] = 0.0f;
+              f[3 * CP] = 0.0f;
+              *sp = 0.0f;
+            }
+          } else {
+            const int h = lane & 1;
+            const int4 xv = *(const int4*)(sxq + t * cols + blk * 32 + h * 16);
+            int p0 = sdot4(w.x, xv.x, 0), p1 = sdot4(w.y, xv.y, 0);
+            int p2 = sdot4(w.z, xv.z, 0), p3 = sdot4(w.w, xv.w, 0);
+            // Lane l's sum takes 4 bytes of each half: add the partner's.
+            p0 += dpp<kQuadXor1>(p0);
+            p1 += dpp<kQuadXor1>(p1);
+            p2 += dpp<kQuadXor1>(p2);
+            p3 += dpp<kQuadXor1>(p3);
+            float* fh = f + 2 * h * CP;
+            if (ok) {
+              fh[0] = (float)(h ? p2 : p0);
+              fh[CP] = (float)(h ? p3 : p1);
+              if (h == 0) *sp = swi * sxs[t * B + blk];
+            } else if (pad) {
+              fh[0] = 0.0f;
+              fh[CP] = 0.0f;
+              if (h == 0) *sp = 0.0f;
+            }
+          }
+        }
+      }
+      // Refill these ring slots with the chunk group one batch ahead.
+      issue(g * RR, pk, pc);
+      advance(pk, pc);
+      if (!p.full || cc == chunks - 1) {
+        // The FMA chains, in block order: over this chunk, or (full-K tiles)
+        // over the whole row at its last chunk.
+        const int end = p.full ? cc * CB + nb4 : nb4;
+        wave_sync();
+        if (lane < CH) {
+          const float* fp = sf + lane * CP;
+          const float* sp = ss + (lane >> 2) * CP;
+#pragma unroll 4
+          for (int b = 0; b < end; b += 4) {
+            const float4 fv = *(const float4*)(fp + b);
+            const float4 sv = *(const float4*)(sp + b);
+            acc = fmaf(fv.x, sv.x, acc);
+            acc = fmaf(fv.y, sv.y, acc);
+            acc = fmaf(fv.z, sv.z, acc);
+            acc = fmaf(fv.w, sv.w, acc);
+          }
+        }
+        wave_sync();
+      }
+      if (cc == chunks - 1) {
+        // (acc0 + acc1) + (acc2 + acc3) over each group of 4 chain lanes.
+        float v = acc + dppf<kQuadXor1>(acc);
+        v = v + dppf<kQuadXor2>(v);
+        acc = 0.0f;
+        const int tr = lane >> 2, t = tr / RR, i = tr - (tr / RR) * RR;
+        const int row = tile * R + (i % R);
+        const bool lead = lane < CH && (lane & 3) == 0 && t < n && row < p.rows;
+        if (kPair) {
+          const float up = __shfl(v, lane + R * 4);  // the up row of this gate row
+          if (lead && i < R) p.y[(size_t)t * p.rows + row] = silu_mul(v, up);
+          if (lead && i >= R && p.y2 != nullptr) p.y2[(size_t)t * p.rows + row] = v;
+        } else {
+          if (lead) p.y[(size_t)t * p.rows + row] = v;
+          if (kArgmax) {
+            const uint64_t key = lead ? argmax_rank(v, (uint32_t)row) : 0;
+            const uint64_t m = wave_max_u64(key);
+            best = m > best ? m : best;
+          }
+        }
+      }
+      advance(ck, cc);
+    }
+  }
+
+  if (kArgmax) {
+    // Grid-wide (max, lowest index) through the atomic words alone, so no
+    // memory fence is needed: each workgroup folds its waves' ranks, then
+    // CAS-updates one of 32 group words (separate cache lines) holding an
+    // arrival count and the group's best rank; the last arrival of a group
+    // carries that rank to the top word the same way, and the last arrival
+    // there writes the token. Every word is reset by its last arrival.
+    __shared__ uint64_t red[kWaves];
+    if (lane == 0) red[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t b = red[0];
+      for (int w = 1; w < kWaves; w++) b = red[w] > b ? red[w] : b;
+      const int grp = blockIdx.x % kArgmaxGroups;
+      const uint64_t in_grp = (gridDim.x - 1 - grp) / kArgmaxGroups + 1;
+      const uint64_t groups = gridDim.x < kArgmaxGroups ? gridDim.x : kArgmaxGroups;
+      const uint64_t got = arrive(&p.ws[grp * 16], b);
+      if ((got >> kRankBits) == in_grp) {
+        atomicExch(&p.ws[grp * 16], 0ull);
+        const uint64_t all = arrive(&p.ws[kArgmaxTop], got & kRankMask);
+        if ((all >> kRankBits) == groups) {
+          atomicExch(&p.ws[kArgmaxTop], 0ull);
+          const uint64_t r = all & kRankMask;
+          // No value (all NaN) -> 0; the rank of a NaN at index 0 is the
+          // largest, and its index field says 0.
+          *p.amax_out = (r >> kIndexBits) == 0 ? 0 : (int64_t)(kIndexMask - (r & kIndexMask));
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ launch
+
+int cu_count() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0) {
+      cus = 256;
+    }
+  }
+  return cus;
+}
+
+// LDS of one workgroup for a chain stride (matches the carving in gemv_kernel).
+size_t lds_for(bool q4, int R, int nt, bool pair, int cols, int stride) {
+  const int RR = R * (pair ? 2 : 1), B = cols / kBlock;
+  return (size_t)nt * cols + 4 * (size_t)((nt * B + 3) & ~3) + (q4 ? (size_t)nt * B * 16 : 0) +
+         (size_t)kWaves * nt * RR * 5 * stride * 4;
+}
+
+// Ring slots per wave (the kernel's Q) for RR rows per tile.
+int ring_units(int RR) { return RR >= 16 ? RR : RR >= 2 ? 16 : 8; }
+
+template <bool kQ4, int R, int NT, bool kPair, bool kArgmax>
+int launch(GemvParams& p, hipStream_t stream) {
+  constexpr int CB = kQ4 ? 64 : 32, RR = R * (kPair ? 2 : 1);
+  const int B = p.cols / kBlock, chunks = (B + CB - 1) / CB;
+  // Full-K tiles when the whole tile fits the ring (small tiles, where the
+  // chain per chunk would otherwise serialize with each chunk's latency).
+  p.full = RR * chunks <= ring_units(RR) &&
+           lds_for(kQ4, R, NT, kPair, p.cols, chunks * CB + 4) <= 64 * 1024;
+  p.stride = (p.full ? chunks * CB : CB) + 4;
+  const size_t lds = lds_for(kQ4, R, NT, kPair, p.cols, p.stride);
+  if (lds > 64 * 1024) return DNX_EINVAL;  // x too wide for one workgroup's LDS
+  auto kernel = gemv_kernel<kQ4, R, NT, kPair, kArgmax>;
+  // Persistent grid: as many workgroups as stay resident (the occupancy is
+  // looked up once per kernel and LDS size).
+  static int cached_per_cu = 0;
+  static size_t cached_lds = 0;
+  if (cached_per_cu == 0 || cached_lds != lds) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) !=
+            hipSuccess ||
+        per_cu < 1) {
+      per_cu = 1;
+    }
+    cached_per_cu = per_cu;
+    cached_lds = lds;
+  }
+  p.tiles = (p.rows + R - 1) / R;
+  const int need = (p.tiles + kWaves - 1) / kWaves;
+  int cap = cached_per_cu * cu_count();
+  if (kArgmax && cap > kArgmaxMaxGrid) cap = kArgmaxMaxGrid;
+  const int grid = need < cap ? need : cap;
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), lds, stream, p);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+// Rows per tile: the largest of 8 that still gives >= 2048
+// tiles (8 per CU), halving down to 1 for small matrices; bounded so a
+// tile's chains fit a wave and the workgroup's LDS stays within 64 KB.
+int pick_rows(bool q4, int rows, int nt, bool pair, int cols) {
+  int r = 8;  // 8 rows keep two chunk groups in the ring (measured faster than 16)
+  while (r * nt * (pair ? 2 : 1) * 4 > 64) r /= 2;
+  while (r > 1 && (rows + r - 1) / r < 2048) r /= 2;
+  while (r > 1 && lds_for(q4, r, nt, pair, cols, (q4 ? 64 : 32) + 4) > 64 * 1024) r /= 2;
+  return r;
+}
+
+template <bool kQ4, int NT, bool kPair, bool kArgmax>
+int launch_nt(GemvParams& p, int R, hipStream_t stream) {
+  constexpr int RR_MAX = 16 / (NT * (kPair ? 2 : 1));
+  switch (R) {
+    case 8:
+      if constexpr (RR_MAX >= 8) return launch<kQ4, 8, NT, kPair, kArgmax>(p, stream);
+      break;
+    case 4:
+      if constexpr (RR_MAX >= 4) return launch<kQ4, 4, NT, kPair, kArgmax>(p, stream);
+      break;
+    case 2:
+      if constexpr (RR_MAX >= 2) return launch<kQ4, 2, NT, kPair, kArgmax>(p, stream);
+      break;
+    case 1:
+      return launch<kQ4, 1, NT, kPair, kArgmax>(p, stream);
+  }
+  return DNX_EINVAL;
+}
+
+template <bool kQ4, bool kPair, bool kArgmax>
+int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, const float* x,
+         float* y, float* y2, int64_t rows, int64_t cols, int64_t n, unsigned long long* ws,
+         int64_t* out, hipStream_t stream) {
+  if (rows <= 0 || cols <= 0 || n <= 0 || n > 4 || cols % kBlock != 0) return DNX_EINVAL;
+  if (rows > (1 << 30) || cols > (1 << 20)) return DNX_EINVAL;
+  if (((uintptr_t)qs0 & 15) || (kPair && ((uintptr_t)qs1 & 15))) return DNX_EINVAL;
+  if (((uintptr_t)x & 3) || ((uintptr_t)sc0 & (kQ4 ? 1 : 3))) return DNX_EINVAL;
+  if ((int64_t)rows * (kQ4 ? cols / 2 : cols) > ((int64_t)1 << 40)) return DNX_EINVAL;
+  if (kArgmax && (n != 1 || ws == nullptr || out == nullptr || rows > (int64_t)kIndexMask))
+    return DNX_EINVAL;
+  GemvParams p{};
+  p.qs[0] = qs0;
+  p.scales[0] = sc0;
+  p.qs[1] = kPair ? qs1 : qs0;
+  p.scales[1] = kPair ? sc1 : sc0;
+  p.x = x;
+  p.y = y;
+  p.y2 = y2;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.n = (int)n;
+  p.ws = ws;
+  p.amax_out = out;
+  const int nt = n == 1 ? 1 : n == 2 ? 2 : 4;
+  const int R = pick_rows(kQ4, (int)rows, nt, kPair, (int)cols);
+  if (kArgmax) return launch_nt<kQ4, 1, false, true>(p, R, stream);
+  switch (nt) {
+    case 1: return launch_nt<kQ4, 1, kPair, false>(p, R, stream);
+    case 2: return launch_nt<kQ4, 2, kPair, false>(p, R, stream);
+    default: return launch_nt<kQ4, 4, kPair, false>(p, R, stream);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int dnx_gemv_q8(const int8_t* qs, const float* scales, const float* x, float* y, int64_t rows,
+                int64_t cols, int64_t n, hipStream_t stream) {
+  return gemv<false, false, false>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, n,
+                                   nullptr, nullptr, stream);
+}
+
+int dnx_gemv_q4(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
+                int64_t rows, int64_t cols, int64_t n, hipStream_t stream) {
+  return gemv<true, false, false>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, n,
+                                  nullptr, nullptr, stream);
+}
+
+int dnx_gemv_q8_argmax(const int8_t* qs, const float* scales, const float* x, float* y,
+                       int64_t rows, int64_t cols, int64_t* out, void* workspace,
+                       hipStream_t stream) {
+  return gemv<false, false, true>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, 1,
+                                  (unsigned long long*)workspace, out, stream);
+}
+
+int dnx_gemv_q4_argmax(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
+                       int64_t rows, int64_t cols, int64_t* out, void* workspace,
+                       hipStream_t stream) {
+  return gemv<true, false, true>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, 1,
+                                 (unsigned long long*)workspace, out, stream);
+}
+
+int dnx_gate_up_q8(const int8_t* gate_qs, const float* gate_scales, const int8_t* up_qs,
+                   const float* up_scales, const float* x, float* h, float* u, int64_t rows,
+                   int64_t cols, int64_t n, hipStream_t stream) {
+  return gemv<false, true, false>(gate_qs, gate_scales, up_qs, up_scales, x, h, u, rows, cols, n,
+                                  nullptr, nullptr, stream);
+}
+
+int dnx_gate_up_q4(const uint8_t* gate_qs, const uint16_t* gate_scales, const uint8_t* up_qs,
+                   const uint16_t* up_scales, const float* x, float* h, float* u, int64_t rows,
+                   int64_t cols, int64_t n, hipStream_t stream) {
+  return gemv<true, true, false>(gate_qs, gate_scales, up_qs, up_scales, x, h, u, rows, cols, n,
+                                 nullptr, nullptr, stream);
+}
+
+int64_t dnx_gemv_argmax_workspace_bytes(void) { return (int64_t)(kArgmaxTop + 16) * 8; }
+
+}  // extern "C"

@@ -90,6 +90,7 @@ int8_t* gXq = nullptr;
 float* gXs = nullptr;
 int64_t gXCapacity = 0;  // values
 void* gArgmaxWs = nullptr;
+void* gGemvArgmaxWs = nullptr;  // zeroed once; each fused argmax leaves it zero
 
 bool valid(int64_t h) { return h >= 0 && h < gBufferCount && gBuffers[h].live; }
 
@@ -224,8 +225,9 @@ void record(Op op, std::initializer_list<int64_t> args) {
   gCmds.push_back(c);
 }
 
-// The matmul of one recorded command: GEMV (bit-exact) for n <= 4, else the
-// activation quantizer and the int8-MFMA GEMM.
+// The matmul of one recorded command: GEMV (bit-exact) for n <= 4, else (or
+// when x is too wide for the GEMV's LDS) the activation quantizer and the
+// int8-MFMA GEMM.
 bool run_matmul(const Cmd& c, bool q4) {
   const int64_t w = c.a[0], qsOff = c.a[1], scOff = c.a[2], x = c.a[3], xOff = c.a[4];
   const int64_t y = c.a[5], yOff = c.a[6], rows = c.a[7], cols = c.a[8], n = c.a[9];
@@ -236,12 +238,14 @@ bool run_matmul(const Cmd& c, bool q4) {
   const float* xs = (const float*)dev_at(x, xOff);
   float* ys = (float*)dev_at(y, yOff);
   int rc;
+  rc = DNX_EINVAL;
   if (n <= 4) {
     rc = q4 ? dnx_gemv_q4((const uint8_t*)qs, (const uint16_t*)sc, xs, ys, rows, cols, n,
                           gStream)
             : dnx_gemv_q8((const int8_t*)qs, (const float*)sc, xs, ys, rows, cols, n, gStream);
     if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
-  } else {
+  }
+  if (rc != DNX_OK) {  // n > 4, or x too wide for the GEMV's LDS
     rc = dnx_quantize_q8(xs, gXq, gXs, n, cols, cols, gStream);
     if (rc == DNX_OK) {
       after_dispatch(kKindQuantize);
@@ -255,6 +259,75 @@ bool run_matmul(const Cmd& c, bool q4) {
   wrote_region(y, yOff, n * rows * 4);
   if (rc != DNX_OK) LOG("matmul %s %ldx%ld n=%ld failed (%d)\n", q4 ? "q4" : "q8", (long)rows,
                         (long)cols, (long)n, rc);
+  return rc == DNX_OK;
+}
+
+// Fusion of a gate/up pair and its glue: commands i, i+1 are matmuls of one
+// format over the same input and shape into g and u (offset 0), and i+2 is
+// lab_gpu_enc_swiglu(g, u, n * rows), as GpuForward encodes an MLP. One
+// kernel computes both products and the glue; it also writes u, so the
+// result is exactly what the three dispatches leave.
+bool fusable_pair(const Cmd& a, const Cmd& b, const Cmd& c) {
+  if (!(a.op == kOpMatmulQ8 || a.op == kOpMatmulQ4) || b.op != a.op || c.op != kOpSwiglu) {
+    return false;
+  }
+  const int64_t n = a.a[9], rows = a.a[7];
+  return n <= 4 && a.a[3] == b.a[3] && a.a[4] == b.a[4] && a.a[7] == b.a[7] &&
+         a.a[8] == b.a[8] && a.a[9] == b.a[9] && a.a[6] == 0 && b.a[6] == 0 &&
+         a.a[5] != b.a[5] && c.a[0] == a.a[5] && c.a[1] == b.a[5] && c.a[2] == n * rows;
+}
+
+bool run_pair(const Cmd& a, const Cmd& b) {
+  const bool q4 = a.op == kOpMatmulQ4;
+  const int64_t x = a.a[3], xOff = a.a[4], rows = a.a[7], cols = a.a[8], n = a.a[9];
+  use_as_weights(a.a[0]);
+  use_as_weights(b.a[0]);
+  read_region(x, xOff, n * cols * 4);
+  const void* gq = dev_at(a.a[0], a.a[1]);
+  const void* gs = dev_at(a.a[0], a.a[2]);
+  const void* uq = dev_at(b.a[0], b.a[1]);
+  const void* us = dev_at(b.a[0], b.a[2]);
+  const float* xs = (const float*)dev_at(x, xOff);
+  float* h = (float*)dev_at(a.a[5], 0);
+  float* u = (float*)dev_at(b.a[5], 0);
+  const int rc =
+      q4 ? dnx_gate_up_q4((const uint8_t*)gq, (const uint16_t*)gs, (const uint8_t*)uq,
+                          (const uint16_t*)us, xs, h, u, rows, cols, n, gStream)
+         : dnx_gate_up_q8((const int8_t*)gq, (const float*)gs, (const int8_t*)uq,
+                          (const float*)us, xs, h, u, rows, cols, n, gStream);
+  if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+  wrote_region(a.a[5], 0, n * rows * 4);
+  wrote_region(b.a[5], 0, n * rows * 4);
+  if (rc != DNX_OK) LOG("gate/up pair %ldx%ld n=%ld failed (%d)\n", (long)rows, (long)cols, (long)n, rc);
+  return rc == DNX_OK;
+}
+
+// Fusion of a decode matmul (n = 1) and the argmax of its whole output.
+bool fusable_argmax(const Cmd& a, const Cmd& b) {
+  return (a.op == kOpMatmulQ8 || a.op == kOpMatmulQ4) && b.op == kOpArgmax && a.a[9] == 1 &&
+         b.a[0] == a.a[5] && b.a[1] == a.a[6] && b.a[2] == a.a[7];
+}
+
+bool run_matmul_argmax(const Cmd& a, const Cmd& b) {
+  const bool q4 = a.op == kOpMatmulQ4;
+  const int64_t w = a.a[0], x = a.a[3], xOff = a.a[4], y = a.a[5], yOff = a.a[6];
+  const int64_t rows = a.a[7], cols = a.a[8];
+  use_as_weights(w);
+  read_region(x, xOff, cols * 4);
+  const void* qs = dev_at(w, a.a[1]);
+  const void* sc = dev_at(w, a.a[2]);
+  const float* xs = (const float*)dev_at(x, xOff);
+  float* ys = (float*)dev_at(y, yOff);
+  int64_t* out = (int64_t*)dev_at(b.a[3], b.a[4]);
+  const int rc =
+      q4 ? dnx_gemv_q4_argmax((const uint8_t*)qs, (const uint16_t*)sc, xs, ys, rows, cols, out,
+                              gGemvArgmaxWs, gStream)
+         : dnx_gemv_q8_argmax((const int8_t*)qs, (const float*)sc, xs, ys, rows, cols, out,
+                              gGemvArgmaxWs, gStream);
+  if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+  wrote_region(y, yOff, rows * 4);
+  wrote_region(b.a[3], b.a[4], 8);
+  if (rc != DNX_OK) LOG("matmul+argmax %ldx%ld failed (%d)\n", (long)rows, (long)cols, rc);
   return rc == DNX_OK;
 }
 
@@ -338,7 +411,9 @@ int64_t lab_gpu_init(void) {
       return 0;
     }
   }
-  if (hipMalloc(&gArgmaxWs, (size_t)dnx_argmax_workspace_bytes(0)) != hipSuccess) {
+  if (hipMalloc(&gArgmaxWs, (size_t)dnx_argmax_workspace_bytes(0)) != hipSuccess ||
+      hipMalloc(&gGemvArgmaxWs, (size_t)dnx_gemv_argmax_workspace_bytes()) != hipSuccess ||
+      hipMemset(gGemvArgmaxWs, 0, (size_t)dnx_gemv_argmax_workspace_bytes()) != hipSuccess) {
     LOG("scratch allocation failed\n");
     return 0;
   }
@@ -417,7 +492,17 @@ int64_t lab_gpu_commit(int64_t wait) {
   gProfiled = 0;
   bool ok = !gFailed;
   (void)hipEventRecord(gStart, gStream);
-  for (const Cmd& c : gCmds) ok = run(c) && ok;
+  for (size_t i = 0; i < gCmds.size(); i++) {
+    if (i + 2 < gCmds.size() && fusable_pair(gCmds[i], gCmds[i + 1], gCmds[i + 2])) {
+      ok = run_pair(gCmds[i], gCmds[i + 1]) && ok;
+      i += 2;
+    } else if (i + 1 < gCmds.size() && fusable_argmax(gCmds[i], gCmds[i + 1])) {
+      ok = run_matmul_argmax(gCmds[i], gCmds[i + 1]) && ok;
+      i += 1;
+    } else {
+      ok = run(gCmds[i]) && ok;
+    }
+  }
   // Results back to the host views.
   for (const Region& r : gWritten) {
     Buffer& b = gBuffers[r.handle];
@@ -457,7 +542,7 @@ static void enc_matmul(Op op, int64_t w, int64_t qsOffset, int64_t scalesOffset,
                   in_bounds(x, xOffset, n * cols * 4) && in_bounds(y, yOffset, n * rows * 4) &&
                   ((uintptr_t)dev_at(w, qsOffset) % 16) == 0 &&
                   ((uintptr_t)dev_at(w, scalesOffset) % (q4 ? 2 : 4)) == 0 &&
-                  (xOffset % 4) == 0 && (yOffset % 4) == 0 && (n <= 4 || grow_scratch(n * cols));
+                  (xOffset % 4) == 0 && (yOffset % 4) == 0 && grow_scratch(n * cols);
   if (!ok) {
     LOG("enc_matmul_%s: invalid arguments (rows=%ld cols=%ld n=%ld)\n", q4 ? "q4" : "q8",
         (long)rows, (long)cols, (long)n);

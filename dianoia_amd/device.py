@@ -55,6 +55,36 @@ def gemv_q4(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> 
                                    _stream(stream)), "dnx_gemv_q4")
 
 
+def gemv_argmax_workspace(device="cuda") -> torch.Tensor:
+    """Zeroed workspace for the fused argmax GEMV; completed calls leave it zero."""
+    nbytes = int(_lib.load().dnx_gemv_argmax_workspace_bytes())
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+
+def gemv_q8_argmax(qs, scales, x, y, out, workspace, rows: int, cols: int, stream=None) -> None:
+    _check(_lib.load().dnx_gemv_q8_argmax(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols,
+                                          _ptr(out), _ptr(workspace), _stream(stream)),
+           "dnx_gemv_q8_argmax")
+
+
+def gemv_q4_argmax(qs, scales, x, y, out, workspace, rows: int, cols: int, stream=None) -> None:
+    _check(_lib.load().dnx_gemv_q4_argmax(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols,
+                                          _ptr(out), _ptr(workspace), _stream(stream)),
+           "dnx_gemv_q4_argmax")
+
+
+def gate_up_q8(gq, gs, uq, us, x, h, rows: int, cols: int, n: int = 1, u=None,
+               stream=None) -> None:
+    _check(_lib.load().dnx_gate_up_q8(_ptr(gq), _ptr(gs), _ptr(uq), _ptr(us), _ptr(x), _ptr(h),
+                                      _ptr(u), rows, cols, n, _stream(stream)), "dnx_gate_up_q8")
+
+
+def gate_up_q4(gq, gs, uq, us, x, h, rows: int, cols: int, n: int = 1, u=None,
+               stream=None) -> None:
+    _check(_lib.load().dnx_gate_up_q4(_ptr(gq), _ptr(gs), _ptr(uq), _ptr(us), _ptr(x), _ptr(h),
+                                      _ptr(u), rows, cols, n, _stream(stream)), "dnx_gate_up_q4")
+
+
 def gemm_q8(qs, scales, xq, xsc, y, rows: int, cols: int, n: int, stream=None) -> None:
     _check(_lib.load().dnx_gemm_q8(_ptr(qs), _ptr(scales), _ptr(xq), _ptr(xsc), _ptr(y), rows,
                                    cols, n, _stream(stream)), "dnx_gemm_q8")

@@ -48,6 +48,31 @@ int dnx_gemv_q8(const int8_t* qs, const float* scales, const float* x, float* y,
 int dnx_gemv_q4(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
                 int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
 
+// The decode GEMV with the greedy argmax fused (argmaxToken, lib/src/
+// sampler.dart:137-152, over y): writes y and the token index to *out.
+// workspace: dnx_gemv_argmax_workspace_bytes() bytes, zero before its first
+// use; every completed call leaves it ready for the next (its arrival
+// counters back at zero). Calls sharing one workspace must not overlap.
+int64_t dnx_gemv_argmax_workspace_bytes(void);
+int dnx_gemv_q8_argmax(const int8_t* qs, const float* scales, const float* x, float* y,
+                       int64_t rows, int64_t cols, int64_t* out, void* workspace,
+                       dnx_stream_t stream);
+int dnx_gemv_q4_argmax(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
+                       int64_t rows, int64_t cols, int64_t* out, void* workspace,
+                       dnx_stream_t stream);
+
+// An MLP's gate and up products and their glue in one pass over x
+// (LayerShard.ffn, lib/src/shard.dart:455-461): h[t][r] = SiLU(g) * u with
+// g = (W_gate x[t])[r], u = (W_up x[t])[r], each bit-identical to the GEMV
+// above and SiLU in double as the Dart glue computes it. u, when not null,
+// also receives the up products. n <= 4.
+int dnx_gate_up_q8(const int8_t* gate_qs, const float* gate_scales, const int8_t* up_qs,
+                   const float* up_scales, const float* x, float* h, float* u, int64_t rows,
+                   int64_t cols, int64_t n, dnx_stream_t stream);
+int dnx_gate_up_q4(const uint8_t* gate_qs, const uint16_t* gate_scales, const uint8_t* up_qs,
+                   const uint16_t* up_scales, const float* x, float* h, float* u, int64_t rows,
+                   int64_t cols, int64_t n, dnx_stream_t stream);
+
 // Prefill / encoder GEMM on int8 MFMA, any n, inputs already quantized
 // (xq int8 [n][cols], xsc fp32 [n][cols/32], e.g. by dnx_quantize_q8):
 // the per-32-block int32 dots are exact, the per-block scaling is fp32

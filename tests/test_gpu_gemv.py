@@ -13,6 +13,7 @@ from gpu_util import bits, dev, host
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+COUNTER_BYTES = (32 * 16 + 16) * 8  # fused-argmax workspace: all arrival words
 
 
 def gemv(fmt, qs, sc, xs, rows, cols, n):
@@ -40,7 +41,8 @@ def test_gemv_matches_golden(gpu_ready, path):
 @pytest.mark.parametrize("rows,cols,n", [(1, 32, 1), (17, 64, 1), (4097, 2048, 1), (3072, 1024, 1),
                                          (6144, 2048, 1), (2048, 6144, 1), (1000, 4320, 1),
                                          (513, 1152, 2), (33, 2048, 3), (130, 2048, 4),
-                                         (70, 96, 4)])
+                                         (70, 96, 4), (40000, 2048, 1), (33000, 1024, 2),
+                                         (9000, 4096, 4), (300, 16384, 1)])
 def test_gemv_matches_oracle(gpu_ready, orc, fmt, rows, cols, n):
     rng = np.random.default_rng(rows * 31 + cols + n)
     if fmt == "q8":
@@ -92,3 +94,88 @@ def test_gemv_rejects_unsupported(gpu_ready):
         D.gemv_q8(z, z, z, z, 4, 48, 1)   # cols not a multiple of 32
     with pytest.raises(RuntimeError):
         D.gemv_q8(z, z, z, z, 4, 64, 5)   # n above the GEMV's 4
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+@pytest.mark.parametrize("rows,cols", [(151936, 2048), (1000, 1024), (7, 64), (50000, 4320)])
+def test_fused_argmax_gemv(gpu_ready, orc, fmt, rows, cols):
+    """GEMV + argmax in one kernel: logits bit-exact, token = argmaxToken;
+    the workspace is reused across calls (each call leaves it zero)."""
+    rng = np.random.default_rng(rows + cols)
+    if fmt == "q8":
+        qs, sc = synth.q8_weights(rng, rows, cols)
+    else:
+        qs, sc = synth.q4_weights(rng, rows, cols)
+    dq, ds = dev(qs), dev(sc)
+    ws = D.gemv_argmax_workspace()
+    f = D.gemv_q8_argmax if fmt == "q8" else D.gemv_q4_argmax
+    for trial in range(3):
+        x = synth.activations(rng, 1, cols)
+        ref = (orc.gemm_q8 if fmt == "q8" else orc.gemm_q4)(qs, sc, x, 1, threads=8, mode=1)[0]
+        y = torch.empty(rows, device="cuda")
+        out = torch.full((1,), -1, dtype=torch.int64, device="cuda")
+        f(dq, ds, dev(x), y, out, ws, rows, cols)
+        assert np.array_equal(bits(host(y)), bits(ref))
+        assert int(host(out)[0]) == orc.argmax(ref)
+        assert not host(ws)[:COUNTER_BYTES].any()  # arrival counters reset
+
+
+def test_fused_argmax_ties_and_nan(gpu_ready, orc):
+    """Rows that are copies of one another tie exactly: the lowest index wins.
+    A NaN logit at index 0 (a NaN scale) is the answer; elsewhere it loses."""
+    rng = np.random.default_rng(8)
+    qs, sc = synth.q8_weights(rng, 5000, 256)
+    qs[4000] = qs[123]
+    sc[4000] = sc[123]
+    qs[4999] = qs[123]
+    sc[4999] = sc[123]
+    x = synth.activations(rng, 1, 256)
+    ref = orc.gemm_q8(qs, sc, x, 1, threads=8, mode=1)[0]
+    # make row 123 the maximum by scaling its block scales up
+    sc[[123, 4000, 4999]] *= np.float32(50.0)
+    ref = orc.gemm_q8(qs, sc, x, 1, threads=8, mode=1)[0]
+    if ref[123] < 0:
+        sc[[123, 4000, 4999]] *= np.float32(-1.0)
+        ref = orc.gemm_q8(qs, sc, x, 1, threads=8, mode=1)[0]
+    assert orc.argmax(ref) == 123 and ref[4000] == ref[123]
+    ws = D.gemv_argmax_workspace()
+    y = torch.empty(5000, device="cuda")
+    out = torch.empty(1, dtype=torch.int64, device="cuda")
+    D.gemv_q8_argmax(dev(qs), dev(sc), dev(x), y, out, ws, 5000, 256)
+    assert int(host(out)[0]) == 123
+    for nan_row, want in ((0, 0), (123, None)):
+        s2 = sc.copy()
+        s2[nan_row, 0] = np.nan
+        r2 = orc.gemm_q8(qs, s2, x, 1, threads=8, mode=1)[0]
+        D.gemv_q8_argmax(dev(qs), dev(s2), dev(x), y, out, ws, 5000, 256)
+        assert int(host(out)[0]) == orc.argmax(r2)
+        if want is not None:
+            assert orc.argmax(r2) == want
+    assert not host(ws)[:COUNTER_BYTES].any()
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+@pytest.mark.parametrize("rows,cols,n", [(6144, 2048, 1), (100, 512, 2), (4000, 1024, 3),
+                                         (33, 2048, 4), (2048, 6144, 1)])
+def test_gate_up_pair(gpu_ready, orc, fmt, rows, cols, n):
+    """Gate and up products and the SiLU glue in one kernel: g and u
+    bit-identical to the GEMV, h = SiLU(g) * u as the CPU glue rounds it."""
+    rng = np.random.default_rng(rows * 5 + cols + n)
+    make = synth.q8_weights if fmt == "q8" else synth.q4_weights
+    gq, gs = make(rng, rows, cols)
+    uq, us = make(rng, rows, cols)
+    x = synth.activations(rng, n, cols)
+    gemm = orc.gemm_q8 if fmt == "q8" else orc.gemm_q4
+    g = gemm(gq, gs, x, n, threads=8, mode=1)
+    u = gemm(uq, us, x, n, threads=8, mode=1)
+    h_ref = orc.silu_mul(g, u)
+    h = torch.empty((n, rows), device="cuda")
+    ud = torch.empty((n, rows), device="cuda")
+    f = D.gate_up_q8 if fmt == "q8" else D.gate_up_q4
+    f(dev(gq), dev(gs), dev(uq), dev(us), dev(x), h, rows, cols, n, u=ud)
+    assert np.array_equal(bits(host(ud)), bits(u))
+    hh = host(h)
+    ulp = np.abs(bits(hh).astype(np.int64) - bits(h_ref).astype(np.int64))
+    # SiLU runs in double on both sides (GPU exp vs the C library's): the
+    # float results agree except, rarely, by one ulp at a rounding boundary.
+    assert ulp.max() <= 1 and np.mean(ulp == 0) > 0.999

@@ -123,6 +123,9 @@ def test_config1_mlp(gpu, orc):
     gpu.apply("gate", x, g_gpu, 1)
     gpu.apply("up", x, u_gpu, 1)
     assert np.array_equal(bits(g_gpu), bits(g[0])) and np.array_equal(bits(u_gpu), bits(u[0]))
+    # The ABI fuses gate, up and the glue into one kernel (peephole at
+    # commit); u must still hold the up products the unfused chain leaves.
+    assert np.array_equal(bits(gpu._aux["u"].view(count=6144)), bits(u[0]))
     h = orc.silu_mul(g, u)
     # down product of the CPU glue output, bit-exact against the GPU's chain
     ref = orc.gemm_q4(dq, ds, h, 1, threads=8, mode=1)[0]
