@@ -7,11 +7,17 @@
 // keeps four partial lanes per block (lab_native.c:480-512); one lane per
 // output here gives a different rounding, within 1e-4 relative.
 //
-// Workgroup tile: BM tokens x BN weight rows, 4 waves in a 2 x 2 grid, each
-// wave a (BM/2) x (BN/2) tile of 32 x 32 MFMA subtiles. K is staged KB
-// blocks at a time in LDS (double buffered): activations as int8, weights
-// unpacked to int8 (Q4 nibbles -> q - 8 once per stage, shared by all BM
-// tokens), scales as fp32.
+// Roofline: per 32 x 32 output tile and block, one MFMA (32K MACs) against
+// 3 x 16 VALU ops per lane for the epilogue (no packed fp32 here): the
+// epilogue, not the MFMA, bounds this kernel (about 1/6 of the int8 peak
+// when VALU and MFMA overlap perfectly).
+//
+// Workgroup tile: BM tokens x BN weight rows, 4 waves in a WM x WN grid,
+// each wave (BM/WM) x (BN/WN) of 32 x 32 MFMA subtiles. K is staged KB
+// blocks at a time in LDS (double buffered through registers): activations
+// as int8, weights unpacked to int8 (Q4 nibbles -> q - 8 once per stage,
+// shared by all BM tokens), scales as fp32. Small tiles keep enough
+// workgroups resident (several waves per SIMD) for MFMA and VALU to overlap.
 
 #include "common.h"
 #include "dnx_kernels.h"
@@ -24,9 +30,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
-constexpr int KB = 2;             // blocks per LDS stage
-constexpr int kRowBytes = KB * 32;
-constexpr int kRowStride = kRowBytes + 16;  // LDS row stride (bank spread)
 
 struct GemmParams {
   const void* qs;
@@ -46,99 +49,129 @@ DNX_DEV void unpack_q4(uint32_t v, uint32_t& lo, uint32_t& hi) {
   hi = ((((v >> 4) & m) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
 }
 
-template <bool kQ4, int BM, int BN>
+template <bool kQ4, int BM, int BN, int WM, int KB>
 __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
-  constexpr int WM = BM / 2, WN = BN / 2;      // wave tile
-  constexpr int SM = WM / 32, SN = WN / 32;    // 32x32 subtiles per wave
-  __shared__ __align__(16) int8_t sa[2][BM * kRowStride];
-  __shared__ __align__(16) int8_t sb[2][BN * kRowStride];
+  constexpr int WN = 4 / WM;
+  constexpr int TM = BM / WM, TN = BN / WN;   // wave tile
+  constexpr int SM = TM / 32, SN = TN / 32;   // 32x32 subtiles per wave
+  static_assert(SM >= 1 && SN >= 1, "wave tile below one MFMA tile");
+  constexpr int RB = KB * 32;                 // bytes of a row per stage
+  constexpr int RS = RB + 16;                 // LDS row stride (bank spread)
+  __shared__ __align__(16) int8_t sa[2][BM * RS];
+  __shared__ __align__(16) int8_t sb[2][BN * RS];
   __shared__ __align__(16) float sxs[2][KB][BM];
   __shared__ __align__(16) float sws[2][KB][BN];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave - (wave / WN) * WN;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int K = p.cols, B = K / kBlock, M = p.n, N = p.rows;
   const int stages = (B + KB - 1) / KB;
 
-  // Global -> register staging of one stage. A: BM rows x 64 B -> 16 B per
-  // thread per pass. B: Q8 the same; Q4 BN rows x 32 B of nibbles.
-  constexpr int APASS = BM * kRowBytes / 16 / kThreads;  // b128 loads per thread
-  constexpr int BPASS = BN * (kQ4 ? kRowBytes / 2 : kRowBytes) / 16 / kThreads;
-  static_assert(APASS >= 1 && BPASS >= 1, "tile too small for the staging");
-  uint4 ra[APASS], rb[BPASS];
-  float rsx, rsw;
+  // Staging of one stage through registers, with bounded buffer loads
+  // (rows past the matrix, blocks past K read as zeros).
+  constexpr int A16 = BM * RB / 16;                 // 16-byte pieces of A per stage
+  constexpr int B16 = BN * (kQ4 ? RB / 2 : RB) / 16;
+  constexpr int AP = (A16 + kThreads - 1) / kThreads;
+  constexpr int BP = (B16 + kThreads - 1) / kThreads;
+  constexpr int SXP = (KB * BM + kThreads - 1) / kThreads;
+  constexpr int SWP = (KB * BN + kThreads - 1) / kThreads;
+  uint4 ra[AP], rb[BP];
+  float rsx[SXP], rsw[SWP];
+  const i32x4 rxq = buffer_rsrc(p.xq, (uint32_t)((size_t)M * K));
+  const i32x4 rqs = buffer_rsrc(p.qs, (uint32_t)((size_t)N * (kQ4 ? K / 2 : K)));
+  const i32x4 rxs = buffer_rsrc(p.xsc, (uint32_t)((size_t)M * B * 4));
+  const i32x4 rws = buffer_rsrc(p.scales, (uint32_t)((size_t)N * B * (kQ4 ? 2 : 4)));
 
   auto load_stage = [&](int s) {
     const int b0 = s * KB;
 #pragma unroll
-    for (int i = 0; i < APASS; i++) {
+    for (int i = 0; i < AP; i++) {
       const int idx = i * kThreads + tid;
-      const int row = idx / (kRowBytes / 16), seg = idx % (kRowBytes / 16);
+      const int row = idx / (RB / 16), seg = idx - row * (RB / 16);
       const int m = m0 + row, blk = b0 + seg / 2;
-      ra[i] = make_uint4(0, 0, 0, 0);
-      if (m < M && blk < B) ra[i] = *(const uint4*)(p.xq + (size_t)m * K + b0 * 32 + seg * 16);
+      const bool ok = idx < A16 && m < M && blk < B;
+      ra[i] = buffer_load16(rxq, ok ? (int)((size_t)m * K + b0 * 32 + seg * 16) : -16);
     }
 #pragma unroll
-    for (int i = 0; i < BPASS; i++) {
+    for (int i = 0; i < BP; i++) {
       const int idx = i * kThreads + tid;
       if (kQ4) {
-        const int row = idx / KB, blk = b0 + idx % KB;
-        const int r = n0 + row;
-        rb[i] = make_uint4(0, 0, 0, 0);
-        if (r < N && blk < B)
-          rb[i] = *(const uint4*)((const uint8_t*)p.qs + (size_t)r * (K / 2) + (size_t)blk * 16);
+        const int row = idx / KB, kb = idx - row * KB;
+        const int r = n0 + row, blk = b0 + kb;
+        const bool ok = idx < B16 && r < N && blk < B;
+        rb[i] = buffer_load16(rqs, ok ? (int)((size_t)r * (K / 2) + (size_t)blk * 16) : -16);
       } else {
-        const int row = idx / (kRowBytes / 16), seg = idx % (kRowBytes / 16);
+        const int row = idx / (RB / 16), seg = idx - row * (RB / 16);
         const int r = n0 + row, blk = b0 + seg / 2;
-        rb[i] = make_uint4(0, 0, 0, 0);
-        if (r < N && blk < B)
-          rb[i] = *(const uint4*)((const int8_t*)p.qs + (size_t)r * K + b0 * 32 + seg * 16);
+        const bool ok = idx < B16 && r < N && blk < B;
+        rb[i] = buffer_load16(rqs, ok ? (int)((size_t)r * K + b0 * 32 + seg * 16) : -16);
       }
     }
-    // Scales: thread t < KB*BM loads sx, thread t < KB*BN loads sw.
-    rsx = 0.0f;
-    rsw = 0.0f;
-    if (tid < KB * BM) {
-      const int kb = tid / BM, m = m0 + tid % BM, blk = b0 + kb;
-      if (m < M && blk < B) rsx = p.xsc[(size_t)m * B + blk];
+#pragma unroll
+    for (int i = 0; i < SXP; i++) {
+      const int idx = i * kThreads + tid;
+      const int kb = idx / BM, m = m0 + idx - kb * BM, blk = b0 + kb;
+      const bool ok = idx < KB * BM && m < M && blk < B;
+      rsx[i] = __int_as_float(dnx_raw_buffer_load_i32(rxs, ok ? (m * B + blk) * 4 : -4, 0, 0));
     }
-    if (tid < KB * BN) {
-      const int kb = tid / BN, r = n0 + tid % BN, blk = b0 + kb;
-      if (r < N && blk < B) {
-        rsw = kQ4 ? half_bits_to_float(((const uint16_t*)p.scales)[(size_t)r * B + blk])
-                  : ((const float*)p.scales)[(size_t)r * B + blk];
+#pragma unroll
+    for (int i = 0; i < SWP; i++) {
+      const int idx = i * kThreads + tid;
+      const int kb = idx / BN, r = n0 + idx - kb * BN, blk = b0 + kb;
+      const bool ok = idx < KB * BN && r < N && blk < B;
+      if (kQ4) {
+        const short h = dnx_raw_buffer_load_i16(rws, ok ? (r * B + blk) * 2 : -2, 0, 0);
+        rsw[i] = __int_as_float((int)(uint16_t)h);  // bits; widened in store_stage
+      } else {
+        rsw[i] = __int_as_float(dnx_raw_buffer_load_i32(rws, ok ? (r * B + blk) * 4 : -4, 0, 0));
       }
     }
   };
 
   auto store_stage = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < APASS; i++) {
+    for (int i = 0; i < AP; i++) {
       const int idx = i * kThreads + tid;
-      const int row = idx / (kRowBytes / 16), seg = idx % (kRowBytes / 16);
-      *(uint4*)(&sa[buf][row * kRowStride + seg * 16]) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < BPASS; i++) {
-      const int idx = i * kThreads + tid;
-      if (kQ4) {
-        const int row = idx / KB, kb = idx % KB;
-        uint4 lo, hi;
-        unpack_q4(rb[i].x, lo.x, hi.x);
-        unpack_q4(rb[i].y, lo.y, hi.y);
-        unpack_q4(rb[i].z, lo.z, hi.z);
-        unpack_q4(rb[i].w, lo.w, hi.w);
-        int8_t* dst = &sb[buf][row * kRowStride + kb * 32];
-        *(uint4*)dst = lo;
-        *(uint4*)(dst + 16) = hi;
-      } else {
-        const int row = idx / (kRowBytes / 16), seg = idx % (kRowBytes / 16);
-        *(uint4*)(&sb[buf][row * kRowStride + seg * 16]) = rb[i];
+      if (idx < A16) {
+        const int row = idx / (RB / 16), seg = idx - row * (RB / 16);
+        *(uint4*)(&sa[buf][row * RS + seg * 16]) = ra[i];
       }
     }
-    if (tid < KB * BM) sxs[buf][tid / BM][tid % BM] = rsx;
-    if (tid < KB * BN) sws[buf][tid / BN][tid % BN] = rsw;
+#pragma unroll
+    for (int i = 0; i < BP; i++) {
+      const int idx = i * kThreads + tid;
+      if (idx < B16) {
+        if (kQ4) {
+          const int row = idx / KB, kb = idx - row * KB;
+          uint4 lo, hi;
+          unpack_q4(rb[i].x, lo.x, hi.x);
+          unpack_q4(rb[i].y, lo.y, hi.y);
+          unpack_q4(rb[i].z, lo.z, hi.z);
+          unpack_q4(rb[i].w, lo.w, hi.w);
+          int8_t* dst = &sb[buf][row * RS + kb * 32];
+          *(uint4*)dst = lo;
+          *(uint4*)(dst + 16) = hi;
+        } else {
+          const int row = idx / (RB / 16), seg = idx - row * (RB / 16);
+          *(uint4*)(&sb[buf][row * RS + seg * 16]) = rb[i];
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < SXP; i++) {
+      const int idx = i * kThreads + tid;
+      if (idx < KB * BM) sxs[buf][idx / BM][idx % BM] = rsx[i];
+    }
+#pragma unroll
+    for (int i = 0; i < SWP; i++) {
+      const int idx = i * kThreads + tid;
+      if (idx < KB * BN) {
+        sws[buf][idx / BN][idx % BN] =
+            kQ4 ? half_bits_to_float((uint16_t)__float_as_int(rsw[i])) : rsw[i];
+      }
+    }
   };
 
   float acc[SM][SN][16];
@@ -157,27 +190,29 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
   for (int s = 0; s < stages; s++) {
     const int buf = s & 1;
     if (s + 1 < stages) load_stage(s + 1);
+    const int nkb = min(KB, B - s * KB);
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
-      if (s * KB + kb >= B) break;
+      if (kb >= nkb) break;
       v4i a[SM], b[SN];
 #pragma unroll
       for (int i = 0; i < SM; i++)
-        a[i] = *(const v4i*)(&sa[buf][(wm * WM + i * 32 + lrow) * kRowStride + kb * 32 + lk]);
+        a[i] = *(const v4i*)(&sa[buf][(wm * TM + i * 32 + lrow) * RS + kb * 32 + lk]);
 #pragma unroll
       for (int j = 0; j < SN; j++)
-        b[j] = *(const v4i*)(&sb[buf][(wn * WN + j * 32 + lrow) * kRowStride + kb * 32 + lk]);
-      // Scales of this lane's outputs: column n = lane % 32 of each N
-      // subtile; rows (v / 4) * 8 + (lane / 32) * 4 + v % 4 of each M subtile.
+        b[j] = *(const v4i*)(&sb[buf][(wn * TN + j * 32 + lrow) * RS + kb * 32 + lk]);
+      // This lane's outputs: column n = lane % 32 of each N subtile; rows
+      // (v / 4) * 8 + (lane / 32) * 4 + v % 4 of each M subtile.
       float swv[SN];
 #pragma unroll
-      for (int j = 0; j < SN; j++) swv[j] = sws[buf][kb][wn * WN + j * 32 + lrow];
+      for (int j = 0; j < SN; j++) swv[j] = sws[buf][kb][wn * TN + j * 32 + lrow];
 #pragma unroll
       for (int i = 0; i < SM; i++) {
         float sxv[16];
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-          const float4 t = *(const float4*)(&sxs[buf][kb][wm * WM + i * 32 + g * 8 + (lane >> 5) * 4]);
+          const float4 t =
+              *(const float4*)(&sxs[buf][kb][wm * TM + i * 32 + g * 8 + (lane >> 5) * 4]);
           sxv[4 * g + 0] = t.x;
           sxv[4 * g + 1] = t.y;
           sxv[4 * g + 2] = t.z;
@@ -188,7 +223,8 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
           v16i d = {};
           d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], d, 0, 0, 0);
 #pragma unroll
-          for (int v = 0; v < 16; v++) acc[i][j][v] = fmaf((float)d[v], sxv[v] * swv[j], acc[i][j][v]);
+          for (int v = 0; v < 16; v++)
+            acc[i][j][v] = fmaf((float)d[v], sxv[v] * swv[j], acc[i][j][v]);
         }
       }
     }
@@ -196,32 +232,41 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
     __syncthreads();
   }
 
-  // Store: lane holds column n0 + wn*WN + j*32 + lane%32 for 16 rows.
+  // Store: lane holds column n0 + wn*TN + j*32 + lane%32 for 16 rows.
 #pragma unroll
   for (int i = 0; i < SM; i++)
 #pragma unroll
     for (int j = 0; j < SN; j++) {
-      const int r = n0 + wn * WN + j * 32 + lrow;
+      const int r = n0 + wn * TN + j * 32 + lrow;
       if (r >= N) continue;
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        const int m = m0 + wm * WM + i * 32 + (v / 4) * 8 + (lane >> 5) * 4 + (v % 4);
+        const int m = m0 + wm * TM + i * 32 + (v / 4) * 8 + (lane >> 5) * 4 + (v % 4);
         if (m < M) p.y[(size_t)m * N + r] = acc[i][j][v];
       }
     }
+}
+
+template <bool kQ4, int BM, int BN, int WM, int KB>
+int launch_tile(const GemmParams& p, hipStream_t stream) {
+  const dim3 grid((unsigned)((p.rows + BN - 1) / BN), (unsigned)((p.n + BM - 1) / BM));
+  hipLaunchKernelGGL((gemm_kernel<kQ4, BM, BN, WM, KB>), grid, dim3(kThreads), 0, stream, p);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 
 template <bool kQ4>
 int launch_gemm(const void* qs, const void* scales, const int8_t* xq, const float* xsc,
                 float* y, int64_t rows, int64_t cols, int64_t n, hipStream_t stream) {
   if (rows <= 0 || cols <= 0 || n <= 0 || cols % kBlock != 0) return DNX_EINVAL;
-  if (rows > INT32_MAX || n > INT32_MAX || cols > INT32_MAX / 2) return DNX_EINVAL;
-  if (((uintptr_t)qs & 15) || ((uintptr_t)xq & 15)) return DNX_EINVAL;
+  // Buffer-load offsets are 32-bit: each operand must stay below 2 GB.
+  if (rows * (kQ4 ? cols / 2 : cols) >= (1ll << 31) || n * cols >= (1ll << 31)) return DNX_EINVAL;
+  if (((uintptr_t)qs & 15) || ((uintptr_t)xq & 15) || (cols % 16)) return DNX_EINVAL;
   GemmParams p{qs, scales, xq, xsc, y, (int)rows, (int)cols, (int)n};
-  constexpr int BM = 128, BN = 128;
-  const dim3 grid((unsigned)((rows + BN - 1) / BN), (unsigned)((n + BM - 1) / BM));
-  hipLaunchKernelGGL((gemm_kernel<kQ4, BM, BN>), grid, dim3(kThreads), 0, stream, p);
-  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+  // 32 tokens: one wave row of 32 x 32 tiles (4 waves across N); else
+  // 64 x 64 tiles (2 x 2 waves), which keep ~3 workgroups per CU resident
+  // at prefill sizes.
+  if (n <= 32) return launch_tile<kQ4, 32, 128, 1, 4>(p, stream);
+  return launch_tile<kQ4, 64, 64, 2, 4>(p, stream);
 }
 
 }  // namespace
