@@ -340,14 +340,139 @@ def cpu_baseline(synth, seconds):
 
 
 def traffic_from_profiles():
-    path = os.path.join(ROOT, "profiles", "traffic_gemv_q4_c1.json")
+    """HBM bytes per launch of the headline's dominant kernel, from the
+    committed FETCH_SIZE / WRITE_SIZE summary (None when absent)."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.json")
     if not os.path.exists(path):
         return None
     try:
         with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
-    except (OSError, ValueError):
+            k = json.load(f)["kernels"]["c1 gate+up Q4 pair, 6144x2048"]
+        return k["hbm_bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
         return None
+
+
+PMC_COPY_BYTES = 1 << 30  # the calibration copy: reads and writes this many bytes
+PMC_KERNELS = {  # kernel-name fragment -> (workload, algorithmic bytes per launch)
+    "gemv_kernel<true, 2, 1, true, false>": (
+        "c1 gate+up Q4 pair, 6144x2048", 2 * q4_bytes(6144, 2048) + 2048 * 4 + 6144 * 4),
+    "gemv_kernel<true, 1, 1, false, false>": (
+        "c1 down Q4, 2048x6144", q4_bytes(2048, 6144) + 6144 * 4 + 2048 * 4),
+    "gemv_kernel<false, 8, 1, false, true>": (
+        "c2 LM head Q8 + argmax, 151936x2048", q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4),
+    "gemm_kernel<true, 64, 64, 2, 4>": (
+        "c3 Q4 GEMM M=512, 6144x2048", q4_bytes(6144, 2048) + 512 * 2048 + 512 * 64 * 4
+        + 512 * 6144 * 4),
+}
+
+
+def pmc_workload(torch, D, synth, reps):
+    """Eager launches for the rocprofv3 --pmc runs: a plain device copy of
+    PMC_COPY_BYTES (the calibration of FETCH_SIZE / WRITE_SIZE), then the
+    config-1 step, the config-2 LM head and the config-3 GEMM, each over
+    rotating weight copies so that every launch reads its weights from HBM."""
+    src = torch.empty(PMC_COPY_BYTES // 4, device="cuda")
+    src.fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    print("pmc: copy calibration done", file=sys.stderr, flush=True)
+
+    (gq, gs), (uq, us), (dq, ds), x = synth.config1()
+    copies = copies_for(2 * q4_bytes(6144, 2048) + q4_bytes(2048, 6144))
+    sets = [tuple(dev(torch, a) for a in (gq, gs, uq, us, dq, ds)) for _ in range(copies)]
+    xd = dev(torch, x)
+    h = torch.empty(6144, device="cuda")
+    y = torch.empty(2048, device="cuda")
+    for i in range(reps):
+        s = sets[i % copies]
+        D.gate_up_q4(s[0], s[1], s[2], s[3], xd, h, 6144, 2048, 1)
+        D.gemv_q4(s[4], s[5], h, y, 2048, 6144, 1)
+    torch.cuda.synchronize()
+    del sets
+    print("pmc: config 1 done", file=sys.stderr, flush=True)
+
+    qs, sc, x = synth.config2()
+    ws = [(dev(torch, qs), dev(torch, sc)) for _ in range(2)]
+    xd = dev(torch, x)
+    y = torch.empty(151936, device="cuda")
+    out = torch.empty(1, dtype=torch.int64, device="cuda")
+    wsp = D.gemv_argmax_workspace()
+    for i in range(reps):
+        q, s = ws[i % 2]
+        D.gemv_q8_argmax(q, s, xd, y, out, wsp, 151936, 2048)
+    torch.cuda.synchronize()
+    del ws
+    print("pmc: config 2 done", file=sys.stderr, flush=True)
+
+    qs, sc, xs = synth.config3()
+    M, N, K = 512, 6144, 2048
+    ws = [(dev(torch, qs), dev(torch, sc)) for _ in range(8)]
+    xd = dev(torch, xs)
+    xq = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    xsc = torch.empty((M, K // 32), dtype=torch.float32, device="cuda")
+    y = torch.empty((M, N), device="cuda")
+    D.quantize_q8(xd, xq, xsc, M, K, K)
+    for i in range(reps):
+        q, s = ws[i % 8]
+        D.gemm_q4(q, s, xq, xsc, y, N, K, M)
+    torch.cuda.synchronize()
+    print("pmc: config 3 done", file=sys.stderr, flush=True)
+
+
+def _pmc_means(path, counter):
+    """Mean value of `counter` per kernel name in a rocprofv3
+    counter_collection.csv (one row per dispatch and counter)."""
+    import csv
+    sums, calls = {}, {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") != counter:
+                continue
+            name = row["Kernel_Name"]
+            sums[name] = sums.get(name, 0.0) + float(row["Counter_Value"])
+            calls[name] = calls.get(name, 0) + 1
+    return {k: (sums[k] / calls[k], calls[k]) for k in sums}
+
+
+def pmc_summary(fetch_csv, write_csv):
+    """HBM bytes per launch of the kernels in PMC_KERNELS from a FETCH_SIZE
+    run and a WRITE_SIZE run (KiB per dispatch), each scaled by what the same
+    counter reads for the calibration copy of PMC_COPY_BYTES."""
+    fetch = _pmc_means(fetch_csv, "FETCH_SIZE")
+    write = _pmc_means(write_csv, "WRITE_SIZE")
+
+    def calib(table):
+        cands = [(v[0], k) for k, v in table.items() if "copy" in k.lower()]
+        if not cands:
+            raise SystemExit("no copy kernel in the counter run")
+        kib, name = max(cands)
+        return PMC_COPY_BYTES / (kib * 1024.0), name, kib
+
+    ff, fname, fkib = calib(fetch)
+    wf, wname, wkib = calib(write)
+    kernels = {}
+    for frag, (workload, algo) in PMC_KERNELS.items():
+        fk = [(v, k) for k, v in fetch.items() if frag in k]
+        wk = [(v, k) for k, v in write.items() if frag in k]
+        if not fk or not wk:
+            continue
+        (fv, fc), name = fk[0]
+        (wv, _), _ = wk[0]
+        rd, wr = fv * 1024.0 * ff, wv * 1024.0 * wf
+        kernels[workload] = {"kernel": name, "launches": fc, "fetch_kib": round(fv, 1),
+                             "write_kib": round(wv, 1), "hbm_read_bytes": round(rd),
+                             "hbm_write_bytes": round(wr), "hbm_bytes_per_launch": round(rd + wr),
+                             "algorithmic_bytes": algo,
+                             "traffic_over_algorithmic": round((rd + wr) / algo, 4)}
+    return {"calibration": {"kernel": fname, "bytes_read_and_written": PMC_COPY_BYTES,
+                            "fetch_kib": round(fkib, 1), "write_kib": round(wkib, 1),
+                            "fetch_factor": round(ff, 5), "write_factor": round(wf, 5),
+                            "write_kernel": wname},
+            "kernels": kernels}
 
 
 def check_graph_replay(torch, D, synth):
@@ -386,7 +511,14 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline config only")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="eager launches for rocprofv3 --pmc runs (no JSON line)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="HBM traffic per launch from two rocprofv3 counter_collection.csv files")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(the quantized linear layer runs on one MI355X; see DESIGN.md for sharding)",
@@ -399,6 +531,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs the GPU", file=sys.stderr)
         sys.exit(1)
+    if args.pmc_workload:
+        pmc_workload(torch, D, synth, max(1, min(args.steps, 20)))
+        return
     timer = Timer(torch)
     check_graph_replay(torch, D, synth)
     print(f"bench: config 1 (steps={args.steps}, warmup={args.warmup})", file=sys.stderr, flush=True)
