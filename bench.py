@@ -190,11 +190,13 @@ def bench_c0(torch, D, synth, timer, steps, warmup):
 
 
 def bench_c2(torch, D, synth, timer, steps, warmup):
-    """Config 2: the LM-head GEMV with the greedy argmax fused into it."""
+    """Config 2: the LM-head GEMV with the greedy argmax fused into it, on the
+    GGUF Q8_0 blocks' own fp16 scales (34 B per 32 weights); the engine
+    layout's fp32 scales (36 B per 32) are timed beside it."""
     qs, sc, x = synth.config2()
     copies = 2
-    ws = [(dev(torch, qs), dev(torch, sc)) for _ in range(copies)]
-    del qs, sc
+    half = sc.astype(np.float16).view(np.uint16)
+    ws = [(dev(torch, qs), dev(torch, half)) for _ in range(copies)]
     xd = dev(torch, x)
     y = torch.empty(151936, device="cuda")
     out = torch.empty(1, dtype=torch.int64, device="cuda")
@@ -202,15 +204,23 @@ def bench_c2(torch, D, synth, timer, steps, warmup):
 
     def step(i):
         q, s = ws[i % copies]
-        D.gemv_q8_argmax(q, s, xd, y, out, wsp, 151936, 2048)
+        D.gemv_q8h_argmax(q, s, xd, y, out, wsp, 151936, 2048)
 
     n = max(20, steps // 2)
     ms = timer.time(step, n, max(2, warmup // 2))
     algo = q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4
     resident = timer.time(lambda i: step(0), n, 2)
+    ws = [(q, dev(torch, sc)) for q, _ in ws]
+
+    def step32(i):
+        q, s = ws[i % copies]
+        D.gemv_q8_argmax(q, s, xd, y, out, wsp, 151936, 2048)
+
+    ms32 = timer.time(step32, n, 2)
     return {"ms": ms, "gbps": algo / ms / 1e6, "frac_hbm": algo / ms / 1e6 / HBM_PEAK_GBS,
-            "kernel": "gemv_q8 + fused argmax", "weight_copies": copies,
-            "resident_gbps": algo / resident / 1e6}
+            "kernel": "gemv_q8h + fused argmax (fp16 block scales)", "weight_copies": copies,
+            "resident_gbps": algo / resident / 1e6,
+            "engine_fp32_scales_ms": ms32, "engine_fp32_scales_gbps": algo / ms32 / 1e6}
 
 
 def bench_c3(torch, D, synth, timer, steps, warmup):
@@ -355,12 +365,13 @@ def traffic_from_profiles():
 
 PMC_COPY_BYTES = 1 << 30  # the calibration copy: reads and writes this many bytes
 PMC_KERNELS = {  # kernel-name fragment -> (workload, algorithmic bytes per launch)
-    "gemv_kernel<true, 2, 1, true, false>": (
+    "gemv_kernel<1, 2, 1, true, false>": (
         "c1 gate+up Q4 pair, 6144x2048", 2 * q4_bytes(6144, 2048) + 2048 * 4 + 6144 * 4),
-    "gemv_kernel<true, 1, 1, false, false>": (
+    "gemv_kernel<1, 1, 1, false, false>": (
         "c1 down Q4, 2048x6144", q4_bytes(2048, 6144) + 6144 * 4 + 2048 * 4),
-    "gemv_kernel<false, 8, 1, false, true>": (
-        "c2 LM head Q8 + argmax, 151936x2048", q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4),
+    "gemv_kernel<2, 8, 1, false, true>": (
+        "c2 LM head Q8 (fp16 scales) + argmax, 151936x2048",
+        q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4),
     "gemm_kernel<true, 64, 64, 2, 4>": (
         "c3 Q4 GEMM M=512, 6144x2048", q4_bytes(6144, 2048) + 512 * 2048 + 512 * 64 * 4
         + 512 * 6144 * 4),
@@ -396,14 +407,15 @@ def pmc_workload(torch, D, synth, reps):
     print("pmc: config 1 done", file=sys.stderr, flush=True)
 
     qs, sc, x = synth.config2()
-    ws = [(dev(torch, qs), dev(torch, sc)) for _ in range(2)]
+    half = sc.astype(np.float16).view(np.uint16)
+    ws = [(dev(torch, qs), dev(torch, half)) for _ in range(2)]
     xd = dev(torch, x)
     y = torch.empty(151936, device="cuda")
     out = torch.empty(1, dtype=torch.int64, device="cuda")
     wsp = D.gemv_argmax_workspace()
     for i in range(reps):
         q, s = ws[i % 2]
-        D.gemv_q8_argmax(q, s, xd, y, out, wsp, 151936, 2048)
+        D.gemv_q8h_argmax(q, s, xd, y, out, wsp, 151936, 2048)
     torch.cuda.synchronize()
     del ws
     print("pmc: config 2 done", file=sys.stderr, flush=True)

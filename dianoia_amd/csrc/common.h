@@ -111,6 +111,16 @@ DNX_DEV uint4 buffer_load16(i32x4 rsrc, int offset) {
   return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
 }
 
+// Cache-policy immediate of a buffer load on gfx950: the non-temporal bit.
+// Weights read once per call stream through the caches without being kept:
+// on the 350 MB LM head this took the GEMV from 69 to 61 us.
+constexpr int kStream = 2;
+
+DNX_DEV uint4 buffer_load16_stream(i32x4 rsrc, int offset) {
+  const i32x4 v = dnx_raw_buffer_load_v4i32(rsrc, offset, 0, kStream);
+  return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+
 DNX_DEV float4 buffer_load_f4(i32x4 rsrc, int offset) {
   const i32x4 v = dnx_raw_buffer_load_v4i32(rsrc, offset, 0, 0);
   return make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z),

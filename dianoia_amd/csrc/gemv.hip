@@ -25,8 +25,11 @@
 //   DPP lane combine gives each row.
 // * Fusions: the gate/up pair of an MLP shares x and finishes with the
 //   SiLU(gate) * up glue (shard.dart:457-461); an LM head can finish with
-//   the greedy argmax (sampler.dart:137-143) reduced across the grid with
-//   64-bit atomics, the last wave to finish writing the token.
+//   the greedy argmax (sampler.dart:137-143): workgroups fold their best
+//   rank into 32 words with 64-bit atomic max, and a one-wave kernel after
+//   the GEMV writes the token.
+
+#include <type_traits>
 
 #include "common.h"
 #include "dnx_kernels.h"
@@ -37,38 +40,24 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-// Fused argmax. A rank orders (value, lowest index): the 32-bit value key
-// of argmax_key above 20 bits of complemented row index (rows < 2^20). A
-// workspace word holds an arrival count above a 52-bit rank. Workspace: 32
-// group words 16 words (128 B) apart, then the top word.
-constexpr int kIndexBits = 20;
-constexpr uint64_t kIndexMask = (1ull << kIndexBits) - 1;
-constexpr int kRankBits = 32 + kIndexBits;
-constexpr uint64_t kRankMask = (1ull << kRankBits) - 1;
+// Weight formats: the engine's Q8 (fp32 scales) and Q4 (fp16 scales), and Q8
+// with the GGUF Q8_0 block's own fp16 scale (34 B per 32 weights, not 36).
+constexpr int kFmtQ8 = 0, kFmtQ4 = 1, kFmtQ8H = 2;
+// Fused argmax. A rank orders (value, lowest index): argmax_key's 32-bit
+// value order above the complemented row. Each workgroup folds its waves'
+// ranks into one of kArgmaxGroups workspace words (128 B apart, so the
+// atomics of different groups go to different channels) with a 64-bit
+// atomic max that nothing waits for; a one-wave finisher launched after the
+// GEMV on the same stream reads and clears the words and writes the token.
+// The kernel boundary orders the atomics before the reads, so no memory
+// fence and no arrival count is needed, and no atomic is ever retried.
 constexpr int kArgmaxGroups = 32;
-constexpr int kArgmaxTop = kArgmaxGroups * 16;
-constexpr int kArgmaxMaxGrid = 4096;  // arrivals per word stay below 2^12
+constexpr int kArgmaxStride = 16;  // words between group words
 
 DNX_DEV uint64_t argmax_rank(float v, uint32_t row) {
-  const uint64_t key = argmax_key(v, row);  // value order << 32 | ~row
-  uint64_t rank = ((key >> 32) << kIndexBits) | (kIndexMask - row);
   // A NaN at index 0 is the answer whatever follows (every comparison with
   // it is false): give it the one rank no value reaches.
-  if (row == 0 && v != v) rank = kRankMask;
-  return rank;
-}
-
-// One arrival at a workspace word: count + 1, rank = max(rank, r). Returns
-// the word after this arrival.
-DNX_DEV uint64_t arrive(unsigned long long* word, uint64_t r) {
-  unsigned long long old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  unsigned long long next;
-  do {
-    const uint64_t best = (old & kRankMask) > r ? (old & kRankMask) : r;
-    next = (((old >> kRankBits) + 1) << kRankBits) | best;
-  } while (!__hip_atomic_compare_exchange_strong(word, &old, next, __ATOMIC_RELAXED,
-                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  return next;
+  return (row == 0 && v != v) ? ~0ull : argmax_key(v, row);
 }
 
 struct GemvParams {
@@ -81,8 +70,7 @@ struct GemvParams {
   int tiles;                   // ceil(rows / R)
   int full;                    // 1: a tile's whole K goes to LDS before its chains run
   int stride;                  // LDS floats per chain: span of blocks + 4
-  unsigned long long* ws;      // argmax: {key, finished waves}, zero between calls
-  int64_t* amax_out;
+  unsigned long long* ws;      // argmax: the group words, zero between calls
 };
 
 // Orders LDS writes and reads among the lanes of one wave (a wave's LDS
@@ -101,8 +89,10 @@ DNX_DEV float silu_mul(float g, float u) {
   return s * u;
 }
 
-template <bool kQ4, int R, int NT, bool kPair, bool kArgmax>
+template <int F, int R, int NT, bool kPair, bool kArgmax>
 __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
+  constexpr bool kQ4 = F == kFmtQ4;
+  constexpr bool kHalf = F != kFmtQ8;          // fp16 block scales
   constexpr int CB = kQ4 ? 64 : 32;           // blocks per 1 KB chunk of a row
   constexpr int M = kPair ? 2 : 1;            // matrices sharing x
   constexpr int RR = R * M;                   // weight rows per tile
@@ -131,8 +121,10 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
   const int lblk = kQ4 ? lane : (lane >> 1);               // lane's block in a chunk
 
   uint4 raw[Q];
-  uint32_t swb[Q];  // scale bits (fp16 or fp32), converted when used: a
-                    // conversion here would wait for the load at once
+  // Raw scale bits, converted only when used: any operation on a loaded
+  // value (even a zero-extension) makes the wave wait for that load there.
+  using ScaleBits = std::conditional_t<kHalf, short, int>;
+  ScaleBits swb[Q];
 
   // Requests the RR row-chunks of chunk c of this wave's k-th tile into ring
   // slots [s0, s0 + RR) with buffer loads bounded by the row: blocks past
@@ -152,15 +144,21 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
                                      live ? (uint32_t)(cols / 2) : 0u);
         const i32x4 rs = buffer_rsrc((const uint16_t*)p.scales[m] + (size_t)row * B,
                                      live ? (uint32_t)(B * 2) : 0u);
-        raw[s0 + i] = buffer_load16(rq, blk * 16);
-        swb[s0 + i] = (uint16_t)dnx_raw_buffer_load_i16(rs, blk * 2, 0, 0);
+        raw[s0 + i] = buffer_load16_stream(rq, blk * 16);
+        swb[s0 + i] = dnx_raw_buffer_load_i16(rs, blk * 2, 0, kStream);
       } else {
         const i32x4 rq = buffer_rsrc((const int8_t*)p.qs[m] + (size_t)row * cols,
                                      live ? (uint32_t)cols : 0u);
-        const i32x4 rs = buffer_rsrc((const float*)p.scales[m] + (size_t)row * B,
-                                     live ? (uint32_t)(B * 4) : 0u);
-        raw[s0 + i] = buffer_load16(rq, blk * 32 + (lane & 1) * 16);
-        swb[s0 + i] = (uint32_t)dnx_raw_buffer_load_i32(rs, blk * 4, 0, 0);
+        raw[s0 + i] = buffer_load16_stream(rq, blk * 32 + (lane & 1) * 16);
+        if (kHalf) {
+          const i32x4 rs = buffer_rsrc((const uint16_t*)p.scales[m] + (size_t)row * B,
+                                       live ? (uint32_t)(B * 2) : 0u);
+          swb[s0 + i] = dnx_raw_buffer_load_i16(rs, blk * 2, 0, kStream);
+        } else {
+          const i32x4 rs = buffer_rsrc((const float*)p.scales[m] + (size_t)row * B,
+                                       live ? (uint32_t)(B * 4) : 0u);
+          swb[s0 + i] = dnx_raw_buffer_load_i32(rs, blk * 4, 0, kStream);
+        }
       }
     }
   };
@@ -230,21 +228,34 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
   float acc = 0.0f;
   uint64_t best = 0;
   int ck = 0, cc = 0;  // position of the chunk group being consumed
+  // Deferred outputs: lane j holds the j-th result of the wave's tiles (value
+  // and destination), stored after the loop. A store among the loads would
+  // make every later wait drain all loads in flight (loads and stores share
+  // one counter on this GPU, and with a store pending the compiler waits for
+  // zero). The launch gives a wave at most 64 / kOut tiles.
+  constexpr int kOut = NT * RR;  // results per tile (chain groups)
+  float outv = 0.0f;
+  float* outp = nullptr;
+  int pend = 0;  // uniform: results recorded so far
   for (int base = 0; base < groups; base += G) {
 #pragma unroll
     for (int g = 0; g < G; g++) {
       if (base + g >= groups) break;  // uniform across the wave
       const int tile = tile0 + ck * stride;
+      // Lanes past the row's last block (ok false) store zeros; their slots
+      // up to the next multiple of 4 are read by the chains, the rest are
+      // in bounds and never read. Selects, not branches: a branch here makes
+      // the compiler wait for every load in flight.
       const int nb = min(CB, B - cc * CB), nb4 = (nb + 3) & ~3;
-      const bool ok = lblk < nb, pad = !ok && lblk < nb4;
+      const bool ok = lblk < nb;
       const int blk = cc * CB + (ok ? lblk : 0);
       const int at = p.full ? cc * CB + lblk : lblk;  // block slot in this chain's LDS
       // Row-chunks -> lane sums and block scales in LDS.
 #pragma unroll
       for (int i = 0; i < RR; i++) {
         const uint4 w = raw[g * RR + i];
-        const float swi = kQ4 ? half_bits_to_float((uint16_t)swb[g * RR + i])
-                              : __uint_as_float(swb[g * RR + i]);
+        const float swi = kHalf ? half_bits_to_float((uint16_t)swb[g * RR + i])
+                                : __int_as_float((int)swb[g * RR + i]);
 #pragma unroll
         for (int t = 0; t < NT; t++) {
           float* f = sf + ((t * RR + i) * 4) * CP + at;
@@ -258,19 +269,12 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
             const int d1 = sdot4(w.y & mk, xa.y, sdot4((w.y >> 4) & mk, xb.y, c8.y));
             const int d2 = sdot4(w.z & mk, xa.z, sdot4((w.z >> 4) & mk, xb.z, c8.z));
             const int d3 = sdot4(w.w & mk, xa.w, sdot4((w.w >> 4) & mk, xb.w, c8.w));
-            if (ok) {
-              f[0] = (float)d0;
-              f[CP] = (float)d1;
-              f[2 * CP] = (float)d2;
-              f[3 * CP] = (float)d3;
-              *sp = swi * sxs[t * B + blk];
-            } else if (pad) {
-              f[0] = 0.0f;
-              f[CP] = 0.0f;
-              f[2 * CP] = 0.0f;
-              f[3 * CP] = 0.0f;
-              *sp = 0.0f;
-            }
+            const float sb = swi * sxs[t * B + blk];
+            f[0] = ok ? (float)d0 : 0.0f;
+            f[CP] = ok ? (float)d1 : 0.0f;
+            f[2 * CP] = ok ? (float)d2 : 0.0f;
+            f[3 * CP] = ok ? (float)d3 : 0.0f;
+            *sp = ok ? sb : 0.0f;
           } else {
             const int h = lane & 1;
             const int4 xv = *(const int4*)(sxq + t * cols + blk * 32 + h * 16);
@@ -282,15 +286,10 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
             p2 += dpp<kQuadXor1>(p2);
             p3 += dpp<kQuadXor1>(p3);
             float* fh = f + 2 * h * CP;
-            if (ok) {
-              fh[0] = (float)(h ? p2 : p0);
-              fh[CP] = (float)(h ? p3 : p1);
-              if (h == 0) *sp = swi * sxs[t * B + blk];
-            } else if (pad) {
-              fh[0] = 0.0f;
-              fh[CP] = 0.0f;
-              if (h == 0) *sp = 0.0f;
-            }
+            const float sb = swi * sxs[t * B + blk];
+            fh[0] = ok ? (float)(h ? p2 : p0) : 0.0f;
+            fh[CP] = ok ? (float)(h ? p3 : p1) : 0.0f;
+            *sp = ok ? sb : 0.0f;  // both lanes of the block: the same value
           }
         }
       }
@@ -325,53 +324,70 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
         const int tr = lane >> 2, t = tr / RR, i = tr - (tr / RR) * RR;
         const int row = tile * R + (i % R);
         const bool lead = lane < CH && (lane & 3) == 0 && t < n && row < p.rows;
+        float val = v;
+        float* dst = nullptr;
         if (kPair) {
           const float up = __shfl(v, lane + R * 4);  // the up row of this gate row
-          if (lead && i < R) p.y[(size_t)t * p.rows + row] = silu_mul(v, up);
-          if (lead && i >= R && p.y2 != nullptr) p.y2[(size_t)t * p.rows + row] = v;
+          if (lead && i < R) {
+            val = silu_mul(v, up);
+            dst = p.y + (size_t)t * p.rows + row;
+          } else if (lead && p.y2 != nullptr) {
+            dst = p.y2 + (size_t)t * p.rows + row;
+          }
         } else {
-          if (lead) p.y[(size_t)t * p.rows + row] = v;
+          if (lead) dst = p.y + (size_t)t * p.rows + row;
           if (kArgmax) {
             const uint64_t key = lead ? argmax_rank(v, (uint32_t)row) : 0;
             const uint64_t m = wave_max_u64(key);
             best = m > best ? m : best;
           }
         }
+        // Result j of this tile (chain group j, lane 4j) -> lane pend + j.
+        const int j = lane - pend;
+        const bool mine = j >= 0 && j < kOut;
+        const int src = mine ? 4 * j : lane;
+        const float mv = __shfl(val, src);
+        const long long mp = __shfl((long long)(uintptr_t)dst, src);
+        if (mine) {
+          outv = mv;
+          outp = (float*)(uintptr_t)mp;
+        }
+        pend += kOut;
       }
       advance(ck, cc);
     }
   }
+  if (outp != nullptr) *outp = outv;
 
   if (kArgmax) {
-    // Grid-wide (max, lowest index) through the atomic words alone, so no
-    // memory fence is needed: each workgroup folds its waves' ranks, then
-    // CAS-updates one of 32 group words (separate cache lines) holding an
-    // arrival count and the group's best rank; the last arrival of a group
-    // carries that rank to the top word the same way, and the last arrival
-    // there writes the token. Every word is reset by its last arrival.
+    // The workgroup's best rank into its group word (the finisher reads it).
     __shared__ uint64_t red[kWaves];
     if (lane == 0) red[wave] = best;
     __syncthreads();
     if (tid == 0) {
       uint64_t b = red[0];
       for (int w = 1; w < kWaves; w++) b = red[w] > b ? red[w] : b;
-      const int grp = blockIdx.x % kArgmaxGroups;
-      const uint64_t in_grp = (gridDim.x - 1 - grp) / kArgmaxGroups + 1;
-      const uint64_t groups = gridDim.x < kArgmaxGroups ? gridDim.x : kArgmaxGroups;
-      const uint64_t got = arrive(&p.ws[grp * 16], b);
-      if ((got >> kRankBits) == in_grp) {
-        atomicExch(&p.ws[grp * 16], 0ull);
-        const uint64_t all = arrive(&p.ws[kArgmaxTop], got & kRankMask);
-        if ((all >> kRankBits) == groups) {
-          atomicExch(&p.ws[kArgmaxTop], 0ull);
-          const uint64_t r = all & kRankMask;
-          // No value (all NaN) -> 0; the rank of a NaN at index 0 is the
-          // largest, and its index field says 0.
-          *p.amax_out = (r >> kIndexBits) == 0 ? 0 : (int64_t)(kIndexMask - (r & kIndexMask));
-        }
+      if (b != 0) {
+        __hip_atomic_fetch_max(&p.ws[(blockIdx.x % kArgmaxGroups) * kArgmaxStride],
+                               (unsigned long long)b, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
+}
+
+// The fused argmax's last step: the best of the group words (clearing each
+// for the next call) -> the token. Rank 0 means no value was a number: 0.
+__global__ void __launch_bounds__(64) argmax_finish_kernel(unsigned long long* ws,
+                                                           int64_t* out) {
+  const int lane = threadIdx.x;
+  uint64_t r = 0;
+  if (lane < kArgmaxGroups) {
+    r = __hip_atomic_exchange(&ws[lane * kArgmaxStride], 0ull, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+  }
+  r = wave_max_u64(r);
+  if (lane == 0) *out = r == 0 ? 0 : (int64_t)(0xffffffffu - (uint32_t)(r & 0xffffffffu));
 }
 
 // ------------------------------------------------------------ launch
@@ -399,8 +415,9 @@ size_t lds_for(bool q4, int R, int nt, bool pair, int cols, int stride) {
 // Ring slots per wave (the kernel's Q) for RR rows per tile.
 int ring_units(int RR) { return RR >= 16 ? RR : RR >= 2 ? 16 : 8; }
 
-template <bool kQ4, int R, int NT, bool kPair, bool kArgmax>
+template <int F, int R, int NT, bool kPair, bool kArgmax>
 int launch(GemvParams& p, hipStream_t stream) {
+  constexpr bool kQ4 = F == kFmtQ4;
   constexpr int CB = kQ4 ? 64 : 32, RR = R * (kPair ? 2 : 1);
   const int B = p.cols / kBlock, chunks = (B + CB - 1) / CB;
   // Full-K tiles when the whole tile fits the ring (small tiles, where the
@@ -410,7 +427,7 @@ int launch(GemvParams& p, hipStream_t stream) {
   p.stride = (p.full ? chunks * CB : CB) + 4;
   const size_t lds = lds_for(kQ4, R, NT, kPair, p.cols, p.stride);
   if (lds > 64 * 1024) return DNX_EINVAL;  // x too wide for one workgroup's LDS
-  auto kernel = gemv_kernel<kQ4, R, NT, kPair, kArgmax>;
+  auto kernel = gemv_kernel<F, R, NT, kPair, kArgmax>;
   // Persistent grid: as many workgroups as stay resident (the occupancy is
   // looked up once per kernel and LDS size).
   static int cached_per_cu = 0;
@@ -428,7 +445,11 @@ int launch(GemvParams& p, hipStream_t stream) {
   p.tiles = (p.rows + R - 1) / R;
   const int need = (p.tiles + kWaves - 1) / kWaves;
   int cap = cached_per_cu * cu_count();
-  if (kArgmax && cap > kArgmaxMaxGrid) cap = kArgmaxMaxGrid;
+  // A wave defers its results in one register across its 64 lanes: at most
+  // 64 / (NT * RR) tiles per wave, so at least this many workgroups.
+  const int per_wave = 64 / (NT * RR);
+  const int floor_grid = (p.tiles + kWaves * per_wave - 1) / (kWaves * per_wave);
+  if (cap < floor_grid) cap = floor_grid;
   const int grid = need < cap ? need : cap;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), lds, stream, p);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
@@ -445,36 +466,37 @@ int pick_rows(bool q4, int rows, int nt, bool pair, int cols) {
   return r;
 }
 
-template <bool kQ4, int NT, bool kPair, bool kArgmax>
+template <int F, int NT, bool kPair, bool kArgmax>
 int launch_nt(GemvParams& p, int R, hipStream_t stream) {
   constexpr int RR_MAX = 16 / (NT * (kPair ? 2 : 1));
   switch (R) {
     case 8:
-      if constexpr (RR_MAX >= 8) return launch<kQ4, 8, NT, kPair, kArgmax>(p, stream);
+      if constexpr (RR_MAX >= 8) return launch<F, 8, NT, kPair, kArgmax>(p, stream);
       break;
     case 4:
-      if constexpr (RR_MAX >= 4) return launch<kQ4, 4, NT, kPair, kArgmax>(p, stream);
+      if constexpr (RR_MAX >= 4) return launch<F, 4, NT, kPair, kArgmax>(p, stream);
       break;
     case 2:
-      if constexpr (RR_MAX >= 2) return launch<kQ4, 2, NT, kPair, kArgmax>(p, stream);
+      if constexpr (RR_MAX >= 2) return launch<F, 2, NT, kPair, kArgmax>(p, stream);
       break;
     case 1:
-      return launch<kQ4, 1, NT, kPair, kArgmax>(p, stream);
+      return launch<F, 1, NT, kPair, kArgmax>(p, stream);
   }
   return DNX_EINVAL;
 }
 
-template <bool kQ4, bool kPair, bool kArgmax>
+template <int F, bool kPair, bool kArgmax>
 int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, const float* x,
          float* y, float* y2, int64_t rows, int64_t cols, int64_t n, unsigned long long* ws,
          int64_t* out, hipStream_t stream) {
   if (rows <= 0 || cols <= 0 || n <= 0 || n > 4 || cols % kBlock != 0) return DNX_EINVAL;
   if (rows > (1 << 30) || cols > (1 << 20)) return DNX_EINVAL;
   if (((uintptr_t)qs0 & 15) || (kPair && ((uintptr_t)qs1 & 15))) return DNX_EINVAL;
-  if (((uintptr_t)x & 3) || ((uintptr_t)sc0 & (kQ4 ? 1 : 3))) return DNX_EINVAL;
+  constexpr bool kQ4 = F == kFmtQ4;
+  if (((uintptr_t)x & 3) || ((uintptr_t)sc0 & (F != kFmtQ8 ? 1 : 3))) return DNX_EINVAL;
+  if (kPair && ((uintptr_t)sc1 & (F != kFmtQ8 ? 1 : 3))) return DNX_EINVAL;
   if ((int64_t)rows * (kQ4 ? cols / 2 : cols) > ((int64_t)1 << 40)) return DNX_EINVAL;
-  if (kArgmax && (n != 1 || ws == nullptr || out == nullptr || rows > (int64_t)kIndexMask))
-    return DNX_EINVAL;
+  if (kArgmax && (n != 1 || ws == nullptr || out == nullptr)) return DNX_EINVAL;
   GemvParams p{};
   p.qs[0] = qs0;
   p.scales[0] = sc0;
@@ -487,14 +509,18 @@ int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, con
   p.cols = (int)cols;
   p.n = (int)n;
   p.ws = ws;
-  p.amax_out = out;
   const int nt = n == 1 ? 1 : n == 2 ? 2 : 4;
   const int R = pick_rows(kQ4, (int)rows, nt, kPair, (int)cols);
-  if (kArgmax) return launch_nt<kQ4, 1, false, true>(p, R, stream);
+  if (kArgmax) {
+    const int rc = launch_nt<F, 1, false, true>(p, R, stream);
+    if (rc != DNX_OK) return rc;
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(64), 0, stream, ws, out);
+    return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+  }
   switch (nt) {
-    case 1: return launch_nt<kQ4, 1, kPair, false>(p, R, stream);
-    case 2: return launch_nt<kQ4, 2, kPair, false>(p, R, stream);
-    default: return launch_nt<kQ4, 4, kPair, false>(p, R, stream);
+    case 1: return launch_nt<F, 1, kPair, false>(p, R, stream);
+    case 2: return launch_nt<F, 2, kPair, false>(p, R, stream);
+    default: return launch_nt<F, 4, kPair, false>(p, R, stream);
   }
 }
 
@@ -504,44 +530,66 @@ extern "C" {
 
 int dnx_gemv_q8(const int8_t* qs, const float* scales, const float* x, float* y, int64_t rows,
                 int64_t cols, int64_t n, hipStream_t stream) {
-  return gemv<false, false, false>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, n,
+  return gemv<kFmtQ8, false, false>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, n,
                                    nullptr, nullptr, stream);
 }
 
 int dnx_gemv_q4(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
                 int64_t rows, int64_t cols, int64_t n, hipStream_t stream) {
-  return gemv<true, false, false>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, n,
+  return gemv<kFmtQ4, false, false>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, n,
                                   nullptr, nullptr, stream);
 }
 
 int dnx_gemv_q8_argmax(const int8_t* qs, const float* scales, const float* x, float* y,
                        int64_t rows, int64_t cols, int64_t* out, void* workspace,
                        hipStream_t stream) {
-  return gemv<false, false, true>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, 1,
+  return gemv<kFmtQ8, false, true>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, 1,
                                   (unsigned long long*)workspace, out, stream);
 }
 
 int dnx_gemv_q4_argmax(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
                        int64_t rows, int64_t cols, int64_t* out, void* workspace,
                        hipStream_t stream) {
-  return gemv<true, false, true>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, 1,
+  return gemv<kFmtQ4, false, true>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, 1,
                                  (unsigned long long*)workspace, out, stream);
 }
 
 int dnx_gate_up_q8(const int8_t* gate_qs, const float* gate_scales, const int8_t* up_qs,
                    const float* up_scales, const float* x, float* h, float* u, int64_t rows,
                    int64_t cols, int64_t n, hipStream_t stream) {
-  return gemv<false, true, false>(gate_qs, gate_scales, up_qs, up_scales, x, h, u, rows, cols, n,
+  return gemv<kFmtQ8, true, false>(gate_qs, gate_scales, up_qs, up_scales, x, h, u, rows, cols, n,
                                   nullptr, nullptr, stream);
 }
 
 int dnx_gate_up_q4(const uint8_t* gate_qs, const uint16_t* gate_scales, const uint8_t* up_qs,
                    const uint16_t* up_scales, const float* x, float* h, float* u, int64_t rows,
                    int64_t cols, int64_t n, hipStream_t stream) {
-  return gemv<true, true, false>(gate_qs, gate_scales, up_qs, up_scales, x, h, u, rows, cols, n,
+  return gemv<kFmtQ4, true, false>(gate_qs, gate_scales, up_qs, up_scales, x, h, u, rows, cols, n,
                                  nullptr, nullptr, stream);
 }
 
-int64_t dnx_gemv_argmax_workspace_bytes(void) { return (int64_t)(kArgmaxTop + 16) * 8; }
+int dnx_gemv_q8h(const int8_t* qs, const uint16_t* scales, const float* x, float* y,
+                 int64_t rows, int64_t cols, int64_t n, hipStream_t stream) {
+  return gemv<kFmtQ8H, false, false>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, n,
+                                     nullptr, nullptr, stream);
+}
+
+int dnx_gemv_q8h_argmax(const int8_t* qs, const uint16_t* scales, const float* x, float* y,
+                        int64_t rows, int64_t cols, int64_t* out, void* workspace,
+                        hipStream_t stream) {
+  return gemv<kFmtQ8H, false, true>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, 1,
+                                    (unsigned long long*)workspace, out, stream);
+}
+
+int dnx_gate_up_q8h(const int8_t* gate_qs, const uint16_t* gate_scales, const int8_t* up_qs,
+                    const uint16_t* up_scales, const float* x, float* h, float* u, int64_t rows,
+                    int64_t cols, int64_t n, hipStream_t stream) {
+  return gemv<kFmtQ8H, true, false>(gate_qs, gate_scales, up_qs, up_scales, x, h, u, rows, cols,
+                                    n, nullptr, nullptr, stream);
+}
+
+int64_t dnx_gemv_argmax_workspace_bytes(void) {
+  return (int64_t)kArgmaxGroups * kArgmaxStride * 8;
+}
 
 }  // extern "C"

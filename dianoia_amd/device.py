@@ -85,6 +85,24 @@ def gate_up_q4(gq, gs, uq, us, x, h, rows: int, cols: int, n: int = 1, u=None,
                                       _ptr(u), rows, cols, n, _stream(stream)), "dnx_gate_up_q4")
 
 
+def gemv_q8h(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> None:
+    """Q8 GEMV with fp16 block scales (uint16 bits, the GGUF Q8_0 d)."""
+    _check(_lib.load().dnx_gemv_q8h(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
+                                    _stream(stream)), "dnx_gemv_q8h")
+
+
+def gemv_q8h_argmax(qs, scales, x, y, out, workspace, rows: int, cols: int, stream=None) -> None:
+    _check(_lib.load().dnx_gemv_q8h_argmax(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols,
+                                           _ptr(out), _ptr(workspace), _stream(stream)),
+           "dnx_gemv_q8h_argmax")
+
+
+def gate_up_q8h(gq, gs, uq, us, x, h, rows: int, cols: int, n: int = 1, u=None,
+                stream=None) -> None:
+    _check(_lib.load().dnx_gate_up_q8h(_ptr(gq), _ptr(gs), _ptr(uq), _ptr(us), _ptr(x), _ptr(h),
+                                       _ptr(u), rows, cols, n, _stream(stream)), "dnx_gate_up_q8h")
+
+
 def gemm_q8(qs, scales, xq, xsc, y, rows: int, cols: int, n: int, stream=None) -> None:
     _check(_lib.load().dnx_gemm_q8(_ptr(qs), _ptr(scales), _ptr(xq), _ptr(xsc), _ptr(y), rows,
                                    cols, n, _stream(stream)), "dnx_gemm_q8")

@@ -51,8 +51,9 @@ int dnx_gemv_q4(const uint8_t* qs, const uint16_t* scales, const float* x, float
 // The decode GEMV with the greedy argmax fused (argmaxToken, lib/src/
 // sampler.dart:137-152, over y): writes y and the token index to *out.
 // workspace: dnx_gemv_argmax_workspace_bytes() bytes, zero before its first
-// use; every completed call leaves it ready for the next (its arrival
-// counters back at zero). Calls sharing one workspace must not overlap.
+// use; every completed call leaves it zero again (the call's last kernel
+// clears it). Calls sharing one workspace must not overlap. Two launches on
+// `stream`: the GEMV, then a one-wave kernel that writes *out.
 int64_t dnx_gemv_argmax_workspace_bytes(void);
 int dnx_gemv_q8_argmax(const int8_t* qs, const float* scales, const float* x, float* y,
                        int64_t rows, int64_t cols, int64_t* out, void* workspace,
@@ -72,6 +73,19 @@ int dnx_gate_up_q8(const int8_t* gate_qs, const float* gate_scales, const int8_t
 int dnx_gate_up_q4(const uint8_t* gate_qs, const uint16_t* gate_scales, const uint8_t* up_qs,
                    const uint16_t* up_scales, const float* x, float* h, float* u, int64_t rows,
                    int64_t cols, int64_t n, dnx_stream_t stream);
+
+// The same three for Q8 weights whose block scales are kept as the GGUF Q8_0
+// block's own fp16 d (gguf.dart:270-282 widens it to fp32 exactly): scales
+// uint16 [rows][cols/32]. Bit-identical to the fp32-scale calls on the
+// widened scales, with 34 instead of 36 bytes streamed per 32 weights.
+int dnx_gemv_q8h(const int8_t* qs, const uint16_t* scales, const float* x, float* y,
+                 int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
+int dnx_gemv_q8h_argmax(const int8_t* qs, const uint16_t* scales, const float* x, float* y,
+                        int64_t rows, int64_t cols, int64_t* out, void* workspace,
+                        dnx_stream_t stream);
+int dnx_gate_up_q8h(const int8_t* gate_qs, const uint16_t* gate_scales, const int8_t* up_qs,
+                    const uint16_t* up_scales, const float* x, float* h, float* u, int64_t rows,
+                    int64_t cols, int64_t n, dnx_stream_t stream);
 
 // Prefill / encoder GEMM on int8 MFMA, any n, inputs already quantized
 // (xq int8 [n][cols], xsc fp32 [n][cols/32], e.g. by dnx_quantize_q8):

@@ -13,12 +13,21 @@ from gpu_util import bits, dev, host
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
-COUNTER_BYTES = (32 * 16 + 16) * 8  # fused-argmax workspace: all arrival words
+COUNTER_BYTES = 32 * 16 * 8  # fused-argmax workspace: the 32 group words, 128 B apart
+
+
+def half_scales(sc):
+    """fp32 scales that are fp16 values -> their fp16 bits (the Q8_0 d)."""
+    h = sc.astype(np.float16)
+    assert np.array_equal(h.astype(np.float32), sc)
+    return h.view(np.uint16)
 
 
 def gemv(fmt, qs, sc, xs, rows, cols, n):
     y = torch.full((n, rows), float("nan"), dtype=torch.float32, device="cuda")
-    f = D.gemv_q4 if fmt == "q4" else D.gemv_q8
+    f = {"q4": D.gemv_q4, "q8": D.gemv_q8, "q8h": D.gemv_q8h}[fmt]
+    if fmt == "q8h":
+        sc = half_scales(sc)
     f(dev(qs), dev(sc), dev(xs), y, rows, cols, n)
     return host(y)
 
@@ -37,7 +46,7 @@ def test_gemv_matches_golden(gpu_ready, path):
         assert np.array_equal(bits(y), bits(d["y_mode1"][t0:t1]))
 
 
-@pytest.mark.parametrize("fmt", ["q8", "q4"])
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q8h"])
 @pytest.mark.parametrize("rows,cols,n", [(1, 32, 1), (17, 64, 1), (4097, 2048, 1), (3072, 1024, 1),
                                          (6144, 2048, 1), (2048, 6144, 1), (1000, 4320, 1),
                                          (513, 1152, 2), (33, 2048, 3), (130, 2048, 4),
@@ -45,12 +54,12 @@ def test_gemv_matches_golden(gpu_ready, path):
                                          (9000, 4096, 4), (300, 16384, 1)])
 def test_gemv_matches_oracle(gpu_ready, orc, fmt, rows, cols, n):
     rng = np.random.default_rng(rows * 31 + cols + n)
-    if fmt == "q8":
-        qs, sc = synth.q8_weights(rng, rows, cols)
-    else:
+    if fmt == "q4":
         qs, sc = synth.q4_weights(rng, rows, cols)
+    else:
+        qs, sc = synth.q8_weights(rng, rows, cols)
     xs = synth.activations(rng, n, cols)
-    ref = (orc.gemm_q8 if fmt == "q8" else orc.gemm_q4)(qs, sc, xs, n, threads=8, mode=1)
+    ref = (orc.gemm_q4 if fmt == "q4" else orc.gemm_q8)(qs, sc, xs, n, threads=8, mode=1)
     y = gemv(fmt, qs, sc, xs, rows, cols, n)
     assert np.array_equal(bits(y), bits(ref))
 
@@ -65,6 +74,13 @@ def test_lm_head_and_argmax_config2(gpu_ready, orc):
     D.argmax(y, out, D.argmax_workspace(151936))
     logits = host(y)
     assert np.array_equal(bits(logits), bits(ref))
+    assert int(host(out)[0]) == orc.argmax(ref)
+    # the fused LM head on the GGUF fp16 scales: same logits, same token
+    y.fill_(float("nan"))
+    out.fill_(-1)
+    D.gemv_q8h_argmax(dev(qs), dev(half_scales(sc)), dev(x), y, out, D.gemv_argmax_workspace(),
+                      151936, 2048)
+    assert np.array_equal(bits(host(y)), bits(ref))
     assert int(host(out)[0]) == orc.argmax(ref)
 
 
@@ -96,28 +112,30 @@ def test_gemv_rejects_unsupported(gpu_ready):
         D.gemv_q8(z, z, z, z, 4, 64, 5)   # n above the GEMV's 4
 
 
-@pytest.mark.parametrize("fmt", ["q8", "q4"])
-@pytest.mark.parametrize("rows,cols", [(151936, 2048), (1000, 1024), (7, 64), (50000, 4320)])
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q8h"])
+@pytest.mark.parametrize("rows,cols", [(151936, 2048), (1000, 1024), (7, 64), (50000, 4320),
+                                       (1100000, 32)])
 def test_fused_argmax_gemv(gpu_ready, orc, fmt, rows, cols):
-    """GEMV + argmax in one kernel: logits bit-exact, token = argmaxToken;
-    the workspace is reused across calls (each call leaves it zero)."""
+    """GEMV + argmax (the GEMV, then a one-wave finisher): logits bit-exact,
+    token = argmaxToken; the workspace is reused across calls (each call
+    leaves it zero)."""
     rng = np.random.default_rng(rows + cols)
-    if fmt == "q8":
-        qs, sc = synth.q8_weights(rng, rows, cols)
-    else:
+    if fmt == "q4":
         qs, sc = synth.q4_weights(rng, rows, cols)
-    dq, ds = dev(qs), dev(sc)
+    else:
+        qs, sc = synth.q8_weights(rng, rows, cols)
+    dq, ds = dev(qs), dev(half_scales(sc) if fmt == "q8h" else sc)
     ws = D.gemv_argmax_workspace()
-    f = D.gemv_q8_argmax if fmt == "q8" else D.gemv_q4_argmax
+    f = {"q4": D.gemv_q4_argmax, "q8": D.gemv_q8_argmax, "q8h": D.gemv_q8h_argmax}[fmt]
     for trial in range(3):
         x = synth.activations(rng, 1, cols)
-        ref = (orc.gemm_q8 if fmt == "q8" else orc.gemm_q4)(qs, sc, x, 1, threads=8, mode=1)[0]
+        ref = (orc.gemm_q4 if fmt == "q4" else orc.gemm_q8)(qs, sc, x, 1, threads=8, mode=1)[0]
         y = torch.empty(rows, device="cuda")
         out = torch.full((1,), -1, dtype=torch.int64, device="cuda")
         f(dq, ds, dev(x), y, out, ws, rows, cols)
         assert np.array_equal(bits(host(y)), bits(ref))
         assert int(host(out)[0]) == orc.argmax(ref)
-        assert not host(ws)[:COUNTER_BYTES].any()  # arrival counters reset
+        assert not host(ws)[:COUNTER_BYTES].any()  # group words cleared
 
 
 def test_fused_argmax_ties_and_nan(gpu_ready, orc):
@@ -154,24 +172,26 @@ def test_fused_argmax_ties_and_nan(gpu_ready, orc):
     assert not host(ws)[:COUNTER_BYTES].any()
 
 
-@pytest.mark.parametrize("fmt", ["q8", "q4"])
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q8h"])
 @pytest.mark.parametrize("rows,cols,n", [(6144, 2048, 1), (100, 512, 2), (4000, 1024, 3),
                                          (33, 2048, 4), (2048, 6144, 1)])
 def test_gate_up_pair(gpu_ready, orc, fmt, rows, cols, n):
     """Gate and up products and the SiLU glue in one kernel: g and u
     bit-identical to the GEMV, h = SiLU(g) * u as the CPU glue rounds it."""
     rng = np.random.default_rng(rows * 5 + cols + n)
-    make = synth.q8_weights if fmt == "q8" else synth.q4_weights
+    make = synth.q4_weights if fmt == "q4" else synth.q8_weights
     gq, gs = make(rng, rows, cols)
     uq, us = make(rng, rows, cols)
     x = synth.activations(rng, n, cols)
-    gemm = orc.gemm_q8 if fmt == "q8" else orc.gemm_q4
+    gemm = orc.gemm_q4 if fmt == "q4" else orc.gemm_q8
     g = gemm(gq, gs, x, n, threads=8, mode=1)
     u = gemm(uq, us, x, n, threads=8, mode=1)
     h_ref = orc.silu_mul(g, u)
     h = torch.empty((n, rows), device="cuda")
     ud = torch.empty((n, rows), device="cuda")
-    f = D.gate_up_q8 if fmt == "q8" else D.gate_up_q4
+    f = {"q4": D.gate_up_q4, "q8": D.gate_up_q8, "q8h": D.gate_up_q8h}[fmt]
+    if fmt == "q8h":
+        gs, us = half_scales(gs), half_scales(us)
     f(dev(gq), dev(gs), dev(uq), dev(us), dev(x), h, rows, cols, n, u=ud)
     assert np.array_equal(bits(host(ud)), bits(u))
     hh = host(h)
