@@ -13,13 +13,15 @@
 //   rows, taken round-robin over a persistent grid sized to what stays
 //   resident, so each workgroup quantizes x once and then streams.
 // * A tile is read in 1 KB chunks per row (32 Q8 blocks or 64 Q4 blocks):
-//   one wave instruction loads 1 KB of one row with 16-byte lanes. Loads go
-//   through a ring of 16 units (row-chunks; 8 for one-row tiles) per wave:
-//   the next ring slots are refilled as soon as a chunk is turned into lane
-//   sums, so about 16 KB per wave stays in flight while the wave runs its
-//   FMA chains. The first
-//   chunks are requested while the prologue quantizes x, so the two
-//   latencies overlap.
+//   one wave instruction loads 1 KB of one row with 16-byte lanes, marked
+//   non-temporal. Loads go through a ring of row-chunks per wave: tiles of
+//   8+ rows keep one tile-chunk (8 KB) in flight and refill each slot as
+//   soon as it is turned into lane sums; smaller tiles keep 16 slots and
+//   refill a group at a time. The first chunks are requested while the
+//   prologue quantizes x, so the two latencies overlap.
+// * Outputs are held in one register across the wave's lanes and stored
+//   after the loop: loads and stores share one wait counter, and a store in
+//   the loop would make every later wait drain the ring.
 // * Lane sums (as floats; exact below 2^24) and per-block scales go to the
 //   wave's own LDS; lanes (t, row, l) then run the chunk's FMA chains and a
 //   DPP lane combine gives each row.
@@ -98,8 +100,12 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
   constexpr int RR = R * M;                   // weight rows per tile
   constexpr int CH = NT * RR * 4;             // chain lanes per tile
   static_assert(CH <= 64, "a tile's chains must fit one wave");
-  constexpr int G = RR >= 16 ? 1 : RR >= 2 ? 16 / RR : 8;  // chunk groups per ring batch
+  constexpr int G = RR >= 8 ? 1 : RR >= 2 ? 16 / RR : 8;  // chunk groups per ring batch
+  // Tiles of 8+ rows refill each ring slot as soon as it is consumed (one
+  // group of RR slots, 4 waves per SIMD); smaller tiles refill a group at a
+  // time from a ring of 16 (measured faster for each).
   constexpr int Q = RR * G;                   // ring slots (row-chunks in flight)
+  constexpr bool kFine = G == 1;
 
   extern __shared__ __align__(16) unsigned char lds[];
   const int cols = p.cols, B = cols / kBlock, n = p.n;
@@ -126,16 +132,15 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
   using ScaleBits = std::conditional_t<kHalf, short, int>;
   ScaleBits swb[Q];
 
-  // Requests the RR row-chunks of chunk c of this wave's k-th tile into ring
-  // slots [s0, s0 + RR) with buffer loads bounded by the row: blocks past
+  // Requests row-chunk i of chunk c of this wave's k-th tile into ring slot
+  // s0 + i (issue: all RR of them) with buffer loads bounded by the row: blocks past
   // the row, rows past the matrix and tiles past this wave's last read as
   // zeros without a memory access (their results are never stored), so the
   // issue has no branch.
-  auto issue = [&](const int s0, const int k, const int c) {
+  auto issue1 = [&](const int s0, const int k, const int c, const int i) {
     const int tile = tile0 + k * stride;
     const int blk = c * CB + lblk;
-#pragma unroll
-    for (int i = 0; i < RR; i++) {
+    {
       const int m = i / R, r = i - (i / R) * R;
       const int row = tile * R + r;
       const bool live = k < my_tiles && row < p.rows;
@@ -161,6 +166,10 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
         }
       }
     }
+  };
+  auto issue = [&](const int s0, const int k, const int c) {
+#pragma unroll
+    for (int i = 0; i < RR; i++) issue1(s0, k, c, i);
   };
   // Next chunk group: the following chunk of the tile, or the next tile.
   auto advance = [&](int& k, int& c) {
@@ -292,9 +301,10 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
             *sp = ok ? sb : 0.0f;  // both lanes of the block: the same value
           }
         }
+        if (kFine) issue1(g * RR, pk, pc, i);  // the slot is free: refill it now
       }
       // Refill these ring slots with the chunk group one batch ahead.
-      issue(g * RR, pk, pc);
+      if (!kFine) issue(g * RR, pk, pc);
       advance(pk, pc);
       if (!p.full || cc == chunks - 1) {
         // The FMA chains, in block order: over this chunk, or (full-K tiles)
@@ -413,7 +423,7 @@ size_t lds_for(bool q4, int R, int nt, bool pair, int cols, int stride) {
 }
 
 // Ring slots per wave (the kernel's Q) for RR rows per tile.
-int ring_units(int RR) { return RR >= 16 ? RR : RR >= 2 ? 16 : 8; }
+int ring_units(int RR) { return RR >= 8 ? RR : RR >= 2 ? 16 : 8; }
 
 template <int F, int R, int NT, bool kPair, bool kArgmax>
 int launch(GemvParams& p, hipStream_t stream) {
