@@ -27,9 +27,9 @@
 //   DPP lane combine gives each row.
 // * Fusions: the gate/up pair of an MLP shares x and finishes with the
 //   SiLU(gate) * up glue (shard.dart:457-461); an LM head can finish with
-//   the greedy argmax (sampler.dart:137-143): workgroups fold their best
-//   rank into 32 words with 64-bit atomic max, and a one-wave kernel after
-//   the GEMV writes the token.
+//   the greedy argmax (sampler.dart:137-143): each workgroup folds its best
+//   rank into a workspace slot with a 64-bit atomic max, and a
+//   one-workgroup kernel after the GEMV reduces the slots to the token.
 
 #include <type_traits>
 
@@ -46,15 +46,14 @@ constexpr int kWaves = 4;
 // with the GGUF Q8_0 block's own fp16 scale (34 B per 32 weights, not 36).
 constexpr int kFmtQ8 = 0, kFmtQ4 = 1, kFmtQ8H = 2;
 // Fused argmax. A rank orders (value, lowest index): argmax_key's 32-bit
-// value order above the complemented row. Each workgroup folds its waves'
-// ranks into one of kArgmaxGroups workspace words (128 B apart, so the
-// atomics of different groups go to different channels) with a 64-bit
-// atomic max that nothing waits for; a one-wave finisher launched after the
-// GEMV on the same stream reads and clears the words and writes the token.
-// The kernel boundary orders the atomics before the reads, so no memory
-// fence and no arrival count is needed, and no atomic is ever retried.
-constexpr int kArgmaxGroups = 32;
-constexpr int kArgmaxStride = 16;  // words between group words
+// value order above the complemented row. Workgroup b folds its waves' best
+// rank into workspace slot b % kArgmaxSlots with a 64-bit atomic max that
+// nothing waits for (slots are shared only by grids above kArgmaxSlots
+// workgroups); a one-workgroup finisher launched after the GEMV on the same
+// stream reads and clears the slots with plain loads and stores and writes
+// the token. The kernel boundary orders the atomics before those reads, so
+// no fence, no arrival count and no atomic retry is needed.
+constexpr int kArgmaxSlots = 2048;
 
 DNX_DEV uint64_t argmax_rank(float v, uint32_t row) {
   // A NaN at index 0 is the answer whatever follows (every comparison with
@@ -72,7 +71,8 @@ struct GemvParams {
   int tiles;                   // ceil(rows / R)
   int full;                    // 1: a tile's whole K goes to LDS before its chains run
   int stride;                  // LDS floats per chain: span of blocks + 4
-  unsigned long long* ws;      // argmax: the group words, zero between calls
+  unsigned long long* ws;      // argmax: the rank slots, zero between calls
+  int grid;                    // set by the launch
 };
 
 // Orders LDS writes and reads among the lanes of one wave (a wave's LDS
@@ -378,26 +378,41 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
       uint64_t b = red[0];
       for (int w = 1; w < kWaves; w++) b = red[w] > b ? red[w] : b;
       if (b != 0) {
-        __hip_atomic_fetch_max(&p.ws[(blockIdx.x % kArgmaxGroups) * kArgmaxStride],
-                               (unsigned long long)b, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_max(&p.ws[blockIdx.x % kArgmaxSlots], (unsigned long long)b,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
 }
 
-// The fused argmax's last step: the best of the group words (clearing each
-// for the next call) -> the token. Rank 0 means no value was a number: 0.
-__global__ void __launch_bounds__(64) argmax_finish_kernel(unsigned long long* ws,
-                                                           int64_t* out) {
-  const int lane = threadIdx.x;
-  uint64_t r = 0;
-  if (lane < kArgmaxGroups) {
-    r = __hip_atomic_exchange(&ws[lane * kArgmaxStride], 0ull, __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
+// The fused argmax's last step: the best of the first `slots` workspace
+// slots (clearing each for the next call) -> the token. Rank 0 means no value
+// was a number: index 0.
+__global__ void __launch_bounds__(kThreads) argmax_finish_kernel(unsigned long long* ws,
+                                                                 int slots, int64_t* out) {
+  const int tid = threadIdx.x;
+  constexpr int kPer = kArgmaxSlots / kThreads;
+  uint64_t v[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; j++) {  // all loads in flight at once
+    const int i = j * kThreads + tid;
+    v[j] = i < slots ? ws[i] : 0;
   }
+  uint64_t r = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; j++) {
+    const int i = j * kThreads + tid;
+    r = v[j] > r ? v[j] : r;
+    if (i < slots) ws[i] = 0;
+  }
+  __shared__ uint64_t red[kWaves];
   r = wave_max_u64(r);
-  if (lane == 0) *out = r == 0 ? 0 : (int64_t)(0xffffffffu - (uint32_t)(r & 0xffffffffu));
+  if ((tid & 63) == 0) red[tid >> 6] = r;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kWaves; w++) r = red[w] > r ? red[w] : r;
+    *out = r == 0 ? 0 : (int64_t)(0xffffffffu - (uint32_t)(r & 0xffffffffu));
+  }
 }
 
 // ------------------------------------------------------------ launch
@@ -461,6 +476,7 @@ int launch(GemvParams& p, hipStream_t stream) {
   const int floor_grid = (p.tiles + kWaves * per_wave - 1) / (kWaves * per_wave);
   if (cap < floor_grid) cap = floor_grid;
   const int grid = need < cap ? need : cap;
+  p.grid = grid;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), lds, stream, p);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
@@ -524,7 +540,8 @@ int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, con
   if (kArgmax) {
     const int rc = launch_nt<F, 1, false, true>(p, R, stream);
     if (rc != DNX_OK) return rc;
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(64), 0, stream, ws, out);
+    const int slots = p.grid < kArgmaxSlots ? p.grid : kArgmaxSlots;
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(kThreads), 0, stream, ws, slots, out);
     return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
   }
   switch (nt) {
@@ -598,8 +615,6 @@ int dnx_gate_up_q8h(const int8_t* gate_qs, const uint16_t* gate_scales, const in
                                     n, nullptr, nullptr, stream);
 }
 
-int64_t dnx_gemv_argmax_workspace_bytes(void) {
-  return (int64_t)kArgmaxGroups * kArgmaxStride * 8;
-}
+int64_t dnx_gemv_argmax_workspace_bytes(void) { return (int64_t)kArgmaxSlots * 8; }
 
 }  // extern "C"

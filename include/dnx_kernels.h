@@ -53,7 +53,7 @@ int dnx_gemv_q4(const uint8_t* qs, const uint16_t* scales, const float* x, float
 // workspace: dnx_gemv_argmax_workspace_bytes() bytes, zero before its first
 // use; every completed call leaves it zero again (the call's last kernel
 // clears it). Calls sharing one workspace must not overlap. Two launches on
-// `stream`: the GEMV, then a one-wave kernel that writes *out.
+// `stream`: the GEMV, then a one-workgroup kernel that writes *out.
 int64_t dnx_gemv_argmax_workspace_bytes(void);
 int dnx_gemv_q8_argmax(const int8_t* qs, const float* scales, const float* x, float* y,
                        int64_t rows, int64_t cols, int64_t* out, void* workspace,
