@@ -41,6 +41,7 @@ SIGNATURES = {
     "lab_gpu_enc_argmax": ([_i64] * 5, None),
     "lab_gpu_enc_gelu": ([_i64] * 3, None),
     "lab_gpu_set_profiling": ([_i64], None),
+    "lab_gpu_set_int8_inputs": ([_i64], _i64),
     "lab_gpu_profile": ([_p, _p, _i64], _i64),
     "lab_gpu_set_decode_rows": ([_i64], None),
     "lab_gpu_set_q8_group": ([_i64], _i64),
@@ -61,6 +62,8 @@ SIGNATURES = {
     "dnx_gemv_q4_argmax": ([_p, _p, _p, _p, _i64, _i64, _p, _p, _p], _i32),
     "dnx_gate_up_q8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gate_up_q4": ([_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dnx_gemv_q8_float": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dnx_gemv_q4_float": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemv_q8h": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemv_q8h_argmax": ([_p, _p, _p, _p, _i64, _i64, _p, _p, _p], _i32),
     "dnx_gate_up_q8h": ([_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),

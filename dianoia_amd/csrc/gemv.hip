@@ -91,8 +91,12 @@ DNX_DEV float silu_mul(float g, float u) {
   return s * u;
 }
 
-template <int F, int R, int NT, bool kPair, bool kArgmax>
+template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF>
 __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
+  // kF: float inputs (lab_gemm_q8 / lab_gemm_q4 mode 0): x is not quantized;
+  // per block, lane l sums fma(float(w_j), x_j, s) over j = 4k + l, k = 0..7
+  // in order (dot_q8_f32 lab_native.c:489-501, dot_q4_f32 :1013-1023), and
+  // the chains run acc_l = fma(s_l, sw, acc_l) on the weight scale alone.
   constexpr bool kQ4 = F == kFmtQ4;
   constexpr bool kHalf = F != kFmtQ8;          // fp16 block scales
   constexpr int CB = kQ4 ? 64 : 32;           // blocks per 1 KB chunk of a row
@@ -112,11 +116,16 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar bookkeeping
 
+  // x in LDS. int8 inputs: sxq [NT][cols], sxs [NT][B], Q4 sxsum [NT][B][4].
+  // Float inputs: sxf [NT][B][4][8], x[t][32b + 4k + l] at [t][b][l][k], so
+  // that one lane-sum chain reads 8 consecutive floats.
   int8_t* sxq = (int8_t*)lds;                              // [NT][cols]
   float* sxs = (float*)(lds + NT * cols);                  // [NT][B]
   int* sxsum = (int*)(sxs + ((NT * B + 3) & ~3));          // Q4: [NT][B][4]
+  float* sxf = (float*)lds;
   const int CP = p.stride;  // floats per chain: a chunk (or the whole K) + 4
-  float* sf = (float*)(sxsum + (kQ4 ? NT * B * 4 : 0)) + wave * (NT * RR * 5 * CP);
+  float* sf = (kF ? sxf + NT * cols : (float*)(sxsum + (kQ4 ? NT * B * 4 : 0))) +
+              wave * (NT * RR * 5 * CP);
   float* ss = sf + NT * RR * 4 * CP;                       // [NT][RR][CP]
 
   const int chunks = (B + CB - 1) / CB;
@@ -208,6 +217,15 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
       const int q = q0 + j * kThreads + tid;
       if (q >= quads) break;  // whole 8-lane groups: quads is a multiple of 8
       const int c = q * 4;
+      if (kF) {
+        // quad q is k = q % 8 of block q / 8, l = 0..3
+        float* d = sxf + (t * B + (q >> 3)) * 32 + (q & 7);
+        d[0] = v[j].x;
+        d[8] = v[j].y;
+        d[16] = v[j].z;
+        d[24] = v[j].w;
+        continue;
+      }
       const float amax = group8_max(fmaxf(0.0f, max4abs(v[j])));
       const float scale = q8_scale(amax);
       const int packed = quant4(v[j], q8_inv(scale));
@@ -269,7 +287,63 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
         for (int t = 0; t < NT; t++) {
           float* f = sf + ((t * RR + i) * 4) * CP + at;
           float* sp = ss + (t * RR + i) * CP + at;
-          if (kQ4) {
+          if (kF && kQ4) {
+            // Lane = block. Weight 4k + l: low nibble of byte 4k + l for
+            // k < 4, high nibble of byte 4(k - 4) + l after.
+            const uint32_t lo[4] = {w.x & 0x0f0f0f0fu, w.y & 0x0f0f0f0fu, w.z & 0x0f0f0f0fu,
+                                    w.w & 0x0f0f0f0fu};
+            const uint32_t hi[4] = {(w.x >> 4) & 0x0f0f0f0fu, (w.y >> 4) & 0x0f0f0f0fu,
+                                    (w.z >> 4) & 0x0f0f0f0fu, (w.w >> 4) & 0x0f0f0f0fu};
+            const float* xb = sxf + (t * B + blk) * 32;
+#pragma unroll
+            for (int l = 0; l < 4; l++) {
+              const float4 xa = *(const float4*)(xb + l * 8);
+              const float4 xc = *(const float4*)(xb + l * 8 + 4);
+              const int sh = 8 * l;
+              float sl = fmaf((float)((lo[0] >> sh) & 0xffu) - 8.0f, xa.x, 0.0f);
+              sl = fmaf((float)((lo[1] >> sh) & 0xffu) - 8.0f, xa.y, sl);
+              sl = fmaf((float)((lo[2] >> sh) & 0xffu) - 8.0f, xa.z, sl);
+              sl = fmaf((float)((lo[3] >> sh) & 0xffu) - 8.0f, xa.w, sl);
+              sl = fmaf((float)((hi[0] >> sh) & 0xffu) - 8.0f, xc.x, sl);
+              sl = fmaf((float)((hi[1] >> sh) & 0xffu) - 8.0f, xc.y, sl);
+              sl = fmaf((float)((hi[2] >> sh) & 0xffu) - 8.0f, xc.z, sl);
+              sl = fmaf((float)((hi[3] >> sh) & 0xffu) - 8.0f, xc.w, sl);
+              f[l * CP] = ok ? sl : 0.0f;
+            }
+            *sp = ok ? swi : 0.0f;
+          } else if (kF) {
+            // Q8, two lanes per block: lane h holds bytes 16h..16h+15 (k =
+            // 4h..4h+3 of every l) and takes lanes l = 2h, 2h + 1. Each lane
+            // keeps bytes 2h, 2h + 1 of its dwords and gives the partner the
+            // other two, so both end with all 8 k of their two l.
+            const int h = lane & 1;
+            const uint32_t keep = h ? 0x07060302u : 0x05040100u;
+            const uint32_t give = h ? 0x05040100u : 0x07060302u;
+            const uint32_t k0 = __builtin_amdgcn_perm(w.y, w.x, keep);
+            const uint32_t k1 = __builtin_amdgcn_perm(w.w, w.z, keep);
+            const uint32_t r0 = (uint32_t)dpp<kQuadXor1>((int)__builtin_amdgcn_perm(w.y, w.x, give));
+            const uint32_t r1 = (uint32_t)dpp<kQuadXor1>((int)__builtin_amdgcn_perm(w.w, w.z, give));
+            const uint32_t a0 = h ? r0 : k0, a1 = h ? r1 : k1;  // k = 0..3
+            const uint32_t c0 = h ? k0 : r0, c1 = h ? k1 : r1;  // k = 4..7
+            const float* xl = sxf + (t * B + blk) * 32 + 2 * h * 8;
+            float* fh = f + 2 * h * CP;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {  // l = 2h + e: bytes e and e + 2 of each word
+              const float4 xa = *(const float4*)(xl + e * 8);
+              const float4 xc = *(const float4*)(xl + e * 8 + 4);
+              const int s0 = 8 * e, s1 = 8 * e + 16;
+              float sl = fmaf((float)(int8_t)(a0 >> s0), xa.x, 0.0f);
+              sl = fmaf((float)(int8_t)(a0 >> s1), xa.y, sl);
+              sl = fmaf((float)(int8_t)(a1 >> s0), xa.z, sl);
+              sl = fmaf((float)(int8_t)(a1 >> s1), xa.w, sl);
+              sl = fmaf((float)(int8_t)(c0 >> s0), xc.x, sl);
+              sl = fmaf((float)(int8_t)(c0 >> s1), xc.y, sl);
+              sl = fmaf((float)(int8_t)(c1 >> s0), xc.z, sl);
+              sl = fmaf((float)(int8_t)(c1 >> s1), xc.w, sl);
+              fh[e * CP] = ok ? sl : 0.0f;
+            }
+            *sp = ok ? swi : 0.0f;  // both lanes of the block: the same value
+          } else if (kQ4) {
             const int4 xa = *(const int4*)(sxq + t * cols + blk * 32);
             const int4 xb = *(const int4*)(sxq + t * cols + blk * 32 + 16);
             const int4 c8 = *(const int4*)(sxsum + (t * B + blk) * 4);
@@ -431,16 +505,18 @@ int cu_count() {
 }
 
 // LDS of one workgroup for a chain stride (matches the carving in gemv_kernel).
-size_t lds_for(bool q4, int R, int nt, bool pair, int cols, int stride) {
+size_t lds_for(bool q4, bool fx, int R, int nt, bool pair, int cols, int stride) {
   const int RR = R * (pair ? 2 : 1), B = cols / kBlock;
-  return (size_t)nt * cols + 4 * (size_t)((nt * B + 3) & ~3) + (q4 ? (size_t)nt * B * 16 : 0) +
-         (size_t)kWaves * nt * RR * 5 * stride * 4;
+  const size_t x = fx ? (size_t)nt * cols * 4
+                      : (size_t)nt * cols + 4 * (size_t)((nt * B + 3) & ~3) +
+                            (q4 ? (size_t)nt * B * 16 : 0);
+  return x + (size_t)kWaves * nt * RR * 5 * stride * 4;
 }
 
 // Ring slots per wave (the kernel's Q) for RR rows per tile.
 int ring_units(int RR) { return RR >= 8 ? RR : RR >= 2 ? 16 : 8; }
 
-template <int F, int R, int NT, bool kPair, bool kArgmax>
+template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF>
 int launch(GemvParams& p, hipStream_t stream) {
   constexpr bool kQ4 = F == kFmtQ4;
   constexpr int CB = kQ4 ? 64 : 32, RR = R * (kPair ? 2 : 1);
@@ -448,11 +524,11 @@ int launch(GemvParams& p, hipStream_t stream) {
   // Full-K tiles when the whole tile fits the ring (small tiles, where the
   // chain per chunk would otherwise serialize with each chunk's latency).
   p.full = RR * chunks <= ring_units(RR) &&
-           lds_for(kQ4, R, NT, kPair, p.cols, chunks * CB + 4) <= 64 * 1024;
+           lds_for(kQ4, kF, R, NT, kPair, p.cols, chunks * CB + 4) <= 64 * 1024;
   p.stride = (p.full ? chunks * CB : CB) + 4;
-  const size_t lds = lds_for(kQ4, R, NT, kPair, p.cols, p.stride);
+  const size_t lds = lds_for(kQ4, kF, R, NT, kPair, p.cols, p.stride);
   if (lds > 64 * 1024) return DNX_EINVAL;  // x too wide for one workgroup's LDS
-  auto kernel = gemv_kernel<F, R, NT, kPair, kArgmax>;
+  auto kernel = gemv_kernel<F, R, NT, kPair, kArgmax, kF>;
   // Persistent grid: as many workgroups as stay resident (the occupancy is
   // looked up once per kernel and LDS size).
   static int cached_per_cu = 0;
@@ -484,34 +560,34 @@ int launch(GemvParams& p, hipStream_t stream) {
 // Rows per tile: the largest of 8 that still gives >= 2048
 // tiles (8 per CU), halving down to 1 for small matrices; bounded so a
 // tile's chains fit a wave and the workgroup's LDS stays within 64 KB.
-int pick_rows(bool q4, int rows, int nt, bool pair, int cols) {
+int pick_rows(bool q4, bool fx, int rows, int nt, bool pair, int cols) {
   int r = 8;  // 8 rows keep two chunk groups in the ring (measured faster than 16)
   while (r * nt * (pair ? 2 : 1) * 4 > 64) r /= 2;
   while (r > 1 && (rows + r - 1) / r < 2048) r /= 2;
-  while (r > 1 && lds_for(q4, r, nt, pair, cols, (q4 ? 64 : 32) + 4) > 64 * 1024) r /= 2;
+  while (r > 1 && lds_for(q4, fx, r, nt, pair, cols, (q4 ? 64 : 32) + 4) > 64 * 1024) r /= 2;
   return r;
 }
 
-template <int F, int NT, bool kPair, bool kArgmax>
+template <int F, int NT, bool kPair, bool kArgmax, bool kF>
 int launch_nt(GemvParams& p, int R, hipStream_t stream) {
   constexpr int RR_MAX = 16 / (NT * (kPair ? 2 : 1));
   switch (R) {
     case 8:
-      if constexpr (RR_MAX >= 8) return launch<F, 8, NT, kPair, kArgmax>(p, stream);
+      if constexpr (RR_MAX >= 8) return launch<F, 8, NT, kPair, kArgmax, kF>(p, stream);
       break;
     case 4:
-      if constexpr (RR_MAX >= 4) return launch<F, 4, NT, kPair, kArgmax>(p, stream);
+      if constexpr (RR_MAX >= 4) return launch<F, 4, NT, kPair, kArgmax, kF>(p, stream);
       break;
     case 2:
-      if constexpr (RR_MAX >= 2) return launch<F, 2, NT, kPair, kArgmax>(p, stream);
+      if constexpr (RR_MAX >= 2) return launch<F, 2, NT, kPair, kArgmax, kF>(p, stream);
       break;
     case 1:
-      return launch<F, 1, NT, kPair, kArgmax>(p, stream);
+      return launch<F, 1, NT, kPair, kArgmax, kF>(p, stream);
   }
   return DNX_EINVAL;
 }
 
-template <int F, bool kPair, bool kArgmax>
+template <int F, bool kPair, bool kArgmax, bool kF = false>
 int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, const float* x,
          float* y, float* y2, int64_t rows, int64_t cols, int64_t n, unsigned long long* ws,
          int64_t* out, hipStream_t stream) {
@@ -536,19 +612,41 @@ int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, con
   p.n = (int)n;
   p.ws = ws;
   const int nt = n == 1 ? 1 : n == 2 ? 2 : 4;
-  const int R = pick_rows(kQ4, (int)rows, nt, kPair, (int)cols);
+  const int R = pick_rows(kQ4, kF, (int)rows, nt, kPair, (int)cols);
   if (kArgmax) {
-    const int rc = launch_nt<F, 1, false, true>(p, R, stream);
+    const int rc = launch_nt<F, 1, false, true, false>(p, R, stream);
     if (rc != DNX_OK) return rc;
     const int slots = p.grid < kArgmaxSlots ? p.grid : kArgmaxSlots;
     hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(kThreads), 0, stream, ws, slots, out);
     return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
   }
   switch (nt) {
-    case 1: return launch_nt<F, 1, kPair, false>(p, R, stream);
-    case 2: return launch_nt<F, 2, kPair, false>(p, R, stream);
-    default: return launch_nt<F, 4, kPair, false>(p, R, stream);
+    case 1: return launch_nt<F, 1, kPair, false, kF>(p, R, stream);
+    case 2: return launch_nt<F, 2, kPair, false, kF>(p, R, stream);
+    default: return launch_nt<F, 4, kPair, false, kF>(p, R, stream);
   }
+}
+
+// Float inputs (mode 0), any n: launches of up to 4 tokens each.
+template <int F>
+int gemv_float(const void* qs, const void* scales, const float* x, float* y, int64_t rows,
+               int64_t cols, int64_t n, hipStream_t stream) {
+  if (n <= 0 || cols <= 0 || cols % kBlock != 0 || cols > (1 << 20)) return DNX_EINVAL;
+  // Tokens per launch: 4, or fewer when their fp32 x would not fit the LDS.
+  constexpr bool kQ4 = F == kFmtQ4;
+  int group = 4;
+  while (group > 1 &&
+         lds_for(kQ4, true, 1, group, false, (int)cols, (kQ4 ? 64 : 32) + 4) > 64 * 1024) {
+    group /= 2;
+  }
+  for (int64_t t0 = 0; t0 < n; t0 += group) {
+    const int64_t nt = n - t0 < group ? n - t0 : group;
+    const int rc = gemv<F, false, false, true>(qs, scales, nullptr, nullptr, x + t0 * cols,
+                                              y + t0 * rows, nullptr, rows, cols, nt, nullptr,
+                                              nullptr, stream);
+    if (rc != DNX_OK) return rc;
+  }
+  return DNX_OK;
 }
 
 }  // namespace
@@ -593,6 +691,16 @@ int dnx_gate_up_q4(const uint8_t* gate_qs, const uint16_t* gate_scales, const ui
                    int64_t cols, int64_t n, hipStream_t stream) {
   return gemv<kFmtQ4, true, false>(gate_qs, gate_scales, up_qs, up_scales, x, h, u, rows, cols, n,
                                  nullptr, nullptr, stream);
+}
+
+int dnx_gemv_q8_float(const int8_t* qs, const float* scales, const float* x, float* y,
+                      int64_t rows, int64_t cols, int64_t n, hipStream_t stream) {
+  return gemv_float<kFmtQ8>(qs, scales, x, y, rows, cols, n, stream);
+}
+
+int dnx_gemv_q4_float(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
+                      int64_t rows, int64_t cols, int64_t n, hipStream_t stream) {
+  return gemv_float<kFmtQ4>(qs, scales, x, y, rows, cols, n, stream);
 }
 
 int dnx_gemv_q8h(const int8_t* qs, const uint16_t* scales, const float* x, float* y,

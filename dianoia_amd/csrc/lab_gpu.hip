@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include <unistd.h>
 
@@ -61,6 +62,7 @@ enum Op { kOpMatmulQ8, kOpMatmulQ4, kOpSwiglu, kOpQuantize, kOpQuantizeBf16, kOp
 struct Cmd {
   Op op;
   int64_t a[10];
+  bool int8_inputs;  // matmuls: the input mode when the command was recorded
 };
 
 struct Region {
@@ -68,6 +70,11 @@ struct Region {
 };
 
 bool gReady = false;
+// Matmul input mode. Int8 inputs (the default): x quantized per block as
+// lab_quantize_q8 does, as the Vulkan layer does on a device with integer
+// dot products (lab_vulkan.c:842-858) and lab_gemm_* mode 1. Float inputs:
+// x used as given, as the Metal layer does and lab_gemm_* mode 0.
+bool gInt8Inputs = true;
 hipStream_t gStream;
 hipEvent_t gStart, gStop;
 hipEvent_t gProfEvents[kMaxProfiled];
@@ -220,6 +227,7 @@ bool wait_pending() {
 void record(Op op, std::initializer_list<int64_t> args) {
   Cmd c;
   c.op = op;
+  c.int8_inputs = gInt8Inputs;
   int i = 0;
   for (int64_t v : args) c.a[i++] = v;
   gCmds.push_back(c);
@@ -239,6 +247,17 @@ bool run_matmul(const Cmd& c, bool q4) {
   float* ys = (float*)dev_at(y, yOff);
   int rc;
   rc = DNX_EINVAL;
+  if (!c.int8_inputs) {  // float inputs: the exact mode-0 GEMV, any n
+    rc = q4 ? dnx_gemv_q4_float((const uint8_t*)qs, (const uint16_t*)sc, xs, ys, rows, cols, n,
+                                gStream)
+            : dnx_gemv_q8_float((const int8_t*)qs, (const float*)sc, xs, ys, rows, cols, n,
+                                gStream);
+    if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4 : kKindGemvQ8);
+    wrote_region(y, yOff, n * rows * 4);
+    if (rc != DNX_OK) LOG("float-input matmul %s %ldx%ld n=%ld failed (%d)\n", q4 ? "q4" : "q8",
+                          (long)rows, (long)cols, (long)n, rc);
+    return rc == DNX_OK;
+  }
   if (n <= 4) {
     rc = q4 ? dnx_gemv_q4((const uint8_t*)qs, (const uint16_t*)sc, xs, ys, rows, cols, n,
                           gStream)
@@ -272,7 +291,7 @@ bool fusable_pair(const Cmd& a, const Cmd& b, const Cmd& c) {
     return false;
   }
   const int64_t n = a.a[9], rows = a.a[7];
-  return n <= 4 && a.a[3] == b.a[3] && a.a[4] == b.a[4] && a.a[7] == b.a[7] &&
+  return a.int8_inputs && b.int8_inputs && n <= 4 && a.a[3] == b.a[3] && a.a[4] == b.a[4] && a.a[7] == b.a[7] &&
          a.a[8] == b.a[8] && a.a[9] == b.a[9] && a.a[6] == 0 && b.a[6] == 0 &&
          a.a[5] != b.a[5] && c.a[0] == a.a[5] && c.a[1] == b.a[5] && c.a[2] == n * rows;
 }
@@ -304,7 +323,8 @@ bool run_pair(const Cmd& a, const Cmd& b) {
 
 // Fusion of a decode matmul (n = 1) and the argmax of its whole output.
 bool fusable_argmax(const Cmd& a, const Cmd& b) {
-  return (a.op == kOpMatmulQ8 || a.op == kOpMatmulQ4) && b.op == kOpArgmax && a.a[9] == 1 &&
+  return (a.op == kOpMatmulQ8 || a.op == kOpMatmulQ4) && a.int8_inputs && b.op == kOpArgmax &&
+         a.a[9] == 1 &&
          b.a[0] == a.a[5] && b.a[1] == a.a[6] && b.a[2] == a.a[7];
 }
 
@@ -417,6 +437,8 @@ int64_t lab_gpu_init(void) {
     LOG("scratch allocation failed\n");
     return 0;
   }
+  const char* mode = getenv("DIANOIA_GPU_INT8_INPUTS");
+  if (mode != nullptr && strcmp(mode, "0") == 0) gInt8Inputs = false;
   gReady = true;
   return 1;
 }
@@ -624,6 +646,12 @@ void lab_gpu_enc_gelu(int64_t x, int64_t xOffset, int64_t count) {
 }
 
 void lab_gpu_set_profiling(int64_t on) { gProfiling = on != 0; }
+
+int64_t lab_gpu_set_int8_inputs(int64_t on) {
+  const int64_t was = gInt8Inputs ? 1 : 0;
+  gInt8Inputs = on != 0;
+  return was;
+}
 
 int64_t lab_gpu_profile(double* ms, int64_t* counts, int64_t kinds) {
   for (int64_t k = 0; k < kinds && k < kKinds; k++) {

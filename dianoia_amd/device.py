@@ -55,6 +55,18 @@ def gemv_q4(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> 
                                    _stream(stream)), "dnx_gemv_q4")
 
 
+def gemv_q8_float(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> None:
+    """Float-input GEMV (lab_gemm_q8 mode 0), any n."""
+    _check(_lib.load().dnx_gemv_q8_float(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
+                                         _stream(stream)), "dnx_gemv_q8_float")
+
+
+def gemv_q4_float(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> None:
+    """Float-input GEMV (lab_gemm_q4 mode 0), any n."""
+    _check(_lib.load().dnx_gemv_q4_float(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
+                                         _stream(stream)), "dnx_gemv_q4_float")
+
+
 def gemv_argmax_workspace(device="cuda") -> torch.Tensor:
     """Zeroed workspace for the fused argmax GEMV; completed calls leave it zero."""
     nbytes = int(_lib.load().dnx_gemv_argmax_workspace_bytes())

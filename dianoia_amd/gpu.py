@@ -64,6 +64,14 @@ class _Matrix:
         f(self.buffer, self.qs, self.scales, x, x_offset, y, y_offset, self.rows, self.cols, n)
 
 
+def set_int8_inputs(on: bool) -> bool:
+    """Input mode of the matmuls recorded from now on (process-wide); returns
+    the previous one. True: x quantized per block (lab_gemm_* mode 1, the
+    Vulkan layer's path); False: float inputs (mode 0, the Metal layer's)."""
+    lib = _lib.load()
+    return bool(lib.lab_gpu_set_int8_inputs(1 if on else 0))
+
+
 def live_buffers() -> int:
     """GpuForward.liveBuffers (gpu.dart): buffers not yet released."""
     return int(_lib.load().lab_gpu_live_buffers())

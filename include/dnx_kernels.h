@@ -48,6 +48,18 @@ int dnx_gemv_q8(const int8_t* qs, const float* scales, const float* x, float* y,
 int dnx_gemv_q4(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
                 int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
 
+// Float-input products, any n: lab_gemm_q8 / lab_gemm_q4 mode 0
+// (dot_q8_f32 lab_native.c:489-501, dot_q4_f32 :1013-1023, lab_gemm_q8
+// :553-579), x used as given (not quantized), in the CPU's exact float order:
+// y is bit-identical to theirs. One launch per group of up to 4 tokens
+// (each reads the weights once); the group shrinks to 2 or 1 token when the
+// group's fp32 x would not fit the workgroup's 64 KB of LDS (DNX_EINVAL when
+// even one row does not: cols above about 14000).
+int dnx_gemv_q8_float(const int8_t* qs, const float* scales, const float* x, float* y,
+                      int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
+int dnx_gemv_q4_float(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
+                      int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
+
 // The decode GEMV with the greedy argmax fused (argmaxToken, lib/src/
 // sampler.dart:137-152, over y): writes y and the token index to *out.
 // workspace: dnx_gemv_argmax_workspace_bytes() bytes, zero before its first

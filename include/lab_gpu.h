@@ -68,16 +68,30 @@ double lab_gpu_last_ms(void);
 // lab_gpu_enc_matmul_q8 / _q4 (lab_vulkan.c:877-890; gpu.dart:125-177):
 // Y[n][rows] = X[n][cols] W^T, W inside buffer w at qsOffset / scalesOffset
 // in the engine's Q8 (int8 + fp32 scales) or Q4 (nibbles + fp16 scales)
-// layout, X at x + xOffset (fp32), Y at y + yOffset (fp32). The inputs are
-// quantized to Q8 per block as lab_native.c does (mode 1): for n <= 4 the
-// products are bit-identical to lab_gemm_q8 / lab_gemm_q4 mode 1; for larger
-// n they run on int8 MFMA within 1e-4 relative. qs must be 16-byte aligned.
+// layout, X at x + xOffset (fp32), Y at y + yOffset (fp32). By default the
+// inputs are quantized to Q8 per block as lab_native.c does (mode 1): for
+// n <= 4 the products are bit-identical to lab_gemm_q8 / lab_gemm_q4 mode 1;
+// for larger n they run on int8 MFMA within 1e-4 relative. With float inputs
+// (lab_gpu_set_int8_inputs below) they are bit-identical to mode 0 for every
+// n. qs must be 16-byte aligned.
 void lab_gpu_enc_matmul_q8(int64_t w, int64_t qsOffset, int64_t scalesOffset, int64_t x,
                            int64_t xOffset, int64_t y, int64_t yOffset, int64_t rows,
                            int64_t cols, int64_t n);
 void lab_gpu_enc_matmul_q4(int64_t w, int64_t qsOffset, int64_t scalesOffset, int64_t x,
                            int64_t xOffset, int64_t y, int64_t yOffset, int64_t rows,
                            int64_t cols, int64_t n);
+
+// Input mode of the matmuls recorded from now on; returns the previous mode
+// (1 int8, 0 float). No counterpart in the reference's ABI, where the layer
+// decides: the Vulkan layer quantizes the inputs per block on a device with
+// integer dot products (lab_vulkan.c:842-858), the Metal layer multiplies
+// float inputs (lab_metal.m:1025-1038). 1 (the default) is the Vulkan
+// behaviour above; 0 is the Metal one, and then the products are
+// bit-identical to lab_gemm_q8 / lab_gemm_q4 mode 0 for every n (what
+// GpuLinear documents, gpu.dart:1271-1275). The environment variable
+// DIANOIA_GPU_INT8_INPUTS=0 sets 0 at lab_gpu_init, for callers that cannot
+// call this. Float inputs are limited to rows of up to about 14000 columns.
+int64_t lab_gpu_set_int8_inputs(int64_t on);
 
 // lab_gpu_enc_swiglu (lab_vulkan.c:974-978; gpu.dart:179-312): g = SiLU(g)
 // * u over `count` floats from offset 0 of each buffer, SiLU in double as

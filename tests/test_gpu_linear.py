@@ -1,14 +1,15 @@
 """GpuLinear through the lab_gpu_* ABI: the reference's gpu_linear_test.dart
 cases (test/gpu_linear_test.dart:26-102), compared with the CPU kernels in
-mode 1 (the GPU path takes int8 inputs as lab_gemm_* mode 1 does), plus the
-configurations' end-to-end chains."""
+mode 1 (int8 inputs, the default) and, with float inputs, in mode 0 (what the
+reference's own test compares against), plus the configurations' end-to-end
+chains."""
 
 import numpy as np
 import pytest
 
 from dianoia_amd import ArgumentError, StateError, synth
 from dianoia_amd.formats import QuantMatrix
-from dianoia_amd.gpu import GpuLinear, live_buffers
+from dianoia_amd.gpu import GpuLinear, live_buffers, set_int8_inputs
 from gpu_util import bits, within_tolerance
 
 pytestmark = pytest.mark.gpu
@@ -221,3 +222,83 @@ def test_invalid_dispatch_fails_its_commit(gpu_ready):
         assert lib.lab_gpu_commit(1) == 1
     finally:
         lib.lab_gpu_release(h)
+
+
+# ------------------------------------------------------------ float inputs
+
+@pytest.fixture()
+def float_inputs(gpu_ready):
+    was = set_int8_inputs(False)
+    yield
+    set_int8_inputs(was)
+
+
+def cpu_mode0(orc, fmt, qs, sc, xs, n):
+    return (orc.gemm_q4 if fmt == "q4" else orc.gemm_q8)(qs, sc, xs, n, threads=4, mode=0)
+
+
+@pytest.mark.parametrize("fmt,rows,cols,n", [("q4", 64, 64, 1), ("q4", 70, 96, 13),
+                                             ("q8", 36, 64, 9), ("q8", 128, 128, 40)])
+def test_float_inputs_match_the_cpu_kernels(float_inputs, gpu, orc, fmt, rows, cols, n):
+    """The reference test as written: GPU vs CPU with float inputs, within
+    1e-4 + 1e-5 |cpu| (gpu_linear_test.dart:44); here also bit-exact."""
+    rng = np.random.default_rng(5)
+    m, qs, sc = quantized(orc, fmt, values(rng, rows * cols), rows, cols)
+    gpu.upload("m", m)
+    xs = values(rng, n * cols)
+    on_gpu = np.zeros(n * rows, np.float32)
+    gpu.apply("m", xs, on_gpu, n)
+    cpu = cpu_mode0(orc, fmt, qs, sc, xs, n).reshape(-1)
+    assert np.all(np.abs(on_gpu - cpu) <= 1e-4 + 1e-5 * np.abs(cpu))
+    assert np.array_equal(bits(on_gpu), bits(cpu))
+
+
+def test_float_inputs_grow_buffers_and_keep_matrices(float_inputs, gpu, orc):
+    rng = np.random.default_rng(6)
+    small, sq, ss = quantized(orc, "q4", values(rng, 32 * 32), 32, 32)
+    large, lq, ls = quantized(orc, "q4", values(rng, 64 * 256), 64, 256)
+    gpu.upload("small", small)
+    gpu.upload("large", large)
+    for name, (q, s), rows, cols, n in [("small", (sq, ss), 32, 32, 3),
+                                        ("large", (lq, ls), 64, 256, 50),
+                                        ("small", (sq, ss), 32, 32, 7)]:
+        xs = values(rng, n * cols)
+        on_gpu = np.zeros(n * rows, np.float32)
+        gpu.apply(name, xs, on_gpu, n)
+        assert np.array_equal(bits(on_gpu), bits(cpu_mode0(orc, "q4", q, s, xs, n).reshape(-1)))
+
+
+def test_float_inputs_mlp_and_lm_head(float_inputs, gpu, orc):
+    """With float inputs the MLP and the LM head run unfused (the fused
+    kernels take int8 inputs); gate, up and the logits are mode-0 exact, the
+    token is argmaxToken of them."""
+    (gq, gs), (uq, us), (dq, ds), x = synth.config1()
+    for name, (q, s) in (("gate", (gq, gs)), ("up", (uq, us)), ("down", (dq, ds))):
+        gpu.upload(name, QuantMatrix.q4(q, s))
+    y = np.zeros(2048, np.float32)
+    gpu.mlp("gate", "up", "down", x, y, 1)
+    g = orc.gemm_q4(gq, gs, x, 1, threads=8, mode=0)
+    u = orc.gemm_q4(uq, us, x, 1, threads=8, mode=0)
+    assert np.array_equal(bits(gpu._aux["u"].view(count=6144)), bits(u[0]))
+    h = orc.silu_mul(g, u)
+    ref = orc.gemm_q4(dq, ds, h, 1, threads=8, mode=0)[0]
+    ok, rel, ab = within_tolerance(y, ref)  # the glue may differ by 1 ulp (double exp)
+    assert ok, (rel, ab)
+    rng = np.random.default_rng(9)
+    qs, sc = synth.q8_weights(rng, 5000, 512)
+    gpu.upload("head", QuantMatrix.q8(qs, sc))
+    xs = synth.activations(rng, 1, 512)
+    logits = np.zeros(5000, np.float32)
+    token = gpu.apply_argmax("head", xs[0], logits)
+    want = orc.gemm_q8(qs, sc, xs, 1, threads=8, mode=0)[0]
+    assert np.array_equal(bits(logits), bits(want))
+    assert token == orc.argmax(want)
+
+
+def test_input_mode_switch_returns_previous(gpu_ready):
+    was = set_int8_inputs(False)
+    try:
+        assert set_int8_inputs(True) is False
+        assert set_int8_inputs(True) is True
+    finally:
+        set_int8_inputs(was)
