@@ -31,9 +31,15 @@ FLAGS = [
 ]
 
 
+# Per-source flags. The GEMM keeps its MFMA results in ordinary VGPRs: its
+# scale epilogue reads every result with VALU instructions, which cannot
+# take accumulation registers (one v_accvgpr_read per value otherwise).
+SOURCE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str, build_dir: str) -> str:
     obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")

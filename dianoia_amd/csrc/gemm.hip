@@ -84,48 +84,69 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
   const i32x4 rxs = buffer_rsrc(p.xsc, (uint32_t)((size_t)M * B * 4));
   const i32x4 rws = buffer_rsrc(p.scales, (uint32_t)((size_t)N * B * (kQ4 ? 2 : 4)));
 
+  // Per-thread offsets at stage 0 and each piece's block within a stage
+  // (kNever when its row lies past the matrix): a stage adds b0 blocks'
+  // bytes, and a piece whose block is past K reads zeros (offset -16 lies
+  // outside the buffer). 32-bit offsets: the launch refuses operands of 2 GB.
+  constexpr int kNever = 1 << 30;
+  int offA[AP], cA[AP], offB[BP], cB[BP], offX[SXP], cX[SXP], offW[SWP], cW[SWP];
+#pragma unroll
+  for (int i = 0; i < AP; i++) {
+    const int idx = i * kThreads + tid;
+    const int row = idx / (RB / 16), seg = idx - row * (RB / 16), m = m0 + row;
+    offA[i] = m * K + seg * 16;
+    cA[i] = idx < A16 && m < M ? seg / 2 : kNever;
+  }
+#pragma unroll
+  for (int i = 0; i < BP; i++) {
+    const int idx = i * kThreads + tid;
+    if (kQ4) {
+      const int row = idx / KB, kb = idx - row * KB, r = n0 + row;
+      offB[i] = r * (K / 2) + kb * 16;
+      cB[i] = idx < B16 && r < N ? kb : kNever;
+    } else {
+      const int row = idx / (RB / 16), seg = idx - row * (RB / 16), r = n0 + row;
+      offB[i] = r * K + seg * 16;
+      cB[i] = idx < B16 && r < N ? seg / 2 : kNever;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < SXP; i++) {
+    const int idx = i * kThreads + tid;
+    const int kb = idx / BM, m = m0 + idx - kb * BM;
+    offX[i] = (m * B + kb) * 4;
+    cX[i] = idx < KB * BM && m < M ? kb : kNever;
+  }
+#pragma unroll
+  for (int i = 0; i < SWP; i++) {
+    const int idx = i * kThreads + tid;
+    const int kb = idx / BN, r = n0 + idx - kb * BN;
+    offW[i] = (r * B + kb) * (kQ4 ? 2 : 4);
+    cW[i] = idx < KB * BN && r < N ? kb : kNever;
+  }
+
   auto load_stage = [&](int s) {
     const int b0 = s * KB;
 #pragma unroll
-    for (int i = 0; i < AP; i++) {
-      const int idx = i * kThreads + tid;
-      const int row = idx / (RB / 16), seg = idx - row * (RB / 16);
-      const int m = m0 + row, blk = b0 + seg / 2;
-      const bool ok = idx < A16 && m < M && blk < B;
-      ra[i] = buffer_load16(rxq, ok ? (int)((size_t)m * K + b0 * 32 + seg * 16) : -16);
-    }
+    for (int i = 0; i < AP; i++)
+      ra[i] = buffer_load16(rxq, b0 + cA[i] < B ? offA[i] + b0 * 32 : -16);
 #pragma unroll
-    for (int i = 0; i < BP; i++) {
-      const int idx = i * kThreads + tid;
-      if (kQ4) {
-        const int row = idx / KB, kb = idx - row * KB;
-        const int r = n0 + row, blk = b0 + kb;
-        const bool ok = idx < B16 && r < N && blk < B;
-        rb[i] = buffer_load16(rqs, ok ? (int)((size_t)r * (K / 2) + (size_t)blk * 16) : -16);
-      } else {
-        const int row = idx / (RB / 16), seg = idx - row * (RB / 16);
-        const int r = n0 + row, blk = b0 + seg / 2;
-        const bool ok = idx < B16 && r < N && blk < B;
-        rb[i] = buffer_load16(rqs, ok ? (int)((size_t)r * K + b0 * 32 + seg * 16) : -16);
-      }
-    }
+    for (int i = 0; i < BP; i++)
+      rb[i] = buffer_load16(rqs, b0 + cB[i] < B ? offB[i] + b0 * (kQ4 ? 16 : 32) : -16);
 #pragma unroll
     for (int i = 0; i < SXP; i++) {
-      const int idx = i * kThreads + tid;
-      const int kb = idx / BM, m = m0 + idx - kb * BM, blk = b0 + kb;
-      const bool ok = idx < KB * BM && m < M && blk < B;
-      rsx[i] = __int_as_float(dnx_raw_buffer_load_i32(rxs, ok ? (m * B + blk) * 4 : -4, 0, 0));
+      rsx[i] = __int_as_float(
+          dnx_raw_buffer_load_i32(rxs, b0 + cX[i] < B ? offX[i] + b0 * 4 : -4, 0, 0));
     }
 #pragma unroll
     for (int i = 0; i < SWP; i++) {
-      const int idx = i * kThreads + tid;
-      const int kb = idx / BN, r = n0 + idx - kb * BN, blk = b0 + kb;
-      const bool ok = idx < KB * BN && r < N && blk < B;
       if (kQ4) {
-        const short h = dnx_raw_buffer_load_i16(rws, ok ? (r * B + blk) * 2 : -2, 0, 0);
+        const short h =
+            dnx_raw_buffer_load_i16(rws, b0 + cW[i] < B ? offW[i] + b0 * 2 : -2, 0, 0);
         rsw[i] = __int_as_float((int)(uint16_t)h);  // bits; widened in store_stage
       } else {
-        rsw[i] = __int_as_float(dnx_raw_buffer_load_i32(rws, ok ? (r * B + blk) * 4 : -4, 0, 0));
+        rsw[i] = __int_as_float(
+            dnx_raw_buffer_load_i32(rws, b0 + cW[i] < B ? offW[i] + b0 * 4 : -4, 0, 0));
       }
     }
   };
