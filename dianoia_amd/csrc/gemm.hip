@@ -38,6 +38,8 @@ struct GemmParams {
   const float* xsc;
   float* y;
   int rows, cols, n;
+  int split_stages;  // K stages per split (blockIdx.z); all of K without split
+  float* part;       // split partials [splits][n][rows], or null: write y
 };
 
 // Q4 byte-dword of 4 nibble pairs -> two dwords of int8 weights q - 8:
@@ -203,14 +205,17 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
 
-  load_stage(0);
+  // This workgroup's K stages: all of them, or split blockIdx.z's share.
+  const int s_begin = blockIdx.z * p.split_stages;
+  const int s_end = min(stages, s_begin + p.split_stages);
+  load_stage(s_begin);
   store_stage(0);
   __syncthreads();
 
   const int lrow = lane & 31, lk = (lane >> 5) * 16;
-  for (int s = 0; s < stages; s++) {
-    const int buf = s & 1;
-    if (s + 1 < stages) load_stage(s + 1);
+  for (int s = s_begin; s < s_end; s++) {
+    const int buf = (s - s_begin) & 1;
+    if (s + 1 < s_end) load_stage(s + 1);
     const int nkb = min(KB, B - s * KB);
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
@@ -249,11 +254,12 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
         }
       }
     }
-    if (s + 1 < stages) store_stage(buf ^ 1);
+    if (s + 1 < s_end) store_stage(buf ^ 1);
     __syncthreads();
   }
 
   // Store: lane holds column n0 + wn*TN + j*32 + lane%32 for 16 rows.
+  float* out = p.part ? p.part + (size_t)blockIdx.z * M * N : p.y;
 #pragma unroll
   for (int i = 0; i < SM; i++)
 #pragma unroll
@@ -263,16 +269,75 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int m = m0 + wm * TM + i * 32 + (v / 4) * 8 + (lane >> 5) * 4 + (v % 4);
-        if (m < M) p.y[(size_t)m * N + r] = acc[i][j][v];
+        if (m < M) out[(size_t)m * N + r] = acc[i][j][v];
       }
     }
 }
 
+// y = the split partials summed in split order (deterministic).
+__global__ void __launch_bounds__(kThreads) splitk_reduce_kernel(const float* __restrict__ part,
+                                                                 float* __restrict__ y,
+                                                                 int64_t count, int splits) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * kThreads) {
+    float v = part[i];
+    for (int z = 1; z < splits; z++) v += part[(size_t)z * count + i];
+    y[i] = v;
+  }
+}
+
+// Library-owned split-K workspace (device 0 of this process), grown on
+// demand: the first call at a larger small-M shape allocates, so such a
+// call must not be the first one inside a graph capture.
+float* gSplitWs = nullptr;
+size_t gSplitBytes = 0;
+
+float* split_workspace(size_t bytes) {
+  if (bytes <= gSplitBytes) return gSplitWs;
+  if (gSplitWs != nullptr) {
+    if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+    (void)hipFree(gSplitWs);
+    gSplitWs = nullptr;
+    gSplitBytes = 0;
+  }
+  if (hipMalloc(&gSplitWs, bytes) != hipSuccess) {
+    gSplitWs = nullptr;
+    return nullptr;
+  }
+  gSplitBytes = bytes;
+  return gSplitWs;
+}
+
 template <bool kQ4, int BM, int BN, int WM, int KB>
-int launch_tile(const GemmParams& p, hipStream_t stream) {
-  const dim3 grid((unsigned)((p.rows + BN - 1) / BN), (unsigned)((p.n + BM - 1) / BM));
-  hipLaunchKernelGGL((gemm_kernel<kQ4, BM, BN, WM, KB>), grid, dim3(kThreads), 0, stream, p);
-  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+int launch_tile(GemmParams p, hipStream_t stream) {
+  const unsigned gx = (unsigned)((p.rows + BN - 1) / BN), gy = (unsigned)((p.n + BM - 1) / BM);
+  const int stages = (p.cols / kBlock + KB - 1) / KB;
+  // Split K when the tiles alone would leave CUs idle (small n): enough
+  // splits for about 512 workgroups, each with at least one stage.
+  int splits = 1;
+  const int64_t tiles = (int64_t)gx * gy;
+  if (tiles < 256 && stages > 1) {
+    splits = (int)((512 + tiles - 1) / tiles);
+    if (splits > stages) splits = stages;
+  }
+  p.split_stages = (stages + splits - 1) / splits;
+  splits = (stages + p.split_stages - 1) / p.split_stages;
+  p.part = nullptr;
+  const int64_t count = (int64_t)p.n * p.rows;
+  if (splits > 1) {
+    p.part = split_workspace((size_t)splits * count * 4);
+    if (p.part == nullptr) return DNX_ENOMEM;
+  }
+  hipLaunchKernelGGL((gemm_kernel<kQ4, BM, BN, WM, KB>), dim3(gx, gy, (unsigned)splits),
+                     dim3(kThreads), 0, stream, p);
+  if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+  if (splits > 1) {
+    const int64_t blocks = (count + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)),
+                       dim3(kThreads), 0, stream, p.part, p.y, count, splits);
+    if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+  }
+  return DNX_OK;
 }
 
 template <bool kQ4>
@@ -282,7 +347,7 @@ int launch_gemm(const void* qs, const void* scales, const int8_t* xq, const floa
   // Buffer-load offsets are 32-bit: each operand must stay below 2 GB.
   if (rows * (kQ4 ? cols / 2 : cols) >= (1ll << 31) || n * cols >= (1ll << 31)) return DNX_EINVAL;
   if (((uintptr_t)qs & 15) || ((uintptr_t)xq & 15) || (cols % 16)) return DNX_EINVAL;
-  GemmParams p{qs, scales, xq, xsc, y, (int)rows, (int)cols, (int)n};
+  GemmParams p{qs, scales, xq, xsc, y, (int)rows, (int)cols, (int)n, 0, nullptr};
   // 32 tokens: one wave row of 32 x 32 tiles (4 waves across N); else
   // 64 x 64 tiles (2 x 2 waves), which keep ~3 workgroups per CU resident
   // at prefill sizes.

@@ -102,7 +102,12 @@ int dnx_gate_up_q8h(const int8_t* gate_qs, const uint16_t* gate_scales, const in
 // Prefill / encoder GEMM on int8 MFMA, any n, inputs already quantized
 // (xq int8 [n][cols], xsc fp32 [n][cols/32], e.g. by dnx_quantize_q8):
 // the per-32-block int32 dots are exact, the per-block scaling is fp32
-// (within 1e-4 relative of the CPU kernels, not bit-identical).
+// (within 1e-4 relative of the CPU kernels, not bit-identical; the same
+// inputs always give the same bits). When n is small (fewer than 256 output
+// tiles) K is split across workgroups and a second kernel sums the partials
+// in a fixed order; their workspace is the library's own, allocated on the
+// first such call at a larger shape (so that call must not be captured into
+// a graph).
 int dnx_gemm_q8(const int8_t* qs, const float* scales, const int8_t* xq, const float* xsc,
                 float* y, int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
 int dnx_gemm_q4(const uint8_t* qs, const uint16_t* scales, const int8_t* xq, const float* xsc,

@@ -57,7 +57,8 @@ def exact_products(orc, fmt, qs, sc, xq, xsc):
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 @pytest.mark.parametrize("rows,cols,n", [(6144, 2048, 512), (70, 96, 13), (36, 64, 9),
                                          (128, 128, 40), (4304, 1152, 64), (1152, 4320, 33),
-                                         (257, 2048, 1), (100, 2048, 64)])
+                                         (257, 2048, 1), (100, 2048, 64), (6144, 2048, 8),
+                                         (6144, 2048, 32), (2048, 6144, 16), (6144, 2048, 64)])
 def test_gemm_within_tolerance(gpu_ready, orc, fmt, rows, cols, n):
     """Against the exact products: the reference kernels' own bar (error /
     sum|terms| < 1e-5, native_kernels_test.dart:56-59), met by the CPU kernels
@@ -89,3 +90,20 @@ def test_gemm_rejects_unsupported(gpu_ready):
     z = torch.zeros(4096, device="cuda")
     with pytest.raises(RuntimeError):
         D.gemm_q8(z, z, z, z, z, 4, 40, 2)
+
+
+@pytest.mark.parametrize("rows,cols,n", [(6144, 2048, 8), (2048, 6144, 40), (6144, 2048, 512)])
+def test_gemm_is_deterministic(gpu_ready, rows, cols, n):
+    """Split-K partials are summed in a fixed order: repeated calls (and
+    calls after a larger one regrew the workspace) give identical bits."""
+    rng = np.random.default_rng(rows + n)
+    qs, sc = synth.q4_weights(rng, rows, cols)
+    xs = synth.activations(rng, n, cols)
+    xq, xsc = dev(np.zeros((n, cols), np.int8)), dev(np.zeros((n, cols // 32), np.float32))
+    D.quantize_q8(dev(xs), xq, xsc, n, cols, cols)
+    outs = []
+    for _ in range(3):
+        y = torch.full((n, rows), float("nan"), device="cuda")
+        D.gemm_q4(dev(qs), dev(sc), xq, xsc, y, rows, cols, n)
+        outs.append(host(y))
+    assert all(np.array_equal(bits(o), bits(outs[0])) for o in outs[1:])
