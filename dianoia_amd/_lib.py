@@ -69,6 +69,10 @@ SIGNATURES = {
     "dnx_gate_up_q8h": ([_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_q8": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_q4": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dnx_gemm_panel_bytes": ([_i64, _i64], _i64),
+    "dnx_pack_panel": ([_p, _p, _p, _i64, _i64, _p], _i32),
+    "dnx_gemm_q8_panel": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dnx_gemm_q4_panel": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_argmax_workspace_bytes": ([_i64], _i64),
     "dnx_argmax": ([_p, _i64, _p, _p, _p], _i32),
     "dnx_swiglu": ([_p, _p, _i64, _p], _i32),

@@ -79,8 +79,13 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
   constexpr int BP = (B16 + kThreads - 1) / kThreads;
   constexpr int SXP = (KB * BM + kThreads - 1) / kThreads;
   constexpr int SWP = (KB * BN + kThreads - 1) / kThreads;
+  // Loaded values stay as loaded (Q4 scales as their raw 16 bits) until
+  // store_stage: any operation on a loaded register, even a zero-extension,
+  // makes the wave wait for that load where the operation is, which would
+  // put the next stage's load latency in front of this stage's MFMAs.
   uint4 ra[AP], rb[BP];
   float rsx[SXP], rsw[SWP];
+  short rsh[SWP];
   const i32x4 rxq = buffer_rsrc(p.xq, (uint32_t)((size_t)M * K));
   const i32x4 rqs = buffer_rsrc(p.qs, (uint32_t)((size_t)N * (kQ4 ? K / 2 : K)));
   const i32x4 rxs = buffer_rsrc(p.xsc, (uint32_t)((size_t)M * B * 4));
@@ -143,9 +148,7 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < SWP; i++) {
       if (kQ4) {
-        const short h =
-            dnx_raw_buffer_load_i16(rws, b0 + cW[i] < B ? offW[i] + b0 * 2 : -2, 0, 0);
-        rsw[i] = __int_as_float((int)(uint16_t)h);  // bits; widened in store_stage
+        rsh[i] = dnx_raw_buffer_load_i16(rws, b0 + cW[i] < B ? offW[i] + b0 * 2 : -2, 0, 0);
       } else {
         rsw[i] = __int_as_float(
             dnx_raw_buffer_load_i32(rws, b0 + cW[i] < B ? offW[i] + b0 * 4 : -4, 0, 0));
@@ -192,7 +195,7 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
       const int idx = i * kThreads + tid;
       if (idx < KB * BN) {
         sws[buf][idx / BN][idx % BN] =
-            kQ4 ? half_bits_to_float((uint16_t)__float_as_int(rsw[i])) : rsw[i];
+            kQ4 ? half_bits_to_float((uint16_t)rsh[i]) : rsw[i];
       }
     }
   };

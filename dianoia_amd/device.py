@@ -125,6 +125,26 @@ def gemm_q4(qs, scales, xq, xsc, y, rows: int, cols: int, n: int, stream=None) -
                                    cols, n, _stream(stream)), "dnx_gemm_q4")
 
 
+def gemm_panel_bytes(n: int, cols: int) -> int:
+    return int(_lib.load().dnx_gemm_panel_bytes(n, cols))
+
+
+def pack_panel(xq, xsc, panel, n: int, cols: int, stream=None) -> None:
+    """xq int8 [n][cols] + xsc fp32 [n][cols/32] -> the GEMM's activation panel."""
+    _check(_lib.load().dnx_pack_panel(_ptr(xq), _ptr(xsc), _ptr(panel), n, cols,
+                                      _stream(stream)), "dnx_pack_panel")
+
+
+def gemm_q8_panel(qs, scales, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _check(_lib.load().dnx_gemm_q8_panel(_ptr(qs), _ptr(scales), _ptr(panel), _ptr(y), rows,
+                                         cols, n, _stream(stream)), "dnx_gemm_q8_panel")
+
+
+def gemm_q4_panel(qs, scales, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _check(_lib.load().dnx_gemm_q4_panel(_ptr(qs), _ptr(scales), _ptr(panel), _ptr(y), rows,
+                                         cols, n, _stream(stream)), "dnx_gemm_q4_panel")
+
+
 def argmax_workspace(n: int, device="cuda") -> torch.Tensor:
     nbytes = int(_lib.load().dnx_argmax_workspace_bytes(n))
     return torch.empty(nbytes, dtype=torch.uint8, device=device)

@@ -113,6 +113,21 @@ int dnx_gemm_q8(const int8_t* qs, const float* scales, const int8_t* xq, const f
 int dnx_gemm_q4(const uint8_t* qs, const uint16_t* scales, const int8_t* xq, const float* xsc,
                 float* y, int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
 
+// The large-n GEMM on fp16/bf16 MFMA (exact int block dots, scale products
+// from an outer-product MFMA, one fma per output per block), on activations
+// laid out as a "panel": per 32 token rows and per 32-block, 2048 bytes of
+// fp16 MFMA fragments of xq and 512 bytes of bf16 pieces of xsc.
+// dnx_gemm_panel_bytes(n, cols) is its size; dnx_pack_panel writes it from
+// xq int8 [n][cols] and xsc fp32 [n][cols/32]. The products are within 1e-4
+// relative of the CPU kernels (the same inputs always give the same bits).
+int64_t dnx_gemm_panel_bytes(int64_t n, int64_t cols);
+int dnx_pack_panel(const int8_t* xq, const float* xsc, void* panel, int64_t n, int64_t cols,
+                   dnx_stream_t stream);
+int dnx_gemm_q8_panel(const int8_t* qs, const float* scales, const void* panel, float* y,
+                      int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
+int dnx_gemm_q4_panel(const uint8_t* qs, const uint16_t* scales, const void* panel, float* y,
+                      int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
+
 // Greedy argmax of v[0..n) (argmaxToken, lib/src/sampler.dart:137-152):
 // the first index of the maximum; a NaN at index 0 wins, other NaNs never.
 // Writes one int64 to *out. workspace: dnx_argmax_workspace_bytes(n) bytes.

@@ -1,4 +1,8 @@
-"""int8-MFMA GEMM: per-block int32 dots exact, fp32 outputs within 1e-4."""
+"""Prefill GEMMs: per-block int32 dots exact, fp32 outputs within 1e-4.
+
+Two paths: "i8" is dnx_gemm_q8/q4 on int8 xq + fp32 xsc; "panel" packs the
+same xq/xsc into the fp16/bf16-MFMA kernel's activation panel
+(dnx_pack_panel) and runs dnx_gemm_q8/q4_panel."""
 
 import numpy as np
 import pytest
@@ -11,16 +15,27 @@ from gpu_util import bits, dev, host, within_tolerance
 pytestmark = pytest.mark.gpu
 
 
-def gemm(fmt, qs, sc, xq, xsc, rows, cols, n):
+PATHS = ["i8", "panel"]
+
+
+def gemm(fmt, qs, sc, xq, xsc, rows, cols, n, path="i8"):
     y = torch.full((n, rows), float("nan"), dtype=torch.float32, device="cuda")
-    f = D.gemm_q4 if fmt == "q4" else D.gemm_q8
-    f(dev(qs), dev(sc), dev(xq), dev(xsc), y, rows, cols, n)
+    if path == "panel":
+        panel = torch.full((D.gemm_panel_bytes(n, cols),), 0x7f, dtype=torch.uint8, device="cuda")
+        D.pack_panel(dev(xq), dev(xsc), panel, n, cols)
+        f = D.gemm_q4_panel if fmt == "q4" else D.gemm_q8_panel
+        f(dev(qs), dev(sc), panel, y, rows, cols, n)
+    else:
+        f = D.gemm_q4 if fmt == "q4" else D.gemm_q8
+        f(dev(qs), dev(sc), dev(xq), dev(xsc), y, rows, cols, n)
     return host(y)
 
 
+@pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
-@pytest.mark.parametrize("rows,cols,n", [(130, 256, 70), (128, 128, 128), (33, 96, 5)])
-def test_block_dots_are_exact(gpu_ready, orc, fmt, rows, cols, n):
+@pytest.mark.parametrize("rows,cols,n", [(130, 256, 70), (128, 128, 128), (33, 96, 5),
+                                         (200, 320, 300)])
+def test_block_dots_are_exact(gpu_ready, orc, fmt, rows, cols, n, path):
     """With scale 1 on one block and 0 on the others, y is that block's
     int32 dot product as a float (exact below 2^24): the MFMA's integer
     result for every block, compared with brute-force sums."""
@@ -40,8 +55,30 @@ def test_block_dots_are_exact(gpu_ready, orc, fmt, rows, cols, n):
         sw[:, b] = one
         xsc = np.zeros((n, B), np.float32)
         xsc[:, b] = 1.0
-        y = gemm(fmt, qs, sw, xq, xsc, rows, cols, n)
+        y = gemm(fmt, qs, sw, xq, xsc, rows, cols, n, path)
         assert np.array_equal(y, want[:, :, b].astype(np.float32)), f"block {b}"
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_panel_unit_scales_sum_blocks_exactly(gpu_ready, orc, fmt):
+    """All scales 1: y is the sum over blocks of the exact int32 dots, exact
+    in float while the total stays below 2^24 (the MFMA's integer-valued
+    fp16 products and the outer-product scale of exactly 1)."""
+    rows, cols, n = 96, 2048, 160
+    rng = np.random.default_rng(7)
+    xq = rng.integers(-127, 128, (n, cols), dtype=np.int8)
+    if fmt == "q8":
+        qs = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+        want = orc.block_dots_q8(qs, xq).sum(axis=2)
+        sw = np.ones((rows, cols // 32), np.float32)
+    else:
+        qs = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+        want = orc.block_dots_q4(qs, xq).sum(axis=2)
+        sw = np.full((rows, cols // 32), np.uint16(0x3C00))
+    assert np.abs(want).max() < 2 ** 24
+    xsc = np.ones((n, cols // 32), np.float32)
+    y = gemm(fmt, qs, sw, xq, xsc, rows, cols, n, "panel")
+    assert np.array_equal(y, want.astype(np.float32))
 
 
 def exact_products(orc, fmt, qs, sc, xq, xsc):
@@ -54,12 +91,14 @@ def exact_products(orc, fmt, qs, sc, xq, xsc):
     return (d * s).sum(axis=2), np.abs(d * s).sum(axis=2)
 
 
+@pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 @pytest.mark.parametrize("rows,cols,n", [(6144, 2048, 512), (70, 96, 13), (36, 64, 9),
                                          (128, 128, 40), (4304, 1152, 64), (1152, 4320, 33),
                                          (257, 2048, 1), (100, 2048, 64), (6144, 2048, 8),
-                                         (6144, 2048, 32), (2048, 6144, 16), (6144, 2048, 64)])
-def test_gemm_within_tolerance(gpu_ready, orc, fmt, rows, cols, n):
+                                         (6144, 2048, 32), (2048, 6144, 16), (6144, 2048, 64),
+                                         (4304, 1152, 300), (1152, 4320, 200), (97, 160, 129)])
+def test_gemm_within_tolerance(gpu_ready, orc, fmt, rows, cols, n, path):
     """Against the exact products: the reference kernels' own bar (error /
     sum|terms| < 1e-5, native_kernels_test.dart:56-59), met by the CPU kernels
     too. Against the CPU outputs: the per-element bar (relative 1e-4, absolute
@@ -75,7 +114,7 @@ def test_gemm_within_tolerance(gpu_ready, orc, fmt, rows, cols, n):
     xs = synth.activations(rng, n, cols)
     xq, xsc = orc.quantize_q8(xs)
     ref = (orc.gemm_q8 if fmt == "q8" else orc.gemm_q4)(qs, sc, xs, n, threads=8, mode=1)
-    y = gemm(fmt, qs, sc, xq, xsc, rows, cols, n)
+    y = gemm(fmt, qs, sc, xq, xsc, rows, cols, n, path)
     exact, mag = exact_products(orc, fmt, qs, sc, xq, xsc)
     assert np.max(np.abs(y - exact) / mag) < 1e-5
     assert np.max(np.abs(ref - exact) / mag) < 1e-5
