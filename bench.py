@@ -242,13 +242,34 @@ def bench_c3(torch, D, synth, timer, steps, warmup):
         q, s = ws[i % copies]
         D.gemm_q4(q, s, xq, xsc, y, N, K, M)
 
+    # The fp16/bf16-MFMA GEMM on the activation panel, which the quantizer
+    # writes directly (dnx_quantize_q8_panel).
+    panel = torch.empty((D.gemm_panel_bytes(M, K),), dtype=torch.uint8, device="cuda")
+
+    def quant_p(i):
+        D.quantize_q8_panel(xd, panel, M, K)
+
+    def gemm_p(i):
+        q, s = ws[i % copies]
+        D.gemm_q4_panel(q, s, panel, y, N, K, M)
+
     n = max(10, steps // 4)
-    ms = timer.time(lambda i: (quant(i), gemm(i)), n, max(2, warmup // 4))
-    means = timer.kernel_means([quant, gemm], n)
+    ms_i8 = timer.time(lambda i: (quant(i), gemm(i)), n, max(2, warmup // 4))
+    ms_p = timer.time(lambda i: (quant_p(i), gemm_p(i)), n, max(2, warmup // 4))
+    means = timer.kernel_means([quant, gemm, quant_p, gemm_p], n)
     ops = 2 * M * N * K
-    out = {"ms": ms, "tops": ops / ms / 1e9, "gemm_ms": means[1], "quantize_ms": means[0],
-           "gemm_tops": ops / means[1] / 1e9,
-           "gemm_frac_i8": ops / means[1] / 1e9 / I8_PEAK_TOPS}
+    paths = {
+        "int8_mfma": {"ms": ms_i8, "gemm_ms": means[1], "quantize_ms": means[0],
+                      "kernel": "quantize_q8 + gemm_kernel (int8 MFMA, scale MFMA, cvt + fma)"},
+        "fp16_panel": {"ms": ms_p, "gemm_ms": means[3], "quantize_ms": means[2],
+                       "kernel": "quantize_q8_panel + gemm_f16_kernel (fp16 MFMA, scale MFMA, fma)"},
+    }
+    best = min(paths, key=lambda k: paths[k]["gemm_ms"])
+    b = paths[best]
+    out = {"ms": b["ms"], "tops": ops / b["ms"] / 1e9, "gemm_ms": b["gemm_ms"],
+           "quantize_ms": b["quantize_ms"], "gemm_tops": ops / b["gemm_ms"] / 1e9,
+           "gemm_frac_i8": ops / b["gemm_ms"] / 1e9 / I8_PEAK_TOPS, "gemm_path": best,
+           "paths": {k: dict(v, gemm_tops=ops / v["gemm_ms"] / 1e9) for k, v in paths.items()}}
     # M = 1..64 sweep: GEMV (exact order) up to 4 tokens, GEMM beyond.
     sweep = {}
     for m in (1, 2, 4, 8, 16, 32, 64):
@@ -368,16 +389,19 @@ def traffic_from_profiles():
 PMC_COPY_BYTES = 1 << 30  # the calibration copy: reads and writes this many bytes
 kArgmaxWordsBytes = 32 * 8  # the finisher reads 32 rank words
 PMC_KERNELS = {  # kernel-name fragment -> (workload, algorithmic bytes per launch)
-    "gemv_kernel<1, 2, 1, true, false>": (
+    "gemv_kernel<1, 2, 1, true, false, false>": (
         "c1 gate+up Q4 pair, 6144x2048", 2 * q4_bytes(6144, 2048) + 2048 * 4 + 6144 * 4),
-    "gemv_kernel<1, 1, 1, false, false>": (
+    "gemv_kernel<1, 1, 1, false, false, false>": (
         "c1 down Q4, 2048x6144", q4_bytes(2048, 6144) + 6144 * 4 + 2048 * 4),
-    "gemv_kernel<2, 8, 1, false, true>": (
+    "gemv_kernel<2, 8, 1, false, true, false>": (
         "c2 LM head Q8 (fp16 scales) + argmax, 151936x2048",
         q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4),
     "argmax_finish_kernel": ("c2 argmax finisher", kArgmaxWordsBytes + 8),
     "gemm_kernel<true, 64, 64, 2, 4>": (
         "c3 Q4 GEMM M=512, 6144x2048", q4_bytes(6144, 2048) + 512 * 2048 + 512 * 64 * 4
+        + 512 * 6144 * 4),
+    "gemm_f16_kernel<true, 3>": (
+        "c3 Q4 panel GEMM M=512, 6144x2048", q4_bytes(6144, 2048) + 512 * 2048 + 512 * 64 * 4
         + 512 * 6144 * 4),
 }
 
@@ -432,9 +456,12 @@ def pmc_workload(torch, D, synth, reps):
     xsc = torch.empty((M, K // 32), dtype=torch.float32, device="cuda")
     y = torch.empty((M, N), device="cuda")
     D.quantize_q8(xd, xq, xsc, M, K, K)
+    panel = torch.empty((D.gemm_panel_bytes(M, K),), dtype=torch.uint8, device="cuda")
+    D.quantize_q8_panel(xd, panel, M, K)
     for i in range(reps):
         q, s = ws[i % 8]
         D.gemm_q4(q, s, xq, xsc, y, N, K, M)
+        D.gemm_q4_panel(q, s, panel, y, N, K, M)
     torch.cuda.synchronize()
     print("pmc: config 3 done", file=sys.stderr, flush=True)
 

@@ -71,6 +71,7 @@ SIGNATURES = {
     "dnx_gemm_q4": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_panel_bytes": ([_i64, _i64], _i64),
     "dnx_pack_panel": ([_p, _p, _p, _i64, _i64, _p], _i32),
+    "dnx_quantize_q8_panel": ([_p, _p, _i64, _i64, _p], _i32),
     "dnx_gemm_q8_panel": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_q4_panel": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_argmax_workspace_bytes": ([_i64], _i64),

@@ -127,6 +127,42 @@ DNX_DEV float4 buffer_load_f4(i32x4 rsrc, int offset) {
                      __int_as_float(v.w));
 }
 
+// x = p0 + p1 + p2 exactly, each piece a bf16 (top 16 bits of a float):
+// truncation keeps 8 significant bits per piece, and the remainders are
+// exact float subtractions.
+DNX_DEV void split3_bf16(float x, uint32_t& p0, uint32_t& p1, uint32_t& p2) {
+  const uint32_t b0 = __float_as_uint(x) & 0xffff0000u;
+  const float r = x - __uint_as_float(b0);
+  const uint32_t b1 = __float_as_uint(r) & 0xffff0000u;
+  const float r2 = r - __uint_as_float(b1);
+  p0 = b0 >> 16;
+  p1 = b1 >> 16;
+  p2 = __float_as_uint(r2) >> 16;
+}
+
+// Block scales applied by an MFMA. The product s = sx * sw of a 32 x 32
+// tile comes from one v_mfma_f32_32x32x8_bf16 used as an outer product:
+// each scale is split into three bf16 pieces and six of the products
+// x_i * w_j (i + j <= 2) sit in the instruction's K slots; the dropped
+// terms are below 3 * 2^-24 relative. Scale pieces in the outer-product
+// MFMA's K slots. Lanes 0..31 hold slots
+// 0..7 of their row (A) or column (B), lanes 32..63 slots 8..15; only the
+// first four slots of each half are used:
+//   A half 0: x0 x0 x1 0   B half 0: w0 w1 w0 0   -> x0w0 + x0w1 + x1w0
+//   A half 1: x0 x1 x2 0   B half 1: w2 w1 w0 0   -> x0w2 + x1w1 + x2w0
+DNX_DEV uint2 a_scale_half0(uint32_t p0, uint32_t p1, uint32_t) {
+  return make_uint2(p0 | (p0 << 16), p1);
+}
+DNX_DEV uint2 a_scale_half1(uint32_t p0, uint32_t p1, uint32_t p2) {
+  return make_uint2(p0 | (p1 << 16), p2);
+}
+DNX_DEV uint2 b_scale_half0(uint32_t p0, uint32_t p1, uint32_t) {
+  return make_uint2(p0 | (p1 << 16), p0);
+}
+DNX_DEV uint2 b_scale_half1(uint32_t p0, uint32_t p1, uint32_t p2) {
+  return make_uint2(p2 | (p1 << 16), p0);
+}
+
 DNX_DEV float bf16_to_float(uint16_t p) { return __uint_as_float((uint32_t)p << 16); }
 
 DNX_DEV float half_bits_to_float(uint16_t h) {

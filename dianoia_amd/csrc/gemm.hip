@@ -28,6 +28,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef short s4 __attribute__((ext_vector_type(4)));   // 4 bf16 (bits)
 
 constexpr int kThreads = 256;
 
@@ -61,8 +63,10 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
   constexpr int RS = RB + 16;                 // LDS row stride (bank spread)
   __shared__ __align__(16) int8_t sa[2][BM * RS];
   __shared__ __align__(16) int8_t sb[2][BN * RS];
-  __shared__ __align__(16) float sxs[2][KB][BM];
-  __shared__ __align__(16) float sws[2][KB][BN];
+  // Block scales as bf16 pieces of the outer-product MFMA (two 8-byte lane
+  // halves per row or column and block).
+  __shared__ __align__(16) uint2 sxs[2][KB][BM][2];
+  __shared__ __align__(16) uint2 sws[2][KB][BN][2];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -188,14 +192,23 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < SXP; i++) {
       const int idx = i * kThreads + tid;
-      if (idx < KB * BM) sxs[buf][idx / BM][idx % BM] = rsx[i];
+      if (idx < KB * BM) {
+        uint32_t p0, p1, p2;
+        split3_bf16(rsx[i], p0, p1, p2);
+        uint2* d = sxs[buf][idx / BM][idx % BM];
+        d[0] = a_scale_half0(p0, p1, p2);
+        d[1] = a_scale_half1(p0, p1, p2);
+      }
     }
 #pragma unroll
     for (int i = 0; i < SWP; i++) {
       const int idx = i * kThreads + tid;
       if (idx < KB * BN) {
-        sws[buf][idx / BN][idx % BN] =
-            kQ4 ? half_bits_to_float((uint16_t)rsh[i]) : rsw[i];
+        uint32_t p0, p1, p2;
+        split3_bf16(kQ4 ? half_bits_to_float((uint16_t)rsh[i]) : rsw[i], p0, p1, p2);
+        uint2* d = sws[buf][idx / BN][idx % BN];
+        d[0] = b_scale_half0(p0, p1, p2);
+        d[1] = b_scale_half1(p0, p1, p2);
       }
     }
   };
@@ -231,29 +244,24 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
       for (int j = 0; j < SN; j++)
         b[j] = *(const v4i*)(&sb[buf][(wn * TN + j * 32 + lrow) * RS + kb * 32 + lk]);
       // This lane's outputs: column n = lane % 32 of each N subtile; rows
-      // (v / 4) * 8 + (lane / 32) * 4 + v % 4 of each M subtile.
-      float swv[SN];
+      // (v / 4) * 8 + (lane / 32) * 4 + v % 4 of each M subtile. The tile's
+      // scale products s = sx * sw come from the outer-product MFMA on the
+      // staged bf16 pieces; the epilogue is cvt + fma per output.
+      s4 bsv[SN];
 #pragma unroll
-      for (int j = 0; j < SN; j++) swv[j] = sws[buf][kb][wn * TN + j * 32 + lrow];
+      for (int j = 0; j < SN; j++)
+        bsv[j] = __builtin_bit_cast(s4, sws[buf][kb][wn * TN + j * 32 + lrow][lane >> 5]);
 #pragma unroll
       for (int i = 0; i < SM; i++) {
-        float sxv[16];
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const float4 t =
-              *(const float4*)(&sxs[buf][kb][wm * TM + i * 32 + g * 8 + (lane >> 5) * 4]);
-          sxv[4 * g + 0] = t.x;
-          sxv[4 * g + 1] = t.y;
-          sxv[4 * g + 2] = t.z;
-          sxv[4 * g + 3] = t.w;
-        }
+        const s4 asv = __builtin_bit_cast(s4, sxs[buf][kb][wm * TM + i * 32 + lrow][lane >> 5]);
 #pragma unroll
         for (int j = 0; j < SN; j++) {
           v16i d = {};
           d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], d, 0, 0, 0);
+          const v16f z = {};
+          const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(asv, bsv[j], z, 0, 0, 0);
 #pragma unroll
-          for (int v = 0; v < 16; v++)
-            acc[i][j][v] = fmaf((float)d[v], sxv[v] * swv[j], acc[i][j][v]);
+          for (int v = 0; v < 16; v++) acc[i][j][v] = fmaf((float)d[v], sc[v], acc[i][j][v]);
         }
       }
     }

@@ -49,6 +49,7 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short s4 __attribute__((ext_vector_type(4)));   // 4 bf16 (bits)
 
@@ -59,37 +60,6 @@ constexpr int kBM = kWaves * kRowsPerWave;   // token rows per workgroup
 constexpr int kPanelA = 2048;                // fp16 fragments of one (group, block)
 constexpr int kPanelS = 512;                 // bf16 scale pieces of one (group, block)
 constexpr int kPanelBlock = kPanelA + kPanelS;
-
-// x = p0 + p1 + p2 exactly, each piece a bf16 (top 16 bits of a float):
-// truncation keeps 8 significant bits per piece, and the remainders are
-// exact float subtractions.
-DNX_DEV void split3_bf16(float x, uint32_t& p0, uint32_t& p1, uint32_t& p2) {
-  const uint32_t b0 = __float_as_uint(x) & 0xffff0000u;
-  const float r = x - __uint_as_float(b0);
-  const uint32_t b1 = __float_as_uint(r) & 0xffff0000u;
-  const float r2 = r - __uint_as_float(b1);
-  p0 = b0 >> 16;
-  p1 = b1 >> 16;
-  p2 = __float_as_uint(r2) >> 16;
-}
-
-// Scale pieces in the outer-product MFMA's K slots. Lanes 0..31 hold slots
-// 0..7 of their row (A) or column (B), lanes 32..63 slots 8..15; only the
-// first four slots of each half are used:
-//   A half 0: x0 x0 x1 0   B half 0: w0 w1 w0 0   -> x0w0 + x0w1 + x1w0
-//   A half 1: x0 x1 x2 0   B half 1: w2 w1 w0 0   -> x0w2 + x1w1 + x2w0
-DNX_DEV uint2 a_scale_half0(uint32_t p0, uint32_t p1, uint32_t) {
-  return make_uint2(p0 | (p0 << 16), p1);
-}
-DNX_DEV uint2 a_scale_half1(uint32_t p0, uint32_t p1, uint32_t p2) {
-  return make_uint2(p0 | (p1 << 16), p2);
-}
-DNX_DEV uint2 b_scale_half0(uint32_t p0, uint32_t p1, uint32_t) {
-  return make_uint2(p0 | (p1 << 16), p0);
-}
-DNX_DEV uint2 b_scale_half1(uint32_t p0, uint32_t p1, uint32_t p2) {
-  return make_uint2(p2 | (p1 << 16), p0);
-}
 
 // Two bytes of `v` (selected by `sel`) as the fp16 pair (1024 + byte),
 // minus `bias` from both halves: exact for bytes 0..255.
@@ -152,6 +122,42 @@ __global__ void __launch_bounds__(kThreads) pack_panel_kernel(const int8_t* __re
     split3_bf16(sx, p0, p1, p2);
     *(uint2*)(dst + kPanelA + r * 8) = a_scale_half0(p0, p1, p2);
     *(uint2*)(dst + kPanelA + (32 + r) * 8) = a_scale_half1(p0, p1, p2);
+  }
+}
+
+// lab_quantize_q8 (lab_native.c:407-429) of fp32 x [n][cols] straight into
+// the panel: the same values as dnx_quantize_q8 (bit-exact: the same block
+// max, scale, 1/scale and rounding), stored as the fp16 fragments and bf16
+// scale pieces the GEMM reads. One thread quantizes 4 consecutive values
+// (8 threads share a block, as in the plain quantizer) over the padded rows
+// of the last group, whose values are zeros.
+__global__ void __launch_bounds__(kThreads) quantize_panel_kernel(const float* __restrict__ x,
+                                                                  uint8_t* __restrict__ panel,
+                                                                  int n, int cols, int groups) {
+  const int B = cols / kBlock;
+  const int64_t quads_per_row = cols / 4;
+  const int64_t total = (int64_t)groups * kRowsPerWave * quads_per_row;
+  for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < total;
+       q += (int64_t)gridDim.x * kThreads) {
+    const int row = (int)(q / quads_per_row);
+    const int c = (int)(q - (int64_t)row * quads_per_row) * 4;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (row < n) v = *(const float4*)(x + (int64_t)row * cols + c);
+    const float amax = group8_max(fmaxf(0.0f, max4abs(v)));
+    const float scale = q8_scale(amax);
+    const float inv = q8_inv(scale);
+    const int g = row / kRowsPerWave, r = row % kRowsPerWave, b = c / kBlock, kk = c % kBlock;
+    uint8_t* dst = panel + ((int64_t)g * B + b) * kPanelBlock;
+    const h4 h = {(_Float16)quant1(v.x, inv), (_Float16)quant1(v.y, inv),
+                  (_Float16)quant1(v.z, inv), (_Float16)quant1(v.w, inv)};
+    *(uint2*)(dst + (kk >> 4) * 1024 + (((kk >> 3) & 1) * 32 + r) * 16 + (kk & 7) * 2) =
+        __builtin_bit_cast(uint2, h);
+    if (kk == 0) {
+      uint32_t p0, p1, p2;
+      split3_bf16(scale, p0, p1, p2);
+      *(uint2*)(dst + kPanelA + r * 8) = a_scale_half0(p0, p1, p2);
+      *(uint2*)(dst + kPanelA + (32 + r) * 8) = a_scale_half1(p0, p1, p2);
+    }
   }
 }
 
@@ -543,6 +549,21 @@ int dnx_pack_panel(const int8_t* xq, const float* xsc, void* panel, int64_t n, i
   const int64_t blocks = (total + kThreads - 1) / kThreads;
   hipLaunchKernelGGL(pack_panel_kernel, dim3((unsigned)(blocks < 8192 ? blocks : 8192)),
                      dim3(kThreads), 0, (hipStream_t)stream, xq, xsc, (uint8_t*)panel, (int)n,
+                     (int)cols, groups);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_quantize_q8_panel(const float* x, void* panel, int64_t n, int64_t cols,
+                          dnx_stream_t stream) {
+  if (n <= 0 || cols <= 0 || cols % kBlock != 0 || ((uintptr_t)x & 15) ||
+      ((uintptr_t)panel & 15) || panel_bytes(n, cols) >= (1ll << 31)) {
+    return DNX_EINVAL;
+  }
+  const int groups = (int)((n + kRowsPerWave - 1) / kRowsPerWave);
+  const int64_t total = (int64_t)groups * kRowsPerWave * (cols / 4);
+  const int64_t blocks = (total + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(quantize_panel_kernel, dim3((unsigned)(blocks < 16384 ? blocks : 16384)),
+                     dim3(kThreads), 0, (hipStream_t)stream, x, (uint8_t*)panel, (int)n,
                      (int)cols, groups);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }

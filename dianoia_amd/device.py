@@ -135,6 +135,12 @@ def pack_panel(xq, xsc, panel, n: int, cols: int, stream=None) -> None:
                                       _stream(stream)), "dnx_pack_panel")
 
 
+def quantize_q8_panel(x, panel, n: int, cols: int, stream=None) -> None:
+    """fp32 x [n][cols] quantized (lab_quantize_q8) straight into the GEMM's panel."""
+    _check(_lib.load().dnx_quantize_q8_panel(_ptr(x), _ptr(panel), n, cols, _stream(stream)),
+           "dnx_quantize_q8_panel")
+
+
 def gemm_q8_panel(qs, scales, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
     _check(_lib.load().dnx_gemm_q8_panel(_ptr(qs), _ptr(scales), _ptr(panel), _ptr(y), rows,
                                          cols, n, _stream(stream)), "dnx_gemm_q8_panel")

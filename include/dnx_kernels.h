@@ -120,9 +120,17 @@ int dnx_gemm_q4(const uint8_t* qs, const uint16_t* scales, const int8_t* xq, con
 // dnx_gemm_panel_bytes(n, cols) is its size; dnx_pack_panel writes it from
 // xq int8 [n][cols] and xsc fp32 [n][cols/32]. The products are within 1e-4
 // relative of the CPU kernels (the same inputs always give the same bits).
+// With fewer than 192 output tiles K is split across workgroups and summed
+// in a fixed order in the library's own workspace, allocated on the first
+// such call at a larger shape (so that call must not be captured into a
+// graph).
 int64_t dnx_gemm_panel_bytes(int64_t n, int64_t cols);
 int dnx_pack_panel(const int8_t* xq, const float* xsc, void* panel, int64_t n, int64_t cols,
                    dnx_stream_t stream);
+// lab_quantize_q8 of fp32 x [n][cols] written straight into the panel (the
+// same quantized values as dnx_quantize_q8; x 16-byte aligned).
+int dnx_quantize_q8_panel(const float* x, void* panel, int64_t n, int64_t cols,
+                          dnx_stream_t stream);
 int dnx_gemm_q8_panel(const int8_t* qs, const float* scales, const void* panel, float* y,
                       int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
 int dnx_gemm_q4_panel(const uint8_t* qs, const uint16_t* scales, const void* panel, float* y,

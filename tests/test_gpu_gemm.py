@@ -146,3 +146,21 @@ def test_gemm_is_deterministic(gpu_ready, rows, cols, n):
         D.gemm_q4(dev(qs), dev(sc), xq, xsc, y, rows, cols, n)
         outs.append(host(y))
     assert all(np.array_equal(bits(o), bits(outs[0])) for o in outs[1:])
+
+
+@pytest.mark.parametrize("n,cols", [(512, 2048), (33, 96), (1, 32), (100, 4320)])
+def test_quantize_panel_matches_pack(gpu_ready, n, cols):
+    """dnx_quantize_q8_panel writes the same panel bytes as dnx_quantize_q8
+    followed by dnx_pack_panel (the quantized values are lab_quantize_q8's),
+    including the zero rows that pad the last 32-row group."""
+    rng = np.random.default_rng(n + cols)
+    x = dev(synth.activations(rng, n, cols))
+    xq = torch.empty((n, cols), dtype=torch.int8, device="cuda")
+    xsc = torch.empty((n, cols // 32), dtype=torch.float32, device="cuda")
+    D.quantize_q8(x, xq, xsc, n, cols, cols)
+    size = D.gemm_panel_bytes(n, cols)
+    a = torch.full((size,), 0x5a, dtype=torch.uint8, device="cuda")
+    b = torch.full((size,), 0xa5, dtype=torch.uint8, device="cuda")
+    D.pack_panel(xq, xsc, a, n, cols)
+    D.quantize_q8_panel(x, b, n, cols)
+    assert np.array_equal(host(a), host(b))
