@@ -323,15 +323,36 @@ def bench_c4(torch, D, synth, timer, steps, warmup):
         D.quantize_q8(h, xq, xs, M, 4320, 4320)
         D.gemm_q8(q2, s2, xq, xs, y, 1152, 4320, M)
 
+    # BF16 -> Q4 (lab_quantize_q4 after _widenBf16) on fc1's weights, and on
+    # a 32768 x 4096 matrix (256 MiB of BF16) for the streaming rate.
+    q4_1 = torch.empty((4304, 576), dtype=torch.uint8, device="cuda")
+    d4_1 = torch.empty((4304, 36), dtype=torch.int16, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    wbig = (torch.randn((32768, 4096), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    wbig = wbig.view(torch.int16)
+    q4_b = torch.empty((32768, 2048), dtype=torch.uint8, device="cuda")
+    d4_b = torch.empty((32768, 128), dtype=torch.int16, device="cuda")
+
+    def quant_q4(i):
+        D.quantize_q4_bf16(w1, q4_1, d4_1, 4304, 1152)
+
+    def quant_q4_big(i):
+        D.quantize_q4_bf16(wbig, q4_b, d4_b, 32768, 4096)
+
     n = max(10, steps // 4)
     quant_w(0)
-    means = timer.kernel_means([quant_w, fc1_, gelu_, fc2_], n)
+    means = timer.kernel_means([quant_w, fc1_, gelu_, fc2_, quant_q4, quant_q4_big], n)
+    q4_bytes = lambda r, c: r * c * 2 + r * c // 2 + r * (c // 32) * 2
     qbytes = (4304 * 1152 * 2 + 4320 * 1152 + 4320 * 36 * 4) + (1152 * 4304 * 2 + 1152 * 4320 + 1152 * 135 * 4)
     ops = 2 * M * 4304 * 1152
     return {"quantize_weights_ms": means[0], "quantize_weights_gbps": qbytes / means[0] / 1e6,
             "fc1_ms": means[1], "fc1_tops": ops / means[1] / 1e9, "gelu_ms": means[2],
             "fc2_ms": means[3], "fc2_tops": ops / means[3] / 1e9,
-            "pair_tops": 2 * ops / (means[1] + means[2] + means[3]) / 1e9}
+            "pair_tops": 2 * ops / (means[1] + means[2] + means[3]) / 1e9,
+            "quantize_q4_fc1_ms": means[4],
+            "quantize_q4_fc1_gbps": q4_bytes(4304, 1152) / means[4] / 1e6,
+            "quantize_q4_32768x4096_ms": means[5],
+            "quantize_q4_32768x4096_gbps": q4_bytes(32768, 4096) / means[5] / 1e6}
 
 
 # ------------------------------------------------------------------ CPU

@@ -36,6 +36,14 @@ DNX_DEV float group8_max(float m) {
   return m;
 }
 
+// Min over the 8 lanes of an aligned lane group; every lane gets it.
+DNX_DEV int group8_min(int m) {
+  m = min(m, dpp<kQuadXor1>(m));
+  m = min(m, dpp<kQuadXor2>(m));
+  m = min(m, dpp<kHalfRowMirror>(m));
+  return m;
+}
+
 // float -> int as x86 cvttss2si does: truncation, with NaN and values
 // outside int32 giving INT_MIN. The reference's (int) cast compiles to that
 // instruction on x86-64; it matters only where 1/scale overflows
@@ -52,6 +60,15 @@ DNX_DEV int quant1(float x, float inv) {
   t = t < 0.0f ? t - 0.5f : t + 0.5f;
   const int v = cvt_trunc_x86(t);
   return v > 127 ? 127 : v < -127 ? -127 : v;
+}
+
+// One value of lab_quantize_q4 (lab_native.c:949-950): (int8_t)(x * id +
+// 8.5f), two float roundings, the conversion as x86 compiles it (cvttss2si,
+// then the low byte), clamped above at 15.
+DNX_DEV int q4_value(float x, float id) {
+  const float t = x * id + 8.5f;
+  const int v = (int8_t)cvt_trunc_x86(t);
+  return v > 15 ? 15 : v;
 }
 
 // scale = amax / 127 and inv = 1 / scale, both correctly rounded

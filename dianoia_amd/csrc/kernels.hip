@@ -68,6 +68,78 @@ quantize_q8_kernel(const void* __restrict__ src, int8_t* __restrict__ qs,
   }
 }
 
+// lab_quantize_q4 (lab_native.c:928-955, llama.cpp's quantize_row_q4_0_ref)
+// over rows x cols values, cols a multiple of 32, into Q4 nibbles
+// [rows][cols/2] and fp16 scale bits [rows][cols/32]. Per block: max = the
+// first value (in column order) of largest magnitude (`a > amax` from 0, so
+// NaN never wins and ties keep the first); d = max / -8; id = 1/d (0 when
+// d == 0); q = (int8_t)(x * id + 8.5f) clamped above at 15 (two float
+// roundings: the reference is built without contraction); byte k = q[k] |
+// q[k + 16] << 4; the scale is d rounded to fp16 (RNE, as _mm_cvtps_ph).
+// One thread takes 4 consecutive values, 8 threads a block: the group's
+// largest magnitude, then the lowest (index, sign) key holding it. Lanes 0-3
+// of a group write the block's 16 bytes, taking the high nibbles (values
+// 16..31) from lanes 4-7. Input is fp32 or bf16 (widened p << 16).
+template <bool kBf16>
+__global__ void __launch_bounds__(kThreads)
+quantize_q4_kernel(const void* __restrict__ src, uint8_t* __restrict__ qs,
+                   uint16_t* __restrict__ scales, int64_t rows, int64_t cols, int vec_ok) {
+  const int64_t quads_per_row = cols / 4;
+  const int64_t total = rows * quads_per_row;
+  for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < total;
+       q += (int64_t)gridDim.x * kThreads) {
+    const int64_t row = q / quads_per_row;
+    const int64_t c = (q - row * quads_per_row) * 4;
+    float4 v;
+    if (kBf16) {
+      const uint16_t* p = (const uint16_t*)src + row * cols + c;
+      if (vec_ok) {
+        const uint2 raw = *(const uint2*)p;
+        v = make_float4(__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                        __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u));
+      } else {
+        v = make_float4(bf16_to_float(p[0]), bf16_to_float(p[1]), bf16_to_float(p[2]),
+                        bf16_to_float(p[3]));
+      }
+    } else {
+      const float* p = (const float*)src + row * cols + c;
+      v = vec_ok ? *(const float4*)p : make_float4(p[0], p[1], p[2], p[3]);
+    }
+    const int k0 = (int)(c & 31);
+    const float amax = group8_max(fmaxf(0.0f, max4abs(v)));
+    // Key 2k + sign of this lane's first value of magnitude amax (64: none).
+    int key = 64;
+    if (amax > 0.0f) {
+      const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 3; i >= 0; i--) {
+        if (fabsf(e[i]) == amax) key = 2 * (k0 + i) + (e[i] < 0.0f ? 1 : 0);
+      }
+    }
+    key = group8_min(key);
+    const float max = key == 64 ? 0.0f : (key & 1) ? -amax : amax;
+    const float d = max / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    // This lane's 4 values as (int8_t) bytes; lanes 0-3 pair with lanes 4-7.
+    const int own = (q4_value(v.x, id) & 0xff) | ((q4_value(v.y, id) & 0xff) << 8) |
+                    ((q4_value(v.z, id) & 0xff) << 16) | ((q4_value(v.w, id) & 0xff) << 24);
+    const int high = __shfl_xor(own, 4);
+    if (k0 < 16) {
+      uint32_t out = 0;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int lo = (int8_t)(own >> (8 * i));
+        const int hi = (int8_t)(high >> (8 * i));
+        out |= (uint32_t)((lo | (hi << 4)) & 0xff) << (8 * i);
+      }
+      *(uint32_t*)(qs + row * (cols / 2) + (c - k0) / 2 + k0) = out;
+    }
+    if (k0 == 0) {
+      scales[row * (cols / 32) + c / 32] = __builtin_bit_cast(uint16_t, (_Float16)d);
+    }
+  }
+}
+
 // ------------------------------------------------------------ argmax
 
 __global__ void __launch_bounds__(kThreads)
@@ -180,6 +252,28 @@ int dnx_quantize_q8_bf16(const uint16_t* w, int8_t* qs, float* scales, int64_t r
   const int grid = grid_for(rows * (cols_pad / 4), kThreads, 65536);
   hipLaunchKernelGGL((quantize_q8_kernel<true>), dim3(grid), dim3(kThreads), 0, stream,
                      (const void*)w, qs, scales, rows, cols, cols_pad, vec);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_quantize_q4(const float* w, uint8_t* qs, uint16_t* scales, int64_t rows, int64_t cols,
+                    hipStream_t stream) {
+  if (rows < 0 || cols <= 0 || cols % kBlock != 0 || ((uintptr_t)qs & 3)) return DNX_EINVAL;
+  if (rows == 0) return DNX_OK;
+  const int vec = ((uintptr_t)w & 15) == 0;
+  const int grid = grid_for(rows * (cols / 4), kThreads, 65536);
+  hipLaunchKernelGGL((quantize_q4_kernel<false>), dim3(grid), dim3(kThreads), 0, stream,
+                     (const void*)w, qs, scales, rows, cols, vec);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_quantize_q4_bf16(const uint16_t* w, uint8_t* qs, uint16_t* scales, int64_t rows,
+                         int64_t cols, hipStream_t stream) {
+  if (rows < 0 || cols <= 0 || cols % kBlock != 0 || ((uintptr_t)qs & 3)) return DNX_EINVAL;
+  if (rows == 0) return DNX_OK;
+  const int vec = ((uintptr_t)w & 7) == 0;
+  const int grid = grid_for(rows * (cols / 4), kThreads, 65536);
+  hipLaunchKernelGGL((quantize_q4_kernel<true>), dim3(grid), dim3(kThreads), 0, stream,
+                     (const void*)w, qs, scales, rows, cols, vec);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 

@@ -57,7 +57,10 @@ struct Buffer {
   bool weights = false;   // HBM copy is authoritative and immutable
 };
 
-enum Op { kOpMatmulQ8, kOpMatmulQ4, kOpSwiglu, kOpQuantize, kOpQuantizeBf16, kOpArgmax, kOpGelu };
+enum Op {
+  kOpMatmulQ8, kOpMatmulQ4, kOpSwiglu, kOpQuantize, kOpQuantizeBf16, kOpQuantizeQ4,
+  kOpQuantizeQ4Bf16, kOpArgmax, kOpGelu
+};
 
 struct Cmd {
   Op op;
@@ -383,6 +386,23 @@ bool run(const Cmd& c) {
       wrote_region(sc, scOff, rows * (pad / 32) * 4);
       return rc == DNX_OK;
     }
+    case kOpQuantizeQ4:
+    case kOpQuantizeQ4Bf16: {
+      const bool bf16 = c.op == kOpQuantizeQ4Bf16;
+      const int64_t src = c.a[0], srcOff = c.a[1], qs = c.a[2], qsOff = c.a[3];
+      const int64_t sc = c.a[4], scOff = c.a[5], rows = c.a[6], cols = c.a[7];
+      read_region(src, srcOff, rows * cols * (bf16 ? 2 : 4));
+      const int rc =
+          bf16 ? dnx_quantize_q4_bf16((const uint16_t*)dev_at(src, srcOff),
+                                      (uint8_t*)dev_at(qs, qsOff), (uint16_t*)dev_at(sc, scOff),
+                                      rows, cols, gStream)
+               : dnx_quantize_q4((const float*)dev_at(src, srcOff), (uint8_t*)dev_at(qs, qsOff),
+                                 (uint16_t*)dev_at(sc, scOff), rows, cols, gStream);
+      after_dispatch(kKindQuantizeWeights);
+      wrote_region(qs, qsOff, rows * (cols / 2));
+      wrote_region(sc, scOff, rows * (cols / 32) * 2);
+      return rc == DNX_OK;
+    }
     case kOpArgmax: {
       const int64_t x = c.a[0], xOff = c.a[1], n = c.a[2], out = c.a[3], outOff = c.a[4];
       read_region(x, xOff, n * 4);
@@ -624,6 +644,34 @@ void lab_gpu_enc_quantize_q8_bf16(int64_t src, int64_t srcOffset, int64_t qs, in
                                   int64_t cols, int64_t colsPad) {
   enc_quantize(kOpQuantizeBf16, src, srcOffset, qs, qsOffset, scales, scalesOffset, rows, cols,
                colsPad);
+}
+
+static void enc_quantize_q4(Op op, int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                            int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols) {
+  const int64_t esize = op == kOpQuantizeQ4Bf16 ? 2 : 4;
+  const bool ok = rows >= 0 && cols > 0 && cols % 32 == 0 &&
+                  in_bounds(src, srcOffset, rows * cols * esize) &&
+                  in_bounds(qs, qsOffset, rows * (cols / 2)) &&
+                  in_bounds(scales, scalesOffset, rows * (cols / 32) * 2) &&
+                  srcOffset % esize == 0 && qsOffset % 4 == 0 && scalesOffset % 2 == 0;
+  if (!ok) {
+    LOG("enc_quantize_q4: invalid arguments\n");
+    gFailed = true;
+    return;
+  }
+  record(op, {src, srcOffset, qs, qsOffset, scales, scalesOffset, rows, cols});
+}
+
+void lab_gpu_enc_quantize_q4(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                             int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols) {
+  enc_quantize_q4(kOpQuantizeQ4, src, srcOffset, qs, qsOffset, scales, scalesOffset, rows, cols);
+}
+
+void lab_gpu_enc_quantize_q4_bf16(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                                  int64_t scales, int64_t scalesOffset, int64_t rows,
+                                  int64_t cols) {
+  enc_quantize_q4(kOpQuantizeQ4Bf16, src, srcOffset, qs, qsOffset, scales, scalesOffset, rows,
+                  cols);
 }
 
 void lab_gpu_enc_argmax(int64_t x, int64_t xOffset, int64_t n, int64_t out, int64_t outOffset) {

@@ -45,6 +45,20 @@ def quantize_q8_bf16(w: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, ro
                                             cols_pad, _stream(stream)), "dnx_quantize_q8_bf16")
 
 
+def quantize_q4(w: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, rows: int, cols: int,
+                stream=None) -> None:
+    """lab_quantize_q4 on the GPU: fp32 [rows][cols] -> nibbles [rows][cols/2] + fp16 bits."""
+    _check(_lib.load().dnx_quantize_q4(_ptr(w), _ptr(qs), _ptr(scales), rows, cols,
+                                       _stream(stream)), "dnx_quantize_q4")
+
+
+def quantize_q4_bf16(w: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, rows: int,
+                     cols: int, stream=None) -> None:
+    """BF16 bits widened (p << 16), then lab_quantize_q4, in one kernel."""
+    _check(_lib.load().dnx_quantize_q4_bf16(_ptr(w), _ptr(qs), _ptr(scales), rows, cols,
+                                            _stream(stream)), "dnx_quantize_q4_bf16")
+
+
 def gemv_q8(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> None:
     _check(_lib.load().dnx_gemv_q8(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
                                    _stream(stream)), "dnx_gemv_q8")

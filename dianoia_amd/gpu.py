@@ -120,44 +120,70 @@ class GpuLinear:
                                     matrix.cols, matrix.cols))
 
     def upload_bf16(self, name: str, bf16: np.ndarray, rows: int, cols: int,
-                    rows_pad: int | None = None) -> None:
-        """Quantizes BF16 weights to Q8 on the GPU (part 4 of the path).
+                    rows_pad: int | None = None, fmt: str = "q8") -> None:
+        """Quantizes BF16 weights to Q8 (or Q4) on the GPU (part 4 of the path).
 
         The reference widens BF16 with ``p << 16`` and quantizes on the CPU
         (``vision_encoder.dart:36-66``, ``safetensors.dart:207-212``,
-        ``lab_quantize_q8``); this does both in one kernel, bit-exactly. A
-        width that is not a multiple of 32 is zero-padded to the next one
-        (the reference refuses it, ``native.dart:634-636``); ``rows_pad``
-        appends zero rows, whose outputs are exactly 0.
+        ``lab_quantize_q8`` / ``lab_quantize_q4``); this does both in one
+        kernel, bit-exactly. For Q8 a width that is not a multiple of 32 is
+        zero-padded to the next one (the reference refuses it,
+        ``native.dart:634-636``); Q4 refuses it as the reference does
+        (``native.dart:793-796``). ``rows_pad`` appends zero rows, whose
+        outputs are exactly 0.
         """
-        self._check_open()
         bf16 = np.ascontiguousarray(bf16, dtype=np.uint16).reshape(-1)
-        if rows <= 0 or cols <= 0 or bf16.size < rows * cols:
-            raise ArgumentError(f"invalid BF16 weights for {rows} x {cols}")
+        self._upload_quantized(name, bf16, 2, rows, cols, rows_pad, fmt)
+
+    def upload_f32(self, name: str, w: np.ndarray, rows: int, cols: int,
+                   rows_pad: int | None = None, fmt: str = "q8") -> None:
+        """Quantizes fp32 weights to Q8 or Q4 on the GPU, bit-exact with
+        ``NativeQ8Matrix.quantize`` / ``NativeQ4Matrix.quantize``
+        (``native.dart:633-641``, ``:793-801``); padding as ``upload_bf16``."""
+        w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+        self._upload_quantized(name, w, 4, rows, cols, rows_pad, fmt)
+
+    def _upload_quantized(self, name: str, src_values: np.ndarray, esize: int, rows: int,
+                          cols: int, rows_pad: int | None, fmt: str) -> None:
+        self._check_open()
+        if fmt not in ("q4", "q8"):
+            raise ArgumentError(f"cannot quantize to {fmt}")
+        if rows <= 0 or cols <= 0 or src_values.size < rows * cols:
+            raise ArgumentError(f"invalid weights for {rows} x {cols}")
+        q4 = fmt == "q4"
+        if q4 and cols % 32 != 0:
+            raise ArgumentError(f"Q4 needs cols to be a multiple of 32, got {cols}")
         cols_pad = (cols + 31) // 32 * 32
         out_rows = rows if rows_pad is None else rows_pad
         if out_rows < rows:
             raise ArgumentError("rows_pad must not be below rows")
-        src = self._lib.lab_gpu_buffer(rows * cols * 2)
+        nsrc = rows * cols * esize
+        src = self._lib.lab_gpu_buffer(nsrc)
         if src < 0:
-            raise StateError("GPU buffer for the BF16 weights failed")
+            raise StateError("GPU buffer for the source weights failed")
         try:
-            self._bytes_view(src, rows * cols * 2)[:] = bf16[: rows * cols].view(np.uint8)
-            qs_bytes = out_rows * cols_pad
+            self._bytes_view(src, nsrc)[:] = src_values[: rows * cols].view(np.uint8)
+            qs_bytes = out_rows * (cols_pad // 2 if q4 else cols_pad)
             scales_at = (qs_bytes + 63) // 64 * 64
-            nbytes = scales_at + out_rows * (cols_pad // 32) * 4
+            nbytes = scales_at + out_rows * (cols_pad // 32) * (2 if q4 else 4)
             dst = self._lib.lab_gpu_buffer(nbytes)
             if dst < 0:
                 raise StateError(f"GPU buffer of {nbytes} bytes failed")
             self._owned.append(dst)
             self._lib.lab_gpu_begin()
-            self._lib.lab_gpu_enc_quantize_q8_bf16(src, 0, dst, 0, dst, scales_at, rows, cols,
-                                                   cols_pad)
+            if q4:
+                enc = (self._lib.lab_gpu_enc_quantize_q4_bf16 if esize == 2
+                       else self._lib.lab_gpu_enc_quantize_q4)
+                enc(src, 0, dst, 0, dst, scales_at, rows, cols)
+            else:
+                enc = (self._lib.lab_gpu_enc_quantize_q8_bf16 if esize == 2
+                       else self._lib.lab_gpu_enc_quantize_q8)
+                enc(src, 0, dst, 0, dst, scales_at, rows, cols, cols_pad)
             if self._lib.lab_gpu_commit(1) != 1:
                 raise StateError("GPU command buffer failed")
         finally:
             self._lib.lab_gpu_release(src)
-        self._replace(name, _Matrix(False, dst, 0, scales_at, out_rows, cols_pad, cols))
+        self._replace(name, _Matrix(q4, dst, 0, scales_at, out_rows, cols_pad, cols))
 
     def quantized(self, name: str) -> tuple[np.ndarray, np.ndarray]:
         """The Q8 values and scales a matrix holds on the GPU (for checks)."""

@@ -40,6 +40,19 @@ int dnx_quantize_q8(const float* x, int8_t* qs, float* scales, int64_t rows, int
 int dnx_quantize_q8_bf16(const uint16_t* w, int8_t* qs, float* scales, int64_t rows,
                          int64_t cols, int64_t cols_pad, dnx_stream_t stream);
 
+// lab_quantize_q4 (lab_native.c:928-955) on the GPU, bit-exact: rows x cols
+// fp32 (cols a multiple of 32, as NativeQ4Matrix.quantize requires,
+// native.dart:793-796) -> Q4 nibbles
+// [rows][cols/2] (byte k: weight k low, weight k + 16 high) + fp16 scale
+// bits [rows][cols/32]. The load-time quantizer of Q4 weights.
+int dnx_quantize_q4(const float* w, uint8_t* qs, uint16_t* scales, int64_t rows, int64_t cols,
+                    dnx_stream_t stream);
+
+// _widenBf16 (safetensors.dart:207-212) then lab_quantize_q4, fused;
+// bit-exact with that CPU pair.
+int dnx_quantize_q4_bf16(const uint16_t* w, uint8_t* qs, uint16_t* scales, int64_t rows,
+                         int64_t cols, dnx_stream_t stream);
+
 // Decode GEMV, n <= 4 tokens, fp32 x quantized in the kernel's prologue:
 // lab_gemm_q8 / lab_gemm_q4 mode 1 (lab_native.c:553-579, :1059-1080) with
 // the CPU's exact float order, so y is bit-identical to theirs.

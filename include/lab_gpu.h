@@ -115,6 +115,19 @@ void lab_gpu_enc_quantize_q8_bf16(int64_t src, int64_t srcOffset, int64_t qs, in
                                   int64_t scales, int64_t scalesOffset, int64_t rows,
                                   int64_t cols, int64_t colsPad);
 
+// Load-time Q4 quantization on the GPU, the Q4 twin of the above: rows x
+// cols values (fp32, or bf16 bits) at src + srcOffset become nibbles
+// [rows][cols/2] at qs + qsOffset and fp16 scale bits [rows][cols/32] at
+// scales + scalesOffset, bit-exact with lab_quantize_q4 (lab_native.c:
+// 928-955, bound at native.dart:178-187) after _widenBf16 for BF16. cols
+// must be a multiple of 32, as NativeQ4Matrix.quantize requires
+// (native.dart:793-796); otherwise the command buffer fails.
+void lab_gpu_enc_quantize_q4(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                             int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols);
+void lab_gpu_enc_quantize_q4_bf16(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                                  int64_t scales, int64_t scalesOffset, int64_t rows,
+                                  int64_t cols);
+
 // Greedy token on the GPU: argmaxToken (sampler.dart:137-152, no
 // suppression) over n floats at x + xOffset, the index written as one int64
 // at out + outOffset. Replaces the logits copy + host argmax of

@@ -61,6 +61,43 @@ def edge_rows() -> np.ndarray:
     return np.stack(rows).astype(np.float32)
 
 
+def q4_edge_rows() -> np.ndarray:
+    """Rows of 64 values whose blocks hit lab_quantize_q4's edge cases."""
+    rows = []
+    z = np.zeros(32, np.float32)
+    # all-zero block (max stays +0: d = -0, id = 0), and one of negative zeros
+    rows.append(np.concatenate([z, -z]))
+    # equal magnitudes of both signs: the first in column order sets d's sign
+    a = np.zeros(32, np.float32)
+    a[[2, 5, 20]] = f32(3.0, -3.0, 1.5)
+    b = np.zeros(32, np.float32)
+    b[[1, 17, 30]] = f32(-3.0, 3.0, -2.0)
+    rows.append(np.concatenate([a, b]))
+    # max = -8 gives d = 1, id = 1: x + 8.5 lands on k + 0.5 and just below
+    h = (np.arange(32, dtype=np.float32) - 8.0) / np.float32(2.0)
+    h[0] = -8.0
+    h2 = np.nextafter(h, np.float32(-np.inf)).astype(np.float32)
+    h2[0] = -8.0
+    rows.append(np.concatenate([h, h2]))
+    # NaN never wins; an infinite max gives d = -inf, id = -0 (inf * -0 is NaN)
+    n = np.linspace(-1.0, 1.0, 32, dtype=np.float32)
+    n[[0, 9]] = np.float32(np.nan)
+    i = np.linspace(-2.0, 2.0, 32, dtype=np.float32)
+    i[4] = np.float32(np.inf)
+    i[6] = np.float32(np.nan)
+    rows.append(np.concatenate([n, i]))
+    # all-NaN block (max stays 0), and a fp16-overflowing scale (|d| > 65504)
+    nn = np.full(32, np.nan, np.float32)
+    big = np.linspace(-1e30, 6e29, 32, dtype=np.float32)
+    rows.append(np.concatenate([nn, big]))
+    # scales below fp16's range (subnormal and zero halves), fp32 denormals
+    tiny = np.linspace(-3e-6, 2e-6, 32, dtype=np.float32)
+    den = np.zeros(32, np.float32)
+    den[:4] = f32(1e-45, -3e-45, 2e-44, -1e-40)
+    rows.append(np.concatenate([tiny, den]))
+    return np.stack(rows).astype(np.float32)
+
+
 def main() -> None:
     ref = O.Reference()
     out = {}
@@ -80,6 +117,9 @@ def main() -> None:
     w[1, 5] = -3.0
     qs4, sc4 = ref.quantize_q4(w)
     np.savez_compressed(os.path.join(HERE, "quantize_q4.npz"), x=w, qs=qs4, scales=sc4)
+    e4 = q4_edge_rows()
+    qs4, sc4 = ref.quantize_q4(e4)
+    np.savez_compressed(os.path.join(HERE, "quantize_q4_edges.npz"), x=e4, qs=qs4, scales=sc4)
 
     # ---- lab_gemm_q8 / lab_gemm_q4, both modes, shapes from the reference's
     # tests (37 x 2048, n = 3 and 6) and from the benchmark widths.

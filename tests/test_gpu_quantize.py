@@ -72,6 +72,89 @@ def test_bf16_quantizer_through_the_abi(gpu_ready, orc):
         gpu.dispose()
 
 
+# ---- lab_quantize_q4 (lab_native.c:928-955)
+
+def gpu_quantize_q4(x, bf16=False):
+    rows, cols = x.shape
+    qs = torch.zeros((rows, cols // 2), dtype=torch.uint8, device="cuda")
+    sc = torch.zeros((rows, cols // 32), dtype=torch.int16, device="cuda")
+    (D.quantize_q4_bf16 if bf16 else D.quantize_q4)(dev(x), qs, sc, rows, cols)
+    return host(qs), host(sc).view(np.uint16)
+
+
+@pytest.mark.parametrize("name", ["quantize_q4", "quantize_q4_edges"])
+def test_quantize_q4_matches_golden(gpu_ready, name):
+    d = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+    qs, sc = gpu_quantize_q4(d["x"])
+    assert np.array_equal(qs, d["qs"])
+    assert np.array_equal(sc, d["scales"])
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 32), (6144, 2048), (2048, 6144), (37, 1152), (3, 96)])
+def test_quantize_q4_matches_oracle(gpu_ready, orc, rows, cols):
+    rng = np.random.default_rng(rows * 5 + cols)
+    x = rng.standard_normal((rows, cols), dtype=np.float32)
+    x *= (np.float32(10.0) ** rng.integers(-8, 9, size=(rows, 1))).astype(np.float32)
+    # Small integers: many blocks whose largest magnitude appears with both
+    # signs, where the first in column order decides d's sign.
+    x[rows // 2:] = rng.integers(-4, 5, size=(rows - rows // 2, cols)).astype(np.float32)
+    qs, sc = gpu_quantize_q4(x)
+    q2, s2 = orc.quantize_q4(x)
+    assert np.array_equal(qs, q2)
+    assert np.array_equal(sc, s2)
+
+
+@pytest.mark.parametrize("rows,cols", [(4304, 1152), (1152, 4320), (5, 64)])
+def test_bf16_q4_weight_quantizer(gpu_ready, orc, rows, cols):
+    from dianoia_amd.synth import bf16_weights
+    w = bf16_weights(np.random.default_rng(rows + 3 * cols), rows, cols)
+    widened = (w.astype(np.uint32) << 16).view(np.float32)
+    qs, sc = gpu_quantize_q4(w, bf16=True)
+    q2, s2 = orc.quantize_q4(widened)
+    assert np.array_equal(qs, q2)
+    assert np.array_equal(sc, s2)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_q4_quantizer_through_the_abi(gpu_ready, orc, bf16):
+    """GpuLinear.upload_f32 / upload_bf16 with fmt="q4" -> lab_gpu_enc_quantize_q4*,
+    then a decode product on the quantized weights, bit-exact with the CPU."""
+    from dianoia_amd.gpu import GpuLinear
+    from dianoia_amd.synth import bf16_weights
+    rows, cols = 300, 2048
+    rng = np.random.default_rng(9)
+    gpu = GpuLinear.start()
+    try:
+        if bf16:
+            w = bf16_weights(rng, rows, cols)
+            gpu.upload_bf16("w", w, rows, cols, fmt="q4")
+            wf = (w.astype(np.uint32) << 16).view(np.float32)
+        else:
+            wf = rng.standard_normal((rows, cols), dtype=np.float32)
+            gpu.upload_f32("w", wf, rows, cols, fmt="q4")
+        qs, sc = gpu.quantized("w")
+        q2, s2 = orc.quantize_q4(wf)
+        assert np.array_equal(qs, q2)
+        assert np.array_equal(sc, s2)
+        xs = rng.standard_normal(cols, dtype=np.float32)
+        ys = np.zeros(rows, np.float32)
+        gpu.apply("w", xs, ys, 1)
+        cpu = orc.gemm_q4(q2, s2, xs, 1, threads=4, mode=1).reshape(-1)
+        assert np.array_equal(bits(ys), bits(cpu))
+    finally:
+        gpu.dispose()
+
+
+def test_q4_quantizer_rejects_bad_shapes(gpu_ready):
+    x = torch.zeros(96, device="cuda")
+    qs = torch.zeros(48, dtype=torch.uint8, device="cuda")
+    sc = torch.zeros(3, dtype=torch.int16, device="cuda")
+    with pytest.raises(RuntimeError):
+        D.quantize_q4(x, qs, sc, 1, 48)   # not a multiple of 32
+    with pytest.raises(RuntimeError):
+        D.quantize_q4(x, qs[1:], sc, 1, 32)  # qs not 4-byte aligned
+
+
 def test_quantizer_rejects_bad_shapes(gpu_ready):
     x = torch.zeros(64, device="cuda")
     out = torch.zeros(64, dtype=torch.int8, device="cuda")

@@ -34,8 +34,9 @@ def test_quantize_q8_matches_golden(orc, name):
     assert np.array_equal(bits(sc), bits(d["scales"]))
 
 
-def test_quantize_q4_matches_golden(orc):
-    d = np.load(os.path.join(GOLDEN, "quantize_q4.npz"))
+@pytest.mark.parametrize("name", ["quantize_q4", "quantize_q4_edges"])
+def test_quantize_q4_matches_golden(orc, name):
+    d = np.load(os.path.join(GOLDEN, f"{name}.npz"))
     qs, sc = orc.quantize_q4(d["x"])
     assert np.array_equal(qs, d["qs"])
     assert np.array_equal(sc, d["scales"])
