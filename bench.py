@@ -323,36 +323,52 @@ def bench_c4(torch, D, synth, timer, steps, warmup):
         D.quantize_q8(h, xq, xs, M, 4320, 4320)
         D.gemm_q8(q2, s2, xq, xs, y, 1152, 4320, M)
 
-    # BF16 -> Q4 (lab_quantize_q4 after _widenBf16) on fc1's weights, and on
-    # a 32768 x 4096 matrix (256 MiB of BF16) for the streaming rate.
-    q4_1 = torch.empty((4304, 576), dtype=torch.uint8, device="cuda")
-    d4_1 = torch.empty((4304, 36), dtype=torch.int16, device="cuda")
-    gen = torch.Generator(device="cuda").manual_seed(4)
-    wbig = (torch.randn((32768, 4096), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
-    wbig = wbig.view(torch.int16)
-    q4_b = torch.empty((32768, 2048), dtype=torch.uint8, device="cuda")
-    d4_b = torch.empty((32768, 128), dtype=torch.int16, device="cuda")
-
-    def quant_q4(i):
-        D.quantize_q4_bf16(w1, q4_1, d4_1, 4304, 1152)
-
-    def quant_q4_big(i):
-        D.quantize_q4_bf16(wbig, q4_b, d4_b, 32768, 4096)
-
     n = max(10, steps // 4)
     quant_w(0)
-    means = timer.kernel_means([quant_w, fc1_, gelu_, fc2_, quant_q4, quant_q4_big], n)
-    q4_bytes = lambda r, c: r * c * 2 + r * c // 2 + r * (c // 32) * 2
+    means = timer.kernel_means([quant_w, fc1_, gelu_, fc2_], n)
     qbytes = (4304 * 1152 * 2 + 4320 * 1152 + 4320 * 36 * 4) + (1152 * 4304 * 2 + 1152 * 4320 + 1152 * 135 * 4)
     ops = 2 * M * 4304 * 1152
     return {"quantize_weights_ms": means[0], "quantize_weights_gbps": qbytes / means[0] / 1e6,
             "fc1_ms": means[1], "fc1_tops": ops / means[1] / 1e9, "gelu_ms": means[2],
             "fc2_ms": means[3], "fc2_tops": ops / means[3] / 1e9,
-            "pair_tops": 2 * ops / (means[1] + means[2] + means[3]) / 1e9,
-            "quantize_q4_fc1_ms": means[4],
-            "quantize_q4_fc1_gbps": q4_bytes(4304, 1152) / means[4] / 1e6,
-            "quantize_q4_32768x4096_ms": means[5],
-            "quantize_q4_32768x4096_gbps": q4_bytes(32768, 4096) / means[5] / 1e6}
+            "pair_tops": 2 * ops / (means[1] + means[2] + means[3]) / 1e9}
+
+
+def bench_loaders(torch, D, timer, steps):
+    """The other load-time converters (beyond the north star's BF16 -> Q8):
+    BF16 -> Q4 (lab_quantize_q4 after _widenBf16) on a 32768 x 4096 matrix
+    (256 MiB of BF16), and the Q6_K -> Q8 adapter (dequantizeQ6K +
+    lab_quantize_q8, gguf.dart:402-414) at the LM-head shape 151936 x 2048.
+    Inputs are generated on the GPU; both kernels are HBM-bound."""
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    wbig = (torch.randn((32768, 4096), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    wbig = wbig.view(torch.int16)
+    q4 = torch.empty((32768, 2048), dtype=torch.uint8, device="cuda")
+    d4 = torch.empty((32768, 128), dtype=torch.int16, device="cuda")
+    rows, cols = 151936, 2048
+    # Q6_K blocks with random low/high bits and scales and a small positive d.
+    blocks = torch.randint(0, 256, (rows * cols // 256, 210), dtype=torch.uint8, device="cuda",
+                           generator=gen)
+    d = (torch.rand(rows * cols // 256, device="cuda", generator=gen) * 0.004).to(torch.float16)
+    blocks[:, 208:210] = d.view(torch.uint8).view(-1, 2)
+    q8 = torch.empty((rows, cols), dtype=torch.int8, device="cuda")
+    s8 = torch.empty((rows, cols // 32), device="cuda")
+
+    def q4_(i):
+        D.quantize_q4_bf16(wbig, q4, d4, 32768, 4096)
+
+    def q6k_(i):
+        D.q6k_to_q8(blocks, q8, s8, rows, cols)
+
+    means = timer.kernel_means([q4_, q6k_], max(10, steps // 4))
+    q4_bytes = 32768 * 4096 * 2 + 32768 * 2048 + 32768 * 128 * 2
+    q6k_bytes = rows * cols // 256 * 210 + rows * cols + rows * (cols // 32) * 4
+    del wbig, blocks
+    return {"bf16_to_q4_32768x4096_ms": means[0],
+            "bf16_to_q4_32768x4096_gbps": q4_bytes / means[0] / 1e6,
+            "q6k_to_q8_151936x2048_ms": means[1],
+            "q6k_to_q8_151936x2048_gbps": q6k_bytes / means[1] / 1e6,
+            "bytes": {"bf16_to_q4": q4_bytes, "q6k_to_q8": q6k_bytes}}
 
 
 # ------------------------------------------------------------------ CPU
@@ -610,6 +626,9 @@ def main():
             print(f"bench: {name}", file=sys.stderr, flush=True)
             configs[name] = fn(torch, D, synth, timer, args.steps, args.warmup)
             torch.cuda.empty_cache()
+        print("bench: load-time converters", file=sys.stderr, flush=True)
+        configs["load_time_converters"] = bench_loaders(torch, D, timer, args.steps)
+        torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
         print("bench: cpu baseline", file=sys.stderr, flush=True)

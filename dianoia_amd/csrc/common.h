@@ -109,6 +109,9 @@ __device__ int dnx_raw_buffer_load_i32(i32x4 rsrc, int voffset, int soffset, int
     __asm("llvm.amdgcn.raw.buffer.load.i32");
 __device__ short dnx_raw_buffer_load_i16(i32x4 rsrc, int voffset, int soffset, int aux)
     __asm("llvm.amdgcn.raw.buffer.load.i16");
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+__device__ i32x2 dnx_raw_buffer_load_v2i32(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v2i32");
 
 constexpr int kBufferFlags = 0x00020000;  // gfx9 resource word 3: 32-bit raw data
 

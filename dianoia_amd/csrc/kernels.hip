@@ -19,123 +19,258 @@ constexpr int kThreads = 256;  // 4 waves per workgroup
 
 // ------------------------------------------------------------ quantizer
 
-// lab_quantize_q8 over rows x cols values into rows x cols_pad int8 and
-// rows x cols_pad/32 fp32 scales (lab_native.c:407-429). cols_pad is a
-// multiple of 32 and >= cols; values at cols..cols_pad are zero padding.
-// One thread quantizes 4 consecutive values; 8 threads share a block.
-// Input is fp32 or bf16 (widened p << 16, safetensors.dart:207-212).
+// Items per thread per pass of the quantizers. A pass issues all of its
+// loads before it uses any: one small load in flight per thread leaves a
+// quantizer latency-bound at a quarter of HBM. The loads are raw buffer
+// loads, so an item past the end or a padding column reads zeros with no
+// branch and no memory access (a branch around a load makes the compiler
+// wait for it right there).
+constexpr int kItems = 8;
+constexpr int kFar = 0x7fffff00;  // an offset past every buffer these kernels read
+
+// One quad (4 values) as loaded: 16 bytes of fp32 or 8 bytes of bf16 bits.
 template <bool kBf16>
-__global__ void __launch_bounds__(kThreads)
-quantize_q8_kernel(const void* __restrict__ src, int8_t* __restrict__ qs,
-                   float* __restrict__ scales, int64_t rows, int64_t cols, int64_t cols_pad,
-                   int vec_ok) {
-  const int64_t quads_per_row = cols_pad / 4;
-  const int64_t total = rows * quads_per_row;
-  // Whole 8-lane groups stay together: quads_per_row is a multiple of 8.
-  for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < total;
-       q += (int64_t)gridDim.x * kThreads) {
-    const int64_t row = q / quads_per_row;
-    const int64_t c = (q - row * quads_per_row) * 4;
-    float4 v;
-    if (kBf16) {
-      const uint16_t* p = (const uint16_t*)src + row * cols + c;
-      if (vec_ok && c + 4 <= cols) {
-        const uint2 raw = *(const uint2*)p;
-        v = make_float4(__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
-                        __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u));
-      } else {
-        v.x = c + 0 < cols ? bf16_to_float(p[0]) : 0.0f;
-        v.y = c + 1 < cols ? bf16_to_float(p[1]) : 0.0f;
-        v.z = c + 2 < cols ? bf16_to_float(p[2]) : 0.0f;
-        v.w = c + 3 < cols ? bf16_to_float(p[3]) : 0.0f;
-      }
-    } else {
-      const float* p = (const float*)src + row * cols + c;
-      if (vec_ok && c + 4 <= cols) {
-        v = *(const float4*)p;
-      } else {
-        v.x = c + 0 < cols ? p[0] : 0.0f;
-        v.y = c + 1 < cols ? p[1] : 0.0f;
-        v.z = c + 2 < cols ? p[2] : 0.0f;
-        v.w = c + 3 < cols ? p[3] : 0.0f;
-      }
-    }
-    const float amax = group8_max(fmaxf(0.0f, max4abs(v)));
-    const float scale = q8_scale(amax);
-    const float inv = q8_inv(scale);
-    *(int*)(qs + row * cols_pad + c) = quant4(v, inv);
-    if ((c & 31) == 0) scales[row * (cols_pad / 32) + c / 32] = scale;
+struct RawQuad {
+  uint32_t w[kBf16 ? 2 : 4];
+};
+template <bool kBf16>
+DNX_DEV RawQuad<kBf16> load_raw_quad(i32x4 rsrc, int off) {
+  RawQuad<kBf16> r;
+  if (kBf16) {
+    const i32x2 v = dnx_raw_buffer_load_v2i32(rsrc, off, 0, 0);
+    r.w[0] = (uint32_t)v.x;
+    r.w[1] = (uint32_t)v.y;
+  } else {
+    const uint4 v = buffer_load16(rsrc, off);
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+    r.w[2] = v.z;
+    r.w[3] = v.w;
   }
+  return r;
+}
+template <bool kBf16>
+DNX_DEV float4 widen(const RawQuad<kBf16>& r) {
+  if (kBf16) {  // bf16 bits p -> float p << 16 (safetensors.dart:207-212)
+    return make_float4(__uint_as_float(r.w[0] << 16), __uint_as_float(r.w[0] & 0xffff0000u),
+                       __uint_as_float(r.w[1] << 16), __uint_as_float(r.w[1] & 0xffff0000u));
+  }
+  return make_float4(__uint_as_float(r.w[0]), __uint_as_float(r.w[1]), __uint_as_float(r.w[2]),
+                     __uint_as_float(r.w[3]));
+}
+
+// Four consecutive values of row `row` from column c with plain loads (the
+// generic path: unaligned inputs, odd widths, inputs of 2 GB or more);
+// columns >= cols are zero.
+template <bool kBf16>
+DNX_DEV float4 load_quad(const void* src, int64_t row, int64_t c, int64_t cols) {
+  float4 v;
+  if (kBf16) {
+    const uint16_t* p = (const uint16_t*)src + row * cols + c;
+    v.x = c + 0 < cols ? bf16_to_float(p[0]) : 0.0f;
+    v.y = c + 1 < cols ? bf16_to_float(p[1]) : 0.0f;
+    v.z = c + 2 < cols ? bf16_to_float(p[2]) : 0.0f;
+    v.w = c + 3 < cols ? bf16_to_float(p[3]) : 0.0f;
+  } else {
+    const float* p = (const float*)src + row * cols + c;
+    v.x = c + 0 < cols ? p[0] : 0.0f;
+    v.y = c + 1 < cols ? p[1] : 0.0f;
+    v.z = c + 2 < cols ? p[2] : 0.0f;
+    v.w = c + 3 < cols ? p[3] : 0.0f;
+  }
+  return v;
+}
+
+// lab_quantize_q8 (lab_native.c:407-429) of quad q: its 8-lane group is
+// one 32-block; int8 at qs + 4q, the block's scale at scales[q / 8] (padded
+// rows keep whole blocks, so the layout is linear in q).
+DNX_DEV void q8_quad(float4 v, int64_t q, int8_t* qs, float* scales) {
+  const float amax = group8_max(fmaxf(0.0f, max4abs(v)));
+  const float scale = q8_scale(amax);
+  const float inv = q8_inv(scale);
+  *(int*)(qs + 4 * q) = quant4(v, inv);
+  if ((q & 7) == 0) scales[q >> 3] = scale;
 }
 
 // lab_quantize_q4 (lab_native.c:928-955, llama.cpp's quantize_row_q4_0_ref)
-// over rows x cols values, cols a multiple of 32, into Q4 nibbles
-// [rows][cols/2] and fp16 scale bits [rows][cols/32]. Per block: max = the
-// first value (in column order) of largest magnitude (`a > amax` from 0, so
-// NaN never wins and ties keep the first); d = max / -8; id = 1/d (0 when
-// d == 0); q = (int8_t)(x * id + 8.5f) clamped above at 15 (two float
-// roundings: the reference is built without contraction); byte k = q[k] |
-// q[k + 16] << 4; the scale is d rounded to fp16 (RNE, as _mm_cvtps_ph).
-// One thread takes 4 consecutive values, 8 threads a block: the group's
-// largest magnitude, then the lowest (index, sign) key holding it. Lanes 0-3
-// of a group write the block's 16 bytes, taking the high nibbles (values
-// 16..31) from lanes 4-7. Input is fp32 or bf16 (widened p << 16).
-template <bool kBf16>
+// of quad q. Per block: max = the first value (in column order) of largest
+// magnitude (`a > amax` from 0, so NaN never wins and ties keep the first);
+// d = max / -8; id = 1/d (0 when d == 0); q = (int8_t)(x * id + 8.5f)
+// clamped above at 15 (two float roundings: the reference is built without
+// contraction); byte k = q[k] | q[k + 16] << 4; the scale is d rounded to
+// fp16 (RNE, as _mm_cvtps_ph). The 8-lane group finds the largest
+// magnitude, then the lowest (index, sign) key holding it; lanes 0-3 write
+// the block's 16 bytes at 16 (q / 8), taking the high nibbles (values
+// 16..31) from lanes 4-7.
+DNX_DEV void q4_quad(float4 v, int64_t q, uint8_t* qs, uint16_t* scales) {
+  const int k0 = (int)((4 * q) & 31);
+  const float amax = group8_max(fmaxf(0.0f, max4abs(v)));
+  // Key 2k + sign of this lane's first value of magnitude amax (64: none).
+  int key = 64;
+  if (amax > 0.0f) {
+    const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 3; i >= 0; i--) {
+      if (fabsf(e[i]) == amax) key = 2 * (k0 + i) + (e[i] < 0.0f ? 1 : 0);
+    }
+  }
+  key = group8_min(key);
+  const float max = key == 64 ? 0.0f : (key & 1) ? -amax : amax;
+  const float d = max / -8.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  // This lane's 4 values as (int8_t) bytes; lanes 0-3 pair with lanes 4-7.
+  const int own = (q4_value(v.x, id) & 0xff) | ((q4_value(v.y, id) & 0xff) << 8) |
+                  ((q4_value(v.z, id) & 0xff) << 16) | ((q4_value(v.w, id) & 0xff) << 24);
+  const int high = __shfl_xor(own, 4);
+  if (k0 < 16) {
+    uint32_t out = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int lo = (int8_t)(own >> (8 * i));
+      const int hi = (int8_t)(high >> (8 * i));
+      out |= (uint32_t)((lo | (hi << 4)) & 0xff) << (8 * i);
+    }
+    *(uint32_t*)(qs + 16 * (q >> 3) + k0) = out;
+  }
+  if (k0 == 0) scales[q >> 3] = __builtin_bit_cast(uint16_t, (_Float16)d);
+}
+
+// Q8 (kQ4 false) or Q4 quantizer over rows x cols values (fp32 or bf16),
+// cols a multiple of 4 and the input below 2 GB: quad q = (row, c) of the
+// output's rows x cols_pad (cols_pad a multiple of 32 >= cols; Q4 has no
+// padding); columns >= cols are zero padding (Q8, R10's extension). One
+// thread per quad, 8 threads per 32-block; a pass takes up to kItems quads
+// per thread, one grid apart (whole 8-lane groups stay together: both the
+// row length and the stride are multiples of 8 quads).
+template <bool kQ4, bool kBf16, bool kPad>
 __global__ void __launch_bounds__(kThreads)
-quantize_q4_kernel(const void* __restrict__ src, uint8_t* __restrict__ qs,
-                   uint16_t* __restrict__ scales, int64_t rows, int64_t cols, int vec_ok) {
-  const int64_t quads_per_row = cols / 4;
-  const int64_t total = rows * quads_per_row;
+quantize_kernel(const void* __restrict__ src, void* __restrict__ qs, void* __restrict__ scales,
+                int64_t rows, int cols, int cols_pad, uint32_t src_bytes) {
+  constexpr int kEsize = kBf16 ? 2 : 4;
+  const int qpr = cols_pad / 4;
+  const int64_t total = rows * qpr;
+  const i32x4 rsrc = buffer_rsrc(src, src_bytes);
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t q0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; q0 < total;
+       q0 += stride * kItems) {
+    RawQuad<kBf16> raw[kItems];
+#pragma unroll
+    for (int u = 0; u < kItems; u++) {
+      const int64_t q = q0 + u * stride;
+      int off;
+      if (kPad) {  // total < 2^31: 32-bit division
+        const uint32_t row = (uint32_t)q / (uint32_t)qpr;
+        const int c = (int)((uint32_t)q - row * (uint32_t)qpr) * 4;
+        off = (q < total && c < cols) ? (int)(((int64_t)row * cols + c) * kEsize) : kFar;
+      } else {
+        off = q < total ? (int)(q * 4 * kEsize) : kFar;
+      }
+      raw[u] = load_raw_quad<kBf16>(rsrc, off);
+    }
+#pragma unroll
+    for (int u = 0; u < kItems; u++) {
+      const int64_t q = q0 + u * stride;
+      if (q >= total) break;
+      if (kQ4) {
+        q4_quad(widen(raw[u]), q, (uint8_t*)qs, (uint16_t*)scales);
+      } else {
+        q8_quad(widen(raw[u]), q, (int8_t*)qs, (float*)scales);
+      }
+    }
+  }
+}
+
+// The generic path of the same quantizers: one quad per thread per step,
+// plain loads (any alignment, any width, any size).
+template <bool kQ4, bool kBf16>
+__global__ void __launch_bounds__(kThreads)
+quantize_generic_kernel(const void* __restrict__ src, void* __restrict__ qs,
+                        void* __restrict__ scales, int64_t rows, int64_t cols, int64_t cols_pad) {
+  const int64_t qpr = cols_pad / 4;
+  const int64_t total = rows * qpr;
   for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < total;
        q += (int64_t)gridDim.x * kThreads) {
-    const int64_t row = q / quads_per_row;
-    const int64_t c = (q - row * quads_per_row) * 4;
-    float4 v;
-    if (kBf16) {
-      const uint16_t* p = (const uint16_t*)src + row * cols + c;
-      if (vec_ok) {
-        const uint2 raw = *(const uint2*)p;
-        v = make_float4(__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
-                        __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u));
-      } else {
-        v = make_float4(bf16_to_float(p[0]), bf16_to_float(p[1]), bf16_to_float(p[2]),
-                        bf16_to_float(p[3]));
-      }
+    const int64_t row = q / qpr;
+    const float4 v = load_quad<kBf16>(src, row, (q - row * qpr) * 4, cols);
+    if (kQ4) {
+      q4_quad(v, q, (uint8_t*)qs, (uint16_t*)scales);
     } else {
-      const float* p = (const float*)src + row * cols + c;
-      v = vec_ok ? *(const float4*)p : make_float4(p[0], p[1], p[2], p[3]);
+      q8_quad(v, q, (int8_t*)qs, (float*)scales);
     }
-    const int k0 = (int)(c & 31);
-    const float amax = group8_max(fmaxf(0.0f, max4abs(v)));
-    // Key 2k + sign of this lane's first value of magnitude amax (64: none).
-    int key = 64;
-    if (amax > 0.0f) {
-      const float e[4] = {v.x, v.y, v.z, v.w};
+  }
+}
+
+// The Q6_K -> Q8 embedding / LM-head adapter (lib/src/gguf.dart:402-414):
+// dequantizeQ6K (:220-254, ggml's dequantize_row_q6_K) then lab_quantize_q8
+// (lab_native.c:407-429), fused. rows x cols values, cols a multiple of 256,
+// arrive as 210-byte super-blocks, row after row: ql[128] (4 low bits),
+// qh[64] (2 high bits each), int8 sc[16] (one per 16 values), fp16 d. Value
+// v of a super-block: half h = v / 128, w = v % 128, quarter u = w / 32,
+// l = w % 32; low bits from ql[64h + l + 32(u & 1)] (high nibble when
+// u >= 2), high bits (qh[32h + l] >> 2u) & 3, scale sc[8h + l/16 + 2u].
+// The reference computes d * sc * (q - 32) in double and stores a float:
+// d * sc is exact in float (at most 19 significant bits), so one float
+// multiply by (q - 32) rounds the same exact product once, identically.
+// Then q8_quad, bit-exact.
+//
+// One wave takes one super-block per item (lane L: values 4L..4L+3, one
+// 16-value scale group; 8 lanes per Q8 block). Super-blocks start 2-byte
+// aligned (210 = 2 x 105), so lane L loads aligned dword L of the block's
+// span (one coalesced load per lane and item, bounded by the buffer) and
+// each lane gathers its bytes from the wave's registers with ds_bpermute:
+// 4 ql bytes and 4 qh bytes (two dwords and an alignbyte each) and its
+// scale byte. d comes from a 2-byte load of the block's last bytes.
+__global__ void __launch_bounds__(kThreads)
+q6k_to_q8_kernel(const uint8_t* __restrict__ src, int8_t* __restrict__ qs,
+                 float* __restrict__ scales, int64_t rows, int64_t cols) {
+  const int64_t total = rows * (cols / 4);   // a multiple of 64: whole waves
+  const int lane = threadIdx.x & 63;
+  const i32x4 rsrc = buffer_rsrc(src, (uint32_t)(rows * (cols / 256) * 210));
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t q0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; q0 < total;
+       q0 += stride * kItems) {
+    uint32_t word[kItems];
+    short dbits[kItems];
 #pragma unroll
-      for (int i = 3; i >= 0; i--) {
-        if (fabsf(e[i]) == amax) key = 2 * (k0 + i) + (e[i] < 0.0f ? 1 : 0);
-      }
+    for (int u = 0; u < kItems; u++) {
+      const int64_t q = q0 + u * stride;   // uniform over the wave's super-block
+      const int64_t base = (q >> 6) * 210;
+      const bool in = q < total;
+      word[u] = (uint32_t)dnx_raw_buffer_load_i32(
+          rsrc, in ? (int)((base & ~3ll) + 4 * lane) : kFar, 0, 0);
+      // d on its own: the dword holding it can reach past the last block,
+      // and a dword past the buffer's end reads as zero.
+      dbits[u] = dnx_raw_buffer_load_i16(rsrc, in ? (int)(base + 208) : kFar, 0, 0);
     }
-    key = group8_min(key);
-    const float max = key == 64 ? 0.0f : (key & 1) ? -amax : amax;
-    const float d = max / -8.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    // This lane's 4 values as (int8_t) bytes; lanes 0-3 pair with lanes 4-7.
-    const int own = (q4_value(v.x, id) & 0xff) | ((q4_value(v.y, id) & 0xff) << 8) |
-                    ((q4_value(v.z, id) & 0xff) << 16) | ((q4_value(v.w, id) & 0xff) << 24);
-    const int high = __shfl_xor(own, 4);
-    if (k0 < 16) {
-      uint32_t out = 0;
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int lo = (int8_t)(own >> (8 * i));
-        const int hi = (int8_t)(high >> (8 * i));
-        out |= (uint32_t)((lo | (hi << 4)) & 0xff) << (8 * i);
+    for (int u = 0; u < kItems; u++) {
+      const int64_t q = q0 + u * stride;
+      if (q >= total) break;
+      const int delta = (int)(((q >> 6) * 210) & 3);   // 0 or 2
+      const int v = 4 * lane, h = v >> 7, qu = (v >> 5) & 3, l = v & 31;
+      auto bytes4 = [&](int rel) {
+        const int r = rel + delta;
+        const uint32_t w0 = (uint32_t)__shfl((int)word[u], r >> 2);
+        const uint32_t w1 = (uint32_t)__shfl((int)word[u], (r >> 2) + 1);
+        return __builtin_amdgcn_alignbyte(w1, w0, (uint32_t)(r & 3));
+      };
+      auto byte_at = [&](int rel) {
+        const int r = rel + delta;
+        return ((uint32_t)__shfl((int)word[u], r >> 2) >> (8 * (r & 3))) & 0xffu;
+      };
+      const uint32_t ql = bytes4(64 * h + l + 32 * (qu & 1));
+      const uint32_t qh = bytes4(128 + 32 * h + l);
+      const int8_t sc = (int8_t)byte_at(192 + 8 * h + (l >> 4) + 2 * qu);
+      const float ds = half_bits_to_float((uint16_t)dbits[u]) * (float)sc;
+      const int lo_shift = (qu >> 1) * 4, hi_shift = 2 * qu;
+      float e[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int qv = (int)((((ql >> (8 * j)) >> lo_shift) & 15) |
+                             ((((qh >> (8 * j)) >> hi_shift) & 3) << 4)) - 32;
+        e[j] = ds * (float)qv;
       }
-      *(uint32_t*)(qs + row * (cols / 2) + (c - k0) / 2 + k0) = out;
-    }
-    if (k0 == 0) {
-      scales[row * (cols / 32) + c / 32] = __builtin_bit_cast(uint16_t, (_Float16)d);
+      q8_quad(make_float4(e[0], e[1], e[2], e[3]), q, qs, scales);
     }
   }
 }
@@ -221,10 +356,49 @@ __global__ void __launch_bounds__(kThreads) gelu_kernel(float* __restrict__ x, i
   }
 }
 
+// Grid of the quantizers: kItems quads per thread when there is enough work,
+// but at least one workgroup per 256 quads up to 2048 workgroups (8 per CU),
+// so small inputs still spread over the chip.
+int quantizer_grid(int64_t quads) {
+  int64_t g = (quads + kThreads * kItems - 1) / (kThreads * kItems);
+  const int64_t spread = (quads + kThreads - 1) / kThreads;
+  const int64_t lo = spread < 2048 ? spread : 2048;
+  if (g < lo) g = lo;
+  if (g < 1) g = 1;
+  return (int)(g > 65536 ? 65536 : g);
+}
+
 int grid_for(int64_t items, int per_block, int cap) {
   int64_t g = (items + per_block - 1) / per_block;
   if (g < 1) g = 1;
   return (int)(g > cap ? cap : g);
+}
+
+// Launches a quantizer: the batched buffer-load kernel when the input is
+// 4-byte aligned, cols a multiple of 4 and the input below 2 GB, else the
+// generic one. Q8: cols_pad >= cols, a multiple of 32; Q4: cols_pad == cols.
+template <bool kQ4, bool kBf16>
+int launch_quantizer(const void* src, void* qs, void* scales, int64_t rows, int64_t cols,
+                     int64_t cols_pad, hipStream_t stream) {
+  const int64_t quads = rows * (cols_pad / 4);
+  const int64_t src_bytes = rows * cols * (kBf16 ? 2 : 4);
+  const bool fast = ((uintptr_t)src & 3) == 0 && cols % 4 == 0 && src_bytes < kFar &&
+                    quads < kFar && cols_pad < kFar;
+  const int grid = quantizer_grid(quads);
+  if (fast && cols == cols_pad) {
+    hipLaunchKernelGGL((quantize_kernel<kQ4, kBf16, false>), dim3(grid), dim3(kThreads), 0,
+                       stream, src, qs, scales, rows, (int)cols, (int)cols_pad,
+                       (uint32_t)src_bytes);
+  } else if (fast) {
+    hipLaunchKernelGGL((quantize_kernel<kQ4, kBf16, true>), dim3(grid), dim3(kThreads), 0,
+                       stream, src, qs, scales, rows, (int)cols, (int)cols_pad,
+                       (uint32_t)src_bytes);
+  } else {
+    hipLaunchKernelGGL((quantize_generic_kernel<kQ4, kBf16>),
+                       dim3(grid_for(quads, kThreads, 65536)), dim3(kThreads), 0, stream, src,
+                       qs, scales, rows, cols, cols_pad);
+  }
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 
 }  // namespace
@@ -235,45 +409,43 @@ extern "C" {
 
 int dnx_quantize_q8(const float* x, int8_t* qs, float* scales, int64_t rows, int64_t cols,
                     int64_t cols_pad, hipStream_t stream) {
-  if (rows < 0 || cols <= 0 || cols_pad < cols || cols_pad % kBlock != 0) return DNX_EINVAL;
+  if (rows < 0 || cols <= 0 || cols_pad < cols || cols_pad % kBlock != 0 || ((uintptr_t)qs & 3))
+    return DNX_EINVAL;
   if (rows == 0) return DNX_OK;
-  const int vec = (((uintptr_t)x & 15) == 0) && (cols % 4 == 0);
-  const int grid = grid_for(rows * (cols_pad / 4), kThreads, 65536);
-  hipLaunchKernelGGL((quantize_q8_kernel<false>), dim3(grid), dim3(kThreads), 0, stream,
-                     (const void*)x, qs, scales, rows, cols, cols_pad, vec);
-  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+  return launch_quantizer<false, false>(x, qs, scales, rows, cols, cols_pad, stream);
 }
 
 int dnx_quantize_q8_bf16(const uint16_t* w, int8_t* qs, float* scales, int64_t rows,
                          int64_t cols, int64_t cols_pad, hipStream_t stream) {
-  if (rows < 0 || cols <= 0 || cols_pad < cols || cols_pad % kBlock != 0) return DNX_EINVAL;
+  if (rows < 0 || cols <= 0 || cols_pad < cols || cols_pad % kBlock != 0 || ((uintptr_t)qs & 3))
+    return DNX_EINVAL;
   if (rows == 0) return DNX_OK;
-  const int vec = (((uintptr_t)w & 7) == 0) && (cols % 4 == 0);
-  const int grid = grid_for(rows * (cols_pad / 4), kThreads, 65536);
-  hipLaunchKernelGGL((quantize_q8_kernel<true>), dim3(grid), dim3(kThreads), 0, stream,
-                     (const void*)w, qs, scales, rows, cols, cols_pad, vec);
-  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+  return launch_quantizer<false, true>(w, qs, scales, rows, cols, cols_pad, stream);
 }
 
 int dnx_quantize_q4(const float* w, uint8_t* qs, uint16_t* scales, int64_t rows, int64_t cols,
                     hipStream_t stream) {
   if (rows < 0 || cols <= 0 || cols % kBlock != 0 || ((uintptr_t)qs & 3)) return DNX_EINVAL;
   if (rows == 0) return DNX_OK;
-  const int vec = ((uintptr_t)w & 15) == 0;
-  const int grid = grid_for(rows * (cols / 4), kThreads, 65536);
-  hipLaunchKernelGGL((quantize_q4_kernel<false>), dim3(grid), dim3(kThreads), 0, stream,
-                     (const void*)w, qs, scales, rows, cols, vec);
-  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+  return launch_quantizer<true, false>(w, qs, scales, rows, cols, cols, stream);
 }
 
 int dnx_quantize_q4_bf16(const uint16_t* w, uint8_t* qs, uint16_t* scales, int64_t rows,
                          int64_t cols, hipStream_t stream) {
   if (rows < 0 || cols <= 0 || cols % kBlock != 0 || ((uintptr_t)qs & 3)) return DNX_EINVAL;
   if (rows == 0) return DNX_OK;
-  const int vec = ((uintptr_t)w & 7) == 0;
-  const int grid = grid_for(rows * (cols / 4), kThreads, 65536);
-  hipLaunchKernelGGL((quantize_q4_kernel<true>), dim3(grid), dim3(kThreads), 0, stream,
-                     (const void*)w, qs, scales, rows, cols, vec);
+  return launch_quantizer<true, true>(w, qs, scales, rows, cols, cols, stream);
+}
+
+int dnx_q6k_to_q8(const void* blocks, int8_t* qs, float* scales, int64_t rows, int64_t cols,
+                  hipStream_t stream) {
+  if (rows < 0 || cols <= 0 || cols % 256 != 0 || ((uintptr_t)qs & 3)) return DNX_EINVAL;
+  // 32-bit buffer offsets into the blocks.
+  if (rows * (cols / 256) * 210 >= (1ll << 31)) return DNX_EINVAL;
+  if (rows == 0) return DNX_OK;
+  const int grid = quantizer_grid(rows * (cols / 4));
+  hipLaunchKernelGGL(q6k_to_q8_kernel, dim3(grid), dim3(kThreads), 0, stream,
+                     (const uint8_t*)blocks, qs, scales, rows, cols);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 

@@ -59,7 +59,7 @@ struct Buffer {
 
 enum Op {
   kOpMatmulQ8, kOpMatmulQ4, kOpSwiglu, kOpQuantize, kOpQuantizeBf16, kOpQuantizeQ4,
-  kOpQuantizeQ4Bf16, kOpArgmax, kOpGelu
+  kOpQuantizeQ4Bf16, kOpQ6kToQ8, kOpArgmax, kOpGelu
 };
 
 struct Cmd {
@@ -403,6 +403,17 @@ bool run(const Cmd& c) {
       wrote_region(sc, scOff, rows * (cols / 32) * 2);
       return rc == DNX_OK;
     }
+    case kOpQ6kToQ8: {
+      const int64_t src = c.a[0], srcOff = c.a[1], qs = c.a[2], qsOff = c.a[3];
+      const int64_t sc = c.a[4], scOff = c.a[5], rows = c.a[6], cols = c.a[7];
+      read_region(src, srcOff, rows * (cols / 256) * 210);
+      const int rc = dnx_q6k_to_q8(dev_at(src, srcOff), (int8_t*)dev_at(qs, qsOff),
+                                   (float*)dev_at(sc, scOff), rows, cols, gStream);
+      after_dispatch(kKindQuantizeWeights);
+      wrote_region(qs, qsOff, rows * cols);
+      wrote_region(sc, scOff, rows * (cols / 32) * 4);
+      return rc == DNX_OK;
+    }
     case kOpArgmax: {
       const int64_t x = c.a[0], xOff = c.a[1], n = c.a[2], out = c.a[3], outOff = c.a[4];
       read_region(x, xOff, n * 4);
@@ -672,6 +683,21 @@ void lab_gpu_enc_quantize_q4_bf16(int64_t src, int64_t srcOffset, int64_t qs, in
                                   int64_t cols) {
   enc_quantize_q4(kOpQuantizeQ4Bf16, src, srcOffset, qs, qsOffset, scales, scalesOffset, rows,
                   cols);
+}
+
+void lab_gpu_enc_q6k_to_q8(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                           int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols) {
+  const bool ok = rows >= 0 && cols > 0 && cols % 256 == 0 &&
+                  in_bounds(src, srcOffset, rows * (cols / 256) * 210) &&
+                  in_bounds(qs, qsOffset, rows * cols) &&
+                  in_bounds(scales, scalesOffset, rows * (cols / 32) * 4) &&
+                  qsOffset % 4 == 0 && scalesOffset % 4 == 0;
+  if (!ok) {
+    LOG("enc_q6k_to_q8: invalid arguments\n");
+    gFailed = true;
+    return;
+  }
+  record(kOpQ6kToQ8, {src, srcOffset, qs, qsOffset, scales, scalesOffset, rows, cols});
 }
 
 void lab_gpu_enc_argmax(int64_t x, int64_t xOffset, int64_t n, int64_t out, int64_t outOffset) {

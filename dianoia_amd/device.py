@@ -52,6 +52,13 @@ def quantize_q4(w: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, rows: i
                                        _stream(stream)), "dnx_quantize_q4")
 
 
+def q6k_to_q8(blocks: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, rows: int, cols: int,
+              stream=None) -> None:
+    """Q6_K super-blocks -> the engine's Q8 (dequantizeQ6K + lab_quantize_q8, fused)."""
+    _check(_lib.load().dnx_q6k_to_q8(_ptr(blocks), _ptr(qs), _ptr(scales), rows, cols,
+                                     _stream(stream)), "dnx_q6k_to_q8")
+
+
 def quantize_q4_bf16(w: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, rows: int,
                      cols: int, stream=None) -> None:
     """BF16 bits widened (p << 16), then lab_quantize_q4, in one kernel."""

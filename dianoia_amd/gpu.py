@@ -143,6 +143,37 @@ class GpuLinear:
         w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
         self._upload_quantized(name, w, 4, rows, cols, rows_pad, fmt)
 
+    def upload_q6k(self, name: str, blocks: np.ndarray, rows: int, cols: int) -> None:
+        """Converts Q6_K super-blocks (GGUF ``token_embd.weight``) to the engine's
+        Q8 on the GPU: ``importGguf``'s tied embedding / LM head
+        (``gguf.dart:402-414``: ``dequantizeQ6K`` then
+        ``NativeQ8Matrix.quantizeRows``), bit-exact."""
+        self._check_open()
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+        if rows <= 0 or cols <= 0 or cols % 256 != 0:
+            raise ArgumentError(f"Q6_K needs cols to be a multiple of 256, got {cols}")
+        nsrc = rows * (cols // 256) * 210
+        if blocks.size < nsrc:
+            raise ArgumentError(f"{blocks.size} bytes hold fewer than {rows} x {cols} Q6_K values")
+        src = self._lib.lab_gpu_buffer(nsrc)
+        if src < 0:
+            raise StateError("GPU buffer for the Q6_K blocks failed")
+        try:
+            self._bytes_view(src, nsrc)[:] = blocks[:nsrc]
+            scales_at = (rows * cols + 63) // 64 * 64
+            nbytes = scales_at + rows * (cols // 32) * 4
+            dst = self._lib.lab_gpu_buffer(nbytes)
+            if dst < 0:
+                raise StateError(f"GPU buffer of {nbytes} bytes failed")
+            self._owned.append(dst)
+            self._lib.lab_gpu_begin()
+            self._lib.lab_gpu_enc_q6k_to_q8(src, 0, dst, 0, dst, scales_at, rows, cols)
+            if self._lib.lab_gpu_commit(1) != 1:
+                raise StateError("GPU command buffer failed")
+        finally:
+            self._lib.lab_gpu_release(src)
+        self._replace(name, _Matrix(False, dst, 0, scales_at, rows, cols, cols))
+
     def _upload_quantized(self, name: str, src_values: np.ndarray, esize: int, rows: int,
                           cols: int, rows_pad: int | None, fmt: str) -> None:
         self._check_open()

@@ -53,6 +53,14 @@ int dnx_quantize_q4(const float* w, uint8_t* qs, uint16_t* scales, int64_t rows,
 int dnx_quantize_q4_bf16(const uint16_t* w, uint8_t* qs, uint16_t* scales, int64_t rows,
                          int64_t cols, dnx_stream_t stream);
 
+// The Q6_K -> Q8 embedding / LM-head adapter (lib/src/gguf.dart:402-414):
+// dequantizeQ6K (:220-254) then lab_quantize_q8, fused and bit-exact with
+// that pair. `blocks` holds rows x cols/256 Q6_K super-blocks of 210 bytes,
+// row after row (cols a multiple of 256); out: int8 [rows][cols] + fp32
+// scales [rows][cols/32], the engine's Q8 layout.
+int dnx_q6k_to_q8(const void* blocks, int8_t* qs, float* scales, int64_t rows, int64_t cols,
+                  dnx_stream_t stream);
+
 // Decode GEMV, n <= 4 tokens, fp32 x quantized in the kernel's prologue:
 // lab_gemm_q8 / lab_gemm_q4 mode 1 (lab_native.c:553-579, :1059-1080) with
 // the CPU's exact float order, so y is bit-identical to theirs.

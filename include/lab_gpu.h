@@ -128,6 +128,16 @@ void lab_gpu_enc_quantize_q4_bf16(int64_t src, int64_t srcOffset, int64_t qs, in
                                   int64_t scales, int64_t scalesOffset, int64_t rows,
                                   int64_t cols);
 
+// The Q6_K -> Q8 embedding / LM-head adapter on the GPU (importGguf's tied
+// embedding, lib/src/gguf.dart:402-414, which dequantizes with
+// dequantizeQ6K :220-254 and quantizes with NativeQ8Matrix.quantizeRows,
+// native.dart:645-672, on the CPU): rows x cols/256 super-blocks of 210
+// bytes at src + srcOffset become int8 [rows][cols] at qs + qsOffset and
+// fp32 scales [rows][cols/32] at scales + scalesOffset, bit-exact. cols
+// must be a multiple of 256; otherwise the command buffer fails.
+void lab_gpu_enc_q6k_to_q8(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                           int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols);
+
 // Greedy token on the GPU: argmaxToken (sampler.dart:137-152, no
 // suppression) over n floats at x + xOffset, the index written as one int64
 // at out + outOffset. Replaces the logits copy + host argmax of

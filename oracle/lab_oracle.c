@@ -22,6 +22,7 @@
 
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define Q_BLOCK 32
@@ -204,6 +205,59 @@ void orc_quantize_q4(const float* w, uint8_t* qs, uint16_t* scales, int64_t rows
       }
     }
   }
+}
+
+// ------------------------------------------------------------ Q6_K
+
+// dequantizeQ6K (lib/src/gguf.dart:220-254), ggml's dequantize_row_q6_K:
+// super-blocks of 256 values in 210 bytes, ql[128] (4 low bits), qh[64]
+// (2 high bits each), sc[16] (int8, one per 16 values), then fp16 d. Per
+// half of 128 values and l < 32: q1..q4 = values l, l+32, l+64, l+96 from
+// the low nibble of ql[l], of ql[l+32], the high nibble of ql[l], of
+// ql[l+32], with qh[l] bits 0-1, 2-3, 4-5, 6-7 above; scales sc[l/16 +
+// 0, 2, 4, 6]. Each value is d * sc * (q - 32) in double (Dart's
+// halfToDouble, native.dart:871-880, is exact), stored to float.
+void orc_dequantize_q6k(const uint8_t* data, float* out, int64_t blocks) {
+  for (int64_t b = 0; b < blocks; b++) {
+    const uint8_t* base = data + b * 210;
+    const double d = (double)orc_half_to_float((uint16_t)(base[208] | base[209] << 8));
+    float* y = out + b * 256;
+    const uint8_t* ql = base;
+    const uint8_t* qh = base + 128;
+    const int8_t* sc = (const int8_t*)(base + 192);
+    for (int half = 0; half < 2; half++) {
+      for (int l = 0; l < 32; l++) {
+        const int i = l / 16;
+        const int h = qh[l];
+        const int q1 = ((ql[l] & 15) | ((h & 3) << 4)) - 32;
+        const int q2 = ((ql[l + 32] & 15) | (((h >> 2) & 3) << 4)) - 32;
+        const int q3 = ((ql[l] >> 4) | (((h >> 4) & 3) << 4)) - 32;
+        const int q4 = ((ql[l + 32] >> 4) | (((h >> 6) & 3) << 4)) - 32;
+        y[l] = (float)(d * sc[i] * q1);
+        y[l + 32] = (float)(d * sc[i + 2] * q2);
+        y[l + 64] = (float)(d * sc[i + 4] * q3);
+        y[l + 96] = (float)(d * sc[i + 6] * q4);
+      }
+      y += 128;
+      ql += 64;
+      qh += 32;
+      sc += 8;
+    }
+  }
+}
+
+// The Q6_K -> Q8 embedding / LM-head adapter (gguf.dart:402-414): rows x
+// cols (cols a multiple of 256) dequantized row by row, then
+// lab_quantize_q8 (NativeQ8Matrix.quantizeRows, native.dart:645-672, which
+// quantizes chunks of whole rows: the result does not depend on the chunk).
+void orc_q6k_to_q8(const uint8_t* data, int8_t* qs, float* scales, int64_t rows, int64_t cols) {
+  float* row = (float*)malloc((size_t)(cols > 0 ? cols : 1) * sizeof(float));
+  const int64_t per_row = cols / 256;
+  for (int64_t r = 0; r < rows; r++) {
+    orc_dequantize_q6k(data + r * per_row * 210, row, per_row);
+    orc_quantize_q8(row, qs + r * cols, scales + r * (cols / Q_BLOCK), 1, cols);
+  }
+  free(row);
 }
 
 // ------------------------------------------------------------ products

@@ -115,6 +115,10 @@ class Oracle(_Kernels):
         for name in ("orc_block_dots_q8", "orc_block_dots_q4"):
             getattr(L, name).argtypes = [_p, _p, _p, _i64, _i64, _i64]
             getattr(L, name).restype = None
+        L.orc_dequantize_q6k.argtypes = [_p, _p, _i64]
+        L.orc_dequantize_q6k.restype = None
+        L.orc_q6k_to_q8.argtypes = [_p, _p, _p, _i64, _i64]
+        L.orc_q6k_to_q8.restype = None
         L.orc_argmax.argtypes = [_p, _i64]
         L.orc_argmax.restype = _i64
         L.orc_silu_mul.argtypes = [_p, _p, _i64]
@@ -143,6 +147,23 @@ class Oracle(_Kernels):
         qs = np.zeros((rows, cols_pad), np.int8)
         scales = np.zeros((rows, cols_pad // 32), np.float32)
         self.lib.orc_quantize_q8_bf16(_ptr(w), _ptr(qs), _ptr(scales), rows, cols, cols_pad)
+        return qs, scales
+
+    def dequantize_q6k(self, blocks: np.ndarray) -> np.ndarray:
+        """Q6_K super-blocks (210 B each) -> float32 values (256 each)."""
+        blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+        count = blocks.size // 210
+        out = np.zeros(count * 256, np.float32)
+        self.lib.orc_dequantize_q6k(_ptr(blocks), _ptr(out), count)
+        return out
+
+    def q6k_to_q8(self, blocks: np.ndarray, rows: int, cols: int):
+        """The Q6_K -> Q8 adapter: dequantize, then lab_quantize_q8."""
+        blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+        assert cols % 256 == 0 and blocks.size == rows * cols // 256 * 210
+        qs = np.zeros((rows, cols), np.int8)
+        scales = np.zeros((rows, cols // 32), np.float32)
+        self.lib.orc_q6k_to_q8(_ptr(blocks), _ptr(qs), _ptr(scales), rows, cols)
         return qs, scales
 
     def gemm_q8_prequant(self, qs, scales, xq, xsc, threads=8):

@@ -155,6 +155,64 @@ def test_q4_quantizer_rejects_bad_shapes(gpu_ready):
         D.quantize_q4(x, qs[1:], sc, 1, 32)  # qs not 4-byte aligned
 
 
+# ---- the Q6_K -> Q8 embedding / LM-head adapter (gguf.dart:402-414)
+
+def gpu_q6k_to_q8(blocks, rows, cols):
+    qs = torch.zeros((rows, cols), dtype=torch.int8, device="cuda")
+    sc = torch.zeros((rows, cols // 32), dtype=torch.float32, device="cuda")
+    D.q6k_to_q8(dev(blocks), qs, sc, rows, cols)
+    return host(qs), host(sc)
+
+
+@pytest.mark.parametrize("rows,cols,raw", [(1, 256, False), (37, 2048, False), (4096, 2048, False),
+                                           (64, 1024, True), (3, 4096, True)])
+def test_q6k_to_q8_matches_oracle(gpu_ready, orc, rows, cols, raw):
+    from q6k_util import pack_q6k, random_blocks
+    rng = np.random.default_rng(rows + cols + raw)
+    nb = rows * cols // 256
+    if raw:  # every byte pattern, fp16 d of any kind included
+        blocks = rng.integers(0, 256, size=(nb, 210), dtype=np.uint8)
+    else:
+        blocks = pack_q6k(*random_blocks(rng, nb))
+    qs, sc = gpu_q6k_to_q8(blocks, rows, cols)
+    q2, s2 = orc.q6k_to_q8(blocks, rows, cols)
+    assert np.array_equal(qs, q2)
+    assert np.array_equal(bits(sc), bits(s2))
+
+
+def test_q6k_adapter_through_the_abi(gpu_ready, orc):
+    """GpuLinear.upload_q6k -> lab_gpu_enc_q6k_to_q8, then the LM head with the
+    fused greedy argmax on the converted weights, bit-exact with the CPU."""
+    from dianoia_amd.gpu import GpuLinear
+    from q6k_util import pack_q6k, random_blocks
+    rows, cols = 1000, 2048
+    rng = np.random.default_rng(63)
+    blocks = pack_q6k(*random_blocks(rng, rows * cols // 256, specials=False))
+    gpu = GpuLinear.start()
+    try:
+        gpu.upload_q6k("head", blocks, rows, cols)
+        qs, sc = gpu.quantized("head")
+        q2, s2 = orc.q6k_to_q8(blocks, rows, cols)
+        assert np.array_equal(qs, q2)
+        assert np.array_equal(bits(sc), bits(s2))
+        xs = rng.standard_normal(cols, dtype=np.float32)
+        logits = np.zeros(rows, np.float32)
+        token = gpu.apply_argmax("head", xs, logits)
+        cpu = orc.gemm_q8(q2, s2, xs, 1, threads=4, mode=1).reshape(-1)
+        assert np.array_equal(bits(logits), bits(cpu))
+        assert token == orc.argmax(cpu)
+    finally:
+        gpu.dispose()
+
+
+def test_q6k_adapter_rejects_bad_shapes(gpu_ready):
+    blocks = torch.zeros(420, dtype=torch.uint8, device="cuda")
+    qs = torch.zeros(512, dtype=torch.int8, device="cuda")
+    sc = torch.zeros(16, device="cuda")
+    with pytest.raises(RuntimeError):
+        D.q6k_to_q8(blocks, qs, sc, 1, 480)  # not a multiple of 256
+
+
 def test_quantizer_rejects_bad_shapes(gpu_ready):
     x = torch.zeros(64, device="cuda")
     out = torch.zeros(64, dtype=torch.int8, device="cuda")

@@ -98,6 +98,33 @@ def test_bf16_quantizer_is_widen_then_quantize(orc):
     assert np.array_equal(qs, qs2) and np.array_equal(bits(sc), bits(sc2))
 
 
+def test_q6k_dequantizer_against_ggml_packing(orc):
+    """dequantizeQ6K (gguf.dart:220-254) on values packed by ggml's
+    quantize_row_q6_K layout equals the definition d * sc * (q - 32)."""
+    from q6k_util import expected_values, pack_q6k, random_blocks
+    rng = np.random.default_rng(61)
+    q, sc, d = random_blocks(rng, 64)
+    # every 6-bit value in every position of one block, extreme scales
+    q[8] = np.arange(256) % 64
+    sc[8] = [-128, 127, -1, 1, 0, 5, -7, 64, -64, 100, -100, 3, 2, -2, 126, -127]
+    got = orc.dequantize_q6k(pack_q6k(q, sc, d))
+    want = expected_values(q, sc, d)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(bits(got[~nan]), bits(want[~nan]))
+
+
+def test_q6k_adapter_is_dequantize_then_quantize(orc):
+    from q6k_util import pack_q6k, random_blocks
+    rows, cols = 5, 512
+    q, sc, d = random_blocks(np.random.default_rng(62), rows * cols // 256)
+    blocks = pack_q6k(q, sc, d)
+    qs, s = orc.q6k_to_q8(blocks, rows, cols)
+    q2, s2 = orc.quantize_q8(orc.dequantize_q6k(blocks).reshape(rows, cols))
+    assert np.array_equal(qs, q2)
+    assert np.array_equal(bits(s), bits(s2))
+
+
 def test_half_conversions_exhaustive(orc):
     h = np.arange(65536, dtype=np.uint16)
     want = h.view(np.float16).astype(np.float32)
