@@ -19,45 +19,14 @@ constexpr int kThreads = 256;  // 4 waves per workgroup
 
 // ------------------------------------------------------------ quantizer
 
-// Items per thread per pass of the quantizers. A pass issues all of its
+// Items per thread per pass of the Q6_K adapter. A pass issues all of its
 // loads before it uses any: one small load in flight per thread leaves a
-// quantizer latency-bound at a quarter of HBM. The loads are raw buffer
+// converter latency-bound at a quarter of HBM. The loads are raw buffer
 // loads, so an item past the end or a padding column reads zeros with no
 // branch and no memory access (a branch around a load makes the compiler
 // wait for it right there).
 constexpr int kItems = 8;
 constexpr int kFar = 0x7fffff00;  // an offset past every buffer these kernels read
-
-// One quad (4 values) as loaded: 16 bytes of fp32 or 8 bytes of bf16 bits.
-template <bool kBf16>
-struct RawQuad {
-  uint32_t w[kBf16 ? 2 : 4];
-};
-template <bool kBf16>
-DNX_DEV RawQuad<kBf16> load_raw_quad(i32x4 rsrc, int off) {
-  RawQuad<kBf16> r;
-  if (kBf16) {
-    const i32x2 v = dnx_raw_buffer_load_v2i32(rsrc, off, 0, 0);
-    r.w[0] = (uint32_t)v.x;
-    r.w[1] = (uint32_t)v.y;
-  } else {
-    const uint4 v = buffer_load16(rsrc, off);
-    r.w[0] = v.x;
-    r.w[1] = v.y;
-    r.w[2] = v.z;
-    r.w[3] = v.w;
-  }
-  return r;
-}
-template <bool kBf16>
-DNX_DEV float4 widen(const RawQuad<kBf16>& r) {
-  if (kBf16) {  // bf16 bits p -> float p << 16 (safetensors.dart:207-212)
-    return make_float4(__uint_as_float(r.w[0] << 16), __uint_as_float(r.w[0] & 0xffff0000u),
-                       __uint_as_float(r.w[1] << 16), __uint_as_float(r.w[1] & 0xffff0000u));
-  }
-  return make_float4(__uint_as_float(r.w[0]), __uint_as_float(r.w[1]), __uint_as_float(r.w[2]),
-                     __uint_as_float(r.w[3]));
-}
 
 // Four consecutive values of row `row` from column c with plain loads (the
 // generic path: unaligned inputs, odd widths, inputs of 2 GB or more);
@@ -90,6 +59,15 @@ DNX_DEV void q8_quad(float4 v, int64_t q, int8_t* qs, float* scales) {
   const float inv = q8_inv(scale);
   *(int*)(qs + 4 * q) = quant4(v, inv);
   if ((q & 7) == 0) scales[q >> 3] = scale;
+}
+
+// float -> fp16 bits, round to nearest even (the reference's float_to_half,
+// lab_native.c:923-925). The value goes through an empty asm first: without
+// it the compiler folds d = max * -0.125 and this conversion into one
+// v_fma_mix with a +0 addend, which turns d = -0 (an all-zero block) into +0.
+DNX_DEV uint16_t half_rne(float f) {
+  asm volatile("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
 // lab_quantize_q4 (lab_native.c:928-955, llama.cpp's quantize_row_q4_0_ref)
@@ -132,56 +110,117 @@ DNX_DEV void q4_quad(float4 v, int64_t q, uint8_t* qs, uint16_t* scales) {
     }
     *(uint32_t*)(qs + 16 * (q >> 3) + k0) = out;
   }
-  if (k0 == 0) scales[q >> 3] = __builtin_bit_cast(uint16_t, (_Float16)d);
+  if (k0 == 0) scales[q >> 3] = half_rne(d);
 }
 
 // Q8 (kQ4 false) or Q4 quantizer over rows x cols values (fp32 or bf16),
-// cols a multiple of 4 and the input below 2 GB: quad q = (row, c) of the
-// output's rows x cols_pad (cols_pad a multiple of 32 >= cols; Q4 has no
-// padding); columns >= cols are zero padding (Q8, R10's extension). One
-// thread per quad, 8 threads per 32-block; a pass takes up to kItems quads
-// per thread, one grid apart (whole 8-lane groups stay together: both the
-// row length and the stride are multiples of 8 quads).
+// with one lane per 32-block: the block's 128 (fp32) or 64 (bf16) bytes
+// arrive in 16-byte buffer loads issued together, then the lane runs the
+// reference's scalar loop itself (block max in column order, one division
+// per block, 32 values) and stores 32 (Q8) or 16 (Q4) bytes and the scale.
+// Lanes of a wave take consecutive blocks, so stores are contiguous. The
+// output has rows x cols_pad values (cols_pad a multiple of 32 >= cols; Q4
+// has no padding); columns >= cols load as zeros (the padding, R10's
+// extension). Requires cols a multiple of 8 (no 16-byte load straddles a
+// row's end) and an input below 2 GB (32-bit buffer offsets).
 template <bool kQ4, bool kBf16, bool kPad>
 __global__ void __launch_bounds__(kThreads)
 quantize_kernel(const void* __restrict__ src, void* __restrict__ qs, void* __restrict__ scales,
                 int64_t rows, int cols, int cols_pad, uint32_t src_bytes) {
   constexpr int kEsize = kBf16 ? 2 : 4;
-  const int qpr = cols_pad / 4;
-  const int64_t total = rows * qpr;
+  constexpr int kLoads = 32 * kEsize / 16;   // 16-byte loads per block
+  constexpr int kPer = 16 / kEsize;          // values per load
+  const int bpr = cols_pad / 32;
+  const int64_t total = rows * bpr;
   const i32x4 rsrc = buffer_rsrc(src, src_bytes);
-  const int64_t stride = (int64_t)gridDim.x * kThreads;
-  for (int64_t q0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; q0 < total;
-       q0 += stride * kItems) {
-    RawQuad<kBf16> raw[kItems];
-#pragma unroll
-    for (int u = 0; u < kItems; u++) {
-      const int64_t q = q0 + u * stride;
-      int off;
-      if (kPad) {  // total < 2^31: 32-bit division
-        const uint32_t row = (uint32_t)q / (uint32_t)qpr;
-        const int c = (int)((uint32_t)q - row * (uint32_t)qpr) * 4;
-        off = (q < total && c < cols) ? (int)(((int64_t)row * cols + c) * kEsize) : kFar;
-      } else {
-        off = q < total ? (int)(q * 4 * kEsize) : kFar;
-      }
-      raw[u] = load_raw_quad<kBf16>(rsrc, off);
+  for (int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x; b < total;
+       b += (int64_t)gridDim.x * kThreads) {
+    int64_t start;   // element offset of the block's first value in src
+    int c0;          // its column
+    if (kPad) {      // total < 2^31: 32-bit division
+      const uint32_t row = (uint32_t)b / (uint32_t)bpr;
+      c0 = (int)((uint32_t)b - row * (uint32_t)bpr) * 32;
+      start = (int64_t)row * cols + c0;
+    } else {
+      c0 = 0;
+      start = b * 32;
     }
+    uint4 raw[kLoads];
 #pragma unroll
-    for (int u = 0; u < kItems; u++) {
-      const int64_t q = q0 + u * stride;
-      if (q >= total) break;
-      if (kQ4) {
-        q4_quad(widen(raw[u]), q, (uint8_t*)qs, (uint16_t*)scales);
-      } else {
-        q8_quad(widen(raw[u]), q, (int8_t*)qs, (float*)scales);
+    for (int j = 0; j < kLoads; j++) {
+      const bool in = !kPad || c0 + j * kPer < cols;
+      raw[j] = buffer_load16(rsrc, in ? (int)((start + j * kPer) * kEsize) : kFar);
+    }
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < kLoads; j++) {
+      const uint32_t w[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        if (kBf16) {  // bf16 bits p -> float p << 16 (safetensors.dart:207-212)
+          v[j * 8 + 2 * i] = __uint_as_float(w[i] << 16);
+          v[j * 8 + 2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        } else {
+          v[j * 4 + i] = __uint_as_float(w[i]);
+        }
       }
+    }
+    if (kQ4) {
+      // lab_quantize_q4 (lab_native.c:933-953): the first value of largest
+      // magnitude, strict `>` from 0 (NaN never wins, ties keep the first).
+      float amax = 0.0f, max = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 32; k++) {
+        const float a = v[k] < 0.0f ? -v[k] : v[k];
+        if (a > amax) {
+          amax = a;
+          max = v[k];
+        }
+      }
+      const float d = max / -8.0f;
+      const float id = d != 0.0f ? 1.0f / d : 0.0f;
+      const uint16_t dh = half_rne(d);
+      uint32_t out[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int lo = q4_value(v[4 * i + k], id);
+          const int hi = q4_value(v[4 * i + k + 16], id);
+          word |= (uint32_t)((lo | (hi << 4)) & 0xff) << (8 * k);
+        }
+        out[i] = word;
+      }
+      *(uint4*)((uint8_t*)qs + 16 * b) = make_uint4(out[0], out[1], out[2], out[3]);
+      ((uint16_t*)scales)[b] = dh;
+    } else {
+      // lab_quantize_q8 (lab_native.c:411-427).
+      float amax = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 32; k++) {
+        const float a = fabsf(v[k]);
+        amax = a > amax ? a : amax;
+      }
+      const float scale = q8_scale(amax);
+      const float inv = q8_inv(scale);
+      uint32_t out[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        out[i] = (uint32_t)quant4(make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]),
+                                  inv);
+      }
+      uint4* dst = (uint4*)((int8_t*)qs + 32 * b);
+      dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
+      dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
+      ((float*)scales)[b] = scale;
     }
   }
 }
 
-// The generic path of the same quantizers: one quad per thread per step,
-// plain loads (any alignment, any width, any size).
+// The quad-per-lane path of the same quantizers: one quad per thread per
+// step, 8 threads per block, plain loads (any alignment, width or size; also
+// the faster one for small matrices).
 template <bool kQ4, bool kBf16>
 __global__ void __launch_bounds__(kThreads)
 quantize_generic_kernel(const void* __restrict__ src, void* __restrict__ qs,
@@ -356,7 +395,7 @@ __global__ void __launch_bounds__(kThreads) gelu_kernel(float* __restrict__ x, i
   }
 }
 
-// Grid of the quantizers: kItems quads per thread when there is enough work,
+// Grid of the Q6_K adapter: kItems quads per thread when there is enough work,
 // but at least one workgroup per 256 quads up to 2048 workgroups (8 per CU),
 // so small inputs still spread over the chip.
 int quantizer_grid(int64_t quads) {
@@ -374,17 +413,21 @@ int grid_for(int64_t items, int per_block, int cap) {
   return (int)(g > cap ? cap : g);
 }
 
-// Launches a quantizer: the batched buffer-load kernel when the input is
-// 4-byte aligned, cols a multiple of 4 and the input below 2 GB, else the
-// generic one. Q8: cols_pad >= cols, a multiple of 32; Q4: cols_pad == cols.
+// Launches a quantizer: the block-per-lane kernel when the input is 4-byte
+// aligned, the output 16-byte aligned, cols a multiple of 8, the input below
+// 2 GB and the matrix at least 64 K blocks, else the quad-per-lane one. Q8: cols_pad >= cols, a multiple of 32;
+// Q4: cols_pad == cols.
 template <bool kQ4, bool kBf16>
 int launch_quantizer(const void* src, void* qs, void* scales, int64_t rows, int64_t cols,
                      int64_t cols_pad, hipStream_t stream) {
-  const int64_t quads = rows * (cols_pad / 4);
+  const int64_t blocks = rows * (cols_pad / 32);
   const int64_t src_bytes = rows * cols * (kBf16 ? 2 : 4);
-  const bool fast = ((uintptr_t)src & 3) == 0 && cols % 4 == 0 && src_bytes < kFar &&
-                    quads < kFar && cols_pad < kFar;
-  const int grid = quantizer_grid(quads);
+  // Below 64 K blocks (fewer than one wave of lanes per SIMD) the quad-per-
+  // lane kernel spreads the work over 8x more lanes and finishes sooner
+  // (512 x 2048 fp32: 2.8 us against 3.4).
+  const bool fast = ((uintptr_t)src & 3) == 0 && ((uintptr_t)qs & 15) == 0 && cols % 8 == 0 &&
+                    src_bytes < kFar && cols_pad < kFar && blocks >= 65536;
+  const int grid = grid_for(blocks, kThreads, 65536);
   if (fast && cols == cols_pad) {
     hipLaunchKernelGGL((quantize_kernel<kQ4, kBf16, false>), dim3(grid), dim3(kThreads), 0,
                        stream, src, qs, scales, rows, (int)cols, (int)cols_pad,
@@ -395,7 +438,8 @@ int launch_quantizer(const void* src, void* qs, void* scales, int64_t rows, int6
                        (uint32_t)src_bytes);
   } else {
     hipLaunchKernelGGL((quantize_generic_kernel<kQ4, kBf16>),
-                       dim3(grid_for(quads, kThreads, 65536)), dim3(kThreads), 0, stream, src,
+                       dim3(grid_for(rows * (cols_pad / 4), kThreads, 65536)), dim3(kThreads), 0,
+                       stream, src,
                        qs, scales, rows, cols, cols_pad);
   }
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;

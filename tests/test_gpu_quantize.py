@@ -30,7 +30,10 @@ def test_quantize_matches_golden(gpu_ready, name):
     assert np.array_equal(bits(sc), bits(d["scales"]))
 
 
-@pytest.mark.parametrize("rows,cols,pad", [(1, 1024, 1024), (512, 2048, 2048), (1024, 1152, 1152),
+# Shapes of 64 K blocks or more take the block-per-lane kernel (2048 x 2048,
+# 1024 x 4304 padded), the others the quad-per-lane one.
+@pytest.mark.parametrize("rows,cols,pad", [(1, 1024, 1024), (512, 2048, 2048), (2048, 2048, 2048),
+                                           (1024, 1152, 1152),
                                            (1024, 4304, 4320), (3, 33, 64), (7, 4, 32)])
 def test_quantize_matches_oracle(gpu_ready, orc, rows, cols, pad):
     rng = np.random.default_rng(rows * 7 + cols)
@@ -143,6 +146,31 @@ def test_q4_quantizer_through_the_abi(gpu_ready, orc, bf16):
         assert np.array_equal(bits(ys), bits(cpu))
     finally:
         gpu.dispose()
+
+
+def test_quantizers_generic_path(gpu_ready, orc):
+    """Inputs the block-per-lane kernel does not take (a bf16 source at an odd
+    element, int8 output not 16-byte aligned) run the generic kernel, with the
+    same results."""
+    from dianoia_amd.synth import bf16_weights
+    rows, cols = 33, 256
+    w = bf16_weights(np.random.default_rng(71), rows, cols + 1)
+    src = dev(w.reshape(-1))[1:1 + rows * cols]          # 2-byte aligned
+    widened = (w.reshape(-1)[1:1 + rows * cols].astype(np.uint32) << 16).view(np.float32)
+    widened = widened.reshape(rows, cols)
+    qs = torch.zeros((rows, cols // 2), dtype=torch.uint8, device="cuda")
+    sc = torch.zeros((rows, cols // 32), dtype=torch.int16, device="cuda")
+    D.quantize_q4_bf16(src, qs, sc, rows, cols)
+    q2, s2 = orc.quantize_q4(widened)
+    assert np.array_equal(host(qs), q2)
+    assert np.array_equal(host(sc).view(np.uint16), s2)
+    x = np.random.default_rng(72).standard_normal((rows, cols), dtype=np.float32)
+    q8 = torch.zeros(rows * cols + 4, dtype=torch.int8, device="cuda")
+    s8 = torch.zeros((rows, cols // 32), dtype=torch.float32, device="cuda")
+    D.quantize_q8(dev(x), q8[4:], s8, rows, cols, cols)  # output 4-byte aligned only
+    q3, s3 = orc.quantize_q8(x)
+    assert np.array_equal(host(q8)[4:].reshape(rows, cols), q3)
+    assert np.array_equal(bits(host(s8)), bits(s3))
 
 
 def test_q4_quantizer_rejects_bad_shapes(gpu_ready):
