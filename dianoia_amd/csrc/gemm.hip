@@ -285,6 +285,206 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
     }
 }
 
+// ------------------------------------------------------------ skinny (n <= 16)
+
+// Few tokens (n <= 16) and K <= 2048: the weights are read once from HBM and
+// the work is too small to hide a memory round trip per stage, so every
+// load of the kernel is issued at its start and waited for once. A
+// workgroup owns 16 weight rows over the whole K:
+// * its 16 rows (Q4 nibbles or Q8 bytes), their scales and the x scales of
+//   all tokens arrive with coalesced 16-byte (scales: 4-byte) loads and go
+//   to LDS (rows padded by 16 bytes against bank conflicts; x scales
+//   transposed [block][token]);
+// * its 4 waves split K into 4 runs of at most 16 blocks (wave w: blocks
+//   wQ .. wQ + Q - 1, Q = ceil(B / 4)), and each wave loads the int8 tokens
+//   of its blocks straight into registers, also at the start.
+// A lane holds column c = lane % 16 (weight row r0 + c) and k-group
+// g = lane / 16 of a block: v_mfma_i32_16x16x32_i8 takes A = 16 tokens x 32
+// (8 int8 of token 16t + c at k = 8g.. per lane), B = 32 x 16 weight rows
+// (8 int8 of row r0 + c at k = 8g.., from LDS) and gives the block's exact
+// int32 dots, the lane holding tokens 16t + 4g + v (v < 4) of column c.
+// Epilogue per output and block: acc = fma(d, sw * sx, acc) (s rounded
+// first, as lab_native.c:509). The 4 waves' sums are added through LDS in
+// wave order (deterministic), with no split-K pass. Rows past the matrix
+// and tokens past n load zeros (bounded buffer loads) and are not stored;
+// blocks past a wave's last load zeros and add exact zeros.
+constexpr int kSkinnyRows = 16;
+constexpr int kSkinnyBlocks = 16;       // blocks per wave: K <= 2048
+constexpr int kSkinnyFar = 0x7fffff00;  // a buffer offset past every operand
+
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+// LDS of the skinny kernel: padded weight rows, weight scales (fp32), x
+// scales [block][token], and waves 1..3's sums.
+size_t skinny_row_bytes(bool q4, int cols) { return (size_t)(q4 ? cols / 2 : cols) + 16; }
+size_t skinny_lds(bool q4, int cols, int mt) {
+  const int blocks = cols / kBlock;
+  return kSkinnyRows * skinny_row_bytes(q4, cols) + (size_t)kSkinnyRows * blocks * 4 +
+         (size_t)blocks * 16 * mt * 4 + (size_t)3 * mt * 4 * 64 * 4;
+}
+
+template <bool kQ4, int MT>
+__global__ void __launch_bounds__(kThreads) skinny_kernel(GemmParams p) {
+  extern __shared__ __align__(16) uint8_t slds[];
+  constexpr int MP = 16 * MT;
+  constexpr int NB = kSkinnyBlocks;
+  const int K = p.cols, B = K / kBlock, M = p.n, N = p.rows;
+  const int RB = kQ4 ? K / 2 : K;            // bytes of a weight row
+  const int RS = RB + 16;                    // its LDS stride
+  uint8_t* sw_rows = slds;                   // [16][RS]
+  float* sws = (float*)(slds + kSkinnyRows * RS);   // [16][B] weight scales
+  float* sxT = sws + kSkinnyRows * B;               // [B][MP] x scales
+  float* red = sxT + B * MP;                        // [3][MT][4][64]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int r0 = blockIdx.x * kSkinnyRows;
+
+  const i32x4 rq = buffer_rsrc(p.qs, (uint32_t)((size_t)N * RB));
+  const i32x4 rs = buffer_rsrc(p.scales, (uint32_t)((size_t)N * B * (kQ4 ? 2 : 4)));
+  const i32x4 rx = buffer_rsrc(p.xq, (uint32_t)((size_t)M * K));
+  const i32x4 rxs = buffer_rsrc(p.xsc, (uint32_t)((size_t)M * B * 4));
+
+  // 1. Every load, issued together. Weight rows: 16-byte pieces, RB / 16
+  // per row, at most 8 per thread (16 rows x 2048 bytes).
+  constexpr int WP = 8;
+  uint4 wraw[WP];
+#pragma unroll
+  for (int e = 0; e < WP; e++) {
+    const int i = e * kThreads + tid, per = RB / 16;
+    const int row = i / per, piece = i - row * per;
+    const bool in = i < kSkinnyRows * per && r0 + row < N;
+    wraw[e] = buffer_load16(rq, in ? (r0 + row) * RB + piece * 16 : kSkinnyFar);
+  }
+  // Weight scales: 16 x B (<= 1024) raw values, 4 per thread.
+  int sraw[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int i = e * kThreads + tid, row = i / B, b = i - (i / B) * B;
+    const bool in = i < kSkinnyRows * B && r0 + row < N;
+    const int off = ((r0 + row) * B + b) * (kQ4 ? 2 : 4);
+    sraw[e] = kQ4 ? (int)dnx_raw_buffer_load_i16(rs, in ? off : kSkinnyFar, 0, 0)
+                  : dnx_raw_buffer_load_i32(rs, in ? off : kSkinnyFar, 0, 0);
+  }
+  // x scales: MP x B (<= 4096) floats, token-major, 16 per thread.
+  float xraw[16];
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    const int i = e * kThreads + tid;
+    xraw[e] = __int_as_float(dnx_raw_buffer_load_i32(rxs, i < M * B ? i * 4 : kSkinnyFar, 0, 0));
+  }
+  // This wave's int8 tokens: block j (= wave * Q + j), token tile t. A
+  // lane's consecutive blocks are adjacent 32-byte pieces of its token's
+  // row, so the wave's loads reuse each cache line 4 times in a row.
+  const int Q = (B + 3) / 4;   // blocks per wave (<= 16)
+  v2i_t ra[NB][MT];
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const int b = j < Q ? wave * Q + j : B;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+      const int m = 16 * t + c;
+      ra[j][t] = dnx_raw_buffer_load_v2i32(
+          rx, b < B && m < M ? m * K + b * 32 + 8 * g : kSkinnyFar, 0, 0);
+    }
+  }
+
+  // 2. Weights, weight scales and x scales to LDS.
+#pragma unroll
+  for (int e = 0; e < WP; e++) {
+    const int i = e * kThreads + tid, per = RB / 16;
+    const int row = i / per, piece = i - row * per;
+    if (i < kSkinnyRows * per) *(uint4*)(sw_rows + row * RS + piece * 16) = wraw[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int i = e * kThreads + tid;
+    if (i < kSkinnyRows * B) {
+      sws[i] = kQ4 ? half_bits_to_float((uint16_t)sraw[e]) : __int_as_float(sraw[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    const int i = e * kThreads + tid;
+    if (i < MP * B) {
+      const int m = i / B, b = i - (i / B) * B;
+      sxT[b * MP + m] = xraw[e];
+    }
+  }
+  __syncthreads();
+
+  // 3. The wave's blocks.
+  float acc[MT][4];
+#pragma unroll
+  for (int t = 0; t < MT; t++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) acc[t][v] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const int b = min(j < Q ? wave * Q + j : B, B - 1);   // past the end: zeros from ra
+    uint2 w = *(const uint2*)(sw_rows + c * RS + b * (kQ4 ? 16 : 32) + (kQ4 ? (g & 1) * 8 : 8 * g));
+    if (kQ4) {  // bytes 8(g & 1).. : low nibbles (k < 16) or high (k >= 16)
+      uint32_t lo0, hi0, lo1, hi1;
+      unpack_q4(w.x, lo0, hi0);
+      unpack_q4(w.y, lo1, hi1);
+      w.x = (g >> 1) ? hi0 : lo0;
+      w.y = (g >> 1) ? hi1 : lo1;
+    }
+    const long bop = (long)(((uint64_t)w.y << 32) | w.x);
+    const float swf = sws[c * B + b];
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+      const long aop = (long)(((uint64_t)(uint32_t)ra[j][t].y << 32) | (uint32_t)ra[j][t].x);
+      const v4i_t z = {};
+      const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, z, 0, 0, 0);
+      const float4 sx = *(const float4*)(sxT + b * MP + 16 * t + 4 * g);
+      acc[t][0] = fmaf((float)d[0], swf * sx.x, acc[t][0]);
+      acc[t][1] = fmaf((float)d[1], swf * sx.y, acc[t][1]);
+      acc[t][2] = fmaf((float)d[2], swf * sx.z, acc[t][2]);
+      acc[t][3] = fmaf((float)d[3], swf * sx.w, acc[t][3]);
+    }
+  }
+
+  // 4. Waves 1..3 hand their sums to wave 0, which adds them in wave order.
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) red[(((wave - 1) * MT + t) * 4 + v) * 64 + lane] = acc[t][v];
+  }
+  __syncthreads();
+  const int row = r0 + c;
+  if (wave > 0 || row >= N) return;
+#pragma unroll
+  for (int t = 0; t < MT; t++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      float s = acc[t][v];
+#pragma unroll
+      for (int w = 0; w < 3; w++) s += red[((w * MT + t) * 4 + v) * 64 + lane];
+      const int m = 16 * t + 4 * g + v;
+      if (m < M) p.y[(size_t)m * N + row] = s;
+    }
+}
+
+// Whether the skinny kernel takes this shape: n <= 16, K <= 2048 (16
+// blocks per wave, 8 row pieces per thread) and the LDS within 64 KB. With
+// more tokens it lost to the split-K tile kernel on 6144 x 2048 Q4 (n = 32:
+// 13.7 against 11.8 us; n = 16: 9.7 against 10.2; n = 8: 8.5 against 9.4).
+bool skinny_fits(bool q4, int64_t cols, int64_t n) {
+  if (n > 16 || cols > 2048 || cols % 16 != 0) return false;
+  return skinny_lds(q4, (int)cols, 1) <= 64 * 1024;
+}
+
+template <bool kQ4, int MT>
+int launch_skinny(const GemmParams& p, hipStream_t stream) {
+  const size_t lds = skinny_lds(kQ4, p.cols, MT);
+  const unsigned grid = (unsigned)((p.rows + kSkinnyRows - 1) / kSkinnyRows);
+  hipLaunchKernelGGL((skinny_kernel<kQ4, MT>), dim3(grid), dim3(kThreads), lds, stream, p);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
 // y = the split partials summed in split order (deterministic).
 __global__ void __launch_bounds__(kThreads) splitk_reduce_kernel(const float* __restrict__ part,
                                                                  float* __restrict__ y,
@@ -359,9 +559,12 @@ int launch_gemm(const void* qs, const void* scales, const int8_t* xq, const floa
   if (rows * (kQ4 ? cols / 2 : cols) >= (1ll << 31) || n * cols >= (1ll << 31)) return DNX_EINVAL;
   if (((uintptr_t)qs & 15) || ((uintptr_t)xq & 15) || (cols % 16)) return DNX_EINVAL;
   GemmParams p{qs, scales, xq, xsc, y, (int)rows, (int)cols, (int)n, 0, nullptr};
+  // Up to 16 tokens and K <= 2048: the skinny kernel (every load at the
+  // start, K shared by a workgroup's waves, no split-K pass);
   // 32 tokens: one wave row of 32 x 32 tiles (4 waves across N); else
   // 64 x 64 tiles (2 x 2 waves), which keep ~3 workgroups per CU resident
   // at prefill sizes.
+  if (skinny_fits(kQ4, cols, n)) return launch_skinny<kQ4, 1>(p, stream);
   if (n <= 32) return launch_tile<kQ4, 32, 128, 1, 4>(p, stream);
   return launch_tile<kQ4, 64, 64, 2, 4>(p, stream);
 }

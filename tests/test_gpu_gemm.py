@@ -34,7 +34,8 @@ def gemm(fmt, qs, sc, xq, xsc, rows, cols, n, path="i8"):
 @pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 @pytest.mark.parametrize("rows,cols,n", [(130, 256, 70), (128, 128, 128), (33, 96, 5),
-                                         (200, 320, 300)])
+                                         (200, 320, 300), (70, 256, 37), (40, 1024, 64),
+                                         (17, 2048, 16)])
 def test_block_dots_are_exact(gpu_ready, orc, fmt, rows, cols, n, path):
     """With scale 1 on one block and 0 on the others, y is that block's
     int32 dot product as a float (exact below 2^24): the MFMA's integer
