@@ -334,6 +334,37 @@ def bench_c4(torch, D, synth, timer, steps, warmup):
             "pair_tops": 2 * ops / (means[1] + means[2] + means[3]) / 1e9}
 
 
+def bench_layers(torch, D, timer, steps):
+    """The decoder's other layer steps (lab_gpu_enc_* semantics): attention
+    decode over a 4096-position cache (32 query heads, 8 KV heads, hd 128;
+    HBM-bound on the cached keys and values) and RMSNorm over a 4096 x 2048
+    prefill block. Inputs generated on the GPU."""
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    heads, kv, hd, pos = 32, 8, 128, 4095
+    q = torch.randn(heads * hd, device="cuda", generator=gen)
+    keys = torch.randn((pos + 1, kv * hd), device="cuda", generator=gen)
+    values = torch.randn((pos + 1, kv * hd), device="cuda", generator=gen)
+    out = torch.empty(heads * hd, device="cuda")
+    x = torch.randn((4096, 2048), device="cuda", generator=gen)
+    w = torch.rand(2048, device="cuda", generator=gen)
+    y = torch.empty_like(x)
+
+    def attn(i):
+        D.attention(q, keys, values, None, out, pos, 1, heads, kv, hd, 0)
+
+    def norm(i):
+        D.rms_norm(x, w, y, 4096, 2048, 1e-5)
+
+    means = timer.kernel_means([attn, norm], max(10, steps // 4))
+    attn_bytes = 2 * (pos + 1) * kv * hd * 4 + 2 * heads * hd * 4
+    norm_bytes = 2 * 4096 * 2048 * 4 + 2048 * 4
+    return {"attention_decode_4096_ms": means[0],
+            "attention_decode_4096_gbps": attn_bytes / means[0] / 1e6,
+            "rms_norm_4096x2048_ms": means[1],
+            "rms_norm_4096x2048_gbps": norm_bytes / means[1] / 1e6,
+            "bytes": {"attention_decode_4096": attn_bytes, "rms_norm_4096x2048": norm_bytes}}
+
+
 def bench_loaders(torch, D, timer, steps):
     """The other load-time converters (beyond the north star's BF16 -> Q8):
     BF16 -> Q4 (lab_quantize_q4 after _widenBf16) on a 32768 x 4096 matrix
@@ -628,6 +659,9 @@ def main():
             torch.cuda.empty_cache()
         print("bench: load-time converters", file=sys.stderr, flush=True)
         configs["load_time_converters"] = bench_loaders(torch, D, timer, args.steps)
+        torch.cuda.empty_cache()
+        print("bench: layer steps", file=sys.stderr, flush=True)
+        configs["layer_steps"] = bench_layers(torch, D, timer, args.steps)
         torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:

@@ -18,6 +18,8 @@ HEADERS = [os.path.join(ROOT, "include", h) for h in ("lab_gpu.h", "dnx_kernels.
 _i64 = ctypes.c_int64
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int
+_f32 = ctypes.c_float
+_f64 = ctypes.c_double
 
 # argtypes / restype of every exported entry point (include/*.h).
 SIGNATURES = {
@@ -36,6 +38,13 @@ SIGNATURES = {
     "lab_gpu_enc_matmul_q8": ([_i64] * 10, None),
     "lab_gpu_enc_matmul_q4": ([_i64] * 10, None),
     "lab_gpu_enc_swiglu": ([_i64] * 3, None),
+    "lab_gpu_enc_rms_norm": ([_i64] * 8 + [_f64, _i64], None),
+    "lab_gpu_enc_head_norm_rope": ([_i64] * 11 + [_f64], None),
+    "lab_gpu_enc_conv": ([_i64] * 8, None),
+    "lab_gpu_enc_attention": ([_i64] * 11, None),
+    "lab_gpu_enc_copy": ([_i64] * 5, None),
+    "lab_gpu_enc_add": ([_i64] * 5, None),
+    "lab_gpu_enc_steer": ([_i64] * 7 + [_f64], None),
     "lab_gpu_enc_quantize_q8": ([_i64] * 9, None),
     "lab_gpu_enc_quantize_q8_bf16": ([_i64] * 9, None),
     "lab_gpu_enc_quantize_q4": ([_i64] * 8, None),
@@ -84,6 +93,14 @@ SIGNATURES = {
     "dnx_argmax": ([_p, _i64, _p, _p, _p], _i32),
     "dnx_swiglu": ([_p, _p, _i64, _p], _i32),
     "dnx_gelu": ([_p, _i64, _p], _i32),
+    "dnx_rms_norm": ([_p, _p, _p, _i64, _i64, _f32, _i32, _p], _i32),
+    "dnx_head_norm_rope": ([_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _f32, _p], _i32),
+    "dnx_short_conv": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dnx_attention_max_keys": ([_i64], _i64),
+    "dnx_attention": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p], _i32),
+    "dnx_add": ([_p, _p, _i64, _p], _i32),
+    "dnx_copy": ([_p, _p, _i64, _p], _i32),
+    "dnx_steer": ([_p, _p, _i64, _i64, _i64, _f32, _p], _i32),
 }
 
 

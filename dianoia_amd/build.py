@@ -17,7 +17,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libdianoia_amd.so")
-SOURCES = ["kernels.hip", "gemv.hip", "gemm.hip", "gemm_f16.hip", "lab_gpu.hip"]
+SOURCES = ["kernels.hip", "gemv.hip", "gemm.hip", "gemm_f16.hip", "layers.hip", "lab_gpu.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -59,12 +59,13 @@ struct Buffer {
 
 enum Op {
   kOpMatmulQ8, kOpMatmulQ4, kOpSwiglu, kOpQuantize, kOpQuantizeBf16, kOpQuantizeQ4,
-  kOpQuantizeQ4Bf16, kOpQ6kToQ8, kOpArgmax, kOpGelu
+  kOpQuantizeQ4Bf16, kOpQ6kToQ8, kOpArgmax, kOpGelu, kOpRmsNorm, kOpHeadNormRope, kOpConv,
+  kOpAttention, kOpCopy, kOpAdd, kOpSteer
 };
 
 struct Cmd {
   Op op;
-  int64_t a[10];
+  int64_t a[12];
   bool int8_inputs;  // matmuls: the input mode when the command was recorded
 };
 
@@ -414,6 +415,95 @@ bool run(const Cmd& c) {
       wrote_region(sc, scOff, rows * (cols / 32) * 4);
       return rc == DNX_OK;
     }
+    case kOpRmsNorm: {
+      const int64_t x = c.a[0], xOff = c.a[1], w = c.a[2], wOff = c.a[3], out = c.a[4];
+      const int64_t outOff = c.a[5], rows = c.a[6], cols = c.a[7], acc = c.a[9];
+      const double eps = __builtin_bit_cast(double, c.a[8]);
+      read_region(x, xOff, rows * cols * 4);
+      read_region(w, wOff, cols * 4);
+      if (acc) read_region(out, outOff, rows * cols * 4);
+      const int rc = dnx_rms_norm((const float*)dev_at(x, xOff), (const float*)dev_at(w, wOff),
+                                  (float*)dev_at(out, outOff), rows, cols, (float)eps,
+                                  acc != 0, gStream);
+      after_dispatch(kKindRmsNorm);
+      wrote_region(out, outOff, rows * cols * 4);
+      return rc == DNX_OK;
+    }
+    case kOpHeadNormRope: {
+      const int64_t x = c.a[0], xOff = c.a[1], xStride = c.a[2], w = c.a[3], wOff = c.a[4];
+      const int64_t rope = c.a[5], ropeOff = c.a[6], ropeStride = c.a[7], heads = c.a[8];
+      const int64_t hd = c.a[9], n = c.a[10];
+      const double eps = __builtin_bit_cast(double, c.a[11]);
+      const int64_t xBytes = ((n - 1) * xStride + heads * hd) * 4;
+      read_region(x, xOff, xBytes);
+      read_region(w, wOff, hd * 4);
+      read_region(rope, ropeOff, ((n - 1) * ropeStride + hd) * 4);
+      const int rc = dnx_head_norm_rope((float*)dev_at(x, xOff), xStride,
+                                        (const float*)dev_at(w, wOff),
+                                        (const float*)dev_at(rope, ropeOff), ropeStride, heads,
+                                        hd, n, (float)eps, gStream);
+      after_dispatch(kKindHeadNormRope);
+      wrote_region(x, xOff, xBytes);
+      return rc == DNX_OK;
+    }
+    case kOpConv: {
+      const int64_t bcx = c.a[0], weight = c.a[1], wOff = c.a[2], history = c.a[3], y = c.a[4];
+      const int64_t width = c.a[5], k = c.a[6], n = c.a[7];
+      read_region(bcx, 0, n * 3 * width * 4);
+      read_region(weight, wOff, width * k * 4);
+      read_region(history, 0, (k - 1) * width * 4);
+      const int rc = dnx_short_conv((const float*)dev_at(bcx, 0),
+                                    (const float*)dev_at(weight, wOff),
+                                    (float*)dev_at(history, 0), (float*)dev_at(y, 0), width, k,
+                                    n, gStream);
+      after_dispatch(kKindConv);
+      wrote_region(history, 0, (k - 1) * width * 4);
+      wrote_region(y, 0, n * width * 4);
+      return rc == DNX_OK;
+    }
+    case kOpAttention: {
+      const int64_t q = c.a[0], keys = c.a[1], values = c.a[2], gate = c.a[3], out = c.a[4];
+      const int64_t position = c.a[5], n = c.a[6], heads = c.a[7], kvHeads = c.a[8];
+      const int64_t hd = c.a[9], window = c.a[10];
+      const int64_t kvBytes = (position + n) * kvHeads * hd * 4;
+      read_region(q, 0, n * heads * hd * 4);
+      read_region(keys, 0, kvBytes);
+      read_region(values, 0, kvBytes);
+      if (gate >= 0) read_region(gate, 0, n * heads * 4);
+      const int rc = dnx_attention(
+          (const float*)dev_at(q, 0), (const float*)dev_at(keys, 0),
+          (const float*)dev_at(values, 0), gate >= 0 ? (const float*)dev_at(gate, 0) : nullptr,
+          (float*)dev_at(out, 0), position, n, heads, kvHeads, hd, window, gStream);
+      after_dispatch(kKindAttention);
+      wrote_region(out, 0, n * heads * hd * 4);
+      return rc == DNX_OK;
+    }
+    case kOpCopy:
+    case kOpAdd: {
+      const int64_t src = c.a[0], srcOff = c.a[1], dst = c.a[2], dstOff = c.a[3], count = c.a[4];
+      read_region(src, srcOff, count * 4);
+      if (c.op == kOpAdd) read_region(dst, dstOff, count * 4);
+      const int rc = c.op == kOpAdd
+                         ? dnx_add((const float*)dev_at(src, srcOff),
+                                   (float*)dev_at(dst, dstOff), count, gStream)
+                         : dnx_copy((const float*)dev_at(src, srcOff),
+                                    (float*)dev_at(dst, dstOff), count, gStream);
+      after_dispatch(c.op == kOpAdd ? kKindAdd : kKindCopy);
+      wrote_region(dst, dstOff, count * 4);
+      return rc == DNX_OK;
+    }
+    case kOpSteer: {
+      const int64_t x = c.a[0], xOff = c.a[1], v = c.a[2], vOff = c.a[3], rows = c.a[4];
+      const int64_t cols = c.a[5], mode = c.a[6];
+      const double scale = __builtin_bit_cast(double, c.a[7]);
+      read_region(x, xOff, rows * cols * 4);
+      read_region(v, vOff, cols * 4);
+      const int rc = dnx_steer((float*)dev_at(x, xOff), (const float*)dev_at(v, vOff), rows, cols,
+                               mode, (float)scale, gStream);
+      after_dispatch(kKindSteer);
+      wrote_region(x, xOff, rows * cols * 4);
+      return rc == DNX_OK;
+    }
     case kOpArgmax: {
       const int64_t x = c.a[0], xOff = c.a[1], n = c.a[2], out = c.a[3], outOff = c.a[4];
       read_region(x, xOff, n * 4);
@@ -698,6 +788,101 @@ void lab_gpu_enc_q6k_to_q8(int64_t src, int64_t srcOffset, int64_t qs, int64_t q
     return;
   }
   record(kOpQ6kToQ8, {src, srcOffset, qs, qsOffset, scales, scalesOffset, rows, cols});
+}
+
+// The layer steps: arguments are checked here (the reference's kernels
+// would read out of bounds); an invalid one fails the command buffer.
+static bool fail_enc(const char* what) {
+  LOG("%s: invalid arguments\n", what);
+  gFailed = true;
+  return false;
+}
+
+void lab_gpu_enc_rms_norm(int64_t x, int64_t xOffset, int64_t w, int64_t wOffset, int64_t out,
+                          int64_t outOffset, int64_t rows, int64_t cols, double eps,
+                          int64_t accumulate) {
+  if (rows < 0 || cols <= 0 || !in_bounds(x, xOffset, rows * cols * 4) ||
+      !in_bounds(w, wOffset, cols * 4) || !in_bounds(out, outOffset, rows * cols * 4) ||
+      xOffset % 4 || wOffset % 4 || outOffset % 4) {
+    fail_enc("enc_rms_norm");
+    return;
+  }
+  record(kOpRmsNorm, {x, xOffset, w, wOffset, out, outOffset, rows, cols,
+                      __builtin_bit_cast(int64_t, eps), accumulate});
+}
+
+void lab_gpu_enc_head_norm_rope(int64_t x, int64_t xOffset, int64_t xStride, int64_t w,
+                                int64_t wOffset, int64_t rope, int64_t ropeOffset,
+                                int64_t ropeStride, int64_t heads, int64_t hd, int64_t n,
+                                double eps) {
+  if (n <= 0 || heads <= 0 || hd <= 0 || hd % 2 || hd > 512 || xStride < heads * hd ||
+      ropeStride < hd || !in_bounds(x, xOffset, ((n - 1) * xStride + heads * hd) * 4) ||
+      !in_bounds(w, wOffset, hd * 4) ||
+      !in_bounds(rope, ropeOffset, ((n - 1) * ropeStride + hd) * 4) || xOffset % 4 ||
+      wOffset % 4 || ropeOffset % 4) {
+    fail_enc("enc_head_norm_rope");
+    return;
+  }
+  record(kOpHeadNormRope, {x, xOffset, xStride, w, wOffset, rope, ropeOffset, ropeStride, heads,
+                           hd, n, __builtin_bit_cast(int64_t, eps)});
+}
+
+void lab_gpu_enc_conv(int64_t bcx, int64_t weight, int64_t weightOffset, int64_t history,
+                      int64_t y, int64_t width, int64_t k, int64_t n) {
+  if (n <= 0 || width <= 0 || k < 2 || k > 16 || !in_bounds(bcx, 0, n * 3 * width * 4) ||
+      !in_bounds(weight, weightOffset, width * k * 4) ||
+      !in_bounds(history, 0, (k - 1) * width * 4) || !in_bounds(y, 0, n * width * 4) ||
+      weightOffset % 4) {
+    fail_enc("enc_conv");
+    return;
+  }
+  record(kOpConv, {bcx, weight, weightOffset, history, y, width, k, n});
+}
+
+void lab_gpu_enc_attention(int64_t q, int64_t keys, int64_t values, int64_t gate, int64_t out,
+                           int64_t position, int64_t n, int64_t heads, int64_t kvHeads,
+                           int64_t hd, int64_t window) {
+  const int64_t kvBytes = (position + n) * kvHeads * hd * 4;
+  if (n <= 0 || position < 0 || heads <= 0 || kvHeads <= 0 || heads % kvHeads || hd <= 0 ||
+      hd % 4 || 256 % hd || window < 0 || !in_bounds(q, 0, n * heads * hd * 4) ||
+      !in_bounds(keys, 0, kvBytes) || !in_bounds(values, 0, kvBytes) ||
+      (gate >= 0 && !in_bounds(gate, 0, n * heads * 4)) ||
+      !in_bounds(out, 0, n * heads * hd * 4)) {
+    fail_enc("enc_attention");
+    return;
+  }
+  record(kOpAttention, {q, keys, values, gate, out, position, n, heads, kvHeads, hd, window});
+}
+
+void lab_gpu_enc_copy(int64_t src, int64_t srcOffset, int64_t dst, int64_t dstOffset,
+                      int64_t count) {
+  if (count < 0 || !in_bounds(src, srcOffset, count * 4) ||
+      !in_bounds(dst, dstOffset, count * 4) || srcOffset % 4 || dstOffset % 4) {
+    fail_enc("enc_copy");
+    return;
+  }
+  record(kOpCopy, {src, srcOffset, dst, dstOffset, count});
+}
+
+void lab_gpu_enc_add(int64_t src, int64_t srcOffset, int64_t dst, int64_t dstOffset,
+                     int64_t count) {
+  if (count < 0 || !in_bounds(src, srcOffset, count * 4) ||
+      !in_bounds(dst, dstOffset, count * 4) || srcOffset % 4 || dstOffset % 4) {
+    fail_enc("enc_add");
+    return;
+  }
+  record(kOpAdd, {src, srcOffset, dst, dstOffset, count});
+}
+
+void lab_gpu_enc_steer(int64_t x, int64_t xOffset, int64_t v, int64_t vOffset, int64_t rows,
+                       int64_t cols, int64_t mode, double scale) {
+  if (rows < 0 || cols <= 0 || (mode != 0 && mode != 1) ||
+      !in_bounds(x, xOffset, rows * cols * 4) || !in_bounds(v, vOffset, cols * 4) ||
+      xOffset % 4 || vOffset % 4) {
+    fail_enc("enc_steer");
+    return;
+  }
+  record(kOpSteer, {x, xOffset, v, vOffset, rows, cols, mode, __builtin_bit_cast(int64_t, scale)});
 }
 
 void lab_gpu_enc_argmax(int64_t x, int64_t xOffset, int64_t n, int64_t out, int64_t outOffset) {

@@ -1,0 +1,543 @@
+// gfx950 kernels of the decoder's other layer steps, behind the reference's
+// lab_gpu_enc_* encoders (lib/src/gpu.dart:179-312; semantics of the Metal
+// layer, src/metal/lab_metal.m:321-579): RMSNorm, the per-head norm + RoPE,
+// the gated short convolution, causal attention over a KV cache, the
+// residual add and copy, and the control-vector steer. All fp32, HBM- or
+// latency-bound; none is on the quantized linear layer's path.
+//
+// Reductions run as a wave butterfly (all lanes end with the total) and then
+// a fixed-order sum of the waves' totals, so every result is deterministic.
+// Their order differs from the Metal layer's SIMD-group sums, so results
+// agree with it (and with the CPU oracle) to fp32 rounding, not bit for bit.
+// Built with -ffp-contract=off: no multiply-add is fused unless written as
+// fmaf.
+
+#include "common.h"
+#include "dnx_kernels.h"
+
+#include <math.h>
+
+using namespace dnx;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+DNX_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+DNX_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Sum over the workgroup: each wave's butterfly, then the waves' totals in
+// wave order. `scratch` holds kWaves floats; every thread gets the total.
+DNX_DEV float block_sum(float v, float* scratch) {
+  v = wave_sum(v);
+  __syncthreads();  // scratch may still be read from a previous call
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = scratch[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; w++) t += scratch[w];
+  return t;
+}
+
+DNX_DEV float block_max(float v, float* scratch) {
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = scratch[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; w++) t = fmaxf(t, scratch[w]);
+  return t;
+}
+
+// RMSNorm of one row per workgroup (lab_metal.m:327-347): r = 1 / sqrt(
+// sum(x^2) / cols + eps); y = w * (x * r), x * r rounded first; with
+// `accumulate` y is added into out (a post-norm added to the residual).
+__global__ void __launch_bounds__(kThreads)
+rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, float* out,
+                int cols, float eps, int accumulate) {
+  __shared__ float scratch[kWaves];
+  const float* xr = x + (size_t)blockIdx.x * cols;
+  float* yr = out + (size_t)blockIdx.x * cols;
+  float sum = 0.0f;
+  for (int j = threadIdx.x; j < cols; j += kThreads) sum += xr[j] * xr[j];
+  sum = block_sum(sum, scratch);
+  const float r = 1.0f / sqrtf(sum / (float)cols + eps);
+  for (int j = threadIdx.x; j < cols; j += kThreads) {
+    const float v = w[j] * (xr[j] * r);
+    yr[j] = accumulate ? yr[j] + v : v;
+  }
+}
+
+// Per (head, token), one wave (lab_metal.m:357-380): RMSNorm over head_dim
+// with weight w, then the half-split RoPE rotation pairing j with
+// j + hd / 2, from the token's tables [cos(hd / 2), sin(hd / 2)]. In place;
+// each lane reads its pairs before the reduction and writes only them.
+__global__ void __launch_bounds__(64)
+head_norm_rope_kernel(float* x, int x_stride, const float* __restrict__ w,
+                      const float* __restrict__ rope, int rope_stride, int hd, float eps) {
+  constexpr int kPairs = 4;  // hd <= 512
+  const int lane = threadIdx.x, pair = hd / 2;
+  float* xh = x + (size_t)blockIdx.y * x_stride + (size_t)blockIdx.x * hd;
+  const float* table = rope + (size_t)blockIdx.y * rope_stride;
+  float x1[kPairs], x2[kPairs];
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < kPairs; e++) {
+    const int j = lane + 64 * e;
+    x1[e] = j < pair ? xh[j] : 0.0f;
+    x2[e] = j < pair ? xh[j + pair] : 0.0f;
+    sum += x1[e] * x1[e] + x2[e] * x2[e];
+  }
+  sum = wave_sum(sum);
+  const float r = 1.0f / sqrtf(sum / (float)hd + eps);
+#pragma unroll
+  for (int e = 0; e < kPairs; e++) {
+    const int j = lane + 64 * e;
+    if (j >= pair) break;
+    const float n1 = w[j] * (x1[e] * r), n2 = w[j + pair] * (x2[e] * r);
+    const float c = table[j], s = table[pair + j];
+    xh[j] = n1 * c - n2 * s;
+    xh[j + pair] = n2 * c + n1 * s;
+  }
+}
+
+constexpr int kMaxConvK = 16;
+
+// The gated short convolution (lab_metal.m:383-412), one thread per
+// channel walking the n tokens in order: z = B * X, a causal depthwise conv
+// of the last k values of z (kernel column k - 1 weighting the newest),
+// y = C * conv. The k - 1 previous z come from `history` (rows oldest
+// first), which is left holding the last k - 1. bcx rows hold B, C, X.
+__global__ void __launch_bounds__(kThreads)
+conv_kernel(const float* __restrict__ bcx, const float* __restrict__ weight, float* history,
+            float* __restrict__ y, int width, int k, int n) {
+  const int ch = blockIdx.x * kThreads + threadIdx.x;
+  if (ch >= width) return;
+  const float* kw = weight + (size_t)ch * k;
+  float past[kMaxConvK];
+  for (int r = 0; r + 1 < k; r++) past[r] = history[(size_t)r * width + ch];
+  for (int t = 0; t < n; t++) {
+    const float* row = bcx + (size_t)t * 3 * width;
+    const float z = row[ch] * row[2 * width + ch];
+    float acc = kw[k - 1] * z;
+    for (int s = 1; s < k; s++) acc += kw[k - 1 - s] * past[k - 1 - s];
+    y[(size_t)t * width + ch] = row[width + ch] * acc;
+    for (int r = 0; r + 2 < k; r++) past[r] = past[r + 1];
+    if (k >= 2) past[k - 2] = z;
+  }
+  for (int r = 0; r + 1 < k; r++) history[(size_t)r * width + ch] = past[r];
+}
+
+// Causal attention of n tokens at positions position.. over their cached
+// keys and values (lab_metal.m:414-521), one workgroup per (head, token):
+// scores q.k / sqrt(hd) against the keys the token may see (window 0:
+// every earlier position; else the last `window`, its own included), a
+// softmax, the weighted sum of values, and the per-head output gate
+// sigmoid(gate) when `gate` is not null. GQA: query head h reads KV head
+// h / (heads / kv_heads). Scores live in LDS (dynamic, sized by the launch
+// for the last token's keys). Each thread takes whole keys for the dots
+// (one key row per lane: 16-byte loads), and the value sum splits the keys
+// over 256 / hd thread groups added in group order.
+__global__ void __launch_bounds__(kThreads)
+attention_kernel(const float* __restrict__ q, const float* __restrict__ keys,
+                 const float* __restrict__ values, const float* __restrict__ gate,
+                 float* __restrict__ out, int position, int heads, int kv_dim, int group,
+                 int hd, int window, float scale) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ float scratch[kWaves];
+  const int head = blockIdx.x, token = blockIdx.y, tid = threadIdx.x;
+  const int pos = position + token;
+  const int start = window > 0 && pos >= window ? pos - window + 1 : 0;
+  const int count = pos - start + 1;
+  const size_t qo = ((size_t)token * heads + head) * hd;
+  const int kvo = head / group * hd;
+  float* qs = lds;                      // [hd]
+  float* scores = lds + hd;             // [count]
+  float* part = scores + ((count + 3) & ~3);   // [groups][hd] value partials
+  for (int d = tid; d < hd; d += kThreads) qs[d] = q[qo + d];
+  __syncthreads();
+
+  const int hd4 = hd / 4;
+  for (int i = tid; i < count; i += kThreads) {
+    const float4* k4 = (const float4*)(keys + (size_t)(start + i) * kv_dim + kvo);
+    float d = 0.0f;
+    for (int c = 0; c < hd4; c++) {
+      const float4 kc = k4[c];
+      const float4 qc = *(const float4*)(qs + 4 * c);
+      d += qc.x * kc.x + qc.y * kc.y + qc.z * kc.z + qc.w * kc.w;
+    }
+    scores[i] = d * scale;
+  }
+  __syncthreads();
+  float m = -INFINITY;
+  for (int i = tid; i < count; i += kThreads) m = fmaxf(m, scores[i]);
+  m = block_max(m, scratch);
+  float sum = 0.0f;
+  for (int i = tid; i < count; i += kThreads) {
+    const float e = expf(scores[i] - m);
+    scores[i] = e;
+    sum += e;
+  }
+  sum = block_sum(sum, scratch);  // its barriers also publish the exponentials
+  const int groups = kThreads / hd;  // >= 1: hd <= 256
+  const int gi = tid / hd, d = tid - gi * hd;
+  if (gi < groups) {
+    const float* v = values + (size_t)start * kv_dim + kvo + d;
+    float acc = 0.0f;
+    int i = gi;
+    for (; i + 3 * groups < count; i += 4 * groups) {  // 4 keys' loads together
+      const float v0 = v[(size_t)i * kv_dim], v1 = v[(size_t)(i + groups) * kv_dim];
+      const float v2 = v[(size_t)(i + 2 * groups) * kv_dim];
+      const float v3 = v[(size_t)(i + 3 * groups) * kv_dim];
+      acc += scores[i] * v0;
+      acc += scores[i + groups] * v1;
+      acc += scores[i + 2 * groups] * v2;
+      acc += scores[i + 3 * groups] * v3;
+    }
+    for (; i < count; i += groups) acc += scores[i] * v[(size_t)i * kv_dim];
+    part[gi * hd + d] = acc;
+  }
+  __syncthreads();
+  if (gi == 0) {
+    float acc = part[d];
+    for (int g2 = 1; g2 < groups; g2++) acc += part[g2 * hd + d];
+    if (gate != nullptr) {
+      const float g = 1.0f / (1.0f + expf(-gate[(size_t)token * heads + head]));
+      out[qo + d] = (acc / sum) * g;
+    } else {
+      out[qo + d] = acc / sum;
+    }
+  }
+}
+
+// Long contexts with few (head, token) pairs (decode) split the keys: each
+// workgroup of attention_split_kernel takes split_keys(hd) keys of one
+// (head, token) and writes its max m, its exponentials' sum l (relative to
+// m) and its unnormalised value sums o[hd] (a row of hd + 4 floats: m, l,
+// two unused, o, so o is 16-byte aligned); attention_combine_kernel
+// rescales the splits to their common max and adds them in split order
+// (deterministic): O = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M). The
+// same softmax as attention_kernel, summed in another order.
+// A split puts hd / 4 lanes on a key row (one 16-byte piece each,
+// coalesced), 256 / (hd / 4) keys per workgroup step, and at most 16 steps:
+// every key and value load of the split is issued at its start, so it
+// waits for memory once. Dots end in a butterfly over the key's lanes;
+// value sums in per-lane float4 partials added in a fixed order.
+constexpr int kSplitSteps = 16;
+constexpr int kSplitMaxKeys = 256;
+
+int split_keys(int hd) {
+  const int step = kThreads / (hd / 4);   // keys per workgroup step
+  const int k = kSplitSteps * step;
+  return k < kSplitMaxKeys ? k : kSplitMaxKeys;
+}
+
+__global__ void __launch_bounds__(kThreads)
+attention_split_kernel(const float* __restrict__ q, const float* __restrict__ keys,
+                       const float* __restrict__ values, float* __restrict__ ws, int position,
+                       int heads, int kv_dim, int group, int hd, int window, float scale,
+                       int splits, int keys_per_split) {
+  __shared__ float scores[kSplitMaxKeys];
+  __shared__ float4 part[kThreads];
+  __shared__ float scratch[kWaves];
+  const int head = blockIdx.x, token = blockIdx.y, split = blockIdx.z, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int pos = position + token;
+  const int start = window > 0 && pos >= window ? pos - window + 1 : 0;
+  const int count = pos - start + 1;
+  const int k0 = split * keys_per_split;
+  const int nk = max(0, min(keys_per_split, count - k0));   // this split's keys
+  const int kvo = head / group * hd;
+  const int L = hd / 4, per = 64 / L, step = kWaves * per;  // lanes per key, keys per step
+  const int c = lane % L, kb = wave * per + lane / L;       // this lane's first key
+  const float4 qr = *(const float4*)(q + ((size_t)token * heads + head) * hd + 4 * c);
+  // Resources over this split's nk key rows: a row past them lies wholly
+  // beyond the range (its offset is at least nk rows) and reads zeros.
+  const size_t first = (size_t)(start + k0) * kv_dim + kvo;
+  const uint32_t range = (uint32_t)nk * (uint32_t)kv_dim * 4u;
+  const i32x4 krs = buffer_rsrc(keys + first, range);
+  const i32x4 vrs = buffer_rsrc(values + first, range);
+  const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float4 kv[kSplitSteps], vv[kSplitSteps];
+#pragma unroll
+  for (int j = 0; j < kSplitSteps; j++)
+    kv[j] = buffer_load_f4(krs, (kb + j * step) * kv_dim * 4 + 16 * c);
+#pragma unroll
+  for (int j = 0; j < kSplitSteps; j++)
+    vv[j] = buffer_load_f4(vrs, (kb + j * step) * kv_dim * 4 + 16 * c);
+#pragma unroll
+  for (int j = 0; j < kSplitSteps; j++) {
+    const int i = kb + j * step;
+    float d = qr.x * kv[j].x + qr.y * kv[j].y + qr.z * kv[j].z + qr.w * kv[j].w;
+    for (int o = L / 2; o > 0; o >>= 1) d += __shfl_xor(d, o);
+    if (i < nk && c == 0) scores[i] = d * scale;
+  }
+  __syncthreads();
+  const float m = block_max(tid < nk ? scores[tid] : -INFINITY, scratch);
+  float e = 0.0f;
+  if (tid < nk) {
+    e = expf(scores[tid] - m);
+    scores[tid] = e;
+  }
+  const float l = block_sum(e, scratch);  // its barriers also publish the exponentials
+  float4 acc = zero;
+#pragma unroll
+  for (int j = 0; j < kSplitSteps; j++) {
+    const int i = kb + j * step;
+    const float p = i < nk ? scores[i] : 0.0f;
+    acc.x += p * vv[j].x;
+    acc.y += p * vv[j].y;
+    acc.z += p * vv[j].z;
+    acc.w += p * vv[j].w;
+  }
+  part[tid] = acc;
+  __syncthreads();
+  float* out = ws + (((size_t)token * heads + head) * splits + split) * (hd + 4);
+  if (tid < L) {  // dimensions 4c..4c+3: the (wave, key-in-step) partials in order
+    float4 t = zero;
+    for (int w = 0; w < kWaves; w++)
+      for (int s2 = 0; s2 < per; s2++) {
+        const float4 p4 = part[w * 64 + s2 * L + tid];
+        t.x += p4.x;
+        t.y += p4.y;
+        t.z += p4.z;
+        t.w += p4.w;
+      }
+    *(float4*)(out + 4 + 4 * tid) = t;
+  }
+  if (tid == 0) {
+    out[0] = m;   // -inf for a split past the token's keys (l = 0, o = 0)
+    out[1] = l;
+  }
+}
+
+// The splits of one (head, token): their maxima and rescaling factors go
+// through LDS once (dynamic: `splits` floats), then each dimension's sum
+// over the splits with 8 loads in flight.
+__global__ void __launch_bounds__(kThreads)
+attention_combine_kernel(const float* __restrict__ ws, const float* __restrict__ gate,
+                         float* __restrict__ out, int heads, int hd, int splits) {
+  extern __shared__ float fs[];   // [splits] e^(m_s - M), 0 for empty splits
+  __shared__ float scratch[kWaves];
+  const int head = blockIdx.x, token = blockIdx.y, tid = threadIdx.x;
+  const float* w = ws + ((size_t)token * heads + head) * splits * (hd + 4);
+  float mx = -INFINITY;
+  for (int s = tid; s < splits; s += kThreads) mx = fmaxf(mx, w[(size_t)s * (hd + 4)]);
+  mx = block_max(mx, scratch);
+  float lp = 0.0f;
+  for (int s = tid; s < splits; s += kThreads) {
+    const float ms = w[(size_t)s * (hd + 4)];
+    const float f = ms != -INFINITY ? expf(ms - mx) : 0.0f;
+    fs[s] = f;
+    lp += w[(size_t)s * (hd + 4) + 1] * f;
+  }
+  const float l = block_sum(lp, scratch);  // its barriers also publish fs
+  const size_t qo = ((size_t)token * heads + head) * hd;
+  const float g = gate != nullptr ? 1.0f / (1.0f + expf(-gate[(size_t)token * heads + head])) : 1.0f;
+  for (int d = tid; d < hd; d += kThreads) {
+    const float* o = w + 4 + d;
+    float acc = 0.0f;
+    int s = 0;
+    for (; s + 8 <= splits; s += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = o[(size_t)(s + u) * (hd + 4)];
+#pragma unroll
+      for (int u = 0; u < 8; u++) acc += v[u] * fs[s + u];
+    }
+    for (; s < splits; s++) acc += o[(size_t)s * (hd + 4)] * fs[s];
+    out[qo + d] = gate != nullptr ? (acc / l) * g : acc / l;
+  }
+}
+
+// Library-owned workspace of the split attention, grown on demand: a call
+// with more (head, token, split) entries than any before allocates, so such
+// a call must not be the first inside a graph capture.
+float* gAttnWs = nullptr;
+size_t gAttnWsBytes = 0;
+
+float* attention_workspace(size_t bytes) {
+  if (bytes <= gAttnWsBytes) return gAttnWs;
+  if (gAttnWs != nullptr) {
+    if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+    (void)hipFree(gAttnWs);
+    gAttnWs = nullptr;
+    gAttnWsBytes = 0;
+  }
+  if (hipMalloc(&gAttnWs, bytes) != hipSuccess) return nullptr;
+  gAttnWsBytes = bytes;
+  return gAttnWs;
+}
+
+// dst += src (lab_metal.m:560-566) and dst = src (:567-572), element-wise.
+__global__ void __launch_bounds__(kThreads)
+add_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t count) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * kThreads) {
+    dst[i] = dst[i] + src[i];
+  }
+}
+
+__global__ void __launch_bounds__(kThreads)
+copy_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t count) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * kThreads) {
+    dst[i] = src[i];
+  }
+}
+
+// A control vector on rows of `cols` values, one workgroup per row
+// (lab_metal.m:531-557): mode 0 adds v; mode 1 removes scale times the
+// row's component along the unit direction v: x - (scale * (x . v)) v.
+__global__ void __launch_bounds__(kThreads)
+steer_kernel(float* x, const float* __restrict__ v, int cols, int mode, float scale) {
+  __shared__ float scratch[kWaves];
+  float* xr = x + (size_t)blockIdx.x * cols;
+  if (mode == 0) {
+    for (int j = threadIdx.x; j < cols; j += kThreads) xr[j] = xr[j] + v[j];
+    return;
+  }
+  float along = 0.0f;
+  for (int j = threadIdx.x; j < cols; j += kThreads) along += xr[j] * v[j];
+  along = block_sum(along, scratch);
+  const float c = scale * along;
+  for (int j = threadIdx.x; j < cols; j += kThreads) xr[j] = xr[j] - c * v[j];
+}
+
+int grid_for(int64_t items) {
+  const int64_t g = (items + kThreads - 1) / kThreads;
+  return (int)(g < 1 ? 1 : g > 65536 ? 65536 : g);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dnx_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64_t cols,
+                 float eps, int accumulate, dnx_stream_t stream) {
+  if (rows < 0 || cols <= 0 || cols > (1 << 30) || rows > 0x7fffffff) return DNX_EINVAL;
+  if (rows == 0) return DNX_OK;
+  hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)rows), dim3(kThreads), 0,
+                     (hipStream_t)stream, x, w, out, (int)cols, eps, accumulate);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_head_norm_rope(float* x, int64_t x_stride, const float* w, const float* rope,
+                       int64_t rope_stride, int64_t heads, int64_t hd, int64_t n, float eps,
+                       dnx_stream_t stream) {
+  if (heads <= 0 || n < 0 || hd <= 0 || hd % 2 != 0 || hd > 512 || x_stride < heads * hd ||
+      rope_stride < hd || x_stride > 0x7fffffff || rope_stride > 0x7fffffff ||
+      heads > 65535 || n > 65535) {
+    return DNX_EINVAL;
+  }
+  if (n == 0) return DNX_OK;
+  hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)heads, (unsigned)n), dim3(64), 0,
+                     (hipStream_t)stream, x, (int)x_stride, w, rope, (int)rope_stride, (int)hd,
+                     eps);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_short_conv(const float* bcx, const float* weight, float* history, float* y,
+                   int64_t width, int64_t k, int64_t n, dnx_stream_t stream) {
+  if (width <= 0 || k < 1 || k > kMaxConvK || n < 0 || width > 0x7fffffff ||
+      n > 0x7fffffff) {
+    return DNX_EINVAL;
+  }
+  if (n == 0) return DNX_OK;
+  hipLaunchKernelGGL(conv_kernel, dim3((unsigned)((width + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, (hipStream_t)stream, bcx, weight, history, y, (int)width,
+                     (int)k, (int)n);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int64_t dnx_attention_max_keys(int64_t hd) {
+  if (hd <= 0 || hd > 256 || kThreads % hd != 0) return -1;
+  // LDS: q (hd) + scores (rounded up to 4) + value partials ((256 / hd) x
+  // hd) + the kernel's 4-float reduction scratch, within 64 KB.
+  return (64 * 1024 / 4) - hd - kThreads - 4 - kWaves;
+}
+
+int dnx_attention(const float* q, const float* keys, const float* values, const float* gate,
+                  float* out, int64_t position, int64_t n, int64_t heads, int64_t kv_heads,
+                  int64_t hd, int64_t window, dnx_stream_t stream) {
+  if (n < 0 || position < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 ||
+      hd <= 0 || hd % 4 != 0 || hd > 256 || kThreads % hd != 0 || window < 0 ||
+      heads > 65535 || n > 65535 || position + n > 0x7fffffff || ((uintptr_t)keys & 15) ||
+      ((uintptr_t)q & 15)) {
+    return DNX_EINVAL;
+  }
+  if (n == 0) return DNX_OK;
+  const int64_t last = position + n - 1;
+  const int64_t keys_of_last = window > 0 && last >= window ? window : last + 1;
+  const float scale = (float)(1.0 / sqrt((double)hd));
+  // Few (head, token) workgroups for many keys: split the keys.
+  const int kps = split_keys((int)hd);
+  const int64_t splits = (keys_of_last + kps - 1) / kps;
+  // (Also when the keys exceed the one-workgroup kernel's LDS.) The split
+  // kernel's buffer offsets reach 4096 key rows: 32-bit up to 2^17 floats
+  // per row.
+  const size_t ws_bytes = (size_t)heads * n * splits * (hd + 4) * 4;
+  if (splits > 1 && (heads * n < 256 || keys_of_last > dnx_attention_max_keys(hd)) &&
+      splits <= 16000 && ws_bytes <= ((size_t)1 << 30) && kv_heads * hd <= (1 << 17)) {
+    float* ws = attention_workspace(ws_bytes);
+    if (ws == nullptr) return DNX_ENOMEM;
+    hipLaunchKernelGGL(attention_split_kernel,
+                       dim3((unsigned)heads, (unsigned)n, (unsigned)splits),
+                       dim3(kThreads), 0, (hipStream_t)stream, q, keys, values, ws, (int)position,
+                       (int)heads, (int)(kv_heads * hd), (int)(heads / kv_heads), (int)hd,
+                       (int)window, scale, (int)splits, kps);
+    if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)heads, (unsigned)n),
+                       dim3(kThreads), (size_t)splits * 4, (hipStream_t)stream, ws, gate, out,
+                       (int)heads, (int)hd, (int)splits);
+    return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+  }
+  if (keys_of_last > dnx_attention_max_keys(hd)) return DNX_EINVAL;
+  const size_t lds = (size_t)(hd + ((keys_of_last + 3) & ~3ll) + kThreads) * 4;
+  hipLaunchKernelGGL(attention_kernel, dim3((unsigned)heads, (unsigned)n), dim3(kThreads), lds,
+                     (hipStream_t)stream, q, keys, values, gate, out, (int)position,
+                     (int)heads, (int)(kv_heads * hd), (int)(heads / kv_heads), (int)hd,
+                     (int)window, scale);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_add(const float* src, float* dst, int64_t count, dnx_stream_t stream) {
+  if (count < 0) return DNX_EINVAL;
+  if (count == 0) return DNX_OK;
+  hipLaunchKernelGGL(add_kernel, dim3(grid_for(count)), dim3(kThreads), 0, (hipStream_t)stream,
+                     src, dst, count);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_copy(const float* src, float* dst, int64_t count, dnx_stream_t stream) {
+  if (count < 0) return DNX_EINVAL;
+  if (count == 0) return DNX_OK;
+  hipLaunchKernelGGL(copy_kernel, dim3(grid_for(count)), dim3(kThreads), 0, (hipStream_t)stream,
+                     src, dst, count);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_steer(float* x, const float* v, int64_t rows, int64_t cols, int64_t mode, float scale,
+              dnx_stream_t stream) {
+  if (rows < 0 || cols <= 0 || (mode != 0 && mode != 1) || rows > 0x7fffffff ||
+      cols > (1 << 30)) {
+    return DNX_EINVAL;
+  }
+  if (rows == 0) return DNX_OK;
+  hipLaunchKernelGGL(steer_kernel, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
+                     x, v, (int)cols, (int)mode, scale);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+}  // extern "C"

@@ -188,3 +188,44 @@ def swiglu(g: torch.Tensor, u: torch.Tensor, stream=None) -> None:
 
 def gelu(x: torch.Tensor, stream=None) -> None:
     _check(_lib.load().dnx_gelu(_ptr(x), x.numel(), _stream(stream)), "dnx_gelu")
+
+
+# ---- the decoder's other layer steps (lab_gpu_enc_* semantics, fp32)
+
+def rms_norm(x, w, out, rows: int, cols: int, eps: float, accumulate: bool = False,
+             stream=None) -> None:
+    _check(_lib.load().dnx_rms_norm(_ptr(x), _ptr(w), _ptr(out), rows, cols, eps,
+                                    1 if accumulate else 0, _stream(stream)), "dnx_rms_norm")
+
+
+def head_norm_rope(x, x_stride: int, w, rope, rope_stride: int, heads: int, hd: int, n: int,
+                   eps: float, stream=None) -> None:
+    _check(_lib.load().dnx_head_norm_rope(_ptr(x), x_stride, _ptr(w), _ptr(rope), rope_stride,
+                                          heads, hd, n, eps, _stream(stream)),
+           "dnx_head_norm_rope")
+
+
+def short_conv(bcx, weight, history, y, width: int, k: int, n: int, stream=None) -> None:
+    _check(_lib.load().dnx_short_conv(_ptr(bcx), _ptr(weight), _ptr(history), _ptr(y), width, k,
+                                      n, _stream(stream)), "dnx_short_conv")
+
+
+def attention(q, keys, values, gate, out, position: int, n: int, heads: int, kv_heads: int,
+              hd: int, window: int = 0, stream=None) -> None:
+    _check(_lib.load().dnx_attention(_ptr(q), _ptr(keys), _ptr(values),
+                                     None if gate is None else _ptr(gate), _ptr(out), position, n,
+                                     heads, kv_heads, hd, window, _stream(stream)),
+           "dnx_attention")
+
+
+def add(src, dst, count: int, stream=None) -> None:
+    _check(_lib.load().dnx_add(_ptr(src), _ptr(dst), count, _stream(stream)), "dnx_add")
+
+
+def copy(src, dst, count: int, stream=None) -> None:
+    _check(_lib.load().dnx_copy(_ptr(src), _ptr(dst), count, _stream(stream)), "dnx_copy")
+
+
+def steer(x, v, rows: int, cols: int, mode: int, scale: float, stream=None) -> None:
+    _check(_lib.load().dnx_steer(_ptr(x), _ptr(v), rows, cols, mode, scale, _stream(stream)),
+           "dnx_steer")

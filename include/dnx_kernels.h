@@ -171,6 +171,47 @@ int dnx_swiglu(float* g, const float* u, int64_t count, dnx_stream_t stream);
 // (lib/src/vision_encoder.dart:260-263, :496-509).
 int dnx_gelu(float* x, int64_t count, dnx_stream_t stream);
 
+// The decoder's other layer steps (the lab_gpu_enc_* encoders of
+// lib/src/gpu.dart:179-312, semantics of src/metal/lab_metal.m:321-579),
+// fp32, deterministic, equal to the reference's to fp32 rounding (their
+// reductions run in another order). Pointers are device pointers.
+//
+// RMSNorm of `rows` rows of `cols` (lab_metal.m:327-347): out = w * (x * r),
+// r = 1 / sqrt(mean(x^2) + eps); accumulate != 0 adds into out instead.
+int dnx_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64_t cols,
+                 float eps, int accumulate, dnx_stream_t stream);
+// Per head and token, in place: RMSNorm over hd (weight w), then the
+// half-split RoPE from the token's tables [cos(hd/2), sin(hd/2)]
+// (lab_metal.m:357-380). Strides in floats between tokens; hd even, <= 512.
+int dnx_head_norm_rope(float* x, int64_t x_stride, const float* w, const float* rope,
+                       int64_t rope_stride, int64_t heads, int64_t hd, int64_t n, float eps,
+                       dnx_stream_t stream);
+// The gated short convolution over n tokens (lab_metal.m:383-412): bcx rows
+// [B | C | X] of `width` each, weight [width][k] (k <= 16), history
+// [k - 1][width] (oldest first, updated), y [n][width].
+int dnx_short_conv(const float* bcx, const float* weight, float* history, float* y,
+                   int64_t width, int64_t k, int64_t n, dnx_stream_t stream);
+// Causal attention of n tokens at positions position.. over cached keys and
+// values [positions][kv_heads * hd] (lab_metal.m:414-521), q and out
+// [n][heads][hd], gate [n][heads] or null (ungated); window 0: every earlier
+// position, else the last `window`. hd a multiple of 4 dividing 256; q and
+// keys 16-byte aligned. Decode-shaped calls (fewer than 256 head-token
+// pairs, more than 256 keys) split the keys over workgroups and a combine
+// pass, with a library-owned workspace grown on demand (a first call at a
+// larger shape allocates: not inside a graph capture); otherwise at most
+// dnx_attention_max_keys(hd) keys per token.
+int64_t dnx_attention_max_keys(int64_t hd);
+int dnx_attention(const float* q, const float* keys, const float* values, const float* gate,
+                  float* out, int64_t position, int64_t n, int64_t heads, int64_t kv_heads,
+                  int64_t hd, int64_t window, dnx_stream_t stream);
+// dst += src and dst = src over `count` floats (lab_metal.m:560-572).
+int dnx_add(const float* src, float* dst, int64_t count, dnx_stream_t stream);
+int dnx_copy(const float* src, float* dst, int64_t count, dnx_stream_t stream);
+// A control vector on `rows` rows of `cols` (lab_metal.m:531-557): mode 0
+// adds v; mode 1 removes scale * (x . v) v (v a unit direction).
+int dnx_steer(float* x, const float* v, int64_t rows, int64_t cols, int64_t mode, float scale,
+              dnx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

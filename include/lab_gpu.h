@@ -93,6 +93,35 @@ void lab_gpu_enc_matmul_q4(int64_t w, int64_t qsOffset, int64_t scalesOffset, in
 // call this. Float inputs are limited to rows of up to about 14000 columns.
 int64_t lab_gpu_set_int8_inputs(int64_t on);
 
+// The decoder's other layer steps, as the reference binds them
+// (lib/src/gpu.dart:179-312; Vulkan lab_vulkan.c:899-1023, Metal
+// lab_metal.m:1046-1196) and with the Metal shaders' semantics
+// (lab_metal.m:321-579); fp32, equal to the reference's to fp32 rounding.
+// Offsets are bytes; strides are floats. An argument the kernel cannot take
+// (a region outside its buffer, hd not a multiple of 4 dividing 256 for
+// attention, conv k above 16) fails the command buffer (commit returns 0),
+// as the reference's kernels would read out of bounds instead.
+void lab_gpu_enc_rms_norm(int64_t x, int64_t xOffset, int64_t w, int64_t wOffset, int64_t out,
+                          int64_t outOffset, int64_t rows, int64_t cols, double eps,
+                          int64_t accumulate);
+void lab_gpu_enc_head_norm_rope(int64_t x, int64_t xOffset, int64_t xStride, int64_t w,
+                                int64_t wOffset, int64_t rope, int64_t ropeOffset,
+                                int64_t ropeStride, int64_t heads, int64_t hd, int64_t n,
+                                double eps);
+void lab_gpu_enc_conv(int64_t bcx, int64_t weight, int64_t weightOffset, int64_t history,
+                      int64_t y, int64_t width, int64_t k, int64_t n);
+// A negative `gate` leaves the heads ungated; `keys` and `values` hold rows
+// of kvHeads * hd floats for positions 0 .. position + n - 1.
+void lab_gpu_enc_attention(int64_t q, int64_t keys, int64_t values, int64_t gate, int64_t out,
+                           int64_t position, int64_t n, int64_t heads, int64_t kvHeads,
+                           int64_t hd, int64_t window);
+void lab_gpu_enc_copy(int64_t src, int64_t srcOffset, int64_t dst, int64_t dstOffset,
+                      int64_t count);
+void lab_gpu_enc_add(int64_t src, int64_t srcOffset, int64_t dst, int64_t dstOffset,
+                     int64_t count);
+void lab_gpu_enc_steer(int64_t x, int64_t xOffset, int64_t v, int64_t vOffset, int64_t rows,
+                       int64_t cols, int64_t mode, double scale);
+
 // lab_gpu_enc_swiglu (lab_vulkan.c:974-978; gpu.dart:179-312): g = SiLU(g)
 // * u over `count` floats from offset 0 of each buffer, SiLU in double as
 // the CPU glue computes it (shard.dart:457-461).

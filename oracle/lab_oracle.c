@@ -19,6 +19,9 @@
 // brute-force integer block dots, argmax ties/NaN). The Dart-only glue
 // (orc_silu_mul, orc_gelu) has no compiled reference here: it is pinned by
 // closed-form values only (see test_oracle.py), not bit-for-bit against Dart.
+// So are the Q6_K decoder (by ggml-layout packing) and the layer steps
+// (orc_rms_norm .. orc_steer: closed forms and invariants), whose
+// reference is a Metal/Vulkan shader.
 
 #include <math.h>
 #include <stdint.h>
@@ -504,5 +507,135 @@ void orc_gelu(float* x, int64_t count) {
   for (int64_t i = 0; i < count; i++) {
     const double v = x[i];
     x[i] = (float)(0.5 * v * (1 + as_erf(v / 1.4142135623730951)));
+  }
+}
+
+// ------------------------------------------------------------ layer steps
+//
+// The decoder's other GPU steps as the reference's Metal shaders define them
+// (src/metal/lab_metal.m:321-579): element values in float, in the shaders'
+// order; sums in double (any GPU summation order rounds within a few ulp of
+// the double sum, which is what the tests compare against with a tolerance).
+
+// RMSNorm (lab_metal.m:327-347): r = 1 / sqrt(sum(x^2) / cols + eps) in
+// float; y = w * (x * r); accumulate adds into out.
+void orc_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64_t cols,
+                  float eps, int accumulate) {
+  for (int64_t r = 0; r < rows; r++) {
+    const float* xr = x + r * cols;
+    float* yr = out + r * cols;
+    double sum = 0.0;
+    for (int64_t j = 0; j < cols; j++) sum += (double)(xr[j] * xr[j]);
+    const float rr = 1.0f / sqrtf((float)sum / (float)cols + eps);
+    for (int64_t j = 0; j < cols; j++) {
+      const float v = w[j] * (xr[j] * rr);
+      yr[j] = accumulate ? yr[j] + v : v;
+    }
+  }
+}
+
+// Per head and token, in place (lab_metal.m:357-380): RMSNorm over hd, then
+// the half-split RoPE: (n1, n2) -> (n1 c - n2 s, n2 c + n1 s).
+void orc_head_norm_rope(float* x, int64_t x_stride, const float* w, const float* rope,
+                        int64_t rope_stride, int64_t heads, int64_t hd, int64_t n, float eps) {
+  const int64_t pair = hd / 2;
+  for (int64_t t = 0; t < n; t++) {
+    const float* table = rope + t * rope_stride;
+    for (int64_t h = 0; h < heads; h++) {
+      float* xh = x + t * x_stride + h * hd;
+      double sum = 0.0;
+      for (int64_t j = 0; j < pair; j++) {
+        sum += (double)(xh[j] * xh[j] + xh[j + pair] * xh[j + pair]);
+      }
+      const float r = 1.0f / sqrtf((float)sum / (float)hd + eps);
+      for (int64_t j = 0; j < pair; j++) {
+        const float x1 = xh[j], x2 = xh[j + pair];
+        const float n1 = w[j] * (x1 * r), n2 = w[j + pair] * (x2 * r);
+        const float c = table[j], s = table[pair + j];
+        xh[j] = n1 * c - n2 * s;
+        xh[j + pair] = n2 * c + n1 * s;
+      }
+    }
+  }
+}
+
+// The gated short convolution (lab_metal.m:383-412), exactly the shader's
+// per-channel loop (it has no reduction to reorder).
+void orc_short_conv(const float* bcx, const float* weight, float* history, float* y,
+                    int64_t width, int64_t k, int64_t n) {
+  for (int64_t ch = 0; ch < width; ch++) {
+    const float* kw = weight + ch * k;
+    float past[16];
+    for (int64_t r = 0; r + 1 < k; r++) past[r] = history[r * width + ch];
+    for (int64_t t = 0; t < n; t++) {
+      const float* row = bcx + t * 3 * width;
+      const float z = row[ch] * row[2 * width + ch];
+      float acc = kw[k - 1] * z;
+      for (int64_t s = 1; s < k; s++) acc += kw[k - 1 - s] * past[k - 1 - s];
+      y[t * width + ch] = row[width + ch] * acc;
+      for (int64_t r = 0; r + 2 < k; r++) past[r] = past[r + 1];
+      if (k >= 2) past[k - 2] = z;
+    }
+    for (int64_t r = 0; r + 1 < k; r++) history[r * width + ch] = past[r];
+  }
+}
+
+// Causal attention (lab_metal.m:414-521; host side :1100-1127): scale =
+// (float)(1 / sqrt(hd)); per (head, token) scores against the visible keys,
+// softmax with exp(s - max), the value sum divided by the exponentials'
+// sum, times sigmoid(gate) when gate is not null. Dots and sums in double.
+void orc_attention(const float* q, const float* keys, const float* values, const float* gate,
+                   float* out, int64_t position, int64_t n, int64_t heads, int64_t kv_heads,
+                   int64_t hd, int64_t window) {
+  const int64_t kv_dim = kv_heads * hd, group = heads / kv_heads;
+  const float scale = (float)(1.0 / sqrt((double)hd));
+  float* scores = (float*)malloc((size_t)(position + n) * sizeof(float));
+  for (int64_t t = 0; t < n; t++) {
+    const int64_t pos = position + t;
+    const int64_t start = window > 0 && pos >= window ? pos - window + 1 : 0;
+    const int64_t count = pos - start + 1;
+    for (int64_t h = 0; h < heads; h++) {
+      const float* qh = q + (t * heads + h) * hd;
+      const int64_t kvo = h / group * hd;
+      float m = -INFINITY;
+      for (int64_t i = 0; i < count; i++) {
+        const float* kr = keys + (start + i) * kv_dim + kvo;
+        double d = 0.0;
+        for (int64_t c = 0; c < hd; c++) d += (double)qh[c] * (double)kr[c];
+        scores[i] = (float)d * scale;
+        if (scores[i] > m) m = scores[i];
+      }
+      double sum = 0.0;
+      for (int64_t i = 0; i < count; i++) {
+        scores[i] = expf(scores[i] - m);
+        sum += scores[i];
+      }
+      const float g = gate ? 1.0f / (1.0f + expf(-gate[t * heads + h])) : 1.0f;
+      for (int64_t d = 0; d < hd; d++) {
+        double acc = 0.0;
+        for (int64_t i = 0; i < count; i++) {
+          acc += (double)scores[i] * (double)values[(start + i) * kv_dim + kvo + d];
+        }
+        const float o = (float)acc / (float)sum;
+        out[(t * heads + h) * hd + d] = gate ? o * g : o;
+      }
+    }
+  }
+  free(scores);
+}
+
+// The control vector (lab_metal.m:531-557): mode 0 adds v to each row;
+// mode 1 computes c = scale * (x . v) and x -= c v.
+void orc_steer(float* x, const float* v, int64_t rows, int64_t cols, int64_t mode, float scale) {
+  for (int64_t r = 0; r < rows; r++) {
+    float* xr = x + r * cols;
+    if (mode == 0) {
+      for (int64_t j = 0; j < cols; j++) xr[j] = xr[j] + v[j];
+      continue;
+    }
+    double along = 0.0;
+    for (int64_t j = 0; j < cols; j++) along += (double)(xr[j] * v[j]);
+    const float c = scale * (float)along;
+    for (int64_t j = 0; j < cols; j++) xr[j] = xr[j] - c * v[j];
   }
 }

@@ -119,6 +119,15 @@ class Oracle(_Kernels):
         L.orc_dequantize_q6k.restype = None
         L.orc_q6k_to_q8.argtypes = [_p, _p, _p, _i64, _i64]
         L.orc_q6k_to_q8.restype = None
+        f32 = ctypes.c_float
+        L.orc_rms_norm.argtypes = [_p, _p, _p, _i64, _i64, f32, ctypes.c_int]
+        L.orc_head_norm_rope.argtypes = [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, f32]
+        L.orc_short_conv.argtypes = [_p, _p, _p, _p, _i64, _i64, _i64]
+        L.orc_attention.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64]
+        L.orc_steer.argtypes = [_p, _p, _i64, _i64, _i64, f32]
+        for name in ("orc_rms_norm", "orc_head_norm_rope", "orc_short_conv", "orc_attention",
+                     "orc_steer"):
+            getattr(L, name).restype = None
         L.orc_argmax.argtypes = [_p, _i64]
         L.orc_argmax.restype = _i64
         L.orc_silu_mul.argtypes = [_p, _p, _i64]
@@ -165,6 +174,51 @@ class Oracle(_Kernels):
         scales = np.zeros((rows, cols // 32), np.float32)
         self.lib.orc_q6k_to_q8(_ptr(blocks), _ptr(qs), _ptr(scales), rows, cols)
         return qs, scales
+
+    # ---- layer steps (Metal shader semantics, sums in double). Every array
+    # handed to C is bound to a name first, so it outlives the call.
+
+    def rms_norm(self, x, w, eps, out=None):
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        rows, cols = x.shape
+        acc = out is not None
+        y = np.array(out, np.float32, order="C") if acc else np.zeros_like(x)
+        self.lib.orc_rms_norm(_ptr(x), _ptr(w), _ptr(y), rows, cols, eps, 1 if acc else 0)
+        return y
+
+    def head_norm_rope(self, x, x_stride, w, rope, rope_stride, heads, hd, n, eps):
+        x = np.array(x, np.float32, order="C")
+        w = np.ascontiguousarray(w, np.float32)
+        rope = np.ascontiguousarray(rope, np.float32)
+        self.lib.orc_head_norm_rope(_ptr(x), x_stride, _ptr(w), _ptr(rope), rope_stride, heads,
+                                    hd, n, eps)
+        return x
+
+    def short_conv(self, bcx, weight, history, width, k, n):
+        bcx = np.ascontiguousarray(bcx, np.float32)
+        weight = np.ascontiguousarray(weight, np.float32)
+        history = np.array(history, np.float32, order="C")
+        y = np.zeros(n * width, np.float32)
+        self.lib.orc_short_conv(_ptr(bcx), _ptr(weight), _ptr(history), _ptr(y), width, k, n)
+        return y, history
+
+    def attention(self, q, keys, values, gate, position, n, heads, kv_heads, hd, window=0):
+        q = np.ascontiguousarray(q, np.float32)
+        keys = np.ascontiguousarray(keys, np.float32)
+        values = np.ascontiguousarray(values, np.float32)
+        g = None if gate is None else np.ascontiguousarray(gate, np.float32)
+        out = np.zeros(n * heads * hd, np.float32)
+        self.lib.orc_attention(_ptr(q), _ptr(keys), _ptr(values), None if g is None else _ptr(g),
+                               _ptr(out), position, n, heads, kv_heads, hd, window)
+        return out
+
+    def steer(self, x, v, mode, scale):
+        x = np.array(x, np.float32, order="C")
+        v = np.ascontiguousarray(v, np.float32)
+        rows, cols = x.shape
+        self.lib.orc_steer(_ptr(x), _ptr(v), rows, cols, mode, scale)
+        return x
 
     def gemm_q8_prequant(self, qs, scales, xq, xsc, threads=8):
         qs = np.ascontiguousarray(qs, np.int8)

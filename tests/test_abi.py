@@ -7,9 +7,9 @@ import subprocess
 
 from dianoia_amd import _lib
 
-# The reference's GPU entry points that Dart binds (lib/src/gpu.dart:36-312)
-# which this tier implements: the matmul path and everything GpuLinear and
-# the GPU layer's lifecycle, profiling and tuning calls reach.
+# The reference's GPU entry points that Dart binds (lib/src/gpu.dart:36-312):
+# the matmul path, everything GpuLinear and the GPU layer's lifecycle,
+# profiling and tuning calls reach, and the decoder's other layer steps.
 REFERENCE_BOUND = [
     "lab_gpu_init", "lab_gpu_max_buffer_length", "lab_gpu_max_shared_memory",
     "lab_gpu_recommended_working_set", "lab_gpu_thermal_state", "lab_gpu_physical_memory",
@@ -18,7 +18,9 @@ REFERENCE_BOUND = [
     "lab_gpu_set_decode_rows", "lab_gpu_set_q8_group", "lab_gpu_set_q8_vector",
     "lab_gpu_register_q8_head", "lab_gpu_set_profiling", "lab_gpu_profile", "lab_gpu_last_ms",
     "lab_gpu_begin", "lab_gpu_commit", "lab_gpu_wait", "lab_gpu_enc_matmul_q8",
-    "lab_gpu_enc_matmul_q4", "lab_gpu_enc_swiglu",
+    "lab_gpu_enc_matmul_q4", "lab_gpu_enc_swiglu", "lab_gpu_enc_rms_norm",
+    "lab_gpu_enc_head_norm_rope", "lab_gpu_enc_conv", "lab_gpu_enc_attention", "lab_gpu_enc_copy",
+    "lab_gpu_enc_add", "lab_gpu_enc_steer",
 ]
 
 

@@ -1,0 +1,225 @@
+"""The decoder's other layer steps on the GPU (lab_gpu_enc_rms_norm ..
+lab_gpu_enc_steer, lib/src/gpu.dart:179-312, Metal semantics
+src/metal/lab_metal.m:321-579) against the CPU oracle's restatement of the
+shaders. Element-wise steps with no reduction (conv, add, copy, steer mode 0)
+are bit-exact; reductions run in another order, so those steps are held to
+fp32 rounding: relative 1e-5, absolute 1e-6."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from dianoia_amd import _lib
+from dianoia_amd import device as D
+from gpu_util import bits, dev, host
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6
+
+
+def close(gpu, cpu, rtol=RTOL, atol=ATOL):
+    gpu, cpu = np.asarray(gpu, np.float64), np.asarray(cpu, np.float64)
+    err = np.abs(gpu - cpu)
+    ok = err <= atol + rtol * np.abs(cpu)
+    return bool(ok.all()), float(err.max(initial=0.0))
+
+
+@pytest.mark.parametrize("rows,cols,acc", [(1, 2048, False), (7, 1024, True), (128, 4096, False),
+                                           (3, 37, True)])
+def test_rms_norm(gpu_ready, orc, rows, cols, acc):
+    rng = np.random.default_rng(rows + cols)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    base = rng.standard_normal((rows, cols)).astype(np.float32)
+    out = dev(base if acc else np.zeros_like(x))
+    D.rms_norm(dev(x), dev(w), out, rows, cols, 1e-5, accumulate=acc)
+    want = orc.rms_norm(x, w, 1e-5, out=base if acc else None)
+    ok, err = close(host(out), want)
+    assert ok, err
+
+
+@pytest.mark.parametrize("heads,hd,n,stride_pad", [(16, 128, 1, 0), (8, 64, 5, 64), (2, 256, 3, 0),
+                                                   (4, 512, 2, 32)])
+def test_head_norm_rope(gpu_ready, orc, heads, hd, n, stride_pad):
+    rng = np.random.default_rng(heads * hd + n)
+    stride = heads * hd + stride_pad
+    x = rng.standard_normal((n, stride)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    pair = hd // 2
+    ang = rng.uniform(0, 6.3, (n, pair))
+    rope_stride = hd + 16
+    table = np.zeros((n, rope_stride), np.float32)
+    table[:, :pair], table[:, pair:hd] = np.cos(ang), np.sin(ang)
+    xd = dev(x)
+    D.head_norm_rope(xd, stride, dev(w), dev(table), rope_stride, heads, hd, n, 1e-6)
+    want = orc.head_norm_rope(x, stride, w, table, rope_stride, heads, hd, n, 1e-6)
+    got = host(xd)
+    ok, err = close(got[:, :heads * hd], want[:, :heads * hd])
+    assert ok, err
+    assert np.array_equal(got[:, heads * hd:], x[:, heads * hd:])  # the padding is untouched
+
+
+@pytest.mark.parametrize("width,k,n", [(6144, 3, 1), (2048, 4, 7), (300, 16, 3), (33, 2, 5)])
+def test_short_conv_bit_exact(gpu_ready, orc, width, k, n):
+    rng = np.random.default_rng(width + k + n)
+    bcx = rng.standard_normal((n, 3, width)).astype(np.float32)
+    weight = rng.standard_normal((width, k)).astype(np.float32)
+    hist = rng.standard_normal((k - 1, width)).astype(np.float32)
+    hd_ = dev(hist)
+    y = torch.zeros(n * width, device="cuda")
+    D.short_conv(dev(bcx), dev(weight), hd_, y, width, k, n)
+    want_y, want_h = orc.short_conv(bcx, weight, hist, width, k, n)
+    assert np.array_equal(bits(host(y)), bits(want_y))
+    assert np.array_equal(bits(host(hd_)), bits(want_h))
+
+
+@pytest.mark.parametrize("heads,kv,hd,pos,n,window,gated", [
+    (16, 4, 128, 2047, 1, 0, False),   # decode at 2 K context, GQA 4:1
+    (8, 8, 64, 100, 7, 0, True),       # prefill chunk, gated heads
+    (4, 2, 256, 600, 3, 128, False),   # sliding window
+    (2, 1, 32, 0, 5, 0, True),         # from position 0
+    (8, 2, 64, 3000, 3, 1000, True),   # split keys: window, gate, 3 tokens
+    (32, 8, 128, 300, 4, 0, False),    # split keys, the tokens' counts differ
+    (1, 1, 16, 20000, 1, 0, False),    # beyond one workgroup's LDS: split
+])
+def test_attention(gpu_ready, orc, heads, kv, hd, pos, n, window, gated):
+    rng = np.random.default_rng(heads + hd + pos + n)
+    total = pos + n
+    q = rng.standard_normal(n * heads * hd).astype(np.float32)
+    keys = rng.standard_normal((total, kv * hd)).astype(np.float32)
+    values = rng.standard_normal((total, kv * hd)).astype(np.float32)
+    gate = rng.standard_normal(n * heads).astype(np.float32) if gated else None
+    out = torch.zeros(n * heads * hd, device="cuda")
+    D.attention(dev(q), dev(keys), dev(values), dev(gate) if gated else None, out, pos, n, heads,
+                kv, hd, window)
+    want = orc.attention(q, keys, values, gate, pos, n, heads, kv, hd, window)
+    ok, err = close(host(out), want)
+    assert ok, err
+
+
+def test_attention_limits(gpu_ready):
+    lib = _lib.load()
+    assert lib.dnx_attention_max_keys(128) >= 15000
+    assert lib.dnx_attention_max_keys(96) == -1  # 256 % 96 != 0
+    q = torch.zeros(128, device="cuda")
+    with pytest.raises(RuntimeError):
+        D.attention(q, q, q, None, q, 0, 1, 1, 1, 96)
+
+
+def test_add_copy_steer(gpu_ready, orc):
+    rng = np.random.default_rng(8)
+    a = rng.standard_normal(100003).astype(np.float32)
+    b = rng.standard_normal(100003).astype(np.float32)
+    dst = dev(b)
+    D.add(dev(a), dst, a.size)
+    assert np.array_equal(bits(host(dst)), bits(b + a))
+    D.copy(dev(a), dst, a.size)
+    assert np.array_equal(bits(host(dst)), bits(a))
+    x = rng.standard_normal((5, 2048)).astype(np.float32)
+    v = rng.standard_normal(2048)
+    v = (v / np.linalg.norm(v)).astype(np.float32)
+    xd = dev(x)
+    D.steer(xd, dev(v), 5, 2048, 0, 1.0)
+    assert np.array_equal(bits(host(xd)), bits(orc.steer(x, v, 0, 1.0)))
+    xd = dev(x)
+    D.steer(xd, dev(v), 5, 2048, 1, 0.75)
+    ok, err = close(host(xd), orc.steer(x, v, 1, 0.75), atol=1e-5)
+    assert ok, err
+
+
+class Bufs:
+    """lab_gpu_* buffers with host views (the ABI's staged coherence)."""
+
+    def __init__(self):
+        self.lib = _lib.load()
+        assert self.lib.lab_gpu_init() == 1
+        self.handles = []
+
+    def new(self, arr):
+        arr = np.ascontiguousarray(arr, np.float32).reshape(-1)
+        h = self.lib.lab_gpu_buffer(max(arr.nbytes, 4))
+        assert h >= 0
+        self.handles.append(h)
+        self.view(h, arr.size)[:] = arr
+        return h
+
+    def view(self, h, count):
+        p = self.lib.lab_gpu_contents(h)
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), (count,))
+
+    def close(self):
+        for h in self.handles:
+            self.lib.lab_gpu_release(h)
+
+
+def test_layer_steps_through_the_abi(gpu_ready, orc):
+    """One command buffer with every layer step, read back through the
+    host views, against the oracle (and bit-exact where the step is)."""
+    rng = np.random.default_rng(9)
+    B = Bufs()
+    try:
+        lib = B.lib
+        rows, cols = 3, 256
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+        hx, hw, hout = B.new(x), B.new(w), B.new(np.zeros_like(x))
+        heads, hd, n = 4, 64, 2
+        xr = rng.standard_normal((n, heads * hd)).astype(np.float32)
+        wr = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+        ang = rng.uniform(0, 6.3, (n, hd // 2))
+        table = np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
+        hxr, hwr, htab = B.new(xr), B.new(wr), B.new(table)
+        width, k, tn = 96, 3, 4
+        bcx = rng.standard_normal((tn, 3, width)).astype(np.float32)
+        cw = rng.standard_normal((width, k)).astype(np.float32)
+        hist = rng.standard_normal((k - 1, width)).astype(np.float32)
+        hb, hcw, hh, hy = B.new(bcx), B.new(cw), B.new(hist), B.new(np.zeros(tn * width))
+        ah, akv, ahd, apos, an = 4, 2, 32, 9, 2
+        q = rng.standard_normal(an * ah * ahd).astype(np.float32)
+        keys = rng.standard_normal((apos + an, akv * ahd)).astype(np.float32)
+        vals = rng.standard_normal((apos + an, akv * ahd)).astype(np.float32)
+        gate = rng.standard_normal(an * ah).astype(np.float32)
+        hq, hk, hv, hg = B.new(q), B.new(keys), B.new(vals), B.new(gate)
+        hao = B.new(np.zeros(an * ah * ahd))
+        src = rng.standard_normal(1000).astype(np.float32)
+        dst = rng.standard_normal(1000).astype(np.float32)
+        hs, hd_, hc = B.new(src), B.new(dst), B.new(np.zeros(1000))
+        sv = rng.standard_normal(cols)
+        sv = (sv / np.linalg.norm(sv)).astype(np.float32)
+        hsx, hsv = B.new(x), B.new(sv)
+
+        lib.lab_gpu_begin()
+        lib.lab_gpu_enc_rms_norm(hx, 0, hw, 0, hout, 0, rows, cols, 1e-5, 0)
+        lib.lab_gpu_enc_head_norm_rope(hxr, 0, heads * hd, hwr, 0, htab, 0, hd, heads, hd, n, 1e-6)
+        lib.lab_gpu_enc_conv(hb, hcw, 0, hh, hy, width, k, tn)
+        lib.lab_gpu_enc_attention(hq, hk, hv, hg, hao, apos, an, ah, akv, ahd, 0)
+        lib.lab_gpu_enc_add(hs, 0, hd_, 0, 1000)
+        lib.lab_gpu_enc_copy(hs, 4 * 10, hc, 0, 990)
+        lib.lab_gpu_enc_steer(hsx, 0, hsv, 0, rows, cols, 1, 1.0)
+        assert lib.lab_gpu_commit(1) == 1
+
+        ok, err = close(B.view(hout, rows * cols), orc.rms_norm(x, w, 1e-5).reshape(-1))
+        assert ok, ("rms_norm", err)
+        want = orc.head_norm_rope(xr, heads * hd, wr, table, hd, heads, hd, n, 1e-6)
+        ok, err = close(B.view(hxr, n * heads * hd), want.reshape(-1))
+        assert ok, ("head_norm_rope", err)
+        wy, wh = orc.short_conv(bcx, cw, hist, width, k, tn)
+        assert np.array_equal(bits(B.view(hy, tn * width)), bits(wy))
+        assert np.array_equal(bits(B.view(hh, (k - 1) * width)), bits(wh.reshape(-1)))
+        wa = orc.attention(q, keys, vals, gate, apos, an, ah, akv, ahd)
+        ok, err = close(B.view(hao, an * ah * ahd), wa)
+        assert ok, ("attention", err)
+        assert np.array_equal(bits(B.view(hd_, 1000)), bits(dst + src))
+        assert np.array_equal(bits(B.view(hc, 990)), bits(src[10:]))
+        ok, err = close(B.view(hsx, rows * cols), orc.steer(x, sv, 1, 1.0).reshape(-1), atol=1e-5)
+        assert ok, ("steer", err)
+
+        # An invalid command fails the buffer instead of reading out of bounds.
+        lib.lab_gpu_begin()
+        lib.lab_gpu_enc_attention(hq, hk, hv, -1, hao, apos + 100, an, ah, akv, ahd, 0)
+        assert lib.lab_gpu_commit(1) == 0
+    finally:
+        B.close()

@@ -231,3 +231,119 @@ def test_oracle_matches_compiled_reference(orc, fmt):
                 a = ref.gemm_q4(qs, sc, xs, n, threads=4, mode=mode)
                 b = orc.gemm_q4(qs, sc, xs, n, threads=2, mode=mode)
                 assert np.array_equal(bits(a), bits(b))
+
+
+# ---- layer steps (Metal shader semantics): closed forms and invariants
+
+def test_rms_norm_closed_forms(orc):
+    cols = 96
+    x = np.stack([np.full(cols, 3.0, np.float32), np.full(cols, -0.5, np.float32),
+                  np.random.default_rng(3).standard_normal(cols).astype(np.float32)])
+    ones = np.ones(cols, np.float32)
+    y = orc.rms_norm(x, ones, 0.0)
+    assert np.allclose(y[0], 1.0, rtol=2e-7) and np.allclose(y[1], -1.0, rtol=2e-7)
+    assert abs(np.sqrt(np.mean(y[2].astype(np.float64) ** 2)) - 1.0) < 1e-6  # unit RMS
+    eps = np.float32(0.25)
+    ye = orc.rms_norm(x[:1], ones, float(eps))
+    assert np.allclose(ye, 3.0 / np.sqrt(9.0 + 0.25), rtol=2e-7)  # mean(x^2) + eps
+    w = np.linspace(-2, 2, cols).astype(np.float32)
+    assert np.array_equal(orc.rms_norm(x, 2 * w, 1e-6), 2 * orc.rms_norm(x, w, 1e-6))
+    base = np.full_like(x, 0.5)
+    acc = orc.rms_norm(x, w, 1e-6, out=base)
+    assert np.array_equal(acc, base + orc.rms_norm(x, w, 1e-6))
+
+
+def test_head_norm_rope_invariants(orc):
+    heads, hd, n = 3, 16, 2
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((n, heads * hd)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    pair = hd // 2
+    ident = np.concatenate([np.ones(pair), np.zeros(pair)]).astype(np.float32)
+    ident = np.tile(ident, (n, 1))
+    y = orc.head_norm_rope(x, heads * hd, w, ident, hd, heads, hd, n, 1e-6)
+    normed = orc.rms_norm(x.reshape(n * heads, hd), w, 1e-6).reshape(n, heads * hd)
+    assert np.array_equal(y, normed)  # cos 1, sin 0: the norm alone
+    quarter = np.tile(np.concatenate([np.zeros(pair), np.ones(pair)]).astype(np.float32), (n, 1))
+    z = orc.head_norm_rope(x, heads * hd, w, quarter, hd, heads, hd, n, 1e-6)
+    nr = normed.reshape(n, heads, 2, pair)
+    assert np.array_equal(z.reshape(n, heads, 2, pair)[:, :, 0], -nr[:, :, 1])  # j <- -(j + hd/2)
+    assert np.array_equal(z.reshape(n, heads, 2, pair)[:, :, 1], nr[:, :, 0])
+    ang = rng.uniform(0, 6.3, (n, pair))
+    table = np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
+    r = orc.head_norm_rope(x, heads * hd, w, table, hd, heads, hd, n, 1e-6).reshape(n, heads, 2, pair)
+    # a rotation keeps each pair's length
+    assert np.allclose((r ** 2).sum(axis=2), (nr ** 2).sum(axis=2), rtol=1e-5)
+
+
+def test_short_conv_closed_forms(orc):
+    width, k, n = 5, 3, 6
+    rng = np.random.default_rng(5)
+    bcx = rng.standard_normal((n, 3, width)).astype(np.float32)
+    weight = rng.standard_normal((width, k)).astype(np.float32)
+    hist = rng.standard_normal((k - 1, width)).astype(np.float32)
+    y, h2 = orc.short_conv(bcx, weight, hist, width, k, n)
+    # z = B * X; a causal conv of [history; z] with the kernel reversed; y = C * conv
+    z = (bcx[:, 0] * bcx[:, 2]).astype(np.float64)
+    full = np.concatenate([hist.astype(np.float64), z])
+    for ch in range(width):
+        conv = np.convolve(full[:, ch], weight[ch, ::-1].astype(np.float64), mode="valid")
+        assert np.allclose(y.reshape(n, width)[:, ch], bcx[:, 1, ch] * conv, rtol=1e-5, atol=1e-6)
+    assert np.array_equal(h2, z[-(k - 1):].astype(np.float32))  # the last k - 1 z
+    # two calls carrying the history equal one call
+    y1, hmid = orc.short_conv(bcx[:2], weight, hist, width, k, 2)
+    y2, hend = orc.short_conv(bcx[2:], weight, hmid, width, k, n - 2)
+    assert np.array_equal(np.concatenate([y1, y2]), y) and np.array_equal(hend, h2)
+
+
+def test_attention_closed_forms(orc):
+    heads, kv, hd, pos, n = 4, 2, 8, 5, 2
+    rng = np.random.default_rng(6)
+    total = pos + n
+    q = rng.standard_normal(n * heads * hd).astype(np.float32)
+    vals = rng.standard_normal((total, kv * hd)).astype(np.float32)
+    same = np.tile(rng.standard_normal(kv * hd).astype(np.float32), (total, 1))
+    out = orc.attention(q, same, vals, None, pos, n, heads, kv, hd).reshape(n, heads, hd)
+    for t in range(n):  # equal keys: the mean of the visible values, KV head h // 2
+        for h in range(heads):
+            want = vals[: pos + t + 1, (h // 2) * hd:(h // 2 + 1) * hd].astype(np.float64).mean(0)
+            assert np.allclose(out[t, h], want, rtol=1e-5, atol=1e-6)
+    keys = rng.standard_normal((total, kv * hd)).astype(np.float32)
+    one = orc.attention(q, keys, vals, None, pos, n, heads, kv, hd, window=1).reshape(n, heads, hd)
+    for t in range(n):  # window 1: the token's own value
+        for h in range(heads):
+            assert np.allclose(one[t, h], vals[pos + t, (h // 2) * hd:(h // 2 + 1) * hd], rtol=1e-6)
+    gate = rng.standard_normal(n * heads).astype(np.float32)
+    gated = orc.attention(q, keys, vals, gate, pos, n, heads, kv, hd).reshape(n, heads, hd)
+    plain = orc.attention(q, keys, vals, None, pos, n, heads, kv, hd).reshape(n, heads, hd)
+    sig = 1.0 / (1.0 + np.exp(-gate.astype(np.float64).reshape(n, heads, 1)))
+    assert np.allclose(gated, plain * sig, rtol=1e-6, atol=1e-7)
+    # a window of 3 ignores the keys and values before it
+    k2, v2 = keys.copy(), vals.copy()
+    k2[:pos + 1 - 3] = 100.0
+    v2[:pos + 1 - 3] = -100.0
+    a = orc.attention(q, keys, vals, None, pos, n, heads, kv, hd, window=3)
+    b = orc.attention(q, k2, v2, None, pos, n, heads, kv, hd, window=3)
+    assert np.array_equal(a, b)
+    # two keys: weights in the ratio exp((q.k0 - q.k1) / sqrt(hd))
+    qq = rng.standard_normal(kv * hd).astype(np.float32)[:hd]
+    kk = rng.standard_normal((2, hd)).astype(np.float32)
+    vv = rng.standard_normal((2, hd)).astype(np.float32)
+    o = orc.attention(qq, kk, vv, None, 1, 1, 1, 1, hd)
+    s = kk.astype(np.float64) @ qq.astype(np.float64) / np.sqrt(hd)
+    p = np.exp(s - s.max()) / np.exp(s - s.max()).sum()
+    assert np.allclose(o, p @ vv.astype(np.float64), rtol=1e-5, atol=1e-6)
+
+
+def test_steer_closed_forms(orc):
+    rng = np.random.default_rng(7)
+    v = rng.standard_normal(64)
+    v = (v / np.linalg.norm(v)).astype(np.float32)
+    u = rng.standard_normal(64)
+    u = (u - (u @ v) * v).astype(np.float32)  # orthogonal to v
+    x = np.stack([u + 3.0 * v, u - 0.5 * v]).astype(np.float32)
+    assert np.array_equal(orc.steer(x, v, 0, 1.0), x + v)
+    removed = orc.steer(x, v, 1, 1.0)
+    assert np.allclose(removed, np.stack([u, u]), atol=1e-5)
+    half = orc.steer(x, v, 1, 0.5)
+    assert np.allclose(half[0], u + 1.5 * v, atol=1e-5)
