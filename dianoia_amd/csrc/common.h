@@ -14,6 +14,7 @@ constexpr int kBlock = 32;  // values per Q8/Q4 block (lab_native.c:405, :902)
 constexpr int kQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
 constexpr int kQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
 constexpr int kHalfRowMirror = 0x141; // lane i <- lane 7-i within 8 lanes
+constexpr int kRowMirror = 0x140;     // lane i <- lane 15-i within 16 lanes
 
 template <int Ctrl>
 DNX_DEV int dpp(int v) {

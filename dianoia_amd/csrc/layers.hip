@@ -223,17 +223,20 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ keys,
 
 // Long contexts with few (head, token) pairs (decode) split the keys: each
 // workgroup of attention_split_kernel takes split_keys(hd) keys of one
-// (head, token) and writes its max m, its exponentials' sum l (relative to
-// m) and its unnormalised value sums o[hd] (a row of hd + 4 floats: m, l,
-// two unused, o, so o is 16-byte aligned); attention_combine_kernel
-// rescales the splits to their common max and adds them in split order
-// (deterministic): O = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M). The
-// same softmax as attention_kernel, summed in another order.
+// token for G query heads that share one KV head, and writes for each head
+// its max m, its exponentials' sum l (relative to m) and its unnormalised
+// value sums o[hd] (a row of hd + 4 floats: m, l, two unused, o, so o is
+// 16-byte aligned); attention_combine_kernel rescales the splits to their
+// common max and adds them in split order (deterministic):
+// O = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M). The same softmax as
+// attention_kernel, summed in another order.
 // A split puts hd / 4 lanes on a key row (one 16-byte piece each,
 // coalesced), 256 / (hd / 4) keys per workgroup step, and at most 16 steps:
 // every key and value load of the split is issued at its start, so it
-// waits for memory once. Dots end in a butterfly over the key's lanes;
-// value sums in per-lane float4 partials added in a fixed order.
+// waits for memory once, and each row is read once for the G heads (GQA).
+// Dots end in a butterfly over the key's lanes; wave w takes the softmax
+// statistics of heads w, w + 4, ...; value sums go to per-lane float4
+// partials added in a fixed order.
 constexpr int kSplitSteps = 16;
 constexpr int kSplitMaxKeys = 256;
 
@@ -243,25 +246,46 @@ int split_keys(int hd) {
   return k < kSplitMaxKeys ? k : kSplitMaxKeys;
 }
 
-__global__ void __launch_bounds__(kThreads)
+// Sum over aligned groups of LT lanes (a power of two up to 32); every lane
+// of a group gets the group's sum. DPP moves up to 16 lanes (no LDS round
+// trip), a swizzle for 32.
+template <int LT>
+DNX_DEV float group_sum(float v) {
+  if constexpr (LT >= 2) v += dppf<kQuadXor1>(v);
+  if constexpr (LT >= 4) v += dppf<kQuadXor2>(v);
+  if constexpr (LT >= 8) v += dppf<kHalfRowMirror>(v);
+  if constexpr (LT >= 16) v += dppf<kRowMirror>(v);
+  if constexpr (LT >= 32) v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+  static_assert(LT <= 32, "group_sum: at most 32 lanes");
+  return v;
+}
+
+// G query heads per workgroup; LT lanes per key when fixed at compile time
+// (hd = 4 * LT), 0 for any hd.
+template <int G, int LT>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
 attention_split_kernel(const float* __restrict__ q, const float* __restrict__ keys,
                        const float* __restrict__ values, float* __restrict__ ws, int position,
                        int heads, int kv_dim, int group, int hd, int window, float scale,
                        int splits, int keys_per_split) {
-  __shared__ float scores[kSplitMaxKeys];
-  __shared__ float4 part[kThreads];
-  __shared__ float scratch[kWaves];
-  const int head = blockIdx.x, token = blockIdx.y, split = blockIdx.z, tid = threadIdx.x;
+  __shared__ float scores[G][kSplitMaxKeys];
+  __shared__ float4 part[G][kThreads];
+  __shared__ float stat[G][2];
+  const int h0 = blockIdx.x * G, token = blockIdx.y, split = blockIdx.z, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int pos = position + token;
   const int start = window > 0 && pos >= window ? pos - window + 1 : 0;
   const int count = pos - start + 1;
   const int k0 = split * keys_per_split;
   const int nk = max(0, min(keys_per_split, count - k0));   // this split's keys
-  const int kvo = head / group * hd;
-  const int L = hd / 4, per = 64 / L, step = kWaves * per;  // lanes per key, keys per step
+  const int kvo = h0 / group * hd;
+  const int L = LT > 0 ? LT : hd / 4;                      // lanes per key
+  const int per = 64 / L, step = kWaves * per;               // keys per wave, per step
   const int c = lane % L, kb = wave * per + lane / L;       // this lane's first key
-  const float4 qr = *(const float4*)(q + ((size_t)token * heads + head) * hd + 4 * c);
+  float4 qr[G];
+#pragma unroll
+  for (int g = 0; g < G; g++)
+    qr[g] = *(const float4*)(q + ((size_t)token * heads + h0 + g) * hd + 4 * c);
   // Resources over this split's nk key rows: a row past them lies wholly
   // beyond the range (its offset is at least nk rows) and reads zeros.
   const size_t first = (size_t)(start + k0) * kv_dim + kvo;
@@ -276,88 +300,181 @@ attention_split_kernel(const float* __restrict__ q, const float* __restrict__ ke
 #pragma unroll
   for (int j = 0; j < kSplitSteps; j++)
     vv[j] = buffer_load_f4(vrs, (kb + j * step) * kv_dim * 4 + 16 * c);
+  // Dots in batches of kBatch steps x G heads: each butterfly stage issues
+  // the batch's lane exchanges together and waits once (L is a run-time
+  // count, so per-dot loops would wait on every exchange).
+  constexpr int kBatch = 4;
+#pragma unroll
+  for (int j0 = 0; j0 < kSplitSteps; j0 += kBatch) {
+    float d[kBatch][G];
+#pragma unroll
+    for (int u = 0; u < kBatch; u++)
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        const float4 k4 = kv[j0 + u];
+        d[u][g] = qr[g].x * k4.x + qr[g].y * k4.y + qr[g].z * k4.z + qr[g].w * k4.w;
+      }
+    if constexpr (LT > 0) {
+#pragma unroll
+      for (int u = 0; u < kBatch; u++)
+#pragma unroll
+        for (int g = 0; g < G; g++) d[u][g] = group_sum<LT>(d[u][g]);
+    } else {
+      for (int o = L / 2; o > 0; o >>= 1) {
+#pragma unroll
+        for (int u = 0; u < kBatch; u++)
+#pragma unroll
+          for (int g = 0; g < G; g++) d[u][g] += __shfl_xor(d[u][g], o);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+      const int i = kb + (j0 + u) * step;
+      if (i < nk && c == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++) scores[g][i] = d[u][g] * scale;
+      }
+    }
+  }
+  __syncthreads();
+  for (int g = wave; g < G; g += kWaves) {  // one wave per head: no block barrier
+    constexpr int kPerLane = kSplitMaxKeys / 64;
+    float v[kPerLane];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kPerLane; u++) {
+      const int i = u * 64 + lane;
+      v[u] = i < nk ? scores[g][i] : -INFINITY;
+      mx = fmaxf(mx, v[u]);
+    }
+    mx = wave_max(mx);
+    float sum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kPerLane; u++) {
+      const int i = u * 64 + lane;
+      if (i < nk) {
+        const float e = expf(v[u] - mx);
+        scores[g][i] = e;
+        sum += e;
+      }
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) {
+      stat[g][0] = mx;   // -inf for a split past the token's keys (l = 0, o = 0)
+      stat[g][1] = sum;
+    }
+  }
+  __syncthreads();
+  float4 acc[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) acc[g] = zero;
 #pragma unroll
   for (int j = 0; j < kSplitSteps; j++) {
     const int i = kb + j * step;
-    float d = qr.x * kv[j].x + qr.y * kv[j].y + qr.z * kv[j].z + qr.w * kv[j].w;
-    for (int o = L / 2; o > 0; o >>= 1) d += __shfl_xor(d, o);
-    if (i < nk && c == 0) scores[i] = d * scale;
-  }
-  __syncthreads();
-  const float m = block_max(tid < nk ? scores[tid] : -INFINITY, scratch);
-  float e = 0.0f;
-  if (tid < nk) {
-    e = expf(scores[tid] - m);
-    scores[tid] = e;
-  }
-  const float l = block_sum(e, scratch);  // its barriers also publish the exponentials
-  float4 acc = zero;
 #pragma unroll
-  for (int j = 0; j < kSplitSteps; j++) {
-    const int i = kb + j * step;
-    const float p = i < nk ? scores[i] : 0.0f;
-    acc.x += p * vv[j].x;
-    acc.y += p * vv[j].y;
-    acc.z += p * vv[j].z;
-    acc.w += p * vv[j].w;
+    for (int g = 0; g < G; g++) {
+      const float p = i < nk ? scores[g][i] : 0.0f;
+      acc[g].x += p * vv[j].x;
+      acc[g].y += p * vv[j].y;
+      acc[g].z += p * vv[j].z;
+      acc[g].w += p * vv[j].w;
+    }
   }
-  part[tid] = acc;
+#pragma unroll
+  for (int g = 0; g < G; g++) part[g][tid] = acc[g];
   __syncthreads();
-  float* out = ws + (((size_t)token * heads + head) * splits + split) * (hd + 4);
-  if (tid < L) {  // dimensions 4c..4c+3: the (wave, key-in-step) partials in order
+  for (int e = tid; e < G * L; e += kThreads) {
+    // Head g, dimensions 4cc..4cc+3: the (wave, key-in-step) partials in order.
+    const int g = e / L, cc = e - g * L;
     float4 t = zero;
     for (int w = 0; w < kWaves; w++)
       for (int s2 = 0; s2 < per; s2++) {
-        const float4 p4 = part[w * 64 + s2 * L + tid];
+        const float4 p4 = part[g][w * 64 + s2 * L + cc];
         t.x += p4.x;
         t.y += p4.y;
         t.z += p4.z;
         t.w += p4.w;
       }
-    *(float4*)(out + 4 + 4 * tid) = t;
-  }
-  if (tid == 0) {
-    out[0] = m;   // -inf for a split past the token's keys (l = 0, o = 0)
-    out[1] = l;
+    float* out = ws + (((size_t)token * heads + h0 + g) * splits + split) * (hd + 4);
+    *(float4*)(out + 4 + 4 * cc) = t;
+    if (cc == 0) {
+      out[0] = stat[g][0];
+      out[1] = stat[g][1];
+    }
   }
 }
 
-// The splits of one (head, token): their maxima and rescaling factors go
-// through LDS once (dynamic: `splits` floats), then each dimension's sum
-// over the splits with 8 loads in flight.
+template <int G>
+void launch_split(dim3 grid, hipStream_t stream, const float* q, const float* keys,
+                  const float* values, float* ws, int position, int heads, int kv_dim, int group,
+                  int hd, int window, float scale, int splits, int kps) {
+  auto kernel = hd == 128 ? attention_split_kernel<G, 32>
+              : hd == 64  ? attention_split_kernel<G, 16>
+                          : attention_split_kernel<G, 0>;
+  hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, stream, q, keys, values, ws, position,
+                     heads, kv_dim, group, hd, window, scale, splits, kps);
+}
+
+// The splits of one (head, token). Thread t takes dimension t % hd of the
+// splits s = t / hd + P j (P = 256 / hd threads per dimension). Its first
+// kChunk value loads and the split statistics are issued together, so a
+// short context waits for memory once; the rescaling factors e^(m_s - M)
+// go through LDS (dynamic: `splits` floats), and the P partial sums of a
+// dimension are added in a fixed order.
 __global__ void __launch_bounds__(kThreads)
 attention_combine_kernel(const float* __restrict__ ws, const float* __restrict__ gate,
                          float* __restrict__ out, int heads, int hd, int splits) {
   extern __shared__ float fs[];   // [splits] e^(m_s - M), 0 for empty splits
   __shared__ float scratch[kWaves];
+  __shared__ float red[kThreads];
+  constexpr int kChunk = 16;
   const int head = blockIdx.x, token = blockIdx.y, tid = threadIdx.x;
-  const float* w = ws + ((size_t)token * heads + head) * splits * (hd + 4);
-  float mx = -INFINITY;
-  for (int s = tid; s < splits; s += kThreads) mx = fmaxf(mx, w[(size_t)s * (hd + 4)]);
+  const int row = hd + 4;
+  const float* w = ws + ((size_t)token * heads + head) * splits * row;
+  // Every offset past the (head, token)'s rows reads zero.
+  const i32x4 rs = buffer_rsrc(w, (uint32_t)splits * (uint32_t)row * 4u);
+  const int P = kThreads / hd, d = tid % hd, part = tid / hd;
+  float v[kChunk];
+#pragma unroll
+  for (int u = 0; u < kChunk; u++) {
+    const int sp = part + u * P;
+    v[u] = __int_as_float(dnx_raw_buffer_load_i32(rs, (sp * row + 4 + d) * 4, 0, 0));
+  }
+  const int s0 = tid;   // the first split whose statistics this thread reads
+  const float m0 = __int_as_float(dnx_raw_buffer_load_i32(rs, s0 * row * 4, 0, 0));
+  const float l0 = __int_as_float(dnx_raw_buffer_load_i32(rs, (s0 * row + 1) * 4, 0, 0));
+  float mx = s0 < splits ? m0 : -INFINITY;
+  for (int s = s0 + kThreads; s < splits; s += kThreads) mx = fmaxf(mx, w[(size_t)s * row]);
   mx = block_max(mx, scratch);
   float lp = 0.0f;
-  for (int s = tid; s < splits; s += kThreads) {
-    const float ms = w[(size_t)s * (hd + 4)];
+  if (s0 < splits) {
+    const float f = m0 != -INFINITY ? expf(m0 - mx) : 0.0f;
+    fs[s0] = f;
+    lp = l0 * f;
+  }
+  for (int s = s0 + kThreads; s < splits; s += kThreads) {
+    const float ms = w[(size_t)s * row];
     const float f = ms != -INFINITY ? expf(ms - mx) : 0.0f;
     fs[s] = f;
-    lp += w[(size_t)s * (hd + 4) + 1] * f;
+    lp += w[(size_t)s * row + 1] * f;
   }
   const float l = block_sum(lp, scratch);  // its barriers also publish fs
-  const size_t qo = ((size_t)token * heads + head) * hd;
-  const float g = gate != nullptr ? 1.0f / (1.0f + expf(-gate[(size_t)token * heads + head])) : 1.0f;
-  for (int d = tid; d < hd; d += kThreads) {
-    const float* o = w + 4 + d;
-    float acc = 0.0f;
-    int s = 0;
-    for (; s + 8 <= splits; s += 8) {
-      float v[8];
+  float acc = 0.0f;
 #pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = o[(size_t)(s + u) * (hd + 4)];
-#pragma unroll
-      for (int u = 0; u < 8; u++) acc += v[u] * fs[s + u];
-    }
-    for (; s < splits; s++) acc += o[(size_t)s * (hd + 4)] * fs[s];
-    out[qo + d] = gate != nullptr ? (acc / l) * g : acc / l;
+  for (int u = 0; u < kChunk; u++) {
+    const int sp = part + u * P;
+    if (sp < splits) acc += v[u] * fs[sp];
+  }
+  for (int sp = part + kChunk * P; sp < splits; sp += P) acc += w[(size_t)sp * row + 4 + d] * fs[sp];
+  red[tid] = acc;
+  __syncthreads();
+  if (part == 0) {
+    float t = red[d];
+    for (int p2 = 1; p2 < P; p2++) t += red[p2 * hd + d];
+    const size_t qo = ((size_t)token * heads + head) * hd;
+    const float g =
+        gate != nullptr ? 1.0f / (1.0f + expf(-gate[(size_t)token * heads + head])) : 1.0f;
+    out[qo + d] = gate != nullptr ? (t / l) * g : t / l;
   }
 }
 
@@ -492,11 +609,23 @@ int dnx_attention(const float* q, const float* keys, const float* values, const 
       splits <= 16000 && ws_bytes <= ((size_t)1 << 30) && kv_heads * hd <= (1 << 17)) {
     float* ws = attention_workspace(ws_bytes);
     if (ws == nullptr) return DNX_ENOMEM;
-    hipLaunchKernelGGL(attention_split_kernel,
-                       dim3((unsigned)heads, (unsigned)n, (unsigned)splits),
-                       dim3(kThreads), 0, (hipStream_t)stream, q, keys, values, ws, (int)position,
-                       (int)heads, (int)(kv_heads * hd), (int)(heads / kv_heads), (int)hd,
-                       (int)window, scale, (int)splits, kps);
+    // G query heads per workgroup: the largest of 8, 4, 2, 1 dividing the
+    // heads per KV head.
+    const int group = (int)(heads / kv_heads);
+    const int G = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    const dim3 grid((unsigned)(heads / G), (unsigned)n, (unsigned)splits);
+    const hipStream_t st = (hipStream_t)stream;
+    const int kv_dim = (int)(kv_heads * hd);
+    switch (G) {
+      case 8: launch_split<8>(grid, st, q, keys, values, ws, (int)position, (int)heads, kv_dim,
+                              group, (int)hd, (int)window, scale, (int)splits, kps); break;
+      case 4: launch_split<4>(grid, st, q, keys, values, ws, (int)position, (int)heads, kv_dim,
+                              group, (int)hd, (int)window, scale, (int)splits, kps); break;
+      case 2: launch_split<2>(grid, st, q, keys, values, ws, (int)position, (int)heads, kv_dim,
+                              group, (int)hd, (int)window, scale, (int)splits, kps); break;
+      default: launch_split<1>(grid, st, q, keys, values, ws, (int)position, (int)heads, kv_dim,
+                               group, (int)hd, (int)window, scale, (int)splits, kps); break;
+    }
     if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
     hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)heads, (unsigned)n),
                        dim3(kThreads), (size_t)splits * 4, (hipStream_t)stream, ws, gate, out,

@@ -84,6 +84,9 @@ def test_short_conv_bit_exact(gpu_ready, orc, width, k, n):
     (8, 2, 64, 3000, 3, 1000, True),   # split keys: window, gate, 3 tokens
     (32, 8, 128, 300, 4, 0, False),    # split keys, the tokens' counts differ
     (1, 1, 16, 20000, 1, 0, False),    # beyond one workgroup's LDS: split
+    (32, 4, 64, 2500, 1, 0, True),     # split keys, 8 query heads per KV head
+    (12, 2, 128, 1500, 2, 0, False),   # split keys, 6 per KV head: pairs of heads
+    (6, 2, 32, 900, 1, 300, False),    # split keys, 3 per KV head: one head each
 ])
 def test_attention(gpu_ready, orc, heads, kv, hd, pos, n, window, gated):
     rng = np.random.default_rng(heads + hd + pos + n)
