@@ -402,6 +402,37 @@ def bench_loaders(torch, D, timer, steps):
             "bytes": {"bf16_to_q4": q4_bytes, "q6k_to_q8": q6k_bytes}}
 
 
+def bench_cache_wrap(reps=3):
+    """Weight loading from disk to HBM (gpu.dart:938-979): a 324 MiB
+    LFM3Q8C1 cache (eight 6144 x 6144 Q8 matrices, written to a temporary
+    file, so its pages are in the page cache) opened, mapped and placed in
+    HBM by GpuLinear.wrap_cache (lab_gpu_wrap: one pageable host-to-device
+    copy). Host wall-clock per wrap; PCIe-bound, not an HBM figure."""
+    import tempfile
+    from dianoia_amd.formats import QuantMatrix
+    from dianoia_amd.gpu import GpuLinear
+    from dianoia_amd.q8_cache import Q8Cache
+    rows = cols = 6144
+    m = QuantMatrix.q8(np.full((rows, cols), 3, np.int8),
+                       np.full(rows * cols // 32, 0.5, np.float32))
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "lfm3-q8.cache")
+        Q8Cache.write(path, "bench", {f"m{i}": m for i in range(8)})
+        nbytes = os.path.getsize(path) - (1 << 20)
+        times = []
+        for _ in range(reps):
+            cache = Q8Cache.open(path, "bench")
+            g = GpuLinear.start()
+            t0 = time.perf_counter()
+            g.wrap_cache(cache)
+            times.append(time.perf_counter() - t0)
+            g.dispose()
+            cache.close()
+    best = min(times)
+    return {"cache_bytes": nbytes, "wrap_ms": best * 1e3, "wrap_gbps": nbytes / best / 1e9,
+            "reps": reps}
+
+
 # ------------------------------------------------------------------ CPU
 
 def cpu_baseline(synth, seconds):
@@ -663,6 +694,8 @@ def main():
         print("bench: layer steps", file=sys.stderr, flush=True)
         configs["layer_steps"] = bench_layers(torch, D, timer, args.steps)
         torch.cuda.empty_cache()
+        print("bench: weight cache to HBM", file=sys.stderr, flush=True)
+        configs["weight_cache_wrap"] = bench_cache_wrap()
     cpu = None
     if not args.no_cpu:
         print("bench: cpu baseline", file=sys.stderr, flush=True)

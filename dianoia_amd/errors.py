@@ -4,6 +4,8 @@
 invalid block data) and ``StateError`` for use after dispose or a failed GPU
 command buffer, where the reference's Dart throws the errors of those names
 (gpu.dart:1264-1267, 1327-1357; native.dart:633-641, 717-721).
+``FormatException`` is raised for a weight cache that cannot be trusted
+(q8_cache.dart:63-104).
 """
 
 
@@ -12,4 +14,8 @@ class ArgumentError(ValueError):
 
 
 class StateError(RuntimeError):
+    pass
+
+
+class FormatException(ValueError):
     pass

@@ -23,6 +23,7 @@ import numpy as np
 from . import _lib
 from .errors import ArgumentError, StateError
 from .formats import QuantMatrix
+from .q8_cache import Q8Cache
 
 
 class _Buffer:
@@ -58,6 +59,7 @@ class _Matrix:
     rows: int
     cols: int
     in_cols: int  # columns the caller's inputs have (cols may be padded)
+    owns: bool = True  # False: a segment of a wrapped cache, shared and kept
 
     def encode(self, lib, x: int, y: int, y_offset: int, n: int, x_offset: int = 0) -> None:
         f = lib.lab_gpu_enc_matmul_q4 if self.q4 else lib.lab_gpu_enc_matmul_q8
@@ -88,6 +90,7 @@ class GpuLinear:
         self._y: _Buffer | None = None
         self._aux: dict[str, _Buffer] = {}
         self._disposed = False
+        self.segments = 0  # buffers made by wrap_cache
 
     @staticmethod
     def start() -> "GpuLinear | None":
@@ -118,6 +121,51 @@ class GpuLinear:
         view[scales_at: scales_at + len(scales)] = scales
         self._replace(name, _Matrix(matrix.format == "q4", handle, 0, scales_at, matrix.rows,
                                     matrix.cols, matrix.cols))
+
+    def wrap_cache(self, cache: Q8Cache, limit: int | None = None) -> dict[str, tuple[int, int]]:
+        """Places an open weight cache in HBM and registers its matrices
+        under their names (gpu.dart:938-979, ``_wrapWeights``).
+
+        One ``lab_gpu_wrap`` per segment: matrices in file order, a segment
+        starting at the 16 KiB page holding its first matrix's values and
+        taking whole matrices while it stays within ``limit`` bytes
+        (``lab_gpu_max_buffer_length()`` unless given). Returns each
+        matrix's buffer handle and that buffer's file offset. Raises
+        ``StateError`` when one matrix alone exceeds the limit or a wrap
+        fails."""
+        self._check_open()
+        page = 16384
+        if limit is None:
+            limit = int(self._lib.lab_gpu_max_buffer_length())
+        matrices = sorted(((name, cache.offsets(name, r, c), r, c) for name, r, c in cache.shapes),
+                          key=lambda t: t[1]["qs"])
+        result: dict[str, tuple[int, int]] = {}
+        pending: list = []
+        start = end = 0
+        for i in range(len(matrices) + 1):
+            item = matrices[i] if i < len(matrices) else None
+            if pending and (item is None or item[1]["end"] - start > limit):
+                nbytes = min(end, cache.file.length) - start
+                h = int(self._lib.lab_gpu_wrap(cache.file.address + start, nbytes))
+                if h < 0:
+                    raise StateError("wrapping the weight cache failed")
+                self._owned.append(h)
+                self.segments += 1
+                for name, o, r, c in pending:
+                    result[name] = (h, start)
+                    self._replace(name, _Matrix(o["format"] == "q4", h, o["qs"] - start,
+                                                o["scales"] - start, r, c, c, owns=False))
+                pending = []
+            if item is None:
+                break
+            name, o = item[0], item[1]
+            if not pending:
+                start = o["qs"] // page * page
+            if o["end"] - start > limit:
+                raise StateError(f"{name} alone exceeds the largest GPU buffer")
+            pending.append(item)
+            end = o["end"]
+        return result
 
     def upload_bf16(self, name: str, bf16: np.ndarray, rows: int, cols: int,
                     rows_pad: int | None = None, fmt: str = "q8") -> None:
@@ -344,7 +392,7 @@ class GpuLinear:
 
     def _replace(self, name: str, m: _Matrix) -> None:
         previous = self._matrices.get(name)
-        if previous is not None:
+        if previous is not None and previous.owns:
             self._owned.remove(previous.buffer)
             self._lib.lab_gpu_release(previous.buffer)
         self._matrices[name] = m
