@@ -369,8 +369,9 @@ def bench_loaders(torch, D, timer, steps):
     """The other load-time converters (beyond the north star's BF16 -> Q8):
     BF16 -> Q4 (lab_quantize_q4 after _widenBf16) on a 32768 x 4096 matrix
     (256 MiB of BF16), and the Q6_K -> Q8 adapter (dequantizeQ6K +
-    lab_quantize_q8, gguf.dart:402-414) at the LM-head shape 151936 x 2048.
-    Inputs are generated on the GPU; both kernels are HBM-bound."""
+    lab_quantize_q8, gguf.dart:402-414) at the LM-head shape 151936 x 2048,
+    and the GGUF Q8_0 split (splitQ8_0, gguf.dart:270-282) at that shape.
+    Inputs are generated on the GPU; the kernels are HBM-bound."""
     gen = torch.Generator(device="cuda").manual_seed(5)
     wbig = (torch.randn((32768, 4096), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
     wbig = wbig.view(torch.int16)
@@ -384,6 +385,9 @@ def bench_loaders(torch, D, timer, steps):
     blocks[:, 208:210] = d.view(torch.uint8).view(-1, 2)
     q8 = torch.empty((rows, cols), dtype=torch.int8, device="cuda")
     s8 = torch.empty((rows, cols // 32), device="cuda")
+    # GGUF Q8_0 blocks of the same LM head, split on the GPU (splitQ8_0).
+    count = rows * cols // 32
+    gguf = torch.randint(0, 256, (count * 34,), dtype=torch.uint8, device="cuda", generator=gen)
 
     def q4_(i):
         D.quantize_q4_bf16(wbig, q4, d4, 32768, 4096)
@@ -391,15 +395,22 @@ def bench_loaders(torch, D, timer, steps):
     def q6k_(i):
         D.q6k_to_q8(blocks, q8, s8, rows, cols)
 
-    means = timer.kernel_means([q4_, q6k_], max(10, steps // 4))
+    def split_(i):
+        D.split_q8_0(gguf, q8, s8, count)
+
+    means = timer.kernel_means([q4_, q6k_, split_], max(10, steps // 4))
     q4_bytes = 32768 * 4096 * 2 + 32768 * 2048 + 32768 * 128 * 2
     q6k_bytes = rows * cols // 256 * 210 + rows * cols + rows * (cols // 32) * 4
-    del wbig, blocks
+    split_bytes = count * 34 + count * 36
+    del wbig, blocks, gguf
     return {"bf16_to_q4_32768x4096_ms": means[0],
             "bf16_to_q4_32768x4096_gbps": q4_bytes / means[0] / 1e6,
             "q6k_to_q8_151936x2048_ms": means[1],
             "q6k_to_q8_151936x2048_gbps": q6k_bytes / means[1] / 1e6,
-            "bytes": {"bf16_to_q4": q4_bytes, "q6k_to_q8": q6k_bytes}}
+            "split_q8_0_151936x2048_ms": means[2],
+            "split_q8_0_151936x2048_gbps": split_bytes / means[2] / 1e6,
+            "bytes": {"bf16_to_q4": q4_bytes, "q6k_to_q8": q6k_bytes,
+                      "split_q8_0": split_bytes}}
 
 
 def bench_cache_wrap(reps=3):

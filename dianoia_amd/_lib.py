@@ -50,6 +50,8 @@ SIGNATURES = {
     "lab_gpu_enc_quantize_q4": ([_i64] * 8, None),
     "lab_gpu_enc_quantize_q4_bf16": ([_i64] * 8, None),
     "lab_gpu_enc_q6k_to_q8": ([_i64] * 8, None),
+    "lab_gpu_enc_split_q8_0": ([_i64] * 8, None),
+    "lab_gpu_enc_split_q4_0": ([_i64] * 8, None),
     "lab_gpu_enc_argmax": ([_i64] * 5, None),
     "lab_gpu_enc_gelu": ([_i64] * 3, None),
     "lab_gpu_set_profiling": ([_i64], None),
@@ -69,6 +71,8 @@ SIGNATURES = {
     "dnx_quantize_q8_bf16": ([_p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_quantize_q4": ([_p, _p, _p, _i64, _i64, _p], _i32),
     "dnx_q6k_to_q8": ([_p, _p, _p, _i64, _i64, _p], _i32),
+    "dnx_split_q8_0": ([_p, _p, _p, _i64, _p], _i32),
+    "dnx_split_q4_0": ([_p, _p, _p, _i64, _p], _i32),
     "dnx_quantize_q4_bf16": ([_p, _p, _p, _i64, _i64, _p], _i32),
     "dnx_gemv_q8": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemv_q4": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),

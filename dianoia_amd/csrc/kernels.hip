@@ -445,6 +445,90 @@ int launch_quantizer(const void* src, void* qs, void* scales, int64_t rows, int6
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 
+// GGUF Q8_0 / Q4_0 blocks -> the engine's layout (splitQ8_0, gguf.dart:
+// 270-282; splitQ4_0, :208-218). A GGUF block is its fp16 d, then the
+// values: 34 bytes (Q8_0: 32 int8) or 18 (Q4_0: 16 nibble bytes, whose
+// order both layouts share). Block b's values start at byte 34b + 2
+// (18b + 2): 4-byte aligned for odd b, 2 mod 4 for even b. A lane makes one
+// 16-byte piece of values (Q8_0: two per block, Q4_0: one) from a 16-byte
+// load at the dword at or below the piece and a 2-byte load after it,
+// realigned with v_alignbyte by 0 or 2 bytes (no branch); neither load
+// reaches past its block, so the last block of a buffer that ends with it
+// reads whole. The lane of a block's first piece also writes the scale:
+// widened to fp32 for Q8 (exact; any NaN becomes 0x7FC00000, as the
+// reference's halfToDouble makes it), the fp16 bits for Q4.
+constexpr int kSplitItems = 4;
+
+template <bool kQ4>
+__global__ void __launch_bounds__(kThreads)
+split_gguf_kernel(const uint8_t* __restrict__ blocks, uint8_t* __restrict__ qs,
+                  void* __restrict__ scales, int count, uint32_t bytes) {
+  constexpr int kBytes = kQ4 ? 18 : 34;
+  constexpr int kPieces = kQ4 ? 1 : 2;
+  const i32x4 rs = buffer_rsrc(blocks, bytes);
+  const int pieces = count * kPieces;
+  const int stride = gridDim.x * kThreads * kSplitItems;
+  for (int p0 = blockIdx.x * kThreads * kSplitItems + threadIdx.x; p0 < pieces; p0 += stride) {
+    uint4 lo[kSplitItems];
+    uint32_t hi[kSplitItems], d[kSplitItems];
+#pragma unroll
+    for (int j = 0; j < kSplitItems; j++) {  // every load in flight at once
+      const int p = p0 + j * kThreads, b = p / kPieces, h = p % kPieces;
+      const int s = b * kBytes + 2 + 16 * h;
+      const bool in = p < pieces;
+      lo[j] = buffer_load16(rs, in ? (s & ~3) : kFar);
+      hi[j] = (uint16_t)dnx_raw_buffer_load_i16(rs, in ? (s & ~3) + 16 : kFar, 0, 0);
+      d[j] = (uint16_t)dnx_raw_buffer_load_i16(rs, in && h == 0 ? b * kBytes : kFar, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < kSplitItems; j++) {
+      const int p = p0 + j * kThreads, b = p / kPieces, h = p % kPieces;
+      if (p >= pieces) continue;
+      const uint32_t sh = (uint32_t)((b * kBytes + 2) & 3);   // 0 or 2
+      uint4 out;
+      out.x = __builtin_amdgcn_alignbyte(lo[j].y, lo[j].x, sh);
+      out.y = __builtin_amdgcn_alignbyte(lo[j].z, lo[j].y, sh);
+      out.z = __builtin_amdgcn_alignbyte(lo[j].w, lo[j].z, sh);
+      out.w = __builtin_amdgcn_alignbyte(hi[j], lo[j].w, sh);
+      *(uint4*)(qs + (size_t)p * 16) = out;
+      if (h == 0) {
+        if (kQ4) {
+          ((uint16_t*)scales)[b] = (uint16_t)d[j];
+        } else {
+          // halfToDouble (native.dart:871-880) gives Dart's double.nan for
+          // every NaN pattern: 0x7FC00000 once stored as a float.
+          const float f = half_bits_to_float((uint16_t)d[j]);
+          ((float*)scales)[b] = f == f ? f : __uint_as_float(0x7FC00000u);
+        }
+      }
+    }
+  }
+}
+
+template <bool kQ4>
+int split_gguf(const void* blocks, uint8_t* qs, void* scales, int64_t count, hipStream_t stream) {
+  constexpr int64_t kBytes = kQ4 ? 18 : 34;
+  if (count < 0 || ((uintptr_t)blocks & 3) || ((uintptr_t)qs & 15) ||
+      ((uintptr_t)scales & (kQ4 ? 1 : 3))) {
+    return DNX_EINVAL;
+  }
+  // Segments of 2^25 blocks keep buffer offsets 32-bit; an even first
+  // block keeps each segment's base 4-byte aligned.
+  constexpr int64_t kSeg = 1ll << 25;
+  for (int64_t first = 0; first < count; first += kSeg) {
+    const int64_t n = count - first < kSeg ? count - first : kSeg;
+    const int64_t pieces = n * (kQ4 ? 1 : 2);
+    int64_t grid = (pieces + kThreads * kSplitItems - 1) / (kThreads * kSplitItems);
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(split_gguf_kernel<kQ4>, dim3((unsigned)grid), dim3(kThreads), 0, stream,
+                       (const uint8_t*)blocks + first * kBytes, qs + first * (kQ4 ? 16 : 32),
+                       kQ4 ? (void*)((uint16_t*)scales + first) : (void*)((float*)scales + first),
+                       (int)n, (uint32_t)(n * kBytes));
+    if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+  }
+  return DNX_OK;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------ C ABI
@@ -491,6 +575,16 @@ int dnx_q6k_to_q8(const void* blocks, int8_t* qs, float* scales, int64_t rows, i
   hipLaunchKernelGGL(q6k_to_q8_kernel, dim3(grid), dim3(kThreads), 0, stream,
                      (const uint8_t*)blocks, qs, scales, rows, cols);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_split_q8_0(const void* blocks, int8_t* qs, float* scales, int64_t count,
+                   hipStream_t stream) {
+  return split_gguf<false>(blocks, (uint8_t*)qs, scales, count, stream);
+}
+
+int dnx_split_q4_0(const void* blocks, uint8_t* qs, uint16_t* scales, int64_t count,
+                   hipStream_t stream) {
+  return split_gguf<true>(blocks, qs, scales, count, stream);
 }
 
 int64_t dnx_argmax_workspace_bytes(int64_t n) {

@@ -59,8 +59,8 @@ struct Buffer {
 
 enum Op {
   kOpMatmulQ8, kOpMatmulQ4, kOpSwiglu, kOpQuantize, kOpQuantizeBf16, kOpQuantizeQ4,
-  kOpQuantizeQ4Bf16, kOpQ6kToQ8, kOpArgmax, kOpGelu, kOpRmsNorm, kOpHeadNormRope, kOpConv,
-  kOpAttention, kOpCopy, kOpAdd, kOpSteer
+  kOpQuantizeQ4Bf16, kOpQ6kToQ8, kOpSplitQ8, kOpSplitQ4, kOpArgmax, kOpGelu, kOpRmsNorm,
+  kOpHeadNormRope, kOpConv, kOpAttention, kOpCopy, kOpAdd, kOpSteer
 };
 
 struct Cmd {
@@ -413,6 +413,22 @@ bool run(const Cmd& c) {
       after_dispatch(kKindQuantizeWeights);
       wrote_region(qs, qsOff, rows * cols);
       wrote_region(sc, scOff, rows * (cols / 32) * 4);
+      return rc == DNX_OK;
+    }
+    case kOpSplitQ8:
+    case kOpSplitQ4: {
+      const bool q4 = c.op == kOpSplitQ4;
+      const int64_t src = c.a[0], srcOff = c.a[1], qs = c.a[2], qsOff = c.a[3];
+      const int64_t sc = c.a[4], scOff = c.a[5], rows = c.a[6], cols = c.a[7];
+      const int64_t count = rows * (cols / 32);
+      read_region(src, srcOff, count * (q4 ? 18 : 34));
+      const int rc = q4 ? dnx_split_q4_0(dev_at(src, srcOff), (uint8_t*)dev_at(qs, qsOff),
+                                         (uint16_t*)dev_at(sc, scOff), count, gStream)
+                        : dnx_split_q8_0(dev_at(src, srcOff), (int8_t*)dev_at(qs, qsOff),
+                                         (float*)dev_at(sc, scOff), count, gStream);
+      after_dispatch(kKindQuantizeWeights);
+      wrote_region(qs, qsOff, count * (q4 ? 16 : 32));
+      wrote_region(sc, scOff, count * (q4 ? 2 : 4));
       return rc == DNX_OK;
     }
     case kOpRmsNorm: {
@@ -790,6 +806,33 @@ void lab_gpu_enc_q6k_to_q8(int64_t src, int64_t srcOffset, int64_t qs, int64_t q
   record(kOpQ6kToQ8, {src, srcOffset, qs, qsOffset, scales, scalesOffset, rows, cols});
 }
 
+static void enc_split(bool q4, int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                      int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols) {
+  const int64_t count = rows >= 0 && cols > 0 ? rows * (cols / 32) : 0;
+  const bool ok = rows >= 0 && cols > 0 && cols % 32 == 0 &&
+                  in_bounds(src, srcOffset, count * (q4 ? 18 : 34)) &&
+                  in_bounds(qs, qsOffset, count * (q4 ? 16 : 32)) &&
+                  in_bounds(scales, scalesOffset, count * (q4 ? 2 : 4)) &&
+                  srcOffset % 4 == 0 && qsOffset % 16 == 0 && scalesOffset % (q4 ? 2 : 4) == 0;
+  if (!ok) {
+    LOG("enc_split_%s: invalid arguments\n", q4 ? "q4_0" : "q8_0");
+    gFailed = true;
+    return;
+  }
+  record(q4 ? kOpSplitQ4 : kOpSplitQ8, {src, srcOffset, qs, qsOffset, scales, scalesOffset,
+                                        rows, cols});
+}
+
+void lab_gpu_enc_split_q8_0(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                            int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols) {
+  enc_split(false, src, srcOffset, qs, qsOffset, scales, scalesOffset, rows, cols);
+}
+
+void lab_gpu_enc_split_q4_0(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                            int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols) {
+  enc_split(true, src, srcOffset, qs, qsOffset, scales, scalesOffset, rows, cols);
+}
+
 // The layer steps: arguments are checked here (the reference's kernels
 // would read out of bounds); an invalid one fails the command buffer.
 static bool fail_enc(const char* what) {
@@ -953,7 +996,7 @@ int64_t lab_gpu_max_buffer_length(void) {
   return (int64_t)total;
 }
 
-// No attention kernel is built here; report the LDS a workgroup may use.
+// The LDS a workgroup may use.
 int64_t lab_gpu_max_shared_memory(void) { return 160 * 1024; }
 
 int64_t lab_gpu_recommended_working_set(void) { return lab_gpu_max_buffer_length(); }

@@ -59,6 +59,20 @@ def q6k_to_q8(blocks: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, rows
                                      _stream(stream)), "dnx_q6k_to_q8")
 
 
+def split_q8_0(blocks: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, count: int,
+               stream=None) -> None:
+    """GGUF Q8_0 blocks -> int8 values + fp32 scales (splitQ8_0, gguf.dart:270-282)."""
+    _check(_lib.load().dnx_split_q8_0(_ptr(blocks), _ptr(qs), _ptr(scales), count,
+                                      _stream(stream)), "dnx_split_q8_0")
+
+
+def split_q4_0(blocks: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, count: int,
+               stream=None) -> None:
+    """GGUF Q4_0 blocks -> nibble bytes + fp16 scale bits (splitQ4_0, gguf.dart:208-218)."""
+    _check(_lib.load().dnx_split_q4_0(_ptr(blocks), _ptr(qs), _ptr(scales), count,
+                                      _stream(stream)), "dnx_split_q4_0")
+
+
 def quantize_q4_bf16(w: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, rows: int,
                      cols: int, stream=None) -> None:
     """BF16 bits widened (p << 16), then lab_quantize_q4, in one kernel."""

@@ -76,6 +76,9 @@ def split_q8_0(blocks: np.ndarray, rows: int, cols: int) -> QuantMatrix:
         raise ArgumentError(f"Q8_0 data does not hold a [{rows}, {cols}] matrix")
     b = blocks.reshape(count, 34)
     scales = half_to_float(b[:, :2].copy().view(np.uint16).reshape(-1))
+    # halfToDouble (native.dart:871-880) returns Dart's double.nan for every
+    # NaN pattern, which a Float32List stores as 0x7FC00000.
+    scales[np.isnan(scales)] = np.uint32(0x7FC00000).view(np.float32)
     qs = b[:, 2:].copy().view(np.int8).reshape(rows, cols)
     return QuantMatrix.q8(qs, scales.reshape(rows, cols // 32))
 

@@ -222,6 +222,42 @@ class GpuLinear:
             self._lib.lab_gpu_release(src)
         self._replace(name, _Matrix(False, dst, 0, scales_at, rows, cols, cols))
 
+    def upload_gguf(self, name: str, blocks: np.ndarray, rows: int, cols: int,
+                    kind: str = "q8_0") -> None:
+        """Uploads GGUF Q8_0 or Q4_0 blocks as they lie in the file and splits
+        them into the engine's Q8 / Q4 layout on the GPU (the reference splits
+        on the CPU first: ``splitQ8_0`` ``gguf.dart:270-282``, ``splitQ4_0``
+        ``:208-218``); the matrix is the same, bit for bit."""
+        self._check_open()
+        if kind not in ("q8_0", "q4_0"):
+            raise ArgumentError(f"cannot split GGUF {kind} blocks")
+        q4 = kind == "q4_0"
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+        count = rows * cols // 32
+        nsrc = count * (18 if q4 else 34)
+        if rows <= 0 or cols <= 0 or cols % 32 != 0 or blocks.size != nsrc:
+            raise ArgumentError(f"{kind.upper()} data does not hold a [{rows}, {cols}] matrix")
+        src = self._lib.lab_gpu_buffer(nsrc)
+        if src < 0:
+            raise StateError(f"GPU buffer for the {kind} blocks failed")
+        try:
+            self._bytes_view(src, nsrc)[:] = blocks
+            qs_bytes = count * (16 if q4 else 32)
+            scales_at = (qs_bytes + 63) // 64 * 64
+            nbytes = scales_at + count * (2 if q4 else 4)
+            dst = self._lib.lab_gpu_buffer(nbytes)
+            if dst < 0:
+                raise StateError(f"GPU buffer of {nbytes} bytes failed")
+            self._owned.append(dst)
+            self._lib.lab_gpu_begin()
+            enc = self._lib.lab_gpu_enc_split_q4_0 if q4 else self._lib.lab_gpu_enc_split_q8_0
+            enc(src, 0, dst, 0, dst, scales_at, rows, cols)
+            if self._lib.lab_gpu_commit(1) != 1:
+                raise StateError("GPU command buffer failed")
+        finally:
+            self._lib.lab_gpu_release(src)
+        self._replace(name, _Matrix(q4, dst, 0, scales_at, rows, cols, cols))
+
     def _upload_quantized(self, name: str, src_values: np.ndarray, esize: int, rows: int,
                           cols: int, rows_pad: int | None, fmt: str) -> None:
         self._check_open()

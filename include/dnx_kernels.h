@@ -157,6 +157,16 @@ int dnx_gemm_q8_panel(const int8_t* qs, const float* scales, const void* panel, 
 int dnx_gemm_q4_panel(const uint8_t* qs, const uint16_t* scales, const void* panel, float* y,
                       int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
 
+// GGUF Q8_0 / Q4_0 blocks split into the engine's layout on the GPU, bit
+// for bit as splitQ8_0 (lib/src/gguf.dart:270-282: int8 values and the fp16
+// d widened to fp32) and splitQ4_0 (:208-218: nibble bytes and the fp16
+// bits) do on the CPU. count = rows * cols / 32 blocks of 34 (Q8_0) or 18
+// (Q4_0) bytes; blocks 4-byte aligned, qs 16-byte aligned.
+int dnx_split_q8_0(const void* blocks, int8_t* qs, float* scales, int64_t count,
+                   dnx_stream_t stream);
+int dnx_split_q4_0(const void* blocks, uint8_t* qs, uint16_t* scales, int64_t count,
+                   dnx_stream_t stream);
+
 // Greedy argmax of v[0..n) (argmaxToken, lib/src/sampler.dart:137-152):
 // the first index of the maximum; a NaN at index 0 wins, other NaNs never.
 // Writes one int64 to *out. workspace: dnx_argmax_workspace_bytes(n) bytes.

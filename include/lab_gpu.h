@@ -167,6 +167,20 @@ void lab_gpu_enc_quantize_q4_bf16(int64_t src, int64_t srcOffset, int64_t qs, in
 void lab_gpu_enc_q6k_to_q8(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
                            int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols);
 
+// GGUF Q8_0 / Q4_0 blocks split into the engine's layout on the GPU. No
+// counterpart in the reference's GPU ABI: its loader splits on the CPU
+// (splitQ8_0, lib/src/gguf.dart:270-282; splitQ4_0, :208-218) before the
+// upload; here the raw blocks are uploaded and split in HBM, bit for bit.
+// rows x cols/32 blocks of 34 (Q8_0) or 18 (Q4_0) bytes at src + srcOffset
+// become the values at qs + qsOffset and the scales at scales +
+// scalesOffset (Q8: fp32, the fp16 d widened exactly; Q4: the fp16 bits).
+// cols must be a multiple of 32, srcOffset a multiple of 4 and qsOffset of
+// 16; otherwise the command buffer fails.
+void lab_gpu_enc_split_q8_0(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                            int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols);
+void lab_gpu_enc_split_q4_0(int64_t src, int64_t srcOffset, int64_t qs, int64_t qsOffset,
+                            int64_t scales, int64_t scalesOffset, int64_t rows, int64_t cols);
+
 // Greedy token on the GPU: argmaxToken (sampler.dart:137-152, no
 // suppression) over n floats at x + xOffset, the index written as one int64
 // at out + outOffset. Replaces the logits copy + host argmax of

@@ -178,6 +178,32 @@ class Oracle(_Kernels):
     # ---- layer steps (Metal shader semantics, sums in double). Every array
     # handed to C is bound to a name first, so it outlives the call.
 
+    def split_q8_0(self, blocks: np.ndarray, count: int):
+        """GGUF Q8_0 blocks -> (int8 values [count * 32], fp32 scales [count]):
+        splitQ8_0, lib/src/gguf.dart:270-282. Block b is 34 bytes: the fp16 d
+        (little-endian) at 34b, the values at 34b + 2. d is widened as
+        halfToDouble (lib/src/native.dart:871-880) then stored as a float:
+        sign * mantissa * 2^-24 (subnormal), +-inf, double.nan (0x7FC00000
+        for every NaN pattern), else sign * (1 + m / 1024) * 2^(e - 15)."""
+        b = np.asarray(blocks, dtype=np.uint8).reshape(count, 34)
+        bits = b[:, 0].astype(np.int64) | (b[:, 1].astype(np.int64) << 8)
+        sign = np.where(bits & 0x8000, -1.0, 1.0)
+        e, m = (bits >> 10) & 0x1F, bits & 0x3FF
+        with np.errstate(invalid="ignore"):
+            d = np.where(e == 0, sign * m * 2.0 ** -24,
+                         np.where(e == 31, np.where(m == 0, sign * np.inf, np.nan),
+                                  sign * (1 + m / 1024) * np.exp2(e - 15.0)))
+        scales = d.astype(np.float32)
+        scales[np.isnan(scales)] = np.uint32(0x7FC00000).view(np.float32)
+        return b[:, 2:].copy().view(np.int8).reshape(-1), scales
+
+    def split_q4_0(self, blocks: np.ndarray, count: int):
+        """GGUF Q4_0 blocks -> (nibble bytes [count * 16], fp16 bits [count]):
+        splitQ4_0, lib/src/gguf.dart:208-218 (bytes copied as they are)."""
+        b = np.asarray(blocks, dtype=np.uint8).reshape(count, 18)
+        d = (b[:, 0].astype(np.uint16) | (b[:, 1].astype(np.uint16) << 8))
+        return b[:, 2:].copy().reshape(-1), d
+
     def rms_norm(self, x, w, eps, out=None):
         x = np.ascontiguousarray(x, np.float32)
         w = np.ascontiguousarray(w, np.float32)

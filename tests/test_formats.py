@@ -27,6 +27,16 @@ def test_split_q8_0_keeps_bytes_and_widens_d_exactly():
     assert np.all(np.abs(got_qs * got_d[:, None] - values.reshape(2, 32)) <= 0.02)
 
 
+def test_split_q8_0_matches_the_oracle_nan_included(orc):
+    rng = np.random.default_rng(9)
+    blocks = rng.integers(0, 256, (64, 34), dtype=np.uint8)
+    blocks[:4, 0:2] = [[0x01, 0x7C], [0x00, 0xFE], [0x00, 0x80], [0x00, 0x7C]]
+    m = split_q8_0(blocks, 2, 1024)
+    qs, sc = orc.split_q8_0(blocks, 64)
+    assert np.array_equal(m.qs_bytes.view(np.int8), qs)
+    assert np.array_equal(m.scale_bytes.view(np.uint32), sc.view(np.uint32))
+
+
 def test_split_q4_0_round_trip():
     rng = np.random.default_rng(0)
     qs = rng.integers(0, 256, (3, 64 // 2), dtype=np.uint8)

@@ -347,3 +347,36 @@ def test_steer_closed_forms(orc):
     assert np.allclose(removed, np.stack([u, u]), atol=1e-5)
     half = orc.steer(x, v, 1, 0.5)
     assert np.allclose(half[0], u + 1.5 * v, atol=1e-5)
+
+
+def test_gguf_split_q8_0_scale_widening(orc):
+    # halfToDouble (native.dart:871-880) on hand-worked patterns, and every
+    # non-NaN pattern against numpy's IEEE binary16 conversion.
+    cases = {0x3C00: 1.0, 0xC000: -2.0, 0x0001: 2.0 ** -24, 0x03FF: 1023 * 2.0 ** -24,
+             0x0400: 2.0 ** -14, 0x3555: 0.333251953125, 0x7BFF: 65504.0,
+             0x7C00: math.inf, 0xFC00: -math.inf}
+    pats = np.array(list(cases) + [0x8000, 0x7C01, 0xFE00, 0x7FFF], np.uint16)
+    blocks = np.zeros((pats.size, 34), np.uint8)
+    blocks[:, 0], blocks[:, 1] = pats & 0xFF, pats >> 8
+    blocks[:, 2:] = np.arange(32, dtype=np.uint8) + 100
+    qs, sc = orc.split_q8_0(blocks, pats.size)
+    for i, want in enumerate(cases.values()):
+        assert sc[i] == want
+    assert sc[len(cases)] == 0 and math.copysign(1, sc[len(cases)]) < 0  # -0 kept
+    assert np.all(sc[len(cases) + 1:].view(np.uint32) == 0x7FC00000)   # double.nan
+    assert np.array_equal(qs.view(np.uint8).reshape(-1, 32), blocks[:, 2:])
+    allp = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    allp = allp[~np.isnan(allp.view(np.float16))]
+    b = np.zeros((allp.size, 34), np.uint8)
+    b[:, 0], b[:, 1] = allp & 0xFF, allp >> 8
+    _, sc = orc.split_q8_0(b, allp.size)
+    assert np.array_equal(sc.view(np.uint32),
+                          allp.view(np.float16).astype(np.float32).view(np.uint32))
+
+
+def test_gguf_split_q4_0_is_a_byte_split(orc):
+    rng = np.random.default_rng(4)
+    blocks = rng.integers(0, 256, (5, 18), dtype=np.uint8)
+    qs, d = orc.split_q4_0(blocks, 5)
+    assert np.array_equal(qs.reshape(5, 16), blocks[:, 2:])
+    assert np.array_equal(d, blocks[:, 0].astype(np.int64) + 256 * blocks[:, 1].astype(np.int64))
