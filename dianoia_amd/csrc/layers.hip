@@ -478,6 +478,283 @@ attention_combine_kernel(const float* __restrict__ ws, const float* __restrict__
   }
 }
 
+// Attention of many tokens (prefill) on the fp32 matrix cores. A wave
+// takes 16 queries of one head, a workgroup 4 waves sharing one KV head
+// (GW heads of a GQA group x 4 / GW query blocks), and the workgroup walks
+// its keys in tiles of 32 staged in LDS (K row-major, V transposed), so a
+// tile is read once for up to 64 queries. Per tile and wave:
+// * S^T = K Q^T on v_mfma_f32_16x16x4f32: A = 16 keys x 4 dims (K from LDS,
+//   dims g * hd / 4 + s for lane group g), B = 4 dims x 16 queries (Q held
+//   in registers); a lane ends with 8 scores of its query (column), so the
+//   online softmax needs two cross-lane exchanges per tile;
+// * O^T += V^T P^T: the lane's exponentials are already the B operand of
+//   step s (keys (s / 4) * 16 + 4 g + s % 4), V^T tiles come from LDS.
+// The running (max, sum) rescale O when the max grows (flash attention).
+// With `splits` > 1 a workgroup takes a run of tiles_per_split tiles and
+// writes per (token, head) the partial (m, l, o) rows that
+// attention_combine_kernel adds (for long contexts with few query blocks);
+// otherwise it writes the output, gated. fp32 throughout: the sums run in
+// another order than the oracle's, not at lower precision.
+constexpr int kPQ = 16;   // queries per wave
+constexpr int kPK = 32;   // keys per tile
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int HD, int GW>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
+attention_prefill_kernel(const float* __restrict__ q, const float* __restrict__ keys,
+                         const float* __restrict__ values, const float* __restrict__ gate,
+                         float* __restrict__ out, float* __restrict__ ws, int position, int n,
+                         int heads, int kv_dim, int group, int window, float scale, int splits,
+                         int tiles_per_split) {
+  constexpr int QW = 4 / GW;
+  constexpr int KS = HD + 4;                     // K row stride in LDS (floats)
+  constexpr int VS = kPK + 4;                    // V^T row stride
+  constexpr int kF4 = HD * kPK / 4 / kThreads;   // float4 per thread per tile and matrix
+  constexpr int kLds = kPK * KS + HD * VS;
+  static_assert(kLds >= 4 * kPQ * (HD + 4), "the output transpose reuses the tiles' LDS");
+  __shared__ __align__(16) float lds[kLds];
+  float* Ks = lds;
+  float* Vt = lds + kPK * KS;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, g4 = lane >> 4;
+  const int head = blockIdx.x * GW + wave % GW;
+  const int split = blockIdx.z;
+  // Odd splits take the query blocks in reverse: workgroups dispatched
+  // together then pair a late block's long key runs with an early block's
+  // short ones (causal work grows with the block).
+  const int yb = split & 1 ? gridDim.y - 1 - blockIdx.y : blockIdx.y;
+  const int t0 = (yb * QW + wave / GW) * kPQ;   // the wave's first token
+  // The workgroup's keys: from its first query's window start through its
+  // last query.
+  const int wq_first = yb * QW * kPQ;
+  const int wq_last = min(n, wq_first + QW * kPQ) - 1;
+  const int kend = position + wq_last + 1;
+  const int kstart = window > 0 ? max(0, position + wq_first - window + 1) : 0;
+  const int ntiles = (kend - kstart + kPK - 1) / kPK;
+  const int tile_lo = split * tiles_per_split;
+  const int tile_hi = min(ntiles, tile_lo + tiles_per_split);
+  const size_t kvo = (size_t)(blockIdx.x * GW / group) * HD;
+
+  // B operand of S^T: the lane's query, dims g4 * HD / 4 + s.
+  const int tq = t0 + c16;
+  const int qpos = position + tq;
+  float qr[HD / 4];
+  {
+    const float* qp = q + ((size_t)min(tq, n - 1) * heads + head) * HD + g4 * (HD / 4);
+#pragma unroll
+    for (int s4 = 0; s4 < HD / 16; s4++) {
+      const float4 v = *(const float4*)(qp + 4 * s4);
+      qr[4 * s4] = v.x;
+      qr[4 * s4 + 1] = v.y;
+      qr[4 * s4 + 2] = v.z;
+      qr[4 * s4 + 3] = v.w;
+    }
+  }
+  float m_run = -INFINITY, l_run = 0.0f;
+  v4f o[HD / 16];
+#pragma unroll
+  for (int e = 0; e < HD / 16; e++) o[e] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // Tile t's keys and values, thread-strided float4s; rows past the keys
+  // read zeros (the resource ends with the last key row).
+  float4 kp[kF4], vp[kF4];
+  auto load_tile = [&](int t) {
+    const int kt = kstart + t * kPK;
+    const uint32_t range = (uint32_t)min(kPK, kend - kt) * (uint32_t)kv_dim * 4u;
+    const i32x4 kr = buffer_rsrc(keys + (size_t)kt * kv_dim + kvo, range);
+    const i32x4 vr = buffer_rsrc(values + (size_t)kt * kv_dim + kvo, range);
+#pragma unroll
+    for (int j = 0; j < kF4; j++) {
+      // K: consecutive threads along a row. V: consecutive threads down a
+      // column, so that its transposed LDS writes fall in distinct banks.
+      const int f = j * kThreads + tid;
+      kp[j] = buffer_load_f4(kr, (f / (HD / 4)) * kv_dim * 4 + (f % (HD / 4)) * 16);
+      vp[j] = buffer_load_f4(vr, (f % kPK) * kv_dim * 4 + (f / kPK) * 16);
+    }
+  };
+  if (tile_lo < tile_hi) load_tile(tile_lo);
+  for (int t = tile_lo; t < tile_hi; t++) {
+    __syncthreads();  // every wave is done with the previous tile
+#pragma unroll
+    for (int j = 0; j < kF4; j++) {
+      const int f = j * kThreads + tid;
+      *(float4*)(Ks + (f / (HD / 4)) * KS + (f % (HD / 4)) * 4) = kp[j];
+      const int row = f % kPK, c4 = f / kPK;
+      Vt[(c4 * 4 + 0) * VS + row] = vp[j].x;
+      Vt[(c4 * 4 + 1) * VS + row] = vp[j].y;
+      Vt[(c4 * 4 + 2) * VS + row] = vp[j].z;
+      Vt[(c4 * 4 + 3) * VS + row] = vp[j].w;
+    }
+    __syncthreads();
+    if (t + 1 < tile_hi) load_tile(t + 1);  // in flight during this tile's math
+    const int kt = kstart + t * kPK;
+
+    // S^T for the tile's two 16-key halves, each as two chains (even and
+    // odd steps) so that dependent MFMAs interleave.
+    v4f sa[2][2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) sa[c][0] = sa[c][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s4 = 0; s4 < HD / 16; s4++) {
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        const float4 k4 = *(const float4*)(Ks + (c * 16 + c16) * KS + g4 * (HD / 4) + 4 * s4);
+        sa[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qr[4 * s4], sa[c][0], 0, 0, 0);
+        sa[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qr[4 * s4 + 1], sa[c][1], 0, 0, 0);
+        sa[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qr[4 * s4 + 2], sa[c][0], 0, 0, 0);
+        sa[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qr[4 * s4 + 3], sa[c][1], 0, 0, 0);
+      }
+    }
+    // Scores of keys kt + 16 c + 4 g4 + v for query tq, masked; online softmax.
+    float p[2][4];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int kpos = kt + c * 16 + 4 * g4 + v;
+        const bool ok = kpos < kend && kpos <= qpos && (window <= 0 || kpos > qpos - window);
+        const float x = (sa[c][0][v] + sa[c][1][v]) * scale;
+        p[c][v] = ok ? x : -INFINITY;
+        mt = fmaxf(mt, p[c][v]);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+    float ps = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        p[c][v] = p[c][v] == -INFINITY ? 0.0f : expf(p[c][v] - m_new);
+        ps += p[c][v];
+      }
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+#pragma unroll
+    for (int e = 0; e < HD / 16; e++) o[e] *= alpha;
+    // O^T += V^T P^T: step s takes keys (s / 4) * 16 + 4 g4 + s % 4.
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      float4 v4[HD / 16];
+#pragma unroll
+      for (int e = 0; e < HD / 16; e++)
+        v4[e] = *(const float4*)(Vt + (e * 16 + c16) * VS + c * 16 + 4 * g4);
+#pragma unroll
+      for (int e = 0; e < HD / 16; e++)
+        o[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[e].x, p[c][0], o[e], 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < HD / 16; e++)
+        o[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[e].y, p[c][1], o[e], 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < HD / 16; e++)
+        o[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[e].z, p[c][2], o[e], 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < HD / 16; e++)
+        o[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[e].w, p[c][3], o[e], 0, 0, 0);
+    }
+  }
+
+  // The wave's O^T (dims x 16 queries) through LDS to rows, then out.
+  __syncthreads();  // the tiles' LDS is free
+  float* tw = lds + wave * kPQ * (HD + 4);
+#pragma unroll
+  for (int e = 0; e < HD / 16; e++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) tw[c16 * (HD + 4) + e * 16 + 4 * g4 + v] = o[e][v];
+  if (g4 == 0) {
+    tw[c16 * (HD + 4) + HD] = m_run;
+    tw[c16 * (HD + 4) + HD + 1] = l_run;
+  }
+  __syncthreads();
+  constexpr int kC4 = HD / 4;            // float4 per row
+  constexpr int kRows = 64 / kC4;        // rows per pass of the wave
+  const int c4 = lane % kC4;
+  for (int r = lane / kC4; r < kPQ; r += kRows) {
+    const int tok = t0 + r;
+    if (tok >= n) break;
+    const float* row = tw + r * (HD + 4);
+    const float4 val = *(const float4*)(row + 4 * c4);
+    const size_t th = (size_t)tok * heads + head;
+    if (splits > 1) {
+      float* w = ws + (th * splits + split) * (HD + 4);
+      *(float4*)(w + 4 + 4 * c4) = val;
+      if (c4 == 0) {
+        w[0] = row[HD];
+        w[1] = row[HD + 1];
+      }
+    } else {
+      const float l = row[HD + 1];
+      const float g = gate != nullptr ? 1.0f / (1.0f + expf(-gate[th])) : 1.0f;
+      float4 y = make_float4(val.x / l, val.y / l, val.z / l, val.w / l);
+      if (gate != nullptr) y = make_float4(y.x * g, y.y * g, y.z * g, y.w * g);
+      *(float4*)(out + th * HD + 4 * c4) = y;
+    }
+  }
+}
+
+// The combine for many (token, head) rows and at most 64 splits (prefill):
+// one wave per row, four rows per workgroup, no barrier. Lane s holds split
+// s's statistics; the value sums run in split order with 8 splits' loads in
+// flight, dims lane + 64 i. Rows past the splits read zeros (the resource
+// ends with the row's last split), and dims past hd are computed but not
+// stored.
+__global__ void __launch_bounds__(kThreads)
+attention_combine_rows_kernel(const float* __restrict__ ws, const float* __restrict__ gate,
+                              float* __restrict__ out, int heads, int hd, int splits, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * kWaves + (threadIdx.x >> 6);   // token * heads + head
+  if (r >= rows) return;
+  const int row = hd + 4;
+  const i32x4 rs = buffer_rsrc(ws + (size_t)r * splits * row, (uint32_t)splits * row * 4u);
+  const float m = lane < splits ? __int_as_float(dnx_raw_buffer_load_i32(rs, lane * row * 4, 0, 0))
+                                : -INFINITY;
+  const float ls = __int_as_float(dnx_raw_buffer_load_i32(rs, (lane * row + 1) * 4, 0, 0));
+  constexpr int kND = 4;   // dims per lane: hd <= 256
+  const int nd = (hd + 63) / 64;
+  float acc[kND] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const float mx = wave_max(m);
+  const float f = m == -INFINITY ? 0.0f : expf(m - mx);
+  const float l = wave_sum(ls * f);
+  for (int s0 = 0; s0 < splits; s0 += 8) {
+    float v[8][kND];
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+#pragma unroll
+      for (int i = 0; i < kND; i++)
+        v[u][i] = i < nd ? __int_as_float(dnx_raw_buffer_load_i32(
+                               rs, ((s0 + u) * row + 4 + lane + 64 * i) * 4, 0, 0))
+                         : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const float fs = __shfl(f, s0 + u);   // 0 past the last split
+#pragma unroll
+      for (int i = 0; i < kND; i++) acc[i] += v[u][i] * fs;
+    }
+  }
+  const float g = gate != nullptr ? 1.0f / (1.0f + expf(-gate[r])) : 1.0f;
+#pragma unroll
+  for (int i = 0; i < kND; i++) {
+    const int d = lane + 64 * i;
+    if (i < nd && d < hd) out[(size_t)r * hd + d] = gate != nullptr ? (acc[i] / l) * g : acc[i] / l;
+  }
+}
+
+template <int HD>
+void launch_prefill(int gw, dim3 grid, hipStream_t st, const float* q, const float* keys,
+                    const float* values, const float* gate, float* out, float* ws, int position,
+                    int n, int heads, int kv_dim, int group, int window, float scale, int splits,
+                    int tps) {
+  auto k = gw == 4 ? attention_prefill_kernel<HD, 4>
+         : gw == 2 ? attention_prefill_kernel<HD, 2> : attention_prefill_kernel<HD, 1>;
+  hipLaunchKernelGGL(k, grid, dim3(kThreads), 0, st, q, keys, values, gate, out, ws, position, n,
+                     heads, kv_dim, group, window, scale, splits, tps);
+}
+
 // Library-owned workspace of the split attention, grown on demand: a call
 // with more (head, token, split) entries than any before allocates, so such
 // a call must not be the first inside a graph capture.
@@ -598,6 +875,63 @@ int dnx_attention(const float* q, const float* keys, const float* values, const 
   const int64_t last = position + n - 1;
   const int64_t keys_of_last = window > 0 && last >= window ? window : last + 1;
   const float scale = (float)(1.0 / sqrt((double)hd));
+  // 8+ tokens at hd 64 or 128: the matrix-core kernel, its keys split over
+  // workgroups while fewer than kTargetWaves waves would run.
+  if ((hd == 64 || hd == 128) && n >= 8 && kv_heads * hd <= (1 << 20) &&
+      ((uintptr_t)out & 15) == 0) {
+    constexpr int64_t kTargetWaves = 2048;
+    const int64_t group = heads / kv_heads;
+    const int gw = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    const int64_t qb = kPQ * (4 / gw);   // queries per workgroup
+    const int64_t by = (n + qb - 1) / qb;
+    int64_t tmax = 1;  // tiles of the longest workgroup range
+    for (int64_t b = 0; b < by; b++) {
+      const int64_t first = b * qb, lastq = (first + qb < n ? first + qb : n) - 1;
+      const int64_t ks = window > 0 && position + first - window + 1 > 0
+                             ? position + first - window + 1 : 0;
+      const int64_t t = (position + lastq + 1 - ks + kPK - 1) / kPK;
+      if (t > tmax) tmax = t;
+    }
+    const int64_t waves = heads / gw * by * 4;
+    int64_t splits = 1;
+    if (waves < kTargetWaves && tmax >= 4) {
+      splits = (kTargetWaves + waves - 1) / waves;
+      if (splits > tmax / 2) splits = tmax / 2;
+    }
+    int64_t tps = (tmax + splits - 1) / splits;
+    splits = (tmax + tps - 1) / tps;
+    size_t pws = splits > 1 ? (size_t)n * heads * splits * (hd + 4) * 4 : 0;
+    if (pws > ((size_t)1 << 30) || splits > 4096) {
+      splits = 1;
+      tps = tmax;
+      pws = 0;
+    }
+    float* ws = nullptr;
+    if (splits > 1 && (ws = attention_workspace(pws)) == nullptr) return DNX_ENOMEM;
+    const dim3 grid((unsigned)(heads / gw), (unsigned)by, (unsigned)splits);
+    const hipStream_t st = (hipStream_t)stream;
+    if (hd == 128) {
+      launch_prefill<128>(gw, grid, st, q, keys, values, gate, out, ws, (int)position, (int)n,
+                          (int)heads, (int)(kv_heads * hd), (int)group, (int)window, scale,
+                          (int)splits, (int)tps);
+    } else {
+      launch_prefill<64>(gw, grid, st, q, keys, values, gate, out, ws, (int)position, (int)n,
+                         (int)heads, (int)(kv_heads * hd), (int)group, (int)window, scale,
+                         (int)splits, (int)tps);
+    }
+    if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+    if (splits > 1 && splits <= 64) {
+      const int64_t rows = n * heads;
+      hipLaunchKernelGGL(attention_combine_rows_kernel, dim3((unsigned)((rows + kWaves - 1) / kWaves)),
+                         dim3(kThreads), 0, st, ws, gate, out, (int)heads, (int)hd, (int)splits,
+                         (int)rows);
+    } else if (splits > 1) {
+      hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)heads, (unsigned)n),
+                         dim3(kThreads), (size_t)splits * 4, st, ws, gate, out, (int)heads,
+                         (int)hd, (int)splits);
+    }
+    return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+  }
   // Few (head, token) workgroups for many keys: split the keys.
   const int kps = split_keys((int)hd);
   const int64_t splits = (keys_of_last + kps - 1) / kps;

@@ -87,6 +87,11 @@ def test_short_conv_bit_exact(gpu_ready, orc, width, k, n):
     (32, 4, 64, 2500, 1, 0, True),     # split keys, 8 query heads per KV head
     (12, 2, 128, 1500, 2, 0, False),   # split keys, 6 per KV head: pairs of heads
     (6, 2, 32, 900, 1, 300, False),    # split keys, 3 per KV head: one head each
+    (32, 8, 128, 0, 512, 0, False),    # prefill on the matrix cores, keys split in two
+    (16, 8, 64, 37, 100, 0, True),     # matrix cores, 2 heads per KV head, gated, ragged
+    (8, 8, 128, 500, 40, 64, False),   # matrix cores, one head per KV head, window 64
+    (12, 4, 64, 3000, 24, 0, False),   # matrix cores, a long context: many key splits
+    (4, 1, 128, 10, 9, 0, True),       # matrix cores, the smallest chunk, 4 heads per KV
 ])
 def test_attention(gpu_ready, orc, heads, kv, hd, pos, n, window, gated):
     rng = np.random.default_rng(heads + hd + pos + n)
