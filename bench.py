@@ -337,8 +337,9 @@ def bench_c4(torch, D, synth, timer, steps, warmup):
 def bench_layers(torch, D, timer, steps):
     """The decoder's other layer steps (lab_gpu_enc_* semantics): attention
     decode over a 4096-position cache (32 query heads, 8 KV heads, hd 128;
-    HBM-bound on the cached keys and values) and RMSNorm over a 4096 x 2048
-    prefill block. Inputs generated on the GPU."""
+    HBM-bound on the cached keys and values), RMSNorm over a 4096 x 2048
+    prefill block, and causal prefill attention of 512 tokens (same heads;
+    fp32 matrix cores). Inputs generated on the GPU."""
     gen = torch.Generator(device="cuda").manual_seed(6)
     heads, kv, hd, pos = 32, 8, 128, 4095
     q = torch.randn(heads * hd, device="cuda", generator=gen)
@@ -348,6 +349,10 @@ def bench_layers(torch, D, timer, steps):
     x = torch.randn((4096, 2048), device="cuda", generator=gen)
     w = torch.rand(2048, device="cuda", generator=gen)
     y = torch.empty_like(x)
+    # Prefill: 512 tokens from position 0 over their own keys (causal).
+    npre = 512
+    qp = torch.randn(npre * heads * hd, device="cuda", generator=gen)
+    outp = torch.empty(npre * heads * hd, device="cuda")
 
     def attn(i):
         D.attention(q, keys, values, None, out, pos, 1, heads, kv, hd, 0)
@@ -355,14 +360,23 @@ def bench_layers(torch, D, timer, steps):
     def norm(i):
         D.rms_norm(x, w, y, 4096, 2048, 1e-5)
 
-    means = timer.kernel_means([attn, norm], max(10, steps // 4))
+    def prefill(i):
+        D.attention(qp, keys, values, None, outp, 0, npre, heads, kv, hd, 0)
+
+    means = timer.kernel_means([attn, norm, prefill], max(10, steps // 4))
     attn_bytes = 2 * (pos + 1) * kv * hd * 4 + 2 * heads * hd * 4
     norm_bytes = 2 * 4096 * 2048 * 4 + 2048 * 4
+    # q.k and p.v: 2 flops per multiply-add, hd each, per visible key.
+    pre_flops = 4 * hd * heads * (npre * (npre + 1) // 2)
     return {"attention_decode_4096_ms": means[0],
             "attention_decode_4096_gbps": attn_bytes / means[0] / 1e6,
             "rms_norm_4096x2048_ms": means[1],
             "rms_norm_4096x2048_gbps": norm_bytes / means[1] / 1e6,
-            "bytes": {"attention_decode_4096": attn_bytes, "rms_norm_4096x2048": norm_bytes}}
+            "attention_prefill_512_ms": means[2],
+            "attention_prefill_512_tflops": pre_flops / means[2] / 1e9,
+            "attention_prefill_512_frac_fp32_mfma": pre_flops / means[2] / 1e9 / 157.3,
+            "bytes": {"attention_decode_4096": attn_bytes, "rms_norm_4096x2048": norm_bytes},
+            "flops": {"attention_prefill_512": pre_flops}}
 
 
 def bench_loaders(torch, D, timer, steps):
