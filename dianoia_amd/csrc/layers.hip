@@ -494,7 +494,8 @@ attention_combine_kernel(const float* __restrict__ ws, const float* __restrict__
 // writes per (token, head) the partial (m, l, o) rows that
 // attention_combine_kernel adds (for long contexts with few query blocks);
 // otherwise it writes the output, gated. fp32 throughout: the sums run in
-// another order than the oracle's, not at lower precision.
+// another order than the oracle's, and the softmax exponentials use the
+// hardware exp2 (__expf, a few ulp) instead of expf.
 constexpr int kPQ = 16;   // queries per wave
 constexpr int kPK = 32;   // keys per tile
 
@@ -622,21 +623,25 @@ attention_prefill_kernel(const float* __restrict__ q, const float* __restrict__ 
     mt = fmaxf(mt, __shfl_xor(mt, 16));
     mt = fmaxf(mt, __shfl_xor(mt, 32));
     const float m_new = fmaxf(m_run, mt);
-    const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+    const float alpha = m_run == -INFINITY ? 0.0f : __expf(m_run - m_new);
     float ps = 0.0f;
 #pragma unroll
     for (int c = 0; c < 2; c++)
 #pragma unroll
       for (int v = 0; v < 4; v++) {
-        p[c][v] = p[c][v] == -INFINITY ? 0.0f : expf(p[c][v] - m_new);
+        p[c][v] = p[c][v] == -INFINITY ? 0.0f : __expf(p[c][v] - m_new);
         ps += p[c][v];
       }
     ps += __shfl_xor(ps, 16);
     ps += __shfl_xor(ps, 32);
     l_run = l_run * alpha + ps;
-    m_run = m_new;
+    // The running sums change only where a max grew (alpha < 1); once the
+    // maxima settle most tiles skip the rescale of the accumulators.
+    if (__any(alpha != 1.0f)) {
 #pragma unroll
-    for (int e = 0; e < HD / 16; e++) o[e] *= alpha;
+      for (int e = 0; e < HD / 16; e++) o[e] *= alpha;
+    }
+    m_run = m_new;
     // O^T += V^T P^T: step s takes keys (s / 4) * 16 + 4 g4 + s % 4.
 #pragma unroll
     for (int c = 0; c < 2; c++) {
