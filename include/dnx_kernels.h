@@ -205,11 +205,14 @@ int dnx_short_conv(const float* bcx, const float* weight, float* history, float*
 // values [positions][kv_heads * hd] (lab_metal.m:414-521), q and out
 // [n][heads][hd], gate [n][heads] or null (ungated); window 0: every earlier
 // position, else the last `window`. hd a multiple of 4 dividing 256; q and
-// keys 16-byte aligned. Decode-shaped calls (fewer than 256 head-token
-// pairs, more than 256 keys) split the keys over workgroups and a combine
-// pass, with a library-owned workspace grown on demand (a first call at a
-// larger shape allocates: not inside a graph capture); otherwise at most
-// dnx_attention_max_keys(hd) keys per token.
+// keys 16-byte aligned. 8+ tokens at hd 64 or 128 with a 16-byte aligned
+// out run on the fp32 matrix cores; decode-shaped calls (fewer than 256
+// head-token pairs, more than 256 keys) split the keys over workgroups.
+// Both may add a combine pass over a library-owned workspace grown on
+// demand: a first call at a larger shape allocates (not inside a graph
+// capture), and calls that overlap (other streams, other threads) must not
+// share the library. Otherwise at most dnx_attention_max_keys(hd) keys per
+// token.
 int64_t dnx_attention_max_keys(int64_t hd);
 int dnx_attention(const float* q, const float* keys, const float* values, const float* gate,
                   float* out, int64_t position, int64_t n, int64_t heads, int64_t kv_heads,
