@@ -10,7 +10,7 @@ token. ``value`` = algorithmic bytes per step (weights at the GGUF Q8_0 size
 of 34 B per 32, x read and y written as fp32) / time, with inputs resident
 in HBM. Two 331 MB weight copies alternate, so the 256 MB Infinity Cache
 cannot serve them. The other configurations (the Q4 MLP pair, the small Q8
-GEMV, the prefill GEMM with its M = 1..64 sweep, BF16 -> Q8 + the vision
+GEMV, the prefill GEMM with its M = 1..256 sweep, BF16 -> Q8 + the vision
 pair) are reported under ``configs``; the prefill GEMM gives the metric's
 TOPS half.
 
@@ -270,9 +270,11 @@ def bench_c3(torch, D, synth, timer, steps, warmup):
            "quantize_ms": b["quantize_ms"], "gemm_tops": ops / b["gemm_ms"] / 1e9,
            "gemm_frac_i8": ops / b["gemm_ms"] / 1e9 / I8_PEAK_TOPS, "gemm_path": best,
            "paths": {k: dict(v, gemm_tops=ops / v["gemm_ms"] / 1e9) for k, v in paths.items()}}
-    # M = 1..64 sweep: GEMV (exact order) up to 4 tokens, GEMM beyond.
+    # M = 1..256 sweep: GEMV (exact order) up to 4 tokens, GEMM beyond. The
+    # batch shapes of the kernels' other callers (audio encoder / generator
+    # and vision attention projections) lie in this range.
     sweep = {}
-    for m in (1, 2, 4, 8, 16, 32, 64):
+    for m in (1, 2, 4, 8, 16, 32, 64, 128, 256):
         xm = xd[:m].contiguous()
         ym = torch.empty((m, N), device="cuda")
         if m <= 4:
