@@ -501,6 +501,28 @@ constexpr int kPK = 32;   // keys per tile
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// Max / sum over lanes i, i ^ 16, i ^ 32 and i ^ 48 (lane i % 16 of the four
+// 16-lane rows), every lane getting the result, on gfx950's VALU lane swaps:
+// with both operands v, permlane16_swap pairs each lane with lane ^ 16 and
+// permlane32_swap with lane ^ 32. No LDS round trip.
+DNX_DEV float rows4_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+DNX_DEV float rows4_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <int HD, int GW>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
 attention_prefill_kernel(const float* __restrict__ q, const float* __restrict__ keys,
@@ -620,8 +642,7 @@ attention_prefill_kernel(const float* __restrict__ q, const float* __restrict__ 
         p[c][v] = ok ? x : -INFINITY;
         mt = fmaxf(mt, p[c][v]);
       }
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    mt = rows4_max(mt);
     const float m_new = fmaxf(m_run, mt);
     const float alpha = m_run == -INFINITY ? 0.0f : __expf(m_run - m_new);
     float ps = 0.0f;
@@ -632,8 +653,7 @@ attention_prefill_kernel(const float* __restrict__ q, const float* __restrict__ 
         p[c][v] = p[c][v] == -INFINITY ? 0.0f : __expf(p[c][v] - m_new);
         ps += p[c][v];
       }
-    ps += __shfl_xor(ps, 16);
-    ps += __shfl_xor(ps, 32);
+    ps = rows4_sum(ps);
     l_run = l_run * alpha + ps;
     // The running sums change only where a max grew (alpha < 1); once the
     // maxima settle most tiles skip the rescale of the accumulators.
