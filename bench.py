@@ -490,11 +490,25 @@ def cpu_baseline(synth, seconds):
         n += 1
     dt = (time.perf_counter() - t0) / n
     algo = q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4
+
+    # The same step on one thread (a few steps; part of the same budget).
+    def step1(i):
+        q, s = sets[i % copies]
+        return orc.argmax(lib.gemm_q8(q, s, x, 1, threads=1, mode=1)[0])
+
+    step1(0)
+    n1, t1 = 0, time.perf_counter()
+    while n1 < 3 or time.perf_counter() - t1 < seconds / 4:
+        step1(n1)
+        n1 += 1
+    dt1 = (time.perf_counter() - t1) / n1
     return {"value": algo / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
             "sample": f"{n} config-2 LM-head steps ({dt * 1e3:.3f} ms each, {copies} rotated "
                       f"weight copies): lab_gemm_q8 mode 1 built from the reference's "
                       f"src/c/lab_native.c on {threads} OpenMP threads + argmaxToken in C",
-            "ms_per_step": dt * 1e3}
+            "ms_per_step": dt * 1e3,
+            "single_thread": {"value": algo / dt1 / 1e9, "unit": "GB/s", "cores": 1,
+                              "ms_per_step": dt1 * 1e3, "steps": n1}}
 
 
 def traffic_from_profiles():
@@ -536,7 +550,8 @@ def pmc_workload(torch, D, synth, reps):
     """Eager launches for the rocprofv3 --pmc runs: a plain device copy of
     PMC_COPY_BYTES (the calibration of FETCH_SIZE / WRITE_SIZE), then the
     config-1 step, the config-2 LM head and the config-3 GEMM, each over
-    rotating weight copies so that every launch reads its weights from HBM."""
+    rotating weight copies so that every launch reads its weights from HBM,
+    then the causal prefill attention of 512 tokens."""
     src = torch.empty(PMC_COPY_BYTES // 4, device="cuda")
     src.fill_(1.0)
     dst = torch.empty_like(src)
@@ -589,7 +604,67 @@ def pmc_workload(torch, D, synth, reps):
         D.gemm_q4(q, s, xq, xsc, y, N, K, M)
         D.gemm_q4_panel(q, s, panel, y, N, K, M)
     torch.cuda.synchronize()
+    del ws
     print("pmc: config 3 done", file=sys.stderr, flush=True)
+
+    # Causal prefill attention, 512 tokens (the layer steps' matrix-core kernel).
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    heads, kv, hd, n = 32, 8, 128, 512
+    q = torch.randn(n * heads * hd, device="cuda", generator=gen)
+    keys = torch.randn((n, kv * hd), device="cuda", generator=gen)
+    values = torch.randn((n, kv * hd), device="cuda", generator=gen)
+    out = torch.empty(n * heads * hd, device="cuda")
+    for i in range(reps):
+        D.attention(q, keys, values, None, out, 0, n, heads, kv, hd, 0)
+    torch.cuda.synchronize()
+    print("pmc: prefill attention done", file=sys.stderr, flush=True)
+
+
+# Matrix-core kernels in the pmc workload -> (workload, ops per launch, peak
+# TOPS of the MFMA type they run on).
+MFMA_KERNELS = {
+    "gemm_kernel<true, 64, 64, 2, 4>": ("c3 Q4 GEMM M=512 (int8 MFMA)", 2 * 512 * 6144 * 2048,
+                                         I8_PEAK_TOPS),
+    "gemm_f16_kernel<true, 3>": ("c3 Q4 GEMM M=512 (fp16 panel)", 2 * 512 * 6144 * 2048,
+                                 I8_PEAK_TOPS),
+    "attention_prefill_kernel<128, 4>": ("prefill attention 512 tokens, 32/8 heads, hd 128",
+                                         4 * 128 * 32 * (512 * 513 // 2), 157.3),
+}
+MFMA_COUNTERS = ("SQ_INSTS_MFMA", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU", "SQ_INSTS_LDS",
+                 "SQ_LDS_BANK_CONFLICT", "SQ_WAIT_INST_LDS", "SQ_BUSY_CU_CYCLES", "SQ_WAVES")
+
+
+def mfma_summary(csv_path, clock_ghz=2.4, simds=1024):
+    """Matrix-core use per launch from one rocprofv3 counter run
+    (MFMA_COUNTERS): mean counters and duration per dispatch of the
+    MFMA_KERNELS, and the fraction of the GPU's SIMD-cycles the matrix
+    cores were busy, SQ_VALU_MFMA_BUSY_CYCLES / (duration x clock x
+    SIMDs), at the peak clock (so a lower bound when the clock drops)."""
+    import csv
+    per = {}
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            frag = next((k for k in MFMA_KERNELS if k in name), None)
+            if frag is None:
+                continue
+            d = per.setdefault(frag, {"name": name, "dispatches": {}, "counters": {}})
+            d["dispatches"][r["Dispatch_Id"]] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            d["counters"].setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    out = {}
+    for frag, d in per.items():
+        workload, ops, peak = MFMA_KERNELS[frag]
+        c = {k: sum(v) / len(v) for k, v in d["counters"].items()}
+        ns = sum(d["dispatches"].values()) / len(d["dispatches"])
+        busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+        out[workload] = {"kernel": d["name"], "launches": len(d["dispatches"]),
+                         "duration_ns_under_counters": round(ns),
+                         "counters_per_launch": {k: round(v) for k, v in c.items()},
+                         "mfma_busy_frac": round(busy / (ns * 1e-9 * clock_ghz * 1e9 * simds), 4),
+                         "ops_per_launch": ops,
+                         "tops_under_counters": round(ops / ns / 1e3, 1),
+                         "frac_of_peak_under_counters": round(ops / ns / 1e3 / peak, 4)}
+    return {"clock_ghz_assumed": clock_ghz, "simds": simds, "kernels": out}
 
 
 def _pmc_means(path, counter):
@@ -684,7 +759,13 @@ def main():
                     help="eager launches for rocprofv3 --pmc runs (no JSON line)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="HBM traffic per launch from two rocprofv3 counter_collection.csv files")
+    ap.add_argument("--mfma-summary", metavar="COUNTER_CSV",
+                    help="matrix-core use per launch from a rocprofv3 counter_collection.csv "
+                         "of the MFMA counters")
     args = ap.parse_args()
+    if args.mfma_summary:
+        print(json.dumps(mfma_summary(args.mfma_summary), indent=1))
+        return
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
         return
