@@ -724,10 +724,11 @@ attention_prefill_kernel(const float* __restrict__ q, const float* __restrict__ 
 
 // The combine for many (token, head) rows and at most 64 splits (prefill):
 // one wave per row, four rows per workgroup, no barrier. Lane s holds split
-// s's statistics; the value sums run in split order with 8 splits' loads in
-// flight, dims lane + 64 i. Rows past the splits read zeros (the resource
+// s's statistics; the value sums run in split order with C splits' loads in
+// flight (the fewest of 2, 4, 8 covering the splits), dims lane + 64 i. Rows past the splits read zeros (the resource
 // ends with the row's last split), and dims past hd are computed but not
 // stored.
+template <int C>  // splits per load batch: 2, 4 or 8
 __global__ void __launch_bounds__(kThreads)
 attention_combine_rows_kernel(const float* __restrict__ ws, const float* __restrict__ gate,
                               float* __restrict__ out, int heads, int hd, int splits, int rows) {
@@ -745,17 +746,17 @@ attention_combine_rows_kernel(const float* __restrict__ ws, const float* __restr
   const float mx = wave_max(m);
   const float f = m == -INFINITY ? 0.0f : expf(m - mx);
   const float l = wave_sum(ls * f);
-  for (int s0 = 0; s0 < splits; s0 += 8) {
-    float v[8][kND];
+  for (int s0 = 0; s0 < splits; s0 += C) {
+    float v[C][kND];
 #pragma unroll
-    for (int u = 0; u < 8; u++)
+    for (int u = 0; u < C; u++)
 #pragma unroll
       for (int i = 0; i < kND; i++)
         v[u][i] = i < nd ? __int_as_float(dnx_raw_buffer_load_i32(
                                rs, ((s0 + u) * row + 4 + lane + 64 * i) * 4, 0, 0))
                          : 0.0f;
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
+    for (int u = 0; u < C; u++) {
       const float fs = __shfl(f, s0 + u);   // 0 past the last split
 #pragma unroll
       for (int i = 0; i < kND; i++) acc[i] += v[u][i] * fs;
@@ -947,9 +948,10 @@ int dnx_attention(const float* q, const float* keys, const float* values, const 
     if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
     if (splits > 1 && splits <= 64) {
       const int64_t rows = n * heads;
-      hipLaunchKernelGGL(attention_combine_rows_kernel, dim3((unsigned)((rows + kWaves - 1) / kWaves)),
-                         dim3(kThreads), 0, st, ws, gate, out, (int)heads, (int)hd, (int)splits,
-                         (int)rows);
+      auto k = splits <= 2 ? attention_combine_rows_kernel<2>
+             : splits <= 4 ? attention_combine_rows_kernel<4> : attention_combine_rows_kernel<8>;
+      hipLaunchKernelGGL(k, dim3((unsigned)((rows + kWaves - 1) / kWaves)), dim3(kThreads), 0, st,
+                         ws, gate, out, (int)heads, (int)hd, (int)splits, (int)rows);
     } else if (splits > 1) {
       hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)heads, (unsigned)n),
                          dim3(kThreads), (size_t)splits * 4, st, ws, gate, out, (int)heads,
