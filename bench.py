@@ -386,7 +386,8 @@ def bench_loaders(torch, D, timer, steps):
     BF16 -> Q4 (lab_quantize_q4 after _widenBf16) on a 32768 x 4096 matrix
     (256 MiB of BF16), and the Q6_K -> Q8 adapter (dequantizeQ6K +
     lab_quantize_q8, gguf.dart:402-414) at the LM-head shape 151936 x 2048,
-    and the GGUF Q8_0 split (splitQ8_0, gguf.dart:270-282) at that shape.
+    and the GGUF Q8_0 split (splitQ8_0, gguf.dart:270-282) at that shape;
+    the north star's BF16 -> Q8 quantizer (part 4) at 32768 x 4096 too.
     Inputs are generated on the GPU; the kernels are HBM-bound."""
     gen = torch.Generator(device="cuda").manual_seed(5)
     wbig = (torch.randn((32768, 4096), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
@@ -405,8 +406,14 @@ def bench_loaders(torch, D, timer, steps):
     count = rows * cols // 32
     gguf = torch.randint(0, 256, (count * 34,), dtype=torch.uint8, device="cuda", generator=gen)
 
+    q8b = torch.empty((32768, 4096), dtype=torch.int8, device="cuda")
+    s8b = torch.empty((32768, 128), device="cuda")
+
     def q4_(i):
         D.quantize_q4_bf16(wbig, q4, d4, 32768, 4096)
+
+    def q8b_(i):
+        D.quantize_q8_bf16(wbig, q8b, s8b, 32768, 4096, 4096)
 
     def q6k_(i):
         D.q6k_to_q8(blocks, q8, s8, rows, cols)
@@ -414,8 +421,9 @@ def bench_loaders(torch, D, timer, steps):
     def split_(i):
         D.split_q8_0(gguf, q8, s8, count)
 
-    means = timer.kernel_means([q4_, q6k_, split_], max(10, steps // 4))
+    means = timer.kernel_means([q4_, q6k_, split_, q8b_], max(10, steps // 4))
     q4_bytes = 32768 * 4096 * 2 + 32768 * 2048 + 32768 * 128 * 2
+    q8b_bytes = 32768 * 4096 * 2 + 32768 * 4096 + 32768 * 128 * 4
     q6k_bytes = rows * cols // 256 * 210 + rows * cols + rows * (cols // 32) * 4
     split_bytes = count * 34 + count * 36
     del wbig, blocks, gguf
@@ -425,8 +433,10 @@ def bench_loaders(torch, D, timer, steps):
             "q6k_to_q8_151936x2048_gbps": q6k_bytes / means[1] / 1e6,
             "split_q8_0_151936x2048_ms": means[2],
             "split_q8_0_151936x2048_gbps": split_bytes / means[2] / 1e6,
+            "bf16_to_q8_32768x4096_ms": means[3],
+            "bf16_to_q8_32768x4096_gbps": q8b_bytes / means[3] / 1e6,
             "bytes": {"bf16_to_q4": q4_bytes, "q6k_to_q8": q6k_bytes,
-                      "split_q8_0": split_bytes}}
+                      "split_q8_0": split_bytes, "bf16_to_q8": q8b_bytes}}
 
 
 def bench_cache_wrap(reps=3):
