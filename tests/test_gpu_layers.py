@@ -92,6 +92,8 @@ def test_short_conv_bit_exact(gpu_ready, orc, width, k, n):
     (8, 8, 128, 500, 40, 64, False),   # matrix cores, one head per KV head, window 64
     (12, 4, 64, 3000, 24, 0, False),   # matrix cores, a long context: many key splits
     (4, 1, 128, 10, 9, 0, True),       # matrix cores, the smallest chunk, 4 heads per KV
+    (8, 2, 64, 0, 64, 0, False),       # matrix cores, hd 64 with 4 heads per KV head
+    (16, 2, 64, 200, 300, 100, True),  # matrix cores, 8 per KV head, window, gate, ragged
 ])
 def test_attention(gpu_ready, orc, heads, kv, hd, pos, n, window, gated):
     rng = np.random.default_rng(heads + hd + pos + n)
