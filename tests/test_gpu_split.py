@@ -120,3 +120,52 @@ def test_upload_gguf_products(gpu_ready, orc, kind, rows, cols, n):
             gpu.upload_gguf("bad", blocks[:-1], rows, cols, kind)
     finally:
         gpu.dispose()
+
+
+def test_split_encoders_at_offsets(gpu_ready, orc):
+    """lab_gpu_enc_split_q8_0 / _q4_0 on buffers at nonzero offsets, both in
+    one command buffer, read back through the host views; a misaligned
+    offset fails the command buffer."""
+    import ctypes
+    from dianoia_amd import _lib
+    lib = _lib.load()
+    assert lib.lab_gpu_init() == 1
+    rng = np.random.default_rng(21)
+    rows, cols = 5, 96
+    count = rows * cols // 32
+    b8 = rng.integers(0, 256, (count, 34), dtype=np.uint8)
+    b4 = rng.integers(0, 256, (count, 18), dtype=np.uint8)
+    handles = []
+
+    def buf(nbytes):
+        h = lib.lab_gpu_buffer(nbytes)
+        assert h >= 0
+        handles.append(h)
+        return h
+
+    def view(h, nbytes):
+        return np.ctypeslib.as_array(
+            ctypes.cast(lib.lab_gpu_contents(h), ctypes.POINTER(ctypes.c_uint8)), (nbytes,))
+
+    try:
+        src = buf(4096)
+        dst = buf(8192)
+        view(src, 4096)[64:64 + b8.size] = b8.reshape(-1)
+        view(src, 4096)[2048:2048 + b4.size] = b4.reshape(-1)
+        lib.lab_gpu_begin()
+        lib.lab_gpu_enc_split_q8_0(src, 64, dst, 16, dst, 1024, rows, cols)
+        lib.lab_gpu_enc_split_q4_0(src, 2048, dst, 2048, dst, 4000, rows, cols)
+        assert lib.lab_gpu_commit(1) == 1
+        out = view(dst, 8192)
+        q8, s8 = orc.split_q8_0(b8, count)
+        q4, d4 = orc.split_q4_0(b4, count)
+        assert np.array_equal(out[16:16 + q8.size], q8.view(np.uint8))
+        assert np.array_equal(out[1024:1024 + 4 * count].view(np.uint32), s8.view(np.uint32))
+        assert np.array_equal(out[2048:2048 + q4.size], q4)
+        assert np.array_equal(out[4000:4000 + 2 * count].view(np.uint16), d4)
+        lib.lab_gpu_begin()
+        lib.lab_gpu_enc_split_q8_0(src, 66, dst, 16, dst, 1024, rows, cols)   # not 4-aligned
+        assert lib.lab_gpu_commit(1) == 0
+    finally:
+        for h in handles:
+            lib.lab_gpu_release(h)
