@@ -252,8 +252,10 @@ quantize_generic_kernel(const void* __restrict__ src, void* __restrict__ qs,
 // multiply by (q - 32) rounds the same exact product once, identically.
 // Then q8_quad, bit-exact.
 //
-// One wave takes one super-block per item (lane L: values 4L..4L+3, one
-// 16-value scale group; 8 lanes per Q8 block). Super-blocks start 2-byte
+// This kernel serves matrices below 64K output blocks (q6k_block_kernel
+// below takes the larger ones). One wave takes one super-block per item
+// (lane L: values 4L..4L+3, one 16-value scale group; 8 lanes per Q8
+// block). Super-blocks start 2-byte
 // aligned (210 = 2 x 105), so lane L loads aligned dword L of the block's
 // span (one coalesced load per lane and item, bounded by the buffer) and
 // each lane gathers its bytes from the wave's registers with ds_bpermute:
@@ -311,6 +313,69 @@ q6k_to_q8_kernel(const uint8_t* __restrict__ src, int8_t* __restrict__ qs,
       }
       q8_quad(make_float4(e[0], e[1], e[2], e[3]), q, qs, scales);
     }
+  }
+}
+
+// The same adapter with one lane per output 32-block (large matrices, as the
+// quantizers' fast path): block j of super-block s (h = j / 4, u = j % 4)
+// takes the 32-byte runs ql[64h + 32(u & 1) ..] (nibble u / 2) and
+// qh[32h ..] (bits 2u, 2u + 1), the scales sc[8h + 2u] (values 0-15) and
+// sc[8h + 2u + 1] (16-31) in one 2-byte load, and d. Each run arrives as 36
+// bytes of 4-byte aligned loads realigned by 0 or 2 bytes (v_alignbyte);
+// none reaches past its super-block. The lane then dequantizes as above and
+// runs lab_quantize_q8's scalar loop on its 32 values: one pair of divisions
+// per block instead of per quad.
+__global__ void __launch_bounds__(kThreads)
+q6k_block_kernel(const uint8_t* __restrict__ src, int8_t* __restrict__ qs,
+                 float* __restrict__ scales, int64_t nblocks, uint32_t src_bytes) {
+  const i32x4 rs = buffer_rsrc(src, src_bytes);
+  for (int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x; b < nblocks;
+       b += (int64_t)gridDim.x * kThreads) {
+    const int j = (int)(b & 7), h = j >> 2, u = j & 3;
+    const int base = (int)((b >> 3) * 210);
+    const int lo_at = base + 64 * h + 32 * (u & 1), hi_at = base + 128 + 32 * h;
+    const uint32_t sh = (uint32_t)(base & 3);   // 0 or 2, the runs' too
+    const uint4 l0 = buffer_load16(rs, lo_at & ~3), l1 = buffer_load16(rs, (lo_at & ~3) + 16);
+    const uint32_t l2 = (uint32_t)dnx_raw_buffer_load_i32(rs, (lo_at & ~3) + 32, 0, 0);
+    const uint4 h0 = buffer_load16(rs, hi_at & ~3), h1 = buffer_load16(rs, (hi_at & ~3) + 16);
+    const uint32_t h2 = (uint32_t)dnx_raw_buffer_load_i32(rs, (hi_at & ~3) + 32, 0, 0);
+    const uint32_t scw = (uint16_t)dnx_raw_buffer_load_i16(rs, base + 192 + 8 * h + 2 * u, 0, 0);
+    const uint32_t dbits = (uint16_t)dnx_raw_buffer_load_i16(rs, base + 208, 0, 0);
+    const uint32_t lw[9] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w, l2};
+    const uint32_t hw[9] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w, h2};
+    const float dd = half_bits_to_float((uint16_t)dbits);
+    const float ds0 = dd * (float)(int8_t)(scw & 0xffu);
+    const float ds1 = dd * (float)(int8_t)(scw >> 8);
+    const int nib = 4 * (u >> 1), bit = 2 * u;
+    float v[32];
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+      const uint32_t ql = __builtin_amdgcn_alignbyte(lw[w + 1], lw[w], sh);
+      const uint32_t qh = __builtin_amdgcn_alignbyte(hw[w + 1], hw[w], sh);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int q = (int)(((ql >> (8 * i + nib)) & 15u) | (((qh >> (8 * i + bit)) & 3u) << 4));
+        v[4 * w + i] = (w < 4 ? ds0 : ds1) * (float)(q - 32);
+      }
+    }
+    // lab_quantize_q8 (lab_native.c:411-427).
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; k++) {
+      const float a = fabsf(v[k]);
+      amax = a > amax ? a : amax;
+    }
+    const float scale = q8_scale(amax);
+    const float inv = q8_inv(scale);
+    uint32_t out[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      out[i] = (uint32_t)quant4(make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]),
+                                inv);
+    uint4* dst = (uint4*)(qs + 32 * b);
+    dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
+    dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
+    scales[b] = scale;
   }
 }
 
@@ -571,6 +636,16 @@ int dnx_q6k_to_q8(const void* blocks, int8_t* qs, float* scales, int64_t rows, i
   // 32-bit buffer offsets into the blocks.
   if (rows * (cols / 256) * 210 >= (1ll << 31)) return DNX_EINVAL;
   if (rows == 0) return DNX_OK;
+  const int64_t nblocks = rows * (cols / 32);
+  if (nblocks >= 65536 && ((uintptr_t)blocks & 3) == 0 && ((uintptr_t)qs & 15) == 0) {
+    // One lane per 32-block: fewer instructions per value at large sizes.
+    int64_t grid = (nblocks + kThreads - 1) / kThreads;
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(q6k_block_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream,
+                       (const uint8_t*)blocks, qs, scales, nblocks,
+                       (uint32_t)(rows * (cols / 256) * 210));
+    return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+  }
   const int grid = quantizer_grid(rows * (cols / 4));
   hipLaunchKernelGGL(q6k_to_q8_kernel, dim3(grid), dim3(kThreads), 0, stream,
                      (const uint8_t*)blocks, qs, scales, rows, cols);

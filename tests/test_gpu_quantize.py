@@ -193,7 +193,8 @@ def gpu_q6k_to_q8(blocks, rows, cols):
 
 
 @pytest.mark.parametrize("rows,cols,raw", [(1, 256, False), (37, 2048, False), (4096, 2048, False),
-                                           (64, 1024, True), (3, 4096, True)])
+                                           (64, 1024, True), (3, 4096, True),
+                                           (2048, 2048, True), (300, 7168, True)])
 def test_q6k_to_q8_matches_oracle(gpu_ready, orc, rows, cols, raw):
     from q6k_util import pack_q6k, random_blocks
     rng = np.random.default_rng(rows + cols + raw)
