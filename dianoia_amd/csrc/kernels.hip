@@ -358,13 +358,12 @@ q6k_block_kernel(const uint8_t* __restrict__ src, int8_t* __restrict__ qs,
         v[4 * w + i] = (w < 4 ? ds0 : ds1) * (float)(q - 32);
       }
     }
-    // lab_quantize_q8 (lab_native.c:411-427).
+    // lab_quantize_q8 (lab_native.c:411-427). The values are products of
+    // converted floats, so any NaN among them is quiet, and v_max_f32 keeps
+    // the non-NaN operand as `a > amax` does.
     float amax = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 32; k++) {
-      const float a = fabsf(v[k]);
-      amax = a > amax ? a : amax;
-    }
+    for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(v[k]));
     const float scale = q8_scale(amax);
     const float inv = q8_inv(scale);
     uint32_t out[8];
