@@ -93,6 +93,13 @@ SIGNATURES = {
     "dnx_quantize_q8_panel": ([_p, _p, _i64, _i64, _p], _i32),
     "dnx_gemm_q8_panel": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_q4_panel": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dnx_f6_panel_bytes": ([_i64, _i64], _i64),
+    "dnx_quantize_q8_f6panel": ([_p, _p, _i64, _i64, _p], _i32),
+    "dnx_pack_f6panel": ([_p, _p, _p, _i64, _i64, _p], _i32),
+    "dnx_gemm_q4_f6": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dnx_q4_f6pack_bytes": ([_i64, _i64], _i64),
+    "dnx_pack_q4_f6": ([_p, _p, _p, _i64, _i64, _p], _i32),
+    "dnx_gemm_q4_f6p": ([_p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_argmax_workspace_bytes": ([_i64], _i64),
     "dnx_argmax": ([_p, _i64, _p, _p, _p], _i32),
     "dnx_swiglu": ([_p, _p, _i64, _p], _i32),

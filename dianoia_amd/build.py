@@ -17,7 +17,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libdianoia_amd.so")
-SOURCES = ["kernels.hip", "gemv.hip", "gemm.hip", "gemm_f16.hip", "layers.hip", "lab_gpu.hip"]
+SOURCES = ["kernels.hip", "gemv.hip", "gemm.hip", "gemm_f16.hip", "gemm_f6.hip", "layers.hip",
+           "lab_gpu.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -34,7 +35,8 @@ FLAGS = [
 # Per-source flags. The GEMM keeps its MFMA results in ordinary VGPRs: its
 # scale epilogue reads every result with VALU instructions, which cannot
 # take accumulation registers (one v_accvgpr_read per value otherwise).
-SOURCE_FLAGS = {src: ["-mllvm", "-amdgpu-mfma-vgpr-form=1"] for src in ("gemm.hip", "gemm_f16.hip")}
+SOURCE_FLAGS = {src: ["-mllvm", "-amdgpu-mfma-vgpr-form=1"] for src in ("gemm.hip", "gemm_f16.hip",
+                                                                       "gemm_f6.hip")}
 
 
 def _compile(src: str, build_dir: str) -> str:

@@ -1,0 +1,863 @@
+// Prefill / encoder GEMM for Q4 weights on the gfx950 fp6 matrix cores:
+//   y[m][r] = sum_b sx[m][b] * sw[r][b] * D_b[m][r],
+//   D_b[m][r] = sum over block b of xq[m][k] * (q[r][k] - 8)   (exact integer)
+// with xq, sx exactly lab_quantize_q8's (lab_native.c:407-429) and the
+// product of lab_gemm_q4 mode 1 (lab_native.c:1059-1080) up to the fp32
+// rounding of the scaled sum.
+//
+// The block dot on one scaled fp6 MFMA. v_mfma_scale_f32_32x32x64_f8f6f4
+// multiplies 32 x 64 by 64 x 32 operands of 6-bit floats, each lane's 32
+// values carrying its own power-of-two (E8M0) scale, in 33 clocks: twice the
+// int8 MFMA's multiply-adds per clock. Both factors of a block dot are
+// exact in it:
+//   * a Q4 nibble q in 0..15 is the fp6 E2M3 code of q / 8 (codes 0..15 are
+//     the subnormals and the first binade, value = code / 8), so a weight
+//     needs no arithmetic beyond moving its 4 bits into a 6-bit field;
+//   * |xq| <= 127 splits as 8 h + l (h in 0..15, l in 0..7), both E2M3
+//     codes with the sign of xq. The 64 K slots hold the block twice:
+//     slots 0..31 pair the h codes (scale 2^6) with the weights (scale
+//     2^3), slots 32..63 the l codes (scale 2^3) with the weights again;
+//   * the -8 of q - 8 enters as the MFMA's C input, -8 * sum(xq) per token.
+// Every product and partial sum is an integer below 2^24, so D_b is exact.
+// The activation scale's exponent rides in the same E8M0 scale (2^e_x),
+// leaving mant(sx) in [1, 2): the scale product s = mant(sx) * sw comes from
+// one v_mfma_f32_32x32x8_f16 used as an outer product (mant(sx) as three
+// fp16 pieces that sum to it exactly, sw as its own fp16 bits), and the
+// epilogue is one fma per output per block, blocks in order.
+// Per 32 x 32 tile and block: 33 + 32 MFMA clocks and 16 fma, against 64 + 32
+// MFMA clocks for the fp16 form (gemm_f16.hip).
+//
+// Operands.
+//   Activations: a "f6 panel" written by the quantizer below from fp32 x
+//   (or from xq + xsc), per 32 tokens and block (kRec bytes): 64 lanes x
+//   32 B in MFMA lane order (6 dwords of fp6 codes, then the scale MFMA's
+//   four fp16 operand slots, the E8M0 scale byte riding in the third: see
+//   write_f6_entries), and the 32 tokens' C values. A wave loads its
+//   tokens' 32-byte lane records straight into registers, four blocks
+//   ahead; the C values are staged through LDS with the weights.
+//   Weights: staged through LDS once per workgroup, shared by its 8 waves:
+//   each 16-byte Q4 block becomes 6 dwords of fp6 codes with 16 VALU
+//   operations (kFieldK below is the resulting order of the weights in the
+//   fields; the panel writes the activations in the same order), next to
+//   the scale MFMA's operand (sw, sw, sw, 0).
+//
+// Workgroup: 512 threads, 128 tokens x SN * 32 weight rows. Wave w takes
+// the 32 tokens (w % 4) and every other block (parity w / 4), so the two
+// waves of a SIMD work on the same outputs and one hides the other's
+// latencies; their sums are added at the end through LDS in a fixed order.
+
+#include "common.h"
+#include "dnx_kernels.h"
+
+using namespace dnx;
+
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPanelThreads = 256;
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
+constexpr int kTokens = 32;                 // tokens per panel group (one MFMA tile)
+constexpr int kRecF = 0;                    // 64 lanes x 32 B: fp6 codes + operand dwords
+constexpr int kRecC = 2048;                 // 2 halves x 16 floats: the MFMA's C input
+constexpr int kRec = 2176;                  // panel bytes per (32 tokens, block)
+
+// The weight index held by each of a block's 32 fp6 fields after
+// q4_to_f6 (below) and so the order in which the panel lays out the
+// activations: field f of the 192-bit operand holds weight kFieldK[f].
+__constant__ const int8_t kFieldK[32] = {0,  20, 17, 6,  3,  23, 16, 5,  2,  22, 19,
+                                         4,  1,  21, 18, 7,  8,  28, 25, 14, 11, 31,
+                                         24, 13, 10, 30, 27, 12, 9,  29, 26, 15};
+constexpr int8_t kFieldKHost[32] = {0,  20, 17, 6,  3,  23, 16, 5,  2,  22, 19,
+                                    4,  1,  21, 18, 7,  8,  28, 25, 14, 11, 31,
+                                    24, 13, 10, 30, 27, 12, 9,  29, 26, 15};
+
+// Two dwords of Q4 nibbles (a: weights 4j.., b: the next dword) -> three
+// dwords of 6-bit fields, each nibble under two zero bits (the E2M3 code of
+// q / 8). Nibbles of a at bits 0, 12, 24 / 4, 16, 28 / 8, 20 stay where
+// they are in the first / second / third output dword; nibbles of b move up
+// by two bits (4 -> 6, ..., 28 -> 30 with its top half carried to the next
+// dword's bits 0-1).
+DNX_DEV void q4_group_to_f6(uint32_t a, uint32_t b, uint32_t* o) {
+  const uint32_t t = b << 2;
+  o[0] = (a & 0x0F00F00Fu) | (t & 0xC03C03C0u);
+  o[1] = (a & 0xF00F00F0u) | (t & 0x03C03C00u) | (b >> 30);
+  o[2] = (a & 0x00F00F00u) | (t & 0x3C03C03Cu);
+}
+
+// ---------------------------------------------------------------- the panel
+
+// One (token, block): its 32 quantized values -> the panel record entries
+// of lane (token, 0) (h codes), lane (token, 1) (l codes), the scale
+// MFMA operand and the C value.
+DNX_DEV void write_f6_entries(uint8_t* rec, int r, const int* xq, float scale) {
+  int sum = 0;
+#pragma unroll
+  for (int k = 0; k < 32; k++) sum += xq[k];
+  // scale = 2^e * mant, mant in [1, 2); a subnormal scale keeps e = -126
+  // and mant < 1 (its products lie far below any fp32 result's ulp).
+  const uint32_t bits = __float_as_uint(scale);
+  const int ef = (int)((bits >> 23) & 0xff);
+  int e = ef == 0 ? -126 : ef - 127;
+  float mant = ef == 0 ? scale * 0x1p126f : __uint_as_float((bits & 0x807fffffu) | 0x3f800000u);
+  if (scale == 0.0f) {
+    e = 0;
+    mant = 0.0f;
+  }
+  // mant = p0 + p1 + p2 exactly (for mant in [1, 2): 11 + 11 + 2 bits).
+  const _Float16 p0 = (_Float16)mant;
+  const float r1 = mant - (float)p0;
+  const _Float16 p1 = (_Float16)r1;
+  const _Float16 p2 = (_Float16)(r1 - (float)p1);
+  uint32_t hw[6] = {0, 0, 0, 0, 0, 0}, lw[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int f = 0; f < 32; f++) {
+    const int v = xq[kFieldKHost[f]];
+    const uint32_t a = (uint32_t)(v < 0 ? -v : v);
+    const uint32_t sg = v < 0 ? 0x20u : 0u;
+    const uint32_t hc = sg | (a >> 3), lc = sg | (a & 7u);
+    const int bit = 6 * f, wd = bit >> 5, sh = bit & 31;
+    hw[wd] |= hc << sh;
+    lw[wd] |= lc << sh;
+    if (sh > 26) {  // the field runs into the next dword
+      hw[wd + 1] |= hc >> (32 - sh);
+      lw[wd + 1] |= lc >> (32 - sh);
+    }
+  }
+  // E8M0 scales: 2^(6 + e) for the h codes (value h / 8 -> 8 h), 2^(3 + e)
+  // for the l codes.
+  const uint32_t sh_h = (uint32_t)(127 + 6 + e), sh_l = (uint32_t)(127 + 3 + e);
+  // Dwords 6-7: the scale MFMA's fp16 slots (p0, p1, E8M0 byte, p2) on the
+  // h lanes and (0, 0, E8M0 byte, 0) on the l lanes. The weights' slots are
+  // (sw, sw, 0, sw), so the byte's slot (a finite subnormal) meets a zero,
+  // and the fp6 MFMA reads the byte as its scale operand (byte 0 of dword 7).
+  const uint32_t s0 = (uint32_t)__builtin_bit_cast(uint16_t, p0) |
+                      ((uint32_t)__builtin_bit_cast(uint16_t, p1) << 16);
+  const uint32_t s1 = sh_h | ((uint32_t)__builtin_bit_cast(uint16_t, p2) << 16);
+  uint4* fh = (uint4*)(rec + kRecF + r * 32);
+  uint4* fl = (uint4*)(rec + kRecF + (32 + r) * 32);
+  fh[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  fh[1] = make_uint4(hw[4], hw[5], s0, s1);
+  fl[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  fl[1] = make_uint4(lw[4], lw[5], 0u, sh_l);
+  // C of output row r: lanes of half (r / 4) % 2 hold it at 4 (r / 8) + r % 4.
+  const float c = sum == 0 ? 0.0f : ldexpf((float)(-8 * sum), e);
+  *(float*)(rec + kRecC + ((((r >> 2) & 1) * 16 + (r >> 3) * 4 + (r & 3)) * 4)) = c;
+}
+
+// fp32 x [n][cols] -> f6 panel [groups][B][kRec]: lab_quantize_q8 of each
+// (token, block) (the same xq and scale bits as dnx_quantize_q8), then its
+// panel entries. One thread per (token, block); consecutive threads take
+// consecutive tokens of a group, so the record writes are contiguous.
+__global__ void __launch_bounds__(kPanelThreads) quantize_f6_panel_kernel(
+    const float* __restrict__ x, uint8_t* __restrict__ panel, int n, int cols, int groups) {
+  const int B = cols / kBlock;
+  const int64_t total = (int64_t)groups * B * kTokens;
+  for (int64_t idx = (int64_t)blockIdx.x * kPanelThreads + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * kPanelThreads) {
+    const int r = (int)(idx & (kTokens - 1));
+    const int64_t gb = idx >> 5;
+    const int b = (int)(gb % B);
+    const int g = (int)(gb / B);
+    const int m = g * kTokens + r;
+    float4 v[8];
+    const bool live = m < n;
+    const float4* src = (const float4*)(x + (int64_t)(live ? m : 0) * cols + b * kBlock);
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = live ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, max4abs(v[i]));
+    const float scale = q8_scale(amax);
+    const float inv = q8_inv(scale);
+    int xq[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      xq[4 * i] = quant1(v[i].x, inv);
+      xq[4 * i + 1] = quant1(v[i].y, inv);
+      xq[4 * i + 2] = quant1(v[i].z, inv);
+      xq[4 * i + 3] = quant1(v[i].w, inv);
+    }
+    write_f6_entries(panel + gb * kRec, r, xq, scale);
+  }
+}
+
+// The same panel from already quantized xq int8 [n][cols] + xsc [n][cols/32].
+__global__ void __launch_bounds__(kPanelThreads) pack_f6_panel_kernel(
+    const int8_t* __restrict__ xq, const float* __restrict__ xsc, uint8_t* __restrict__ panel,
+    int n, int cols, int groups) {
+  const int B = cols / kBlock;
+  const int64_t total = (int64_t)groups * B * kTokens;
+  for (int64_t idx = (int64_t)blockIdx.x * kPanelThreads + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * kPanelThreads) {
+    const int r = (int)(idx & (kTokens - 1));
+    const int64_t gb = idx >> 5;
+    const int b = (int)(gb % B);
+    const int g = (int)(gb / B);
+    const int m = g * kTokens + r;
+    int q[32];
+    float scale = 0.0f;
+    if (m < n) {
+      const uint4* src = (const uint4*)(xq + (int64_t)m * cols + b * kBlock);
+      const uint4 lo = src[0], hi = src[1];
+      const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int k = 0; k < 32; k++) q[k] = (int)(int8_t)(w[k >> 2] >> (8 * (k & 3)));
+      scale = xsc[(int64_t)m * B + b];
+    } else {
+#pragma unroll
+      for (int k = 0; k < 32; k++) q[k] = 0;
+    }
+    write_f6_entries(panel + gb * kRec, r, q, scale);
+  }
+}
+
+// ----------------------------------------------------------------- the GEMM
+
+struct F6Params {
+  const uint8_t* qs;       // Q4 nibbles [rows][cols/2]
+  const uint16_t* scales;  // fp16 bits [rows][cols/32]
+  const uint8_t* panel;    // f6 panel of the n tokens
+  float* y;                // [n][rows]
+  float* part;             // split partials [splits][n][rows], or null
+  int rows, cols, n;
+  int tiles_m, tiles;      // workgroup tiles (128 tokens x BN rows) of one K split
+  int split_blocks;        // blocks per K split (blockIdx.y), a multiple of kKB
+};
+
+constexpr int kTileM = 4;   // 32-token groups per workgroup
+constexpr int kKB = 16;     // blocks per stage
+constexpr int kRecW = 32;   // LDS bytes per staged (row, block): 6 fp6 dwords + 2 operand dwords
+constexpr int kRing = 4;    // activation records in flight per wave (its next blocks)
+
+template <int SN>
+__global__ void __launch_bounds__(kThreads) gemm_f6_q4_kernel(F6Params p) {
+  constexpr int BN = SN * 32;
+  constexpr int RS = kKB * kRecW + 16;          // LDS bytes per staged weight row (bank spread)
+  constexpr int kW = BN * RS;                   // staged weights of a stage
+  constexpr int kC = kTileM * kKB * 128;        // staged C inputs of a stage
+  constexpr int kStage = kW + kC;
+  constexpr int kPairs = BN * kKB;              // (row, block) per stage
+  constexpr int PP = (kPairs + kThreads - 1) / kThreads;
+  constexpr int kCPieces = kC / 16;
+  constexpr int CP = (kCPieces + kThreads - 1) / kThreads;
+  constexpr int kRed = kTileM * SN * 16 * 64 * 4;  // the odd parity's sums
+  constexpr int kLds = 2 * kStage > kRed ? 2 * kStage : kRed;
+  static_assert((kKB / 2) % kRing == 0, "ring slots must repeat each stage");
+  __shared__ __align__(16) uint8_t lds[kLds];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int mg = wave & 3, kp = wave >> 2;
+  const int K = p.cols, B = K / kBlock, M = p.n, N = p.rows;
+
+  // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs, so
+  // workgroup i runs tile (i % 8) * (tiles / 8) + i / 8 and each XCD walks a
+  // contiguous run of tiles (all token groups of consecutive weight rows).
+  const int i = blockIdx.x;
+  const int t = (p.tiles % 8 == 0) ? (i % 8) * (p.tiles / 8) + i / 8 : i;
+  const int tm = t % p.tiles_m, tn = t / p.tiles_m;
+  const int n0 = tn * BN;
+  const int groups = (M + kTokens - 1) / kTokens;
+  const int g = tm * kTileM + mg;                // this wave's token group
+  const int b_begin = blockIdx.y * p.split_blocks;
+  const int b_end = min(B, b_begin + p.split_blocks);
+  const int stages = (b_end - b_begin + kKB - 1) / kKB;
+
+  const i32x4 rpanel = buffer_rsrc(p.panel, (uint32_t)((size_t)groups * B * kRec));
+  const i32x4 rqs = buffer_rsrc(p.qs, (uint32_t)((size_t)N * (K / 2)));
+  const i32x4 rsc = buffer_rsrc(p.scales, (uint32_t)((size_t)N * B * 2));
+
+  // ---- staging of a stage: weights as (row j, block kb) pairs, kb fastest
+  // (coalesced rows), and the C inputs of the workgroup's 4 token groups.
+  // Offsets are recomputed per stage from the thread index (few registers).
+  uint4 rq[PP];
+  short rs[PP];
+  float4 rc[CP];
+  // Loads of stage s; blocks past this split's end read zeros.
+  auto load_stage = [&](int s) {
+    const int b0 = b_begin + s * kKB;
+#pragma unroll
+    for (int e = 0; e < PP; e++) {
+      const int q = e * kThreads + tid;
+      const int j = q / kKB, b = b0 + (q - j * kKB);
+      const bool ok = q < kPairs && n0 + j < N && b < b_end;
+      rq[e] = buffer_load16(rqs, ok ? (n0 + j) * (K / 2) + b * 16 : -64);
+      rs[e] = dnx_raw_buffer_load_i16(rsc, ok ? ((n0 + j) * B + b) * 2 : -4, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < CP; e++) {
+      const int q = e * kThreads + tid;        // 16-byte piece: (group, block, piece of 8)
+      const int gg = q / (kKB * 8), b = b0 + (q / 8) % kKB;
+      const bool ok = q < kCPieces && tm * kTileM + gg < groups && b < b_end;
+      rc[e] = buffer_load_f4(rpanel,
+                             ok ? ((tm * kTileM + gg) * B + b) * kRec + kRecC + (q % 8) * 16 : -64);
+    }
+  };
+  auto store_stage = [&](int buf) {
+    uint8_t* base = lds + buf * kStage;
+#pragma unroll
+    for (int e = 0; e < PP; e++) {
+      const int q = e * kThreads + tid;
+      if (q >= kPairs) continue;
+      const int j = q / kKB, kb = q - j * kKB;
+      uint32_t f[6];
+      q4_group_to_f6(rq[e].x, rq[e].y, f);
+      q4_group_to_f6(rq[e].z, rq[e].w, f + 3);
+      const uint32_t sw = (uint32_t)(uint16_t)rs[e];
+      uint4* d = (uint4*)(base + j * RS + kb * kRecW);
+      d[0] = make_uint4(f[0], f[1], f[2], f[3]);
+      // The scale MFMA's weight slots (sw, sw, 0, sw).
+      d[1] = make_uint4(f[4], f[5], sw | (sw << 16), sw << 16);
+    }
+#pragma unroll
+    for (int e = 0; e < CP; e++) {
+      const int q = e * kThreads + tid;
+      if (q >= kCPieces) continue;
+      const int gg = q / (kKB * 8), kb = (q / 8) % kKB;
+      *(float4*)(base + kW + (gg * kKB + kb) * 128 + (q % 8) * 16) = rc[e];
+    }
+  };
+
+  // ---- this wave's activation lane records, kRing blocks ahead
+  const bool live = g < groups;
+  // Out-of-range blocks (past this split, or a token group past n) read
+  // zeros through an offset past the resource. The select is arithmetic:
+  // a branch here splits the loop into blocks the scheduler cannot cross.
+  auto load_a = [&](int b, i32x4& lo, i32x4& hi) {
+    const int ok = -(int)(live & (b < b_end));
+    const int base = (((g * B + b) * kRec + kRecF) & ok) | (~ok & -(1 << 20));
+    lo = dnx_raw_buffer_load_v4i32(rpanel, base + lane * 32, 0, 0);
+    hi = dnx_raw_buffer_load_v4i32(rpanel, base + lane * 32 + 16, 0, 0);
+  };
+
+  v16f acc[SN];
+#pragma unroll
+  for (int j = 0; j < SN; j++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[j][v] = 0.0f;
+
+  // One block of this wave: SN tiles, each an fp6 MFMA (the exact dot with
+  // the -8 sum(xq) C input, scaled by 2^e_x), an f16 outer-product MFMA
+  // (mant(sx) * sw) and 16 fma. Software-pipelined over (block, tile): the
+  // fmas of a tile run after the next tile's MFMAs are issued (the last
+  // tile's fmas open the next block), and a tile's weight fragment is read
+  // from LDS while the previous tile's fmas run.
+  v16f pd, ps;  // MFMA results of the tile before, not yet folded
+  auto fold = [&](int j) {
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[j][v] = fmaf(pd[v], ps[v], acc[j][v]);
+  };
+  auto compute = [&](const uint8_t* sbase, int kb, i32x4 lo, i32x4 hi, bool first) {
+    // The MFMA wants the 6 code dwords in consecutive registers; the two
+    // loads land apart, so the compiler copies one half next to the other.
+    // Defining both halves here keeps that copy (which waits for its load)
+    // at the point of use, blocks after the load, not right behind it.
+    asm volatile("" : "+v"(lo), "+v"(hi));
+    const v8i a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    const int sa = hi[3];  // byte 0: the E8M0 scale
+    const h4 as = __builtin_bit_cast(h4, make_uint2((uint32_t)hi[2], (uint32_t)hi[3]));
+    const float* cp = (const float*)(sbase + kW + (mg * kKB + kb) * 128 + (lane >> 5) * 64);
+    const uint8_t* wrow = sbase + (lane & 31) * RS + kb * kRecW;
+    v16f c;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float4 cv = *(const float4*)(cp + 4 * j);
+      c[4 * j] = cv.x;
+      c[4 * j + 1] = cv.y;
+      c[4 * j + 2] = cv.z;
+      c[4 * j + 3] = cv.w;
+    }
+    uint4 w0 = *(const uint4*)wrow, w1 = *(const uint4*)(wrow + 16);
+#pragma unroll
+    for (int j = 0; j < SN; j++) {
+      const v8i bq = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, 0, 0};
+      const h4 bs = __builtin_bit_cast(h4, make_uint2(w1.z, w1.w));
+      const v16f z = {};
+      const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(as, bs, z, 0, 0, 0);
+      const v16f d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bq, c, 2, 2, 0, sa, 0, 130);
+      if (j + 1 < SN) {
+        w0 = *(const uint4*)(wrow + (j + 1) * 32 * RS);
+        w1 = *(const uint4*)(wrow + (j + 1) * 32 * RS + 16);
+      }
+      if (j > 0) {
+        fold(j - 1);
+      } else if (!first) {
+        fold(SN - 1);
+      }
+      pd = d;
+      ps = sc;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // ---- main loop: stages of kKB blocks; this wave takes blocks of its parity
+  i32x4 rlo[kRing], rhi[kRing];
+#pragma unroll
+  for (int r = 0; r < kRing; r++) load_a(b_begin + kp + 2 * r, rlo[r], rhi[r]);
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  bool first = true;
+  for (int s = 0; s < stages; s++) {
+    const int buf = s & 1;
+    if (s + 1 < stages) load_stage(s + 1);
+    const uint8_t* sbase = lds + buf * kStage;
+    const int b0 = b_begin + s * kKB;
+#pragma unroll 1
+    for (int u0 = 0; u0 < kKB / 2; u0 += kRing) {
+#pragma unroll
+      for (int r = 0; r < kRing; r++) {
+        const int kb = kp + 2 * (u0 + r);
+        compute(sbase, kb, rlo[r], rhi[r], first);
+        first = false;
+        load_a(b0 + kb + 2 * kRing, rlo[r], rhi[r]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (s + 1 < stages) store_stage(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (!first) fold(SN - 1);
+
+  // ---- the two parities' sums, added in a fixed order (even + odd)
+  float* red = (float*)lds + (size_t)mg * SN * 16 * 64;
+  if (kp == 1) {
+#pragma unroll
+    for (int j = 0; j < SN; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) red[(j * 16 + v) * 64 + lane] = acc[j][v];
+  }
+  __syncthreads();
+  if (kp == 1 || !live) return;
+  float* out = p.part ? p.part + (size_t)blockIdx.y * M * N : p.y;
+#pragma unroll
+  for (int j = 0; j < SN; j++) {
+    const int r = n0 + j * 32 + (lane & 31);
+    if (r >= N) continue;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int m = g * kTokens + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+      if (m < M) out[(size_t)m * N + r] = acc[j][v] + red[(j * 16 + v) * 64 + lane];
+    }
+  }
+}
+
+// ----------------------------------------------- prepacked weights (load time)
+//
+// The engine's Q4 layout needs 16 VALU operations per 32 weights to become
+// fp6 fields, and its -8 offset costs the MFMA a C input (16 more register
+// reads per tile). Weights are immutable after upload, so they can be
+// re-encoded once: per (row, block) 32 bytes, the E2M3 codes of the signed
+// weights w = q - 8 (sign bit, |w| in 0..8 as the code of |w| / 8) in the
+// fields' order, then the scale MFMA's slots (sw, sw, 0, sw). The GEMM on
+// that layout stages it to LDS with plain copies and runs the dot without a
+// C input.
+
+DNX_DEV uint32_t f6_signed_code(uint32_t q) {
+  return q >= 8 ? q - 8 : 0x20u | (8 - q);
+}
+
+// One thread per (row, block): 16 nibble bytes + the fp16 scale -> 32 bytes.
+__global__ void __launch_bounds__(kPanelThreads) pack_q4_f6_kernel(
+    const uint8_t* __restrict__ qs, const uint16_t* __restrict__ scales,
+    uint8_t* __restrict__ out, int64_t count) {
+  for (int64_t i = (int64_t)blockIdx.x * kPanelThreads + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * kPanelThreads) {
+    const uint4 v = *(const uint4*)(qs + i * 16);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int f = 0; f < 32; f++) {
+      const int k = kFieldKHost[f];
+      const int byte = k & 15;
+      const uint32_t q = (w[byte >> 2] >> (8 * (byte & 3) + (k >= 16 ? 4 : 0))) & 15u;
+      const uint32_t c = f6_signed_code(q);
+      const int bit = 6 * f, wd = bit >> 5, sh = bit & 31;
+      o[wd] |= c << sh;
+      if (sh > 26) o[wd + 1] |= c >> (32 - sh);
+    }
+    const uint32_t sw = scales[i];
+    uint4* d = (uint4*)(out + i * 32);
+    d[0] = make_uint4(o[0], o[1], o[2], o[3]);
+    d[1] = make_uint4(o[4], o[5], sw | (sw << 16), sw << 16);
+  }
+}
+
+constexpr int kPKB = 16;    // blocks per stage of the prepacked GEMM
+
+struct F6PParams {
+  const uint8_t* packed;   // [rows][cols/32][32 B]
+  const uint8_t* panel;    // f6 panel of the n tokens
+  float* y;
+  float* part;
+  int rows, cols, n;
+  int tiles_m, tiles;
+  int split_blocks;        // a multiple of kPKB
+};
+
+template <int SN>
+__global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
+  constexpr int BN = SN * 32;
+  constexpr int kHalf = BN * 16 + 16;           // one (block, half): BN rows x 16 B (+ bank pad)
+  constexpr int kStage = kPKB * 2 * kHalf;
+  constexpr int kPieces = BN * kPKB * 2;        // 16-byte pieces per stage
+  constexpr int PW = (kPieces + kThreads - 1) / kThreads;
+  constexpr int kRed = kTileM * SN * 16 * 64 * 4;
+  constexpr int kLds = 2 * kStage > kRed ? 2 * kStage : kRed;
+  __shared__ __align__(16) uint8_t lds[kLds];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int mg = wave & 3, kp = wave >> 2;
+  const int K = p.cols, B = K / kBlock, M = p.n, N = p.rows;
+
+  const int i = blockIdx.x;
+  const int t = (p.tiles % 8 == 0) ? (i % 8) * (p.tiles / 8) + i / 8 : i;
+  const int tm = t % p.tiles_m, tn = t / p.tiles_m;
+  const int n0 = tn * BN;
+  const int groups = (M + kTokens - 1) / kTokens;
+  const int g = tm * kTileM + mg;
+  const int b_begin = blockIdx.y * p.split_blocks;
+  const int b_end = min(B, b_begin + p.split_blocks);
+  const int stages = (b_end - b_begin + kPKB - 1) / kPKB;
+  const i32x4 rpanel = buffer_rsrc(p.panel, (uint32_t)((size_t)groups * B * kRec));
+
+  // Staging of a stage through registers: thread q of a pass takes the
+  // 16-byte half (q % 2) of record (row, block) with the block and half
+  // fastest, so a wave reads 1 KB of consecutive records; the halves go to
+  // LDS [block][half][row][16 B] (rows consecutive: conflict-free reads of a
+  // tile's 32 rows). Rows past the matrix and blocks past this split read a
+  // valid row / block instead (clamped): their products meet zero
+  // activations or are never stored.
+  const i32x4 rpk = buffer_rsrc(p.packed, (uint32_t)((size_t)N * B * 32));
+  i32x4 rw[PW];
+  auto load_w = [&](int s) {
+    const int b0 = b_begin + s * kPKB;
+#pragma unroll
+    for (int e = 0; e < PW; e++) {
+      const int q = e * kThreads + tid;
+      const int h = q & 1, kb = (q >> 1) % kPKB, row = (q >> 1) / kPKB;
+      const int b = min(b0 + kb, b_end - 1);
+      const int grow = min(n0 + row, N - 1);
+      rw[e] = dnx_raw_buffer_load_v4i32(rpk, ((grow * B + b) * 32 + h * 16) | (q < kPieces ? 0 : -(1 << 30)), 0, 0);
+    }
+  };
+  auto store_w = [&](int buf) {
+#pragma unroll
+    for (int e = 0; e < PW; e++) {
+      const int q = e * kThreads + tid;
+      if (q >= kPieces) continue;
+      const int h = q & 1, kb = (q >> 1) % kPKB, row = (q >> 1) / kPKB;
+      *(i32x4*)(lds + buf * kStage + (kb * 2 + h) * kHalf + row * 16) = rw[e];
+    }
+  };
+
+  const bool live = g < groups;
+  auto load_a = [&](int b, i32x4& lo, i32x4& hi) {
+    const int ok = -(int)(live & (b < b_end));
+    const int base = (((g * B + b) * kRec + kRecF) & ok) | (~ok & -(1 << 20));
+    lo = dnx_raw_buffer_load_v4i32(rpanel, base + lane * 32, 0, 0);
+    hi = dnx_raw_buffer_load_v4i32(rpanel, base + lane * 32 + 16, 0, 0);
+  };
+
+  v16f acc[SN];
+#pragma unroll
+  for (int j = 0; j < SN; j++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[j][v] = 0.0f;
+  v16f pd, ps;
+  auto fold = [&](int j) {
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[j][v] = fmaf(pd[v], ps[v], acc[j][v]);
+  };
+  auto compute = [&](const uint8_t* sbase, int kb, i32x4 lo, i32x4 hi, bool first) {
+    asm volatile("" : "+v"(lo), "+v"(hi));
+    const v8i a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    const int sa = hi[3];
+    const h4 as = __builtin_bit_cast(h4, make_uint2((uint32_t)hi[2], (uint32_t)hi[3]));
+    const uint8_t* w0p = sbase + (kb * 2) * kHalf + (lane & 31) * 16;
+    uint4 w0 = *(const uint4*)w0p, w1 = *(const uint4*)(w0p + kHalf);
+#pragma unroll
+    for (int j = 0; j < SN; j++) {
+      const v8i bq = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, 0, 0};
+      const h4 bs = __builtin_bit_cast(h4, make_uint2(w1.z, w1.w));
+      const v16f z = {};
+      const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(as, bs, z, 0, 0, 0);
+      const v16f d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bq, z, 2, 2, 0, sa, 0, 130);
+      if (j + 1 < SN) {
+        w0 = *(const uint4*)(w0p + (j + 1) * 32 * 16);
+        w1 = *(const uint4*)(w0p + kHalf + (j + 1) * 32 * 16);
+      }
+      if (j > 0) {
+        fold(j - 1);
+      } else if (!first) {
+        fold(SN - 1);
+      }
+      pd = d;
+      ps = sc;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  i32x4 rlo[kRing], rhi[kRing];
+#pragma unroll
+  for (int r = 0; r < kRing; r++) load_a(b_begin + kp + 2 * r, rlo[r], rhi[r]);
+  load_w(0);
+  store_w(0);
+  __syncthreads();
+  bool first = true;
+  for (int s = 0; s < stages; s++) {
+    const int buf = s & 1;
+    if (s + 1 < stages) load_w(s + 1);
+    const uint8_t* sbase = lds + buf * kStage;
+    const int b0 = b_begin + s * kPKB;
+#pragma unroll 1
+    for (int u0 = 0; u0 < kPKB / 2; u0 += kRing) {
+#pragma unroll
+      for (int r = 0; r < kRing; r++) {
+        const int kb = kp + 2 * (u0 + r);
+        compute(sbase, kb, rlo[r], rhi[r], first);
+        first = false;
+        load_a(b0 + kb + 2 * kRing, rlo[r], rhi[r]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (s + 1 < stages) store_w(buf ^ 1);
+    __syncthreads();
+  }
+  if (!first) fold(SN - 1);
+
+  float* red = (float*)lds + (size_t)mg * SN * 16 * 64;
+  if (kp == 1) {
+#pragma unroll
+    for (int j = 0; j < SN; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) red[(j * 16 + v) * 64 + lane] = acc[j][v];
+  }
+  __syncthreads();
+  if (kp == 1 || !live) return;
+  float* out = p.part ? p.part + (size_t)blockIdx.y * M * N : p.y;
+#pragma unroll
+  for (int j = 0; j < SN; j++) {
+    const int r = n0 + j * 32 + (lane & 31);
+    if (r >= N) continue;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int m = g * kTokens + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+      if (m < M) out[(size_t)m * N + r] = acc[j][v] + red[(j * 16 + v) * 64 + lane];
+    }
+  }
+}
+
+// y = the split partials summed in split order (deterministic).
+__global__ void __launch_bounds__(256) f6_splitk_reduce_kernel(const float* __restrict__ part,
+                                                               float* __restrict__ y,
+                                                               int64_t count, int splits) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * 256) {
+    float v = part[i];
+    for (int z = 1; z < splits; z++) v += part[(size_t)z * count + i];
+    y[i] = v;
+  }
+}
+
+// Library-owned split partials, grown on demand: a call at a larger shape
+// than any before allocates, so such a call must not be the first inside a
+// graph capture.
+float* gF6Part = nullptr;
+size_t gF6PartBytes = 0;
+
+float* part_workspace(size_t bytes) {
+  if (bytes <= gF6PartBytes) return gF6Part;
+  if (gF6Part != nullptr) {
+    if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+    (void)hipFree(gF6Part);
+    gF6Part = nullptr;
+    gF6PartBytes = 0;
+  }
+  if (hipMalloc(&gF6Part, bytes) != hipSuccess) {
+    gF6Part = nullptr;
+    return nullptr;
+  }
+  gF6PartBytes = bytes;
+  return gF6Part;
+}
+
+int64_t f6_panel_bytes(int64_t n, int64_t cols) {
+  return (n + kTokens - 1) / kTokens * (cols / kBlock) * kRec;
+}
+
+bool f6_shape_ok(int64_t rows, int64_t cols, int64_t n) {
+  if (rows <= 0 || cols <= 0 || n <= 0 || cols % kBlock != 0) return false;
+  // 32-bit buffer offsets: each operand below 2 GB.
+  return rows * (cols / 2) < (1ll << 31) && f6_panel_bytes(n, cols) < (1ll << 31) &&
+         rows * (cols / kBlock) * 2 < (1ll << 31) && n * rows < (1ll << 31);
+}
+
+template <int SN>
+int launch_f6(const uint8_t* qs, const uint16_t* scales, const uint8_t* panel, float* y,
+              int64_t rows, int64_t cols, int64_t n, hipStream_t stream) {
+  constexpr int BN = SN * 32;
+  F6Params p{};
+  p.qs = qs;
+  p.scales = scales;
+  p.panel = panel;
+  p.y = y;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.n = (int)n;
+  p.tiles_m = (int)((n + kTileM * kTokens - 1) / (kTileM * kTokens));
+  p.tiles = p.tiles_m * (int)((rows + BN - 1) / BN);
+  const int B = (int)(cols / kBlock);
+  // Split K when the tiles alone leave CUs idle: about 256 workgroups, each
+  // with at least one stage of blocks.
+  int splits = 1;
+  if (p.tiles < 192) {
+    splits = (256 + p.tiles - 1) / p.tiles;
+    const int max_splits = (B + kKB - 1) / kKB;
+    if (splits > max_splits) splits = max_splits;
+  }
+  p.split_blocks = (B + splits - 1) / splits;
+  p.split_blocks = (p.split_blocks + kKB - 1) / kKB * kKB;  // whole stages per split
+  splits = (B + p.split_blocks - 1) / p.split_blocks;
+  const int64_t count = n * rows;
+  p.part = nullptr;
+  if (splits > 1) {
+    p.part = part_workspace((size_t)splits * count * 4);
+    if (p.part == nullptr) return DNX_ENOMEM;
+  }
+  hipLaunchKernelGGL((gemm_f6_q4_kernel<SN>), dim3((unsigned)p.tiles, (unsigned)splits),
+                     dim3(kThreads), 0, stream, p);
+  if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+  if (splits > 1) {
+    const int64_t blocks = (count + 255) / 256;
+    hipLaunchKernelGGL(f6_splitk_reduce_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)),
+                       dim3(256), 0, stream, p.part, y, count, splits);
+    if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+  }
+  return DNX_OK;
+}
+
+template <int SN>
+int launch_f6p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t rows,
+               int64_t cols, int64_t n, hipStream_t stream) {
+  constexpr int BN = SN * 32;
+  F6PParams p{};
+  p.packed = packed;
+  p.panel = panel;
+  p.y = y;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.n = (int)n;
+  p.tiles_m = (int)((n + kTileM * kTokens - 1) / (kTileM * kTokens));
+  p.tiles = p.tiles_m * (int)((rows + BN - 1) / BN);
+  const int B = (int)(cols / kBlock);
+  int splits = 1;
+  if (p.tiles < 192) {
+    splits = (256 + p.tiles - 1) / p.tiles;
+    const int max_splits = (B + kPKB - 1) / kPKB;
+    if (splits > max_splits) splits = max_splits;
+  }
+  p.split_blocks = (B + splits - 1) / splits;
+  p.split_blocks = (p.split_blocks + kPKB - 1) / kPKB * kPKB;
+  splits = (B + p.split_blocks - 1) / p.split_blocks;
+  const int64_t count = n * rows;
+  p.part = nullptr;
+  if (splits > 1) {
+    p.part = part_workspace((size_t)splits * count * 4);
+    if (p.part == nullptr) return DNX_ENOMEM;
+  }
+  hipLaunchKernelGGL((gemm_f6p_kernel<SN>), dim3((unsigned)p.tiles, (unsigned)splits),
+                     dim3(kThreads), 0, stream, p);
+  if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+  if (splits > 1) {
+    const int64_t blocks = (count + 255) / 256;
+    hipLaunchKernelGGL(f6_splitk_reduce_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)),
+                       dim3(256), 0, stream, p.part, y, count, splits);
+    if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+  }
+  return DNX_OK;
+}
+
+int panel_grid(int64_t total) {
+  const int64_t blocks = (total + kPanelThreads - 1) / kPanelThreads;
+  return (int)(blocks < 16384 ? blocks : 16384);
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t dnx_f6_panel_bytes(int64_t n, int64_t cols) {
+  if (n <= 0 || cols <= 0 || cols % kBlock != 0) return -1;
+  return f6_panel_bytes(n, cols);
+}
+
+int dnx_quantize_q8_f6panel(const float* x, void* panel, int64_t n, int64_t cols,
+                            dnx_stream_t stream) {
+  if (n <= 0 || cols <= 0 || cols % kBlock != 0 || ((uintptr_t)x & 15) ||
+      ((uintptr_t)panel & 15) || f6_panel_bytes(n, cols) >= (1ll << 31)) {
+    return DNX_EINVAL;
+  }
+  const int groups = (int)((n + kTokens - 1) / kTokens);
+  const int64_t total = (int64_t)groups * (cols / kBlock) * kTokens;
+  hipLaunchKernelGGL(quantize_f6_panel_kernel, dim3(panel_grid(total)), dim3(kPanelThreads), 0,
+                     (hipStream_t)stream, x, (uint8_t*)panel, (int)n, (int)cols, groups);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_pack_f6panel(const int8_t* xq, const float* xsc, void* panel, int64_t n, int64_t cols,
+                     dnx_stream_t stream) {
+  if (n <= 0 || cols <= 0 || cols % kBlock != 0 || ((uintptr_t)xq & 15) || (cols % 16) ||
+      ((uintptr_t)panel & 15) || f6_panel_bytes(n, cols) >= (1ll << 31)) {
+    return DNX_EINVAL;
+  }
+  const int groups = (int)((n + kTokens - 1) / kTokens);
+  const int64_t total = (int64_t)groups * (cols / kBlock) * kTokens;
+  hipLaunchKernelGGL(pack_f6_panel_kernel, dim3(panel_grid(total)), dim3(kPanelThreads), 0,
+                     (hipStream_t)stream, xq, xsc, (uint8_t*)panel, (int)n, (int)cols, groups);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_gemm_q4_f6(const uint8_t* qs, const uint16_t* scales, const void* panel, float* y,
+                   int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream) {
+  if (!f6_shape_ok(rows, cols, n) || ((uintptr_t)panel & 15) || ((uintptr_t)qs & 15) ||
+      ((uintptr_t)scales & 1) || ((uintptr_t)y & 3)) {
+    return DNX_EINVAL;
+  }
+  return launch_f6<3>(qs, scales, (const uint8_t*)panel, y, rows, cols, n, (hipStream_t)stream);
+}
+
+int64_t dnx_q4_f6pack_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0 || cols % kBlock != 0) return -1;
+  return rows * (cols / kBlock) * 32;
+}
+
+int dnx_pack_q4_f6(const uint8_t* qs, const uint16_t* scales, void* packed, int64_t rows,
+                   int64_t cols, dnx_stream_t stream) {
+  if (rows <= 0 || cols <= 0 || cols % kBlock != 0 || ((uintptr_t)qs & 15) ||
+      ((uintptr_t)scales & 1) || ((uintptr_t)packed & 15)) {
+    return DNX_EINVAL;
+  }
+  const int64_t count = rows * (cols / kBlock);
+  hipLaunchKernelGGL(pack_q4_f6_kernel, dim3(panel_grid(count)), dim3(kPanelThreads), 0,
+                     (hipStream_t)stream, qs, scales, (uint8_t*)packed, count);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_gemm_q4_f6p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
+                    int64_t n, dnx_stream_t stream) {
+  if (!f6_shape_ok(rows, cols, n) || ((uintptr_t)panel & 15) || ((uintptr_t)packed & 15) ||
+      ((uintptr_t)y & 3)) {
+    return DNX_EINVAL;
+  }
+  return launch_f6p<3>((const uint8_t*)packed, (const uint8_t*)panel, y, rows, cols, n,
+                       (hipStream_t)stream);
+}
+
+}  // extern "C"

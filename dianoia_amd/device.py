@@ -186,6 +186,42 @@ def gemm_q4_panel(qs, scales, panel, y, rows: int, cols: int, n: int, stream=Non
                                          cols, n, _stream(stream)), "dnx_gemm_q4_panel")
 
 
+def f6_panel_bytes(n: int, cols: int) -> int:
+    return int(_lib.load().dnx_f6_panel_bytes(n, cols))
+
+
+def quantize_q8_f6panel(x, panel, n: int, cols: int, stream=None) -> None:
+    """fp32 x [n][cols] quantized (lab_quantize_q8) into the fp6 GEMM's panel."""
+    _check(_lib.load().dnx_quantize_q8_f6panel(_ptr(x), _ptr(panel), n, cols, _stream(stream)),
+           "dnx_quantize_q8_f6panel")
+
+
+def pack_f6panel(xq, xsc, panel, n: int, cols: int, stream=None) -> None:
+    """xq int8 [n][cols] + xsc fp32 [n][cols/32] -> the fp6 GEMM's panel."""
+    _check(_lib.load().dnx_pack_f6panel(_ptr(xq), _ptr(xsc), _ptr(panel), n, cols,
+                                        _stream(stream)), "dnx_pack_f6panel")
+
+
+def gemm_q4_f6(qs, scales, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _check(_lib.load().dnx_gemm_q4_f6(_ptr(qs), _ptr(scales), _ptr(panel), _ptr(y), rows, cols,
+                                      n, _stream(stream)), "dnx_gemm_q4_f6")
+
+
+def q4_f6pack_bytes(rows: int, cols: int) -> int:
+    return int(_lib.load().dnx_q4_f6pack_bytes(rows, cols))
+
+
+def pack_q4_f6(qs, scales, packed, rows: int, cols: int, stream=None) -> None:
+    """Load-time re-encoding of Q4 weights for the fp6 GEMM (dnx_gemm_q4_f6p)."""
+    _check(_lib.load().dnx_pack_q4_f6(_ptr(qs), _ptr(scales), _ptr(packed), rows, cols,
+                                      _stream(stream)), "dnx_pack_q4_f6")
+
+
+def gemm_q4_f6p(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _check(_lib.load().dnx_gemm_q4_f6p(_ptr(packed), _ptr(panel), _ptr(y), rows, cols, n,
+                                       _stream(stream)), "dnx_gemm_q4_f6p")
+
+
 def argmax_workspace(n: int, device="cuda") -> torch.Tensor:
     nbytes = int(_lib.load().dnx_argmax_workspace_bytes(n))
     return torch.empty(nbytes, dtype=torch.uint8, device=device)

@@ -157,6 +157,43 @@ int dnx_gemm_q8_panel(const int8_t* qs, const float* scales, const void* panel, 
 int dnx_gemm_q4_panel(const uint8_t* qs, const uint16_t* scales, const void* panel, float* y,
                       int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
 
+// The large-n Q4 GEMM on the fp6 matrix cores (lab_gemm_q4 mode 1,
+// lab_native.c:1059-1080): each block's exact int dot from one scaled
+// v_mfma_scale_f32_32x32x64_f8f6f4 (weights as the E2M3 codes of q / 8,
+// activations as two E2M3 pieces of xq with power-of-two scales, the -8 of
+// q - 8 as the MFMA's C input), the scale products from an fp16
+// outer-product MFMA, one fma per output per block. The activations arrive
+// as an "f6 panel" (per 32 tokens and block, the MFMA operands in lane
+// order); dnx_f6_panel_bytes(n, cols) is its size. dnx_quantize_q8_f6panel
+// writes it from fp32 x [n][cols] (lab_quantize_q8's values, bit-exact with
+// dnx_quantize_q8; x 16-byte aligned), dnx_pack_f6panel from xq int8
+// [n][cols] + xsc fp32 [n][cols/32]. The products are within 1e-4 relative
+// of the CPU kernels; the same inputs always give the same bits. With fewer
+// than 192 workgroup tiles (128 tokens x 96 rows) K is split across
+// workgroups and summed in a fixed order in a library-owned workspace,
+// allocated on the first such call at a larger shape (so that call must not
+// be captured into a graph).
+int64_t dnx_f6_panel_bytes(int64_t n, int64_t cols);
+int dnx_quantize_q8_f6panel(const float* x, void* panel, int64_t n, int64_t cols,
+                            dnx_stream_t stream);
+int dnx_pack_f6panel(const int8_t* xq, const float* xsc, void* panel, int64_t n, int64_t cols,
+                     dnx_stream_t stream);
+int dnx_gemm_q4_f6(const uint8_t* qs, const uint16_t* scales, const void* panel, float* y,
+                   int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
+
+// The same GEMM on a load-time re-encoding of the Q4 weights: per (row,
+// block) 32 bytes holding the E2M3 codes of the signed weights q - 8 and the
+// scale MFMA's operand (dnx_q4_f6pack_bytes(rows, cols) bytes, written once
+// by dnx_pack_q4_f6 from the engine's Q4 layout; weights are immutable after
+// upload, as GpuLinear.upload treats them, gpu.dart:1295-1323). The GEMM
+// stages it to LDS with plain copies and needs no per-call conversion of the
+// weights; results equal dnx_gemm_q4_f6's to fp32 rounding.
+int64_t dnx_q4_f6pack_bytes(int64_t rows, int64_t cols);
+int dnx_pack_q4_f6(const uint8_t* qs, const uint16_t* scales, void* packed, int64_t rows,
+                   int64_t cols, dnx_stream_t stream);
+int dnx_gemm_q4_f6p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
+                    int64_t n, dnx_stream_t stream);
+
 // GGUF Q8_0 / Q4_0 blocks split into the engine's layout on the GPU, bit
 // for bit as splitQ8_0 (lib/src/gguf.dart:270-282: int8 values and the fp16
 // d widened to fp32) and splitQ4_0 (:208-218: nibble bytes and the fp16
