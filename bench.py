@@ -253,16 +253,47 @@ def bench_c3(torch, D, synth, timer, steps, warmup):
         q, s = ws[i % copies]
         D.gemm_q4_panel(q, s, panel, y, N, K, M)
 
+    # The fp6 matrix-core GEMM (gfx950 scaled MFMA): the quantizer writes
+    # the fp6 activation panel; the weights are read in the engine's Q4
+    # layout, or from the fp6 prepack a load-time converter writes once.
+    f6panel = torch.empty((D.f6_panel_bytes(M, K),), dtype=torch.uint8, device="cuda")
+    packed = [torch.empty((D.q4_f6pack_bytes(N, K),), dtype=torch.uint8, device="cuda")
+              for _ in range(copies)]
+    for c in range(copies):
+        D.pack_q4_f6(ws[c][0], ws[c][1], packed[c], N, K)
+
+    def quant_f6(i):
+        D.quantize_q8_f6panel(xd, f6panel, M, K)
+
+    def gemm_f6(i):
+        q, s = ws[i % copies]
+        D.gemm_q4_f6(q, s, f6panel, y, N, K, M)
+
+    def gemm_f6p(i):
+        D.gemm_q4_f6p(packed[i % copies], f6panel, y, N, K, M)
+
+    def prepack(i):
+        D.pack_q4_f6(ws[i % copies][0], ws[i % copies][1], packed[i % copies], N, K)
+
     n = max(10, steps // 4)
     ms_i8 = timer.time(lambda i: (quant(i), gemm(i)), n, max(2, warmup // 4))
     ms_p = timer.time(lambda i: (quant_p(i), gemm_p(i)), n, max(2, warmup // 4))
-    means = timer.kernel_means([quant, gemm, quant_p, gemm_p], n)
+    ms_f6 = timer.time(lambda i: (quant_f6(i), gemm_f6(i)), n, max(2, warmup // 4))
+    ms_f6p = timer.time(lambda i: (quant_f6(i), gemm_f6p(i)), n, max(2, warmup // 4))
+    means = timer.kernel_means([quant, gemm, quant_p, gemm_p, quant_f6, gemm_f6, gemm_f6p, prepack], n)
     ops = 2 * M * N * K
     paths = {
         "int8_mfma": {"ms": ms_i8, "gemm_ms": means[1], "quantize_ms": means[0],
                       "kernel": "quantize_q8 + gemm_kernel (int8 MFMA, scale MFMA, cvt + fma)"},
         "fp16_panel": {"ms": ms_p, "gemm_ms": means[3], "quantize_ms": means[2],
                        "kernel": "quantize_q8_panel + gemm_f16_kernel (fp16 MFMA, scale MFMA, fma)"},
+        "fp6_engine_layout": {"ms": ms_f6, "gemm_ms": means[5], "quantize_ms": means[4],
+                              "kernel": "quantize_f6_panel + gemm_f6_q4_kernel (fp6 scaled MFMA on "
+                                        "Q4 qs/scales, scale MFMA, fma)"},
+        "fp6_prepacked": {"ms": ms_f6p, "gemm_ms": means[6], "quantize_ms": means[4],
+                          "kernel": "quantize_f6_panel + gemm_f6p_kernel (fp6 scaled MFMA on the "
+                                    "load-time fp6 prepack, scale MFMA, fma)",
+                          "prepack_ms_load_time": means[7]},
     }
     best = min(paths, key=lambda k: paths[k]["gemm_ms"])
     b = paths[best]
@@ -270,6 +301,7 @@ def bench_c3(torch, D, synth, timer, steps, warmup):
            "quantize_ms": b["quantize_ms"], "gemm_tops": ops / b["gemm_ms"] / 1e9,
            "gemm_frac_i8": ops / b["gemm_ms"] / 1e9 / I8_PEAK_TOPS, "gemm_path": best,
            "paths": {k: dict(v, gemm_tops=ops / v["gemm_ms"] / 1e9) for k, v in paths.items()}}
+    out["issue_floor"] = c3_issue_floor(M, N, K)
     # M = 1..256 sweep: GEMV (exact order) up to 4 tokens, GEMM beyond. The
     # batch shapes of the kernels' other callers (audio encoder / generator
     # and vision attention projections) lie in this range.
@@ -293,6 +325,58 @@ def bench_c3(torch, D, synth, timer, steps, warmup):
                          "kernel": "gemv_q4" if m <= 4 else "quantize+gemm_q4"}
     out["sweep_m"] = sweep
     return out
+
+
+def issue_bound(iters=3000, ctas=256):
+    """The prefill GEMM's inner step run from registers only
+    (libdnx_ubench.so, csrc/ubench_tile.hip): ns per step per SIMD for each
+    mix of the step's instructions, with one and two waves per SIMD. A step
+    is one 32x32 tile of one Q4 block: the f16 scale MFMA (mask bit 0), the
+    fp6 scaled dot MFMA (bit 1) and `nvalu` fmas."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(os.path.join(ROOT, "dianoia_amd", "libdnx_ubench.so"))
+    lib.dnx_ubench_tile_issue.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p, ctypes.c_void_p]
+    out = torch.zeros(ctas * 512, device="cuda")
+    ms = ctypes.c_float()
+    rows = {}
+    for mask, label in ((3, "scale MFMA + dot MFMA"), (2, "dot MFMA"), (1, "scale MFMA"),
+                        (0, "VALU only")):
+        for nv in (0, 8, 16, 24, 32):
+            if mask == 0 and nv == 0:
+                continue
+            row = {}
+            for threads in (256, 512):
+                waves = threads // 256
+                rc = lib.dnx_ubench_tile_issue(nv, mask, 100, ctas, threads, out.data_ptr(),
+                                               ctypes.byref(ms))
+                rc = rc or lib.dnx_ubench_tile_issue(nv, mask, iters, ctas, threads,
+                                                     out.data_ptr(), ctypes.byref(ms))
+                if rc != 0:
+                    raise RuntimeError(f"dnx_ubench_tile_issue returned {rc}")
+                # ctas workgroups on 256 CUs x 4 SIMDs: `waves` waves per SIMD,
+                # each doing iters x 3 steps.
+                row[f"{waves}_wave"] = round(ms.value * 1e6 / (iters * 3 * waves), 2)
+            rows[f"{label}, {nv} fma"] = row
+    return {"unit": "ns per step per SIMD", "iters": iters, "workgroups": ctas, "steps": rows}
+
+
+_ISSUE = {}
+
+
+def c3_issue_floor(M, N, K):
+    """The GEMM's compute floor from the measured step: tile-blocks per SIMD
+    (32-token x 32-row x one-block steps over 1024 SIMDs) x the
+    two-waves-per-SIMD time of the full step (both MFMAs + 16 fmas)."""
+    if "t" not in _ISSUE:
+        _ISSUE["t"] = issue_bound(iters=1500)
+    t = _ISSUE["t"]["steps"]["scale MFMA + dot MFMA, 16 fma"]["2_wave"]
+    steps_per_simd = (M // 32) * (N // 32) * (K // 32) / 1024
+    floor_ms = steps_per_simd * t * 1e-6
+    ops = 2 * M * N * K
+    return {"step_ns": t, "steps_per_simd": steps_per_simd, "floor_ms": floor_ms,
+            "floor_frac_i8": ops / floor_ms / 1e9 / I8_PEAK_TOPS,
+            "note": "compute issue only: launch, prologue and the output store come on top"}
 
 
 def bench_c4(torch, D, synth, timer, steps, warmup):
@@ -765,10 +849,14 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline config only")
+    ap.add_argument("--only", default=None,
+                    help="comma-separated names of the other configs to run (default: all)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="eager launches for rocprofv3 --pmc runs (no JSON line)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="HBM traffic per launch from two rocprofv3 counter_collection.csv files")
+    ap.add_argument("--issue-bound", action="store_true",
+                    help="the prefill GEMM step's issue-bound microbenchmark (JSON table)")
     ap.add_argument("--mfma-summary", metavar="COUNTER_CSV",
                     help="matrix-core use per launch from a rocprofv3 counter_collection.csv "
                          "of the MFMA counters")
@@ -794,6 +882,9 @@ def main():
     if args.pmc_workload:
         pmc_workload(torch, D, synth, max(1, min(args.steps, 20)))
         return
+    if args.issue_bound:
+        print(json.dumps(issue_bound(), indent=1))
+        return
     timer = Timer(torch)
     check_graph_replay(torch, D, synth)
     print(f"bench: config 2 (steps={args.steps}, warmup={args.warmup})", file=sys.stderr, flush=True)
@@ -801,19 +892,22 @@ def main():
     configs = {"c2_q8_lmhead_argmax": c2}
     torch.cuda.empty_cache()
     if not args.quick:
+        only = set(args.only.split(",")) if args.only else None
         for name, fn in (("c1_q4_mlp", bench_c1), ("c0_q8_gemv", bench_c0),
                          ("c3_q4_prefill_gemm", bench_c3), ("c4_vision_bf16_pair", bench_c4)):
+            if only is not None and name not in only:
+                continue
             print(f"bench: {name}", file=sys.stderr, flush=True)
             configs[name] = fn(torch, D, synth, timer, args.steps, args.warmup)
             torch.cuda.empty_cache()
-        print("bench: load-time converters", file=sys.stderr, flush=True)
-        configs["load_time_converters"] = bench_loaders(torch, D, timer, args.steps)
-        torch.cuda.empty_cache()
-        print("bench: layer steps", file=sys.stderr, flush=True)
-        configs["layer_steps"] = bench_layers(torch, D, timer, args.steps)
-        torch.cuda.empty_cache()
-        print("bench: weight cache to HBM", file=sys.stderr, flush=True)
-        configs["weight_cache_wrap"] = bench_cache_wrap()
+        for name, fn in (("load_time_converters", lambda: bench_loaders(torch, D, timer, args.steps)),
+                         ("layer_steps", lambda: bench_layers(torch, D, timer, args.steps)),
+                         ("weight_cache_wrap", bench_cache_wrap)):
+            if only is not None and name not in only:
+                continue
+            print(f"bench: {name}", file=sys.stderr, flush=True)
+            configs[name] = fn()
+            torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
         print("bench: cpu baseline", file=sys.stderr, flush=True)

@@ -17,6 +17,10 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libdianoia_amd.so")
+# The issue-bound microbenchmark of the GEMM step, kept out of the product
+# library (bench.py --issue-bound loads it).
+UBENCH_SRC = "ubench_tile.hip"
+UBENCH_LIB = os.path.join(HERE, "libdnx_ubench.so")
 SOURCES = ["kernels.hip", "gemv.hip", "gemm.hip", "gemm_f16.hip", "gemm_f6.hip", "layers.hip",
            "lab_gpu.hip"]
 ARCH = "gfx950"
@@ -35,8 +39,8 @@ FLAGS = [
 # Per-source flags. The GEMM keeps its MFMA results in ordinary VGPRs: its
 # scale epilogue reads every result with VALU instructions, which cannot
 # take accumulation registers (one v_accvgpr_read per value otherwise).
-SOURCE_FLAGS = {src: ["-mllvm", "-amdgpu-mfma-vgpr-form=1"] for src in ("gemm.hip", "gemm_f16.hip",
-                                                                       "gemm_f6.hip")}
+SOURCE_FLAGS = {src: ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+                for src in ("gemm.hip", "gemm_f16.hip", "gemm_f6.hip", UBENCH_SRC)}
 
 
 def _compile(src: str, build_dir: str) -> str:
@@ -48,17 +52,23 @@ def _compile(src: str, build_dir: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    build_dir = os.path.join(HERE, "_build")
-    os.makedirs(build_dir, exist_ok=True)
-    with concurrent.futures.ThreadPoolExecutor(len(SOURCES)) as pool:
-        objs = list(pool.map(lambda s: _compile(s, build_dir), SOURCES))
-    tmp = LIB + ".tmp"
+def _link(objs: list, lib: str) -> None:
+    tmp = lib + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> str:
+    build_dir = os.path.join(HERE, "_build")
+    os.makedirs(build_dir, exist_ok=True)
+    with concurrent.futures.ThreadPoolExecutor(len(SOURCES) + 1) as pool:
+        objs = list(pool.map(lambda s: _compile(s, build_dir), SOURCES + [UBENCH_SRC]))
+    ubench_obj = objs.pop()
+    _link([ubench_obj], UBENCH_LIB)
+    _link(objs, LIB)
     if verbose:
         print(f"built {LIB}")
     return LIB

@@ -570,36 +570,59 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   for (int j = 0; j < SN; j++)
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[j][v] = 0.0f;
+  // Software pipeline over tiles: the products of tile j are folded into
+  // the accumulators while the matrix cores run tile j + 1, and the LDS
+  // fragments of the next tile are read while they run tile j. The order
+  // inside a tile is pinned (MFMAs, then LDS reads, then the previous fold):
+  // left to itself the scheduler folds a tile right behind its own MFMA and
+  // every fold then waits out the MFMA latency.
   v16f pd, ps;
+#pragma unroll
+  for (int v = 0; v < 16; v++) pd[v] = ps[v] = 0.0f;
   auto fold = [&](int j) {
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[j][v] = fmaf(pd[v], ps[v], acc[j][v]);
   };
-  auto compute = [&](const uint8_t* sbase, int kb, i32x4 lo, i32x4 hi, bool first) {
+  // B fragment of one tile: the 24 code bytes (w0 + wc) and the scale pair ws.
+  struct BFrag {
+    uint4 w0;
+    uint2 wc, ws;
+  };
+  auto read_b = [&](const uint8_t* sbase, int kb, int j) {
+    const uint8_t* q = sbase + (kb * 2) * kHalf + (lane & 31) * 16 + j * 32 * 16;
+    BFrag f;
+    f.w0 = *(const uint4*)q;
+    f.wc = *(const uint2*)(q + kHalf);
+    f.ws = *(const uint2*)(q + kHalf + 8);
+    return f;
+  };
+  // One block of K for the SN tiles; `nb` holds tile 0 of this block on
+  // entry and tile 0 of block kb_next on exit.
+  auto compute = [&](const uint8_t* sbase, int kb, int kb_next, i32x4 lo, i32x4 hi, BFrag& nb) {
     asm volatile("" : "+v"(lo), "+v"(hi));
     const v8i a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     const int sa = hi[3];
     const h4 as = __builtin_bit_cast(h4, make_uint2((uint32_t)hi[2], (uint32_t)hi[3]));
-    const uint8_t* w0p = sbase + (kb * 2) * kHalf + (lane & 31) * 16;
-    uint4 w0 = *(const uint4*)w0p, w1 = *(const uint4*)(w0p + kHalf);
+    BFrag cur = nb;
 #pragma unroll
     for (int j = 0; j < SN; j++) {
-      const v8i bq = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, 0, 0};
-      const h4 bs = __builtin_bit_cast(h4, make_uint2(w1.z, w1.w));
+      const v8i bq = {(int)cur.w0.x, (int)cur.w0.y, (int)cur.w0.z, (int)cur.w0.w,
+                      (int)cur.wc.x, (int)cur.wc.y, 0, 0};
+      const h4 bs = __builtin_bit_cast(h4, cur.ws);
       const v16f z = {};
       const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(as, bs, z, 0, 0, 0);
       const v16f d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bq, z, 2, 2, 0, sa, 0, 130);
       if (j + 1 < SN) {
-        w0 = *(const uint4*)(w0p + (j + 1) * 32 * 16);
-        w1 = *(const uint4*)(w0p + kHalf + (j + 1) * 32 * 16);
+        cur = read_b(sbase, kb, j + 1);
+      } else {
+        nb = read_b(sbase, kb_next, 0);
       }
-      if (j > 0) {
-        fold(j - 1);
-      } else if (!first) {
-        fold(SN - 1);
-      }
+      fold(j > 0 ? j - 1 : SN - 1);
       pd = d;
       ps = sc;
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // the two MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);   // next fragments
+      __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // previous fold
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -610,19 +633,20 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   load_w(0);
   store_w(0);
   __syncthreads();
-  bool first = true;
   for (int s = 0; s < stages; s++) {
     const int buf = s & 1;
     if (s + 1 < stages) load_w(s + 1);
     const uint8_t* sbase = lds + buf * kStage;
     const int b0 = b_begin + s * kPKB;
+    // Tile 0 of the stage's first block; later blocks get theirs from the
+    // block before (clamped to the stage: the last block's read is unused).
+    BFrag nb = read_b(sbase, kp, 0);
 #pragma unroll 1
     for (int u0 = 0; u0 < kPKB / 2; u0 += kRing) {
 #pragma unroll
       for (int r = 0; r < kRing; r++) {
         const int kb = kp + 2 * (u0 + r);
-        compute(sbase, kb, rlo[r], rhi[r], first);
-        first = false;
+        compute(sbase, kb, min(kb + 2, kPKB - 1), rlo[r], rhi[r], nb);
         load_a(b0 + kb + 2 * kRing, rlo[r], rhi[r]);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -630,7 +654,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
     if (s + 1 < stages) store_w(buf ^ 1);
     __syncthreads();
   }
-  if (!first) fold(SN - 1);
+  fold(SN - 1);
 
   float* red = (float*)lds + (size_t)mg * SN * 16 * 64;
   if (kp == 1) {
