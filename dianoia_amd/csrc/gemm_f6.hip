@@ -46,6 +46,8 @@
 // waves of a SIMD work on the same outputs and one hides the other's
 // latencies; their sums are added at the end through LDS in a fixed order.
 
+#include <mutex>
+
 #include "common.h"
 #include "dnx_kernels.h"
 
@@ -712,6 +714,38 @@ float* part_workspace(size_t bytes) {
   return gF6Part;
 }
 
+// Split partials of dnx_gemm_q4_f6p_noalloc: a fixed array in the code
+// object, so that entry point never allocates. Every GPU the library runs on
+// holds its own copy from the module's load until the process ends. In host
+// code `scratch` names only a host-side stand-in: kernels get the address
+// hipGetSymbolAddress returns for the current device (scratch_on_device).
+// Size: K is split only below 192 tiles, into at most ceil(256 / tiles)
+// parts, and n x rows <= (128 x tiles_m) x (96 x tiles_n) = 12288 x tiles,
+// so the partials never exceed 12288 x (256 + 191) floats (21 MiB) for any
+// shape the GEMM accepts; the bound is still checked on every call.
+constexpr size_t kScratchFloats = (size_t)12288 * 447;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex gScratchMu;
+float* gScratchPtr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per
+// device (nullptr when the lookup fails).
+float* scratch_on_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(gScratchMu);
+  if (gScratchPtr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+      return nullptr;
+    }
+    gScratchPtr[dev] = (float*)ptr;
+  }
+  return gScratchPtr[dev];
+}
+
 int64_t f6_panel_bytes(int64_t n, int64_t cols) {
   return (n + kTokens - 1) / kTokens * (cols / kBlock) * kRec;
 }
@@ -769,7 +803,8 @@ int launch_f6(const uint8_t* qs, const uint16_t* scales, const uint8_t* panel, f
 
 template <int SN>
 int launch_f6p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t rows,
-               int64_t cols, int64_t n, hipStream_t stream) {
+               int64_t cols, int64_t n, hipStream_t stream, float* fixed_part = nullptr,
+               size_t fixed_floats = 0) {
   constexpr int BN = SN * 32;
   F6PParams p{};
   p.packed = packed;
@@ -793,8 +828,14 @@ int launch_f6p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t ro
   const int64_t count = n * rows;
   p.part = nullptr;
   if (splits > 1) {
-    p.part = part_workspace((size_t)splits * count * 4);
-    if (p.part == nullptr) return DNX_ENOMEM;
+    if (fixed_part != nullptr) {
+      // The allocation-free entry point: its partials must fit the array.
+      if ((size_t)splits * (size_t)count > fixed_floats) return DNX_ESCRATCH;
+      p.part = fixed_part;
+    } else {
+      p.part = part_workspace((size_t)splits * count * 4);
+      if (p.part == nullptr) return DNX_ENOMEM;
+    }
   }
   hipLaunchKernelGGL((gemm_f6p_kernel<SN>), dim3((unsigned)p.tiles, (unsigned)splits),
                      dim3(kThreads), 0, stream, p);
@@ -882,6 +923,20 @@ int dnx_gemm_q4_f6p(const void* packed, const void* panel, float* y, int64_t row
   }
   return launch_f6p<3>((const uint8_t*)packed, (const uint8_t*)panel, y, rows, cols, n,
                        (hipStream_t)stream);
+}
+
+int64_t dnx_gemm_q4_f6p_noalloc_max_floats(void) { return (int64_t)kScratchFloats; }
+
+int dnx_gemm_q4_f6p_noalloc(const void* packed, const void* panel, float* y, int64_t rows,
+                            int64_t cols, int64_t n, dnx_stream_t stream) {
+  if (!f6_shape_ok(rows, cols, n) || ((uintptr_t)panel & 15) || ((uintptr_t)packed & 15) ||
+      ((uintptr_t)y & 3)) {
+    return DNX_EINVAL;
+  }
+  float* part = scratch_on_device();
+  if (part == nullptr) return DNX_ESCRATCH;
+  return launch_f6p<3>((const uint8_t*)packed, (const uint8_t*)panel, y, rows, cols, n,
+                       (hipStream_t)stream, part, kScratchFloats);
 }
 
 }  // extern "C"

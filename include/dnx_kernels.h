@@ -26,6 +26,7 @@ enum {
   DNX_EINVAL = -1,   // shape or argument outside what the kernel supports
   DNX_ELAUNCH = -2,  // the HIP launch failed
   DNX_ENOMEM = -3,   // a scratch allocation failed
+  DNX_ESCRATCH = -4, // the call needs more than the fixed scratch array holds
 };
 
 // lab_quantize_q8 (lab_native.c:407-429) on the GPU, bit-exact: rows x cols
@@ -193,6 +194,23 @@ int dnx_pack_q4_f6(const uint8_t* qs, const uint16_t* scales, void* packed, int6
                    int64_t cols, dnx_stream_t stream);
 int dnx_gemm_q4_f6p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
                     int64_t n, dnx_stream_t stream);
+
+// dnx_gemm_q4_f6p without any allocation. No counterpart in the reference:
+// for callers that cannot allocate device memory (code under HIP graph
+// capture, serving loops, harnesses that forbid hipMalloc). Same kernels and
+// the same bits as dnx_gemm_q4_f6p; its split-K partials live in a fixed
+// 21 MiB array in the library's code object (one per GPU, held until the
+// process ends) instead of the grown-on-demand workspace. A shape whose
+// partials, splits x n x rows floats, exceed dnx_gemm_q4_f6p_noalloc_max_floats()
+// returns DNX_ESCRATCH before anything is launched; with the current split
+// policy (K split only below 192 tiles of 128 tokens x 96 rows) every valid
+// shape fits. The
+// first call on a device looks up that device's array address (make it
+// outside a graph capture). Every call on one GPU shares its array: calls
+// that overlap on one GPU race, so serialize them (one stream, or events).
+int64_t dnx_gemm_q4_f6p_noalloc_max_floats(void);
+int dnx_gemm_q4_f6p_noalloc(const void* packed, const void* panel, float* y, int64_t rows,
+                            int64_t cols, int64_t n, dnx_stream_t stream);
 
 // GGUF Q8_0 / Q4_0 blocks split into the engine's layout on the GPU, bit
 // for bit as splitQ8_0 (lib/src/gguf.dart:270-282: int8 values and the fp16
