@@ -42,6 +42,7 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
 I8_PEAK_TOPS = 5000.0       # MI355X dense int8 MFMA, TOPS
 METRIC = "Q4_0/Q8_0 GEMV GB/s (% HBM peak) @batch 1; prefill GEMM TOPS (% i8 MFMA peak)"
 ROTATE_BYTES = 600 << 20    # distinct weight bytes cycled per config (> 2 x MALL)
+SETTLE_S = 0.05             # untimed graph replays before each timed one
 
 
 def q4_bytes(rows, cols):
@@ -75,14 +76,22 @@ class Timer:
         return g
 
     def time(self, fn, steps, warmup):
-        """Mean ms per step over `steps` steps replayed from one graph."""
+        """Mean ms per step over `steps` steps replayed from one graph. Before
+        the timed replay the graph is replayed untimed for SETTLE_S: the
+        first ~20 ms of work after the GPU has idled run up to 10% slower
+        (the config-2 step measured 58-63 us per step over its first 15
+        replays, then 56.5-57 us)."""
         torch = self.torch
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
         g = self.graph(fn, steps)
-        g.replay()  # warm replay
-        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while True:  # untimed warm replays
+            g.replay()
+            torch.cuda.synchronize()
+            if time.perf_counter() - t0 >= SETTLE_S:
+                break
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         g.replay()

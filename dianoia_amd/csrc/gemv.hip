@@ -53,7 +53,7 @@ constexpr int kFmtQ8 = 0, kFmtQ4 = 1, kFmtQ8H = 2;
 // stream reads and clears the slots with plain loads and stores and writes
 // the token. The kernel boundary orders the atomics before those reads, so
 // no fence, no arrival count and no atomic retry is needed.
-constexpr int kArgmaxSlots = 2048;
+constexpr int kArgmaxSlots = 256;
 
 DNX_DEV uint64_t argmax_rank(float v, uint32_t row) {
   // A NaN at index 0 is the answer whatever follows (every comparison with
