@@ -433,8 +433,9 @@ def bench_layers(torch, D, timer, steps):
     """The decoder's other layer steps (lab_gpu_enc_* semantics): attention
     decode over a 4096-position cache (32 query heads, 8 KV heads, hd 128;
     HBM-bound on the cached keys and values), RMSNorm over a 4096 x 2048
-    prefill block, and causal prefill attention of 512 tokens (same heads;
-    fp32 matrix cores). Inputs generated on the GPU."""
+    prefill block, causal prefill attention of 512 tokens (same heads;
+    fp32 matrix cores) and the short convolution at 1 and 512 tokens.
+    Inputs generated on the GPU."""
     gen = torch.Generator(device="cuda").manual_seed(6)
     heads, kv, hd, pos = 32, 8, 128, 4095
     q = torch.randn(heads * hd, device="cuda", generator=gen)
@@ -458,11 +459,27 @@ def bench_layers(torch, D, timer, steps):
     def prefill(i):
         D.attention(qp, keys, values, None, outp, 0, npre, heads, kv, hd, 0)
 
-    means = timer.kernel_means([attn, norm, prefill], max(10, steps // 4))
+    # The short convolution (LFM2 conv block: width 2048, 3 taps) at decode
+    # (1 token) and prefill (512 tokens).
+    cw, ck = 2048, 3
+    bcx = torch.randn((npre, 3 * cw), device="cuda", generator=gen)
+    cweight = torch.randn((cw, ck), device="cuda", generator=gen)
+    chist = torch.randn((ck - 1, cw), device="cuda", generator=gen)
+    cy = torch.empty((npre, cw), device="cuda")
+
+    def conv1(i):
+        D.short_conv(bcx, cweight, chist, cy, cw, ck, 1)
+
+    def conv512(i):
+        D.short_conv(bcx, cweight, chist, cy, cw, ck, npre)
+
+    means = timer.kernel_means([attn, norm, prefill, conv1, conv512], max(10, steps // 4))
     attn_bytes = 2 * (pos + 1) * kv * hd * 4 + 2 * heads * hd * 4
     norm_bytes = 2 * 4096 * 2048 * 4 + 2048 * 4
     # q.k and p.v: 2 flops per multiply-add, hd each, per visible key.
     pre_flops = 4 * hd * heads * (npre * (npre + 1) // 2)
+    # Conv: B, C, X read and y written once, the taps and two state rows.
+    conv_bytes = npre * 4 * cw * 4 + cw * ck * 4 + 2 * (ck - 1) * cw * 4
     return {"attention_decode_4096_ms": means[0],
             "attention_decode_4096_gbps": attn_bytes / means[0] / 1e6,
             "rms_norm_4096x2048_ms": means[1],
@@ -470,7 +487,11 @@ def bench_layers(torch, D, timer, steps):
             "attention_prefill_512_ms": means[2],
             "attention_prefill_512_tflops": pre_flops / means[2] / 1e9,
             "attention_prefill_512_frac_fp32_mfma": pre_flops / means[2] / 1e9 / 157.3,
-            "bytes": {"attention_decode_4096": attn_bytes, "rms_norm_4096x2048": norm_bytes},
+            "short_conv_2048x3_decode_ms": means[3],
+            "short_conv_2048x3_prefill_512_ms": means[4],
+            "short_conv_2048x3_prefill_512_gbps": conv_bytes / means[4] / 1e6,
+            "bytes": {"attention_decode_4096": attn_bytes, "rms_norm_4096x2048": norm_bytes,
+                      "short_conv_prefill_512": conv_bytes},
             "flops": {"attention_prefill_512": pre_flops}}
 
 

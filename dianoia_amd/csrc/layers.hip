@@ -113,30 +113,86 @@ head_norm_rope_kernel(float* x, int x_stride, const float* __restrict__ w,
 }
 
 constexpr int kMaxConvK = 16;
+constexpr int kConvCh = 64;   // channels per workgroup (one wave's lanes)
+constexpr int kConvT = 16;    // tokens per workgroup tile (>= kMaxConvK - 1)
 
-// The gated short convolution (lab_metal.m:383-412), one thread per
-// channel walking the n tokens in order: z = B * X, a causal depthwise conv
-// of the last k values of z (kernel column k - 1 weighting the newest),
-// y = C * conv. The k - 1 previous z come from `history` (rows oldest
-// first), which is left holding the last k - 1. bcx rows hold B, C, X.
+// Gated short convolution (LFM2's conv block; semantics of lab_metal.m:383-412),
+// token-parallel. Per channel c the input sequence is z_j = B_j[c] * X_j[c]
+// for tokens j >= 0, and the carried state for j < 0: history row k - 1 + j
+// (rows oldest first). Output y_t[c] = C_t[c] * a_t with
+//   a_t = w[k-1] z_t + w[k-2] z_{t-1} + ... + w[0] z_{t-k+1},
+// each product rounded, summed left to right from the newest term. Afterwards
+// history row r holds z_{n-k+1+r}.
+//
+// Workgroup (slab, tile) owns kConvCh consecutive channels and kConvT
+// consecutive tokens. It stages z for its tokens and the k - 1 before them in
+// LDS (one product per value, coalesced along channels), then each thread
+// forms whole outputs from the staged window: no token waits on another.
+// Only tile 0 reaches back into the carried state, so tile 0 alone rewrites
+// it: every old row it needs is already in its LDS copy, and no other
+// workgroup reads the state, so the in-place update cannot race.
 __global__ void __launch_bounds__(kThreads)
 conv_kernel(const float* __restrict__ bcx, const float* __restrict__ weight, float* history,
             float* __restrict__ y, int width, int k, int n) {
-  const int ch = blockIdx.x * kThreads + threadIdx.x;
-  if (ch >= width) return;
-  const float* kw = weight + (size_t)ch * k;
-  float past[kMaxConvK];
-  for (int r = 0; r + 1 < k; r++) past[r] = history[(size_t)r * width + ch];
-  for (int t = 0; t < n; t++) {
-    const float* row = bcx + (size_t)t * 3 * width;
-    const float z = row[ch] * row[2 * width + ch];
-    float acc = kw[k - 1] * z;
-    for (int s = 1; s < k; s++) acc += kw[k - 1 - s] * past[k - 1 - s];
-    y[(size_t)t * width + ch] = row[width + ch] * acc;
-    for (int r = 0; r + 2 < k; r++) past[r] = past[r + 1];
-    if (k >= 2) past[k - 2] = z;
+  __shared__ float zs[kConvT + kMaxConvK - 1][kConvCh];
+  const int lane = threadIdx.x % kConvCh, part = threadIdx.x / kConvCh;
+  constexpr int kParts = kThreads / kConvCh;
+  const int c = blockIdx.x * kConvCh + lane;
+  const bool live = c < width;
+  const int t0 = blockIdx.y * kConvT;
+  const int tn = min(kConvT, n - t0);
+  const int span = tn + k - 1;  // staged rows: tokens t0 - (k - 1) .. t0 + tn - 1
+  const size_t row3 = (size_t)3 * width;
+
+  constexpr int kStageIters = (kConvT + kMaxConvK - 1 + kParts - 1) / kParts;
+#pragma unroll
+  for (int m = 0; m < kStageIters; m++) {  // all loads of a thread in flight together
+    const int i = part + m * kParts;
+    if (i < span) {
+      const int j = t0 - (k - 1) + i;
+      float z = 0.0f;
+      if (live) {
+        z = j >= 0 ? bcx[(size_t)j * row3 + c] * bcx[(size_t)j * row3 + 2 * (size_t)width + c]
+                   : history[(size_t)(k - 1 + j) * width + c];
+      }
+      zs[i][lane] = z;
+    }
   }
-  for (int r = 0; r + 1 < k; r++) history[(size_t)r * width + ch] = past[r];
+  __syncthreads();
+  if (!live) return;
+
+  // Taps by lag: wl[s] weights z_{t-s} (register indices stay constant).
+  float wl[kMaxConvK];
+#pragma unroll
+  for (int s = 0; s < kMaxConvK; s++) wl[s] = s < k ? weight[(size_t)c * k + (k - 1 - s)] : 0.0f;
+#pragma unroll
+  for (int m = 0; m < kConvT / kParts; m++) {
+    const int i = part + m * kParts;
+    if (i >= tn) break;
+    const int t = t0 + i;
+    // Row of z_t in the staged window is i + k - 1; z_{t-s} sits s rows up.
+    float a = wl[0] * zs[i + k - 1][lane];
+#pragma unroll
+    for (int s = 1; s < kMaxConvK; s++) {
+      if (s < k) a += wl[s] * zs[i + k - 1 - s][lane];
+    }
+    y[(size_t)t * width + c] = bcx[(size_t)t * row3 + width + c] * a;
+  }
+
+  if (blockIdx.y == 0) {
+    // New state row r = z_{n-k+1+r}: from the staged window when that token
+    // is in it (or is an old state row), else a product of the last tokens.
+    for (int r = part; r + 1 < k; r += kParts) {
+      const int j = n - (k - 1) + r;
+      float z;
+      if (j < tn) {
+        z = zs[j + k - 1][lane];
+      } else {
+        z = bcx[(size_t)j * row3 + c] * bcx[(size_t)j * row3 + 2 * (size_t)width + c];
+      }
+      history[(size_t)r * width + c] = z;
+    }
+  }
 }
 
 // Causal attention of n tokens at positions position.. over their cached
@@ -875,9 +931,10 @@ int dnx_short_conv(const float* bcx, const float* weight, float* history, float*
     return DNX_EINVAL;
   }
   if (n == 0) return DNX_OK;
-  hipLaunchKernelGGL(conv_kernel, dim3((unsigned)((width + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, (hipStream_t)stream, bcx, weight, history, y, (int)width,
-                     (int)k, (int)n);
+  const int64_t slabs = (width + kConvCh - 1) / kConvCh, tiles = (n + kConvT - 1) / kConvT;
+  if (slabs > 0x7fffffff || tiles > 65535) return DNX_EINVAL;
+  hipLaunchKernelGGL(conv_kernel, dim3((unsigned)slabs, (unsigned)tiles), dim3(kThreads), 0,
+                     (hipStream_t)stream, bcx, weight, history, y, (int)width, (int)k, (int)n);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 

@@ -62,8 +62,13 @@ def test_head_norm_rope(gpu_ready, orc, heads, hd, n, stride_pad):
     assert np.array_equal(got[:, heads * hd:], x[:, heads * hd:])  # the padding is untouched
 
 
-@pytest.mark.parametrize("width,k,n", [(6144, 3, 1), (2048, 4, 7), (300, 16, 3), (33, 2, 5)])
+@pytest.mark.parametrize("width,k,n", [(6144, 3, 1), (2048, 4, 7), (300, 16, 3), (33, 2, 5),
+                                       (2048, 3, 512), (300, 16, 100), (100, 16, 7), (64, 4, 3),
+                                       (65, 1, 10), (2048, 4, 129), (130, 16, 14), (70, 16, 79)])
 def test_short_conv_bit_exact(gpu_ready, orc, width, k, n):
+    """y and the carried state bit for bit, across token tiles (n > 64), with
+    fewer new tokens than state rows (old rows shift down), n = k - 1, k = 1
+    (no state) and widths that leave a partial channel slab."""
     rng = np.random.default_rng(width + k + n)
     bcx = rng.standard_normal((n, 3, width)).astype(np.float32)
     weight = rng.standard_normal((width, k)).astype(np.float32)
