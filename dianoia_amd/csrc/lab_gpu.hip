@@ -300,7 +300,10 @@ bool fusable_pair(const Cmd& a, const Cmd& b, const Cmd& c) {
          a.a[5] != b.a[5] && c.a[0] == a.a[5] && c.a[1] == b.a[5] && c.a[2] == n * rows;
 }
 
-bool run_pair(const Cmd& a, const Cmd& b) {
+// DNX_OK, or the launcher's code; DNX_EINVAL means the pair kernel refused
+// the shape before launching anything (x too wide for its LDS at this n), and
+// the caller then runs the three commands unfused.
+int run_pair(const Cmd& a, const Cmd& b) {
   const bool q4 = a.op == kOpMatmulQ4;
   const int64_t x = a.a[3], xOff = a.a[4], rows = a.a[7], cols = a.a[8], n = a.a[9];
   use_as_weights(a.a[0]);
@@ -318,11 +321,12 @@ bool run_pair(const Cmd& a, const Cmd& b) {
                           (const uint16_t*)us, xs, h, u, rows, cols, n, gStream)
          : dnx_gate_up_q8((const int8_t*)gq, (const float*)gs, (const int8_t*)uq,
                           (const float*)us, xs, h, u, rows, cols, n, gStream);
+  if (rc == DNX_EINVAL) return rc;
   if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
   wrote_region(a.a[5], 0, n * rows * 4);
   wrote_region(b.a[5], 0, n * rows * 4);
   if (rc != DNX_OK) LOG("gate/up pair %ldx%ld n=%ld failed (%d)\n", (long)rows, (long)cols, (long)n, rc);
-  return rc == DNX_OK;
+  return rc;
 }
 
 // Fusion of a decode matmul (n = 1) and the argmax of its whole output.
@@ -653,7 +657,14 @@ int64_t lab_gpu_commit(int64_t wait) {
   (void)hipEventRecord(gStart, gStream);
   for (size_t i = 0; i < gCmds.size(); i++) {
     if (i + 2 < gCmds.size() && fusable_pair(gCmds[i], gCmds[i + 1], gCmds[i + 2])) {
-      ok = run_pair(gCmds[i], gCmds[i + 1]) && ok;
+      const int rc = run_pair(gCmds[i], gCmds[i + 1]);
+      if (rc == DNX_EINVAL) {  // not launched: the two matmuls and the glue as recorded
+        ok = run(gCmds[i]) && ok;
+        ok = run(gCmds[i + 1]) && ok;
+        ok = run(gCmds[i + 2]) && ok;
+      } else {
+        ok = rc == DNX_OK && ok;
+      }
       i += 2;
     } else if (i + 1 < gCmds.size() && fusable_argmax(gCmds[i], gCmds[i + 1])) {
       ok = run_matmul_argmax(gCmds[i], gCmds[i + 1]) && ok;

@@ -137,6 +137,34 @@ def test_config1_mlp(gpu, orc):
     assert ok, (rel, ab)
 
 
+@pytest.mark.parametrize("fmt,rows,cols,n", [("q4", 512, 4096, 2), ("q4", 512, 4096, 3),
+                                             ("q4", 512, 4096, 4), ("q8", 256, 10240, 4),
+                                             ("q8", 256, 10240, 3), ("q4", 64, 1024, 4)])
+def test_mlp_short_prompts_wide_hidden(gpu, orc, fmt, rows, cols, n):
+    """The MLP of a 2-4 token prompt tail: where x is too wide for the fused
+    gate/up kernel's LDS (Q4 from about 3400 columns at n = 3..4, Q8 from
+    about 9400) the commit runs the two GEMVs and the glue unfused, with the
+    same bits; where it fits, the fused kernel's result is the same. The up
+    products are compared bit for bit, y to the north-star bar (the glue's
+    SiLU can differ from the CPU's by 1 ulp)."""
+    rng = np.random.default_rng(rows + cols + n)
+    mats = {}
+    for name, (r, c) in (("gate", (rows, cols)), ("up", (rows, cols)), ("down", (cols, rows))):
+        m, qs, sc = quantized(orc, fmt, values(rng, r * c) * 0.1, r, c)
+        gpu.upload(name, m)
+        mats[name] = (qs, sc)
+    x = values(rng, n * cols)
+    y = np.zeros(n * cols, np.float32)
+    gpu.mlp("gate", "up", "down", x, y, n)
+    g = cpu_mode1(orc, fmt, *mats["gate"], x, n)
+    u = cpu_mode1(orc, fmt, *mats["up"], x, n)
+    assert np.array_equal(bits(gpu._aux["u"].view(count=n * rows)), bits(u.reshape(-1)))
+    h = orc.silu_mul(g, u)
+    ref = cpu_mode1(orc, fmt, *mats["down"], h, n).reshape(-1)
+    ok, rel, ab = within_tolerance(y, ref)
+    assert ok, (rel, ab)
+
+
 def test_config2_lm_head_argmax(gpu, orc):
     qs, sc, x = synth.config2()
     gpu.upload("head", QuantMatrix.q8(qs, sc))
