@@ -21,8 +21,9 @@ that figure as ``eager_host_driven_ms_per_step``). ``roofline`` is for the
 headline call: algorithmic bytes per call / its mean time. ``traffic`` comes
 from rocprofv3 FETCH_SIZE / WRITE_SIZE runs committed under profiles/ (null
 when absent). ``cpu_baseline`` times the reference's own CPU kernels
-(oracle/_ref, built from src/c/lab_native.c) on this host over a bounded
-sample of the same workload.
+(oracle/_ref, built from src/c/lab_native.c) on this host, on the headline
+workload and on config 3's GEMM, all cores and 1 thread, medians of 12 runs
+(oracle/cpu_bench.py).
 """
 
 from __future__ import annotations
@@ -586,53 +587,40 @@ def bench_cache_wrap(reps=3):
 
 # ------------------------------------------------------------------ CPU
 
-def cpu_baseline(synth, seconds):
-    """The reference's CPU kernels on this host, on the headline workload:
-    lab_gemm_q8 mode 1 (src/c/lab_native.c:553-579, with its single-threaded
-    input quantization) over the config-2 LM head, then the greedy argmax
-    (argmaxToken, restated in C by the oracle), two weight copies rotated
-    like the GPU run; a bounded number of steps (about `seconds` of work)."""
-    from oracle import oracle as O
-    O.build()
-    kind = "reference" if O.reference_available() else "port"
-    lib = O.Reference() if kind == "reference" else O.get()
-    orc = O.get()
-    threads = min(16, len(os.sched_getaffinity(0)))
-    qs, sc, x = synth.config2()
-    copies = 2
-    sets = [(qs, sc)] + [(qs.copy(), sc.copy()) for _ in range(copies - 1)]
-
-    def step(i):
-        q, s = sets[i % copies]
-        y = lib.gemm_q8(q, s, x, 1, threads=threads, mode=1)[0]
-        return orc.argmax(y)
-
-    step(0)
-    n, t0 = 0, time.perf_counter()
-    while n < 5 or time.perf_counter() - t0 < seconds:
-        step(n)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    algo = q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4
-
-    # The same step on one thread (a few steps; part of the same budget).
-    def step1(i):
-        q, s = sets[i % copies]
-        return orc.argmax(lib.gemm_q8(q, s, x, 1, threads=1, mode=1)[0])
-
-    step1(0)
-    n1, t1 = 0, time.perf_counter()
-    while n1 < 3 or time.perf_counter() - t1 < seconds / 4:
-        step1(n1)
-        n1 += 1
-    dt1 = (time.perf_counter() - t1) / n1
-    return {"value": algo / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{n} config-2 LM-head steps ({dt * 1e3:.3f} ms each, {copies} rotated "
-                      f"weight copies): lab_gemm_q8 mode 1 built from the reference's "
-                      f"src/c/lab_native.c on {threads} OpenMP threads + argmaxToken in C",
-            "ms_per_step": dt * 1e3,
-            "single_thread": {"value": algo / dt1 / 1e9, "unit": "GB/s", "cores": 1,
-                              "ms_per_step": dt1 * 1e3, "steps": n1}}
+def cpu_baseline(runs):
+    """The reference's CPU kernels on this host (oracle/cpu_bench.py in a
+    child process, so that OMP_PROC_BIND=close and OMP_PLACES=cores reach
+    its OpenMP runtime at start-up): lab_gemm_q8 mode 1 + argmaxToken over
+    the config-2 LM head (the headline's workload; `value`), and
+    lab_gemm_q4 mode 1 at config 3's M = 512 (the metric's TOPS half), each
+    on every core this job may use and on 1 thread, median of `runs` runs
+    after 2 warm-ups, built from the reference's src/c/lab_native.c."""
+    import subprocess
+    env = dict(os.environ, OMP_PROC_BIND="close", OMP_PLACES="cores")
+    r = subprocess.run([sys.executable, "-m", "oracle.cpu_bench", "--runs", str(runs),
+                        "--warmup", "2"], cwd=ROOT, env=env, capture_output=True, text=True,
+                       timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError(f"oracle.cpu_bench failed ({r.returncode}):\n{r.stderr[-2000:]}")
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    c2a, c21, c3a, c31 = d["c2_all"], d["c2_1"], d["c3_all"], d["c3_1"]
+    return {"value": c2a["gbps"], "unit": "GB/s", "cores": d["threads"], "kind": d["kind"],
+            "sample": f"config-2 LM-head step (lab_gemm_q8 mode 1 + argmaxToken, 2 rotated "
+                      f"weight copies), median of {d['runs']} runs after {d['warmup']} warm-ups "
+                      f"on {d['threads']} threads ({c2a['ms']:.3f} ms), "
+                      f"{d['library']} built from the reference's src/c/lab_native.c",
+            "ms_per_step": c2a["ms"],
+            "host": {"nproc": d["nproc"], "affinity_cores": d["affinity_cores"],
+                     "omp_num_threads": d["omp_num_threads"], "omp_proc_bind": d["omp_proc_bind"],
+                     "omp_places": d["omp_places"],
+                     "threads_rule": "every core in the affinity mask, capped by the job's "
+                                     "OMP_NUM_THREADS share where set"},
+            "single_thread": {"value": c21["gbps"], "unit": "GB/s", "cores": 1,
+                              "ms_per_step": c21["ms"]},
+            "c3_prefill_gemm_m512": {
+                "unit": "TOPS", "ops": d["c3_ops"],
+                "all_cores": {"value": c3a["tops"], "cores": c3a["threads"], "ms": c3a["ms"]},
+                "single_thread": {"value": c31["tops"], "cores": 1, "ms": c31["ms"]}}}
 
 
 def traffic_from_profiles():
@@ -877,7 +865,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-runs", type=int, default=12,
+                    help="timed runs per CPU-baseline figure (median reported)")
     ap.add_argument("--quick", action="store_true", help="headline config only")
     ap.add_argument("--only", default=None,
                     help="comma-separated names of the other configs to run (default: all)")
@@ -941,7 +930,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(synth, args.cpu_seconds)
+        cpu = cpu_baseline(args.cpu_runs)
 
     line = {
         "metric": METRIC,
