@@ -405,35 +405,6 @@ void orc_gemm_q4(const uint8_t* qs, const uint16_t* scales, const float* xs, int
   }
 }
 
-// Mode-1 products from inputs that are already quantized (xq / xsc given):
-// the second half of lab_gemm_q8 / lab_gemm_q4 alone. Used for stage-wise
-// checks where the GPU's own quantized inputs are fed to both sides.
-void orc_gemm_q8_prequant(const int8_t* qs, const float* scales, const int8_t* xq,
-                          const float* xsc, float* ys, int64_t rows, int64_t cols,
-                          int64_t n, int64_t threads) {
-  const int64_t blocks = cols / Q_BLOCK;
-#pragma omp parallel for num_threads((int)(threads < 1 ? 1 : threads)) schedule(static)
-  for (int64_t r = 0; r < rows; r++) {
-    for (int64_t t = 0; t < n; t++) {
-      ys[t * rows + r] = dot_q8_int8(qs + r * cols, scales + r * blocks, xq + t * cols,
-                                     xsc + t * blocks, blocks);
-    }
-  }
-}
-
-void orc_gemm_q4_prequant(const uint8_t* qs, const uint16_t* scales, const int8_t* xq,
-                          const float* xsc, float* ys, int64_t rows, int64_t cols,
-                          int64_t n, int64_t threads) {
-  const int64_t blocks = cols / Q_BLOCK;
-#pragma omp parallel for num_threads((int)(threads < 1 ? 1 : threads)) schedule(static)
-  for (int64_t r = 0; r < rows; r++) {
-    for (int64_t t = 0; t < n; t++) {
-      ys[t * rows + r] = dot_q4_int8(qs + r * cols / 2, scales + r * blocks, xq + t * cols,
-                                     xsc + t * blocks, blocks);
-    }
-  }
-}
-
 // Per-block int32 dot products d[t][r][b] = sum over the 32 values of block b
 // of w * xq (the sum of the four lane sums above). Integer-exact, so any
 // summation order gives the same value; the GEMM's MFMA tiles must match it.

@@ -109,9 +109,6 @@ class Oracle(_Kernels):
         for name in ("orc_quantize_q8_bf16", "orc_quantize_q8_padded"):
             getattr(L, name).argtypes = [_p, _p, _p, _i64, _i64, _i64]
             getattr(L, name).restype = None
-        for name in ("orc_gemm_q8_prequant", "orc_gemm_q4_prequant"):
-            getattr(L, name).argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64]
-            getattr(L, name).restype = None
         for name in ("orc_block_dots_q8", "orc_block_dots_q4"):
             getattr(L, name).argtypes = [_p, _p, _p, _i64, _i64, _i64]
             getattr(L, name).restype = None
@@ -245,30 +242,6 @@ class Oracle(_Kernels):
         rows, cols = x.shape
         self.lib.orc_steer(_ptr(x), _ptr(v), rows, cols, mode, scale)
         return x
-
-    def gemm_q8_prequant(self, qs, scales, xq, xsc, threads=8):
-        qs = np.ascontiguousarray(qs, np.int8)
-        scales = np.ascontiguousarray(scales, np.float32)
-        rows, cols = qs.shape
-        xq = np.ascontiguousarray(xq, np.int8).reshape(-1, cols)
-        xsc = np.ascontiguousarray(xsc, np.float32).reshape(xq.shape[0], -1)
-        n = xq.shape[0]
-        ys = np.zeros((n, rows), np.float32)
-        self.lib.orc_gemm_q8_prequant(_ptr(qs), _ptr(scales), _ptr(xq), _ptr(xsc), _ptr(ys),
-                                      rows, cols, n, threads)
-        return ys
-
-    def gemm_q4_prequant(self, qs, scales, xq, xsc, threads=8):
-        qs = np.ascontiguousarray(qs, np.uint8)
-        scales = np.ascontiguousarray(scales, np.uint16)
-        rows, cols = qs.shape[0], qs.shape[1] * 2
-        xq = np.ascontiguousarray(xq, np.int8).reshape(-1, cols)
-        xsc = np.ascontiguousarray(xsc, np.float32).reshape(xq.shape[0], -1)
-        n = xq.shape[0]
-        ys = np.zeros((n, rows), np.float32)
-        self.lib.orc_gemm_q4_prequant(_ptr(qs), _ptr(scales), _ptr(xq), _ptr(xsc), _ptr(ys),
-                                      rows, cols, n, threads)
-        return ys
 
     def block_dots_q8(self, qs, xq):
         qs = np.ascontiguousarray(qs, np.int8)
