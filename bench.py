@@ -430,6 +430,54 @@ def bench_c4(torch, D, synth, timer, steps, warmup):
             "pair_tops": 2 * ops / (means[1] + means[2] + means[3]) / 1e9}
 
 
+def bench_callers(torch, D, synth, timer, steps):
+    """The quantized products' other callers at their own shapes, on the
+    product route (dnx_matmul_*, what lab_gpu_enc_matmul_* runs): the audio
+    encoder's Q4 linears (hidden 768, FFN 1792, projector into 2048;
+    audio_encoder.dart:197-205) at 1, 13 and 375 rows, and the vision
+    encoder's Q8 attention projections (1024 x 1024) and projector
+    (4096 -> 4096 -> 2048; vision_encoder.dart:252-316) at its patch and
+    image-token counts; int8 inputs (the ABI's default), plus the float-input
+    route at two vision shapes. Weights rotate over copies past the MALL."""
+    rng = np.random.default_rng(9)
+    cases = ([("audio_enc", "q4", r, c, n, True)
+              for r, c in ((1792, 768), (768, 1792), (2304, 768), (768, 768), (2048, 768),
+                           (2048, 2048)) for n in (1, 13, 375)] +
+             [("vision", "q8", r, c, n, True)
+              for r, c, n in ((1024, 1024, 1024), (1024, 1024, 4096), (4096, 4096, 256),
+                              (4096, 4096, 1024), (2048, 4096, 256), (2048, 4096, 1024))] +
+             [("vision", "q8", 1024, 1024, 1024, False), ("vision", "q8", 4096, 4096, 256, False)])
+    out = {}
+    reps = max(10, steps // 10)
+    for who, fmt, rows, cols, n, int8 in cases:
+        if fmt == "q4":
+            q, sc = synth.q4_weights(rng, rows, cols)
+            nbytes = q4_bytes(rows, cols)
+            f = D.matmul_q4
+        else:
+            q, sc = synth.q8_weights(rng, rows, cols)
+            nbytes = q8_bytes(rows, cols)
+            f = D.matmul_q8
+        copies = min(copies_for(nbytes), 256)
+        q0, s0 = dev(torch, q), dev(torch, sc)
+        ws = [(q0, s0)] + [(q0.clone(), s0.clone()) for _ in range(copies - 1)]
+        x = dev(torch, synth.activations(rng, n, cols))
+        y = torch.empty((n, rows), device="cuda")
+        wsp = D.matmul_workspace(cols, n)
+
+        def fn(i, ws=ws, x=x, y=y, wsp=wsp, f=f, rows=rows, cols=cols, n=n, int8=int8):
+            w = ws[i % len(ws)]
+            f(w[0], w[1], x, y, rows, cols, n, int8, wsp)
+
+        ms = timer.time(fn, reps, 3)
+        key = f"{who}_{fmt}_{rows}x{cols}_n{n}" + ("" if int8 else "_float_inputs")
+        out[key] = {"ms": ms, "weight_gbps": nbytes / ms / 1e6,
+                    "tops": 2 * n * rows * cols / ms / 1e9, "weight_copies": copies}
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_layers(torch, D, timer, steps):
     """The decoder's other layer steps (lab_gpu_enc_* semantics): attention
     decode over a 4096-position cache (32 query heads, 8 KV heads, hd 128;
@@ -919,7 +967,8 @@ def main():
             print(f"bench: {name}", file=sys.stderr, flush=True)
             configs[name] = fn(torch, D, synth, timer, args.steps, args.warmup)
             torch.cuda.empty_cache()
-        for name, fn in (("load_time_converters", lambda: bench_loaders(torch, D, timer, args.steps)),
+        for name, fn in (("other_callers", lambda: bench_callers(torch, D, synth, timer, args.steps)),
+                         ("load_time_converters", lambda: bench_loaders(torch, D, timer, args.steps)),
                          ("layer_steps", lambda: bench_layers(torch, D, timer, args.steps)),
                          ("weight_cache_wrap", bench_cache_wrap)):
             if only is not None and name not in only:

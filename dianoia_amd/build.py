@@ -22,7 +22,7 @@ LIB = os.path.join(HERE, "libdianoia_amd.so")
 UBENCH_SRC = "ubench_tile.hip"
 UBENCH_LIB = os.path.join(HERE, "libdnx_ubench.so")
 SOURCES = ["kernels.hip", "gemv.hip", "gemm.hip", "gemm_f16.hip", "gemm_f6.hip", "layers.hip",
-           "lab_gpu.hip"]
+           "matmul.hip", "lab_gpu.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -31,6 +31,7 @@
 #include <vector>
 
 #include "dnx_kernels.h"
+#include "matmul_route.h"
 #include "lab_gpu.h"
 
 #define LOG(...) fprintf(stderr, "lab_gpu: " __VA_ARGS__)
@@ -96,10 +97,9 @@ std::vector<Region> gWritten;
 Buffer gBuffers[kMaxBuffers];
 int64_t gBufferCount = 0, gFree[kMaxBuffers], gFreeCount = 0, gLive = 0;
 
-// Quantized-activation scratch for the GEMM path, and argmax partials.
-int8_t* gXq = nullptr;
-float* gXs = nullptr;
-int64_t gXCapacity = 0;  // values
+// Quantized-activation workspace of the GEMM routes, and argmax partials.
+void* gWs = nullptr;
+int64_t gWsBytes = 0;
 void* gArgmaxWs = nullptr;
 void* gGemvArgmaxWs = nullptr;  // zeroed once; each fused argmax leaves it zero
 
@@ -193,17 +193,18 @@ void after_dispatch(int kind) {
   }
 }
 
-bool grow_scratch(int64_t values) {
-  if (values <= gXCapacity) return true;
-  const int64_t cap = values > (1 << 20) ? values : (1 << 20);
-  if (gXq) (void)hipFree(gXq);
-  if (gXs) (void)hipFree(gXs);
-  gXq = nullptr;
-  gXs = nullptr;
-  gXCapacity = 0;
-  if (hipMalloc(&gXq, (size_t)cap) != hipSuccess) return false;
-  if (hipMalloc(&gXs, (size_t)(cap / 32) * 4) != hipSuccess) return false;
-  gXCapacity = cap;
+// Grows the matmul workspace to what a command of this shape needs (at
+// encode time: outside the commit that launches it).
+bool grow_scratch(int64_t cols, int64_t n) {
+  const int64_t need = dnx_matmul_workspace_bytes(cols, n);
+  if (need < 0) return false;
+  if (need <= gWsBytes) return true;
+  const int64_t cap = need > (4 << 20) ? need : (4 << 20);
+  if (gWs) (void)hipFree(gWs);
+  gWs = nullptr;
+  gWsBytes = 0;
+  if (hipMalloc(&gWs, (size_t)cap) != hipSuccess) return false;
+  gWsBytes = cap;
   return true;
 }
 
@@ -237,51 +238,31 @@ void record(Op op, std::initializer_list<int64_t> args) {
   gCmds.push_back(c);
 }
 
-// The matmul of one recorded command: GEMV (bit-exact) for n <= 4, else (or
-// when x is too wide for the GEMV's LDS) the activation quantizer and the
-// int8-MFMA GEMM.
+// The matmul of one recorded command, on the product route of
+// matmul_route.h (the same as dnx_matmul_q8 / _q4).
 bool run_matmul(const Cmd& c, bool q4) {
   const int64_t w = c.a[0], qsOff = c.a[1], scOff = c.a[2], x = c.a[3], xOff = c.a[4];
   const int64_t y = c.a[5], yOff = c.a[6], rows = c.a[7], cols = c.a[8], n = c.a[9];
   use_as_weights(w);
   read_region(x, xOff, n * cols * 4);
-  const void* qs = dev_at(w, qsOff);
-  const void* sc = dev_at(w, scOff);
-  const float* xs = (const float*)dev_at(x, xOff);
-  float* ys = (float*)dev_at(y, yOff);
-  int rc;
-  rc = DNX_EINVAL;
-  if (!c.int8_inputs) {  // float inputs: the exact mode-0 GEMV, any n
-    rc = q4 ? dnx_gemv_q4_float((const uint8_t*)qs, (const uint16_t*)sc, xs, ys, rows, cols, n,
-                                gStream)
-            : dnx_gemv_q8_float((const int8_t*)qs, (const float*)sc, xs, ys, rows, cols, n,
-                                gStream);
-    if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4 : kKindGemvQ8);
-    wrote_region(y, yOff, n * rows * 4);
-    if (rc != DNX_OK) LOG("float-input matmul %s %ldx%ld n=%ld failed (%d)\n", q4 ? "q4" : "q8",
-                          (long)rows, (long)cols, (long)n, rc);
-    return rc == DNX_OK;
-  }
-  if (n <= 4) {
-    rc = q4 ? dnx_gemv_q4((const uint8_t*)qs, (const uint16_t*)sc, xs, ys, rows, cols, n,
-                          gStream)
-            : dnx_gemv_q8((const int8_t*)qs, (const float*)sc, xs, ys, rows, cols, n, gStream);
-    if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
-  }
-  if (rc != DNX_OK) {  // n > 4, or x too wide for the GEMV's LDS
-    rc = dnx_quantize_q8(xs, gXq, gXs, n, cols, cols, gStream);
-    if (rc == DNX_OK) {
-      after_dispatch(kKindQuantize);
-      rc = q4 ? dnx_gemm_q4((const uint8_t*)qs, (const uint16_t*)sc, gXq, gXs, ys, rows, cols, n,
-                            gStream)
-              : dnx_gemm_q8((const int8_t*)qs, (const float*)sc, gXq, gXs, ys, rows, cols, n,
-                            gStream);
-      if (rc == DNX_OK) after_dispatch(q4 ? kKindGemmQ4I8 : kKindGemmQ8I8);
-    }
-  }
+  const int rc = dnx::matmul_route(
+      q4, dev_at(w, qsOff), dev_at(w, scOff), (const float*)dev_at(x, xOff),
+      (float*)dev_at(y, yOff), rows, cols, n, c.int8_inputs, gWs, gWsBytes, gStream,
+      [q4](dnx::MatmulStep step) {
+        switch (step) {
+          case dnx::MatmulStep::kGemvFloat: after_dispatch(q4 ? kKindGemvQ4 : kKindGemvQ8); break;
+          case dnx::MatmulStep::kGemv: after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8); break;
+          case dnx::MatmulStep::kQuantize:
+          case dnx::MatmulStep::kQuantizeF6: after_dispatch(kKindQuantize); break;
+          case dnx::MatmulStep::kGemm:
+          case dnx::MatmulStep::kGemmF6: after_dispatch(q4 ? kKindGemmQ4I8 : kKindGemmQ8I8); break;
+        }
+      });
   wrote_region(y, yOff, n * rows * 4);
-  if (rc != DNX_OK) LOG("matmul %s %ldx%ld n=%ld failed (%d)\n", q4 ? "q4" : "q8", (long)rows,
-                        (long)cols, (long)n, rc);
+  if (rc != DNX_OK) {
+    LOG("matmul %s %ldx%ld n=%ld (%s inputs) failed (%d)\n", q4 ? "q4" : "q8", (long)rows,
+        (long)cols, (long)n, c.int8_inputs ? "int8" : "float", rc);
+  }
   return rc == DNX_OK;
 }
 
@@ -712,7 +693,7 @@ static void enc_matmul(Op op, int64_t w, int64_t qsOffset, int64_t scalesOffset,
                   in_bounds(x, xOffset, n * cols * 4) && in_bounds(y, yOffset, n * rows * 4) &&
                   ((uintptr_t)dev_at(w, qsOffset) % 16) == 0 &&
                   ((uintptr_t)dev_at(w, scalesOffset) % (q4 ? 2 : 4)) == 0 &&
-                  (xOffset % 4) == 0 && (yOffset % 4) == 0 && grow_scratch(n * cols);
+                  (xOffset % 4) == 0 && (yOffset % 4) == 0 && grow_scratch(cols, n);
   if (!ok) {
     LOG("enc_matmul_%s: invalid arguments (rows=%ld cols=%ld n=%ld)\n", q4 ? "q4" : "q8",
         (long)rows, (long)cols, (long)n);

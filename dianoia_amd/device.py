@@ -279,3 +279,27 @@ def copy(src, dst, count: int, stream=None) -> None:
 def steer(x, v, rows: int, cols: int, mode: int, scale: float, stream=None) -> None:
     _check(_lib.load().dnx_steer(_ptr(x), _ptr(v), rows, cols, mode, scale, _stream(stream)),
            "dnx_steer")
+
+
+def matmul_workspace(cols: int, n: int, device="cuda") -> torch.Tensor:
+    """Device workspace for dnx_matmul_q8 / _q4 at this shape."""
+    nbytes = int(_lib.load().dnx_matmul_workspace_bytes(cols, n))
+    if nbytes < 0:
+        raise RuntimeError(f"dnx_matmul_workspace_bytes({cols}, {n}) refused the shape")
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+
+
+def matmul_q8(qs, scales, x, y, rows: int, cols: int, n: int, int8_inputs: bool, workspace,
+              stream=None) -> None:
+    """The product route of lab_gpu_enc_matmul_q8 (dnx_matmul_q8)."""
+    _check(_lib.load().dnx_matmul_q8(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
+                                     int(int8_inputs), _ptr(workspace), workspace.numel(),
+                                     _stream(stream)), "dnx_matmul_q8")
+
+
+def matmul_q4(qs, scales, x, y, rows: int, cols: int, n: int, int8_inputs: bool, workspace,
+              stream=None) -> None:
+    """The product route of lab_gpu_enc_matmul_q4 (dnx_matmul_q4)."""
+    _check(_lib.load().dnx_matmul_q4(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
+                                     int(int8_inputs), _ptr(workspace), workspace.numel(),
+                                     _stream(stream)), "dnx_matmul_q4")

@@ -212,6 +212,24 @@ int64_t dnx_gemm_q4_f6p_noalloc_max_floats(void);
 int dnx_gemm_q4_f6p_noalloc(const void* packed, const void* panel, float* y, int64_t rows,
                             int64_t cols, int64_t n, dnx_stream_t stream);
 
+// One matmul command's product route on device pointers: the kernels
+// lab_gpu_enc_matmul_q8 / _q4 (lib/src/gpu.dart:137-190) run at commit, for
+// engines that call the ABI's products without its command buffer.
+// int8_inputs 1 (mode 1): n <= 4 the exact GEMV above (bit-identical to
+// lab_gemm_* mode 1), else x quantized into `workspace` and a GEMM (the
+// int8-MFMA GEMM; for Q4 at >= 320 tokens, >= 4096 rows and K <= 4096 the
+// fp6-MFMA GEMM, which is faster there). int8_inputs 0 (mode 0): the exact
+// float-input GEMV, 4 tokens per weight pass. workspace: at least
+// dnx_matmul_workspace_bytes(cols, n) bytes of device memory (unused by the
+// GEMV routes; may be null there).
+int64_t dnx_matmul_workspace_bytes(int64_t cols, int64_t n);
+int dnx_matmul_q8(const int8_t* qs, const float* scales, const float* x, float* y, int64_t rows,
+                  int64_t cols, int64_t n, int int8_inputs, void* workspace,
+                  int64_t workspace_bytes, dnx_stream_t stream);
+int dnx_matmul_q4(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
+                  int64_t rows, int64_t cols, int64_t n, int int8_inputs, void* workspace,
+                  int64_t workspace_bytes, dnx_stream_t stream);
+
 // GGUF Q8_0 / Q4_0 blocks split into the engine's layout on the GPU, bit
 // for bit as splitQ8_0 (lib/src/gguf.dart:270-282: int8 values and the fp16
 // d widened to fp32) and splitQ4_0 (:208-218: nibble bytes and the fp16
