@@ -219,6 +219,62 @@ __global__ void __launch_bounds__(kPanelThreads) pack_f6_panel_kernel(
 
 // ----------------------------------------------------------------- the GEMM
 
+constexpr int kTileM = 4;   // 32-token groups per workgroup
+
+// Bytes of LDS the epilogue below uses: both parities' partial tiles of the
+// workgroup, [token group][parity][32 tokens][BN + 4 floats].
+template <int SN>
+constexpr int epilogue_lds_bytes() {
+  return kTileM * 2 * kTokens * (SN * 32 + 4) * 4;
+}
+
+// The workgroup's 128 x BN outputs: every wave puts its partial sums (one
+// parity of K) into LDS in [token][row] order, then every wave adds the two
+// parities (even + odd, a fixed order) for 1/8 of the outputs and stores
+// them 16 bytes per lane, consecutive lanes along a token's row (a row of
+// BN floats is BN / 4 lanes). `vec` (uniform): out and N allow 16-byte
+// stores; otherwise each value is stored alone. Called by all waves after
+// the K loop's last barrier (the partials overwrite the stage buffers).
+template <int SN>
+DNX_DEV void store_tile_sums(uint8_t* lds, const v16f* acc, int wave, int lane, int m0, int n0,
+                             int M, int N, float* out, bool vec) {
+  constexpr int BN = SN * 32;
+  constexpr int RS = BN + 4;  // row stride in floats (spreads the two rows a write covers)
+  constexpr int C4 = BN / 4;  // float4 per token row
+  constexpr int PER = kTileM * kTokens * C4 / kWaves / 64;
+  static_assert(kTileM * kTokens * C4 % (kWaves * 64) == 0, "whole float4 per lane");
+  const int mg = wave & 3, kp = wave >> 2;
+  float* part = (float*)lds + (size_t)(mg * 2 + kp) * kTokens * RS;
+#pragma unroll
+  for (int j = 0; j < SN; j++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int m = (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+      part[m * RS + j * 32 + (lane & 31)] = acc[j][v];
+    }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < PER; it++) {
+    const int idx = (wave * PER + it) * 64 + lane;
+    const int tok = idx / C4, c4 = idx - tok * C4;
+    const float* e = (const float*)lds + ((size_t)((tok >> 5) * 2) * kTokens + (tok & 31)) * RS + c4 * 4;
+    const float4 a = *(const float4*)e;
+    const float4 b = *(const float4*)(e + kTokens * RS);
+    const int m = m0 + tok, r = n0 + c4 * 4;
+    if (m >= M || r >= N) continue;
+    const float4 o = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    float* dst = out + (size_t)m * N + r;
+    if (vec) {
+      *(float4*)dst = o;
+    } else {
+      dst[0] = o.x;
+      if (r + 1 < N) dst[1] = o.y;
+      if (r + 2 < N) dst[2] = o.z;
+      if (r + 3 < N) dst[3] = o.w;
+    }
+  }
+}
+
 struct F6Params {
   const uint8_t* qs;       // Q4 nibbles [rows][cols/2]
   const uint16_t* scales;  // fp16 bits [rows][cols/32]
@@ -228,9 +284,9 @@ struct F6Params {
   int rows, cols, n;
   int tiles_m, tiles;      // workgroup tiles (128 tokens x BN rows) of one K split
   int split_blocks;        // blocks per K split (blockIdx.y), a multiple of kKB
+  int vec;                 // the output allows 16-byte stores (16-byte aligned, rows % 4 == 0)
 };
 
-constexpr int kTileM = 4;   // 32-token groups per workgroup
 constexpr int kKB = 16;     // blocks per stage
 constexpr int kRecW = 32;   // LDS bytes per staged (row, block): 6 fp6 dwords + 2 operand dwords
 constexpr int kRing = 4;    // activation records in flight per wave (its next blocks)
@@ -246,8 +302,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f6_q4_kernel(F6Params p) {
   constexpr int PP = (kPairs + kThreads - 1) / kThreads;
   constexpr int kCPieces = kC / 16;
   constexpr int CP = (kCPieces + kThreads - 1) / kThreads;
-  constexpr int kRed = kTileM * SN * 16 * 64 * 4;  // the odd parity's sums
-  constexpr int kLds = 2 * kStage > kRed ? 2 * kStage : kRed;
+  constexpr int kLds = 2 * kStage > epilogue_lds_bytes<SN>() ? 2 * kStage : epilogue_lds_bytes<SN>();
   static_assert((kKB / 2) % kRing == 0, "ring slots must repeat each stage");
   __shared__ __align__(16) uint8_t lds[kLds];
 
@@ -426,27 +481,8 @@ __global__ void __launch_bounds__(kThreads) gemm_f6_q4_kernel(F6Params p) {
 
   if (!first) fold(SN - 1);
 
-  // ---- the two parities' sums, added in a fixed order (even + odd)
-  float* red = (float*)lds + (size_t)mg * SN * 16 * 64;
-  if (kp == 1) {
-#pragma unroll
-    for (int j = 0; j < SN; j++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) red[(j * 16 + v) * 64 + lane] = acc[j][v];
-  }
-  __syncthreads();
-  if (kp == 1 || !live) return;
   float* out = p.part ? p.part + (size_t)blockIdx.y * M * N : p.y;
-#pragma unroll
-  for (int j = 0; j < SN; j++) {
-    const int r = n0 + j * 32 + (lane & 31);
-    if (r >= N) continue;
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int m = g * kTokens + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      if (m < M) out[(size_t)m * N + r] = acc[j][v] + red[(j * 16 + v) * 64 + lane];
-    }
-  }
+  store_tile_sums<SN>(lds, acc, wave, lane, tm * kTileM * kTokens, n0, M, N, out, p.vec != 0);
 }
 
 // ----------------------------------------------- prepacked weights (load time)
@@ -500,6 +536,7 @@ struct F6PParams {
   int rows, cols, n;
   int tiles_m, tiles;
   int split_blocks;        // a multiple of kPKB
+  int vec;                 // the output allows 16-byte stores
 };
 
 template <int SN>
@@ -509,8 +546,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   constexpr int kStage = kPKB * 2 * kHalf;
   constexpr int kPieces = BN * kPKB * 2;        // 16-byte pieces per stage
   constexpr int PW = (kPieces + kThreads - 1) / kThreads;
-  constexpr int kRed = kTileM * SN * 16 * 64 * 4;
-  constexpr int kLds = 2 * kStage > kRed ? 2 * kStage : kRed;
+  constexpr int kLds = 2 * kStage > epilogue_lds_bytes<SN>() ? 2 * kStage : epilogue_lds_bytes<SN>();
   __shared__ __align__(16) uint8_t lds[kLds];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -657,27 +693,8 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
     __syncthreads();
   }
   fold(SN - 1);
-
-  float* red = (float*)lds + (size_t)mg * SN * 16 * 64;
-  if (kp == 1) {
-#pragma unroll
-    for (int j = 0; j < SN; j++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) red[(j * 16 + v) * 64 + lane] = acc[j][v];
-  }
-  __syncthreads();
-  if (kp == 1 || !live) return;
   float* out = p.part ? p.part + (size_t)blockIdx.y * M * N : p.y;
-#pragma unroll
-  for (int j = 0; j < SN; j++) {
-    const int r = n0 + j * 32 + (lane & 31);
-    if (r >= N) continue;
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int m = g * kTokens + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      if (m < M) out[(size_t)m * N + r] = acc[j][v] + red[(j * 16 + v) * 64 + lane];
-    }
-  }
+  store_tile_sums<SN>(lds, acc, wave, lane, tm * kTileM * kTokens, n0, M, N, out, p.vec != 0);
 }
 
 // y = the split partials summed in split order (deterministic).
@@ -789,6 +806,7 @@ int launch_f6(const uint8_t* qs, const uint16_t* scales, const uint8_t* panel, f
     p.part = part_workspace((size_t)splits * count * 4);
     if (p.part == nullptr) return DNX_ENOMEM;
   }
+  p.vec = (rows % 4 == 0 && ((uintptr_t)(p.part ? (void*)p.part : (void*)y) & 15) == 0) ? 1 : 0;
   hipLaunchKernelGGL((gemm_f6_q4_kernel<SN>), dim3((unsigned)p.tiles, (unsigned)splits),
                      dim3(kThreads), 0, stream, p);
   if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
@@ -837,6 +855,7 @@ int launch_f6p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t ro
       if (p.part == nullptr) return DNX_ENOMEM;
     }
   }
+  p.vec = (rows % 4 == 0 && ((uintptr_t)(p.part ? (void*)p.part : (void*)y) & 15) == 0) ? 1 : 0;
   hipLaunchKernelGGL((gemm_f6p_kernel<SN>), dim3((unsigned)p.tiles, (unsigned)splits),
                      dim3(kThreads), 0, stream, p);
   if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
