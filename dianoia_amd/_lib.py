@@ -35,6 +35,8 @@ SIGNATURES = {
     "lab_gpu_commit": ([_i64], _i64),
     "lab_gpu_wait": ([], _i64),
     "lab_gpu_last_ms": ([], ctypes.c_double),
+    "lab_gpu_transfer_bytes": ([_p, _p], None),
+    "lab_gpu_tracking_writes": ([], _i64),
     "lab_gpu_enc_matmul_q8": ([_i64] * 10, None),
     "lab_gpu_enc_matmul_q4": ([_i64] * 10, None),
     "lab_gpu_enc_swiglu": ([_i64] * 3, None),

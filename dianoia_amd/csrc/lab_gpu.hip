@@ -16,17 +16,31 @@
 //   wrote is copied back to the shadow. Stream order gives each dispatch
 //   the previous one's writes (the reference's barrier after each
 //   dispatch, lab_vulkan.c:769-787).
+// * Host writes are tracked per page, so that a commit uploads only what
+//   the host changed: a shadow page whose bytes equal HBM's is "clean" and
+//   write-protected (mprotect). The host's first write to it faults; the
+//   SIGSEGV handler installed by lab_gpu_init marks the page dirty, lifts
+//   the protection and returns, and the write proceeds. A read region
+//   uploads its dirty pages whole (protected again before the copy is
+//   queued, so a later write faults again), and a copy-back makes the
+//   pages it covers whole clean. Faults the handler does not own go to the
+//   handler installed before it. DIANOIA_GPU_TRACK_WRITES=0 turns tracking
+//   off (every read region is uploaded, as the reference's coherent
+//   memory implies); so does a buffer whose shadow cannot be protected.
 // * Scratch (quantized activations, argmax partials) is internal device
 //   memory: it does not count as a live buffer.
 
 #include <hip/hip_runtime.h>
+#include <signal.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/mman.h>
 #include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
 #include <utility>
 #include <vector>
 
@@ -56,6 +70,17 @@ struct Buffer {
   int64_t size = 0;
   bool live = false;
   bool weights = false;   // HBM copy is authoritative and immutable
+  bool tracked = false;   // host writes tracked per page (see Tracked below)
+};
+
+// Page tracking of a shadow, read by the SIGSEGV handler: [start, end) is the
+// shadow (whole pages), clean[p] = 1 while page p equals HBM and is
+// write-protected. start is published last on creation and cleared first on
+// release, so the handler never sees a half-made entry.
+struct Tracked {
+  std::atomic<uintptr_t> start{0};
+  uintptr_t end = 0;
+  uint8_t* clean = nullptr;
 };
 
 enum Op {
@@ -97,6 +122,15 @@ std::vector<Region> gWritten;
 Buffer gBuffers[kMaxBuffers];
 int64_t gBufferCount = 0, gFree[kMaxBuffers], gFreeCount = 0, gLive = 0;
 
+// Host-write tracking (see the header comment).
+Tracked gTracked[kMaxBuffers];
+std::atomic<int64_t> gTrackedSpan{0};  // entries [0, span) may be in use
+bool gTrack = false;                    // tracking enabled and handler installed
+int64_t gPage = 4096;
+struct sigaction gPrevSegv;
+// Bytes moved over PCIe by commits and first weight uploads (cumulative).
+int64_t gUpBytes = 0, gDownBytes = 0;
+
 // Quantized-activation workspace of the GEMM routes, and argmax partials.
 void* gWs = nullptr;
 int64_t gWsBytes = 0;
@@ -111,6 +145,107 @@ bool in_bounds(int64_t h, int64_t offset, int64_t bytes) {
 
 char* dev_at(int64_t h, int64_t offset) { return (char*)gBuffers[h].dev + offset; }
 
+// ---------------------------------------------------------------- host-write tracking
+
+// A write to a write-protected shadow page: that page becomes dirty and
+// writable again, and the write is retried. Anything else goes to the
+// handler that was installed before lab_gpu_init.
+void on_segv(int sig, siginfo_t* info, void* ctx) {
+  const uintptr_t a = (uintptr_t)info->si_addr;
+  if (info->si_code == SEGV_ACCERR) {
+    const int64_t span = gTrackedSpan.load(std::memory_order_acquire);
+    for (int64_t i = 0; i < span; i++) {
+      const uintptr_t start = gTracked[i].start.load(std::memory_order_acquire);
+      if (start == 0 || a < start || a >= gTracked[i].end) continue;
+      const uintptr_t page = (a - start) / (uintptr_t)gPage;
+      __atomic_store_n(&gTracked[i].clean[page], (uint8_t)0, __ATOMIC_RELEASE);
+      if (mprotect((void*)(start + page * (uintptr_t)gPage), (size_t)gPage,
+                   PROT_READ | PROT_WRITE) == 0) {
+        return;
+      }
+      break;
+    }
+  }
+  if (gPrevSegv.sa_flags & SA_SIGINFO) {
+    if (gPrevSegv.sa_sigaction != nullptr) {
+      gPrevSegv.sa_sigaction(sig, info, ctx);
+      return;
+    }
+  } else if (gPrevSegv.sa_handler != SIG_DFL && gPrevSegv.sa_handler != SIG_IGN) {
+    gPrevSegv.sa_handler(sig);
+    return;
+  }
+  // The default action: restored, the access repeats and ends the process
+  // as it would have without this handler.
+  signal(SIGSEGV, SIG_DFL);
+}
+
+int64_t shadow_pages(int64_t bytes) { return (bytes + gPage - 1) / gPage; }
+
+// Stops tracking h: every page counts as dirty from now on.
+void untrack(int64_t h) {
+  Buffer& b = gBuffers[h];
+  if (!b.tracked) return;
+  gTracked[h].start.store(0, std::memory_order_release);
+  (void)mprotect(b.host, (size_t)(shadow_pages(b.size) * gPage), PROT_READ | PROT_WRITE);
+  b.tracked = false;
+}
+
+// Marks pages [p0, p1) of h clean, then write-protects them: a host write
+// before the protection lands before any copy queued after this call reads
+// the page, and one after it faults and marks the page dirty again.
+void make_clean(int64_t h, int64_t p0, int64_t p1) {
+  Buffer& b = gBuffers[h];
+  if (!b.tracked || p1 <= p0) return;
+  uint8_t* c = gTracked[h].clean;
+  for (int64_t p = p0; p < p1; p++) __atomic_store_n(&c[p], (uint8_t)1, __ATOMIC_RELEASE);
+  if (mprotect((char*)b.host + p0 * gPage, (size_t)((p1 - p0) * gPage), PROT_READ) != 0) {
+    LOG("write-protecting a host view failed; buffer %ld is uploaded whole from now on\n",
+        (long)h);
+    untrack(h);
+  }
+}
+
+bool page_clean(int64_t h, int64_t p) {
+  return __atomic_load_n(&gTracked[h].clean[p], __ATOMIC_ACQUIRE) != 0;
+}
+
+// Starts tracking a new shadow whose bytes equal HBM: every page clean.
+void track(int64_t h) {
+  Buffer& b = gBuffers[h];
+  b.tracked = false;
+  if (!gTrack || b.host == nullptr || ((uintptr_t)b.host % (uintptr_t)gPage) != 0) return;
+  const int64_t pages = shadow_pages(b.size);
+  Tracked& t = gTracked[h];
+  uint8_t* c = (uint8_t*)realloc(t.clean, (size_t)pages);
+  if (c == nullptr) return;
+  memset(c, 0, (size_t)pages);
+  t.clean = c;
+  t.end = (uintptr_t)b.host + (uintptr_t)(pages * gPage);
+  t.start.store((uintptr_t)b.host, std::memory_order_release);
+  int64_t span = gTrackedSpan.load(std::memory_order_relaxed);
+  while (span < h + 1 && !gTrackedSpan.compare_exchange_weak(span, h + 1)) {
+  }
+  b.tracked = true;
+  make_clean(h, 0, pages);
+}
+
+// The handler stays ours only while nobody replaced it; otherwise tracking
+// stops (a write fault would no longer reach it).
+void check_handler() {
+  if (!gTrack) return;
+  struct sigaction cur;
+  if (sigaction(SIGSEGV, nullptr, &cur) == 0 && (cur.sa_flags & SA_SIGINFO) &&
+      cur.sa_sigaction == on_segv) {
+    return;
+  }
+  LOG("another SIGSEGV handler replaced this library's; host-write tracking is off\n");
+  for (int64_t h = 0; h < gBufferCount; h++) {
+    if (gBuffers[h].live) untrack(h);
+  }
+  gTrack = false;
+}
+
 int64_t create(int64_t bytes, bool shadow) {
   if (!gReady || bytes <= 0) return -1;
   int64_t handle;
@@ -123,7 +258,8 @@ int64_t create(int64_t bytes, bool shadow) {
   }
   Buffer b;
   if (hipMalloc(&b.dev, (size_t)bytes) != hipSuccess) return -1;
-  if (shadow && hipHostMalloc(&b.host, (size_t)bytes, hipHostMallocDefault) != hipSuccess) {
+  if (shadow && hipHostMalloc(&b.host, (size_t)(shadow_pages(bytes) * gPage),
+                              hipHostMallocDefault) != hipSuccess) {
     (void)hipFree(b.dev);
     return -1;
   }
@@ -156,20 +292,40 @@ void upload_gaps(int64_t h, int64_t offset, int64_t bytes) {
     if (c.first > at) {
       (void)hipMemcpyAsync(dev_at(h, at), (char*)b.host + at, (size_t)(c.first - at),
                            hipMemcpyHostToDevice, gStream);
+      gUpBytes += c.first - at;
     }
     if (c.second > at) at = c.second;
   }
   if (at < end) {
     (void)hipMemcpyAsync(dev_at(h, at), (char*)b.host + at, (size_t)(end - at),
                          hipMemcpyHostToDevice, gStream);
+    gUpBytes += end - at;
   }
 }
 
-// Makes the device copy of [offset, offset + bytes) of h current.
+// Makes the device copy of [offset, offset + bytes) of h current: with
+// tracking, each run of dirty pages it touches is uploaded whole (and made
+// clean first); without, the whole region.
 void read_region(int64_t h, int64_t offset, int64_t bytes) {
   Buffer& b = gBuffers[h];
   if (b.weights || b.host == nullptr || bytes <= 0) return;
-  upload_gaps(h, offset, bytes);
+  if (!b.tracked) {
+    upload_gaps(h, offset, bytes);
+    return;
+  }
+  const int64_t last = (offset + bytes - 1) / gPage;
+  for (int64_t p = offset / gPage; p <= last;) {
+    if (page_clean(h, p)) {
+      p++;
+      continue;
+    }
+    int64_t q = p + 1;
+    while (q <= last && !page_clean(h, q)) q++;
+    make_clean(h, p, q);
+    const int64_t end = std::min(q * gPage, b.size);
+    upload_gaps(h, p * gPage, end - p * gPage);
+    p = q;
+  }
 }
 
 // First use of h as weights: its host content goes to HBM once (except what
@@ -178,7 +334,13 @@ void read_region(int64_t h, int64_t offset, int64_t bytes) {
 void use_as_weights(int64_t h) {
   Buffer& b = gBuffers[h];
   if (b.weights) return;
-  if (b.host != nullptr) upload_gaps(h, 0, b.size);
+  if (b.host != nullptr) {
+    if (b.tracked) {
+      read_region(h, 0, b.size);
+    } else {
+      upload_gaps(h, 0, b.size);
+    }
+  }
   b.weights = true;
 }
 
@@ -561,6 +723,17 @@ int64_t lab_gpu_init(void) {
   }
   const char* mode = getenv("DIANOIA_GPU_INT8_INPUTS");
   if (mode != nullptr && strcmp(mode, "0") == 0) gInt8Inputs = false;
+  const long page = sysconf(_SC_PAGESIZE);
+  if (page > 0) gPage = page;
+  const char* track = getenv("DIANOIA_GPU_TRACK_WRITES");
+  if (track == nullptr || strcmp(track, "0") != 0) {
+    struct sigaction sa;
+    memset(&sa, 0, sizeof(sa));
+    sa.sa_sigaction = on_segv;
+    sa.sa_flags = SA_SIGINFO | SA_ONSTACK | SA_RESTART;
+    sigemptyset(&sa.sa_mask);
+    gTrack = sigaction(SIGSEGV, &sa, &gPrevSegv) == 0;
+  }
   gReady = true;
   return 1;
 }
@@ -568,11 +741,12 @@ int64_t lab_gpu_init(void) {
 int64_t lab_gpu_buffer(int64_t bytes) {
   const int64_t h = create(bytes, true);
   if (h < 0) return -1;
-  memset(gBuffers[h].host, 0, (size_t)bytes);
+  memset(gBuffers[h].host, 0, (size_t)(shadow_pages(bytes) * gPage));
   if (hipMemset(gBuffers[h].dev, 0, (size_t)bytes) != hipSuccess) {
     lab_gpu_release(h);
     return -1;
   }
+  track(h);  // host and HBM both zero: every page clean
   return h;
 }
 
@@ -611,9 +785,17 @@ void* lab_gpu_contents(int64_t handle) {
 
 double lab_gpu_last_ms(void) { return gLastMs; }
 
+void lab_gpu_transfer_bytes(int64_t* up, int64_t* down) {
+  if (up != nullptr) *up = gUpBytes;
+  if (down != nullptr) *down = gDownBytes;
+}
+
+int64_t lab_gpu_tracking_writes(void) { return gTrack ? 1 : 0; }
+
 void lab_gpu_release(int64_t handle) {
   if (!valid(handle)) return;
   wait_pending();
+  untrack(handle);
   Buffer& b = gBuffers[handle];
   (void)hipFree(b.dev);
   if (b.host) (void)hipHostFree(b.host);
@@ -632,6 +814,7 @@ void lab_gpu_begin(void) {
 
 int64_t lab_gpu_commit(int64_t wait) {
   if (!gReady) return 0;
+  check_handler();
   gWritten.clear();
   gProfiled = 0;
   bool ok = !gFailed;
@@ -654,12 +837,36 @@ int64_t lab_gpu_commit(int64_t wait) {
       ok = run(gCmds[i]) && ok;
     }
   }
-  // Results back to the host views.
+  // Results back to the host views, each written byte once (regions of a
+  // buffer merged where they overlap or touch). A dirty page a copy covers
+  // whole is made clean (and protected) before the copy is queued.
+  std::sort(gWritten.begin(), gWritten.end(), [](const Region& a, const Region& b) {
+    return a.handle != b.handle ? a.handle < b.handle : a.offset < b.offset;
+  });
+  std::vector<Region> merged;
   for (const Region& r : gWritten) {
+    if (r.bytes <= 0) continue;
+    if (!merged.empty() && merged.back().handle == r.handle &&
+        r.offset <= merged.back().offset + merged.back().bytes) {
+      Region& m = merged.back();
+      m.bytes = std::max(m.offset + m.bytes, r.offset + r.bytes) - m.offset;
+    } else {
+      merged.push_back(r);
+    }
+  }
+  for (const Region& r : merged) {
     Buffer& b = gBuffers[r.handle];
     if (b.host != nullptr && r.bytes > 0) {
+      if (b.tracked) {
+        const int64_t end = r.offset + r.bytes;
+        const int64_t p1 = end == b.size ? shadow_pages(b.size) : end / gPage;
+        for (int64_t p = (r.offset + gPage - 1) / gPage; p < p1; p++) {
+          if (!page_clean(r.handle, p)) make_clean(r.handle, p, p + 1);
+        }
+      }
       (void)hipMemcpyAsync((char*)b.host + r.offset, dev_at(r.handle, r.offset), (size_t)r.bytes,
                            hipMemcpyDeviceToHost, gStream);
+      gDownBytes += r.bytes;
     }
   }
   if (hipEventRecord(gStop, gStream) != hipSuccess) ok = false;

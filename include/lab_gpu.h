@@ -10,10 +10,13 @@
 // recorded dispatch sees every earlier one's writes. On this discrete GPU a
 // buffer is a device allocation plus a pinned host shadow: commit uploads the
 // host regions a dispatch reads (unless an earlier dispatch of the same
-// command buffer wrote them), uploads a weight buffer once on its first use
-// as weights (weights are immutable, as in GpuLinear.upload,
+// command buffer wrote them; with host-write tracking, only their pages the
+// host wrote since HBM last matched them), uploads a weight buffer once on
+// its first use as weights (weights are immutable, as in GpuLinear.upload,
 // gpu.dart:1295-1323), and copies every region a dispatch wrote back to the
-// host before the commit completes.
+// host before the commit completes. Tracking write-protects clean host pages
+// and installs a SIGSEGV handler at lab_gpu_init that chains to the one
+// installed before it.
 //
 // Not re-entrant: one thread drives the GPU layer at a time (gpu.dart:
 // 1277-1278).
@@ -64,6 +67,18 @@ void lab_gpu_begin(void);
 int64_t lab_gpu_commit(int64_t wait);
 int64_t lab_gpu_wait(void);
 double lab_gpu_last_ms(void);
+
+// Host-write tracking of the host views. No counterpart in the reference,
+// whose host-visible memory needs no copies: the bytes this library has
+// copied host -> HBM (commit uploads and first weight uploads) and HBM ->
+// host (copy-backs) since lab_gpu_init, for callers that measure the PCIe
+// cost of a command buffer (a decode step). lab_gpu_tracking_writes is 1
+// while page-granular tracking is on (a commit then uploads only the pages
+// the host wrote since HBM last matched them), 0 when it is off
+// (DIANOIA_GPU_TRACK_WRITES=0, or another SIGSEGV handler replaced this
+// library's; every read region is then uploaded).
+void lab_gpu_transfer_bytes(int64_t* up, int64_t* down);
+int64_t lab_gpu_tracking_writes(void);
 
 // lab_gpu_enc_matmul_q8 / _q4 (lab_vulkan.c:877-890; gpu.dart:125-177):
 // Y[n][rows] = X[n][cols] W^T, W inside buffer w at qsOffset / scalesOffset
