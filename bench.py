@@ -31,6 +31,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -633,6 +634,71 @@ def bench_cache_wrap(reps=3):
             "reps": reps}
 
 
+def bench_decode_step(steps=20, position=4095, child=False):
+    """One decode step of a Qwen3-1.7B-shaped decoder (28 layers, random Q4
+    body, Q8 LM head) through the lab_gpu_* ABI, encoded as GpuForward.forward
+    does (dianoia_amd/forward.py, gpu.dart:1036-1239): host wall-clock per
+    token (ctypes encoding + commit + wait), the command buffer's GPU time
+    (lab_gpu_last_ms), and the PCIe bytes per token. The KV history is
+    `position` rows of 8 KV heads x 128 (fp32, as the reference keeps it).
+    With host-write tracking (the default) a step uploads the token's
+    embedding and RoPE row; the same step with DIANOIA_GPU_TRACK_WRITES=0 (a
+    child process: the switch is read at lab_gpu_init) uploads every region
+    it reads, including the whole KV history."""
+    from dianoia_amd import forward as F
+    cfg = F.qwen3_1_7b()
+    fwd = F.GpuForward(cfg, max_seq=position + 1, max_chunk=1, seed=11)
+    rng = np.random.default_rng(12)
+    try:
+        emb = (rng.standard_normal(cfg.hidden) * 0.5).astype(np.float32)
+        for _ in range(3):
+            fwd.residual[:cfg.hidden] = emb
+            fwd.forward(1, position)
+        wall, gpu, ups, downs = [], [], [], []
+        for _ in range(steps):
+            u0, d0 = F.transfer_bytes()
+            t0 = time.perf_counter()
+            fwd.residual[:cfg.hidden] = emb
+            fwd.forward(1, position)
+            wall.append(time.perf_counter() - t0)
+            gpu.append(fwd.last_ms())
+            u1, d1 = F.transfer_bytes()
+            ups.append(u1 - u0)
+            downs.append(d1 - d0)
+        token = int(np.argmax(fwd.logits))
+    finally:
+        fwd.dispose()
+    weights = sum(b for b in (
+        cfg.layers * (q4_bytes(cfg.heads * cfg.head_dim, cfg.hidden)
+                      + 2 * q4_bytes(cfg.kv_dim, cfg.hidden)
+                      + q4_bytes(cfg.hidden, cfg.heads * cfg.head_dim)
+                      + 2 * q4_bytes(cfg.intermediate, cfg.hidden)
+                      + q4_bytes(cfg.hidden, cfg.intermediate)),
+        q8_bytes(cfg.vocab, cfg.hidden)))
+    kv = cfg.layers * 2 * (position + 1) * cfg.kv_dim * 4
+    out = {"model": "Qwen3-1.7B-shaped: 28 layers, hidden 2048, SwiGLU 6144, 16/8 heads of 128, "
+                    "vocab 151936; random Q4 body, Q8 LM head",
+           "position": position, "steps": steps,
+           "tracking_writes": F.tracking_writes(),
+           "wall_ms": float(np.median(wall)) * 1e3, "gpu_ms": float(np.median(gpu)),
+           "up_bytes_per_token": int(np.median(ups)), "down_bytes_per_token": int(np.median(downs)),
+           "weight_bytes": int(weights), "kv_bytes_read": int(kv),
+           "gpu_gbps": (weights + kv) / float(np.median(gpu)) / 1e6, "token": token}
+    if child:
+        return out
+    env = dict(os.environ, DIANOIA_GPU_TRACK_WRITES="0")
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--decode-child"], env=env,
+                       capture_output=True, text=True, timeout=600)
+    if r.returncode == 0:
+        off = json.loads(r.stdout.strip().splitlines()[-1])
+        out["tracking_off"] = {k: off[k] for k in ("tracking_writes", "wall_ms", "gpu_ms",
+                                                   "up_bytes_per_token", "down_bytes_per_token",
+                                                   "token")}
+    else:
+        out["tracking_off"] = {"error": r.stderr[-500:]}
+    return out
+
+
 # ------------------------------------------------------------------ CPU
 
 def cpu_baseline(runs):
@@ -924,6 +990,7 @@ def main():
                     help="HBM traffic per launch from two rocprofv3 counter_collection.csv files")
     ap.add_argument("--issue-bound", action="store_true",
                     help="the prefill GEMM step's issue-bound microbenchmark (JSON table)")
+    ap.add_argument("--decode-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--mfma-summary", metavar="COUNTER_CSV",
                     help="matrix-core use per launch from a rocprofv3 counter_collection.csv "
                          "of the MFMA counters")
@@ -952,6 +1019,9 @@ def main():
     if args.issue_bound:
         print(json.dumps(issue_bound(), indent=1))
         return
+    if args.decode_child:
+        print(json.dumps(bench_decode_step(child=True)), flush=True)
+        return
     timer = Timer(torch)
     check_graph_replay(torch, D, synth)
     print(f"bench: config 2 (steps={args.steps}, warmup={args.warmup})", file=sys.stderr, flush=True)
@@ -970,6 +1040,7 @@ def main():
         for name, fn in (("other_callers", lambda: bench_callers(torch, D, synth, timer, args.steps)),
                          ("load_time_converters", lambda: bench_loaders(torch, D, timer, args.steps)),
                          ("layer_steps", lambda: bench_layers(torch, D, timer, args.steps)),
+                         ("decode_step_abi", bench_decode_step),
                          ("weight_cache_wrap", bench_cache_wrap)):
             if only is not None and name not in only:
                 continue

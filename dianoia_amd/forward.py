@@ -260,11 +260,14 @@ class GpuForward:
         (int8 in [-127, 127], fp32 scales |N(0,1)| * 0.01) matrix, wrapped."""
         blocks = cols // 32
         if q4:
-            qs = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
-            sc = (np.abs(rng.standard_normal(rows * blocks)) * 0.02).astype(np.float16).view(np.uint8)
+            qs = np.frombuffer(rng.bytes(rows * cols // 2), np.uint8)
+            sc = (np.abs(rng.standard_normal(rows * blocks, np.float32)) * 0.02).astype(np.float16)
         else:
-            qs = rng.integers(-127, 128, rows * cols, dtype=np.int8).view(np.uint8)
-            sc = (np.abs(rng.standard_normal(rows * blocks)) * 0.01).astype(np.float32).view(np.uint8)
+            # Uniform bytes with -128 moved to -127 (Q8 values lie in [-127, 127]).
+            qs = np.frombuffer(rng.bytes(rows * cols), np.uint8).copy()
+            qs[qs == 0x80] = 0x81
+            sc = np.abs(rng.standard_normal(rows * blocks, np.float32)) * np.float32(0.01)
+        sc = sc.view(np.uint8)
         scales_at = (len(qs) + 63) // 64 * 64
         host = np.zeros(scales_at + len(sc), np.uint8)
         host[:len(qs)] = qs
