@@ -420,15 +420,27 @@ def bench_c4(torch, D, synth, timer, steps, warmup):
         D.quantize_q8(h, xq, xs, M, 4320, 4320)
         D.gemm_q8(q2, s2, xq, xs, y, 1152, 4320, M)
 
+    # The same pair with float inputs (mode 0, the vision encoder's CPU
+    # products, vision_encoder.dart:252-271): the bf16-MFMA float GEMM.
+    def fc1f_(i):
+        D.gemm_q8_float(q1, s1, xd, h, 4320, 1152, M)
+
+    def fc2f_(i):
+        D.gemm_q8_float(q2, s2, h, y, 1152, 4320, M)
+
     n = max(10, steps // 4)
     quant_w(0)
-    means = timer.kernel_means([quant_w, fc1_, gelu_, fc2_], n)
+    means = timer.kernel_means([quant_w, fc1_, gelu_, fc2_, fc1f_, fc2f_], n)
     qbytes = (4304 * 1152 * 2 + 4320 * 1152 + 4320 * 36 * 4) + (1152 * 4304 * 2 + 1152 * 4320 + 1152 * 135 * 4)
     ops = 2 * M * 4304 * 1152
     return {"quantize_weights_ms": means[0], "quantize_weights_gbps": qbytes / means[0] / 1e6,
             "fc1_ms": means[1], "fc1_tops": ops / means[1] / 1e9, "gelu_ms": means[2],
             "fc2_ms": means[3], "fc2_tops": ops / means[3] / 1e9,
-            "pair_tops": 2 * ops / (means[1] + means[2] + means[3]) / 1e9}
+            "pair_tops": 2 * ops / (means[1] + means[2] + means[3]) / 1e9,
+            "float_inputs": {"fc1_ms": means[4], "fc1_tops": ops / means[4] / 1e9,
+                             "fc2_ms": means[5], "fc2_tops": ops / means[5] / 1e9,
+                             "kernel": "gemm_float_kernel (x in three exact bf16 pieces, "
+                                       "bf16 MFMA, fma with the row scale)"}}
 
 
 def bench_callers(torch, D, synth, timer, steps):

@@ -89,6 +89,8 @@ SIGNATURES = {
     "dnx_gemv_q8h_argmax": ([_p, _p, _p, _p, _i64, _i64, _p, _p, _p], _i32),
     "dnx_gate_up_q8h": ([_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_q8": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dnx_gemm_q8_float": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dnx_gemm_q4_float": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_q4": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_panel_bytes": ([_i64, _i64], _i64),
     "dnx_pack_panel": ([_p, _p, _p, _i64, _i64, _p], _i32),

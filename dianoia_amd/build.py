@@ -21,8 +21,8 @@ LIB = os.path.join(HERE, "libdianoia_amd.so")
 # library (bench.py --issue-bound loads it).
 UBENCH_SRC = "ubench_tile.hip"
 UBENCH_LIB = os.path.join(HERE, "libdnx_ubench.so")
-SOURCES = ["kernels.hip", "gemv.hip", "gemm.hip", "gemm_f16.hip", "gemm_f6.hip", "layers.hip",
-           "matmul.hip", "lab_gpu.hip"]
+SOURCES = ["kernels.hip", "gemv.hip", "gemm.hip", "gemm_f16.hip", "gemm_f6.hip", "gemm_float.hip",
+           "layers.hip", "matmul.hip", "lab_gpu.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -40,7 +40,7 @@ FLAGS = [
 # scale epilogue reads every result with VALU instructions, which cannot
 # take accumulation registers (one v_accvgpr_read per value otherwise).
 SOURCE_FLAGS = {src: ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
-                for src in ("gemm.hip", "gemm_f16.hip", "gemm_f6.hip", UBENCH_SRC)}
+                for src in ("gemm.hip", "gemm_f16.hip", "gemm_f6.hip", "gemm_float.hip", UBENCH_SRC)}
 
 
 def _compile(src: str, build_dir: str) -> str:

@@ -413,6 +413,7 @@ bool run_matmul(const Cmd& c, bool q4) {
       [q4](dnx::MatmulStep step) {
         switch (step) {
           case dnx::MatmulStep::kGemvFloat: after_dispatch(q4 ? kKindGemvQ4 : kKindGemvQ8); break;
+          case dnx::MatmulStep::kGemmFloat: after_dispatch(q4 ? kKindGemmQ4 : kKindGemmQ8); break;
           case dnx::MatmulStep::kGemv: after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8); break;
           case dnx::MatmulStep::kQuantize:
           case dnx::MatmulStep::kQuantizeF6: after_dispatch(kKindQuantize); break;

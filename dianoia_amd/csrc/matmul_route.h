@@ -14,7 +14,7 @@
 namespace dnx {
 
 // Kernel launches of a route, reported to the caller's hook after each one.
-enum class MatmulStep { kGemvFloat, kGemv, kQuantize, kGemm, kQuantizeF6, kGemmF6 };
+enum class MatmulStep { kGemvFloat, kGemmFloat, kGemv, kQuantize, kGemm, kQuantizeF6, kGemmF6 };
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
@@ -39,7 +39,8 @@ inline int64_t matmul_workspace_bytes(int64_t cols, int64_t n) {
 // int8_inputs (mode 1, lab_native.c:553-579, :1059-1080): n <= 4 runs the
 // exact GEMV (its prologue quantizes x); wider n, or an x too wide for the
 // GEMV's LDS, quantizes x into the workspace and runs a GEMM. Float inputs
-// (mode 0): the exact float-input GEMV, up to 4 tokens per weight pass.
+// (mode 0): n <= 4 the exact float-input GEMV; wider n, or an x too wide for
+// the GEMV's LDS, the bf16-MFMA float GEMM (fp32 rounding of the CPU's).
 // after(step) follows every successful launch. Returns the first error.
 template <class After>
 int matmul_route(bool q4, const void* qs, const void* scales, const float* x, float* y,
@@ -48,9 +49,16 @@ int matmul_route(bool q4, const void* qs, const void* scales, const float* x, fl
   auto s = (dnx_stream_t)stream;
   int rc;
   if (!int8_inputs) {
-    rc = q4 ? dnx_gemv_q4_float((const uint8_t*)qs, (const uint16_t*)scales, x, y, rows, cols, n, s)
-            : dnx_gemv_q8_float((const int8_t*)qs, (const float*)scales, x, y, rows, cols, n, s);
-    if (rc == DNX_OK) after(MatmulStep::kGemvFloat);
+    if (n <= 4) {
+      rc = q4 ? dnx_gemv_q4_float((const uint8_t*)qs, (const uint16_t*)scales, x, y, rows, cols,
+                                  n, s)
+              : dnx_gemv_q8_float((const int8_t*)qs, (const float*)scales, x, y, rows, cols, n, s);
+      if (rc == DNX_OK) after(MatmulStep::kGemvFloat);
+      if (rc != DNX_EINVAL) return rc;  // EINVAL: x too wide for the GEMV, nothing launched
+    }
+    rc = q4 ? dnx_gemm_q4_float((const uint8_t*)qs, (const uint16_t*)scales, x, y, rows, cols, n, s)
+            : dnx_gemm_q8_float((const int8_t*)qs, (const float*)scales, x, y, rows, cols, n, s);
+    if (rc == DNX_OK) after(MatmulStep::kGemmFloat);
     return rc;
   }
   if (n <= 4) {

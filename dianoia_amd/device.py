@@ -150,6 +150,17 @@ def gate_up_q8h(gq, gs, uq, us, x, h, rows: int, cols: int, n: int = 1, u=None,
                                        _ptr(u), rows, cols, n, _stream(stream)), "dnx_gate_up_q8h")
 
 
+def gemm_q8_float(qs, scales, x, y, rows: int, cols: int, n: int, stream=None) -> None:
+    """Float-input (mode 0) GEMM on bf16 MFMA, within fp32 rounding of the CPU."""
+    _check(_lib.load().dnx_gemm_q8_float(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
+                                         _stream(stream)), "dnx_gemm_q8_float")
+
+
+def gemm_q4_float(qs, scales, x, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _check(_lib.load().dnx_gemm_q4_float(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
+                                         _stream(stream)), "dnx_gemm_q4_float")
+
+
 def gemm_q8(qs, scales, xq, xsc, y, rows: int, cols: int, n: int, stream=None) -> None:
     _check(_lib.load().dnx_gemm_q8(_ptr(qs), _ptr(scales), _ptr(xq), _ptr(xsc), _ptr(y), rows,
                                    cols, n, _stream(stream)), "dnx_gemm_q8")

@@ -121,6 +121,21 @@ int dnx_gate_up_q8h(const int8_t* gate_qs, const uint16_t* gate_scales, const in
                     const uint16_t* up_scales, const float* x, float* h, float* u, int64_t rows,
                     int64_t cols, int64_t n, dnx_stream_t stream);
 
+// Float-input GEMM (lab_gemm_q8 / lab_gemm_q4 mode 0 for many tokens,
+// lab_native.c:489-501, :1013-1023; the reference's float GPU GEMMs,
+// lab_metal.m:79-144, :174-258) on bf16 MFMA: x (fp32 [n][cols]) split
+// exactly into three bf16 pieces, weights exact in bf16, so every product
+// is exact and only the fp32 summation order differs from the CPU's (within
+// 1e-4 relative, not bit-identical; the same inputs always give the same
+// bits). Any n and cols % 32 == 0; qs 16-byte aligned. When the tiles alone
+// would leave CUs idle, K is split and a second kernel sums the partials in
+// a fixed order, in a workspace the library owns (grown on the first call
+// at a larger shape: not the first call inside a graph capture).
+int dnx_gemm_q8_float(const int8_t* qs, const float* scales, const float* x, float* y,
+                      int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
+int dnx_gemm_q4_float(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
+                      int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
+
 // Prefill / encoder GEMM on int8 MFMA, any n, inputs already quantized
 // (xq int8 [n][cols], xsc fp32 [n][cols/32], e.g. by dnx_quantize_q8):
 // the per-32-block int32 dots are exact, the per-block scaling is fp32

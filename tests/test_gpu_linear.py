@@ -269,7 +269,8 @@ def cpu_mode0(orc, fmt, qs, sc, xs, n):
                                              ("q8", 36, 64, 9), ("q8", 128, 128, 40)])
 def test_float_inputs_match_the_cpu_kernels(float_inputs, gpu, orc, fmt, rows, cols, n):
     """The reference test as written: GPU vs CPU with float inputs, within
-    1e-4 + 1e-5 |cpu| (gpu_linear_test.dart:44); here also bit-exact."""
+    1e-4 + 1e-5 |cpu| (gpu_linear_test.dart:44); for n <= 4 (the exact
+    float-input GEMV) also bit-exact."""
     rng = np.random.default_rng(5)
     m, qs, sc = quantized(orc, fmt, values(rng, rows * cols), rows, cols)
     gpu.upload("m", m)
@@ -278,7 +279,8 @@ def test_float_inputs_match_the_cpu_kernels(float_inputs, gpu, orc, fmt, rows, c
     gpu.apply("m", xs, on_gpu, n)
     cpu = cpu_mode0(orc, fmt, qs, sc, xs, n).reshape(-1)
     assert np.all(np.abs(on_gpu - cpu) <= 1e-4 + 1e-5 * np.abs(cpu))
-    assert np.array_equal(bits(on_gpu), bits(cpu))
+    if n <= 4:
+        assert np.array_equal(bits(on_gpu), bits(cpu))
 
 
 def test_float_inputs_grow_buffers_and_keep_matrices(float_inputs, gpu, orc):
@@ -293,7 +295,11 @@ def test_float_inputs_grow_buffers_and_keep_matrices(float_inputs, gpu, orc):
         xs = values(rng, n * cols)
         on_gpu = np.zeros(n * rows, np.float32)
         gpu.apply(name, xs, on_gpu, n)
-        assert np.array_equal(bits(on_gpu), bits(cpu_mode0(orc, "q4", q, s, xs, n).reshape(-1)))
+        want = cpu_mode0(orc, "q4", q, s, xs, n).reshape(-1)
+        if n <= 4:
+            assert np.array_equal(bits(on_gpu), bits(want))
+        else:  # the float GEMM: the reference GPU test's bar
+            assert np.all(np.abs(on_gpu - want) <= 1e-4 + 1e-5 * np.abs(want))
 
 
 def test_float_inputs_mlp_and_lm_head(float_inputs, gpu, orc):
