@@ -781,6 +781,14 @@ PMC_KERNELS = {  # kernel-name fragment -> (workload, algorithmic bytes per laun
     "gemm_f16_kernel<true, 3>": (
         "c3 Q4 panel GEMM M=512, 6144x2048", q4_bytes(6144, 2048) + 512 * 2048 + 512 * 64 * 4
         + 512 * 6144 * 4),
+    # The fp6 GEMM reads the prepacked weights (32 B per block) and the fp6
+    # activation panel (2176 B per 32 tokens and block).
+    "gemm_f6p_kernel<3>": (
+        "c3 Q4 fp6 GEMM (prepacked) M=512, 6144x2048", 6144 * 64 * 32 + 16 * 64 * 2176
+        + 512 * 6144 * 4),
+    "gemm_float_kernel<false, 4>": (
+        "c4 fc1 float-input Q8 GEMM M=1024, 4320x1152", 4320 * 1152 + 4320 * 36 * 4
+        + 1024 * 1152 * 4 + 1024 * 4320 * 4),
 }
 
 
@@ -837,13 +845,33 @@ def pmc_workload(torch, D, synth, reps):
     D.quantize_q8(xd, xq, xsc, M, K, K)
     panel = torch.empty((D.gemm_panel_bytes(M, K),), dtype=torch.uint8, device="cuda")
     D.quantize_q8_panel(xd, panel, M, K)
+    f6panel = torch.empty((D.f6_panel_bytes(M, K),), dtype=torch.uint8, device="cuda")
+    D.quantize_q8_f6panel(xd, f6panel, M, K)
+    packed = [torch.empty((D.q4_f6pack_bytes(N, K),), dtype=torch.uint8, device="cuda")
+              for _ in range(8)]
+    for c in range(8):
+        D.pack_q4_f6(ws[c][0], ws[c][1], packed[c], N, K)
     for i in range(reps):
         q, s = ws[i % 8]
         D.gemm_q4(q, s, xq, xsc, y, N, K, M)
         D.gemm_q4_panel(q, s, panel, y, N, K, M)
+        D.gemm_q4_f6p(packed[i % 8], f6panel, y, N, K, M)
     torch.cuda.synchronize()
-    del ws
+    del ws, packed
     print("pmc: config 3 done", file=sys.stderr, flush=True)
+
+    # Config 4's fc1 with float inputs (the bf16-MFMA float GEMM).
+    fc1, _, x4 = synth.config4()
+    w1 = dev(torch, fc1)
+    q1 = torch.zeros((4320, 1152), dtype=torch.int8, device="cuda")
+    s1 = torch.zeros((4320, 36), device="cuda")
+    D.quantize_q8_bf16(w1, q1, s1, 4304, 1152, 1152)
+    x4d = dev(torch, x4)
+    h4 = torch.empty((1024, 4320), device="cuda")
+    for i in range(reps):
+        D.gemm_q8_float(q1, s1, x4d, h4, 4320, 1152, 1024)
+    torch.cuda.synchronize()
+    print("pmc: config 4 float done", file=sys.stderr, flush=True)
 
     # Causal prefill attention, 512 tokens (the layer steps' matrix-core kernel).
     gen = torch.Generator(device="cuda").manual_seed(6)
@@ -865,6 +893,10 @@ MFMA_KERNELS = {
                                          I8_PEAK_TOPS),
     "gemm_f16_kernel<true, 3>": ("c3 Q4 GEMM M=512 (fp16 panel)", 2 * 512 * 6144 * 2048,
                                  I8_PEAK_TOPS),
+    "gemm_f6p_kernel<3>": ("c3 Q4 GEMM M=512 (fp6, prepacked)", 2 * 512 * 6144 * 2048,
+                           I8_PEAK_TOPS),
+    "gemm_float_kernel<false, 4>": ("c4 fc1 float inputs M=1024 (bf16)",
+                                    2 * 1024 * 4320 * 1152, 2500.0),
     "attention_prefill_kernel<128, 4>": ("prefill attention 512 tokens, 32/8 heads, hd 128",
                                          4 * 128 * 32 * (512 * 513 // 2), 157.3),
 }
