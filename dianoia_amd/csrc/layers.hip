@@ -79,6 +79,59 @@ rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, float*
   }
 }
 
+// The same RMSNorm with a row held in registers (V float4 per thread, rows
+// of up to 1024 V floats, 16-byte aligned operands): every load of x, w and
+// (accumulating) out is issued at the start, so the row costs one memory
+// round trip instead of a dependent walk over it. The decode step's norms
+// (one row of the hidden size) are latency, not bandwidth: 6.6 -> ~3 us.
+template <int V>
+__global__ void __launch_bounds__(kThreads)
+rms_norm_vec_kernel(const float* __restrict__ x, const float* __restrict__ w, float* out,
+                    int cols, float eps, int accumulate) {
+  __shared__ float scratch[kWaves];
+  const int q = cols / 4;
+  const float4* xr = (const float4*)(x + (size_t)blockIdx.x * cols);
+  const float4* wr = (const float4*)w;
+  float4* yr = (float4*)(out + (size_t)blockIdx.x * cols);
+  float4 xv[V], wv[V], ov[V];
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    const int i = e * kThreads + threadIdx.x;
+    const bool ok = i < q;
+    xv[e] = ok ? xr[i] : z;
+    wv[e] = ok ? wr[i] : z;
+    ov[e] = (ok && accumulate) ? yr[i] : z;
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    sum += xv[e].x * xv[e].x;
+    sum += xv[e].y * xv[e].y;
+    sum += xv[e].z * xv[e].z;
+    sum += xv[e].w * xv[e].w;
+  }
+  sum = block_sum(sum, scratch);
+  const float r = 1.0f / sqrtf(sum / (float)cols + eps);
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    const int i = e * kThreads + threadIdx.x;
+    if (i >= q) break;
+    float4 v;
+    v.x = wv[e].x * (xv[e].x * r);
+    v.y = wv[e].y * (xv[e].y * r);
+    v.z = wv[e].z * (xv[e].z * r);
+    v.w = wv[e].w * (xv[e].w * r);
+    if (accumulate) {
+      v.x = ov[e].x + v.x;
+      v.y = ov[e].y + v.y;
+      v.z = ov[e].z + v.z;
+      v.w = ov[e].w + v.w;
+    }
+    yr[i] = v;
+  }
+}
+
 // Per (head, token), one wave (lab_metal.m:357-380): RMSNorm over head_dim
 // with weight w, then the half-split RoPE rotation pairing j with
 // j + hd / 2, from the token's tables [cos(hd / 2), sin(hd / 2)]. In place;
@@ -904,8 +957,35 @@ int dnx_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64
                  float eps, int accumulate, dnx_stream_t stream) {
   if (rows < 0 || cols <= 0 || cols > (1 << 30) || rows > 0x7fffffff) return DNX_EINVAL;
   if (rows == 0) return DNX_OK;
-  hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)rows), dim3(kThreads), 0,
-                     (hipStream_t)stream, x, w, out, (int)cols, eps, accumulate);
+  // Register rows for the latency-bound case (no more rows than CUs, as in a
+  // decode step); at prefill sizes the streaming loop keeps more rows in
+  // flight (4096 x 2048: 14 against 21 us).
+  const bool vec = rows <= 256 && cols % 4 == 0 && cols <= 16 * 4 * kThreads &&
+                   (((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 15) == 0;
+  const unsigned grid = (unsigned)rows;
+  const hipStream_t s = (hipStream_t)stream;
+  if (vec) {
+    const int64_t per = (cols / 4 + kThreads - 1) / kThreads;  // float4 per thread
+    if (per <= 1) {
+      hipLaunchKernelGGL(rms_norm_vec_kernel<1>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
+                         (int)cols, eps, accumulate);
+    } else if (per <= 2) {
+      hipLaunchKernelGGL(rms_norm_vec_kernel<2>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
+                         (int)cols, eps, accumulate);
+    } else if (per <= 4) {
+      hipLaunchKernelGGL(rms_norm_vec_kernel<4>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
+                         (int)cols, eps, accumulate);
+    } else if (per <= 8) {
+      hipLaunchKernelGGL(rms_norm_vec_kernel<8>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
+                         (int)cols, eps, accumulate);
+    } else {
+      hipLaunchKernelGGL(rms_norm_vec_kernel<16>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
+                         (int)cols, eps, accumulate);
+    }
+  } else {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(grid), dim3(kThreads), 0, s, x, w, out, (int)cols,
+                       eps, accumulate);
+  }
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 

@@ -28,7 +28,9 @@ def close(gpu, cpu, rtol=RTOL, atol=ATOL):
 
 
 @pytest.mark.parametrize("rows,cols,acc", [(1, 2048, False), (7, 1024, True), (128, 4096, False),
-                                           (3, 37, True)])
+                                           (3, 37, True), (2, 16384, True), (5, 6144, False),
+                                           (1, 2052, True), (1, 20000, False), (512, 2048, True),
+                                           (256, 2048, True)])
 def test_rms_norm(gpu_ready, orc, rows, cols, acc):
     rng = np.random.default_rng(rows + cols)
     x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
