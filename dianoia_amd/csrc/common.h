@@ -15,6 +15,7 @@ constexpr int kQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
 constexpr int kQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
 constexpr int kHalfRowMirror = 0x141; // lane i <- lane 7-i within 8 lanes
 constexpr int kRowMirror = 0x140;     // lane i <- lane 15-i within 16 lanes
+constexpr int kRowShl4 = 0x104;       // lane i <- lane i+4 within 16 lanes (0 past the row)
 
 template <int Ctrl>
 DNX_DEV int dpp(int v) {
@@ -37,6 +38,25 @@ DNX_DEV float group8_max(float m) {
   return m;
 }
 
+// group8_max for values >= 0 (or +inf, never NaN): their bit patterns order
+// as integers, so integer max moves through DPP without the float max's
+// NaN canonicalization.
+DNX_DEV float group8_max_nonneg(float m) {
+  int b = __float_as_int(m);
+  b = max(b, dpp<kQuadXor1>(b));
+  b = max(b, dpp<kQuadXor2>(b));
+  b = max(b, dpp<kHalfRowMirror>(b));
+  return __int_as_float(b);
+}
+
+// Lane j's value of each aligned 8-lane group, to every lane of the group
+// (ds_swizzle bit mode within 32 lanes: source = (lane & 0x18) | j). Every
+// lane of the group must be active.
+template <int J>
+DNX_DEV float bcast8(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x18 | (J << 5)));
+}
+
 // Min over the 8 lanes of an aligned lane group; every lane gets it.
 DNX_DEV int group8_min(int m) {
   m = min(m, dpp<kQuadXor1>(m));
@@ -56,11 +76,18 @@ DNX_DEV int cvt_trunc_x86(float t) {
 // One value of lab_quantize_q8 (lab_native.c:422-425): q = x * inv, then
 // +-0.5 in float, truncation, clamp to [-127, 127]. Two roundings: the file
 // is compiled with -ffp-contract=off.
+//
+// Written for few instructions: t + copysign(0.5, t) is t - 0.5 below zero
+// and t + 0.5 above (at -0 it gives -0.5 instead of 0.5, which truncates to
+// the same 0); clamping to [-127, 127] before the truncation equals clamping
+// after it; x86's INT_MIN for NaN and t >= 2^31 becomes -127 through the
+// clamp, and below -2^31 the clamp gives -127 already. The two forms agree
+// for every float t (checked exhaustively over all 2^32 bit patterns).
 DNX_DEV int quant1(float x, float inv) {
   float t = x * inv;
-  t = t < 0.0f ? t - 0.5f : t + 0.5f;
-  const int v = cvt_trunc_x86(t);
-  return v > 127 ? 127 : v < -127 ? -127 : v;
+  t = t + __builtin_copysignf(0.5f, t);
+  const int v = (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
+  return t < 2147483648.0f ? v : -127;
 }
 
 // One value of lab_quantize_q4 (lab_native.c:949-950): (int8_t)(x * id +
@@ -79,8 +106,12 @@ DNX_DEV float q8_inv(float scale) { return scale > 0.0f ? 1.0f / scale : 0.0f; }
 
 // Four values quantized with one block's inv, packed little-endian.
 DNX_DEV int quant4(float4 v, float inv) {
-  return (quant1(v.x, inv) & 0xff) | ((quant1(v.y, inv) & 0xff) << 8) |
-         ((quant1(v.z, inv) & 0xff) << 16) | ((quant1(v.w, inv) & 0xff) << 24);
+  // Low bytes of the four values: (x, y) and (z, w) pairs, then the pairs.
+  const uint32_t xy = __builtin_amdgcn_perm((uint32_t)quant1(v.y, inv),
+                                            (uint32_t)quant1(v.x, inv), 0x0c0c0400u);
+  const uint32_t zw = __builtin_amdgcn_perm((uint32_t)quant1(v.w, inv),
+                                            (uint32_t)quant1(v.z, inv), 0x0c0c0400u);
+  return (int)__builtin_amdgcn_perm(zw, xy, 0x05040100u);
 }
 
 // max |v| of four values. The reference keeps amax with `a > amax` from 0
@@ -91,6 +122,7 @@ DNX_DEV float max4abs(float4 v) {
 }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte load marked non-temporal: weights are streamed once, so they
 // should not displace the inputs other workgroups still reuse.

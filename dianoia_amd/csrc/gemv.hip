@@ -54,6 +54,16 @@ constexpr int kFmtQ8 = 0, kFmtQ4 = 1, kFmtQ8H = 2;
 // the token. The kernel boundary orders the atomics before those reads, so
 // no fence, no arrival count and no atomic retry is needed.
 constexpr int kArgmaxSlots = 256;
+// Buffer offset of a request that must read zeros: past every matrix range
+// (a launch covers less than 2 GB of codes).
+constexpr uint32_t kDead = 0x80000000u;
+constexpr int64_t kMaxLaunchBytes = ((int64_t)1 << 31) - 4096;
+// Blocks per step of the FMA chains (two steps alternate, so a chain runs
+// over a multiple of two steps; tiles of one or two rows take steps of
+// 2 kChainStep, with registers to spare); each chain row carries kChainPad
+// floats past its blocks (keeps the rows 16-byte aligned).
+constexpr int kChainStep = 8;
+constexpr int kChainPad = 4;
 
 DNX_DEV uint64_t argmax_rank(float v, uint32_t row) {
   // A NaN at index 0 is the answer whatever follows (every comparison with
@@ -65,9 +75,11 @@ struct GemvParams {
   const void* qs[2];
   const void* scales[2];
   const float* x;              // [n][cols] fp32
-  float* y;                    // [n][rows]; the pair writes SiLU(gate) * up
+  float* y;                    // [n][ldy]; the pair writes SiLU(gate) * up
   float* y2;                   // pair: the up products too, when not null
-  int rows, cols, n;
+  int rows, cols, n;           // rows of this launch (qs, scales, y start at its first)
+  int ldy;                     // row stride of y and y2 (the matrix's rows)
+  int row0;                    // the launch's first row in the matrix (argmax ranks)
   int tiles;                   // ceil(rows / R)
   int full;                    // 1: a tile's whole K goes to LDS before its chains run
   int stride;                  // LDS floats per chain: span of blocks + 4
@@ -91,8 +103,8 @@ DNX_DEV float silu_mul(float g, float u) {
   return s * u;
 }
 
-template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF>
-__global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
+template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, int W>
+__global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
   // kF: float inputs (lab_gemm_q8 / lab_gemm_q4 mode 0): x is not quantized;
   // per block, lane l sums fma(float(w_j), x_j, s) over j = 4k + l, k = 0..7
   // in order (dot_q8_f32 lab_native.c:489-501, dot_q4_f32 :1013-1023), and
@@ -110,6 +122,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
   // time from a ring of 16 (measured faster for each).
   constexpr int Q = RR * G;                   // ring slots (row-chunks in flight)
   constexpr bool kFine = G == 1;
+  constexpr int CS = RR <= 2 ? 2 * kChainStep : kChainStep;  // blocks per chain step
+  constexpr int T = 64 * W;                   // threads of the workgroup (W waves)
 
   extern __shared__ __align__(16) unsigned char lds[];
   const int cols = p.cols, B = cols / kBlock, n = p.n;
@@ -123,17 +137,27 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
   float* sxs = (float*)(lds + NT * cols);                  // [NT][B]
   int* sxsum = (int*)(sxs + ((NT * B + 3) & ~3));          // Q4: [NT][B][4]
   float* sxf = (float*)lds;
-  const int CP = p.stride;  // floats per chain: a chunk (or the whole K) + 4
+  const int CP = p.stride;  // floats per chain: a chunk (or the whole K) + kChainPad
   float* sf = (kF ? sxf + NT * cols : (float*)(sxsum + (kQ4 ? NT * B * 4 : 0))) +
               wave * (NT * RR * 5 * CP);
   float* ss = sf + NT * RR * 4 * CP;                       // [NT][RR][CP]
 
   const int chunks = (B + CB - 1) / CB;
-  const int stride = gridDim.x * kWaves;
-  const int tile0 = blockIdx.x * kWaves + wave;
+  const int stride = gridDim.x * W;
+  const int tile0 = blockIdx.x * W + wave;
   const int my_tiles = tile0 < p.tiles ? (p.tiles - 1 - tile0) / stride + 1 : 0;
   const int groups = my_tiles * chunks;                    // chunk groups of this wave
   const int lblk = kQ4 ? lane : (lane >> 1);               // lane's block in a chunk
+
+  // Code and scale bytes per row, and one resource per matrix.
+  const uint32_t qrow = kQ4 ? (uint32_t)cols / 2 : (uint32_t)cols;
+  const uint32_t srow = (uint32_t)B * (kHalf ? 2 : 4);
+  i32x4 rq[M], rs[M];
+#pragma unroll
+  for (int m = 0; m < M; m++) {
+    rq[m] = buffer_rsrc(p.qs[m], (uint32_t)p.rows * qrow);
+    rs[m] = buffer_rsrc(p.scales[m], (uint32_t)p.rows * srow);
+  }
 
   uint4 raw[Q];
   // Raw scale bits, converted only when used: any operation on a loaded
@@ -142,38 +166,25 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
   ScaleBits swb[Q];
 
   // Requests row-chunk i of chunk c of this wave's k-th tile into ring slot
-  // s0 + i (issue: all RR of them) with buffer loads bounded by the row: blocks past
-  // the row, rows past the matrix and tiles past this wave's last read as
-  // zeros without a memory access (their results are never stored), so the
-  // issue has no branch.
+  // s0 + i. One buffer resource spans each matrix (the launch keeps a matrix
+  // under 2 GB), so a request is an offset: rows past the matrix fall outside
+  // the range and read zeros without a memory access, and so does a slot
+  // past this wave's last tile (offset kDead); lanes past a row's last block
+  // read the next row, and their results are never used. The issue has no
+  // branch.
   auto issue1 = [&](const int s0, const int k, const int c, const int i) {
     const int tile = tile0 + k * stride;
     const int blk = c * CB + lblk;
-    {
-      const int m = i / R, r = i - (i / R) * R;
-      const int row = tile * R + r;
-      const bool live = k < my_tiles && row < p.rows;
-      if (kQ4) {
-        const i32x4 rq = buffer_rsrc((const uint8_t*)p.qs[m] + (size_t)row * (cols / 2),
-                                     live ? (uint32_t)(cols / 2) : 0u);
-        const i32x4 rs = buffer_rsrc((const uint16_t*)p.scales[m] + (size_t)row * B,
-                                     live ? (uint32_t)(B * 2) : 0u);
-        raw[s0 + i] = buffer_load16_stream(rq, blk * 16);
-        swb[s0 + i] = dnx_raw_buffer_load_i16(rs, blk * 2, 0, kStream);
-      } else {
-        const i32x4 rq = buffer_rsrc((const int8_t*)p.qs[m] + (size_t)row * cols,
-                                     live ? (uint32_t)cols : 0u);
-        raw[s0 + i] = buffer_load16_stream(rq, blk * 32 + (lane & 1) * 16);
-        if (kHalf) {
-          const i32x4 rs = buffer_rsrc((const uint16_t*)p.scales[m] + (size_t)row * B,
-                                       live ? (uint32_t)(B * 2) : 0u);
-          swb[s0 + i] = dnx_raw_buffer_load_i16(rs, blk * 2, 0, kStream);
-        } else {
-          const i32x4 rs = buffer_rsrc((const float*)p.scales[m] + (size_t)row * B,
-                                       live ? (uint32_t)(B * 4) : 0u);
-          swb[s0 + i] = dnx_raw_buffer_load_i32(rs, blk * 4, 0, kStream);
-        }
-      }
+    const int m = i / R, r = i - (i / R) * R;
+    const uint32_t row = (uint32_t)(tile * R + r);
+    const bool live = k < my_tiles;
+    const uint32_t oq = row * qrow + (kQ4 ? blk * 16 : blk * 32 + (lane & 1) * 16);
+    const uint32_t os = row * srow + blk * (kHalf ? 2 : 4);
+    raw[s0 + i] = buffer_load16_stream(rq[m], (int)(live ? oq : kDead));
+    if (kHalf) {
+      swb[s0 + i] = dnx_raw_buffer_load_i16(rs[m], (int)(live ? os : kDead), 0, kStream);
+    } else {
+      swb[s0 + i] = dnx_raw_buffer_load_i32(rs[m], (int)(live ? os : kDead), 0, kStream);
     }
   };
   auto issue = [&](const int s0, const int k, const int c) {
@@ -193,59 +204,89 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
   // complete in order, so x must not queue behind the weights), then the
   // weight ring is filled, then x is quantized while the weights stream.
   // Rows of tokens t >= n are never stored, so their LDS is left as is.
-  constexpr int PQ = 8;  // x quads per thread per batch
+  // A batch is PQ = 8 quads per thread: quad q0 + j T + tid for j < 8, so for
+  // each j the 8 lanes of an aligned group hold one 32-value block.
+  constexpr int PQ = 8;
   const int quads = cols / 4;
   float4 v[PQ];
   auto load_x = [&](const int t, const int q0) {
     const i32x4 rx = buffer_rsrc(p.x + (size_t)t * cols, (uint32_t)cols * 4);
 #pragma unroll
     for (int j = 0; j < PQ; j++) {
-      const int q = q0 + j * kThreads + tid;  // past the row: zeros, unused
+      const int q = q0 + j * T + tid;  // past the row: zeros, unused
       v[j] = buffer_load_f4(rx, q * 16);
     }
   };
-  load_x(0, 0);
   int pk = 0, pc = 0;  // position of the next chunk group to request
-#pragma unroll
-  for (int g = 0; g < G; g++) {
-    issue(g * RR, pk, pc);
-    advance(pk, pc);
-  }
   auto quantize_x = [&](const int t, const int q0) {
+    if (kF) {
 #pragma unroll
-    for (int j = 0; j < PQ; j++) {
-      const int q = q0 + j * kThreads + tid;
-      if (q >= quads) break;  // whole 8-lane groups: quads is a multiple of 8
-      const int c = q * 4;
-      if (kF) {
+      for (int j = 0; j < PQ; j++) {
+        const int q = q0 + j * T + tid;
+        if (q >= quads) break;
         // quad q is k = q % 8 of block q / 8, l = 0..3
         float* d = sxf + (t * B + (q >> 3)) * 32 + (q & 7);
         d[0] = v[j].x;
         d[8] = v[j].y;
         d[16] = v[j].z;
         d[24] = v[j].w;
-        continue;
       }
-      const float amax = group8_max(fmaxf(0.0f, max4abs(v[j])));
-      const float scale = q8_scale(amax);
-      const int packed = quant4(v[j], q8_inv(scale));
+      return;
+    }
+    // Each group's 8 block maxima (one per j), then one correctly rounded
+    // scale and inverse per lane: lane 8g + k divides for j = k, and the
+    // group's lanes fetch the other seven inverses with a swizzle broadcast
+    // (every lane is active here: the loop below diverges, this does not).
+    float am[PQ];
+#pragma unroll
+    for (int j = 0; j < PQ; j++) am[j] = group8_max_nonneg(fmaxf(0.0f, max4abs(v[j])));
+    const int k = lane & 7;
+    float a = am[0];
+#pragma unroll
+    for (int j = 1; j < PQ; j++) a = k == j ? am[j] : a;
+    const float scale = q8_scale(a);
+    const float inv_k = q8_inv(scale);
+    {
+      const int q = q0 + k * T + (tid & ~7);  // first quad of lane k's block
+      if (q < quads) sxs[t * B + (q >> 3)] = scale;
+    }
+    static_assert(PQ == 8, "one division per lane of an 8-lane group");
+    const float inv[PQ] = {bcast8<0>(inv_k), bcast8<1>(inv_k), bcast8<2>(inv_k),
+                           bcast8<3>(inv_k), bcast8<4>(inv_k), bcast8<5>(inv_k),
+                           bcast8<6>(inv_k), bcast8<7>(inv_k)};
+#pragma unroll
+    for (int j = 0; j < PQ; j++) {
+      const int q = q0 + j * T + tid;
+      if (q >= quads) break;  // whole 8-lane groups: quads is a multiple of 8
+      const int c = q * 4;
+      const int packed = quant4(v[j], inv[j]);
       *(int*)(sxq + t * cols + c) = packed;
-      const int jq = q & 7;  // quad within the block
-      if (jq == 0) sxs[t * B + (q >> 3)] = scale;
       if (kQ4) {
         // -8 * (sum of the x bytes meeting lane l's low and high nibbles):
         // quads l and l + 4 of the block, so the nibbles enter sdot as 0..15.
+        const int jq = q & 7;  // quad within the block
         const int s = sdot4(packed, 0x01010101, 0);
-        const int other = __builtin_amdgcn_ds_swizzle(s, 0x101F);  // lane ^ 4
+        const int other = dpp<kRowShl4>(s);  // lane + 4: quad jq + 4 of the block
         if (jq < 4) sxsum[(t * B + (q >> 3)) * 4 + jq] = -8 * (s + other);
       }
     }
   };
+  load_x(0, 0);
+  // Slots past the wave's last tile are not requested (a uniform branch:
+  // such requests would read nothing and only cost their instructions).
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    if (pk < my_tiles) issue(g * RR, pk, pc);
+    advance(pk, pc);
+  }
   // The first batch straight after the ring is filled (no loop around it,
-  // so waiting for x does not wait for the weights behind it).
+  // so waiting for x does not wait for the weights behind it). The
+  // scheduling barrier keeps every weight request ahead of the first wait
+  // for x (the scheduler would otherwise start the block maxima in between).
+  __builtin_amdgcn_sched_barrier(0);
   quantize_x(0, 0);
   for (int t = 0; t < n; t++) {
-    for (int q0 = t == 0 ? kThreads * PQ : 0; q0 < quads; q0 += kThreads * PQ) {
+    for (int q0 = t == 0 ? T * PQ : 0; q0 < quads; q0 += T * PQ) {
       load_x(t, q0);
       quantize_x(t, q0);
     }
@@ -273,10 +314,28 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
       // up to the next multiple of 4 are read by the chains, the rest are
       // in bounds and never read. Selects, not branches: a branch here makes
       // the compiler wait for every load in flight.
-      const int nb = min(CB, B - cc * CB), nb4 = (nb + 3) & ~3;
+      const int nb = min(CB, B - cc * CB);
       const bool ok = lblk < nb;
       const int blk = cc * CB + (ok ? lblk : 0);
       const int at = p.full ? cc * CB + lblk : lblk;  // block slot in this chain's LDS
+      // The chunk's quantized x for this lane's block, read once for all the
+      // tile's rows (int8 inputs; read per row, the reads would wait behind
+      // each row's LDS writes).
+      int4 xfa[NT], xfb[NT], xfc[NT];
+      float xfs[NT];
+      if (!kF) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          if (kQ4) {
+            xfa[t] = *(const int4*)(sxq + t * cols + blk * 32);
+            xfb[t] = *(const int4*)(sxq + t * cols + blk * 32 + 16);
+            xfc[t] = *(const int4*)(sxsum + (t * B + blk) * 4);
+          } else {
+            xfa[t] = *(const int4*)(sxq + t * cols + blk * 32 + (lane & 1) * 16);
+          }
+          xfs[t] = sxs[t * B + blk];
+        }
+      }
       // Row-chunks -> lane sums and block scales in LDS.
 #pragma unroll
       for (int i = 0; i < RR; i++) {
@@ -344,15 +403,13 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
             }
             *sp = ok ? swi : 0.0f;  // both lanes of the block: the same value
           } else if (kQ4) {
-            const int4 xa = *(const int4*)(sxq + t * cols + blk * 32);
-            const int4 xb = *(const int4*)(sxq + t * cols + blk * 32 + 16);
-            const int4 c8 = *(const int4*)(sxsum + (t * B + blk) * 4);
+            const int4 xa = xfa[t], xb = xfb[t], c8 = xfc[t];
             const int mk = 0x0f0f0f0f;
             const int d0 = sdot4(w.x & mk, xa.x, sdot4((w.x >> 4) & mk, xb.x, c8.x));
             const int d1 = sdot4(w.y & mk, xa.y, sdot4((w.y >> 4) & mk, xb.y, c8.y));
             const int d2 = sdot4(w.z & mk, xa.z, sdot4((w.z >> 4) & mk, xb.z, c8.z));
             const int d3 = sdot4(w.w & mk, xa.w, sdot4((w.w >> 4) & mk, xb.w, c8.w));
-            const float sb = swi * sxs[t * B + blk];
+            const float sb = swi * xfs[t];
             f[0] = ok ? (float)d0 : 0.0f;
             f[CP] = ok ? (float)d1 : 0.0f;
             f[2 * CP] = ok ? (float)d2 : 0.0f;
@@ -360,7 +417,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
             *sp = ok ? sb : 0.0f;
           } else {
             const int h = lane & 1;
-            const int4 xv = *(const int4*)(sxq + t * cols + blk * 32 + h * 16);
+            const int4 xv = xfa[t];
             int p0 = sdot4(w.x, xv.x, 0), p1 = sdot4(w.y, xv.y, 0);
             int p2 = sdot4(w.z, xv.z, 0), p3 = sdot4(w.w, xv.w, 0);
             // Lane l's sum takes 4 bytes of each half: add the partner's.
@@ -369,34 +426,64 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
             p2 += dpp<kQuadXor1>(p2);
             p3 += dpp<kQuadXor1>(p3);
             float* fh = f + 2 * h * CP;
-            const float sb = swi * sxs[t * B + blk];
+            const float sb = swi * xfs[t];
             fh[0] = ok ? (float)(h ? p2 : p0) : 0.0f;
             fh[CP] = ok ? (float)(h ? p3 : p1) : 0.0f;
             *sp = ok ? sb : 0.0f;  // both lanes of the block: the same value
           }
         }
-        if (kFine) issue1(g * RR, pk, pc, i);  // the slot is free: refill it now
+        // The slot is free: refill it now (unconditionally: a branch here
+        // makes the compiler wait for every load in flight).
+        if (kFine) issue1(g * RR, pk, pc, i);
       }
       // Refill these ring slots with the chunk group one batch ahead.
-      if (!kFine) issue(g * RR, pk, pc);
+      if (!kFine && pk < my_tiles) issue(g * RR, pk, pc);
       advance(pk, pc);
       if (!p.full || cc == chunks - 1) {
         // The FMA chains, in block order: over this chunk, or (full-K tiles)
         // over the whole row at its last chunk.
-        const int end = p.full ? cc * CB + nb4 : nb4;
+        // Two register buffers of CS blocks alternate: one step's chain
+        // runs while the other's LDS reads are in flight. Every slot of a
+        // chunk is written (zeros past the row's last block, and
+        // fma(0, 0, acc) = acc: acc is never -0), so the chain may run on to
+        // a multiple of 2 CS. Buffer a starts as zeros rather than a read:
+        // with a read there the compiler folds both buffers' reads back into
+        // one read at the top of each step, and the latency returns.
+        const int end = (p.full ? cc * CB : 0) + ((nb + 2 * CS - 1) & ~(2 * CS - 1));
         wave_sync();
         if (lane < CH) {
           const float* fp = sf + lane * CP;
           const float* sp = ss + (lane >> 2) * CP;
-#pragma unroll 4
-          for (int b = 0; b < end; b += 4) {
-            const float4 fv = *(const float4*)(fp + b);
-            const float4 sv = *(const float4*)(sp + b);
-            acc = fmaf(fv.x, sv.x, acc);
-            acc = fmaf(fv.y, sv.y, acc);
-            acc = fmaf(fv.z, sv.z, acc);
-            acc = fmaf(fv.w, sv.w, acc);
+          float4 fa[CS / 4], sa[CS / 4], fb[CS / 4], sb[CS / 4];
+          auto read = [&](float4* f, float4* sv, const int b) {
+#pragma unroll
+            for (int i = 0; i < CS / 4; i++) {
+              f[i] = *(const float4*)(fp + b + 4 * i);
+              sv[i] = *(const float4*)(sp + b + 4 * i);
+            }
+          };
+          auto chain = [&](const float4* f, const float4* sv) {
+#pragma unroll
+            for (int i = 0; i < CS / 4; i++) {
+              acc = fmaf(f[i].x, sv[i].x, acc);
+              acc = fmaf(f[i].y, sv[i].y, acc);
+              acc = fmaf(f[i].z, sv[i].z, acc);
+              acc = fmaf(f[i].w, sv[i].w, acc);
+            }
+          };
+#pragma unroll
+          for (int i = 0; i < CS / 4; i++) {
+            fa[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            sa[i] = fa[i];
           }
+          // a: blocks [b - CS, b); b: blocks [b, b + CS).
+          for (int b = 0; b < end; b += 2 * CS) {
+            read(fb, sb, b);
+            chain(fa, sa);
+            read(fa, sa, b + CS);
+            chain(fb, sb);
+          }
+          chain(fa, sa);
         }
         wave_sync();
       }
@@ -414,14 +501,14 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
           const float up = __shfl(v, lane + R * 4);  // the up row of this gate row
           if (lead && i < R) {
             val = silu_mul(v, up);
-            dst = p.y + (size_t)t * p.rows + row;
+            dst = p.y + (size_t)t * p.ldy + row;
           } else if (lead && p.y2 != nullptr) {
-            dst = p.y2 + (size_t)t * p.rows + row;
+            dst = p.y2 + (size_t)t * p.ldy + row;
           }
         } else {
-          if (lead) dst = p.y + (size_t)t * p.rows + row;
+          if (lead) dst = p.y + (size_t)t * p.ldy + row;
           if (kArgmax) {
-            const uint64_t key = lead ? argmax_rank(v, (uint32_t)row) : 0;
+            const uint64_t key = lead ? argmax_rank(v, (uint32_t)(p.row0 + row)) : 0;
             const uint64_t m = wave_max_u64(key);
             best = m > best ? m : best;
           }
@@ -445,12 +532,12 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(GemvParams p) {
 
   if (kArgmax) {
     // The workgroup's best rank into its group word (the finisher reads it).
-    __shared__ uint64_t red[kWaves];
+    __shared__ uint64_t red[W];
     if (lane == 0) red[wave] = best;
     __syncthreads();
     if (tid == 0) {
       uint64_t b = red[0];
-      for (int w = 1; w < kWaves; w++) b = red[w] > b ? red[w] : b;
+      for (int w = 1; w < W; w++) b = red[w] > b ? red[w] : b;
       if (b != 0) {
         __hip_atomic_fetch_max(&p.ws[blockIdx.x % kArgmaxSlots], (unsigned long long)b,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -504,38 +591,56 @@ int cu_count() {
   return cus;
 }
 
-// LDS of one workgroup for a chain stride (matches the carving in gemv_kernel).
-size_t lds_for(bool q4, bool fx, int R, int nt, bool pair, int cols, int stride) {
+// LDS of one workgroup of W waves for a chain stride (matches the carving in
+// gemv_kernel).
+size_t lds_for(bool q4, bool fx, int R, int nt, bool pair, int cols, int stride, int W) {
   const int RR = R * (pair ? 2 : 1), B = cols / kBlock;
   const size_t x = fx ? (size_t)nt * cols * 4
                       : (size_t)nt * cols + 4 * (size_t)((nt * B + 3) & ~3) +
                             (q4 ? (size_t)nt * B * 16 : 0);
-  return x + (size_t)kWaves * nt * RR * 5 * stride * 4;
+  return x + (size_t)W * nt * RR * 5 * stride * 4;
 }
+
+// Matrices of at most kWideRows rows are "small" (the decode step's
+// projections); an x of at least kWideCols columns is "long".
+constexpr int kWideRows = 16384;
+constexpr int kWideCols = 4096;
+
+// LDS budgets: 4-wave workgroups share a CU with others and keep to 64 KB;
+// an 8-wave workgroup runs alone on its CU and may use the CU's 160 KB.
+constexpr size_t kLdsShared = 64 * 1024;
+constexpr size_t kLdsAlone = 160 * 1024;
+size_t lds_budget(int W) { return W >= 8 ? kLdsAlone : kLdsShared; }
 
 // Ring slots per wave (the kernel's Q) for RR rows per tile.
 int ring_units(int RR) { return RR >= 8 ? RR : RR >= 2 ? 16 : 8; }
 
-template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF>
+template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, int W>
 int launch(GemvParams& p, hipStream_t stream) {
   constexpr bool kQ4 = F == kFmtQ4;
   constexpr int CB = kQ4 ? 64 : 32, RR = R * (kPair ? 2 : 1);
   const int B = p.cols / kBlock, chunks = (B + CB - 1) / CB;
+  const size_t budget = lds_budget(W);
   // Full-K tiles when the whole tile fits the ring (small tiles, where the
   // chain per chunk would otherwise serialize with each chunk's latency).
   p.full = RR * chunks <= ring_units(RR) &&
-           lds_for(kQ4, kF, R, NT, kPair, p.cols, chunks * CB + 4) <= 64 * 1024;
-  p.stride = (p.full ? chunks * CB : CB) + 4;
-  const size_t lds = lds_for(kQ4, kF, R, NT, kPair, p.cols, p.stride);
-  if (lds > 64 * 1024) return DNX_EINVAL;  // x too wide for one workgroup's LDS
-  auto kernel = gemv_kernel<F, R, NT, kPair, kArgmax, kF>;
+           lds_for(kQ4, kF, R, NT, kPair, p.cols, chunks * CB + kChainPad, W) <= budget;
+  p.stride = (p.full ? chunks * CB : CB) + kChainPad;
+  const size_t lds = lds_for(kQ4, kF, R, NT, kPair, p.cols, p.stride, W);
+  if (lds > budget) return DNX_EINVAL;  // x too wide for one workgroup's LDS
+  auto kernel = gemv_kernel<F, R, NT, kPair, kArgmax, kF, W>;
   // Persistent grid: as many workgroups as stay resident (the occupancy is
   // looked up once per kernel and LDS size).
   static int cached_per_cu = 0;
   static size_t cached_lds = 0;
   if (cached_per_cu == 0 || cached_lds != lds) {
+    if (lds > kLdsShared &&
+        hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess) {
+      return DNX_ELAUNCH;
+    }
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64 * W, lds) !=
             hipSuccess ||
         per_cu < 1) {
       per_cu = 1;
@@ -544,51 +649,77 @@ int launch(GemvParams& p, hipStream_t stream) {
     cached_lds = lds;
   }
   p.tiles = (p.rows + R - 1) / R;
-  const int need = (p.tiles + kWaves - 1) / kWaves;
+  const int need = (p.tiles + W - 1) / W;
   int cap = cached_per_cu * cu_count();
   // A wave defers its results in one register across its 64 lanes: at most
   // 64 / (NT * RR) tiles per wave, so at least this many workgroups.
   const int per_wave = 64 / (NT * RR);
-  const int floor_grid = (p.tiles + kWaves * per_wave - 1) / (kWaves * per_wave);
+  const int floor_grid = (p.tiles + W * per_wave - 1) / (W * per_wave);
   // Small matrices (a few thousand tiles: the decode step's projections)
-  // run faster on two workgroups per CU than on every resident slot: fewer
-  // workgroups quantize x and wait at their one barrier, and the waves left
-  // keep enough loads in flight (3.4 MB Q8 GEMV: 5.2 -> 4.4 us; 14 MB Q4
-  // gate/up pair: 8.5 -> 7.6 us). The LM head keeps the full grid.
-  if (p.tiles <= 4096 && cap > 2 * cu_count()) cap = 2 * cu_count();
+  // run 8-wave workgroups, one per CU, so that each CU quantizes x once;
+  // 4-wave launches of them keep two workgroups per CU (fewer workgroups
+  // quantize x and wait at their one barrier, and the waves left keep
+  // enough loads in flight). The LM head keeps the full grid.
+  const int per_cu_small = W >= 8 ? 1 : 2;
+  if (p.tiles <= 4096 && cap > per_cu_small * cu_count()) cap = per_cu_small * cu_count();
   if (cap < floor_grid) cap = floor_grid;
   const int grid = need < cap ? need : cap;
   p.grid = grid;
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), lds, stream, p);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * W), lds, stream, p);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 
-// Rows per tile: the largest of 8 that still gives >= 2048
-// tiles (8 per CU), halving down to 1 for small matrices; bounded so a
-// tile's chains fit a wave and the workgroup's LDS stays within 64 KB.
+// Rows per tile: the largest of 8 that still gives at least kMinTiles
+// tiles, halving down to 1 for small matrices; bounded so a tile's chains
+// fit a wave and a 4-wave workgroup's LDS stays within 64 KB. Single
+// matrices with a short x take fewer, larger tiles (fewer workgroups
+// quantize x): measured graph-timed, 3072 x 1024 Q8 4.41 -> 4.13 us with
+// 4-row tiles, 2048 x 2048 Q4 4.64 -> 4.32 us with 2-row tiles.
+constexpr int kMinTiles = 2048, kMinTilesShortX = 768;
 int pick_rows(bool q4, bool fx, int rows, int nt, bool pair, int cols) {
   int r = 8;  // 8 rows keep two chunk groups in the ring (measured faster than 16)
   while (r * nt * (pair ? 2 : 1) * 4 > 64) r /= 2;
-  while (r > 1 && (rows + r - 1) / r < 2048) r /= 2;
-  while (r > 1 && lds_for(q4, fx, r, nt, pair, cols, (q4 ? 64 : 32) + 4) > 64 * 1024) r /= 2;
+  const int min_tiles = pair || cols >= kWideCols ? kMinTiles : kMinTilesShortX;
+  while (r > 1 && (rows + r - 1) / r < min_tiles) r /= 2;
+  while (r > 1 &&
+         lds_for(q4, fx, r, nt, pair, cols, (q4 ? 64 : 32) + kChainPad, 4) > kLdsShared) {
+    r /= 2;
+  }
   return r;
 }
 
+// Waves per workgroup: 8 (one workgroup per CU, so each CU quantizes x
+// once) for matrices of at most kWideRows rows and at least kWideCols
+// columns whose chains fit the CU's LDS, else 4. Measured graph-timed:
+// 2048 x 6144 Q4 7.5 -> 6.9 us with 8 waves; a short x does better on two
+// 4-wave workgroups per CU (3072 x 1024 Q8 4.6 against 5.0 us, the
+// 6144 x 2048 Q4 pair 7.3 against 9.0 us).
+int pick_waves(bool q4, bool fx, int rows, int R, int nt, bool pair, int cols) {
+  if (rows > kWideRows || cols < kWideCols) return 4;
+  return lds_for(q4, fx, R, nt, pair, cols, (q4 ? 64 : 32) + kChainPad, 8) <= kLdsAlone ? 8 : 4;
+}
+
+template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF>
+int launch_w(GemvParams& p, int W, hipStream_t stream) {
+  return W >= 8 ? launch<F, R, NT, kPair, kArgmax, kF, 8>(p, stream)
+                : launch<F, R, NT, kPair, kArgmax, kF, 4>(p, stream);
+}
+
 template <int F, int NT, bool kPair, bool kArgmax, bool kF>
-int launch_nt(GemvParams& p, int R, hipStream_t stream) {
+int launch_nt(GemvParams& p, int R, int W, hipStream_t stream) {
   constexpr int RR_MAX = 16 / (NT * (kPair ? 2 : 1));
   switch (R) {
     case 8:
-      if constexpr (RR_MAX >= 8) return launch<F, 8, NT, kPair, kArgmax, kF>(p, stream);
+      if constexpr (RR_MAX >= 8) return launch_w<F, 8, NT, kPair, kArgmax, kF>(p, W, stream);
       break;
     case 4:
-      if constexpr (RR_MAX >= 4) return launch<F, 4, NT, kPair, kArgmax, kF>(p, stream);
+      if constexpr (RR_MAX >= 4) return launch_w<F, 4, NT, kPair, kArgmax, kF>(p, W, stream);
       break;
     case 2:
-      if constexpr (RR_MAX >= 2) return launch<F, 2, NT, kPair, kArgmax, kF>(p, stream);
+      if constexpr (RR_MAX >= 2) return launch_w<F, 2, NT, kPair, kArgmax, kF>(p, W, stream);
       break;
     case 1:
-      return launch<F, 1, NT, kPair, kArgmax, kF>(p, stream);
+      return launch_w<F, 1, NT, kPair, kArgmax, kF>(p, W, stream);
   }
   return DNX_EINVAL;
 }
@@ -605,32 +736,51 @@ int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, con
   if (kPair && ((uintptr_t)sc1 & (F != kFmtQ8 ? 1 : 3))) return DNX_EINVAL;
   if ((int64_t)rows * (kQ4 ? cols / 2 : cols) > ((int64_t)1 << 40)) return DNX_EINVAL;
   if (kArgmax && (n != 1 || ws == nullptr || out == nullptr)) return DNX_EINVAL;
-  GemvParams p{};
-  p.qs[0] = qs0;
-  p.scales[0] = sc0;
-  p.qs[1] = kPair ? qs1 : qs0;
-  p.scales[1] = kPair ? sc1 : sc0;
-  p.x = x;
-  p.y = y;
-  p.y2 = y2;
-  p.rows = (int)rows;
-  p.cols = (int)cols;
-  p.n = (int)n;
-  p.ws = ws;
+  // Launches over row ranges of under 2 GB of codes each (one buffer
+  // resource spans a launch's matrix); the fused argmax folds every range
+  // into the same slots, and one finisher follows.
+  const int64_t qrow = kQ4 ? cols / 2 : cols;
+  const int64_t srow = (cols / kBlock) * (F != kFmtQ8 ? 2 : 4);
+  const int64_t range = kMaxLaunchBytes / qrow;
   const int nt = n == 1 ? 1 : n == 2 ? 2 : 4;
-  const int R = pick_rows(kQ4, kF, (int)rows, nt, kPair, (int)cols);
-  if (kArgmax) {
-    const int rc = launch_nt<F, 1, false, true, false>(p, R, stream);
+  int slots = 0;
+  for (int64_t r0 = 0; r0 < rows; r0 += range) {
+    const int64_t nr = rows - r0 < range ? rows - r0 : range;
+    GemvParams p{};
+    p.qs[0] = (const uint8_t*)qs0 + r0 * qrow;
+    p.scales[0] = (const uint8_t*)sc0 + r0 * srow;
+    p.qs[1] = kPair ? (const uint8_t*)qs1 + r0 * qrow : p.qs[0];
+    p.scales[1] = kPair ? (const uint8_t*)sc1 + r0 * srow : p.scales[0];
+    p.x = x;
+    p.y = y + r0;
+    p.y2 = y2 != nullptr ? y2 + r0 : nullptr;
+    p.rows = (int)nr;
+    p.ldy = (int)rows;
+    p.row0 = (int)r0;
+    p.cols = (int)cols;
+    p.n = (int)n;
+    p.ws = ws;
+    const int R = pick_rows(kQ4, kF, (int)nr, nt, kPair, (int)cols);
+    const int W = pick_waves(kQ4, kF, (int)nr, R, nt, kPair, (int)cols);
+    int rc;
+    if (kArgmax) {
+      rc = launch_nt<F, 1, false, true, false>(p, R, W, stream);
+      slots = p.grid > slots ? p.grid : slots;
+    } else {
+      switch (nt) {
+        case 1: rc = launch_nt<F, 1, kPair, false, kF>(p, R, W, stream); break;
+        case 2: rc = launch_nt<F, 2, kPair, false, kF>(p, R, W, stream); break;
+        default: rc = launch_nt<F, 4, kPair, false, kF>(p, R, W, stream); break;
+      }
+    }
     if (rc != DNX_OK) return rc;
-    const int slots = p.grid < kArgmaxSlots ? p.grid : kArgmaxSlots;
+  }
+  if (kArgmax) {
+    if (slots > kArgmaxSlots) slots = kArgmaxSlots;
     hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(kThreads), 0, stream, ws, slots, out);
     return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
   }
-  switch (nt) {
-    case 1: return launch_nt<F, 1, kPair, false, kF>(p, R, stream);
-    case 2: return launch_nt<F, 2, kPair, false, kF>(p, R, stream);
-    default: return launch_nt<F, 4, kPair, false, kF>(p, R, stream);
-  }
+  return DNX_OK;
 }
 
 // Float inputs (mode 0), any n: launches of up to 4 tokens each.
@@ -642,7 +792,8 @@ int gemv_float(const void* qs, const void* scales, const float* x, float* y, int
   constexpr bool kQ4 = F == kFmtQ4;
   int group = 4;
   while (group > 1 &&
-         lds_for(kQ4, true, 1, group, false, (int)cols, (kQ4 ? 64 : 32) + 4) > 64 * 1024) {
+         lds_for(kQ4, true, 1, group, false, (int)cols, (kQ4 ? 64 : 32) + kChainPad, 4) >
+             kLdsShared) {
     group /= 2;
   }
   for (int64_t t0 = 0; t0 < n; t0 += group) {
