@@ -85,7 +85,27 @@ struct GemvParams {
   int stride;                  // LDS floats per chain: span of blocks + 4
   unsigned long long* ws;      // argmax: the rank slots, zero between calls
   int grid;                    // set by the launch
+  // Segmented launches (kSeg, n = 1): up to kMaxSegs matrices of one format
+  // and width over the same x, their tiles laid end to end; seg_end holds
+  // the cumulative tile ends (INT_MAX past the last segment).
+  int seg_end[4];
+  int seg_rows[4];
+  const void* seg_qs[4];
+  const void* seg_scales[4];
+  float* seg_y[4];
 };
+constexpr int kMaxSegs = 4;
+
+// The segment of a uniform tile index, as selects (an indexed read of the
+// kernel's argument array would go through private memory).
+template <class T>
+DNX_DEV T seg_pick(const T (&a)[4], const int s) {
+  return s == 0 ? a[0] : s == 1 ? a[1] : s == 2 ? a[2] : a[3];
+}
+DNX_DEV void seg_of(const GemvParams& p, const int tile, int& s, int& local) {
+  s = (tile >= p.seg_end[0]) + (tile >= p.seg_end[1]) + (tile >= p.seg_end[2]);
+  local = tile - (s == 0 ? 0 : s == 1 ? p.seg_end[0] : s == 2 ? p.seg_end[1] : p.seg_end[2]);
+}
 
 // Orders LDS writes and reads among the lanes of one wave (a wave's LDS
 // operations execute in issue order; this keeps the compiler from moving
@@ -103,7 +123,7 @@ DNX_DEV float silu_mul(float g, float u) {
   return s * u;
 }
 
-template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, int W>
+template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, int W, bool kSeg>
 __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
   // kF: float inputs (lab_gemm_q8 / lab_gemm_q4 mode 0): x is not quantized;
   // per block, lane l sums fma(float(w_j), x_j, s) over j = 4k + l, k = 0..7
@@ -172,19 +192,29 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
   // past this wave's last tile (offset kDead); lanes past a row's last block
   // read the next row, and their results are never used. The issue has no
   // branch.
+  // A segmented launch builds the resources of the tile's segment per
+  // request (scalar selects).
   auto issue1 = [&](const int s0, const int k, const int c, const int i) {
     const int tile = tile0 + k * stride;
     const int blk = c * CB + lblk;
     const int m = i / R, r = i - (i / R) * R;
-    const uint32_t row = (uint32_t)(tile * R + r);
+    int seg = 0, lt = tile;
+    if (kSeg) seg_of(p, tile, seg, lt);
+    const uint32_t row = (uint32_t)(lt * R + r);
     const bool live = k < my_tiles;
     const uint32_t oq = row * qrow + (kQ4 ? blk * 16 : blk * 32 + (lane & 1) * 16);
     const uint32_t os = row * srow + blk * (kHalf ? 2 : 4);
-    raw[s0 + i] = buffer_load16_stream(rq[m], (int)(live ? oq : kDead));
+    i32x4 q = rq[m], sc = rs[m];
+    if (kSeg) {
+      const uint32_t rows_s = (uint32_t)seg_pick(p.seg_rows, seg);
+      q = buffer_rsrc(seg_pick(p.seg_qs, seg), rows_s * qrow);
+      sc = buffer_rsrc(seg_pick(p.seg_scales, seg), rows_s * srow);
+    }
+    raw[s0 + i] = buffer_load16_stream(q, (int)(live ? oq : kDead));
     if (kHalf) {
-      swb[s0 + i] = dnx_raw_buffer_load_i16(rs[m], (int)(live ? os : kDead), 0, kStream);
+      swb[s0 + i] = dnx_raw_buffer_load_i16(sc, (int)(live ? os : kDead), 0, kStream);
     } else {
-      swb[s0 + i] = dnx_raw_buffer_load_i32(rs[m], (int)(live ? os : kDead), 0, kStream);
+      swb[s0 + i] = dnx_raw_buffer_load_i32(sc, (int)(live ? os : kDead), 0, kStream);
     }
   };
   auto issue = [&](const int s0, const int k, const int c) {
@@ -493,8 +523,11 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
         v = v + dppf<kQuadXor2>(v);
         acc = 0.0f;
         const int tr = lane >> 2, t = tr / RR, i = tr - (tr / RR) * RR;
-        const int row = tile * R + (i % R);
-        const bool lead = lane < CH && (lane & 3) == 0 && t < n && row < p.rows;
+        int seg = 0, lt = tile;
+        if (kSeg) seg_of(p, tile, seg, lt);
+        const int row = lt * R + (i % R);
+        const int rows_here = kSeg ? seg_pick(p.seg_rows, seg) : p.rows;
+        const bool lead = lane < CH && (lane & 3) == 0 && t < n && row < rows_here;
         float val = v;
         float* dst = nullptr;
         if (kPair) {
@@ -505,6 +538,8 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
           } else if (lead && p.y2 != nullptr) {
             dst = p.y2 + (size_t)t * p.ldy + row;
           }
+        } else if (kSeg) {
+          if (lead) dst = seg_pick(p.seg_y, seg) + row;  // n = 1
         } else {
           if (lead) dst = p.y + (size_t)t * p.ldy + row;
           if (kArgmax) {
@@ -615,7 +650,7 @@ size_t lds_budget(int W) { return W >= 8 ? kLdsAlone : kLdsShared; }
 // Ring slots per wave (the kernel's Q) for RR rows per tile.
 int ring_units(int RR) { return RR >= 8 ? RR : RR >= 2 ? 16 : 8; }
 
-template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, int W>
+template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, int W, bool kSeg = false>
 int launch(GemvParams& p, hipStream_t stream) {
   constexpr bool kQ4 = F == kFmtQ4;
   constexpr int CB = kQ4 ? 64 : 32, RR = R * (kPair ? 2 : 1);
@@ -628,7 +663,7 @@ int launch(GemvParams& p, hipStream_t stream) {
   p.stride = (p.full ? chunks * CB : CB) + kChainPad;
   const size_t lds = lds_for(kQ4, kF, R, NT, kPair, p.cols, p.stride, W);
   if (lds > budget) return DNX_EINVAL;  // x too wide for one workgroup's LDS
-  auto kernel = gemv_kernel<F, R, NT, kPair, kArgmax, kF, W>;
+  auto kernel = gemv_kernel<F, R, NT, kPair, kArgmax, kF, W, kSeg>;
   // Persistent grid: as many workgroups as stay resident (the occupancy is
   // looked up once per kernel and LDS size).
   static int cached_per_cu = 0;
@@ -648,7 +683,21 @@ int launch(GemvParams& p, hipStream_t stream) {
     cached_per_cu = per_cu;
     cached_lds = lds;
   }
-  p.tiles = (p.rows + R - 1) / R;
+  if (kSeg) {
+    // Each segment starts on a tile: cumulative tile ends at R rows per tile.
+    int end = 0;
+    for (int i = 0; i < kMaxSegs; i++) {
+      if (p.seg_rows[i] > 0) {
+        end += (p.seg_rows[i] + R - 1) / R;
+        p.seg_end[i] = end;
+      } else {
+        p.seg_end[i] = 0x7fffffff;
+      }
+    }
+    p.tiles = end;
+  } else {
+    p.tiles = (p.rows + R - 1) / R;
+  }
   const int need = (p.tiles + W - 1) / W;
   int cap = cached_per_cu * cu_count();
   // A wave defers its results in one register across its 64 lanes: at most
@@ -699,10 +748,21 @@ int pick_waves(bool q4, bool fx, int rows, int R, int nt, bool pair, int cols) {
   return lds_for(q4, fx, R, nt, pair, cols, (q4 ? 64 : 32) + kChainPad, 8) <= kLdsAlone ? 8 : 4;
 }
 
-template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF>
+template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, bool kSeg = false>
 int launch_w(GemvParams& p, int W, hipStream_t stream) {
-  return W >= 8 ? launch<F, R, NT, kPair, kArgmax, kF, 8>(p, stream)
-                : launch<F, R, NT, kPair, kArgmax, kF, 4>(p, stream);
+  return W >= 8 ? launch<F, R, NT, kPair, kArgmax, kF, 8, kSeg>(p, stream)
+                : launch<F, R, NT, kPair, kArgmax, kF, 4, kSeg>(p, stream);
+}
+
+// A segmented launch (one token, int8 inputs), R rows per tile.
+template <int F>
+int launch_seg(GemvParams& p, int R, int W, hipStream_t stream) {
+  switch (R) {
+    case 8: return launch_w<F, 8, 1, false, false, false, true>(p, W, stream);
+    case 4: return launch_w<F, 4, 1, false, false, false, true>(p, W, stream);
+    case 2: return launch_w<F, 2, 1, false, false, false, true>(p, W, stream);
+    default: return launch_w<F, 1, 1, false, false, false, true>(p, W, stream);
+  }
 }
 
 template <int F, int NT, bool kPair, bool kArgmax, bool kF>
@@ -781,6 +841,54 @@ int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, con
     return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
   }
   return DNX_OK;
+}
+
+// Up to kMaxSegs matrices of one format and width over the same x (one
+// token): y_i = W_i x for each, in one launch that quantizes x once. Each
+// matrix keeps its own pointers and rows; the results are bit-identical to
+// one gemv per matrix.
+template <int F>
+int gemv_multi(const void* const* qs, const void* const* scales, float* const* y,
+               const int64_t* rows, int segs, const float* x, int64_t cols, hipStream_t stream) {
+  if (segs < 1 || segs > kMaxSegs || cols <= 0 || cols % kBlock != 0 || cols > (1 << 20)) {
+    return DNX_EINVAL;
+  }
+  if (qs == nullptr || scales == nullptr || y == nullptr || rows == nullptr) return DNX_EINVAL;
+  if ((uintptr_t)x & 3) return DNX_EINVAL;
+  constexpr bool kQ4 = F == kFmtQ4;
+  const int64_t qrow = kQ4 ? cols / 2 : cols;
+  GemvParams p{};
+  int64_t total = 0;
+  for (int i = 0; i < kMaxSegs; i++) {
+    p.seg_rows[i] = 0;
+    p.seg_qs[i] = qs[0];
+    p.seg_scales[i] = scales[0];
+    p.seg_y[i] = y[0];
+  }
+  for (int i = 0; i < segs; i++) {
+    if (rows[i] <= 0 || rows[i] * qrow > kMaxLaunchBytes) return DNX_EINVAL;
+    if (((uintptr_t)qs[i] & 15) || ((uintptr_t)scales[i] & (F != kFmtQ8 ? 1 : 3))) {
+      return DNX_EINVAL;
+    }
+    if (y[i] == nullptr) return DNX_EINVAL;
+    p.seg_rows[i] = (int)rows[i];
+    p.seg_qs[i] = qs[i];
+    p.seg_scales[i] = scales[i];
+    p.seg_y[i] = y[i];
+    total += rows[i];
+  }
+  if (total > (1 << 30)) return DNX_EINVAL;
+  p.qs[0] = p.qs[1] = qs[0];
+  p.scales[0] = p.scales[1] = scales[0];
+  p.x = x;
+  p.y = y[0];
+  p.rows = (int)total;
+  p.ldy = (int)total;
+  p.cols = (int)cols;
+  p.n = 1;
+  const int R = pick_rows(kQ4, false, (int)total, 1, false, (int)cols);
+  const int W = pick_waves(kQ4, false, (int)total, R, 1, false, (int)cols);
+  return launch_seg<F>(p, R, W, stream);
 }
 
 // Float inputs (mode 0), any n: launches of up to 4 tokens each.
@@ -881,5 +989,26 @@ int dnx_gate_up_q8h(const int8_t* gate_qs, const uint16_t* gate_scales, const in
 }
 
 int64_t dnx_gemv_argmax_workspace_bytes(void) { return (int64_t)kArgmaxSlots * 8; }
+
+int dnx_gemv_multi_q8(const int8_t* const* qs, const float* const* scales, float* const* y,
+                      const int64_t* rows, int segs, const float* x, int64_t cols,
+                      hipStream_t stream) {
+  return gemv_multi<kFmtQ8>((const void* const*)qs, (const void* const*)scales, y, rows, segs,
+                            x, cols, stream);
+}
+
+int dnx_gemv_multi_q4(const uint8_t* const* qs, const uint16_t* const* scales, float* const* y,
+                      const int64_t* rows, int segs, const float* x, int64_t cols,
+                      hipStream_t stream) {
+  return gemv_multi<kFmtQ4>((const void* const*)qs, (const void* const*)scales, y, rows, segs,
+                            x, cols, stream);
+}
+
+int dnx_gemv_multi_q8h(const int8_t* const* qs, const uint16_t* const* scales, float* const* y,
+                       const int64_t* rows, int segs, const float* x, int64_t cols,
+                       hipStream_t stream) {
+  return gemv_multi<kFmtQ8H>((const void* const*)qs, (const void* const*)scales, y, rows, segs,
+                             x, cols, stream);
+}
 
 }  // extern "C"

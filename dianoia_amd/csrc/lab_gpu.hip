@@ -473,6 +473,70 @@ int run_pair(const Cmd& a, const Cmd& b) {
   return rc;
 }
 
+// Fusion of up to four decode matmuls over the same input: commands
+// i .. i+L-1 (L >= 2) are one-token matmuls of one format, int8 inputs, the
+// same x region and width (GpuForward.forward's q, k, v and gate
+// projections, gpu.dart:1148-1156). Their outputs must be disjoint from each
+// other and from x, so running them in one launch leaves what the L
+// dispatches leave. Returns L, or 0.
+bool overlaps(int64_t h0, int64_t o0, int64_t b0, int64_t h1, int64_t o1, int64_t b1) {
+  return h0 == h1 && o0 < o1 + b1 && o1 < o0 + b0;
+}
+
+size_t fusable_multi(const std::vector<Cmd>& cmds, size_t i) {
+  const Cmd& a = cmds[i];
+  if (!(a.op == kOpMatmulQ8 || a.op == kOpMatmulQ4) || !a.int8_inputs || a.a[9] != 1) return 0;
+  const int64_t x = a.a[3], xOff = a.a[4], cols = a.a[8];
+  size_t len = 0;
+  for (size_t j = i; j < cmds.size() && len < 4; j++, len++) {
+    const Cmd& b = cmds[j];
+    if (b.op != a.op || !b.int8_inputs || b.a[9] != 1 || b.a[3] != x || b.a[4] != xOff ||
+        b.a[8] != cols) {
+      break;
+    }
+    if (overlaps(b.a[5], b.a[6], b.a[7] * 4, x, xOff, cols * 4)) break;
+    bool clash = false;
+    for (size_t k = i; k < j; k++) {
+      clash = clash || overlaps(b.a[5], b.a[6], b.a[7] * 4, cmds[k].a[5], cmds[k].a[6],
+                                cmds[k].a[7] * 4);
+    }
+    if (clash) break;
+  }
+  return len >= 2 ? len : 0;
+}
+
+// DNX_OK, or the launcher's code; DNX_EINVAL means nothing was launched (the
+// caller then runs the commands one by one).
+int run_multi(const std::vector<Cmd>& cmds, size_t i, size_t len) {
+  const Cmd& a = cmds[i];
+  const bool q4 = a.op == kOpMatmulQ4;
+  const int64_t x = a.a[3], xOff = a.a[4], cols = a.a[8];
+  const void* qs[4];
+  const void* sc[4];
+  float* ys[4];
+  int64_t rows[4];
+  for (size_t k = 0; k < len; k++) {
+    const Cmd& c = cmds[i + k];
+    use_as_weights(c.a[0]);
+    qs[k] = dev_at(c.a[0], c.a[1]);
+    sc[k] = dev_at(c.a[0], c.a[2]);
+    ys[k] = (float*)dev_at(c.a[5], c.a[6]);
+    rows[k] = c.a[7];
+  }
+  read_region(x, xOff, cols * 4);
+  const float* xs = (const float*)dev_at(x, xOff);
+  const int rc =
+      q4 ? dnx_gemv_multi_q4((const uint8_t* const*)qs, (const uint16_t* const*)sc, ys, rows,
+                             (int)len, xs, cols, gStream)
+         : dnx_gemv_multi_q8((const int8_t* const*)qs, (const float* const*)sc, ys, rows,
+                             (int)len, xs, cols, gStream);
+  if (rc == DNX_EINVAL) return rc;
+  if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+  for (size_t k = 0; k < len; k++) wrote_region(cmds[i + k].a[5], cmds[i + k].a[6], rows[k] * 4);
+  if (rc != DNX_OK) LOG("%zu fused matmuls of width %ld failed (%d)\n", len, (long)cols, rc);
+  return rc;
+}
+
 // Fusion of a decode matmul (n = 1) and the argmax of its whole output.
 bool fusable_argmax(const Cmd& a, const Cmd& b) {
   return (a.op == kOpMatmulQ8 || a.op == kOpMatmulQ4) && a.int8_inputs && b.op == kOpArgmax &&
@@ -834,6 +898,14 @@ int64_t lab_gpu_commit(int64_t wait) {
     } else if (i + 1 < gCmds.size() && fusable_argmax(gCmds[i], gCmds[i + 1])) {
       ok = run_matmul_argmax(gCmds[i], gCmds[i + 1]) && ok;
       i += 1;
+    } else if (const size_t len = fusable_multi(gCmds, i)) {
+      const int rc = run_multi(gCmds, i, len);
+      if (rc == DNX_EINVAL) {  // not launched: the matmuls as recorded
+        for (size_t k = 0; k < len; k++) ok = run(gCmds[i + k]) && ok;
+      } else {
+        ok = rc == DNX_OK && ok;
+      }
+      i += len - 1;
     } else {
       ok = run(gCmds[i]) && ok;
     }

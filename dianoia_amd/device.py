@@ -8,6 +8,8 @@ nothing was launched.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -148,6 +150,21 @@ def gate_up_q8h(gq, gs, uq, us, x, h, rows: int, cols: int, n: int = 1, u=None,
                 stream=None) -> None:
     _check(_lib.load().dnx_gate_up_q8h(_ptr(gq), _ptr(gs), _ptr(uq), _ptr(us), _ptr(x), _ptr(h),
                                        _ptr(u), rows, cols, n, _stream(stream)), "dnx_gate_up_q8h")
+
+
+def gemv_multi(fmt: str, mats, x, ys, cols: int, stream=None) -> None:
+    """Up to 4 one-token GEMVs over the same x in one launch: mats is a list of
+    (qs, scales, rows), ys the matching outputs; fmt "q8", "q4" or "q8h"."""
+    segs = len(mats)
+    P = ctypes.c_void_p * max(segs, 1)
+    qs = P(*[_ptr(m[0]) for m in mats])
+    sc = P(*[_ptr(m[1]) for m in mats])
+    yp = P(*[_ptr(y) for y in ys])
+    rows = (ctypes.c_int64 * max(segs, 1))(*[int(m[2]) for m in mats])
+    name = {"q8": "dnx_gemv_multi_q8", "q4": "dnx_gemv_multi_q4", "q8h": "dnx_gemv_multi_q8h"}[fmt]
+    _check(getattr(_lib.load(), name)(ctypes.cast(qs, ctypes.c_void_p), ctypes.cast(sc, ctypes.c_void_p),
+                                      ctypes.cast(yp, ctypes.c_void_p), ctypes.cast(rows, ctypes.c_void_p),
+                                      segs, _ptr(x), cols, _stream(stream)), name)
 
 
 def gemm_q8_float(qs, scales, x, y, rows: int, cols: int, n: int, stream=None) -> None:

@@ -121,6 +121,22 @@ int dnx_gate_up_q8h(const int8_t* gate_qs, const uint16_t* gate_scales, const in
                     const uint16_t* up_scales, const float* x, float* h, float* u, int64_t rows,
                     int64_t cols, int64_t n, dnx_stream_t stream);
 
+// Up to 4 decode GEMVs over the same x in one launch (one token, int8
+// inputs): y[i] = W_i x for i < segs, W_i with rows[i] rows of cols columns
+// at qs[i] / scales[i], each y[i] bit-identical to dnx_gemv_*(W_i, x) (the
+// attention projections q, k, v and gate of GpuForward.forward, lib/src/
+// gpu.dart:1148-1156, read the same normed x). x is quantized once for all.
+// The pointer arrays are read on the host at the call.
+int dnx_gemv_multi_q8(const int8_t* const* qs, const float* const* scales, float* const* y,
+                      const int64_t* rows, int segs, const float* x, int64_t cols,
+                      dnx_stream_t stream);
+int dnx_gemv_multi_q4(const uint8_t* const* qs, const uint16_t* const* scales, float* const* y,
+                      const int64_t* rows, int segs, const float* x, int64_t cols,
+                      dnx_stream_t stream);
+int dnx_gemv_multi_q8h(const int8_t* const* qs, const uint16_t* const* scales, float* const* y,
+                       const int64_t* rows, int segs, const float* x, int64_t cols,
+                       dnx_stream_t stream);
+
 // Float-input GEMM (lab_gemm_q8 / lab_gemm_q4 mode 0 for many tokens,
 // lab_native.c:489-501, :1013-1023; the reference's float GPU GEMMs,
 // lab_metal.m:79-144, :174-258) on bf16 MFMA: x (fp32 [n][cols]) split

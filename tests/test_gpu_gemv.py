@@ -198,3 +198,39 @@ def test_gate_up_pair(gpu_ready, orc, fmt, rows, cols, n):
     # SiLU runs in double on both sides (GPU exp vs the C library's): the
     # float results agree except, rarely, by one ulp at a rounding boundary.
     assert ulp.max() <= 1 and np.mean(ulp == 0) > 0.999
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q8h"])
+@pytest.mark.parametrize("rows,cols", [((2048, 1024, 1024), 2048), ((2048, 1024, 1024, 2048), 2048),
+                                       ((70, 1, 129), 96), ((3072, 512), 1024),
+                                       ((1000, 33), 6144), ((4097, 8, 300, 17), 64)])
+def test_multi_gemv(gpu_ready, orc, fmt, rows, cols):
+    """Up to four one-token GEMVs over the same x in one launch (the
+    attention projections of a decode step): each output bit-identical to
+    lab_gemm mode 1 on its own matrix, and nothing written past its rows."""
+    rng = np.random.default_rng(sum(rows) * 7 + cols)
+    make = synth.q4_weights if fmt == "q4" else synth.q8_weights
+    mats = [make(rng, r, cols) for r in rows]
+    x = synth.activations(rng, 1, cols)
+    gemm = orc.gemm_q4 if fmt == "q4" else orc.gemm_q8
+    refs = [gemm(q, s, x, 1, threads=8, mode=1) for q, s in mats]
+    ys = [torch.full((r + 64,), float("nan"), device="cuda") for r in rows]
+    args = [(dev(q), dev(half_scales(s) if fmt == "q8h" else s), r) for (q, s), r in zip(mats, rows)]
+    D.gemv_multi(fmt, args, dev(x), ys, cols)
+    for y, ref, r in zip(ys, refs, rows):
+        yh = host(y)
+        assert np.array_equal(bits(yh[:r]), bits(ref[0]))
+        assert np.isnan(yh[r:]).all()
+
+
+def test_multi_gemv_rejects_unsupported(gpu_ready):
+    z = torch.zeros(4096, device="cuda")
+    q = torch.zeros(4096, dtype=torch.int8, device="cuda")
+    with pytest.raises(RuntimeError):
+        D.gemv_multi("q8", [], z, [], 64)                               # no matrices
+    with pytest.raises(RuntimeError):
+        D.gemv_multi("q8", [(q, z, 4)] * 5, z, [z] * 5, 64)              # more than four
+    with pytest.raises(RuntimeError):
+        D.gemv_multi("q8", [(q, z, 4), (q, z, 0)], z, [z, z], 64)        # an empty matrix
+    with pytest.raises(RuntimeError):
+        D.gemv_multi("q8", [(q, z, 4)], z, [z], 48)                      # cols % 32 != 0
