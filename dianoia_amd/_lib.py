@@ -89,6 +89,7 @@ SIGNATURES = {
     "dnx_gemv_q8h_argmax": ([_p, _p, _p, _p, _i64, _i64, _p, _p, _p], _i32),
     "dnx_gate_up_q8h": ([_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemv_multi_q8": ([_p, _p, _p, _p, _i32, _p, _i64, _p], _i32),
+    "dnx_copy_regions": ([_p, _p, _p, _i32, _p], _i32),
     "dnx_gemv_multi_q4": ([_p, _p, _p, _p, _i32, _p, _i64, _p], _i32),
     "dnx_gemv_multi_q8h": ([_p, _p, _p, _p, _i32, _p, _i64, _p], _i32),
     "dnx_gemm_q8": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),

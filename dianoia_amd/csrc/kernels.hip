@@ -593,6 +593,44 @@ int split_gguf(const void* blocks, uint8_t* qs, void* scales, int64_t count, hip
   return DNX_OK;
 }
 
+// Region copies in one launch (the copy-backs of a commit to the host
+// views). The table travels in the kernel arguments; workgroup b copies the
+// kCopyChunk-byte chunk b - chunk0[r] of region r, the region whose chunk
+// range holds b (a binary search over the table). Regions whose pointers
+// and size are 16-byte multiples copy 16 bytes per lane, the rest byte by
+// byte. Plain vector stores, so a destination may be pinned host memory.
+constexpr int kCopyChunk = 16384;
+constexpr int kCopyMax = DNX_COPY_MAX;
+struct CopyTable {
+  const uint8_t* src[kCopyMax];
+  uint8_t* dst[kCopyMax];
+  int64_t bytes[kCopyMax];
+  int chunk0[kCopyMax + 1];
+  int count;
+};
+
+__global__ void __launch_bounds__(kThreads) copy_regions_kernel(const CopyTable t) {
+  const int b = blockIdx.x;
+  int lo = 0, hi = t.count - 1;  // the last r with chunk0[r] <= b
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (t.chunk0[mid] <= b) lo = mid; else hi = mid - 1;
+  }
+  const int r = lo;
+  const int64_t off = (int64_t)(b - t.chunk0[r]) * kCopyChunk;
+  const int64_t left = t.bytes[r] - off;
+  const int64_t len = left < kCopyChunk ? left : kCopyChunk;
+  const uint8_t* src = t.src[r] + off;
+  uint8_t* dst = t.dst[r] + off;
+  if ((((uintptr_t)t.src[r] | (uintptr_t)t.dst[r] | (uintptr_t)t.bytes[r]) & 15) == 0) {
+    for (int64_t i = threadIdx.x; i < len / 16; i += kThreads) {
+      ((uint4*)dst)[i] = ((const uint4*)src)[i];
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < len; i += kThreads) dst[i] = src[i];
+  }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------ C ABI
@@ -681,6 +719,33 @@ int dnx_swiglu(float* g, const float* u, int64_t count, hipStream_t stream) {
   if (count == 0) return DNX_OK;
   hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(count, kThreads, 65536)), dim3(kThreads), 0,
                      stream, g, u, count);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_copy_regions(const void* const* src, void* const* dst, const int64_t* bytes, int count,
+                     hipStream_t stream) {
+  if (count < 0 || count > kCopyMax || (count > 0 && (!src || !dst || !bytes))) return DNX_EINVAL;
+  CopyTable t{};
+  int chunks = 0;
+  int used = 0;
+  for (int i = 0; i < count; i++) {
+    if (bytes[i] < 0 || (bytes[i] > 0 && (src[i] == nullptr || dst[i] == nullptr))) {
+      return DNX_EINVAL;
+    }
+    if (bytes[i] == 0) continue;
+    const int64_t c = (bytes[i] + kCopyChunk - 1) / kCopyChunk;
+    if (c > (1 << 24) || chunks + c > (1 << 30)) return DNX_EINVAL;
+    t.src[used] = (const uint8_t*)src[i];
+    t.dst[used] = (uint8_t*)dst[i];
+    t.bytes[used] = bytes[i];
+    t.chunk0[used] = chunks;
+    chunks += (int)c;
+    used++;
+  }
+  t.chunk0[used] = chunks;
+  t.count = used;
+  if (used == 0) return DNX_OK;
+  hipLaunchKernelGGL(copy_regions_kernel, dim3(chunks), dim3(kThreads), 0, stream, t);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 

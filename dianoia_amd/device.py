@@ -152,6 +152,19 @@ def gate_up_q8h(gq, gs, uq, us, x, h, rows: int, cols: int, n: int = 1, u=None,
                                        _ptr(u), rows, cols, n, _stream(stream)), "dnx_gate_up_q8h")
 
 
+def copy_regions(regions, stream=None) -> None:
+    """Byte copies in one launch: regions is a list of (src_ptr, dst_ptr,
+    bytes) with device or pinned-host pointers (ints)."""
+    count = len(regions)
+    P = ctypes.c_void_p * max(count, 1)
+    src = P(*[r[0] for r in regions])
+    dst = P(*[r[1] for r in regions])
+    nb = (ctypes.c_int64 * max(count, 1))(*[int(r[2]) for r in regions])
+    _check(_lib.load().dnx_copy_regions(ctypes.cast(src, ctypes.c_void_p), ctypes.cast(dst, ctypes.c_void_p),
+                                        ctypes.cast(nb, ctypes.c_void_p), count, _stream(stream)),
+           "dnx_copy_regions")
+
+
 def gemv_multi(fmt: str, mats, x, ys, cols: int, stream=None) -> None:
     """Up to 4 one-token GEMVs over the same x in one launch: mats is a list of
     (qs, scales, rows), ys the matching outputs; fmt "q8", "q4" or "q8h"."""

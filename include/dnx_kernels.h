@@ -29,6 +29,17 @@ enum {
   DNX_ESCRATCH = -4, // the call needs more than the fixed scratch array holds
 };
 
+// Up to DNX_COPY_MAX byte copies (src[i] -> dst[i], bytes[i] each) in one
+// launch on `stream`; a destination may be pinned host memory
+// (hipHostMalloc), which the kernel writes directly. No counterpart in the
+// reference: the lab_gpu_* recorder copies a commit's written regions back
+// to their host views with it (one launch instead of one copy per region).
+// Regions are copied concurrently: destinations must not overlap each other
+// or any source. The arrays are read on the host at the call.
+enum { DNX_COPY_MAX = 96 };
+int dnx_copy_regions(const void* const* src, void* const* dst, const int64_t* bytes, int count,
+                     dnx_stream_t stream);
+
 // lab_quantize_q8 (lab_native.c:407-429) on the GPU, bit-exact: rows x cols
 // fp32 -> int8 [rows][cols_pad] + fp32 scales [rows][cols_pad/32]. cols_pad
 // is a multiple of 32 >= cols; the values past cols are zero padding (the
