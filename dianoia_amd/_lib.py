@@ -119,6 +119,8 @@ SIGNATURES = {
     "dnx_gelu": ([_p, _i64, _p], _i32),
     "dnx_rms_norm": ([_p, _p, _p, _i64, _i64, _f32, _i32, _p], _i32),
     "dnx_head_norm_rope": ([_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _f32, _p], _i32),
+    "dnx_head_norm_rope2": ([_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _f32, _p], _i32),
+    "dnx_add_rms_norm": ([_p, _p, _p, _p, _i64, _i64, _f32, _p], _i32),
     "dnx_short_conv": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_attention_max_keys": ([_i64], _i64),
     "dnx_attention": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p], _i32),

@@ -537,6 +537,80 @@ int run_multi(const std::vector<Cmd>& cmds, size_t i, size_t len) {
   return rc;
 }
 
+// Fusion of a residual add and the RMSNorm of its result (GpuForward.forward
+// adds the block's output into x, then norms x for the next block,
+// gpu.dart:1180-1187): dnx_add_rms_norm, when the norm reads exactly the
+// add's destination, does not accumulate, and m, x and out do not overlap.
+bool fusable_add_norm(const Cmd& a, const Cmd& b) {
+  if (a.op != kOpAdd || b.op != kOpRmsNorm || b.a[9] != 0) return false;
+  const int64_t m = a.a[0], mOff = a.a[1], x = a.a[2], xOff = a.a[3], count = a.a[4];
+  const int64_t out = b.a[4], outOff = b.a[5], rows = b.a[6], cols = b.a[7];
+  if (b.a[0] != x || b.a[1] != xOff || rows * cols != count) return false;
+  const int64_t bytes = count * 4;
+  return !overlaps(m, mOff, bytes, x, xOff, bytes) && !overlaps(out, outOff, bytes, x, xOff, bytes) &&
+         !overlaps(out, outOff, bytes, m, mOff, bytes);
+}
+
+int run_add_norm(const Cmd& a, const Cmd& b) {
+  const int64_t m = a.a[0], mOff = a.a[1], x = a.a[2], xOff = a.a[3], count = a.a[4];
+  const int64_t w = b.a[2], wOff = b.a[3], out = b.a[4], outOff = b.a[5], rows = b.a[6];
+  const int64_t cols = b.a[7];
+  const double eps = __builtin_bit_cast(double, b.a[8]);
+  read_region(m, mOff, count * 4);
+  read_region(x, xOff, count * 4);
+  read_region(w, wOff, cols * 4);
+  const int rc = dnx_add_rms_norm((const float*)dev_at(m, mOff), (float*)dev_at(x, xOff),
+                                  (const float*)dev_at(w, wOff), (float*)dev_at(out, outOff), rows,
+                                  cols, (float)eps, gStream);
+  if (rc == DNX_EINVAL) return rc;
+  if (rc == DNX_OK) after_dispatch(kKindRmsNorm);
+  wrote_region(x, xOff, count * 4);
+  wrote_region(out, outOff, count * 4);
+  if (rc != DNX_OK) LOG("add + rms_norm %ldx%ld failed (%d)\n", (long)rows, (long)cols, rc);
+  return rc;
+}
+
+// Fusion of two head norm + RoPE steps over one rope table (a decode step's
+// q and k, gpu.dart:1162-1163) whose operands do not overlap each other or
+// the weights and table they read.
+int64_t head_rope_bytes(const Cmd& c) { return ((c.a[10] - 1) * c.a[2] + c.a[8] * c.a[9]) * 4; }
+
+bool fusable_rope_pair(const Cmd& a, const Cmd& b) {
+  if (a.op != kOpHeadNormRope || b.op != kOpHeadNormRope) return false;
+  for (int k = 5; k <= 11; k++) {
+    if (k != 8 && a.a[k] != b.a[k]) return false;  // rope, stride, hd, n, eps; heads may differ
+  }
+  if (a.a[10] <= 0) return false;
+  const int64_t ab = head_rope_bytes(a), bb = head_rope_bytes(b);
+  const int64_t rb = ((a.a[10] - 1) * a.a[7] + a.a[9]) * 4, wb = a.a[9] * 4;
+  return !overlaps(a.a[0], a.a[1], ab, b.a[0], b.a[1], bb) &&
+         !overlaps(a.a[0], a.a[1], ab, a.a[5], a.a[6], rb) &&
+         !overlaps(b.a[0], b.a[1], bb, a.a[5], a.a[6], rb) &&
+         !overlaps(a.a[0], a.a[1], ab, b.a[3], b.a[4], wb) &&
+         !overlaps(b.a[0], b.a[1], bb, a.a[3], a.a[4], wb);
+}
+
+int run_rope_pair(const Cmd& a, const Cmd& b) {
+  const int64_t rope = a.a[5], ropeOff = a.a[6], ropeStride = a.a[7], hd = a.a[9], n = a.a[10];
+  const double eps = __builtin_bit_cast(double, a.a[11]);
+  const int64_t ab = head_rope_bytes(a), bb = head_rope_bytes(b);
+  read_region(a.a[0], a.a[1], ab);
+  read_region(b.a[0], b.a[1], bb);
+  read_region(a.a[3], a.a[4], hd * 4);
+  read_region(b.a[3], b.a[4], hd * 4);
+  read_region(rope, ropeOff, ((n - 1) * ropeStride + hd) * 4);
+  const int rc = dnx_head_norm_rope2(
+      (float*)dev_at(a.a[0], a.a[1]), a.a[2], (const float*)dev_at(a.a[3], a.a[4]), a.a[8],
+      (float*)dev_at(b.a[0], b.a[1]), b.a[2], (const float*)dev_at(b.a[3], b.a[4]), b.a[8],
+      (const float*)dev_at(rope, ropeOff), ropeStride, hd, n, (float)eps, gStream);
+  if (rc == DNX_EINVAL) return rc;
+  if (rc == DNX_OK) after_dispatch(kKindHeadNormRope);
+  wrote_region(a.a[0], a.a[1], ab);
+  wrote_region(b.a[0], b.a[1], bb);
+  if (rc != DNX_OK) LOG("head norm + rope pair failed (%d)\n", rc);
+  return rc;
+}
+
 // Fusion of a decode matmul (n = 1) and the argmax of its whole output.
 bool fusable_argmax(const Cmd& a, const Cmd& b) {
   return (a.op == kOpMatmulQ8 || a.op == kOpMatmulQ4) && a.int8_inputs && b.op == kOpArgmax &&
@@ -897,6 +971,24 @@ int64_t lab_gpu_commit(int64_t wait) {
       i += 2;
     } else if (i + 1 < gCmds.size() && fusable_argmax(gCmds[i], gCmds[i + 1])) {
       ok = run_matmul_argmax(gCmds[i], gCmds[i + 1]) && ok;
+      i += 1;
+    } else if (i + 1 < gCmds.size() && fusable_add_norm(gCmds[i], gCmds[i + 1])) {
+      const int rc = run_add_norm(gCmds[i], gCmds[i + 1]);
+      if (rc == DNX_EINVAL) {
+        ok = run(gCmds[i]) && ok;
+        ok = run(gCmds[i + 1]) && ok;
+      } else {
+        ok = rc == DNX_OK && ok;
+      }
+      i += 1;
+    } else if (i + 1 < gCmds.size() && fusable_rope_pair(gCmds[i], gCmds[i + 1])) {
+      const int rc = run_rope_pair(gCmds[i], gCmds[i + 1]);
+      if (rc == DNX_EINVAL) {
+        ok = run(gCmds[i]) && ok;
+        ok = run(gCmds[i + 1]) && ok;
+      } else {
+        ok = rc == DNX_OK && ok;
+      }
       i += 1;
     } else if (const size_t len = fusable_multi(gCmds, i)) {
       const int rc = run_multi(gCmds, i, len);

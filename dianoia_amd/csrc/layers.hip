@@ -84,16 +84,22 @@ rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, float*
 // (accumulating) out is issued at the start, so the row costs one memory
 // round trip instead of a dependent walk over it. The decode step's norms
 // (one row of the hidden size) are latency, not bandwidth: 6.6 -> ~3 us.
-template <int V>
+//
+// kAdd: the residual add before the norm in the same pass (x += m, as
+// add_kernel rounds it, stored back to x, then the norm of the new x): the
+// pair dnx_add + dnx_rms_norm in one launch.
+template <int V, bool kAdd = false>
 __global__ void __launch_bounds__(kThreads)
-rms_norm_vec_kernel(const float* __restrict__ x, const float* __restrict__ w, float* out,
-                    int cols, float eps, int accumulate) {
+rms_norm_vec_kernel(const float* x_in, const float* __restrict__ w, float* out, int cols,
+                    float eps, int accumulate, const float* __restrict__ m, float* x_out) {
   __shared__ float scratch[kWaves];
   const int q = cols / 4;
-  const float4* xr = (const float4*)(x + (size_t)blockIdx.x * cols);
+  const float4* xr = (const float4*)(x_in + (size_t)blockIdx.x * cols);
+  const float4* mr = (const float4*)(m + (size_t)blockIdx.x * cols);
+  float4* xw = (float4*)(x_out + (size_t)blockIdx.x * cols);
   const float4* wr = (const float4*)w;
   float4* yr = (float4*)(out + (size_t)blockIdx.x * cols);
-  float4 xv[V], wv[V], ov[V];
+  float4 xv[V], wv[V], ov[V], mv[V];
   const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int e = 0; e < V; e++) {
@@ -102,6 +108,18 @@ rms_norm_vec_kernel(const float* __restrict__ x, const float* __restrict__ w, fl
     xv[e] = ok ? xr[i] : z;
     wv[e] = ok ? wr[i] : z;
     ov[e] = (ok && accumulate) ? yr[i] : z;
+    mv[e] = (ok && kAdd) ? mr[i] : z;
+  }
+  if (kAdd) {
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+      const int i = e * kThreads + threadIdx.x;
+      xv[e].x = xv[e].x + mv[e].x;
+      xv[e].y = xv[e].y + mv[e].y;
+      xv[e].z = xv[e].z + mv[e].z;
+      xv[e].w = xv[e].w + mv[e].w;
+      if (i < q) xw[i] = xv[e];
+    }
   }
   float sum = 0.0f;
 #pragma unroll
@@ -136,12 +154,24 @@ rms_norm_vec_kernel(const float* __restrict__ x, const float* __restrict__ w, fl
 // with weight w, then the half-split RoPE rotation pairing j with
 // j + hd / 2, from the token's tables [cos(hd / 2), sin(hd / 2)]. In place;
 // each lane reads its pairs before the reduction and writes only them.
+//
+// Two operands may share a launch (a decode step's q and k heads, one rope
+// table): workgroups with blockIdx.x below heads0 take (x, x_stride, w) and
+// the rest (xb, xb_stride, wb), head blockIdx.x - heads0.
 __global__ void __launch_bounds__(64)
 head_norm_rope_kernel(float* x, int x_stride, const float* __restrict__ w,
-                      const float* __restrict__ rope, int rope_stride, int hd, float eps) {
+                      const float* __restrict__ rope, int rope_stride, int hd, float eps,
+                      int heads0, float* xb, int xb_stride, const float* __restrict__ wb) {
   constexpr int kPairs = 4;  // hd <= 512
   const int lane = threadIdx.x, pair = hd / 2;
-  float* xh = x + (size_t)blockIdx.y * x_stride + (size_t)blockIdx.x * hd;
+  const bool second = (int)blockIdx.x >= heads0;
+  if (second) {
+    x = xb;
+    x_stride = xb_stride;
+    w = wb;
+  }
+  const int head = second ? (int)blockIdx.x - heads0 : (int)blockIdx.x;
+  float* xh = x + (size_t)blockIdx.y * x_stride + (size_t)head * hd;
   const float* table = rope + (size_t)blockIdx.y * rope_stride;
   float x1[kPairs], x2[kPairs];
   float sum = 0.0f;
@@ -968,23 +998,52 @@ int dnx_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64
     const int64_t per = (cols / 4 + kThreads - 1) / kThreads;  // float4 per thread
     if (per <= 1) {
       hipLaunchKernelGGL(rms_norm_vec_kernel<1>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
-                         (int)cols, eps, accumulate);
+                         (int)cols, eps, accumulate, nullptr, nullptr);
     } else if (per <= 2) {
       hipLaunchKernelGGL(rms_norm_vec_kernel<2>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
-                         (int)cols, eps, accumulate);
+                         (int)cols, eps, accumulate, nullptr, nullptr);
     } else if (per <= 4) {
       hipLaunchKernelGGL(rms_norm_vec_kernel<4>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
-                         (int)cols, eps, accumulate);
+                         (int)cols, eps, accumulate, nullptr, nullptr);
     } else if (per <= 8) {
       hipLaunchKernelGGL(rms_norm_vec_kernel<8>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
-                         (int)cols, eps, accumulate);
+                         (int)cols, eps, accumulate, nullptr, nullptr);
     } else {
       hipLaunchKernelGGL(rms_norm_vec_kernel<16>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
-                         (int)cols, eps, accumulate);
+                         (int)cols, eps, accumulate, nullptr, nullptr);
     }
   } else {
     hipLaunchKernelGGL(rms_norm_kernel, dim3(grid), dim3(kThreads), 0, s, x, w, out, (int)cols,
                        eps, accumulate);
+  }
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_add_rms_norm(const float* m, float* x, const float* w, float* out, int64_t rows,
+                     int64_t cols, float eps, dnx_stream_t stream) {
+  if (rows < 0 || cols <= 0 || rows > 256 || cols % 4 != 0 || cols > 16 * 4 * kThreads ||
+      (((uintptr_t)m | (uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 15) != 0) {
+    return DNX_EINVAL;
+  }
+  if (rows == 0) return DNX_OK;
+  const unsigned grid = (unsigned)rows;
+  const hipStream_t s = (hipStream_t)stream;
+  const int64_t per = (cols / 4 + kThreads - 1) / kThreads;  // float4 per thread
+  if (per <= 1) {
+    hipLaunchKernelGGL((rms_norm_vec_kernel<1, true>), dim3(grid), dim3(kThreads), 0, s, x, w,
+                       out, (int)cols, eps, 0, m, x);
+  } else if (per <= 2) {
+    hipLaunchKernelGGL((rms_norm_vec_kernel<2, true>), dim3(grid), dim3(kThreads), 0, s, x, w,
+                       out, (int)cols, eps, 0, m, x);
+  } else if (per <= 4) {
+    hipLaunchKernelGGL((rms_norm_vec_kernel<4, true>), dim3(grid), dim3(kThreads), 0, s, x, w,
+                       out, (int)cols, eps, 0, m, x);
+  } else if (per <= 8) {
+    hipLaunchKernelGGL((rms_norm_vec_kernel<8, true>), dim3(grid), dim3(kThreads), 0, s, x, w,
+                       out, (int)cols, eps, 0, m, x);
+  } else {
+    hipLaunchKernelGGL((rms_norm_vec_kernel<16, true>), dim3(grid), dim3(kThreads), 0, s, x, w,
+                       out, (int)cols, eps, 0, m, x);
   }
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
@@ -1000,7 +1059,24 @@ int dnx_head_norm_rope(float* x, int64_t x_stride, const float* w, const float* 
   if (n == 0) return DNX_OK;
   hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)heads, (unsigned)n), dim3(64), 0,
                      (hipStream_t)stream, x, (int)x_stride, w, rope, (int)rope_stride, (int)hd,
-                     eps);
+                     eps, (int)heads, x, (int)x_stride, w);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_head_norm_rope2(float* x0, int64_t x0_stride, const float* w0, int64_t heads0,
+                        float* x1, int64_t x1_stride, const float* w1, int64_t heads1,
+                        const float* rope, int64_t rope_stride, int64_t hd, int64_t n, float eps,
+                        dnx_stream_t stream) {
+  if (heads0 <= 0 || heads1 <= 0 || n < 0 || hd <= 0 || hd % 2 != 0 || hd > 512 ||
+      x0_stride < heads0 * hd || x1_stride < heads1 * hd || rope_stride < hd ||
+      x0_stride > 0x7fffffff || x1_stride > 0x7fffffff || rope_stride > 0x7fffffff ||
+      heads0 + heads1 > 65535 || n > 65535) {
+    return DNX_EINVAL;
+  }
+  if (n == 0) return DNX_OK;
+  hipLaunchKernelGGL(head_norm_rope_kernel, dim3((unsigned)(heads0 + heads1), (unsigned)n),
+                     dim3(64), 0, (hipStream_t)stream, x0, (int)x0_stride, w0, rope,
+                     (int)rope_stride, (int)hd, eps, (int)heads0, x1, (int)x1_stride, w1);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 

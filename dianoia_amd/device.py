@@ -296,6 +296,18 @@ def head_norm_rope(x, x_stride: int, w, rope, rope_stride: int, heads: int, hd: 
            "dnx_head_norm_rope")
 
 
+def head_norm_rope2(x0, x0_stride: int, w0, heads0: int, x1, x1_stride: int, w1, heads1: int,
+                    rope, rope_stride: int, hd: int, n: int, eps: float, stream=None) -> None:
+    _check(_lib.load().dnx_head_norm_rope2(_ptr(x0), x0_stride, _ptr(w0), heads0, _ptr(x1),
+                                           x1_stride, _ptr(w1), heads1, _ptr(rope), rope_stride,
+                                           hd, n, eps, _stream(stream)), "dnx_head_norm_rope2")
+
+
+def add_rms_norm(m, x, w, out, rows: int, cols: int, eps: float, stream=None) -> None:
+    _check(_lib.load().dnx_add_rms_norm(_ptr(m), _ptr(x), _ptr(w), _ptr(out), rows, cols, eps,
+                                        _stream(stream)), "dnx_add_rms_norm")
+
+
 def short_conv(bcx, weight, history, y, width: int, k: int, n: int, stream=None) -> None:
     _check(_lib.load().dnx_short_conv(_ptr(bcx), _ptr(weight), _ptr(history), _ptr(y), width, k,
                                       n, _stream(stream)), "dnx_short_conv")

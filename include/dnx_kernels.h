@@ -311,6 +311,20 @@ int dnx_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64
 int dnx_head_norm_rope(float* x, int64_t x_stride, const float* w, const float* rope,
                        int64_t rope_stride, int64_t heads, int64_t hd, int64_t n, float eps,
                        dnx_stream_t stream);
+// Two dnx_head_norm_rope calls that share the rope table, hd, n and eps (a
+// decode step's q and k, gpu.dart:1162-1163) in one launch; the two operands
+// must not overlap. Bit-identical to the two calls.
+int dnx_head_norm_rope2(float* x0, int64_t x0_stride, const float* w0, int64_t heads0,
+                        float* x1, int64_t x1_stride, const float* w1, int64_t heads1,
+                        const float* rope, int64_t rope_stride, int64_t hd, int64_t n, float eps,
+                        dnx_stream_t stream);
+// dnx_add(m, x, rows * cols) then dnx_rms_norm(x, w, out, rows, cols, eps, 0)
+// in one launch (the residual add and the next norm of GpuForward.forward,
+// gpu.dart:1180-1187): bit-identical to the pair. rows <= 256, cols a
+// multiple of 4 up to 16384, 16-byte aligned operands, out not overlapping
+// x or m (DNX_EINVAL otherwise, nothing launched).
+int dnx_add_rms_norm(const float* m, float* x, const float* w, float* out, int64_t rows,
+                     int64_t cols, float eps, dnx_stream_t stream);
 // The gated short convolution over n tokens (lab_metal.m:383-412): bcx rows
 // [B | C | X] of `width` each, weight [width][k] (k <= 16), history
 // [k - 1][width] (oldest first, updated), y [n][width].

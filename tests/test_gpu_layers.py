@@ -240,3 +240,56 @@ def test_layer_steps_through_the_abi(gpu_ready, orc):
         assert lib.lab_gpu_commit(1) == 0
     finally:
         B.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 2048), (3, 6144), (256, 1024), (1, 4), (2, 16384)])
+def test_add_rms_norm_fused(gpu_ready, orc, rows, cols):
+    """The residual add and the following norm in one launch: x and out bit
+    for bit what dnx_add then dnx_rms_norm leave, and out within the norm's
+    bar of the oracle."""
+    rng = np.random.default_rng(rows * 7 + cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    m = rng.standard_normal((rows, cols)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    x1, out1 = dev(x), torch.empty((rows, cols), device="cuda")
+    D.add(dev(m), x1, rows * cols)
+    D.rms_norm(x1, dev(w), out1, rows, cols, 1e-6)
+    x2, out2 = dev(x), torch.empty((rows, cols), device="cuda")
+    D.add_rms_norm(dev(m), x2, dev(w), out2, rows, cols, 1e-6)
+    assert np.array_equal(bits(host(x2)), bits(host(x1)))
+    assert np.array_equal(bits(host(out2)), bits(host(out1)))
+    ok, err = close(host(out2), orc.rms_norm(x + m, w, 1e-6))
+    assert ok, err
+
+
+def test_add_rms_norm_rejects(gpu_ready):
+    z = torch.zeros(1 << 16, device="cuda")
+    with pytest.raises(RuntimeError):
+        D.add_rms_norm(z, z[4096:], z, z[8192:], 257, 8, 1e-6)   # more rows than it holds in registers
+    with pytest.raises(RuntimeError):
+        D.add_rms_norm(z, z[4096:], z, z[8192:], 1, 6, 1e-6)     # cols not a multiple of 4
+    with pytest.raises(RuntimeError):
+        D.add_rms_norm(z, z[4097:], z, z[8192:], 1, 8, 1e-6)     # x not 16-byte aligned
+
+
+@pytest.mark.parametrize("h0,h1,hd,n", [(16, 8, 128, 1), (32, 8, 64, 3), (2, 1, 256, 2)])
+def test_head_norm_rope_pair(gpu_ready, h0, h1, hd, n):
+    """q and k heads in one launch: bit-identical to the two calls."""
+    rng = np.random.default_rng(h0 * hd + n)
+    s0, s1 = h0 * hd + 32, h1 * hd
+    q = rng.standard_normal((n, s0)).astype(np.float32)
+    k = rng.standard_normal((n, s1)).astype(np.float32)
+    w0 = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    w1 = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    pair = hd // 2
+    ang = rng.uniform(0, 6.3, (n, pair))
+    rs = hd + 16
+    table = np.zeros((n, rs), np.float32)
+    table[:, :pair], table[:, pair:hd] = np.cos(ang), np.sin(ang)
+    qa, ka = dev(q), dev(k)
+    D.head_norm_rope(qa, s0, dev(w0), dev(table), rs, h0, hd, n, 1e-6)
+    D.head_norm_rope(ka, s1, dev(w1), dev(table), rs, h1, hd, n, 1e-6)
+    qb, kb = dev(q), dev(k)
+    D.head_norm_rope2(qb, s0, dev(w0), h0, kb, s1, dev(w1), h1, dev(table), rs, hd, n, 1e-6)
+    assert np.array_equal(bits(host(qb)), bits(host(qa)))
+    assert np.array_equal(bits(host(kb)), bits(host(ka)))
