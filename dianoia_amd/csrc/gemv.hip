@@ -236,26 +236,30 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
   // Rows of tokens t >= n are never stored, so their LDS is left as is.
   // A batch is PQ = 8 quads per thread: quad q0 + j T + tid for j < 8, so for
   // each j the 8 lanes of an aligned group hold one 32-value block.
+  // The n rows are one flat array of n * cols / 4 quads (x is [n][cols] and
+  // the LDS copies are [NT][...] in the same order, and a block never
+  // straddles two rows), so the first batch covers up to 2048 quads of all
+  // tokens: at n = 4 the tokens no longer wait for each other's loads.
   constexpr int PQ = 8;
-  const int quads = cols / 4;
+  const int quads = n * (cols / 4);
   float4 v[PQ];
-  auto load_x = [&](const int t, const int q0) {
-    const i32x4 rx = buffer_rsrc(p.x + (size_t)t * cols, (uint32_t)cols * 4);
+  const i32x4 rx = buffer_rsrc(p.x, (uint32_t)(n * cols) * 4);
+  auto load_x = [&](const int q0) {
 #pragma unroll
     for (int j = 0; j < PQ; j++) {
-      const int q = q0 + j * T + tid;  // past the row: zeros, unused
+      const int q = q0 + j * T + tid;  // past the rows: zeros, unused
       v[j] = buffer_load_f4(rx, q * 16);
     }
   };
   int pk = 0, pc = 0;  // position of the next chunk group to request
-  auto quantize_x = [&](const int t, const int q0) {
+  auto quantize_x = [&](const int q0) {
     if (kF) {
 #pragma unroll
       for (int j = 0; j < PQ; j++) {
         const int q = q0 + j * T + tid;
         if (q >= quads) break;
-        // quad q is k = q % 8 of block q / 8, l = 0..3
-        float* d = sxf + (t * B + (q >> 3)) * 32 + (q & 7);
+        // quad q is k = q % 8 of (flat) block q / 8, l = 0..3
+        float* d = sxf + (q >> 3) * 32 + (q & 7);
         d[0] = v[j].x;
         d[8] = v[j].y;
         d[16] = v[j].z;
@@ -278,7 +282,7 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
     const float inv_k = q8_inv(scale);
     {
       const int q = q0 + k * T + (tid & ~7);  // first quad of lane k's block
-      if (q < quads) sxs[t * B + (q >> 3)] = scale;
+      if (q < quads) sxs[q >> 3] = scale;
     }
     static_assert(PQ == 8, "one division per lane of an 8-lane group");
     const float inv[PQ] = {bcast8<0>(inv_k), bcast8<1>(inv_k), bcast8<2>(inv_k),
@@ -288,20 +292,19 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
     for (int j = 0; j < PQ; j++) {
       const int q = q0 + j * T + tid;
       if (q >= quads) break;  // whole 8-lane groups: quads is a multiple of 8
-      const int c = q * 4;
       const int packed = quant4(v[j], inv[j]);
-      *(int*)(sxq + t * cols + c) = packed;
+      *(int*)(sxq + q * 4) = packed;
       if (kQ4) {
         // -8 * (sum of the x bytes meeting lane l's low and high nibbles):
         // quads l and l + 4 of the block, so the nibbles enter sdot as 0..15.
         const int jq = q & 7;  // quad within the block
         const int s = sdot4(packed, 0x01010101, 0);
         const int other = dpp<kRowShl4>(s);  // lane + 4: quad jq + 4 of the block
-        if (jq < 4) sxsum[(t * B + (q >> 3)) * 4 + jq] = -8 * (s + other);
+        if (jq < 4) sxsum[(q >> 3) * 4 + jq] = -8 * (s + other);
       }
     }
   };
-  load_x(0, 0);
+  load_x(0);
   // Slots past the wave's last tile are not requested (a uniform branch:
   // such requests would read nothing and only cost their instructions).
 #pragma unroll
@@ -314,12 +317,10 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
   // scheduling barrier keeps every weight request ahead of the first wait
   // for x (the scheduler would otherwise start the block maxima in between).
   __builtin_amdgcn_sched_barrier(0);
-  quantize_x(0, 0);
-  for (int t = 0; t < n; t++) {
-    for (int q0 = t == 0 ? T * PQ : 0; q0 < quads; q0 += T * PQ) {
-      load_x(t, q0);
-      quantize_x(t, q0);
-    }
+  quantize_x(0);
+  for (int q0 = T * PQ; q0 < quads; q0 += T * PQ) {
+    load_x(q0);
+    quantize_x(q0);
   }
   __syncthreads();  // the only workgroup barrier: x is ready
 
