@@ -41,6 +41,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <thread>
 #include <utility>
 #include <vector>
 
@@ -827,6 +828,61 @@ bool run(const Cmd& c) {
   return false;
 }
 
+// Host (pageable, e.g. a mapped cache file) -> HBM for lab_gpu_wrap. Large
+// regions go in kWrapChunk pieces through kWrapBuffers pinned staging
+// buffers: kWrapThreads host threads copy a piece (and take its page faults)
+// while the DMA engine moves the pieces before it, on a stream of its own
+// (default priority). Small regions, or no staging memory, take one
+// hipMemcpy. Returns when the data is in HBM.
+constexpr size_t kWrapChunk = (size_t)8 << 20;
+constexpr int kWrapBuffers = 4;
+constexpr int kWrapThreads = 8;
+void* gWrapStage[kWrapBuffers] = {};
+hipEvent_t gWrapDone[kWrapBuffers];
+hipStream_t gWrapStream;
+bool gWrapReady = false, gWrapFailed = false;
+
+void parallel_copy(void* dst, const void* src, size_t bytes) {
+  const size_t part = ((bytes + kWrapThreads - 1) / kWrapThreads + 4095) & ~(size_t)4095;
+  std::thread pool[kWrapThreads - 1];
+  int started = 0;
+  for (int t = 1; t < kWrapThreads; t++) {
+    const size_t off = (size_t)t * part;
+    if (off >= bytes) break;
+    const size_t n = std::min(part, bytes - off);
+    pool[started++] = std::thread([=] { memcpy((char*)dst + off, (const char*)src + off, n); });
+  }
+  memcpy(dst, src, std::min(part, bytes));
+  for (int t = 0; t < started; t++) pool[t].join();
+}
+
+bool wrap_copy(void* dev, const void* src, size_t bytes) {
+  if (bytes >= 2 * kWrapChunk && !gWrapReady && !gWrapFailed) {
+    bool ok = hipStreamCreateWithFlags(&gWrapStream, hipStreamNonBlocking) == hipSuccess;
+    for (int b = 0; ok && b < kWrapBuffers; b++) {
+      ok = hipHostMalloc(&gWrapStage[b], kWrapChunk, hipHostMallocDefault) == hipSuccess &&
+           hipEventCreate(&gWrapDone[b]) == hipSuccess;
+    }
+    gWrapReady = ok;
+    gWrapFailed = !ok;
+  }
+  if (bytes < 2 * kWrapChunk || !gWrapReady) {
+    return hipMemcpy(dev, src, bytes, hipMemcpyHostToDevice) == hipSuccess;
+  }
+  bool ok = true;
+  size_t i = 0;
+  for (size_t off = 0; ok && off < bytes; off += kWrapChunk, i++) {
+    const int b = (int)(i % kWrapBuffers);
+    if (i >= kWrapBuffers) ok = hipEventSynchronize(gWrapDone[b]) == hipSuccess;
+    const size_t n = std::min(kWrapChunk, bytes - off);
+    if (ok) parallel_copy(gWrapStage[b], (const char*)src + off, n);
+    ok = ok && hipMemcpyAsync((char*)dev + off, gWrapStage[b], n, hipMemcpyHostToDevice,
+                              gWrapStream) == hipSuccess &&
+         hipEventRecord(gWrapDone[b], gWrapStream) == hipSuccess;
+  }
+  return hipStreamSynchronize(gWrapStream) == hipSuccess && ok;
+}
+
 }  // namespace
 
 extern "C" {
@@ -895,7 +951,7 @@ int64_t lab_gpu_wrap(void* address, int64_t bytes) {
   if (address == nullptr) return -1;
   const int64_t h = create(bytes, false);
   if (h < 0) return -1;
-  if (hipMemcpy(gBuffers[h].dev, address, (size_t)bytes, hipMemcpyHostToDevice) != hipSuccess) {
+  if (!wrap_copy(gBuffers[h].dev, address, (size_t)bytes)) {
     lab_gpu_release(h);
     return -1;
   }

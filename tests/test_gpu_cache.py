@@ -96,3 +96,24 @@ def test_a_matrix_larger_than_the_limit_is_refused(gpu_ready, cache):
             g.wrap_cache(c, limit=8192)
     finally:
         g.dispose()
+
+
+@pytest.mark.parametrize("nbytes", [(40 << 20) + 12345, (16 << 20), (3 << 20) + 7])
+def test_wrap_copies_every_byte(gpu_ready, nbytes):
+    """lab_gpu_wrap of a pageable region (large ones go through the pinned
+    staging pieces): the HBM copy, read back through lab_gpu_contents, holds
+    every byte."""
+    import ctypes
+    from dianoia_amd import _lib
+    lib = _lib.load()
+    assert lib.lab_gpu_init() == 1
+    src = np.random.default_rng(nbytes % 1000).integers(0, 256, size=nbytes, dtype=np.uint8)
+    h = lib.lab_gpu_wrap(src.ctypes.data, nbytes)
+    assert h >= 0
+    try:
+        view = lib.lab_gpu_contents(h)
+        assert view
+        back = np.ctypeslib.as_array((ctypes.c_uint8 * nbytes).from_address(view))
+        assert np.array_equal(back, src)
+    finally:
+        lib.lab_gpu_release(h)
