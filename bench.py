@@ -767,11 +767,11 @@ def traffic_from_profiles():
 PMC_COPY_BYTES = 1 << 30  # the calibration copy: reads and writes this many bytes
 kArgmaxWordsBytes = 32 * 8  # the finisher reads 32 rank words
 PMC_KERNELS = {  # kernel-name fragment -> (workload, algorithmic bytes per launch)
-    "gemv_kernel<1, 2, 1, true, false, false>": (
+    "gemv_kernel<1, 2, 1, true, false, false, 4, false>": (
         "c1 gate+up Q4 pair, 6144x2048", 2 * q4_bytes(6144, 2048) + 2048 * 4 + 6144 * 4),
-    "gemv_kernel<1, 1, 1, false, false, false>": (
+    "gemv_kernel<1, 1, 1, false, false, false, 8, false>": (
         "c1 down Q4, 2048x6144", q4_bytes(2048, 6144) + 6144 * 4 + 2048 * 4),
-    "gemv_kernel<2, 8, 1, false, true, false>": (
+    "gemv_kernel<2, 8, 1, false, true, false, 4, false>": (
         "c2 LM head Q8 (fp16 scales) + argmax, 151936x2048",
         q8_bytes(151936, 2048) + 2048 * 4 + 151936 * 4),
     "argmax_finish_kernel": ("c2 argmax finisher", kArgmaxWordsBytes + 8),
