@@ -92,6 +92,12 @@ SIGNATURES = {
     "dnx_copy_regions": ([_p, _p, _p, _i32, _p], _i32),
     "dnx_gemv_multi_q4": ([_p, _p, _p, _p, _i32, _p, _i64, _p], _i32),
     "dnx_gemv_multi_q8h": ([_p, _p, _p, _p, _i32, _p, _i64, _p], _i32),
+    "dnx_gemv_add_q8": ([_p, _p, _p, _p, _p, _i64, _i64, _p], _i32),
+    "dnx_gemv_add_q4": ([_p, _p, _p, _p, _p, _i64, _i64, _p], _i32),
+    "dnx_gate_up_norm_q8": ([_p, _p, _p, _p, _p, _p, _p, _f32, _p, _p, _i64, _i64, _p], _i32),
+    "dnx_gate_up_norm_q4": ([_p, _p, _p, _p, _p, _p, _p, _f32, _p, _p, _i64, _i64, _p], _i32),
+    "dnx_gemv_multi_norm_q8": ([_p, _p, _p, _p, _i32, _p, _p, _p, _f32, _i64, _p], _i32),
+    "dnx_gemv_multi_norm_q4": ([_p, _p, _p, _p, _i32, _p, _p, _p, _f32, _i64, _p], _i32),
     "dnx_gemm_q8": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_q8_float": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_q4_float": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),

@@ -57,6 +57,16 @@ DNX_DEV float bcast8(float v) {
   return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x18 | (J << 5)));
 }
 
+// Sum over a wave by an xor butterfly (offsets 32, 16, ..., 1). Each step
+// adds the same two values on both partner lanes, so every lane ends with
+// the same bits. The RMSNorm kernels and the GEMV's fused norm share it, so
+// their row sums round alike.
+DNX_DEV float wave_sum_xor(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
 // Min over the 8 lanes of an aligned lane group; every lane gets it.
 DNX_DEV int group8_min(int m) {
   m = min(m, dpp<kQuadXor1>(m));

@@ -93,6 +93,15 @@ struct GemvParams {
   const void* seg_qs[4];
   const void* seg_scales[4];
   float* seg_y[4];
+  // Residual add (plain launches, n = 1): when not null, each output is also
+  // added into resid[row] (resid[row] + y[row], one rounding, as add_kernel).
+  float* resid;
+  // Fused RMSNorm of x (gemv_norm_kernel, n = 1): the launch quantizes
+  // norm_w * (x * r) instead of x, and workgroup 0 writes it to norm_out.
+  const float* norm_w;
+  float* norm_out;
+  float norm_eps;
+  int norm_lds;                // LDS byte offset of workgroup 0's staged copy
 };
 constexpr int kMaxSegs = 4;
 
@@ -123,8 +132,10 @@ DNX_DEV float silu_mul(float g, float u) {
   return s * u;
 }
 
-template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, int W, bool kSeg>
-__global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
+// The kernel body; kNorm: RMSNorm of x fused into the prologue (n = 1,
+// 4 waves, one batch of quads; the launch checks these).
+template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, int W, bool kSeg, bool kNorm>
+__device__ __forceinline__ void gemv_body(const GemvParams p) {
   // kF: float inputs (lab_gemm_q8 / lab_gemm_q4 mode 0): x is not quantized;
   // per block, lane l sums fma(float(w_j), x_j, s) over j = 4k + l, k = 0..7
   // in order (dot_q8_f32 lab_native.c:489-501, dot_q4_f32 :1013-1023), and
@@ -243,14 +254,30 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
   constexpr int PQ = 8;
   const int quads = n * (cols / 4);
   float4 v[PQ];
+  float4 nw[kNorm ? PQ : 1];  // kNorm: the norm weights of the same quads
   const i32x4 rx = buffer_rsrc(p.x, (uint32_t)(n * cols) * 4);
+  const i32x4 rnw = buffer_rsrc(kNorm ? p.norm_w : p.x, (uint32_t)cols * 4);
   auto load_x = [&](const int q0) {
 #pragma unroll
     for (int j = 0; j < PQ; j++) {
       const int q = q0 + j * T + tid;  // past the rows: zeros, unused
       v[j] = buffer_load_f4(rx, q * 16);
+      if constexpr (kNorm) nw[j] = buffer_load_f4(rnw, q * 16);
     }
   };
+  // Residual add (plain one-token launches): this lane's deferred result is
+  // chain group j of the wave's tile k (lane = k * R + j, the order the loop
+  // records results in), so its x[row] is requested now, first of all, and
+  // left raw until the end.
+  constexpr bool kResid = !kPair && !kArgmax && !kSeg && !kF && !kNorm && NT == 1;
+  int resid_bits = 0;
+  if (kResid && p.resid != nullptr) {
+    const int k = lane / R, j = lane - (lane / R) * R;
+    const int row = (tile0 + k * stride) * R + j;
+    const bool ok = k < my_tiles && row < p.rows;
+    const i32x4 rr = buffer_rsrc(p.resid, (uint32_t)p.rows * 4);
+    resid_bits = dnx_raw_buffer_load_i32(rr, (int)(ok ? (uint32_t)row * 4 : kDead), 0, 0);
+  }
   int pk = 0, pc = 0;  // position of the next chunk group to request
   auto quantize_x = [&](const int q0) {
     if (kF) {
@@ -317,6 +344,38 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
   // scheduling barrier keeps every weight request ahead of the first wait
   // for x (the scheduler would otherwise start the block maxima in between).
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kNorm) {
+    // RMSNorm of the one row (rms_norm_vec_kernel's values): thread t holds
+    // quads t + 256 j, as there; its sum of squares in that order (quads
+    // past the row are zeros and add +0), the wave butterfly, then the four
+    // waves in order; r = 1 / sqrt(sum / cols + eps); a = w * (x * r).
+    __shared__ float nred[4];
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PQ; j++) {
+      sum += v[j].x * v[j].x;
+      sum += v[j].y * v[j].y;
+      sum += v[j].z * v[j].z;
+      sum += v[j].w * v[j].w;
+    }
+    sum = wave_sum_xor(sum);
+    if (lane == 0) nred[wave] = sum;
+    __syncthreads();
+    float total = nred[0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) total += nred[w];
+    const float r = 1.0f / sqrtf(total / (float)cols + p.norm_eps);
+    float4* staged = (float4*)(lds + p.norm_lds);  // workgroup 0's copy of a
+#pragma unroll
+    for (int j = 0; j < PQ; j++) {
+      v[j].x = nw[j].x * (v[j].x * r);
+      v[j].y = nw[j].y * (v[j].y * r);
+      v[j].z = nw[j].z * (v[j].z * r);
+      v[j].w = nw[j].w * (v[j].w * r);
+      const int q = j * T + tid;
+      if (blockIdx.x == 0 && q < quads) staged[q] = v[j];
+    }
+  }
   quantize_x(0);
   for (int q0 = T * PQ; q0 < quads; q0 += T * PQ) {
     load_x(q0);
@@ -565,6 +624,22 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
     }
   }
   if (outp != nullptr) *outp = outv;
+  if (kResid && p.resid != nullptr && outp != nullptr) {
+    float* rp = p.resid + (outp - p.y);  // n = 1: the same row of x
+    *rp = __int_as_float(resid_bits) + outv;
+  }
+  if constexpr (kNorm) {
+    // The normed row to its own buffer (each thread its staged quads; the
+    // stores wait until here so that none queues among the weight loads).
+    if (blockIdx.x == 0) {
+      const float4* staged = (const float4*)(lds + p.norm_lds);
+#pragma unroll
+      for (int j = 0; j < PQ; j++) {
+        const int q = j * T + tid;
+        if (q < quads) ((float4*)p.norm_out)[q] = staged[q];
+      }
+    }
+  }
 
   if (kArgmax) {
     // The workgroup's best rank into its group word (the finisher reads it).
@@ -580,6 +655,19 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
       }
     }
   }
+}
+
+template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, int W, bool kSeg>
+__global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
+  gemv_body<F, R, NT, kPair, kArgmax, kF, W, kSeg, false>(p);
+}
+
+// One token whose x is first normed (the standalone RMSNorm's values: the
+// same partition of the row over 256 threads and the same reduction), then
+// quantized and multiplied: a gate/up pair or a segmented launch.
+template <int F, int R, bool kPair, bool kSeg>
+__global__ void __launch_bounds__(256) gemv_norm_kernel(GemvParams p) {
+  gemv_body<F, R, 1, kPair, false, false, 4, kSeg, true>(p);
 }
 
 // The fused argmax's last step: the best of the first `slots` workspace
@@ -651,20 +739,31 @@ size_t lds_budget(int W) { return W >= 8 ? kLdsAlone : kLdsShared; }
 // Ring slots per wave (the kernel's Q) for RR rows per tile.
 int ring_units(int RR) { return RR >= 8 ? RR : RR >= 2 ? 16 : 8; }
 
-template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, int W, bool kSeg = false>
+template <int F, int R, int NT, bool kPair, bool kArgmax, bool kF, int W, bool kSeg = false,
+          bool kNorm = false>
 int launch(GemvParams& p, hipStream_t stream) {
   constexpr bool kQ4 = F == kFmtQ4;
   constexpr int CB = kQ4 ? 64 : 32, RR = R * (kPair ? 2 : 1);
+  static_assert(!kNorm || (NT == 1 && W == 4 && !kArgmax && !kF), "the fused norm's shape");
   const int B = p.cols / kBlock, chunks = (B + CB - 1) / CB;
   const size_t budget = lds_budget(W);
+  // The fused norm stages workgroup 0's normed row past everything else.
+  const size_t extra = kNorm ? (size_t)p.cols * 4 : 0;
   // Full-K tiles when the whole tile fits the ring (small tiles, where the
   // chain per chunk would otherwise serialize with each chunk's latency).
   p.full = RR * chunks <= ring_units(RR) &&
-           lds_for(kQ4, kF, R, NT, kPair, p.cols, chunks * CB + kChainPad, W) <= budget;
+           lds_for(kQ4, kF, R, NT, kPair, p.cols, chunks * CB + kChainPad, W) + extra <= budget;
   p.stride = (p.full ? chunks * CB : CB) + kChainPad;
-  const size_t lds = lds_for(kQ4, kF, R, NT, kPair, p.cols, p.stride, W);
+  const size_t lds0 = lds_for(kQ4, kF, R, NT, kPair, p.cols, p.stride, W);
+  const size_t lds = lds0 + extra;
   if (lds > budget) return DNX_EINVAL;  // x too wide for one workgroup's LDS
-  auto kernel = gemv_kernel<F, R, NT, kPair, kArgmax, kF, W, kSeg>;
+  p.norm_lds = (int)lds0;  // a multiple of 16 (cols is a multiple of 32)
+  void (*kernel)(GemvParams);
+  if constexpr (kNorm) {
+    kernel = gemv_norm_kernel<F, R, kPair, kSeg>;
+  } else {
+    kernel = gemv_kernel<F, R, NT, kPair, kArgmax, kF, W, kSeg>;
+  }
   // Persistent grid: as many workgroups as stay resident (the occupancy is
   // looked up once per kernel and LDS size).
   static int cached_per_cu = 0;
@@ -726,13 +825,13 @@ int launch(GemvParams& p, hipStream_t stream) {
 // quantize x): measured graph-timed, 3072 x 1024 Q8 4.41 -> 4.13 us with
 // 4-row tiles, 2048 x 2048 Q4 4.64 -> 4.32 us with 2-row tiles.
 constexpr int kMinTiles = 2048, kMinTilesShortX = 768;
-int pick_rows(bool q4, bool fx, int rows, int nt, bool pair, int cols) {
+int pick_rows(bool q4, bool fx, int rows, int nt, bool pair, int cols, size_t extra = 0) {
   int r = 8;  // 8 rows keep two chunk groups in the ring (measured faster than 16)
   while (r * nt * (pair ? 2 : 1) * 4 > 64) r /= 2;
   const int min_tiles = pair || cols >= kWideCols ? kMinTiles : kMinTilesShortX;
   while (r > 1 && (rows + r - 1) / r < min_tiles) r /= 2;
-  while (r > 1 &&
-         lds_for(q4, fx, r, nt, pair, cols, (q4 ? 64 : 32) + kChainPad, 4) > kLdsShared) {
+  while (r > 1 && lds_for(q4, fx, r, nt, pair, cols, (q4 ? 64 : 32) + kChainPad, 4) + extra >
+                      kLdsShared) {
     r /= 2;
   }
   return r;
@@ -766,6 +865,42 @@ int launch_seg(GemvParams& p, int R, int W, hipStream_t stream) {
   }
 }
 
+// A fused-norm launch (one token, 4 waves): a gate/up pair or a segmented
+// launch, R rows per tile.
+template <int F, bool kPair, bool kSeg>
+int launch_norm(GemvParams& p, int R, hipStream_t stream) {
+  switch (R) {
+    case 8: return launch<F, 8, 1, kPair, false, false, 4, kSeg, true>(p, stream);
+    case 4: return launch<F, 4, 1, kPair, false, false, 4, kSeg, true>(p, stream);
+    case 2: return launch<F, 2, 1, kPair, false, false, 4, kSeg, true>(p, stream);
+    case 1: return launch<F, 1, 1, kPair, false, false, 4, kSeg, true>(p, stream);
+  }
+  return DNX_EINVAL;
+}
+
+// The fused norm's operands: RMSNorm(x) * w (one row) goes to out, and the
+// launch multiplies it.
+struct NormArgs {
+  const float* w;
+  float* out;
+  float eps;
+};
+
+// Shapes the fused norm takes: one row of cols % 4 == 0 held by 256 threads
+// in one batch of 8 quads each (cols <= 8192), 16-byte aligned operands (the
+// alignment under which dnx_rms_norm itself runs the register-row kernel
+// whose values the fusion reproduces), out disjoint from x.
+bool disjoint(const void* a, int64_t abytes, const void* b, int64_t bbytes) {
+  const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+  return a0 + (uintptr_t)abytes <= b0 || b0 + (uintptr_t)bbytes <= a0;
+}
+
+bool norm_ok(const float* x, const NormArgs& nm, int64_t cols) {
+  if (cols <= 0 || cols % 4 != 0 || cols > 4 * 256 * 8) return false;
+  if ((((uintptr_t)x | (uintptr_t)nm.w | (uintptr_t)nm.out) & 15) != 0) return false;
+  return disjoint(x, cols * 4, nm.out, cols * 4) && disjoint(nm.w, cols * 4, nm.out, cols * 4);
+}
+
 template <int F, int NT, bool kPair, bool kArgmax, bool kF>
 int launch_nt(GemvParams& p, int R, int W, hipStream_t stream) {
   constexpr int RR_MAX = 16 / (NT * (kPair ? 2 : 1));
@@ -788,8 +923,13 @@ int launch_nt(GemvParams& p, int R, int W, hipStream_t stream) {
 template <int F, bool kPair, bool kArgmax, bool kF = false>
 int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, const float* x,
          float* y, float* y2, int64_t rows, int64_t cols, int64_t n, unsigned long long* ws,
-         int64_t* out, hipStream_t stream) {
+         int64_t* out, hipStream_t stream, float* resid = nullptr,
+         const NormArgs* norm = nullptr) {
   if (rows <= 0 || cols <= 0 || n <= 0 || n > 4 || cols % kBlock != 0) return DNX_EINVAL;
+  if (resid != nullptr && (kPair || kArgmax || kF || n != 1 || ((uintptr_t)resid & 3))) {
+    return DNX_EINVAL;
+  }
+  if (norm != nullptr && (!kPair || kF || n != 1 || !norm_ok(x, *norm, cols))) return DNX_EINVAL;
   if (rows > (1 << 30) || cols > (1 << 20)) return DNX_EINVAL;
   if (((uintptr_t)qs0 & 15) || (kPair && ((uintptr_t)qs1 & 15))) return DNX_EINVAL;
   constexpr bool kQ4 = F == kFmtQ4;
@@ -804,6 +944,7 @@ int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, con
   const int64_t srow = (cols / kBlock) * (F != kFmtQ8 ? 2 : 4);
   const int64_t range = kMaxLaunchBytes / qrow;
   const int nt = n == 1 ? 1 : n == 2 ? 2 : 4;
+  if (norm != nullptr && rows > range) return DNX_EINVAL;  // one launch writes the norm
   int slots = 0;
   for (int64_t r0 = 0; r0 < rows; r0 += range) {
     const int64_t nr = rows - r0 < range ? rows - r0 : range;
@@ -821,9 +962,23 @@ int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, con
     p.cols = (int)cols;
     p.n = (int)n;
     p.ws = ws;
+    p.resid = resid != nullptr ? resid + r0 : nullptr;
+    int rc;
+    if (norm != nullptr) {
+      if constexpr (kPair && !kArgmax && !kF) {
+        p.norm_w = norm->w;
+        p.norm_out = norm->out;
+        p.norm_eps = norm->eps;
+        const int R = pick_rows(kQ4, false, (int)nr, 1, true, (int)cols, (size_t)cols * 4);
+        rc = launch_norm<F, true, false>(p, R, stream);
+      } else {
+        rc = DNX_EINVAL;
+      }
+      if (rc != DNX_OK) return rc;
+      continue;
+    }
     const int R = pick_rows(kQ4, kF, (int)nr, nt, kPair, (int)cols);
     const int W = pick_waves(kQ4, kF, (int)nr, R, nt, kPair, (int)cols);
-    int rc;
     if (kArgmax) {
       rc = launch_nt<F, 1, false, true, false>(p, R, W, stream);
       slots = p.grid > slots ? p.grid : slots;
@@ -850,10 +1005,12 @@ int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, con
 // one gemv per matrix.
 template <int F>
 int gemv_multi(const void* const* qs, const void* const* scales, float* const* y,
-               const int64_t* rows, int segs, const float* x, int64_t cols, hipStream_t stream) {
+               const int64_t* rows, int segs, const float* x, int64_t cols, hipStream_t stream,
+               const NormArgs* norm = nullptr) {
   if (segs < 1 || segs > kMaxSegs || cols <= 0 || cols % kBlock != 0 || cols > (1 << 20)) {
     return DNX_EINVAL;
   }
+  if (norm != nullptr && !norm_ok(x, *norm, cols)) return DNX_EINVAL;
   if (qs == nullptr || scales == nullptr || y == nullptr || rows == nullptr) return DNX_EINVAL;
   if ((uintptr_t)x & 3) return DNX_EINVAL;
   constexpr bool kQ4 = F == kFmtQ4;
@@ -887,6 +1044,13 @@ int gemv_multi(const void* const* qs, const void* const* scales, float* const* y
   p.ldy = (int)total;
   p.cols = (int)cols;
   p.n = 1;
+  if (norm != nullptr) {
+    p.norm_w = norm->w;
+    p.norm_out = norm->out;
+    p.norm_eps = norm->eps;
+    const int R = pick_rows(kQ4, false, (int)total, 1, false, (int)cols, (size_t)cols * 4);
+    return launch_norm<F, false, true>(p, R, stream);
+  }
   const int R = pick_rows(kQ4, false, (int)total, 1, false, (int)cols);
   const int W = pick_waves(kQ4, false, (int)total, R, 1, false, (int)cols);
   return launch_seg<F>(p, R, W, stream);
@@ -1010,6 +1174,61 @@ int dnx_gemv_multi_q8h(const int8_t* const* qs, const uint16_t* const* scales, f
                        hipStream_t stream) {
   return gemv_multi<kFmtQ8H>((const void* const*)qs, (const void* const*)scales, y, rows, segs,
                              x, cols, stream);
+}
+
+int dnx_gemv_add_q8(const int8_t* qs, const float* scales, const float* x, float* y,
+                    float* resid, int64_t rows, int64_t cols, hipStream_t stream) {
+  if (resid == nullptr || !disjoint(resid, rows * 4, x, cols * 4) ||
+      !disjoint(resid, rows * 4, y, rows * 4)) {
+    return DNX_EINVAL;
+  }
+  return gemv<kFmtQ8, false, false>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, 1,
+                                   nullptr, nullptr, stream, resid);
+}
+
+int dnx_gemv_add_q4(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
+                    float* resid, int64_t rows, int64_t cols, hipStream_t stream) {
+  if (resid == nullptr || !disjoint(resid, rows * 4, x, cols * 4) ||
+      !disjoint(resid, rows * 4, y, rows * 4)) {
+    return DNX_EINVAL;
+  }
+  return gemv<kFmtQ4, false, false>(qs, scales, nullptr, nullptr, x, y, nullptr, rows, cols, 1,
+                                  nullptr, nullptr, stream, resid);
+}
+
+int dnx_gate_up_norm_q8(const int8_t* gate_qs, const float* gate_scales, const int8_t* up_qs,
+                        const float* up_scales, const float* x, const float* norm_w,
+                        float* norm_out, float eps, float* h, float* u, int64_t rows,
+                        int64_t cols, hipStream_t stream) {
+  const NormArgs nm{norm_w, norm_out, eps};
+  return gemv<kFmtQ8, true, false>(gate_qs, gate_scales, up_qs, up_scales, x, h, u, rows, cols, 1,
+                                  nullptr, nullptr, stream, nullptr, &nm);
+}
+
+int dnx_gate_up_norm_q4(const uint8_t* gate_qs, const uint16_t* gate_scales, const uint8_t* up_qs,
+                        const uint16_t* up_scales, const float* x, const float* norm_w,
+                        float* norm_out, float eps, float* h, float* u, int64_t rows,
+                        int64_t cols, hipStream_t stream) {
+  const NormArgs nm{norm_w, norm_out, eps};
+  return gemv<kFmtQ4, true, false>(gate_qs, gate_scales, up_qs, up_scales, x, h, u, rows, cols, 1,
+                                 nullptr, nullptr, stream, nullptr, &nm);
+}
+
+int dnx_gemv_multi_norm_q8(const int8_t* const* qs, const float* const* scales, float* const* y,
+                           const int64_t* rows, int segs, const float* x, const float* norm_w,
+                           float* norm_out, float eps, int64_t cols, hipStream_t stream) {
+  const NormArgs nm{norm_w, norm_out, eps};
+  return gemv_multi<kFmtQ8>((const void* const*)qs, (const void* const*)scales, y, rows, segs,
+                            x, cols, stream, &nm);
+}
+
+int dnx_gemv_multi_norm_q4(const uint8_t* const* qs, const uint16_t* const* scales,
+                           float* const* y, const int64_t* rows, int segs, const float* x,
+                           const float* norm_w, float* norm_out, float eps, int64_t cols,
+                           hipStream_t stream) {
+  const NormArgs nm{norm_w, norm_out, eps};
+  return gemv_multi<kFmtQ4>((const void* const*)qs, (const void* const*)scales, y, rows, segs,
+                            x, cols, stream, &nm);
 }
 
 }  // extern "C"

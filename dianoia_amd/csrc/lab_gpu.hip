@@ -484,7 +484,9 @@ bool overlaps(int64_t h0, int64_t o0, int64_t b0, int64_t h1, int64_t o1, int64_
   return h0 == h1 && o0 < o1 + b1 && o1 < o0 + b0;
 }
 
-size_t fusable_multi(const std::vector<Cmd>& cmds, size_t i) {
+// The number of commands from i on that one segmented launch can run (1 when
+// only cmds[i] qualifies, 0 when it does not).
+size_t multi_len(const std::vector<Cmd>& cmds, size_t i) {
   const Cmd& a = cmds[i];
   if (!(a.op == kOpMatmulQ8 || a.op == kOpMatmulQ4) || !a.int8_inputs || a.a[9] != 1) return 0;
   const int64_t x = a.a[3], xOff = a.a[4], cols = a.a[8];
@@ -503,6 +505,11 @@ size_t fusable_multi(const std::vector<Cmd>& cmds, size_t i) {
     }
     if (clash) break;
   }
+  return len;
+}
+
+size_t fusable_multi(const std::vector<Cmd>& cmds, size_t i) {
+  const size_t len = multi_len(cmds, i);
   return len >= 2 ? len : 0;
 }
 
@@ -535,6 +542,156 @@ int run_multi(const std::vector<Cmd>& cmds, size_t i, size_t len) {
   if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
   for (size_t k = 0; k < len; k++) wrote_region(cmds[i + k].a[5], cmds[i + k].a[6], rows[k] * 4);
   if (rc != DNX_OK) LOG("%zu fused matmuls of width %ld failed (%d)\n", len, (long)cols, rc);
+  return rc;
+}
+
+// Fusion of a one-token matmul and the residual add of its output into x
+// (GpuForward adds each block's output into x, gpu.dart:1180-1187): the
+// GEMV's epilogue also adds each output into its row of x (dnx_gemv_add_*),
+// when the add reads exactly the matmul's output and x overlaps neither the
+// matmul's input (which every workgroup reads first), its output nor its
+// weights.
+bool fusable_matmul_add(const Cmd& a, const Cmd& b) {
+  if (!(a.op == kOpMatmulQ8 || a.op == kOpMatmulQ4) || !a.int8_inputs || a.a[9] != 1 ||
+      b.op != kOpAdd) {
+    return false;
+  }
+  const int64_t rows = a.a[7], cols = a.a[8];
+  const int64_t m = b.a[0], mOff = b.a[1], x = b.a[2], xOff = b.a[3], count = b.a[4];
+  if (m != a.a[5] || mOff != a.a[6] || count != rows) return false;
+  return x != a.a[0] && !overlaps(x, xOff, rows * 4, a.a[3], a.a[4], cols * 4) &&
+         !overlaps(x, xOff, rows * 4, m, mOff, rows * 4);
+}
+
+// DNX_OK, or the launcher's code; DNX_EINVAL means nothing was launched.
+int run_matmul_add(const Cmd& a, const Cmd& b) {
+  const bool q4 = a.op == kOpMatmulQ4;
+  const int64_t w = a.a[0], x = a.a[3], xOff = a.a[4], y = a.a[5], yOff = a.a[6];
+  const int64_t rows = a.a[7], cols = a.a[8], res = b.a[2], resOff = b.a[3];
+  use_as_weights(w);
+  read_region(x, xOff, cols * 4);
+  read_region(res, resOff, rows * 4);
+  const float* xs = (const float*)dev_at(x, xOff);
+  float* ys = (float*)dev_at(y, yOff);
+  float* rs = (float*)dev_at(res, resOff);
+  const int rc =
+      q4 ? dnx_gemv_add_q4((const uint8_t*)dev_at(w, a.a[1]), (const uint16_t*)dev_at(w, a.a[2]),
+                           xs, ys, rs, rows, cols, gStream)
+         : dnx_gemv_add_q8((const int8_t*)dev_at(w, a.a[1]), (const float*)dev_at(w, a.a[2]), xs,
+                           ys, rs, rows, cols, gStream);
+  if (rc == DNX_EINVAL) return rc;
+  if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+  wrote_region(y, yOff, rows * 4);
+  wrote_region(res, resOff, rows * 4);
+  if (rc != DNX_OK) LOG("matmul + add %ldx%ld failed (%d)\n", (long)rows, (long)cols, rc);
+  return rc;
+}
+
+// Fusion of the RMSNorm of one row with the one-token matmuls that read its
+// output (GpuForward norms x before each block, gpu.dart:1145-1156 and
+// :1180-1185): the GEMV norms x in its prologue with the standalone kernel's
+// values, quantizes the result and writes it to the norm's output
+// (dnx_gate_up_norm_* for an MLP's gate/up pair and glue,
+// dnx_gemv_multi_norm_* for one to four projections). The norm must not
+// accumulate, its output must not overlap its input or weight and must be
+// exactly the matmuls' input, and no matmul output may overlap the norm's
+// input, weight or output (the prologue reads the first two in every
+// workgroup; workgroup 0 writes the third at its end). Returns the number of
+// commands after the norm that the launch covers (3 for a pair and its glue),
+// or 0.
+bool clear_of_norm(const Cmd& nrm, int64_t h, int64_t off, int64_t bytes) {
+  const int64_t nb = nrm.a[7] * 4;
+  return !overlaps(h, off, bytes, nrm.a[0], nrm.a[1], nb) &&
+         !overlaps(h, off, bytes, nrm.a[2], nrm.a[3], nb) &&
+         !overlaps(h, off, bytes, nrm.a[4], nrm.a[5], nb);
+}
+
+size_t fusable_norm_matmul(const std::vector<Cmd>& cmds, size_t i, bool& pair) {
+  const Cmd& nrm = cmds[i];
+  if (nrm.op != kOpRmsNorm || nrm.a[9] != 0 || nrm.a[6] != 1 || i + 1 >= cmds.size()) return 0;
+  const int64_t nb = nrm.a[7] * 4;
+  if (overlaps(nrm.a[4], nrm.a[5], nb, nrm.a[0], nrm.a[1], nb) ||
+      overlaps(nrm.a[4], nrm.a[5], nb, nrm.a[2], nrm.a[3], nb)) {
+    return 0;
+  }
+  const Cmd& a = cmds[i + 1];
+  if (a.a[3] != nrm.a[4] || a.a[4] != nrm.a[5] || a.a[8] != nrm.a[7]) return 0;
+  if (i + 3 < cmds.size() && fusable_pair(a, cmds[i + 2], cmds[i + 3])) {
+    const int64_t rb = a.a[7] * 4;
+    if (a.a[9] != 1 || !clear_of_norm(nrm, a.a[5], 0, rb) ||
+        !clear_of_norm(nrm, cmds[i + 2].a[5], 0, rb)) {
+      return 0;
+    }
+    pair = true;
+    return 3;
+  }
+  const size_t len = multi_len(cmds, i + 1);
+  for (size_t k = 0; k < len; k++) {
+    const Cmd& c = cmds[i + 1 + k];
+    if (!clear_of_norm(nrm, c.a[5], c.a[6], c.a[7] * 4)) return 0;
+  }
+  pair = false;
+  return len;
+}
+
+// DNX_OK, or the launcher's code; DNX_EINVAL means nothing was launched (the
+// caller then runs the norm alone and goes on with the commands after it).
+int run_norm_matmul(const std::vector<Cmd>& cmds, size_t i, size_t len, bool pair) {
+  const Cmd& nrm = cmds[i];
+  const int64_t x = nrm.a[0], xOff = nrm.a[1], w = nrm.a[2], wOff = nrm.a[3];
+  const int64_t out = nrm.a[4], outOff = nrm.a[5], cols = nrm.a[7];
+  const float eps = (float)__builtin_bit_cast(double, nrm.a[8]);
+  const Cmd& a = cmds[i + 1];
+  const bool q4 = a.op == kOpMatmulQ4;
+  read_region(x, xOff, cols * 4);
+  read_region(w, wOff, cols * 4);
+  const float* xs = (const float*)dev_at(x, xOff);
+  const float* ws = (const float*)dev_at(w, wOff);
+  float* os = (float*)dev_at(out, outOff);
+  int rc;
+  if (pair) {
+    const Cmd& b = cmds[i + 2];
+    const int64_t rows = a.a[7];
+    use_as_weights(a.a[0]);
+    use_as_weights(b.a[0]);
+    const void* gq = dev_at(a.a[0], a.a[1]);
+    const void* gs = dev_at(a.a[0], a.a[2]);
+    const void* uq = dev_at(b.a[0], b.a[1]);
+    const void* us = dev_at(b.a[0], b.a[2]);
+    float* h = (float*)dev_at(a.a[5], 0);
+    float* u = (float*)dev_at(b.a[5], 0);
+    rc = q4 ? dnx_gate_up_norm_q4((const uint8_t*)gq, (const uint16_t*)gs, (const uint8_t*)uq,
+                                  (const uint16_t*)us, xs, ws, os, eps, h, u, rows, cols, gStream)
+            : dnx_gate_up_norm_q8((const int8_t*)gq, (const float*)gs, (const int8_t*)uq,
+                                  (const float*)us, xs, ws, os, eps, h, u, rows, cols, gStream);
+    if (rc == DNX_EINVAL) return rc;
+    wrote_region(a.a[5], 0, rows * 4);
+    wrote_region(b.a[5], 0, rows * 4);
+  } else {
+    const void* qs[4];
+    const void* sc[4];
+    float* ys[4];
+    int64_t rows[4];
+    for (size_t k = 0; k < len; k++) {
+      const Cmd& c = cmds[i + 1 + k];
+      use_as_weights(c.a[0]);
+      qs[k] = dev_at(c.a[0], c.a[1]);
+      sc[k] = dev_at(c.a[0], c.a[2]);
+      ys[k] = (float*)dev_at(c.a[5], c.a[6]);
+      rows[k] = c.a[7];
+    }
+    rc = q4 ? dnx_gemv_multi_norm_q4((const uint8_t* const*)qs, (const uint16_t* const*)sc, ys,
+                                     rows, (int)len, xs, ws, os, eps, cols, gStream)
+            : dnx_gemv_multi_norm_q8((const int8_t* const*)qs, (const float* const*)sc, ys, rows,
+                                     (int)len, xs, ws, os, eps, cols, gStream);
+    if (rc == DNX_EINVAL) return rc;
+    for (size_t k = 0; k < len; k++) {
+      wrote_region(cmds[i + 1 + k].a[5], cmds[i + 1 + k].a[6], rows[k] * 4);
+    }
+  }
+  if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+  wrote_region(out, outOff, cols * 4);
+  if (rc != DNX_OK) LOG("rms_norm + %zu matmuls of width %ld failed (%d)\n", len, (long)cols, rc);
   return rc;
 }
 
@@ -1015,6 +1172,7 @@ int64_t lab_gpu_commit(int64_t wait) {
   bool ok = !gFailed;
   (void)hipEventRecord(gStart, gStream);
   for (size_t i = 0; i < gCmds.size(); i++) {
+    bool pair = false;
     if (i + 2 < gCmds.size() && fusable_pair(gCmds[i], gCmds[i + 1], gCmds[i + 2])) {
       const int rc = run_pair(gCmds[i], gCmds[i + 1]);
       if (rc == DNX_EINVAL) {  // not launched: the two matmuls and the glue as recorded
@@ -1028,6 +1186,22 @@ int64_t lab_gpu_commit(int64_t wait) {
     } else if (i + 1 < gCmds.size() && fusable_argmax(gCmds[i], gCmds[i + 1])) {
       ok = run_matmul_argmax(gCmds[i], gCmds[i + 1]) && ok;
       i += 1;
+    } else if (size_t len = fusable_norm_matmul(gCmds, i, pair)) {
+      const int rc = run_norm_matmul(gCmds, i, len, pair);
+      if (rc == DNX_EINVAL) {  // not launched: the norm alone, then what follows it
+        ok = run(gCmds[i]) && ok;
+      } else {
+        ok = rc == DNX_OK && ok;
+        i += len;
+      }
+    } else if (i + 1 < gCmds.size() && fusable_matmul_add(gCmds[i], gCmds[i + 1])) {
+      const int rc = run_matmul_add(gCmds[i], gCmds[i + 1]);
+      if (rc == DNX_EINVAL) {  // not launched: the matmul alone, then the add
+        ok = run(gCmds[i]) && ok;
+      } else {
+        ok = rc == DNX_OK && ok;
+        i += 1;
+      }
     } else if (i + 1 < gCmds.size() && fusable_add_norm(gCmds[i], gCmds[i + 1])) {
       const int rc = run_add_norm(gCmds[i], gCmds[i + 1]);
       if (rc == DNX_EINVAL) {

@@ -24,11 +24,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
-DNX_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
+DNX_DEV float wave_sum(float v) { return wave_sum_xor(v); }
 
 DNX_DEV float wave_max(float v) {
 #pragma unroll

@@ -180,6 +180,38 @@ def gemv_multi(fmt: str, mats, x, ys, cols: int, stream=None) -> None:
                                       segs, _ptr(x), cols, _stream(stream)), name)
 
 
+def gemv_add(fmt: str, qs, scales, x, y, resid, rows: int, cols: int, stream=None) -> None:
+    """One-token GEMV whose epilogue also adds y into resid (fmt "q8" or "q4")."""
+    name = {"q8": "dnx_gemv_add_q8", "q4": "dnx_gemv_add_q4"}[fmt]
+    _check(getattr(_lib.load(), name)(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), _ptr(resid), rows,
+                                      cols, _stream(stream)), name)
+
+
+def gate_up_norm(fmt: str, gq, gs, uq, us, x, norm_w, norm_out, eps: float, h, u, rows: int,
+                 cols: int, stream=None) -> None:
+    """The gate/up pair and glue on RMSNorm(x) * norm_w, which also goes to norm_out."""
+    name = {"q8": "dnx_gate_up_norm_q8", "q4": "dnx_gate_up_norm_q4"}[fmt]
+    _check(getattr(_lib.load(), name)(_ptr(gq), _ptr(gs), _ptr(uq), _ptr(us), _ptr(x), _ptr(norm_w),
+                                      _ptr(norm_out), eps, _ptr(h), _ptr(u), rows, cols,
+                                      _stream(stream)), name)
+
+
+def gemv_multi_norm(fmt: str, mats, x, norm_w, norm_out, eps: float, ys, cols: int,
+                    stream=None) -> None:
+    """gemv_multi on RMSNorm(x) * norm_w, which also goes to norm_out."""
+    segs = len(mats)
+    P = ctypes.c_void_p * max(segs, 1)
+    qs = P(*[_ptr(m[0]) for m in mats])
+    sc = P(*[_ptr(m[1]) for m in mats])
+    yp = P(*[_ptr(y) for y in ys])
+    rows = (ctypes.c_int64 * max(segs, 1))(*[int(m[2]) for m in mats])
+    name = {"q8": "dnx_gemv_multi_norm_q8", "q4": "dnx_gemv_multi_norm_q4"}[fmt]
+    _check(getattr(_lib.load(), name)(ctypes.cast(qs, ctypes.c_void_p), ctypes.cast(sc, ctypes.c_void_p),
+                                      ctypes.cast(yp, ctypes.c_void_p), ctypes.cast(rows, ctypes.c_void_p),
+                                      segs, _ptr(x), _ptr(norm_w), _ptr(norm_out), eps, cols,
+                                      _stream(stream)), name)
+
+
 def gemm_q8_float(qs, scales, x, y, rows: int, cols: int, n: int, stream=None) -> None:
     """Float-input (mode 0) GEMM on bf16 MFMA, within fp32 rounding of the CPU."""
     _check(_lib.load().dnx_gemm_q8_float(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,

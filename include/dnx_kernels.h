@@ -148,6 +148,41 @@ int dnx_gemv_multi_q8h(const int8_t* const* qs, const uint16_t* const* scales, f
                        const int64_t* rows, int segs, const float* x, int64_t cols,
                        dnx_stream_t stream);
 
+// One-token GEMV with the residual add of its output in the epilogue
+// (GpuForward adds each block's output into x, gpu.dart:1180-1187): y is
+// dnx_gemv_*'s output and then resid[r] = resid[r] + y[r] (the bits of
+// dnx_add(y, resid, rows) after the GEMV). resid must not overlap x or y
+// (DNX_EINVAL, nothing launched).
+int dnx_gemv_add_q8(const int8_t* qs, const float* scales, const float* x, float* y,
+                    float* resid, int64_t rows, int64_t cols, dnx_stream_t stream);
+int dnx_gemv_add_q4(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
+                    float* resid, int64_t rows, int64_t cols, dnx_stream_t stream);
+
+// One-token GEMVs over the RMSNorm of x (GpuForward norms x before each
+// block, gpu.dart:1145-1156, :1180-1185): norm_out = dnx_rms_norm(x, norm_w,
+// eps) of the one row, bit for bit, and the products are those of the GEMVs
+// on norm_out: the gate/up pair and glue of dnx_gate_up_* (h, u), or the
+// segmented launch of dnx_gemv_multi_* (y[i]). Every workgroup norms x in its
+// prologue; workgroup 0 writes norm_out at its end. cols % 32 == 0 and
+// cols <= 8192; x, norm_w and norm_out 16-byte aligned; norm_out disjoint
+// from x and norm_w (DNX_EINVAL otherwise, nothing launched). The outputs
+// must not overlap x, norm_w or norm_out.
+int dnx_gate_up_norm_q8(const int8_t* gate_qs, const float* gate_scales, const int8_t* up_qs,
+                        const float* up_scales, const float* x, const float* norm_w,
+                        float* norm_out, float eps, float* h, float* u, int64_t rows,
+                        int64_t cols, dnx_stream_t stream);
+int dnx_gate_up_norm_q4(const uint8_t* gate_qs, const uint16_t* gate_scales, const uint8_t* up_qs,
+                        const uint16_t* up_scales, const float* x, const float* norm_w,
+                        float* norm_out, float eps, float* h, float* u, int64_t rows,
+                        int64_t cols, dnx_stream_t stream);
+int dnx_gemv_multi_norm_q8(const int8_t* const* qs, const float* const* scales, float* const* y,
+                           const int64_t* rows, int segs, const float* x, const float* norm_w,
+                           float* norm_out, float eps, int64_t cols, dnx_stream_t stream);
+int dnx_gemv_multi_norm_q4(const uint8_t* const* qs, const uint16_t* const* scales,
+                           float* const* y, const int64_t* rows, int segs, const float* x,
+                           const float* norm_w, float* norm_out, float eps, int64_t cols,
+                           dnx_stream_t stream);
+
 // Float-input GEMM (lab_gemm_q8 / lab_gemm_q4 mode 0 for many tokens,
 // lab_native.c:489-501, :1013-1023; the reference's float GPU GEMMs,
 // lab_metal.m:79-144, :174-258) on bf16 MFMA: x (fp32 [n][cols]) split
