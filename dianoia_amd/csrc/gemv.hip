@@ -929,7 +929,7 @@ int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, con
   if (resid != nullptr && (kPair || kArgmax || kF || n != 1 || ((uintptr_t)resid & 3))) {
     return DNX_EINVAL;
   }
-  if (norm != nullptr && (!kPair || kF || n != 1 || !norm_ok(x, *norm, cols))) return DNX_EINVAL;
+  if (norm != nullptr && (kArgmax || kF || n != 1 || !norm_ok(x, *norm, cols))) return DNX_EINVAL;
   if (rows > (1 << 30) || cols > (1 << 20)) return DNX_EINVAL;
   if (((uintptr_t)qs0 & 15) || (kPair && ((uintptr_t)qs1 & 15))) return DNX_EINVAL;
   constexpr bool kQ4 = F == kFmtQ4;
@@ -965,12 +965,12 @@ int gemv(const void* qs0, const void* sc0, const void* qs1, const void* sc1, con
     p.resid = resid != nullptr ? resid + r0 : nullptr;
     int rc;
     if (norm != nullptr) {
-      if constexpr (kPair && !kArgmax && !kF) {
+      if constexpr (!kArgmax && !kF) {
         p.norm_w = norm->w;
         p.norm_out = norm->out;
         p.norm_eps = norm->eps;
-        const int R = pick_rows(kQ4, false, (int)nr, 1, true, (int)cols, (size_t)cols * 4);
-        rc = launch_norm<F, true, false>(p, R, stream);
+        const int R = pick_rows(kQ4, false, (int)nr, 1, kPair, (int)cols, (size_t)cols * 4);
+        rc = launch_norm<F, kPair, false>(p, R, stream);
       } else {
         rc = DNX_EINVAL;
       }
@@ -1012,6 +1012,11 @@ int gemv_multi(const void* const* qs, const void* const* scales, float* const* y
   }
   if (norm != nullptr && !norm_ok(x, *norm, cols)) return DNX_EINVAL;
   if (qs == nullptr || scales == nullptr || y == nullptr || rows == nullptr) return DNX_EINVAL;
+  if (norm != nullptr && segs == 1) {
+    // One matrix: the plain launch (no per-request segment selects).
+    return gemv<F, false, false>(qs[0], scales[0], nullptr, nullptr, x, y[0], nullptr, rows[0],
+                                 cols, 1, nullptr, nullptr, stream, nullptr, norm);
+  }
   if ((uintptr_t)x & 3) return DNX_EINVAL;
   constexpr bool kQ4 = F == kFmtQ4;
   const int64_t qrow = kQ4 ? cols / 2 : cols;

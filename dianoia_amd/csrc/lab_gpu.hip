@@ -606,6 +606,8 @@ bool clear_of_norm(const Cmd& nrm, int64_t h, int64_t off, int64_t bytes) {
          !overlaps(h, off, bytes, nrm.a[4], nrm.a[5], nb);
 }
 
+bool fusable_argmax(const Cmd& a, const Cmd& b);
+
 size_t fusable_norm_matmul(const std::vector<Cmd>& cmds, size_t i, bool& pair) {
   const Cmd& nrm = cmds[i];
   if (nrm.op != kOpRmsNorm || nrm.a[9] != 0 || nrm.a[6] != 1 || i + 1 >= cmds.size()) return 0;
@@ -626,6 +628,9 @@ size_t fusable_norm_matmul(const std::vector<Cmd>& cmds, size_t i, bool& pair) {
     return 3;
   }
   const size_t len = multi_len(cmds, i + 1);
+  // A matmul whose output an argmax reads keeps its own fusion (the LM head
+  // and the token, gpu.dart:1222-1236): the norm then runs alone.
+  if (len == 1 && i + 2 < cmds.size() && fusable_argmax(a, cmds[i + 2])) return 0;
   for (size_t k = 0; k < len; k++) {
     const Cmd& c = cmds[i + 1 + k];
     if (!clear_of_norm(nrm, c.a[5], c.a[6], c.a[7] * 4)) return 0;

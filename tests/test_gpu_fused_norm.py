@@ -102,7 +102,8 @@ def test_gate_up_norm_matches_norm_then_pair(gpu_ready, orc, fmt, rows, cols, sp
 
 
 @pytest.mark.parametrize("fmt,rows,cols", [("q4", (2048, 1024, 1024), 2048), ("q8", (4096,), 1024),
-                                           ("q4", (64, 96, 32, 128), 256), ("q8", (3, 5), 8192)])
+                                           ("q4", (64, 96, 32, 128), 256), ("q8", (3, 5), 8192),
+                                           ("q8", (50000,), 2048), ("q4", (7,), 64)])
 def test_multi_norm_matches_norm_then_multi(gpu_ready, orc, fmt, rows, cols):
     rng = np.random.default_rng(sum(rows) + cols)
     mats = [weights(fmt, rng, r, cols) for r in rows]
