@@ -26,6 +26,30 @@ constexpr int kWaves = kThreads / 64;
 
 DNX_DEV float wave_sum(float v) { return wave_sum_xor(v); }
 
+// Max and sum over a wave without an LDS round trip: DPP inside each row of
+// 16 lanes (quad xor 1, xor 2, half-row and row mirrors: every lane of a row
+// ends with the row's result), then the four rows' results read into
+// scalars and combined in a fixed order. Every lane gets the same bits. All
+// lanes must be active.
+DNX_DEV float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+DNX_DEV float wave_max_dpp(float v) {
+  v = fmaxf(v, dppf<kQuadXor1>(v));
+  v = fmaxf(v, dppf<kQuadXor2>(v));
+  v = fmaxf(v, dppf<kHalfRowMirror>(v));
+  v = fmaxf(v, dppf<kRowMirror>(v));
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)),
+               fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+DNX_DEV float wave_sum_dpp(float v) {
+  v += dppf<kQuadXor1>(v);
+  v += dppf<kQuadXor2>(v);
+  v += dppf<kHalfRowMirror>(v);
+  v += dppf<kRowMirror>(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
 DNX_DEV float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
@@ -366,13 +390,17 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ keys,
 // O = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M). The same softmax as
 // attention_kernel, summed in another order.
 // A split puts hd / 4 lanes on a key row (one 16-byte piece each,
-// coalesced), 256 / (hd / 4) keys per workgroup step, and at most 16 steps:
-// every key and value load of the split is issued at its start, so it
-// waits for memory once, and each row is read once for the G heads (GQA).
+// coalesced), 256 / (hd / 4) keys per workgroup step, and kSplitSteps
+// steps: every key and value load of the split is issued at its start, so
+// it waits for memory once, and each row is read once for the G heads
+// (GQA). Eight steps (64 keys at hd 128: 512 workgroups at 4096 positions
+// of 8 KV heads) read faster than 16 with half the workgroups (Qwen3-1.7B
+// at position 4095: 9.0 against 11.0 us; a pure read of the same bytes in
+// the two patterns: 7.2 against 8.1-9.5 us).
 // Dots end in a butterfly over the key's lanes; wave w takes the softmax
 // statistics of heads w, w + 4, ...; value sums go to per-lane float4
 // partials added in a fixed order.
-constexpr int kSplitSteps = 16;
+constexpr int kSplitSteps = 8;
 constexpr int kSplitMaxKeys = 256;
 
 int split_keys(int hd) {
@@ -397,7 +425,7 @@ DNX_DEV float group_sum(float v) {
 
 // G query heads per workgroup; LT lanes per key when fixed at compile time
 // (hd = 4 * LT), 0 for any hd.
-template <int G, int LT>
+template <int G, int LT, int STEPS = kSplitSteps>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
 attention_split_kernel(const float* __restrict__ q, const float* __restrict__ keys,
                        const float* __restrict__ values, float* __restrict__ ws, int position,
@@ -428,19 +456,19 @@ attention_split_kernel(const float* __restrict__ q, const float* __restrict__ ke
   const i32x4 krs = buffer_rsrc(keys + first, range);
   const i32x4 vrs = buffer_rsrc(values + first, range);
   const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  float4 kv[kSplitSteps], vv[kSplitSteps];
+  float4 kv[STEPS], vv[STEPS];
 #pragma unroll
-  for (int j = 0; j < kSplitSteps; j++)
+  for (int j = 0; j < STEPS; j++)
     kv[j] = buffer_load_f4(krs, (kb + j * step) * kv_dim * 4 + 16 * c);
 #pragma unroll
-  for (int j = 0; j < kSplitSteps; j++)
+  for (int j = 0; j < STEPS; j++)
     vv[j] = buffer_load_f4(vrs, (kb + j * step) * kv_dim * 4 + 16 * c);
   // Dots in batches of kBatch steps x G heads: each butterfly stage issues
   // the batch's lane exchanges together and waits once (L is a run-time
   // count, so per-dot loops would wait on every exchange).
   constexpr int kBatch = 4;
 #pragma unroll
-  for (int j0 = 0; j0 < kSplitSteps; j0 += kBatch) {
+  for (int j0 = 0; j0 < STEPS; j0 += kBatch) {
     float d[kBatch][G];
 #pragma unroll
     for (int u = 0; u < kBatch; u++)
@@ -482,7 +510,7 @@ attention_split_kernel(const float* __restrict__ q, const float* __restrict__ ke
       v[u] = i < nk ? scores[g][i] : -INFINITY;
       mx = fmaxf(mx, v[u]);
     }
-    mx = wave_max(mx);
+    mx = wave_max_dpp(mx);
     float sum = 0.0f;
 #pragma unroll
     for (int u = 0; u < kPerLane; u++) {
@@ -493,7 +521,7 @@ attention_split_kernel(const float* __restrict__ q, const float* __restrict__ ke
         sum += e;
       }
     }
-    sum = wave_sum(sum);
+    sum = wave_sum_dpp(sum);
     if (lane == 0) {
       stat[g][0] = mx;   // -inf for a split past the token's keys (l = 0, o = 0)
       stat[g][1] = sum;
@@ -504,7 +532,7 @@ attention_split_kernel(const float* __restrict__ q, const float* __restrict__ ke
 #pragma unroll
   for (int g = 0; g < G; g++) acc[g] = zero;
 #pragma unroll
-  for (int j = 0; j < kSplitSteps; j++) {
+  for (int j = 0; j < STEPS; j++) {
     const int i = kb + j * step;
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -556,28 +584,10 @@ void launch_split(dim3 grid, hipStream_t stream, const float* q, const float* ke
 // short context waits for memory once; the rescaling factors e^(m_s - M)
 // go through LDS (dynamic: `splits` floats), and the P partial sums of a
 // dimension are added in a fixed order.
-__global__ void __launch_bounds__(kThreads)
-attention_combine_kernel(const float* __restrict__ ws, const float* __restrict__ gate,
-                         float* __restrict__ out, int heads, int hd, int splits) {
-  extern __shared__ float fs[];   // [splits] e^(m_s - M), 0 for empty splits
-  __shared__ float scratch[kWaves];
-  __shared__ float red[kThreads];
-  constexpr int kChunk = 16;
-  const int head = blockIdx.x, token = blockIdx.y, tid = threadIdx.x;
-  const int row = hd + 4;
-  const float* w = ws + ((size_t)token * heads + head) * splits * row;
-  // Every offset past the (head, token)'s rows reads zero.
-  const i32x4 rs = buffer_rsrc(w, (uint32_t)splits * (uint32_t)row * 4u);
-  const int P = kThreads / hd, d = tid % hd, part = tid / hd;
-  float v[kChunk];
-#pragma unroll
-  for (int u = 0; u < kChunk; u++) {
-    const int sp = part + u * P;
-    v[u] = __int_as_float(dnx_raw_buffer_load_i32(rs, (sp * row + 4 + d) * 4, 0, 0));
-  }
-  const int s0 = tid;   // the first split whose statistics this thread reads
-  const float m0 = __int_as_float(dnx_raw_buffer_load_i32(rs, s0 * row * 4, 0, 0));
-  const float l0 = __int_as_float(dnx_raw_buffer_load_i32(rs, (s0 * row + 1) * 4, 0, 0));
+// More than 64 splits: each thread takes splits s0, s0 + 256, ...; the max
+// and l over the workgroup (the block reductions' barriers also publish fs).
+DNX_DEV float combine_stats(const float* w, int splits, int row, int s0, float m0, float l0,
+                            float* fs, float* scratch) {
   float mx = s0 < splits ? m0 : -INFINITY;
   for (int s = s0 + kThreads; s < splits; s += kThreads) mx = fmaxf(mx, w[(size_t)s * row]);
   mx = block_max(mx, scratch);
@@ -593,7 +603,49 @@ attention_combine_kernel(const float* __restrict__ ws, const float* __restrict__
     fs[s] = f;
     lp += w[(size_t)s * row + 1] * f;
   }
-  const float l = block_sum(lp, scratch);  // its barriers also publish fs
+  return block_sum(lp, scratch);
+}
+
+__global__ void __launch_bounds__(kThreads)
+attention_combine_kernel(const float* __restrict__ ws, const float* __restrict__ gate,
+                         float* __restrict__ out, int heads, int hd, int splits) {
+  extern __shared__ float fs[];   // [splits] e^(m_s - M), 0 for empty splits
+  __shared__ float scratch[kWaves];
+  __shared__ float red[kThreads];
+  constexpr int kChunk = 32;
+  const int head = blockIdx.x, token = blockIdx.y, tid = threadIdx.x;
+  const int row = hd + 4;
+  const float* w = ws + ((size_t)token * heads + head) * splits * row;
+  // Every offset past the (head, token)'s rows reads zero.
+  const i32x4 rs = buffer_rsrc(w, (uint32_t)splits * (uint32_t)row * 4u);
+  const int P = kThreads / hd, d = tid % hd, part = tid / hd;
+  float v[kChunk];
+#pragma unroll
+  for (int u = 0; u < kChunk; u++) {
+    const int sp = part + u * P;
+    v[u] = __int_as_float(dnx_raw_buffer_load_i32(rs, (sp * row + 4 + d) * 4, 0, 0));
+  }
+  const int s0 = tid;   // the first split whose statistics this thread reads
+  const float m0 = __int_as_float(dnx_raw_buffer_load_i32(rs, s0 * row * 4, 0, 0));
+  const float l0 = __int_as_float(dnx_raw_buffer_load_i32(rs, (s0 * row + 1) * 4, 0, 0));
+  float l;
+  if (splits <= 64) {
+    // One wave holds every split's statistics (lane s): the max, the
+    // factors and l without a block reduction; one barrier publishes them.
+    if (tid < 64) {
+      const bool live = s0 < splits;
+      const float m = live ? m0 : -INFINITY;
+      const float mx = wave_max_dpp(m);
+      const float f = live && m != -INFINITY ? expf(m - mx) : 0.0f;
+      if (live) fs[s0] = f;
+      const float lsum = wave_sum_dpp(live ? l0 * f : 0.0f);
+      if (tid == 0) scratch[0] = lsum;
+    }
+    __syncthreads();
+    l = scratch[0];
+  } else {
+    l = combine_stats(w, splits, row, s0, m0, l0, fs, scratch);
+  }
   float acc = 0.0f;
 #pragma unroll
   for (int u = 0; u < kChunk; u++) {
