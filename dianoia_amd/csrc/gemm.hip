@@ -524,12 +524,19 @@ int launch_tile(GemmParams p, hipStream_t stream) {
   const unsigned gx = (unsigned)((p.rows + BN - 1) / BN), gy = (unsigned)((p.n + BM - 1) / BM);
   const int stages = (p.cols / kBlock + KB - 1) / KB;
   // Split K when the tiles alone would leave CUs idle (small n): enough
-  // splits for about 512 workgroups, each with at least one stage.
+  // splits for about 512 workgroups, each with at least one stage. Between
+  // one and three workgroups per CU (the resident count of the 64 x 64
+  // tiles) a long K is split too, into runs of at least 8 stages, so that
+  // the slots fill: the vision fc2 (1152 x 4320 at 1024 tokens, 288 tiles)
+  // ran one or two workgroups per CU over all 34 stages.
   int splits = 1;
   const int64_t tiles = (int64_t)gx * gy;
   if (tiles < 256 && stages > 1) {
     splits = (int)((512 + tiles - 1) / tiles);
     if (splits > stages) splits = stages;
+  } else if (tiles < 768 && stages >= 16) {
+    splits = (int)((768 + tiles - 1) / tiles);
+    if (splits > stages / 8) splits = stages / 8;
   }
   p.split_stages = (stages + splits - 1) / splits;
   splits = (stages + p.split_stages - 1) / p.split_stages;
