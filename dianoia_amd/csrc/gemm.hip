@@ -526,15 +526,17 @@ int launch_tile(GemmParams p, hipStream_t stream) {
   // Split K when the tiles alone would leave CUs idle (small n): enough
   // splits for about 512 workgroups, each with at least one stage. Between
   // one and three workgroups per CU (the resident count of the 64 x 64
-  // tiles) a long K is split too, into runs of at least 8 stages, so that
-  // the slots fill: the vision fc2 (1152 x 4320 at 1024 tokens, 288 tiles)
-  // ran one or two workgroups per CU over all 34 stages.
+  // tiles) a long K (32+ stages) is split too, into runs of at least 8
+  // stages, so that the slots fill: the vision fc2 (1152 x 4320 at 1024
+  // tokens, 288 tiles) ran one or two workgroups per CU over all 34 stages
+  // (47.9 -> 42.6 us with 3 splits). A shorter K loses more to the partials'
+  // round trip than it gains (6144 x 2048 at 256 tokens: 24 -> 27 us).
   int splits = 1;
   const int64_t tiles = (int64_t)gx * gy;
   if (tiles < 256 && stages > 1) {
     splits = (int)((512 + tiles - 1) / tiles);
     if (splits > stages) splits = stages;
-  } else if (tiles < 768 && stages >= 16) {
+  } else if (tiles < 768 && stages >= 32) {
     splits = (int)((768 + tiles - 1) / tiles);
     if (splits > stages / 8) splits = stages / 8;
   }

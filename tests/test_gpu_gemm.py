@@ -99,7 +99,7 @@ def exact_products(orc, fmt, qs, sc, xq, xsc):
                                          (257, 2048, 1), (100, 2048, 64), (6144, 2048, 8),
                                          (6144, 2048, 32), (2048, 6144, 16), (6144, 2048, 64),
                                          (4304, 1152, 300), (1152, 4320, 200), (97, 160, 129),
-                                         (1152, 2048, 960)])
+                                         (1152, 4096, 960)])
 def test_gemm_within_tolerance(gpu_ready, orc, fmt, rows, cols, n, path):
     """Against the exact products: the reference kernels' own bar (error /
     sum|terms| < 1e-5, native_kernels_test.dart:56-59), met by the CPU kernels
