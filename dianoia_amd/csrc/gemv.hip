@@ -664,7 +664,8 @@ __global__ void __launch_bounds__(64 * W) gemv_kernel(GemvParams p) {
 
 // One token whose x is first normed (the standalone RMSNorm's values: the
 // same partition of the row over 256 threads and the same reduction), then
-// quantized and multiplied: a gate/up pair or a segmented launch.
+// quantized and multiplied: one matrix, a gate/up pair or a segmented
+// launch.
 template <int F, int R, bool kPair, bool kSeg>
 __global__ void __launch_bounds__(256) gemv_norm_kernel(GemvParams p) {
   gemv_body<F, R, 1, kPair, false, false, 4, kSeg, true>(p);
@@ -865,8 +866,8 @@ int launch_seg(GemvParams& p, int R, int W, hipStream_t stream) {
   }
 }
 
-// A fused-norm launch (one token, 4 waves): a gate/up pair or a segmented
-// launch, R rows per tile.
+// A fused-norm launch (one token, 4 waves): one matrix, a gate/up pair or a
+// segmented launch, R rows per tile.
 template <int F, bool kPair, bool kSeg>
 int launch_norm(GemvParams& p, int R, hipStream_t stream) {
   switch (R) {
