@@ -67,6 +67,29 @@ DNX_DEV float wave_sum_xor(float v) {
   return v;
 }
 
+// Element i of `splits` split-K partials (part[z][count], z in order):
+// part[0][i] + part[1][i] + ... added in split order (deterministic), with
+// the loads of 8 splits issued together (a loop that adds as it loads waits
+// for each partial in turn). Splits past the last reload the last one
+// (always in bounds) and are not added.
+DNX_DEV float split_sum(const float* __restrict__ part, int64_t count, int64_t i, int splits) {
+  constexpr int U = 8;
+  float v = 0.0f;
+  for (int z0 = 0; z0 < splits; z0 += U) {
+    float t[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int z = z0 + u < splits ? z0 + u : splits - 1;
+      t[u] = part[(size_t)z * count + i];
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      if (z0 + u < splits) v = z0 + u == 0 ? t[u] : v + t[u];
+    }
+  }
+  return v;
+}
+
 // Min over the 8 lanes of an aligned lane group; every lane gets it.
 DNX_DEV int group8_min(int m) {
   m = min(m, dpp<kQuadXor1>(m));

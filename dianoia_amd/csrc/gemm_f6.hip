@@ -703,9 +703,7 @@ __global__ void __launch_bounds__(256) f6_splitk_reduce_kernel(const float* __re
                                                                int64_t count, int splits) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count;
        i += (int64_t)gridDim.x * 256) {
-    float v = part[i];
-    for (int z = 1; z < splits; z++) v += part[(size_t)z * count + i];
-    y[i] = v;
+    y[i] = split_sum(part, count, i, splits);
   }
 }
 

@@ -270,9 +270,7 @@ __global__ void __launch_bounds__(kThreads) float_splitk_reduce_kernel(
     const float* __restrict__ part, float* __restrict__ y, int64_t count, int splits) {
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < count;
        i += (int64_t)gridDim.x * kThreads) {
-    float v = part[i];
-    for (int z = 1; z < splits; z++) v += part[(size_t)z * count + i];
-    y[i] = v;
+    y[i] = split_sum(part, count, i, splits);
   }
 }
 
