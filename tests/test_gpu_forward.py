@@ -76,6 +76,45 @@ def test_one_command_buffer_equals_one_per_command(gpu_ready, name):
         split.dispose()
 
 
+def test_decode_step_fuses_norms_and_adds(gpu_ready):
+    """A one-token step dispatches no standalone RMSNorm or residual add:
+    each RMSNorm runs in the prologue of the GEMV that reads it and each add
+    in the epilogue of the GEMV whose output it adds (the commit's fusions,
+    checked for their bits by the test above); the same step one command per
+    commit runs them all."""
+    import ctypes
+    from dianoia_amd import _lib
+    lib = _lib.load()
+    cfg = qwen3_small()
+    ms = (ctypes.c_double * 21)()
+
+    def profiled_step(fwd):
+        fwd.residual[:6 * cfg.hidden] = embeddings(cfg, 0, 6)
+        fwd.forward(6, 0)
+        lib.lab_gpu_profile(ms, (ctypes.c_int64 * 21)(), 21)  # clear the counts
+        lib.lab_gpu_set_profiling(1)
+        fwd.residual[:cfg.hidden] = embeddings(cfg, 6, 1)
+        fwd.forward(1, 6)
+        lib.lab_gpu_set_profiling(0)
+        counts = (ctypes.c_int64 * 21)()
+        assert lib.lab_gpu_profile(ms, counts, 21) == 21
+        return list(counts)
+
+    fused = F.GpuForward(cfg, max_seq=16, max_chunk=8, seed=3)
+    split = F.GpuForward(cfg, max_seq=16, max_chunk=8, seed=3)
+    split.split_commits = True
+    try:
+        a, b = profiled_step(fused), profiled_step(split)
+    finally:
+        fused.dispose()
+        split.dispose()
+    rms_norm, add, gemv_q8, gemv_q4 = 4, 17, 13, 14
+    layers = len(cfg.layer_types)
+    assert a[rms_norm] == 0 and a[add] == 0, a
+    assert a[gemv_q8] + a[gemv_q4] > 0, a
+    assert b[rms_norm] == 2 * layers + 1 and b[add] == 2 * layers, b
+
+
 class StageCheck:
     """checker for GpuForward.split_commits: each command against the oracle
     on the host views before it. Matmuls (n <= 4, exact GEMV) and the conv,
