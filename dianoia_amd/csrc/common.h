@@ -59,8 +59,7 @@ DNX_DEV float bcast8(float v) {
 
 // Sum over a wave by an xor butterfly (offsets 32, 16, ..., 1). Each step
 // adds the same two values on both partner lanes, so every lane ends with
-// the same bits. The RMSNorm kernels and the GEMV's fused norm share it, so
-// their row sums round alike.
+// the same bits.
 DNX_DEV float wave_sum_xor(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -88,6 +87,45 @@ DNX_DEV float split_sum(const float* __restrict__ part, int64_t count, int64_t i
     }
   }
   return v;
+}
+
+// Max and sum over a wave without an LDS round trip: DPP inside each row of
+// 16 lanes (quad xor 1, xor 2, half-row and row mirrors: every lane of a row
+// ends with the row's result), then the four rows' results read into
+// scalars and combined in a fixed order. Every lane gets the same bits. All
+// lanes must be active.
+DNX_DEV float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+DNX_DEV float wave_max_dpp(float v) {
+  v = fmaxf(v, dppf<kQuadXor1>(v));
+  v = fmaxf(v, dppf<kQuadXor2>(v));
+  v = fmaxf(v, dppf<kHalfRowMirror>(v));
+  v = fmaxf(v, dppf<kRowMirror>(v));
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)),
+               fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+DNX_DEV float wave_sum_dpp(float v) {
+  v += dppf<kQuadXor1>(v);
+  v += dppf<kQuadXor2>(v);
+  v += dppf<kHalfRowMirror>(v);
+  v += dppf<kRowMirror>(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
+// The row sum of a 256-thread RMSNorm (rms_norm_vec_kernel, and the GEMV
+// prologue that reproduces it): each wave's DPP sum, then the four wave
+// totals in wave order through `scratch` (4 floats). Every thread gets the
+// same bits.
+DNX_DEV float norm_row_sum(float v, float* scratch) {
+  v = wave_sum_dpp(v);
+  __syncthreads();  // scratch may still be read from a previous call
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = scratch[0];
+#pragma unroll
+  for (int w = 1; w < 4; w++) t += scratch[w];
+  return t;
 }
 
 // Min over the 8 lanes of an aligned lane group; every lane gets it.

@@ -346,19 +346,24 @@ __device__ __forceinline__ void gemv_body(const GemvParams p) {
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (kNorm) {
     // RMSNorm of the one row (rms_norm_vec_kernel's values): thread t holds
-    // quads t + 256 j, as there; its sum of squares in that order (quads
-    // past the row are zeros and add +0), the wave butterfly, then the four
-    // waves in order; r = 1 / sqrt(sum / cols + eps); a = w * (x * r).
+    // quads t + 256 j, as there; its sum of squares in that order over the
+    // batches that hold quads of the row (the rest are zeros, which would
+    // add +0), each wave's DPP sum, then the four waves in order (the
+    // arithmetic of norm_row_sum); r = 1 / sqrt(sum / cols + eps);
+    // a = w * (x * r).
     __shared__ float nred[4];
+    const int live_j = (quads + T - 1) / T;  // uniform
     float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < PQ; j++) {
-      sum += v[j].x * v[j].x;
-      sum += v[j].y * v[j].y;
-      sum += v[j].z * v[j].z;
-      sum += v[j].w * v[j].w;
+      if (j < live_j) {
+        sum += v[j].x * v[j].x;
+        sum += v[j].y * v[j].y;
+        sum += v[j].z * v[j].z;
+        sum += v[j].w * v[j].w;
+      }
     }
-    sum = wave_sum_xor(sum);
+    sum = wave_sum_dpp(sum);
     if (lane == 0) nred[wave] = sum;
     __syncthreads();
     float total = nred[0];
@@ -368,12 +373,14 @@ __device__ __forceinline__ void gemv_body(const GemvParams p) {
     float4* staged = (float4*)(lds + p.norm_lds);  // workgroup 0's copy of a
 #pragma unroll
     for (int j = 0; j < PQ; j++) {
-      v[j].x = nw[j].x * (v[j].x * r);
-      v[j].y = nw[j].y * (v[j].y * r);
-      v[j].z = nw[j].z * (v[j].z * r);
-      v[j].w = nw[j].w * (v[j].w * r);
-      const int q = j * T + tid;
-      if (blockIdx.x == 0 && q < quads) staged[q] = v[j];
+      if (j < live_j) {
+        v[j].x = nw[j].x * (v[j].x * r);
+        v[j].y = nw[j].y * (v[j].y * r);
+        v[j].z = nw[j].z * (v[j].z * r);
+        v[j].w = nw[j].w * (v[j].w * r);
+        const int q = j * T + tid;
+        if (blockIdx.x == 0 && q < quads) staged[q] = v[j];
+      }
     }
   }
   quantize_x(0);

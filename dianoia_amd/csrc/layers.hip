@@ -26,29 +26,6 @@ constexpr int kWaves = kThreads / 64;
 
 DNX_DEV float wave_sum(float v) { return wave_sum_xor(v); }
 
-// Max and sum over a wave without an LDS round trip: DPP inside each row of
-// 16 lanes (quad xor 1, xor 2, half-row and row mirrors: every lane of a row
-// ends with the row's result), then the four rows' results read into
-// scalars and combined in a fixed order. Every lane gets the same bits. All
-// lanes must be active.
-DNX_DEV float lane_value(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-DNX_DEV float wave_max_dpp(float v) {
-  v = fmaxf(v, dppf<kQuadXor1>(v));
-  v = fmaxf(v, dppf<kQuadXor2>(v));
-  v = fmaxf(v, dppf<kHalfRowMirror>(v));
-  v = fmaxf(v, dppf<kRowMirror>(v));
-  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)),
-               fmaxf(lane_value(v, 32), lane_value(v, 48)));
-}
-DNX_DEV float wave_sum_dpp(float v) {
-  v += dppf<kQuadXor1>(v);
-  v += dppf<kQuadXor2>(v);
-  v += dppf<kHalfRowMirror>(v);
-  v += dppf<kRowMirror>(v);
-  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
-}
 
 DNX_DEV float wave_max(float v) {
 #pragma unroll
@@ -149,7 +126,7 @@ rms_norm_vec_kernel(const float* x_in, const float* __restrict__ w, float* out, 
     sum += xv[e].z * xv[e].z;
     sum += xv[e].w * xv[e].w;
   }
-  sum = block_sum(sum, scratch);
+  sum = norm_row_sum(sum, scratch);
   const float r = 1.0f / sqrtf(sum / (float)cols + eps);
 #pragma unroll
   for (int e = 0; e < V; e++) {
