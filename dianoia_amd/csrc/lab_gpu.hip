@@ -774,6 +774,64 @@ int run_rope_pair(const Cmd& a, const Cmd& b) {
   return rc;
 }
 
+// Fusion of a decode token's q and k head norms + RoPE with its attention
+// (gpu.dart:1157-1175): the norm of q (offset 0, the attention's q), the
+// norm of the token's key row keys[position] with the same rope row, hd and
+// eps, then the one-token attention over them. dnx_attention_rope norms
+// both inside the split-key attention and leaves q, the key row and out as
+// the three dispatches would. out and gate must not share a buffer with q
+// or the keys, and the norm weights and rope table must not lie in q's or
+// the keys' buffers.
+bool fusable_rope_attention(const Cmd& a, const Cmd& b, const Cmd& c) {
+  if (a.op != kOpHeadNormRope || b.op != kOpHeadNormRope || c.op != kOpAttention) return false;
+  const int64_t q = c.a[0], keys = c.a[1], values = c.a[2], gate = c.a[3], out = c.a[4];
+  const int64_t position = c.a[5], n = c.a[6], heads = c.a[7], kvHeads = c.a[8], hd = c.a[9];
+  if (n != 1 || a.a[10] != 1 || b.a[10] != 1) return false;
+  if (a.a[0] != q || a.a[1] != 0 || a.a[8] != heads || a.a[9] != hd) return false;
+  if (b.a[0] != keys || b.a[1] != position * kvHeads * hd * 4 || b.a[8] != kvHeads ||
+      b.a[9] != hd) {
+    return false;
+  }
+  for (int k = 5; k <= 7; k++) {
+    if (a.a[k] != b.a[k]) return false;  // rope table, offset, stride
+  }
+  if (a.a[11] != b.a[11] || q == keys || q == values || keys == values) return false;
+  for (const int64_t h : {out, gate, a.a[3], b.a[3], a.a[5]}) {
+    if (h == q || h == keys) return false;
+  }
+  return out != values;
+}
+
+// DNX_OK, or the launcher's code; DNX_EINVAL means nothing was launched.
+int run_rope_attention(const Cmd& a, const Cmd& b, const Cmd& c) {
+  const int64_t q = c.a[0], keys = c.a[1], values = c.a[2], gate = c.a[3], out = c.a[4];
+  const int64_t position = c.a[5], heads = c.a[7], kvHeads = c.a[8], hd = c.a[9];
+  const int64_t window = c.a[10];
+  const int64_t rope = a.a[5], ropeOff = a.a[6];
+  const double eps = __builtin_bit_cast(double, a.a[11]);
+  const int64_t kvBytes = (position + 1) * kvHeads * hd * 4;
+  read_region(q, 0, heads * hd * 4);
+  read_region(keys, 0, kvBytes);
+  read_region(values, 0, kvBytes);
+  if (gate >= 0) read_region(gate, 0, heads * 4);
+  read_region(a.a[3], a.a[4], hd * 4);
+  read_region(b.a[3], b.a[4], hd * 4);
+  read_region(rope, ropeOff, hd * 4);
+  const int rc = dnx_attention_rope(
+      (float*)dev_at(q, 0), (float*)dev_at(keys, 0), (const float*)dev_at(values, 0),
+      gate >= 0 ? (const float*)dev_at(gate, 0) : nullptr, (float*)dev_at(out, 0), position,
+      heads, kvHeads, hd, window, (const float*)dev_at(a.a[3], a.a[4]),
+      (const float*)dev_at(b.a[3], b.a[4]), (const float*)dev_at(rope, ropeOff), (float)eps,
+      gStream);
+  if (rc == DNX_EINVAL) return rc;
+  if (rc == DNX_OK) after_dispatch(kKindAttention);
+  wrote_region(q, 0, heads * hd * 4);
+  wrote_region(keys, b.a[1], kvHeads * hd * 4);
+  wrote_region(out, 0, heads * hd * 4);
+  if (rc != DNX_OK) LOG("head norms + attention failed (%d)\n", rc);
+  return rc;
+}
+
 // Fusion of a decode matmul (n = 1) and the argmax of its whole output.
 bool fusable_argmax(const Cmd& a, const Cmd& b) {
   return (a.op == kOpMatmulQ8 || a.op == kOpMatmulQ4) && a.int8_inputs && b.op == kOpArgmax &&
@@ -1214,6 +1272,24 @@ int64_t lab_gpu_commit(int64_t wait) {
         ok = run(gCmds[i + 1]) && ok;
       } else {
         ok = rc == DNX_OK && ok;
+      }
+      i += 1;
+    } else if (i + 2 < gCmds.size() &&
+               fusable_rope_attention(gCmds[i], gCmds[i + 1], gCmds[i + 2])) {
+      const int rc = run_rope_attention(gCmds[i], gCmds[i + 1], gCmds[i + 2]);
+      if (rc == DNX_EINVAL) {  // not launched: the norms here, the attention next
+        const int rp = fusable_rope_pair(gCmds[i], gCmds[i + 1])
+                           ? run_rope_pair(gCmds[i], gCmds[i + 1])
+                           : DNX_EINVAL;
+        if (rp == DNX_EINVAL) {
+          ok = run(gCmds[i]) && ok;
+          ok = run(gCmds[i + 1]) && ok;
+        } else {
+          ok = rp == DNX_OK && ok;
+        }
+      } else {
+        ok = rc == DNX_OK && ok;
+        i += 1;
       }
       i += 1;
     } else if (i + 1 < gCmds.size() && fusable_rope_pair(gCmds[i], gCmds[i + 1])) {

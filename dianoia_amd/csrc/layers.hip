@@ -12,6 +12,8 @@
 // Built with -ffp-contract=off: no multiply-add is fused unless written as
 // fmaf.
 
+#include <type_traits>
+
 #include "common.h"
 #include "dnx_kernels.h"
 
@@ -155,12 +157,67 @@ rms_norm_vec_kernel(const float* x_in, const float* __restrict__ w, float* out, 
 // Two operands may share a launch (a decode step's q and k heads, one rope
 // table): workgroups with blockIdx.x below heads0 take (x, x_stride, w) and
 // the rest (xb, xb_stride, wb), head blockIdx.x - heads0.
+// One head's RMSNorm over hd with weight w, then the half-split RoPE
+// rotation pairing j with j + hd / 2 from the table row [cos(hd / 2),
+// sin(hd / 2)], by one wave (lane j holds the pairs j + 64 e, e < P):
+// rope_row_load requests a lane's operands, rope_row_finish computes and
+// writes dst (which may be src: every lane reads its pairs before it writes
+// them). Shared by head_norm_rope_kernel and the attention that folds it in,
+// so both give the same bits (pairs past hd / 2 would only add +0 to the
+// sum, so any P covering hd / 2 gives the same result).
+template <int P>
+struct RopeRow {
+  float x1[P], x2[P], w1[P], w2[P], c[P], s[P];
+};
+
+template <int P>
+DNX_DEV RopeRow<P> rope_row_load(const float* src, const float* __restrict__ w,
+                                 const float* __restrict__ table, int hd, int lane) {
+  const int pair = hd / 2;
+  RopeRow<P> r;
+#pragma unroll
+  for (int e = 0; e < P; e++) {
+    const int j = lane + 64 * e;
+    const bool ok = j < pair;
+    r.x1[e] = ok ? src[j] : 0.0f;
+    r.x2[e] = ok ? src[j + pair] : 0.0f;
+    r.w1[e] = ok ? w[j] : 0.0f;
+    r.w2[e] = ok ? w[j + pair] : 0.0f;
+    r.c[e] = ok ? table[j] : 0.0f;
+    r.s[e] = ok ? table[pair + j] : 0.0f;
+  }
+  return r;
+}
+
+template <int P>
+DNX_DEV void rope_row_finish(const RopeRow<P>& r, int hd, float eps, float* dst, int lane) {
+  const int pair = hd / 2;
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < P; e++) sum += r.x1[e] * r.x1[e] + r.x2[e] * r.x2[e];
+  sum = wave_sum(sum);
+  const float rr = 1.0f / sqrtf(sum / (float)hd + eps);
+#pragma unroll
+  for (int e = 0; e < P; e++) {
+    const int j = lane + 64 * e;
+    if (j >= pair) break;
+    const float n1 = r.w1[e] * (r.x1[e] * rr), n2 = r.w2[e] * (r.x2[e] * rr);
+    dst[j] = n1 * r.c[e] - n2 * r.s[e];
+    dst[j + pair] = n2 * r.c[e] + n1 * r.s[e];
+  }
+}
+
+DNX_DEV void head_norm_rope_row(float* x, const float* __restrict__ w,
+                                const float* __restrict__ table, int hd, float eps, int lane) {
+  constexpr int kPairs = 4;  // hd <= 512
+  rope_row_finish<kPairs>(rope_row_load<kPairs>(x, w, table, hd, lane), hd, eps, x, lane);
+}
+
 __global__ void __launch_bounds__(64)
 head_norm_rope_kernel(float* x, int x_stride, const float* __restrict__ w,
                       const float* __restrict__ rope, int rope_stride, int hd, float eps,
                       int heads0, float* xb, int xb_stride, const float* __restrict__ wb) {
-  constexpr int kPairs = 4;  // hd <= 512
-  const int lane = threadIdx.x, pair = hd / 2;
+  const int lane = threadIdx.x;
   const bool second = (int)blockIdx.x >= heads0;
   if (second) {
     x = xb;
@@ -170,26 +227,7 @@ head_norm_rope_kernel(float* x, int x_stride, const float* __restrict__ w,
   const int head = second ? (int)blockIdx.x - heads0 : (int)blockIdx.x;
   float* xh = x + (size_t)blockIdx.y * x_stride + (size_t)head * hd;
   const float* table = rope + (size_t)blockIdx.y * rope_stride;
-  float x1[kPairs], x2[kPairs];
-  float sum = 0.0f;
-#pragma unroll
-  for (int e = 0; e < kPairs; e++) {
-    const int j = lane + 64 * e;
-    x1[e] = j < pair ? xh[j] : 0.0f;
-    x2[e] = j < pair ? xh[j + pair] : 0.0f;
-    sum += x1[e] * x1[e] + x2[e] * x2[e];
-  }
-  sum = wave_sum(sum);
-  const float r = 1.0f / sqrtf(sum / (float)hd + eps);
-#pragma unroll
-  for (int e = 0; e < kPairs; e++) {
-    const int j = lane + 64 * e;
-    if (j >= pair) break;
-    const float n1 = w[j] * (x1[e] * r), n2 = w[j + pair] * (x2[e] * r);
-    const float c = table[j], s = table[pair + j];
-    xh[j] = n1 * c - n2 * s;
-    xh[j + pair] = n2 * c + n1 * s;
-  }
+  head_norm_rope_row(xh, w, table, hd, eps, lane);
 }
 
 constexpr int kMaxConvK = 16;
@@ -402,12 +440,24 @@ DNX_DEV float group_sum(float v) {
 
 // G query heads per workgroup; LT lanes per key when fixed at compile time
 // (hd = 4 * LT), 0 for any hd.
-template <int G, int LT, int STEPS = kSplitSteps>
+// The q and k head norms + RoPE of a decode step folded into its attention
+// (one token): the table row of the token, the two norm weights, eps, and
+// the cache's keys (written: the new key row, normed in place).
+struct RopeArgs {
+  const float* table;
+  const float* qw;
+  const float* kw;
+  float* keys;
+  float eps;
+};
+constexpr int kRopeMaxHd = 256;
+
+template <int G, int LT, int STEPS = kSplitSteps, bool kRope = false>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
-attention_split_kernel(const float* __restrict__ q, const float* __restrict__ keys,
+attention_split_kernel(const float* __restrict__ q, const float* keys,
                        const float* __restrict__ values, float* __restrict__ ws, int position,
                        int heads, int kv_dim, int group, int hd, int window, float scale,
-                       int splits, int keys_per_split) {
+                       int splits, int keys_per_split, RopeArgs rp) {
   __shared__ float scores[G][kSplitMaxKeys];
   __shared__ float4 part[G][kThreads];
   __shared__ float stat[G][2];
@@ -423,9 +473,11 @@ attention_split_kernel(const float* __restrict__ q, const float* __restrict__ ke
   const int per = 64 / L, step = kWaves * per;               // keys per wave, per step
   const int c = lane % L, kb = wave * per + lane / L;       // this lane's first key
   float4 qr[G];
+  if constexpr (!kRope) {
 #pragma unroll
-  for (int g = 0; g < G; g++)
-    qr[g] = *(const float4*)(q + ((size_t)token * heads + h0 + g) * hd + 4 * c);
+    for (int g = 0; g < G; g++)
+      qr[g] = *(const float4*)(q + ((size_t)token * heads + h0 + g) * hd + 4 * c);
+  }
   // Resources over this split's nk key rows: a row past them lies wholly
   // beyond the range (its offset is at least nk rows) and reads zeros.
   const size_t first = (size_t)(start + k0) * kv_dim + kvo;
@@ -433,6 +485,28 @@ attention_split_kernel(const float* __restrict__ q, const float* __restrict__ ke
   const i32x4 krs = buffer_rsrc(keys + first, range);
   const i32x4 vrs = buffer_rsrc(values + first, range);
   const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  // Folded head norms (one token): wave w norms and rotates q heads h0 + w,
+  // h0 + w + 4, ..., and in the split that holds the token's own key, the
+  // wave after the last q head its key row (as stored). Their operands are
+  // requested before the keys and values, which return in order after them.
+  const int cur = count - 1 - k0;                // the token's key within the split
+  const bool has_cur = kRope && cur >= 0 && cur < nk;
+  constexpr int kRP = kRopeMaxHd / 128;          // pairs per lane
+  constexpr int kRows = kRope ? (G + kWaves) / kWaves : 1;
+  RopeRow<kRP> rrow[kRows];
+  float dcur[G];  // the token's own key's dots (folded norms)
+  if constexpr (kRope) {
+#pragma unroll
+    for (int r = 0; r < kRows; r++) {
+      // Rows a wave does not norm load q's first head (always valid), unused.
+      const int g = wave + r * kWaves;
+      const bool is_k = g == G && has_cur;
+      const float* src = g < G ? q + ((size_t)h0 + g) * hd
+                         : is_k ? keys + (size_t)pos * kv_dim + kvo : q + (size_t)h0 * hd;
+      rrow[r] = rope_row_load<kRP>(src, is_k ? rp.kw : rp.qw, rp.table, hd, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
   float4 kv[STEPS], vv[STEPS];
 #pragma unroll
   for (int j = 0; j < STEPS; j++)
@@ -440,6 +514,44 @@ attention_split_kernel(const float* __restrict__ q, const float* __restrict__ ke
 #pragma unroll
   for (int j = 0; j < STEPS; j++)
     vv[j] = buffer_load_f4(vrs, (kb + j * step) * kv_dim * 4 + 16 * c);
+  // The folded norms' results go through LDS to the lanes that need them;
+  // the keys and values are in flight meanwhile.
+  if constexpr (kRope) {
+    __shared__ float qn[G][kRopeMaxHd];
+    __shared__ float kn[kRopeMaxHd];
+#pragma unroll
+    for (int r = 0; r < kRows; r++) {
+      const int g = wave + r * kWaves;
+      if (g < G) {
+        rope_row_finish<kRP>(rrow[r], hd, rp.eps, qn[g], lane);
+      } else if (g == G && has_cur) {
+        rope_row_finish<kRP>(rrow[r], hd, rp.eps, kn, lane);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; g++) qr[g] = *(const float4*)(qn[g] + 4 * c);
+    if (has_cur) {
+      // The token's own key scores against its normed row (every key group
+      // holds all dims, so every lane computes the same dot, reduced as the
+      // other keys' dots are); its loaded copy is not used.
+      const float4 k4 = *(const float4*)(kn + 4 * c);
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        float d = qr[g].x * k4.x + qr[g].y * k4.y + qr[g].z * k4.z + qr[g].w * k4.w;
+        if constexpr (LT > 0) {
+          d = group_sum<LT>(d);
+        } else {
+          for (int o = L / 2; o > 0; o >>= 1) d += __shfl_xor(d, o);
+        }
+        dcur[g] = d;
+      }
+      // The normed key row back into the cache (only this workgroup reads it).
+      if (tid < hd / 4) {
+        *(float4*)(rp.keys + (size_t)pos * kv_dim + kvo + 4 * tid) = *(const float4*)(kn + 4 * tid);
+      }
+    }
+  }
   // Dots in batches of kBatch steps x G heads: each butterfly stage issues
   // the batch's lane exchanges together and waits once (L is a run-time
   // count, so per-dot loops would wait on every exchange).
@@ -472,7 +584,7 @@ attention_split_kernel(const float* __restrict__ q, const float* __restrict__ ke
       const int i = kb + (j0 + u) * step;
       if (i < nk && c == 0) {
 #pragma unroll
-        for (int g = 0; g < G; g++) scores[g][i] = d[u][g] * scale;
+        for (int g = 0; g < G; g++) scores[g][i] = (has_cur && i == cur ? dcur[g] : d[u][g]) * scale;
       }
     }
   }
@@ -544,15 +656,15 @@ attention_split_kernel(const float* __restrict__ q, const float* __restrict__ ke
   }
 }
 
-template <int G>
+template <int G, bool kRope = false>
 void launch_split(dim3 grid, hipStream_t stream, const float* q, const float* keys,
                   const float* values, float* ws, int position, int heads, int kv_dim, int group,
-                  int hd, int window, float scale, int splits, int kps) {
-  auto kernel = hd == 128 ? attention_split_kernel<G, 32>
-              : hd == 64  ? attention_split_kernel<G, 16>
-                          : attention_split_kernel<G, 0>;
+                  int hd, int window, float scale, int splits, int kps, RopeArgs rp = {}) {
+  auto kernel = hd == 128 ? attention_split_kernel<G, 32, kSplitSteps, kRope>
+              : hd == 64  ? attention_split_kernel<G, 16, kSplitSteps, kRope>
+                          : attention_split_kernel<G, 0, kSplitSteps, kRope>;
   hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, stream, q, keys, values, ws, position,
-                     heads, kv_dim, group, hd, window, scale, splits, kps);
+                     heads, kv_dim, group, hd, window, scale, splits, kps, rp);
 }
 
 // The splits of one (head, token). Thread t takes dimension t % hd of the
@@ -583,9 +695,11 @@ DNX_DEV float combine_stats(const float* w, int splits, int row, int s0, float m
   return block_sum(lp, scratch);
 }
 
+template <bool kRope = false>
 __global__ void __launch_bounds__(kThreads)
 attention_combine_kernel(const float* __restrict__ ws, const float* __restrict__ gate,
-                         float* __restrict__ out, int heads, int hd, int splits) {
+                         float* __restrict__ out, int heads, int hd, int splits,
+                         float* qio = nullptr, RopeArgs rp = {}) {
   extern __shared__ float fs[];   // [splits] e^(m_s - M), 0 for empty splits
   __shared__ float scratch[kWaves];
   __shared__ float red[kThreads];
@@ -605,6 +719,13 @@ attention_combine_kernel(const float* __restrict__ ws, const float* __restrict__
   const int s0 = tid;   // the first split whose statistics this thread reads
   const float m0 = __int_as_float(dnx_raw_buffer_load_i32(rs, s0 * row * 4, 0, 0));
   const float l0 = __int_as_float(dnx_raw_buffer_load_i32(rs, (s0 * row + 1) * 4, 0, 0));
+  if constexpr (kRope) {
+    // The folded q norm of this head, in place (one token): the split
+    // kernel normed its own copies; every split has finished reading q.
+    if (tid < 64) {
+      head_norm_rope_row(qio + (size_t)head * hd, rp.qw, rp.table, hd, rp.eps, tid);
+    }
+  }
   float l;
   if (splits <= 64) {
     // One wave holds every split's statistics (lane s): the max, the
@@ -1004,6 +1125,69 @@ int grid_for(int64_t items) {
   return (int)(g < 1 ? 1 : g > 65536 ? 65536 : g);
 }
 
+// The split-key attention (few (head, token) pairs, many keys): the split
+// kernel, then the combine. DNX_EINVAL when it does not apply (nothing
+// launched). rp: the q and k head norms folded in (one token, one
+// workgroup per KV head and split), or null.
+int attention_split(const float* q, const float* keys, const float* values, const float* gate,
+                    float* out, int64_t position, int64_t n, int64_t heads, int64_t kv_heads,
+                    int64_t hd, int64_t window, float scale, dnx_stream_t stream,
+                    const RopeArgs* rp) {
+  const int64_t last = position + n - 1;
+  const int64_t keys_of_last = window > 0 && last >= window ? window : last + 1;
+  const int kps = split_keys((int)hd);
+  const int64_t splits = (keys_of_last + kps - 1) / kps;
+  // (Also when the keys exceed the one-workgroup kernel's LDS.) The split
+  // kernel's buffer offsets reach 4096 key rows: 32-bit up to 2^17 floats
+  // per row.
+  const size_t ws_bytes = (size_t)heads * n * splits * (hd + 4) * 4;
+  if (!(splits > 1 && (heads * n < 256 || keys_of_last > dnx_attention_max_keys(hd)) &&
+        splits <= 16000 && ws_bytes <= ((size_t)1 << 30) && kv_heads * hd <= (1 << 17))) {
+    return DNX_EINVAL;
+  }
+  // G query heads per workgroup: the largest of 8, 4, 2, 1 dividing the
+  // heads per KV head.
+  const int group = (int)(heads / kv_heads);
+  const int G = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+  if (rp != nullptr && (n != 1 || G != group || hd > kRopeMaxHd)) return DNX_EINVAL;
+  float* ws = attention_workspace(ws_bytes);
+  if (ws == nullptr) return DNX_ENOMEM;
+  const dim3 grid((unsigned)(heads / G), (unsigned)n, (unsigned)splits);
+  const hipStream_t st = (hipStream_t)stream;
+  const int kv_dim = (int)(kv_heads * hd);
+  const RopeArgs ra = rp != nullptr ? *rp : RopeArgs{};
+  auto split = [&](auto g_tag, auto rope_tag) {
+    constexpr int kG = decltype(g_tag)::value;
+    constexpr bool kR = decltype(rope_tag)::value;
+    launch_split<kG, kR>(grid, st, q, keys, values, ws, (int)position, (int)heads, kv_dim, group,
+                         (int)hd, (int)window, scale, (int)splits, kps, ra);
+  };
+  auto by_g = [&](auto rope_tag) {
+    switch (G) {
+      case 8: split(std::integral_constant<int, 8>{}, rope_tag); break;
+      case 4: split(std::integral_constant<int, 4>{}, rope_tag); break;
+      case 2: split(std::integral_constant<int, 2>{}, rope_tag); break;
+      default: split(std::integral_constant<int, 1>{}, rope_tag); break;
+    }
+  };
+  if (rp != nullptr) {
+    by_g(std::true_type{});
+  } else {
+    by_g(std::false_type{});
+  }
+  if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+  if (rp != nullptr) {
+    hipLaunchKernelGGL(attention_combine_kernel<true>, dim3((unsigned)heads, (unsigned)n),
+                       dim3(kThreads), (size_t)splits * 4, st, ws, gate, out, (int)heads,
+                       (int)hd, (int)splits, const_cast<float*>(q), ra);
+  } else {
+    hipLaunchKernelGGL(attention_combine_kernel<false>, dim3((unsigned)heads, (unsigned)n),
+                       dim3(kThreads), (size_t)splits * 4, st, ws, gate, out, (int)heads,
+                       (int)hd, (int)splits, (float*)nullptr, RopeArgs{});
+  }
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1119,6 +1303,21 @@ int dnx_short_conv(const float* bcx, const float* weight, float* history, float*
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 
+int dnx_attention_rope(float* q, float* keys, const float* values, const float* gate, float* out,
+                       int64_t position, int64_t heads, int64_t kv_heads, int64_t hd,
+                       int64_t window, const float* q_norm, const float* k_norm,
+                       const float* rope, float eps, dnx_stream_t stream) {
+  if (position < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || hd <= 0 ||
+      hd % 4 != 0 || hd > kRopeMaxHd || kThreads % hd != 0 || window < 0 || heads > 65535 ||
+      position + 1 > 0x7fffffff || ((uintptr_t)keys & 15) || ((uintptr_t)q & 15) ||
+      q_norm == nullptr || k_norm == nullptr || rope == nullptr) {
+    return DNX_EINVAL;
+  }
+  const RopeArgs rp{rope, q_norm, k_norm, keys, eps};
+  return attention_split(q, keys, values, gate, out, position, 1, heads, kv_heads, hd, window,
+                         (float)(1.0 / sqrt((double)hd)), stream, &rp);
+}
+
 int64_t dnx_attention_max_keys(int64_t hd) {
   if (hd <= 0 || hd > 256 || kThreads % hd != 0) return -1;
   // LDS: q (hd) + scores (rounded up to 4) + value partials ((256 / hd) x
@@ -1191,46 +1390,16 @@ int dnx_attention(const float* q, const float* keys, const float* values, const 
       hipLaunchKernelGGL(k, dim3((unsigned)((rows + kWaves - 1) / kWaves)), dim3(kThreads), 0, st,
                          ws, gate, out, (int)heads, (int)hd, (int)splits, (int)rows);
     } else if (splits > 1) {
-      hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)heads, (unsigned)n),
+      hipLaunchKernelGGL(attention_combine_kernel<false>, dim3((unsigned)heads, (unsigned)n),
                          dim3(kThreads), (size_t)splits * 4, st, ws, gate, out, (int)heads,
-                         (int)hd, (int)splits);
+                         (int)hd, (int)splits, (float*)nullptr, RopeArgs{});
     }
     return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
   }
   // Few (head, token) workgroups for many keys: split the keys.
-  const int kps = split_keys((int)hd);
-  const int64_t splits = (keys_of_last + kps - 1) / kps;
-  // (Also when the keys exceed the one-workgroup kernel's LDS.) The split
-  // kernel's buffer offsets reach 4096 key rows: 32-bit up to 2^17 floats
-  // per row.
-  const size_t ws_bytes = (size_t)heads * n * splits * (hd + 4) * 4;
-  if (splits > 1 && (heads * n < 256 || keys_of_last > dnx_attention_max_keys(hd)) &&
-      splits <= 16000 && ws_bytes <= ((size_t)1 << 30) && kv_heads * hd <= (1 << 17)) {
-    float* ws = attention_workspace(ws_bytes);
-    if (ws == nullptr) return DNX_ENOMEM;
-    // G query heads per workgroup: the largest of 8, 4, 2, 1 dividing the
-    // heads per KV head.
-    const int group = (int)(heads / kv_heads);
-    const int G = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
-    const dim3 grid((unsigned)(heads / G), (unsigned)n, (unsigned)splits);
-    const hipStream_t st = (hipStream_t)stream;
-    const int kv_dim = (int)(kv_heads * hd);
-    switch (G) {
-      case 8: launch_split<8>(grid, st, q, keys, values, ws, (int)position, (int)heads, kv_dim,
-                              group, (int)hd, (int)window, scale, (int)splits, kps); break;
-      case 4: launch_split<4>(grid, st, q, keys, values, ws, (int)position, (int)heads, kv_dim,
-                              group, (int)hd, (int)window, scale, (int)splits, kps); break;
-      case 2: launch_split<2>(grid, st, q, keys, values, ws, (int)position, (int)heads, kv_dim,
-                              group, (int)hd, (int)window, scale, (int)splits, kps); break;
-      default: launch_split<1>(grid, st, q, keys, values, ws, (int)position, (int)heads, kv_dim,
-                               group, (int)hd, (int)window, scale, (int)splits, kps); break;
-    }
-    if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
-    hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)heads, (unsigned)n),
-                       dim3(kThreads), (size_t)splits * 4, (hipStream_t)stream, ws, gate, out,
-                       (int)heads, (int)hd, (int)splits);
-    return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
-  }
+  const int rc = attention_split(q, keys, values, gate, out, position, n, heads, kv_heads, hd,
+                                 window, scale, stream, nullptr);
+  if (rc != DNX_EINVAL) return rc;
   if (keys_of_last > dnx_attention_max_keys(hd)) return DNX_EINVAL;
   const size_t lds = (size_t)(hd + ((keys_of_last + 3) & ~3ll) + kThreads) * 4;
   hipLaunchKernelGGL(attention_kernel, dim3((unsigned)heads, (unsigned)n), dim3(kThreads), lds,

@@ -353,6 +353,17 @@ def attention(q, keys, values, gate, out, position: int, n: int, heads: int, kv_
            "dnx_attention")
 
 
+def attention_rope(q, keys, values, gate, out, position: int, heads: int, kv_heads: int, hd: int,
+                   window: int, q_norm, k_norm, rope_row, eps: float, stream=None) -> None:
+    """One decode token: head norm + RoPE of q and of keys[position], folded
+    into the split-key attention (q and the key row are normed in place)."""
+    _check(_lib.load().dnx_attention_rope(_ptr(q), _ptr(keys), _ptr(values),
+                                          None if gate is None else _ptr(gate), _ptr(out),
+                                          position, heads, kv_heads, hd, window, _ptr(q_norm),
+                                          _ptr(k_norm), _ptr(rope_row), eps, _stream(stream)),
+           "dnx_attention_rope")
+
+
 def add(src, dst, count: int, stream=None) -> None:
     _check(_lib.load().dnx_add(_ptr(src), _ptr(dst), count, _stream(stream)), "dnx_add")
 

@@ -381,6 +381,18 @@ int64_t dnx_attention_max_keys(int64_t hd);
 int dnx_attention(const float* q, const float* keys, const float* values, const float* gate,
                   float* out, int64_t position, int64_t n, int64_t heads, int64_t kv_heads,
                   int64_t hd, int64_t window, dnx_stream_t stream);
+// One decode token's q and k head norms + RoPE folded into its attention
+// (gpu.dart:1157-1175: dnx_head_norm_rope of q with q_norm, of the token's
+// key row keys[position] with k_norm, both with the table row `rope`
+// [cos(hd / 2), sin(hd / 2)], then dnx_attention with n = 1): the same bits
+// in out, in q (normed in place) and in keys[position] (normed in place).
+// The split-key path only, with one workgroup per KV head (the query heads
+// per KV head a power of two up to 8) and hd <= 256: DNX_EINVAL otherwise,
+// nothing launched. out must not overlap q, keys or values.
+int dnx_attention_rope(float* q, float* keys, const float* values, const float* gate, float* out,
+                       int64_t position, int64_t heads, int64_t kv_heads, int64_t hd,
+                       int64_t window, const float* q_norm, const float* k_norm,
+                       const float* rope, float eps, dnx_stream_t stream);
 // dst += src and dst = src over `count` floats (lab_metal.m:560-572).
 int dnx_add(const float* src, float* dst, int64_t count, dnx_stream_t stream);
 int dnx_copy(const float* src, float* dst, int64_t count, dnx_stream_t stream);

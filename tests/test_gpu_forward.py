@@ -322,3 +322,39 @@ def test_tracking_off_uploads_the_history_and_agrees(gpu_ready):
     assert int(out["tracking"]) == 0
     assert same(out["logits16"], want) and same(out["logits17"], want17)
     assert int(out["up17"]) >= up_tracked + 2 * 17 * cfg.kv_dim * 4 * cfg.layers
+
+
+def test_long_context_decode_folds_head_norms(gpu_ready):
+    """Decode steps past 64 positions take the split-key attention, where the
+    commit folds the q and k head norms into it: one command buffer per pass
+    against one per command, bit for bit (logits and KV rows), and the
+    folded step dispatches no standalone head norm."""
+    import ctypes
+    from dianoia_amd import _lib
+    lib = _lib.load()
+    cfg = qwen3_small()
+    # hd 64 splits the keys in runs of 128: decode at 160 and 161
+    plan = [(8, p) for p in range(0, 160, 8)] + [(1, 160), (1, 161)]
+    fused = F.GpuForward(cfg, max_seq=192, max_chunk=8, seed=5)
+    split = F.GpuForward(cfg, max_seq=192, max_chunk=8, seed=5)
+    split.split_commits = True
+    try:
+        a = run(fused, plan[:-1])
+        b = run(split, plan[:-1])
+        for (la, sa), (lb, sb), chunk in zip(a, b, plan):
+            assert same(la, lb), f"logits differ after chunk {chunk}"
+            assert all(same(x, y) for x, y in zip(sa, sb)), f"state differs after chunk {chunk}"
+        ms = (ctypes.c_double * 21)()
+        lib.lab_gpu_profile(ms, (ctypes.c_int64 * 21)(), 21)
+        lib.lab_gpu_set_profiling(1)
+        la = run(fused, plan[-1:])
+        lib.lab_gpu_set_profiling(0)
+        counts = (ctypes.c_int64 * 21)()
+        lib.lab_gpu_profile(ms, counts, 21)
+        lb = run(split, plan[-1:])
+        assert same(la[0][0], lb[0][0])
+        head_norm_rope, attention = 5, 7
+        assert counts[head_norm_rope] == 0 and counts[attention] == len(cfg.layer_types), list(counts)
+    finally:
+        fused.dispose()
+        split.dispose()

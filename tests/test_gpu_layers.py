@@ -293,3 +293,52 @@ def test_head_norm_rope_pair(gpu_ready, h0, h1, hd, n):
     D.head_norm_rope2(qb, s0, dev(w0), h0, kb, s1, dev(w1), h1, dev(table), rs, hd, n, 1e-6)
     assert np.array_equal(bits(host(qb)), bits(host(qa)))
     assert np.array_equal(bits(host(kb)), bits(host(ka)))
+
+
+@pytest.mark.parametrize("heads,kv,hd,pos,window,gated", [(16, 8, 128, 4095, 0, False),
+                                                          (32, 8, 128, 700, 0, True),
+                                                          (8, 8, 64, 300, 0, False),
+                                                          (16, 2, 64, 1000, 256, True),
+                                                          (4, 1, 128, 64, 0, False)])
+def test_attention_rope_equals_norms_then_attention(gpu_ready, heads, kv, hd, pos, window, gated):
+    """dnx_attention_rope (the q and k head norms + RoPE folded into a decode
+    token's split-key attention) against dnx_head_norm_rope on q and on the
+    token's key row, then dnx_attention: out, q and the key row bit for bit;
+    every other key row untouched."""
+    rng = np.random.default_rng(heads * 7 + pos)
+    kvd = kv * hd
+    q0 = rng.standard_normal(heads * hd).astype(np.float32)
+    keys0 = rng.standard_normal((pos + 1) * kvd).astype(np.float32)
+    vals = dev(rng.standard_normal((pos + 1) * kvd).astype(np.float32))
+    qw = dev(rng.uniform(0.5, 1.5, hd).astype(np.float32))
+    kw = dev(rng.uniform(0.5, 1.5, hd).astype(np.float32))
+    ang = rng.uniform(0, 6.3, hd // 2)
+    rope = dev(np.concatenate([np.cos(ang), np.sin(ang)]).astype(np.float32))
+    gate = dev(rng.standard_normal(heads).astype(np.float32)) if gated else None
+    eps = 1e-6
+    q_ref, k_ref = dev(q0), dev(keys0)
+    out_ref = torch.empty(heads * hd, device="cuda")
+    D.head_norm_rope(q_ref, heads * hd, qw, rope, hd, heads, hd, 1, eps)
+    D.head_norm_rope(k_ref[pos * kvd:], kvd, kw, rope, hd, kv, hd, 1, eps)
+    D.attention(q_ref, k_ref, vals, gate, out_ref, pos, 1, heads, kv, hd, window)
+    q, k = dev(q0), dev(keys0)
+    out = torch.full((heads * hd,), float("nan"), device="cuda")
+    D.attention_rope(q, k, vals, gate, out, pos, heads, kv, hd, window, qw, kw, rope, eps)
+    assert np.array_equal(bits(host(out)), bits(host(out_ref)))
+    assert np.array_equal(bits(host(q)), bits(host(q_ref)))
+    assert np.array_equal(bits(host(k)), bits(host(k_ref)))
+
+
+def test_attention_rope_refuses_short_or_unsplit(gpu_ready):
+    hd, heads, kv = 128, 16, 8
+    z = torch.zeros(64 * kv * hd, device="cuda")
+    w = torch.ones(hd, device="cuda")
+    out = torch.zeros(heads * hd, device="cuda")
+    q = torch.zeros(heads * hd, device="cuda")
+    with pytest.raises(RuntimeError):   # 10 keys: one split, not the split-key path
+        D.attention_rope(q, z, z, None, out, 9, heads, kv, hd, 0, w, w, w, 1e-6)
+    z2 = torch.zeros(201 * 4 * 128, device="cuda")
+    q2 = torch.zeros(12 * 128, device="cuda")
+    out2 = torch.zeros(12 * 128, device="cuda")
+    with pytest.raises(RuntimeError):   # three query heads per KV head: no single workgroup
+        D.attention_rope(q2, z2, z2, None, out2, 200, 12, 4, 128, 0, w, w, w, 1e-6)
