@@ -722,8 +722,9 @@ attention_combine_kernel(const float* __restrict__ ws, const float* __restrict__
   if constexpr (kRope) {
     // The folded q norm of this head, in place (one token): the split
     // kernel normed its own copies; every split has finished reading q.
-    if (tid < 64) {
-      head_norm_rope_row(qio + (size_t)head * hd, rp.qw, rp.table, hd, rp.eps, tid);
+    // Wave 1, while wave 0 reduces the split statistics.
+    if (tid >= 64 && tid < 128) {
+      head_norm_rope_row(qio + (size_t)head * hd, rp.qw, rp.table, hd, rp.eps, tid - 64);
     }
   }
   float l;
