@@ -621,7 +621,8 @@ size_t fusable_norm_matmul(const std::vector<Cmd>& cmds, size_t i, bool& pair) {
   if (i + 3 < cmds.size() && fusable_pair(a, cmds[i + 2], cmds[i + 3])) {
     const int64_t rb = a.a[7] * 4;
     if (a.a[9] != 1 || !clear_of_norm(nrm, a.a[5], 0, rb) ||
-        !clear_of_norm(nrm, cmds[i + 2].a[5], 0, rb)) {
+        !clear_of_norm(nrm, cmds[i + 2].a[5], 0, rb) || a.a[0] == nrm.a[4] ||
+        cmds[i + 2].a[0] == nrm.a[4]) {
       return 0;
     }
     pair = true;
@@ -633,7 +634,8 @@ size_t fusable_norm_matmul(const std::vector<Cmd>& cmds, size_t i, bool& pair) {
   if (len == 1 && i + 2 < cmds.size() && fusable_argmax(a, cmds[i + 2])) return 0;
   for (size_t k = 0; k < len; k++) {
     const Cmd& c = cmds[i + 1 + k];
-    if (!clear_of_norm(nrm, c.a[5], c.a[6], c.a[7] * 4)) return 0;
+    // The weights are read while workgroup 0 writes the norm's output.
+    if (!clear_of_norm(nrm, c.a[5], c.a[6], c.a[7] * 4) || c.a[0] == nrm.a[4]) return 0;
   }
   pair = false;
   return len;
@@ -780,8 +782,8 @@ int run_rope_pair(const Cmd& a, const Cmd& b) {
 // eps, then the one-token attention over them. dnx_attention_rope norms
 // both inside the split-key attention and leaves q, the key row and out as
 // the three dispatches would. out and gate must not share a buffer with q
-// or the keys, and the norm weights and rope table must not lie in q's or
-// the keys' buffers.
+// or the keys, the norm weights and rope table must not lie in q's or the
+// keys' buffers, and out shares no buffer with anything the launch reads.
 bool fusable_rope_attention(const Cmd& a, const Cmd& b, const Cmd& c) {
   if (a.op != kOpHeadNormRope || b.op != kOpHeadNormRope || c.op != kOpAttention) return false;
   const int64_t q = c.a[0], keys = c.a[1], values = c.a[2], gate = c.a[3], out = c.a[4];
@@ -799,7 +801,12 @@ bool fusable_rope_attention(const Cmd& a, const Cmd& b, const Cmd& c) {
   for (const int64_t h : {out, gate, a.a[3], b.a[3], a.a[5]}) {
     if (h == q || h == keys) return false;
   }
-  return out != values;
+  // out is written while the norm weights, the rope table, the gate and the
+  // values are read: no shared buffer.
+  for (const int64_t h : {values, gate, a.a[3], b.a[3], a.a[5]}) {
+    if (h == out) return false;
+  }
+  return true;
 }
 
 // DNX_OK, or the launcher's code; DNX_EINVAL means nothing was launched.
