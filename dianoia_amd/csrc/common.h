@@ -195,6 +195,10 @@ DNX_DEV float max4abs(float4 v) {
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// s_waitcnt immediate (gfx9 encoding): vmcnt <= vm, lgkmcnt <= 0, expcnt
+// unconstrained.
+constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
+
 // 16-byte load marked non-temporal: weights are streamed once, so they
 // should not displace the inputs other workgroups still reuse.
 DNX_DEV uint4 load_stream16(const void* p) {
@@ -243,6 +247,41 @@ constexpr int kStream = 2;
 DNX_DEV uint4 buffer_load16_stream(i32x4 rsrc, int offset) {
   const i32x4 v = dnx_raw_buffer_load_v4i32(rsrc, offset, 0, kStream);
   return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+
+// 16 bytes per lane from a buffer resource straight into LDS, at lds_addr +
+// 16 * lane (gfx950's LDS DMA: no VGPRs; counted by vmcnt like any load).
+// lds_addr is the wave-uniform LDS byte address (lds_address below).
+// Inline asm on purpose: the compiler cannot tell which part of an LDS
+// array a DMA writes, so for its own LDS DMA it waits for every outstanding
+// load before the next LDS read of that array. Hidden from it, the caller
+// owns the wait: an s_waitcnt vmcnt that covers the DMA, then a barrier,
+// before any wave reads the bytes. The compiler's own vmcnt waits do not
+// count these loads, which only makes them stricter. It sets M0, which
+// LLVM treats as reserved (a clobber of it is ignored): use it only in
+// kernels where nothing else reads M0 (gfx950 LDS instructions do not; the
+// gemm_f6 kernels' code has no other M0 access).
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+DNX_DEV uint32_t lds_address(const void* p) { return (uint32_t)(size_t)(lds_ptr_t)p; }
+DNX_DEV void buffer_load16_to_lds(i32x4 rsrc, uint32_t lds_addr, int voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voffset), "s"(rsrc)
+               : "memory");
+}
+
+// Write-through stores (gfx950 cache policy sc0 sc1): the line goes on to
+// memory now instead of staying dirty in the L2 until the end-of-kernel
+// write-back. For large outputs written once at a kernel's end (a GEMM's
+// 12.6 MB at 512 x 6144) this took the fp6 GEMM from 22.9 to 19.0 us.
+// Inline asm: the compiler does not count these in its wait counters, which
+// only makes its later waits for its own loads stricter.
+DNX_DEV void store_wt(float* p, float v) {
+  asm volatile("global_store_dword %0, %1, off sc0 sc1" : : "v"(p), "v"(v) : "memory");
+}
+DNX_DEV void store_wt4(float* p, float4 v) {
+  const f32x4 w = {v.x, v.y, v.z, v.w};
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" : : "v"(p), "v"(w) : "memory");
 }
 
 DNX_DEV float4 buffer_load_f4(i32x4 rsrc, int offset) {

@@ -280,7 +280,7 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int m = m0 + wm * TM + i * 32 + (v / 4) * 8 + (lane >> 5) * 4 + (v % 4);
-        if (m < M) out[(size_t)m * N + r] = acc[i][j][v];
+        if (m < M) store_wt(out + (size_t)m * N + r, acc[i][j][v]);
       }
     }
 }
@@ -464,7 +464,7 @@ __global__ void __launch_bounds__(kThreads) skinny_kernel(GemmParams p) {
 #pragma unroll
       for (int w = 0; w < 3; w++) s += red[((w * MT + t) * 4 + v) * 64 + lane];
       const int m = 16 * t + 4 * g + v;
-      if (m < M) p.y[(size_t)m * N + row] = s;
+      if (m < M) store_wt(p.y + (size_t)m * N + row, s);
     }
 }
 
@@ -491,7 +491,7 @@ __global__ void __launch_bounds__(kThreads) splitk_reduce_kernel(const float* __
                                                                  int64_t count, int splits) {
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < count;
        i += (int64_t)gridDim.x * kThreads) {
-    y[i] = split_sum(part, count, i, splits);
+    store_wt(y + i, split_sum(part, count, i, splits));
   }
 }
 

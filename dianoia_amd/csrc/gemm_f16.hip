@@ -424,7 +424,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_f16_kernel(Params p) {
 #pragma unroll
     for (int v = 0; v < 16; v++) {
       const int m = g * kRowsPerWave + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      if (m < M) out[(size_t)m * N + r] = acc[j][v];
+      if (m < M) store_wt(out + (size_t)m * N + r, acc[j][v]);
     }
   }
 }
@@ -441,7 +441,7 @@ __global__ void __launch_bounds__(kThreads) f16_splitk_reduce_kernel(const float
        i += (int64_t)gridDim.x * kThreads) {
     float v = part[i];
     for (int z = 1; z < splits; z++) v += part[(size_t)z * count + i];
-    y[i] = v;
+    store_wt(y + i, v);
   }
 }
 

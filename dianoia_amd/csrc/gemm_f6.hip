@@ -29,12 +29,14 @@
 //
 // Operands.
 //   Activations: a "f6 panel" written by the quantizer below from fp32 x
-//   (or from xq + xsc), per 32 tokens and block (kRec bytes): 64 lanes x
-//   32 B in MFMA lane order (6 dwords of fp6 codes, then the scale MFMA's
+//   (or from xq + xsc), per 32 tokens and block (kRec bytes): each MFMA
+//   lane's 32-byte record (6 dwords of fp6 codes, then the scale MFMA's
 //   four fp16 operand slots, the E8M0 scale byte riding in the third: see
-//   write_f6_entries), and the 32 tokens' C values. A wave loads its
-//   tokens' 32-byte lane records straight into registers, four blocks
-//   ahead; the C values are staged through LDS with the weights.
+//   write_f6_entries) split into two 1 KB halves, [half][64 lanes][16 B],
+//   so that each of a wave's two 16-byte loads reads 1 KB contiguous; then
+//   the 32 tokens' C values. A wave loads its tokens' records straight into
+//   registers, four blocks ahead; the C values are staged through LDS with
+//   the weights.
 //   Weights: staged through LDS once per workgroup, shared by its 8 waves:
 //   each 16-byte Q4 block becomes 6 dwords of fp6 codes with 16 VALU
 //   operations (kFieldK below is the resulting order of the weights in the
@@ -63,7 +65,8 @@ constexpr int kPanelThreads = 256;
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kTokens = 32;                 // tokens per panel group (one MFMA tile)
-constexpr int kRecF = 0;                    // 64 lanes x 32 B: fp6 codes + operand dwords
+constexpr int kRecF = 0;                    // [2 halves][64 lanes][16 B]: fp6 codes + operand dwords
+constexpr int kRecHalf = 1024;              // the second 16 bytes of every lane's record
 constexpr int kRecC = 2048;                 // 2 halves x 16 floats: the MFMA's C input
 constexpr int kRec = 2176;                  // panel bytes per (32 tokens, block)
 
@@ -139,12 +142,13 @@ DNX_DEV void write_f6_entries(uint8_t* rec, int r, const int* xq, float scale) {
   const uint32_t s0 = (uint32_t)__builtin_bit_cast(uint16_t, p0) |
                       ((uint32_t)__builtin_bit_cast(uint16_t, p1) << 16);
   const uint32_t s1 = sh_h | ((uint32_t)__builtin_bit_cast(uint16_t, p2) << 16);
-  uint4* fh = (uint4*)(rec + kRecF + r * 32);
-  uint4* fl = (uint4*)(rec + kRecF + (32 + r) * 32);
-  fh[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-  fh[1] = make_uint4(hw[4], hw[5], s0, s1);
-  fl[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-  fl[1] = make_uint4(lw[4], lw[5], 0u, sh_l);
+  // Lane r holds the h codes of token r, lane 32 + r its l codes.
+  uint8_t* fh = rec + kRecF + r * 16;
+  uint8_t* fl = rec + kRecF + (32 + r) * 16;
+  *(uint4*)fh = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  *(uint4*)(fh + kRecHalf) = make_uint4(hw[4], hw[5], s0, s1);
+  *(uint4*)fl = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  *(uint4*)(fl + kRecHalf) = make_uint4(lw[4], lw[5], 0u, sh_l);
   // C of output row r: lanes of half (r / 4) % 2 hold it at 4 (r / 8) + r % 4.
   const float c = sum == 0 ? 0.0f : ldexpf((float)(-8 * sum), e);
   *(float*)(rec + kRecC + ((((r >> 2) & 1) * 16 + (r >> 3) * 4 + (r & 3)) * 4)) = c;
@@ -232,7 +236,7 @@ constexpr int epilogue_lds_bytes() {
 // parity of K) into LDS in [token][row] order, then every wave adds the two
 // parities (even + odd, a fixed order) for 1/8 of the outputs and stores
 // them 16 bytes per lane, consecutive lanes along a token's row (a row of
-// BN floats is BN / 4 lanes). `vec` (uniform): out and N allow 16-byte
+// BN floats is BN / 4 lanes), write-through (store_wt4). `vec` (uniform): out and N allow 16-byte
 // stores; otherwise each value is stored alone. Called by all waves after
 // the K loop's last barrier (the partials overwrite the stage buffers).
 template <int SN>
@@ -265,12 +269,12 @@ DNX_DEV void store_tile_sums(uint8_t* lds, const v16f* acc, int wave, int lane, 
     const float4 o = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
     float* dst = out + (size_t)m * N + r;
     if (vec) {
-      *(float4*)dst = o;
+      store_wt4(dst, o);
     } else {
-      dst[0] = o.x;
-      if (r + 1 < N) dst[1] = o.y;
-      if (r + 2 < N) dst[2] = o.z;
-      if (r + 3 < N) dst[3] = o.w;
+      store_wt(dst, o.x);
+      if (r + 1 < N) store_wt(dst + 1, o.y);
+      if (r + 2 < N) store_wt(dst + 2, o.z);
+      if (r + 3 < N) store_wt(dst + 3, o.w);
     }
   }
 }
@@ -387,8 +391,8 @@ __global__ void __launch_bounds__(kThreads) gemm_f6_q4_kernel(F6Params p) {
   auto load_a = [&](int b, i32x4& lo, i32x4& hi) {
     const int ok = -(int)(live & (b < b_end));
     const int base = (((g * B + b) * kRec + kRecF) & ok) | (~ok & -(1 << 20));
-    lo = dnx_raw_buffer_load_v4i32(rpanel, base + lane * 32, 0, 0);
-    hi = dnx_raw_buffer_load_v4i32(rpanel, base + lane * 32 + 16, 0, 0);
+    lo = dnx_raw_buffer_load_v4i32(rpanel, base + lane * 16, 0, 0);
+    hi = dnx_raw_buffer_load_v4i32(rpanel, base + kRecHalf + lane * 16, 0, 0);
   };
 
   v16f acc[SN];
@@ -490,62 +494,82 @@ __global__ void __launch_bounds__(kThreads) gemm_f6_q4_kernel(F6Params p) {
 // The engine's Q4 layout needs 16 VALU operations per 32 weights to become
 // fp6 fields, and its -8 offset costs the MFMA a C input (16 more register
 // reads per tile). Weights are immutable after upload, so they can be
-// re-encoded once: per (row, block) 32 bytes, the E2M3 codes of the signed
-// weights w = q - 8 (sign bit, |w| in 0..8 as the code of |w| / 8) in the
-// fields' order, then the scale MFMA's slots (sw, sw, 0, sw). The GEMM on
-// that layout stages it to LDS with plain copies and runs the dot without a
-// C input.
+// re-encoded once: per (row, block) a 32-byte record, the E2M3 codes of the
+// signed weights w = q - 8 (sign bit, |w| in 0..8 as the code of |w| / 8) in
+// the fields' order, then the scale MFMA's slots (sw, sw, 0, sw).
+//
+// The records are laid out tile-major, exactly as one B fragment sits in
+// LDS: per 32-row group and block one 1 KB chunk, [half][32 rows][16 B]
+// (half 0 = each record's first 16 bytes). Rows past the matrix, up to the
+// group's 32, hold zero records. One 16-byte LDS DMA per lane moves a whole
+// chunk from HBM into LDS, with no registers and no staging pass.
+
+constexpr int kChunk = 1024;  // one (32-row group, block) of the prepack
 
 DNX_DEV uint32_t f6_signed_code(uint32_t q) {
   return q >= 8 ? q - 8 : 0x20u | (8 - q);
 }
 
-// One thread per (row, block): 16 nibble bytes + the fp16 scale -> 32 bytes.
+// One thread per (row, block) of the matrix padded to whole 32-row groups:
+// 16 nibble bytes + the fp16 scale -> the record's two halves.
 __global__ void __launch_bounds__(kPanelThreads) pack_q4_f6_kernel(
     const uint8_t* __restrict__ qs, const uint16_t* __restrict__ scales,
-    uint8_t* __restrict__ out, int64_t count) {
+    uint8_t* __restrict__ out, int rows, int B, int64_t count) {
   for (int64_t i = (int64_t)blockIdx.x * kPanelThreads + threadIdx.x; i < count;
        i += (int64_t)gridDim.x * kPanelThreads) {
-    const uint4 v = *(const uint4*)(qs + i * 16);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const int r = (int)(i / B), b = (int)(i - (int64_t)r * B);
     uint32_t o[6] = {0, 0, 0, 0, 0, 0};
+    uint32_t sw = 0;
+    if (r < rows) {
+      const uint4 v = *(const uint4*)(qs + i * 16);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int f = 0; f < 32; f++) {
-      const int k = kFieldKHost[f];
-      const int byte = k & 15;
-      const uint32_t q = (w[byte >> 2] >> (8 * (byte & 3) + (k >= 16 ? 4 : 0))) & 15u;
-      const uint32_t c = f6_signed_code(q);
-      const int bit = 6 * f, wd = bit >> 5, sh = bit & 31;
-      o[wd] |= c << sh;
-      if (sh > 26) o[wd + 1] |= c >> (32 - sh);
+      for (int f = 0; f < 32; f++) {
+        const int k = kFieldKHost[f];
+        const int byte = k & 15;
+        const uint32_t q = (w[byte >> 2] >> (8 * (byte & 3) + (k >= 16 ? 4 : 0))) & 15u;
+        const uint32_t c = f6_signed_code(q);
+        const int bit = 6 * f, wd = bit >> 5, sh = bit & 31;
+        o[wd] |= c << sh;
+        if (sh > 26) o[wd + 1] |= c >> (32 - sh);
+      }
+      sw = scales[i];
     }
-    const uint32_t sw = scales[i];
-    uint4* d = (uint4*)(out + i * 32);
-    d[0] = make_uint4(o[0], o[1], o[2], o[3]);
-    d[1] = make_uint4(o[4], o[5], sw | (sw << 16), sw << 16);
+    uint8_t* d = out + ((int64_t)(r >> 5) * B + b) * kChunk + (r & 31) * 16;
+    *(uint4*)d = make_uint4(o[0], o[1], o[2], o[3]);
+    *(uint4*)(d + kChunk / 2) = make_uint4(o[4], o[5], sw | (sw << 16), sw << 16);
   }
 }
 
-constexpr int kPKB = 16;    // blocks per stage of the prepacked GEMM
+constexpr int kPKB = 8;     // blocks per stage of the prepacked GEMM
+static_assert(kKB % kPKB == 0, "a K split holds whole prepacked stages");
 
 struct F6PParams {
-  const uint8_t* packed;   // [rows][cols/32][32 B]
+  const uint8_t* packed;   // tile-major prepack [groups of 32 rows][cols/32][1 KB]
   const uint8_t* panel;    // f6 panel of the n tokens
   float* y;
   float* part;
   int rows, cols, n;
   int tiles_m, tiles;
-  int split_blocks;        // a multiple of kPKB
+  int split_blocks;        // a multiple of kKB (whole stages)
   int vec;                 // the output allows 16-byte stores
 };
 
+// Stages of kPKB blocks; a stage's weights (kPKB x SN chunks, 24 KB) move
+// into one of two LDS buffers by DMA, three chunks per wave, issued at the
+// start of the stage before: they arrive while that stage computes. The
+// activation records stay in a register ring one stage (kPKB / 2 own
+// blocks) ahead. The DMA is inline asm (buffer_load16_to_lds), so the
+// compiler's waits ignore it; each stage ends with an explicit vmcnt that
+// covers this wave's DMA (only the stage's ring refills are younger) and a
+// barrier that publishes every wave's DMA and retires the buffer just read.
 template <int SN>
 __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   constexpr int BN = SN * 32;
-  constexpr int kHalf = BN * 16 + 16;           // one (block, half): BN rows x 16 B (+ bank pad)
-  constexpr int kStage = kPKB * 2 * kHalf;
-  constexpr int kPieces = BN * kPKB * 2;        // 16-byte pieces per stage
-  constexpr int PW = (kPieces + kThreads - 1) / kThreads;
+  constexpr int kStage = kPKB * SN * kChunk;
+  constexpr int kChunks = kPKB * SN;                  // DMA chunks per stage
+  constexpr int kPerWave = (kChunks + kWaves - 1) / kWaves;
+  constexpr int kRingP = kPKB / 2;                    // own-parity blocks per stage
   constexpr int kLds = 2 * kStage > epilogue_lds_bytes<SN>() ? 2 * kStage : epilogue_lds_bytes<SN>();
   __shared__ __align__(16) uint8_t lds[kLds];
 
@@ -553,45 +577,35 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int mg = wave & 3, kp = wave >> 2;
   const int K = p.cols, B = K / kBlock, M = p.n, N = p.rows;
+  const int groups_n = (N + 31) >> 5;
 
   const int i = blockIdx.x;
   const int t = (p.tiles % 8 == 0) ? (i % 8) * (p.tiles / 8) + i / 8 : i;
   const int tm = t % p.tiles_m, tn = t / p.tiles_m;
-  const int n0 = tn * BN;
+  const int n0 = tn * BN, g0 = tn * SN;
   const int groups = (M + kTokens - 1) / kTokens;
   const int g = tm * kTileM + mg;
   const int b_begin = blockIdx.y * p.split_blocks;
   const int b_end = min(B, b_begin + p.split_blocks);
   const int stages = (b_end - b_begin + kPKB - 1) / kPKB;
   const i32x4 rpanel = buffer_rsrc(p.panel, (uint32_t)((size_t)groups * B * kRec));
+  const i32x4 rpk = buffer_rsrc(p.packed, (uint32_t)((size_t)groups_n * B * kChunk));
+  const uint32_t lds0 = lds_address(lds);
 
-  // Staging of a stage through registers: thread q of a pass takes the
-  // 16-byte half (q % 2) of record (row, block) with the block and half
-  // fastest, so a wave reads 1 KB of consecutive records; the halves go to
-  // LDS [block][half][row][16 B] (rows consecutive: conflict-free reads of a
-  // tile's 32 rows). Rows past the matrix and blocks past this split read a
-  // valid row / block instead (clamped): their products meet zero
-  // activations or are never stored.
-  const i32x4 rpk = buffer_rsrc(p.packed, (uint32_t)((size_t)N * B * 32));
-  i32x4 rw[PW];
-  auto load_w = [&](int s) {
+  // Stage s's weights into buffer `buf`, chunk (kb, j) at [kb][j]. Blocks
+  // past this split and groups past the matrix read a valid chunk instead
+  // (clamped): their products meet zero activations or are never stored.
+  auto dma_w = [&](int s, int buf) {
     const int b0 = b_begin + s * kPKB;
 #pragma unroll
-    for (int e = 0; e < PW; e++) {
-      const int q = e * kThreads + tid;
-      const int h = q & 1, kb = (q >> 1) % kPKB, row = (q >> 1) / kPKB;
-      const int b = min(b0 + kb, b_end - 1);
-      const int grow = min(n0 + row, N - 1);
-      rw[e] = dnx_raw_buffer_load_v4i32(rpk, ((grow * B + b) * 32 + h * 16) | (q < kPieces ? 0 : -(1 << 30)), 0, 0);
-    }
-  };
-  auto store_w = [&](int buf) {
-#pragma unroll
-    for (int e = 0; e < PW; e++) {
-      const int q = e * kThreads + tid;
-      if (q >= kPieces) continue;
-      const int h = q & 1, kb = (q >> 1) % kPKB, row = (q >> 1) / kPKB;
-      *(i32x4*)(lds + buf * kStage + (kb * 2 + h) * kHalf + row * 16) = rw[e];
+    for (int e = 0; e < kPerWave; e++) {
+      const int c = wave * kPerWave + e;
+      if (c < kChunks) {
+        const int kb = c / SN, j = c - kb * SN;
+        const int b = min(b0 + kb, b_end - 1);
+        const int gg = min(g0 + j, groups_n - 1);
+        buffer_load16_to_lds(rpk, lds0 + buf * kStage + c * kChunk, (gg * B + b) * kChunk + lane * 16);
+      }
     }
   };
 
@@ -599,8 +613,8 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   auto load_a = [&](int b, i32x4& lo, i32x4& hi) {
     const int ok = -(int)(live & (b < b_end));
     const int base = (((g * B + b) * kRec + kRecF) & ok) | (~ok & -(1 << 20));
-    lo = dnx_raw_buffer_load_v4i32(rpanel, base + lane * 32, 0, 0);
-    hi = dnx_raw_buffer_load_v4i32(rpanel, base + lane * 32 + 16, 0, 0);
+    lo = dnx_raw_buffer_load_v4i32(rpanel, base + lane * 16, 0, 0);
+    hi = dnx_raw_buffer_load_v4i32(rpanel, base + kRecHalf + lane * 16, 0, 0);
   };
 
   v16f acc[SN];
@@ -621,17 +635,16 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[j][v] = fmaf(pd[v], ps[v], acc[j][v]);
   };
-  // B fragment of one tile: the 24 code bytes (w0 + wc) and the scale pair ws.
+  // B fragment of one tile: lane l takes row l % 32's record (both lane
+  // halves the same weights: the K slots of the h and the l codes).
   struct BFrag {
-    uint4 w0;
-    uint2 wc, ws;
+    uint4 h0, h1;
   };
   auto read_b = [&](const uint8_t* sbase, int kb, int j) {
-    const uint8_t* q = sbase + (kb * 2) * kHalf + (lane & 31) * 16 + j * 32 * 16;
+    const uint8_t* q = sbase + (kb * SN + j) * kChunk + (lane & 31) * 16;
     BFrag f;
-    f.w0 = *(const uint4*)q;
-    f.wc = *(const uint2*)(q + kHalf);
-    f.ws = *(const uint2*)(q + kHalf + 8);
+    f.h0 = *(const uint4*)q;
+    f.h1 = *(const uint4*)(q + kChunk / 2);
     return f;
   };
   // One block of K for the SN tiles; `nb` holds tile 0 of this block on
@@ -644,9 +657,9 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
     BFrag cur = nb;
 #pragma unroll
     for (int j = 0; j < SN; j++) {
-      const v8i bq = {(int)cur.w0.x, (int)cur.w0.y, (int)cur.w0.z, (int)cur.w0.w,
-                      (int)cur.wc.x, (int)cur.wc.y, 0, 0};
-      const h4 bs = __builtin_bit_cast(h4, cur.ws);
+      const v8i bq = {(int)cur.h0.x, (int)cur.h0.y, (int)cur.h0.z, (int)cur.h0.w,
+                      (int)cur.h1.x, (int)cur.h1.y, 0, 0};
+      const h4 bs = __builtin_bit_cast(h4, make_uint2(cur.h1.z, cur.h1.w));
       const v16f z = {};
       const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(as, bs, z, 0, 0, 0);
       const v16f d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bq, z, 2, 2, 0, sa, 0, 130);
@@ -659,37 +672,36 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
       pd = d;
       ps = sc;
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // the two MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);   // next fragments
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // next fragment
       __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // previous fold
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  i32x4 rlo[kRing], rhi[kRing];
+  i32x4 rlo[kRingP], rhi[kRingP];
+  dma_w(0, 0);
 #pragma unroll
-  for (int r = 0; r < kRing; r++) load_a(b_begin + kp + 2 * r, rlo[r], rhi[r]);
-  load_w(0);
-  store_w(0);
+  for (int r = 0; r < kRingP; r++) load_a(b_begin + kp + 2 * r, rlo[r], rhi[r]);
+  if (stages > 1) dma_w(1, 1);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int s = 0; s < stages; s++) {
     const int buf = s & 1;
-    if (s + 1 < stages) load_w(s + 1);
+    // W(s + 1) into the buffer stage s - 1 read (every wave is past it).
+    if (s >= 1 && s + 1 < stages) dma_w(s + 1, buf ^ 1);
     const uint8_t* sbase = lds + buf * kStage;
     const int b0 = b_begin + s * kPKB;
-    // Tile 0 of the stage's first block; later blocks get theirs from the
-    // block before (clamped to the stage: the last block's read is unused).
     BFrag nb = read_b(sbase, kp, 0);
-#pragma unroll 1
-    for (int u0 = 0; u0 < kPKB / 2; u0 += kRing) {
 #pragma unroll
-      for (int r = 0; r < kRing; r++) {
-        const int kb = kp + 2 * (u0 + r);
-        compute(sbase, kb, min(kb + 2, kPKB - 1), rlo[r], rhi[r], nb);
-        load_a(b0 + kb + 2 * kRing, rlo[r], rhi[r]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int r = 0; r < kRingP; r++) {
+      const int kb = kp + 2 * r;
+      compute(sbase, kb, min(kb + 2, kPKB - 1), rlo[r], rhi[r], nb);
+      load_a(b0 + kb + 2 * kRingP, rlo[r], rhi[r]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (s + 1 < stages) store_w(buf ^ 1);
+    // This wave's W(s + 1) has landed: only the 2 * kRingP ring refills of
+    // this stage were issued after it.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2 * kRingP));
     __syncthreads();
   }
   fold(SN - 1);
@@ -703,7 +715,7 @@ __global__ void __launch_bounds__(256) f6_splitk_reduce_kernel(const float* __re
                                                                int64_t count, int splits) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count;
        i += (int64_t)gridDim.x * 256) {
-    y[i] = split_sum(part, count, i, splits);
+    store_wt(y + i, split_sum(part, count, i, splits));
   }
 }
 
@@ -772,6 +784,12 @@ bool f6_shape_ok(int64_t rows, int64_t cols, int64_t n) {
          rows * (cols / kBlock) * 2 < (1ll << 31) && n * rows < (1ll << 31);
 }
 
+// The prepacked operand (whole 32-row groups, 1 KB per group and block)
+// below 2 GB as well.
+bool f6p_shape_ok(int64_t rows, int64_t cols, int64_t n) {
+  return f6_shape_ok(rows, cols, n) && (rows + 31) / 32 * (cols / kBlock) * kChunk < (1ll << 31);
+}
+
 template <int SN>
 int launch_f6(const uint8_t* qs, const uint16_t* scales, const uint8_t* panel, float* y,
               int64_t rows, int64_t cols, int64_t n, hipStream_t stream) {
@@ -832,14 +850,16 @@ int launch_f6p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t ro
   p.tiles_m = (int)((n + kTileM * kTokens - 1) / (kTileM * kTokens));
   p.tiles = p.tiles_m * (int)((rows + BN - 1) / BN);
   const int B = (int)(cols / kBlock);
+  // The same split of K as launch_f6 (whole kKB-block parts, kKB a multiple
+  // of kPKB), so that both kernels add the same partials in the same order.
   int splits = 1;
   if (p.tiles < 192) {
     splits = (256 + p.tiles - 1) / p.tiles;
-    const int max_splits = (B + kPKB - 1) / kPKB;
+    const int max_splits = (B + kKB - 1) / kKB;
     if (splits > max_splits) splits = max_splits;
   }
   p.split_blocks = (B + splits - 1) / splits;
-  p.split_blocks = (p.split_blocks + kPKB - 1) / kPKB * kPKB;
+  p.split_blocks = (p.split_blocks + kKB - 1) / kKB * kKB;
   splits = (B + p.split_blocks - 1) / p.split_blocks;
   const int64_t count = n * rows;
   p.part = nullptr;
@@ -917,24 +937,25 @@ int dnx_gemm_q4_f6(const uint8_t* qs, const uint16_t* scales, const void* panel,
 
 int64_t dnx_q4_f6pack_bytes(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0 || cols % kBlock != 0) return -1;
-  return rows * (cols / kBlock) * 32;
+  return (rows + 31) / 32 * (cols / kBlock) * kChunk;
 }
 
 int dnx_pack_q4_f6(const uint8_t* qs, const uint16_t* scales, void* packed, int64_t rows,
                    int64_t cols, dnx_stream_t stream) {
-  if (rows <= 0 || cols <= 0 || cols % kBlock != 0 || ((uintptr_t)qs & 15) ||
+  if (rows <= 0 || cols <= 0 || cols % kBlock != 0 || rows >= (1ll << 31) || ((uintptr_t)qs & 15) ||
       ((uintptr_t)scales & 1) || ((uintptr_t)packed & 15)) {
     return DNX_EINVAL;
   }
-  const int64_t count = rows * (cols / kBlock);
+  const int64_t count = (rows + 31) / 32 * 32 * (cols / kBlock);
   hipLaunchKernelGGL(pack_q4_f6_kernel, dim3(panel_grid(count)), dim3(kPanelThreads), 0,
-                     (hipStream_t)stream, qs, scales, (uint8_t*)packed, count);
+                     (hipStream_t)stream, qs, scales, (uint8_t*)packed, (int)rows,
+                     (int)(cols / kBlock), count);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 
 int dnx_gemm_q4_f6p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
                     int64_t n, dnx_stream_t stream) {
-  if (!f6_shape_ok(rows, cols, n) || ((uintptr_t)panel & 15) || ((uintptr_t)packed & 15) ||
+  if (!f6p_shape_ok(rows, cols, n) || ((uintptr_t)panel & 15) || ((uintptr_t)packed & 15) ||
       ((uintptr_t)y & 3)) {
     return DNX_EINVAL;
   }
@@ -946,7 +967,7 @@ int64_t dnx_gemm_q4_f6p_noalloc_max_floats(void) { return (int64_t)kScratchFloat
 
 int dnx_gemm_q4_f6p_noalloc(const void* packed, const void* panel, float* y, int64_t rows,
                             int64_t cols, int64_t n, dnx_stream_t stream) {
-  if (!f6_shape_ok(rows, cols, n) || ((uintptr_t)panel & 15) || ((uintptr_t)packed & 15) ||
+  if (!f6p_shape_ok(rows, cols, n) || ((uintptr_t)panel & 15) || ((uintptr_t)packed & 15) ||
       ((uintptr_t)y & 3)) {
     return DNX_EINVAL;
   }

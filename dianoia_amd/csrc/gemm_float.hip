@@ -260,7 +260,7 @@ __global__ void __launch_bounds__(kThreads) gemm_float_kernel(FParams p) {
 #pragma unroll
     for (int v = 0; v < 16; v++) {
       const int m = m0 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      if (m < M) out[(size_t)m * N + r] = acc[j][v];
+      if (m < M) store_wt(out + (size_t)m * N + r, acc[j][v]);
     }
   }
 }
@@ -270,7 +270,7 @@ __global__ void __launch_bounds__(kThreads) float_splitk_reduce_kernel(
     const float* __restrict__ part, float* __restrict__ y, int64_t count, int splits) {
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < count;
        i += (int64_t)gridDim.x * kThreads) {
-    y[i] = split_sum(part, count, i, splits);
+    store_wt(y + i, split_sum(part, count, i, splits));
   }
 }
 

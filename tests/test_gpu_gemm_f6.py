@@ -187,11 +187,22 @@ FIELD_K = [0, 20, 17, 6, 3, 23, 16, 5, 2, 22, 19, 4, 1, 21, 18, 7,
            8, 28, 25, 14, 11, 31, 24, 13, 10, 30, 27, 12, 9, 29, 26, 15]
 
 
+def packed_records(packed, rows, cols):
+    """The tile-major prepack ([32-row group][block][half][32 rows][16 B])
+    as one 32-byte record per (row, block); also checks that the rows that
+    pad the last group hold zero records."""
+    groups, nb = (rows + 31) // 32, cols // 32
+    chunks = packed.reshape(groups, nb, 2, 32, 16)
+    rec = chunks.transpose(0, 3, 1, 2, 4).reshape(groups * 32, nb, 32)
+    assert not rec[rows:].any()
+    return np.ascontiguousarray(rec[:rows])
+
+
 def decode_packed(packed, rows, cols):
     """Record (row, block) -> the 32 signed weights its fp6 fields encode
     (E2M3: sign bit 5, magnitude code |w| <= 8 is the value |w| / 8, here
     times the kernel's scale 8) and its two operand dwords."""
-    rec = packed.reshape(rows, cols // 32, 32)
+    rec = packed_records(packed, rows, cols)
     words = rec[:, :, :24].copy().view(np.uint32).astype(np.uint64)   # 6 dwords
     bits = np.zeros(words.shape[:2], dtype=object)
     w = np.zeros((rows, cols // 32, 32), np.int64)
