@@ -313,27 +313,45 @@ def bench_c3(torch, D, synth, timer, steps, warmup):
            "gemm_frac_i8": ops / b["gemm_ms"] / 1e9 / I8_PEAK_TOPS, "gemm_path": best,
            "paths": {k: dict(v, gemm_tops=ops / v["gemm_ms"] / 1e9) for k, v in paths.items()}}
     out["issue_floor"] = c3_issue_floor(M, N, K)
-    # M = 1..256 sweep: GEMV (exact order) up to 4 tokens, GEMM beyond. The
-    # batch shapes of the kernels' other callers (audio encoder / generator
-    # and vision attention projections) lie in this range.
+    # M = 1..256 sweep on the ABI's route (lab_gpu_enc_matmul_q4): the GEMV
+    # (exact order) up to 4 tokens; prefill chunks of 5..64 tokens (the
+    # reference's prefill, lib/src/model.dart:91) as the fp6 panel quantizer
+    # + the chunk GEMM on the weights' prepack (made once, at first use);
+    # the int8-MFMA GEMM beyond. The batch shapes of the kernels' other
+    # callers (audio encoder / generator and vision attention projections)
+    # lie in this range. Beside each GEMM: the other route's time.
     sweep = {}
     for m in (1, 2, 4, 8, 16, 32, 64, 128, 256):
         xm = xd[:m].contiguous()
         ym = torch.empty((m, N), device="cuda")
+        xqm = torch.empty((m, K), dtype=torch.int8, device="cuda")
+        xsm = torch.empty((m, K // 32), device="cuda")
+        pm = torch.empty((D.f6_panel_bytes(m, K),), dtype=torch.uint8, device="cuda")
+
+        def int8_route(i, xm=xm, ym=ym, m=m, xqm=xqm, xsm=xsm):
+            D.quantize_q8(xm, xqm, xsm, m, K, K)
+            D.gemm_q4(ws[i % copies][0], ws[i % copies][1], xqm, xsm, ym, N, K, m)
+
+        def chunk_route(i, xm=xm, ym=ym, m=m, pm=pm):
+            D.quantize_q8_f6panel(xm, pm, m, K)
+            D.gemm_q4_f6s(packed[i % copies], pm, ym, N, K, m)
+
+        nbytes = q4_bytes(N, K) + m * K * 4 + m * N * 4
         if m <= 4:
             fn = lambda i, xm=xm, ym=ym, m=m: D.gemv_q4(ws[i % copies][0], ws[i % copies][1],  # noqa: E731
                                                         xm, ym, N, K, m)
+            kernel, other = "gemv_q4", None
+        elif m <= 64:
+            fn, kernel = chunk_route, "quantize_f6panel + gemm_f6s (prepacked chunk GEMM)"
+            other = ("int8_route_ms", int8_route)
         else:
-            xqm = torch.empty((m, K), dtype=torch.int8, device="cuda")
-            xsm = torch.empty((m, K // 32), device="cuda")
-
-            def fn(i, xm=xm, ym=ym, m=m, xqm=xqm, xsm=xsm):
-                D.quantize_q8(xm, xqm, xsm, m, K, K)
-                D.gemm_q4(ws[i % copies][0], ws[i % copies][1], xqm, xsm, ym, N, K, m)
+            fn, kernel = int8_route, "quantize_q8 + gemm_q4 (int8 MFMA)"
+            other = ("chunk_route_ms", chunk_route)
         t = timer.time(fn, n, 3)
-        nbytes = q4_bytes(N, K) + m * K * 4 + m * N * 4
         sweep[str(m)] = {"ms": t, "gbps": nbytes / t / 1e6, "tops": 2 * m * N * K / t / 1e9,
-                         "kernel": "gemv_q4" if m <= 4 else "quantize+gemm_q4"}
+                         "kernel": kernel}
+        if other is not None:
+            sweep[str(m)][other[0]] = timer.time(other[1], n, 3)
     out["sweep_m"] = sweep
     return out
 
@@ -486,6 +504,29 @@ def bench_callers(torch, D, synth, timer, steps):
         key = f"{who}_{fmt}_{rows}x{cols}_n{n}" + ("" if int8 else "_float_inputs")
         out[key] = {"ms": ms, "weight_gbps": nbytes / ms / 1e6,
                     "tops": 2 * n * rows * cols / ms / 1e9, "weight_copies": copies}
+        if fmt == "q4" and int8 and n > 4:
+            # The chunk GEMM on the weights' prepack, which the lab_gpu_*
+            # command buffer keeps per weight region (its route for 5..64
+            # tokens; timed here at the other token counts too).
+            packs = [torch.empty((D.q4_f6pack_bytes(rows, cols),), dtype=torch.uint8,
+                                 device="cuda") for _ in range(len(ws))]
+            for w, pk in zip(ws, packs):
+                D.pack_q4_f6(w[0], w[1], pk, rows, cols)
+            pnl = torch.empty((D.f6_panel_bytes(n, cols),), dtype=torch.uint8, device="cuda")
+
+            def chunk(i, packs=packs, pnl=pnl, x=x, y=y, rows=rows, cols=cols, n=n):
+                D.quantize_q8_f6panel(x, pnl, n, cols)
+                D.gemm_q4_f6s(packs[i % len(packs)], pnl, y, rows, cols, n)
+
+            cms = timer.time(chunk, reps, 3)
+            out[key]["chunk_route_ms"] = cms
+            if n <= 64:
+                out[key].update({"dnx_matmul_ms": ms, "ms": cms,
+                                 "weight_gbps": nbytes / cms / 1e6,
+                                 "tops": 2 * n * rows * cols / cms / 1e9,
+                                 "route": "lab_gpu_enc_matmul_q4: quantize_f6panel + gemm_f6s "
+                                          "(prepack)"})
+            del packs
         del ws
         torch.cuda.empty_cache()
     return out

@@ -709,6 +709,129 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   store_tile_sums<SN>(lds, acc, wave, lane, tm * kTileM * kTokens, n0, M, N, out, p.vec != 0);
 }
 
+// ------------------------------------------- skinny prefill (5..64 tokens)
+//
+// A prefill chunk of at most 64 tokens (the reference prefills in chunks of
+// up to 64, lib/src/model.dart:91) against a whole weight matrix: the
+// weights dominate the bytes, the MFMA work is small. One workgroup owns 32
+// weight rows and 64 tokens (G groups of 32; more tokens take more
+// workgroups along y, which read the same weights) over the whole K, so no
+// K split, no partials and no reduce launch: its 8 waves take blocks b = w,
+// w + 8, ..., each wave loads its B chunks (the prepack) and A records (the
+// panel) straight into a 4-block register ring, runs the fp6 dot and the
+// scale MFMA per (token group, block) and folds; then the 8 waves' sums are
+// added through LDS in wave order (deterministic) and stored write-through.
+
+constexpr int kSkRing = 4;      // blocks in flight per wave
+
+struct F6SParams {
+  const uint8_t* packed;   // tile-major prepack
+  const uint8_t* panel;    // f6 panel of the n tokens
+  float* y;                // [n][rows]
+  int rows, cols, n;
+};
+
+template <int G>
+__global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
+  constexpr int kOut = G * kTokens * 32;               // outputs of the workgroup
+  __shared__ __align__(16) float red[kWaves * kOut];   // each wave's sums, [wave][token][row]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int K = p.cols, B = K / kBlock, M = p.n, N = p.rows;
+  const int rg = blockIdx.x;                           // 32-row group
+  const int t0 = blockIdx.y * G;                       // first token group
+  const int groups = (M + kTokens - 1) / kTokens;
+  const int groups_n = (N + 31) >> 5;
+  const i32x4 rpanel = buffer_rsrc(p.panel, (uint32_t)((size_t)groups * B * kRec));
+  const i32x4 rpk = buffer_rsrc(p.packed, (uint32_t)((size_t)groups_n * B * kChunk));
+
+  // Block i of this wave is b = wave + 8 i; blocks past K read zeros (offset
+  // past the resources), so their products vanish.
+  struct Slot {
+    i32x4 w0, w1;       // B: the record halves of row lane % 32
+    i32x4 lo[G], hi[G]; // A: the token groups' lane records
+  };
+  auto load = [&](int i, Slot& sl) {
+    const int b = wave + kWaves * i;
+    const int ok = -(int)(b < B);
+    const int wb = ((rg * B + b) * kChunk & ok) | (~ok & -(1 << 30));
+    sl.w0 = dnx_raw_buffer_load_v4i32(rpk, wb + (lane & 31) * 16, 0, 0);
+    sl.w1 = dnx_raw_buffer_load_v4i32(rpk, wb + kChunk / 2 + (lane & 31) * 16, 0, 0);
+#pragma unroll
+    for (int t = 0; t < G; t++) {
+      const int tok = -(int)(t0 + t < groups);
+      const int ab = ((((t0 + t) * B + b) * kRec + kRecF) & ok & tok) | (~(ok & tok) & -(1 << 30));
+      sl.lo[t] = dnx_raw_buffer_load_v4i32(rpanel, ab + lane * 16, 0, 0);
+      sl.hi[t] = dnx_raw_buffer_load_v4i32(rpanel, ab + kRecHalf + lane * 16, 0, 0);
+    }
+  };
+
+  v16f acc[G];
+#pragma unroll
+  for (int t = 0; t < G; t++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
+  const int nb = (B - wave + kWaves - 1) / kWaves;     // this wave's blocks
+  Slot ring[kSkRing];
+#pragma unroll
+  for (int r = 0; r < kSkRing; r++) load(r, ring[r]);
+  for (int i0 = 0; i0 < nb; i0 += kSkRing) {
+#pragma unroll
+    for (int r = 0; r < kSkRing; r++) {
+      Slot& sl = ring[r];
+      asm volatile("" : "+v"(sl.w0), "+v"(sl.w1));
+      const v8i bq = {sl.w0[0], sl.w0[1], sl.w0[2], sl.w0[3], sl.w1[0], sl.w1[1], 0, 0};
+      const h4 bs = __builtin_bit_cast(h4, make_uint2((uint32_t)sl.w1[2], (uint32_t)sl.w1[3]));
+#pragma unroll
+      for (int t = 0; t < G; t++) {
+        i32x4 lo = sl.lo[t], hi = sl.hi[t];
+        asm volatile("" : "+v"(lo), "+v"(hi));
+        const v8i a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        const h4 as = __builtin_bit_cast(h4, make_uint2((uint32_t)hi[2], (uint32_t)hi[3]));
+        const v16f z = {};
+        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(as, bs, z, 0, 0, 0);
+        const v16f d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bq, z, 2, 2, 0, hi[3],
+                                                                       0, 130);
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[t][v] = fmaf(d[v], sc[v], acc[t][v]);
+      }
+      load(i0 + r + kSkRing, sl);
+    }
+  }
+
+  // Each wave's sums into LDS as [token][row], then every thread adds one
+  // float4 of rows over the 8 waves in wave order and stores it.
+  float* mine = red + wave * kOut;
+#pragma unroll
+  for (int t = 0; t < G; t++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int m = t * kTokens + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+      mine[m * 32 + (lane & 31)] = acc[t][v];
+    }
+  __syncthreads();
+  for (int q = tid; q < kOut / 4; q += kThreads) {
+    const int m = q >> 3, c = (q & 7) * 4;
+    float4 o = *(const float4*)(red + m * 32 + c);
+#pragma unroll
+    for (int w = 1; w < kWaves; w++) {
+      const float4 e = *(const float4*)(red + w * kOut + m * 32 + c);
+      o = make_float4(o.x + e.x, o.y + e.y, o.z + e.z, o.w + e.w);
+    }
+    const int r = rg * 32 + c, mt = t0 * kTokens + m;
+    if (mt >= M || r >= N) continue;
+    float* dst = p.y + (size_t)mt * N + r;
+    if (r + 3 < N && ((uintptr_t)dst & 15) == 0) {
+      store_wt4(dst, o);
+    } else {
+      store_wt(dst, o.x);
+      if (r + 1 < N) store_wt(dst + 1, o.y);
+      if (r + 2 < N) store_wt(dst + 2, o.z);
+      if (r + 3 < N) store_wt(dst + 3, o.w);
+    }
+  }
+}
+
 // y = the split partials summed in split order (deterministic).
 __global__ void __launch_bounds__(256) f6_splitk_reduce_kernel(const float* __restrict__ part,
                                                                float* __restrict__ y,
@@ -961,6 +1084,28 @@ int dnx_gemm_q4_f6p(const void* packed, const void* panel, float* y, int64_t row
   }
   return launch_f6p<3>((const uint8_t*)packed, (const uint8_t*)panel, y, rows, cols, n,
                        (hipStream_t)stream);
+}
+
+int dnx_gemm_q4_f6s(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
+                    int64_t n, dnx_stream_t stream) {
+  if (!f6p_shape_ok(rows, cols, n) || n > 65535 * 2 * kTokens || ((uintptr_t)panel & 15) ||
+      ((uintptr_t)packed & 15) || ((uintptr_t)y & 3)) {
+    return DNX_EINVAL;
+  }
+  F6SParams p{};
+  p.packed = (const uint8_t*)packed;
+  p.panel = (const uint8_t*)panel;
+  p.y = y;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.n = (int)n;
+  const dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((n + 2 * kTokens - 1) / (2 * kTokens)));
+  if (n > kTokens) {
+    hipLaunchKernelGGL(gemm_f6s_kernel<2>, grid, dim3(kThreads), 0, (hipStream_t)stream, p);
+  } else {
+    hipLaunchKernelGGL(gemm_f6s_kernel<1>, grid, dim3(kThreads), 0, (hipStream_t)stream, p);
+  }
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 
 int64_t dnx_gemm_q4_f6p_noalloc_max_floats(void) { return (int64_t)kScratchFloats; }

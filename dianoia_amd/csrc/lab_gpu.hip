@@ -356,6 +356,15 @@ void after_dispatch(int kind) {
   }
 }
 
+// A fused launch (the commit peepholes below) runs several encoded
+// commands: its time goes to the kind of its main kernel (after_dispatch),
+// and every other command it ran is counted under its own kind with no time
+// of its own, so the profile counts the same dispatches per kind as one
+// launch per command would.
+void also_ran(int kind, int times = 1) {
+  if (gProfiling) gKindCount[kind] += times;
+}
+
 // Grows the matmul workspace to what a command of this shape needs (at
 // encode time: outside the commit that launches it).
 bool grow_scratch(int64_t cols, int64_t n) {
@@ -401,13 +410,101 @@ void record(Op op, std::initializer_list<int64_t> args) {
   gCmds.push_back(c);
 }
 
+// Prepacked copies of Q4 weight matrices for the fp6 GEMMs (the routes of
+// prefill chunks, dnx::matmul_uses_f6_chunk, and of large prefill shapes,
+// dnx::matmul_uses_f6). Weights are immutable once used (use_as_weights), so
+// a matrix region is re-encoded once, on its first such matmul, into the
+// GEMMs' tile-major layout (dnx_pack_q4_f6), and every later prefill of it
+// runs on the prepack. The copy's memory is
+// reserved when the command is encoded (no allocation inside a commit); it
+// is freed with the buffer. Not a live buffer: lab_gpu_live_buffers does not
+// count it.
+struct Prepack {
+  int64_t handle, qs_off, sc_off, rows, cols;
+  void* dev;
+  bool packed;
+};
+std::vector<Prepack> gPrepacks;
+
+Prepack* find_prepack(int64_t h, int64_t qs_off, int64_t sc_off, int64_t rows, int64_t cols) {
+  for (Prepack& p : gPrepacks) {
+    if (p.handle == h && p.qs_off == qs_off && p.sc_off == sc_off && p.rows == rows &&
+        p.cols == cols) {
+      return &p;
+    }
+  }
+  return nullptr;
+}
+
+// At encode time: the prepack a Q4 int8-input matmul of this shape will use,
+// reserved now. Where the device has no memory for it (or the copy would
+// pass the GEMM's 2 GB operand limit) the command runs on the engine layout.
+void reserve_prepack(int64_t h, int64_t qs_off, int64_t sc_off, int64_t rows, int64_t cols) {
+  if (find_prepack(h, qs_off, sc_off, rows, cols) != nullptr) return;
+  const int64_t bytes = dnx_q4_f6pack_bytes(rows, cols);
+  void* dev = nullptr;
+  if (bytes <= 0 || bytes >= (1ll << 31) || hipMalloc(&dev, (size_t)bytes) != hipSuccess) return;
+  gPrepacks.push_back({h, qs_off, sc_off, rows, cols, dev, false});
+}
+
+void free_prepacks(int64_t h) {
+  for (size_t i = 0; i < gPrepacks.size();) {
+    if (gPrepacks[i].handle == h) {
+      (void)hipFree(gPrepacks[i].dev);
+      gPrepacks[i] = gPrepacks.back();
+      gPrepacks.pop_back();
+    } else {
+      i++;
+    }
+  }
+}
+
+// The prepacked route: the prepack (made on first use), the activation
+// panel from fp32 x, the GEMM: the chunk GEMM for up to 64 tokens (one
+// launch over the whole K), else the tiled GEMM (the same products as the
+// engine-layout fp6 GEMM, bit for bit).
+int run_matmul_prepacked(Prepack& pp, int64_t w, int64_t qsOff, int64_t scOff, const float* x,
+                         float* y, int64_t rows, int64_t cols, int64_t n) {
+  auto s = (dnx_stream_t)gStream;
+  int rc;
+  if (!pp.packed) {
+    rc = dnx_pack_q4_f6((const uint8_t*)dev_at(w, qsOff), (const uint16_t*)dev_at(w, scOff),
+                        pp.dev, rows, cols, s);
+    if (rc != DNX_OK) return rc;
+    after_dispatch(kKindQuantizeWeights);
+    pp.packed = true;
+  }
+  rc = dnx_quantize_q8_f6panel(x, gWs, n, cols, s);
+  if (rc != DNX_OK) return rc;
+  after_dispatch(kKindQuantize);
+  rc = dnx::matmul_uses_f6_chunk(true, n) ? dnx_gemm_q4_f6s(pp.dev, gWs, y, rows, cols, n, s)
+                                           : dnx_gemm_q4_f6p(pp.dev, gWs, y, rows, cols, n, s);
+  if (rc == DNX_OK) after_dispatch(kKindGemmQ4I8);
+  return rc;
+}
+
 // The matmul of one recorded command, on the product route of
-// matmul_route.h (the same as dnx_matmul_q8 / _q4).
+// matmul_route.h (the same as dnx_matmul_q8 / _q4), with the fp6 GEMM on a
+// prepacked copy of the weights where one is reserved.
 bool run_matmul(const Cmd& c, bool q4) {
   const int64_t w = c.a[0], qsOff = c.a[1], scOff = c.a[2], x = c.a[3], xOff = c.a[4];
   const int64_t y = c.a[5], yOff = c.a[6], rows = c.a[7], cols = c.a[8], n = c.a[9];
   use_as_weights(w);
   read_region(x, xOff, n * cols * 4);
+  Prepack* pp = q4 && c.int8_inputs && (dnx::matmul_uses_f6(true, rows, cols, n) ||
+                                         dnx::matmul_uses_f6_chunk(true, n))
+                    ? find_prepack(w, qsOff, scOff, rows, cols)
+                    : nullptr;
+  if (pp != nullptr) {
+    const int rc = run_matmul_prepacked(*pp, w, qsOff, scOff, (const float*)dev_at(x, xOff),
+                                        (float*)dev_at(y, yOff), rows, cols, n);
+    wrote_region(y, yOff, n * rows * 4);
+    if (rc != DNX_OK) {
+      LOG("matmul q4 %ldx%ld n=%ld (prepacked fp6) failed (%d)\n", (long)rows, (long)cols,
+          (long)n, rc);
+    }
+    return rc == DNX_OK;
+  }
   const int rc = dnx::matmul_route(
       q4, dev_at(w, qsOff), dev_at(w, scOff), (const float*)dev_at(x, xOff),
       (float*)dev_at(y, yOff), rows, cols, n, c.int8_inputs, gWs, gWsBytes, gStream,
@@ -467,7 +564,11 @@ int run_pair(const Cmd& a, const Cmd& b) {
          : dnx_gate_up_q8((const int8_t*)gq, (const float*)gs, (const int8_t*)uq,
                           (const float*)us, xs, h, u, rows, cols, n, gStream);
   if (rc == DNX_EINVAL) return rc;
-  if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+  if (rc == DNX_OK) {
+    after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+    also_ran(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+    also_ran(kKindSwiglu);
+  }
   wrote_region(a.a[5], 0, n * rows * 4);
   wrote_region(b.a[5], 0, n * rows * 4);
   if (rc != DNX_OK) LOG("gate/up pair %ldx%ld n=%ld failed (%d)\n", (long)rows, (long)cols, (long)n, rc);
@@ -539,7 +640,10 @@ int run_multi(const std::vector<Cmd>& cmds, size_t i, size_t len) {
          : dnx_gemv_multi_q8((const int8_t* const*)qs, (const float* const*)sc, ys, rows,
                              (int)len, xs, cols, gStream);
   if (rc == DNX_EINVAL) return rc;
-  if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+  if (rc == DNX_OK) {
+    after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+    also_ran(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8, (int)len - 1);
+  }
   for (size_t k = 0; k < len; k++) wrote_region(cmds[i + k].a[5], cmds[i + k].a[6], rows[k] * 4);
   if (rc != DNX_OK) LOG("%zu fused matmuls of width %ld failed (%d)\n", len, (long)cols, rc);
   return rc;
@@ -580,7 +684,10 @@ int run_matmul_add(const Cmd& a, const Cmd& b) {
          : dnx_gemv_add_q8((const int8_t*)dev_at(w, a.a[1]), (const float*)dev_at(w, a.a[2]), xs,
                            ys, rs, rows, cols, gStream);
   if (rc == DNX_EINVAL) return rc;
-  if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+  if (rc == DNX_OK) {
+    after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+    also_ran(kKindAdd);
+  }
   wrote_region(y, yOff, rows * 4);
   wrote_region(res, resOff, rows * 4);
   if (rc != DNX_OK) LOG("matmul + add %ldx%ld failed (%d)\n", (long)rows, (long)cols, rc);
@@ -696,7 +803,16 @@ int run_norm_matmul(const std::vector<Cmd>& cmds, size_t i, size_t len, bool pai
       wrote_region(cmds[i + 1 + k].a[5], cmds[i + 1 + k].a[6], rows[k] * 4);
     }
   }
-  if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+  if (rc == DNX_OK) {
+    after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+    also_ran(kKindRmsNorm);
+    if (pair) {
+      also_ran(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+      also_ran(kKindSwiglu);
+    } else {
+      also_ran(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8, (int)len - 1);
+    }
+  }
   wrote_region(out, outOff, cols * 4);
   if (rc != DNX_OK) LOG("rms_norm + %zu matmuls of width %ld failed (%d)\n", len, (long)cols, rc);
   return rc;
@@ -728,7 +844,10 @@ int run_add_norm(const Cmd& a, const Cmd& b) {
                                   (const float*)dev_at(w, wOff), (float*)dev_at(out, outOff), rows,
                                   cols, (float)eps, gStream);
   if (rc == DNX_EINVAL) return rc;
-  if (rc == DNX_OK) after_dispatch(kKindRmsNorm);
+  if (rc == DNX_OK) {
+    after_dispatch(kKindRmsNorm);
+    also_ran(kKindAdd);
+  }
   wrote_region(x, xOff, count * 4);
   wrote_region(out, outOff, count * 4);
   if (rc != DNX_OK) LOG("add + rms_norm %ldx%ld failed (%d)\n", (long)rows, (long)cols, rc);
@@ -769,7 +888,10 @@ int run_rope_pair(const Cmd& a, const Cmd& b) {
       (float*)dev_at(b.a[0], b.a[1]), b.a[2], (const float*)dev_at(b.a[3], b.a[4]), b.a[8],
       (const float*)dev_at(rope, ropeOff), ropeStride, hd, n, (float)eps, gStream);
   if (rc == DNX_EINVAL) return rc;
-  if (rc == DNX_OK) after_dispatch(kKindHeadNormRope);
+  if (rc == DNX_OK) {
+    after_dispatch(kKindHeadNormRope);
+    also_ran(kKindHeadNormRope);
+  }
   wrote_region(a.a[0], a.a[1], ab);
   wrote_region(b.a[0], b.a[1], bb);
   if (rc != DNX_OK) LOG("head norm + rope pair failed (%d)\n", rc);
@@ -831,7 +953,10 @@ int run_rope_attention(const Cmd& a, const Cmd& b, const Cmd& c) {
       (const float*)dev_at(b.a[3], b.a[4]), (const float*)dev_at(rope, ropeOff), (float)eps,
       gStream);
   if (rc == DNX_EINVAL) return rc;
-  if (rc == DNX_OK) after_dispatch(kKindAttention);
+  if (rc == DNX_OK) {
+    after_dispatch(kKindAttention);
+    also_ran(kKindHeadNormRope, 2);
+  }
   wrote_region(q, 0, heads * hd * 4);
   wrote_region(keys, b.a[1], kvHeads * hd * 4);
   wrote_region(out, 0, heads * hd * 4);
@@ -862,7 +987,10 @@ bool run_matmul_argmax(const Cmd& a, const Cmd& b) {
                               gGemvArgmaxWs, gStream)
          : dnx_gemv_q8_argmax((const int8_t*)qs, (const float*)sc, xs, ys, rows, cols, out,
                               gGemvArgmaxWs, gStream);
-  if (rc == DNX_OK) after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+  if (rc == DNX_OK) {
+    after_dispatch(q4 ? kKindGemvQ4I8 : kKindGemvQ8I8);
+    also_ran(kKindArgmax);
+  }
   wrote_region(y, yOff, rows * 4);
   wrote_region(b.a[3], b.a[4], 8);
   if (rc != DNX_OK) LOG("matmul+argmax %ldx%ld failed (%d)\n", (long)rows, (long)cols, rc);
@@ -1190,6 +1318,10 @@ int64_t lab_gpu_wrap_copies(void) { return 1; }
 
 void* lab_gpu_contents(int64_t handle) {
   if (!valid(handle)) return nullptr;
+  // A caller takes views here before writing through them: a SIGSEGV
+  // handler installed since the last check turns tracking off now, before
+  // those writes (a write to a protected page would go to that handler).
+  check_handler();
   Buffer& b = gBuffers[handle];
   if (b.host == nullptr) {
     // A wrapped buffer: its host view is made on request from HBM.
@@ -1218,6 +1350,7 @@ void lab_gpu_release(int64_t handle) {
   if (!valid(handle)) return;
   wait_pending();
   untrack(handle);
+  free_prepacks(handle);
   Buffer& b = gBuffers[handle];
   (void)hipFree(b.dev);
   if (b.host) (void)hipHostFree(b.host);
@@ -1230,6 +1363,7 @@ int64_t lab_gpu_live_buffers(void) { return gLive; }
 
 void lab_gpu_begin(void) {
   wait_pending();
+  check_handler();  // as in lab_gpu_contents: before the host fills inputs
   gCmds.clear();
   gFailed = false;
 }
@@ -1408,6 +1542,10 @@ static void enc_matmul(Op op, int64_t w, int64_t qsOffset, int64_t scalesOffset,
         (long)rows, (long)cols, (long)n);
     gFailed = true;
     return;
+  }
+  if (q4 && gInt8Inputs &&
+      (dnx::matmul_uses_f6(true, rows, cols, n) || dnx::matmul_uses_f6_chunk(true, n))) {
+    reserve_prepack(w, qsOffset, scalesOffset, rows, cols);
   }
   record(op, {w, qsOffset, scalesOffset, x, xOffset, y, yOffset, rows, cols, n});
 }

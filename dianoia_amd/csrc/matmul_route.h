@@ -27,6 +27,12 @@ inline bool matmul_uses_f6(bool q4, int64_t rows, int64_t cols, int64_t n) {
   return q4 && n >= 320 && rows >= 4096 && cols <= 4096;
 }
 
+// A prefill chunk (5..64 tokens; the reference prefills in chunks of up to
+// 64, lib/src/model.dart:91) of a Q4 matrix: with a prepacked copy of the
+// weights (the lab_gpu_* command buffer keeps one per weight region) it runs
+// as the f6 panel quantizer + dnx_gemm_q4_f6s, one launch over the whole K.
+inline bool matmul_uses_f6_chunk(bool q4, int64_t n) { return q4 && n >= 5 && n <= 64; }
+
 // Device bytes a route needs for its quantized activations: int8 xq and fp32
 // block scales (each 256-byte aligned), or the fp6 activation panel.
 inline int64_t matmul_workspace_bytes(int64_t cols, int64_t n) {

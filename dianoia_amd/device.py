@@ -295,6 +295,12 @@ def gemm_q4_f6p(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> 
                                        _stream(stream)), "dnx_gemm_q4_f6p")
 
 
+def gemm_q4_f6s(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
+    """The prefill chunk GEMM (n <= 64) on prepacked Q4 weights."""
+    _check(_lib.load().dnx_gemm_q4_f6s(_ptr(packed), _ptr(panel), _ptr(y), rows, cols, n,
+                                       _stream(stream)), "dnx_gemm_q4_f6s")
+
+
 def argmax_workspace(n: int, device="cuda") -> torch.Tensor:
     nbytes = int(_lib.load().dnx_argmax_workspace_bytes(n))
     return torch.empty(nbytes, dtype=torch.uint8, device=device)

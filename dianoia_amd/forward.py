@@ -325,9 +325,16 @@ class GpuForward:
             after()
 
     def forward(self, n: int, position: int, with_logits: bool = True,
-                capture: bool = False) -> None:
+                capture: bool = False, meanwhile=None) -> None:
         """GpuForward.forward (gpu.dart:1036-1239): n tokens at positions
-        position.. whose embeddings are in ``residual``."""
+        position.. whose embeddings are in ``residual``.
+
+        With ``meanwhile`` the command buffer is committed without waiting
+        (lab_gpu_commit(0)), ``meanwhile`` runs on the host while the GPU
+        computes, and the pass then waits (lab_gpu_wait), also when
+        ``meanwhile`` raises, whose error then propagates
+        (gpu.dart:1223-1233). It must not use the GPU or the buffers of the
+        pass."""
         if self._disposed:
             raise StateError("the GPU forward pass is disposed")
         if n < 1 or n > self.max_chunk:
@@ -415,9 +422,20 @@ class GpuForward:
             f = lib.lab_gpu_enc_matmul_q4 if w.q4 else lib.lab_gpu_enc_matmul_q8
             self._run("matmul", f, w.buffer, w.qs, w.scales, self._normed.handle, 0,
                       self._logits.handle, 0, w.rows, w.cols, 1)
-        if not self.split_commits:
+        if self.split_commits:
+            if meanwhile is not None:
+                meanwhile()
+        elif meanwhile is None:
             if lib.lab_gpu_commit(1) != 1:
                 raise StateError("GPU command buffer failed")
+        else:
+            if lib.lab_gpu_commit(0) != 1:
+                raise StateError("GPU command buffer failed")
+            try:
+                meanwhile()
+            finally:
+                if lib.lab_gpu_wait() != 1:
+                    raise StateError("GPU command buffer failed")
         if with_logits:
             self.logits[:] = self._logits.view
 

@@ -86,8 +86,10 @@ int dnx_gemv_q4(const uint8_t* qs, const uint16_t* scales, const float* x, float
 // :553-579), x used as given (not quantized), in the CPU's exact float order:
 // y is bit-identical to theirs. One launch per group of up to 4 tokens
 // (each reads the weights once); the group shrinks to 2 or 1 token when the
-// group's fp32 x would not fit the workgroup's 64 KB of LDS (DNX_EINVAL when
-// even one row does not: cols above about 14000).
+// group's fp32 x would not fit the workgroup's LDS: 160 KB for matrices of
+// up to 16384 rows with x of 4096 columns or more (8-wave workgroups, one
+// per CU), 64 KB otherwise. DNX_EINVAL when even one row does not fit: cols
+// above about 35000 (about 14000 for more than 16384 rows).
 int dnx_gemv_q8_float(const int8_t* qs, const float* scales, const float* x, float* y,
                       int64_t rows, int64_t cols, int64_t n, dnx_stream_t stream);
 int dnx_gemv_q4_float(const uint8_t* qs, const uint16_t* scales, const float* x, float* y,
@@ -261,15 +263,27 @@ int dnx_gemm_q4_f6(const uint8_t* qs, const uint16_t* scales, const void* panel,
 
 // The same GEMM on a load-time re-encoding of the Q4 weights: per (row,
 // block) 32 bytes holding the E2M3 codes of the signed weights q - 8 and the
-// scale MFMA's operand (dnx_q4_f6pack_bytes(rows, cols) bytes, written once
-// by dnx_pack_q4_f6 from the engine's Q4 layout; weights are immutable after
+// scale MFMA's operand, laid out tile-major (per 32-row group and block one
+// 1 KB chunk; dnx_q4_f6pack_bytes(rows, cols) bytes, written once by
+// dnx_pack_q4_f6 from the engine's Q4 layout; weights are immutable after
 // upload, as GpuLinear.upload treats them, gpu.dart:1295-1323). The GEMM
-// stages it to LDS with plain copies and needs no per-call conversion of the
-// weights; results equal dnx_gemm_q4_f6's to fp32 rounding.
+// moves the chunks into LDS by DMA and needs no per-call conversion of the
+// weights; results are bit-identical to dnx_gemm_q4_f6's (the same K split
+// and order).
 int64_t dnx_q4_f6pack_bytes(int64_t rows, int64_t cols);
 int dnx_pack_q4_f6(const uint8_t* qs, const uint16_t* scales, void* packed, int64_t rows,
                    int64_t cols, dnx_stream_t stream);
 int dnx_gemm_q4_f6p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
+                    int64_t n, dnx_stream_t stream);
+
+// The prefill chunk GEMM (lab_gemm_q4 mode 1, lab_native.c:1059-1080, at
+// the reference's prefill chunks of up to 64 tokens, lib/src/model.dart:91)
+// on prepacked weights: one launch over the whole K (no split partials, no
+// reduce launch), a workgroup per 32 rows and 64 tokens (more tokens, more
+// workgroups); exact block dots, fp32 within 1e-4 relative (1e-5 absolute
+// near zero) of the CPU kernel. Deterministic (a fixed order of the K
+// parts).
+int dnx_gemm_q4_f6s(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
                     int64_t n, dnx_stream_t stream);
 
 // dnx_gemm_q4_f6p without any allocation. No counterpart in the reference:
@@ -295,10 +309,18 @@ int dnx_gemm_q4_f6p_noalloc(const void* packed, const void* panel, float* y, int
 // int8_inputs 1 (mode 1): n <= 4 the exact GEMV above (bit-identical to
 // lab_gemm_* mode 1), else x quantized into `workspace` and a GEMM (the
 // int8-MFMA GEMM; for Q4 at >= 320 tokens, >= 4096 rows and K <= 4096 the
-// fp6-MFMA GEMM, which is faster there). int8_inputs 0 (mode 0): the exact
-// float-input GEMV, 4 tokens per weight pass. workspace: at least
-// dnx_matmul_workspace_bytes(cols, n) bytes of device memory (unused by the
-// GEMV routes; may be null there).
+// fp6-MFMA GEMM, which is faster there). int8_inputs 0 (mode 0): for n <= 4
+// and x narrow enough for its LDS the exact float-input GEMV (bit-identical
+// to lab_gemm_* mode 0), else the bf16-MFMA float GEMM (any width; within
+// 1e-4 + 1e-5 |y| of mode 0). workspace: at least
+// dnx_matmul_workspace_bytes(cols, n) bytes of device memory for the
+// quantized activations (unused by the GEMV routes; may be null there).
+// Split-K partials are not in it: when a GEMM splits K (few output tiles),
+// its partials go to a buffer the library owns per GEMM kind and grows on
+// demand (a hipMalloc after a device synchronize). So calls share library
+// state: serialize them (one stream, or events between streams), and do
+// not make the first call of a new, larger split shape inside a graph
+// capture.
 int64_t dnx_matmul_workspace_bytes(int64_t cols, int64_t n);
 int dnx_matmul_q8(const int8_t* qs, const float* scales, const float* x, float* y, int64_t rows,
                   int64_t cols, int64_t n, int int8_inputs, void* workspace,

@@ -85,10 +85,15 @@ int64_t lab_gpu_tracking_writes(void);
 // in the engine's Q8 (int8 + fp32 scales) or Q4 (nibbles + fp16 scales)
 // layout, X at x + xOffset (fp32), Y at y + yOffset (fp32). By default the
 // inputs are quantized to Q8 per block as lab_native.c does (mode 1): for
-// n <= 4 the products are bit-identical to lab_gemm_q8 / lab_gemm_q4 mode 1;
-// for larger n they run on int8 MFMA within 1e-4 relative. With float inputs
-// (lab_gpu_set_int8_inputs below) they are bit-identical to mode 0 for every
-// n. qs must be 16-byte aligned.
+// n <= 4 (and x narrow enough for the GEMV's LDS) the products are
+// bit-identical to lab_gemm_q8 / lab_gemm_q4 mode 1; otherwise a GEMM with
+// exact per-block integer dots computes them within 1e-4 relative (1e-5
+// absolute near zero). With float inputs (lab_gpu_set_int8_inputs below):
+// for n <= 4 and x narrow enough for the GEMV (one token's fp32 x fits its
+// LDS up to about 35000 columns; 14000 above 16384 rows), bit-identical to
+// mode 0; otherwise the bf16-MFMA float GEMM, any width, within
+// 1e-4 + 1e-5 |y| of mode 0 (the reference GPU test's bar). qs must be
+// 16-byte aligned.
 void lab_gpu_enc_matmul_q8(int64_t w, int64_t qsOffset, int64_t scalesOffset, int64_t x,
                            int64_t xOffset, int64_t y, int64_t yOffset, int64_t rows,
                            int64_t cols, int64_t n);
@@ -101,11 +106,14 @@ void lab_gpu_enc_matmul_q4(int64_t w, int64_t qsOffset, int64_t scalesOffset, in
 // decides: the Vulkan layer quantizes the inputs per block on a device with
 // integer dot products (lab_vulkan.c:842-858), the Metal layer multiplies
 // float inputs (lab_metal.m:1025-1038). 1 (the default) is the Vulkan
-// behaviour above; 0 is the Metal one, and then the products are
-// bit-identical to lab_gemm_q8 / lab_gemm_q4 mode 0 for every n (what
-// GpuLinear documents, gpu.dart:1271-1275). The environment variable
-// DIANOIA_GPU_INT8_INPUTS=0 sets 0 at lab_gpu_init, for callers that cannot
-// call this. Float inputs are limited to rows of up to about 14000 columns.
+// behaviour above; 0 is the Metal one: lab_gemm_q8 / lab_gemm_q4 mode 0's
+// products (what GpuLinear documents, gpu.dart:1271-1275), bit-identical
+// for n <= 4 with x narrow enough for the exact float GEMV (its LDS takes
+// the tokens of a weight pass, 4 down to 1 as x widens, up to about 35000
+// fp32 columns; 14000 for more than 16384 rows), and within
+// 1e-4 + 1e-5 |y| otherwise (the bf16-MFMA float GEMM, any width).
+// The environment variable DIANOIA_GPU_INT8_INPUTS=0 sets 0 at
+// lab_gpu_init, for callers that cannot call this.
 int64_t lab_gpu_set_int8_inputs(int64_t on);
 
 // The decoder's other layer steps, as the reference binds them

@@ -1,8 +1,18 @@
 """Child process of tests/test_gpu_forward.py: the same small decoder pass
-with the environment the parent sets (DIANOIA_GPU_TRACK_WRITES=0); writes
-its logits and upload bytes to gpurun_out/forward_child.npz."""
+in a process of its own, writing its results to gpurun_out/ for the parent.
+
+* no argument: with the environment the parent sets
+  (DIANOIA_GPU_TRACK_WRITES=0); writes its logits and upload bytes to
+  gpurun_out/forward_child.npz;
+* ``replace-handler``: after a first pass with host-write tracking on,
+  another SIGSEGV handler (the default action) replaces the library's; the
+  next lab_gpu_contents must see that and turn tracking off, unprotecting
+  every page, before the host writes again (a write to a still protected
+  page would now end the process). Writes gpurun_out/forward_child_handler.npz.
+"""
 
 import os
+import signal
 import sys
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -29,5 +39,23 @@ def main():
              logits17=logits17, up17=up17, tracking=int(F.tracking_writes()))
 
 
+def replace_handler():
+    fwd = F.GpuForward(qwen3_small(), max_seq=64, max_chunk=8, seed=9)
+    run(fwd, [(8, 0), (8, 8)])
+    before = int(F.tracking_writes())
+    signal.signal(signal.SIGSEGV, signal.SIG_DFL)
+    fwd.residual  # a view: lab_gpu_contents
+    after = int(F.tracking_writes())
+    run(fwd, [(1, 16)])   # host writes into pages that were write-protected
+    logits16 = fwd.logits.copy()
+    fwd.dispose()
+    os.makedirs(os.path.join(ROOT, "gpurun_out"), exist_ok=True)
+    np.savez(os.path.join(ROOT, "gpurun_out", "forward_child_handler.npz"), logits16=logits16,
+             before=before, after=after)
+
+
 if __name__ == "__main__":
-    main()
+    if len(sys.argv) > 1 and sys.argv[1] == "replace-handler":
+        replace_handler()
+    else:
+        main()

@@ -76,12 +76,81 @@ def test_one_command_buffer_equals_one_per_command(gpu_ready, name):
         split.dispose()
 
 
+def run_meanwhile(fwd, plan, work):
+    """run() with every chunk committed without waiting and `work` run on the
+    host while the GPU computes (GpuForward.forward(meanwhile:))."""
+    out = []
+    for n, pos in plan:
+        fwd.residual[:n * fwd.config.hidden] = embeddings(fwd.config, pos, n)
+        fwd.forward(n, pos, meanwhile=work)
+        out.append((fwd.logits.copy(), [b.copy() for b in fwd.state_blocks(pos + n)]))
+    return out
+
+
+@pytest.mark.parametrize("name", sorted(CONFIGS))
+def test_forward_meanwhile_equals_waiting_commit(gpu_ready, name):
+    """forward(meanwhile=...) (lab_gpu_commit(0), host work, lab_gpu_wait)
+    leaves the logits, KV rows and conv histories of a waiting commit bit for
+    bit, and runs the host work once per pass (forward_meanwhile_test.dart:
+    23-47). The work computes on the host while the copy-backs of the pass
+    are still landing in the pinned views."""
+    cfg = CONFIGS[name]()
+    plain = F.GpuForward(cfg, max_seq=16, max_chunk=8, seed=3)
+    overlap = F.GpuForward(cfg, max_seq=16, max_chunk=8, seed=3)
+    runs = []
+
+    def work():
+        rng = np.random.default_rng(len(runs))
+        a = rng.standard_normal((256, 256))
+        runs.append(float(np.linalg.norm(a @ a.T)))
+
+    try:
+        a, b = run(plain, PLAN), run_meanwhile(overlap, PLAN, work)
+        assert len(runs) == len(PLAN)
+        for (la, sa), (lb, sb), chunk in zip(a, b, PLAN):
+            assert same(la, lb), f"logits differ after chunk {chunk}"
+            assert all(same(x, y) for x, y in zip(sa, sb)), f"state differs after chunk {chunk}"
+    finally:
+        plain.dispose()
+        overlap.dispose()
+
+
+def test_forward_meanwhile_error_comes_after_the_pass(gpu_ready):
+    """An error raised by the host work propagates after the pass has waited
+    for the GPU (gpu.dart:1226-1233); the pass's results stand in its
+    buffers and the next step continues from them. As in GpuForward, the
+    raise skips the copy into ``logits`` (TextModel defers the error past
+    that copy, model.dart:753-784, which forward_meanwhile_test.dart:57-66
+    checks one level up): the logits buffer's view holds the pass's."""
+    cfg = qwen3_small()
+    plain = F.GpuForward(cfg, max_seq=16, max_chunk=8, seed=3)
+    failing = F.GpuForward(cfg, max_seq=16, max_chunk=8, seed=3)
+
+    def boom():
+        raise ValueError("meanwhile")
+
+    try:
+        want = run(plain, PLAN)
+        n, pos = PLAN[0]
+        failing.residual[:n * cfg.hidden] = embeddings(cfg, pos, n)
+        with pytest.raises(ValueError, match="meanwhile"):
+            failing.forward(n, pos, meanwhile=boom)
+        assert same(failing._logits.view, want[0][0])
+        rest = run(failing, PLAN[1:])
+        for (la, sa), (lb, sb) in zip(want[1:], rest):
+            assert same(la, lb) and all(same(x, y) for x, y in zip(sa, sb))
+    finally:
+        plain.dispose()
+        failing.dispose()
+
+
 def test_decode_step_fuses_norms_and_adds(gpu_ready):
     """A one-token step dispatches no standalone RMSNorm or residual add:
     each RMSNorm runs in the prologue of the GEMV that reads it and each add
     in the epilogue of the GEMV whose output it adds (the commit's fusions,
     checked for their bits by the test above); the same step one command per
-    commit runs them all."""
+    commit runs them all. The profile still counts each of them once (with
+    no time of its own when fused)."""
     import ctypes
     from dianoia_amd import _lib
     lib = _lib.load()
@@ -98,21 +167,26 @@ def test_decode_step_fuses_norms_and_adds(gpu_ready):
         lib.lab_gpu_set_profiling(0)
         counts = (ctypes.c_int64 * 21)()
         assert lib.lab_gpu_profile(ms, counts, 21) == 21
-        return list(counts)
+        return list(counts), list(ms)
 
     fused = F.GpuForward(cfg, max_seq=16, max_chunk=8, seed=3)
     split = F.GpuForward(cfg, max_seq=16, max_chunk=8, seed=3)
     split.split_commits = True
     try:
-        a, b = profiled_step(fused), profiled_step(split)
+        (a, a_ms), (b, b_ms) = profiled_step(fused), profiled_step(split)
     finally:
         fused.dispose()
         split.dispose()
     rms_norm, add, gemv_q8, gemv_q4 = 4, 17, 13, 14
     layers = len(cfg.layer_types)
-    assert a[rms_norm] == 0 and a[add] == 0, a
-    assert a[gemv_q8] + a[gemv_q4] > 0, a
     assert b[rms_norm] == 2 * layers + 1 and b[add] == 2 * layers, b
+    assert b[gemv_q8] + b[gemv_q4] > 0, b
+    # A fused launch counts every command it ran under that command's kind
+    # (its time goes to its main kernel's kind), so the counts per kind are
+    # those of one launch per command.
+    assert a == b, (a, b)
+    assert a_ms[rms_norm] == 0 and a_ms[add] == 0, a_ms
+    assert b_ms[rms_norm] > 0 and b_ms[add] > 0, b_ms
 
 
 class StageCheck:
@@ -324,11 +398,35 @@ def test_tracking_off_uploads_the_history_and_agrees(gpu_ready):
     assert int(out["up17"]) >= up_tracked + 2 * 17 * cfg.kv_dim * 4 * cfg.layers
 
 
+def test_replaced_segv_handler_turns_tracking_off(gpu_ready):
+    """A SIGSEGV handler installed after lab_gpu_init (here the default
+    action, in a child process) is noticed by the next lab_gpu_contents,
+    which turns host-write tracking off and unprotects every page before
+    the host writes through its views again: the pass then runs to the
+    same logits as with tracking (a write to a still protected page would
+    have ended the child)."""
+    script = os.path.join(ROOT, "tests", "forward_child.py")
+    cfg = qwen3_small()
+    fwd = F.GpuForward(cfg, max_seq=64, max_chunk=8, seed=9)
+    try:
+        run(fwd, [(8, 0), (8, 8), (1, 16)])
+        want = fwd.logits.copy()
+    finally:
+        fwd.dispose()
+    r = subprocess.run([sys.executable, script, "replace-handler"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 0, (r.returncode, r.stderr[-2000:])
+    out = np.load(os.path.join(ROOT, "gpurun_out", "forward_child_handler.npz"))
+    assert int(out["before"]) == 1 and int(out["after"]) == 0
+    assert same(out["logits16"], want)
+
+
 def test_long_context_decode_folds_head_norms(gpu_ready):
     """Decode steps past 64 positions take the split-key attention, where the
     commit folds the q and k head norms into it: one command buffer per pass
     against one per command, bit for bit (logits and KV rows), and the
-    folded step dispatches no standalone head norm."""
+    folded step dispatches no standalone head norm (the profile counts the
+    folded norms under their kind with no time)."""
     import ctypes
     from dianoia_amd import _lib
     lib = _lib.load()
@@ -354,7 +452,11 @@ def test_long_context_decode_folds_head_norms(gpu_ready):
         lb = run(split, plan[-1:])
         assert same(la[0][0], lb[0][0])
         head_norm_rope, attention = 5, 7
-        assert counts[head_norm_rope] == 0 and counts[attention] == len(cfg.layer_types), list(counts)
+        layers = len(cfg.layer_types)
+        # The folded head norms are counted under their own kind (q and k per
+        # layer) with no time of their own: no standalone launch.
+        assert counts[head_norm_rope] == 2 * layers and ms[head_norm_rope] == 0, list(counts)
+        assert counts[attention] == layers and ms[attention] > 0, list(counts)
     finally:
         fused.dispose()
         split.dispose()

@@ -259,3 +259,80 @@ def test_prepacked_gemm_equals_engine_layout(gpu_ready, orc, rows, cols, n):
     ref = orc.gemm_q4(qs, sc, xs, n, threads=8, mode=1)
     ok, worst_rel, worst_abs = within_tolerance(b, ref)
     assert ok, (worst_rel, worst_abs)
+
+
+# ------------------------------------------- the prefill chunk GEMM (n <= 64)
+
+def gemm_f6s(qs, sc, xq, xsc, rows, cols, n):
+    panel = torch.full((D.f6_panel_bytes(n, cols),), 0x7f, dtype=torch.uint8, device="cuda")
+    D.pack_f6panel(dev(xq), dev(xsc), panel, n, cols)
+    packed = torch.empty(D.q4_f6pack_bytes(rows, cols), dtype=torch.uint8, device="cuda")
+    D.pack_q4_f6(dev(qs), dev(sc), packed, rows, cols)
+    y = torch.full((n, rows), float("nan"), dtype=torch.float32, device="cuda")
+    D.gemm_q4_f6s(packed, panel, y, rows, cols, n)
+    return host(y)
+
+
+@pytest.mark.parametrize("rows,cols,n", [(130, 256, 64), (33, 96, 5), (17, 2048, 16),
+                                         (97, 1024, 33), (64, 512, 32)])
+def test_chunk_gemm_block_dots_are_exact(gpu_ready, orc, rows, cols, n):
+    """dnx_gemm_q4_f6s: scale 1 on one block and 0 on the others gives that
+    block's exact dot, for every block (every |xq| up to 127, every nibble)."""
+    rng = np.random.default_rng(rows + cols + n + 1)
+    B = cols // 32
+    xq = rng.integers(-127, 128, (n, cols), dtype=np.int8)
+    xq[0, :32] = 127
+    xq[-1, -32:] = -127
+    qs = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+    qs[0, :16] = 0x00
+    qs[-1, -16:] = 0xff
+    want = orc.block_dots_q4(qs, xq)
+    for b in range(B):
+        sw = np.zeros((rows, B), np.uint16)
+        sw[:, b] = 0x3C00
+        xsc = np.zeros((n, B), np.float32)
+        xsc[:, b] = 1.0
+        y = gemm_f6s(qs, sw, xq, xsc, rows, cols, n)
+        assert np.array_equal(y, want[:, :, b].astype(np.float32)), f"block {b}"
+
+
+def test_chunk_gemm_unit_scales_sum_blocks_exactly(gpu_ready, orc):
+    rows, cols, n = 200, 4096, 64
+    rng = np.random.default_rng(8)
+    xq = rng.integers(-127, 128, (n, cols), dtype=np.int8)
+    qs = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+    want = orc.block_dots_q4(qs, xq).sum(axis=2)
+    assert np.abs(want).max() < 2 ** 24
+    y = gemm_f6s(qs, np.full((rows, cols // 32), np.uint16(0x3C00)), xq,
+                 np.ones((n, cols // 32), np.float32), rows, cols, n)
+    assert np.array_equal(y, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("rows,cols,n", [(6144, 2048, 64), (6144, 2048, 8), (2048, 6144, 33),
+                                         (768, 768, 13), (97, 160, 5), (257, 2048, 32),
+                                         (1152, 4320, 17), (100, 96, 64), (1792, 768, 48),
+                                         (4304, 1152, 64), (768, 768, 375), (2048, 768, 130)])
+def test_chunk_gemm_within_tolerance(gpu_ready, orc, rows, cols, n):
+    """Against the exact products (error / sum|terms| below 1e-5) and the CPU
+    kernel's outputs (relative 1e-4, absolute 1e-5 near zero); the same
+    inputs twice give the same bits (a fixed order of the K parts)."""
+    rng = np.random.default_rng(rows * 5 + cols + n)
+    qs, sc = synth.q4_weights(rng, rows, cols)
+    xs = synth.activations(rng, n, cols)
+    xq, xsc = orc.quantize_q8(xs)
+    ref = orc.gemm_q4(qs, sc, xs, n, threads=8, mode=1)
+    y = gemm_f6s(qs, sc, xq, xsc, rows, cols, n)
+    exact, mag = exact_products(orc, qs, sc, xq, xsc)
+    assert np.all(np.abs(y - exact) <= 1e-5 * mag)
+    ok, worst_rel, worst_abs = within_tolerance(y, ref)
+    assert ok, (worst_rel, worst_abs)
+    assert np.array_equal(bits(y), bits(gemm_f6s(qs, sc, xq, xsc, rows, cols, n)))
+
+
+def test_chunk_gemm_refuses_bad_shapes(gpu_ready):
+    z = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    y = torch.zeros(65 * 64, device="cuda")
+    with pytest.raises(RuntimeError):
+        D.gemm_q4_f6s(z, z, y, 64, 48, 5)    # cols not a multiple of 32
+    with pytest.raises(RuntimeError):
+        D.gemm_q4_f6s(z, z, y, 64, 64, 0)    # no tokens

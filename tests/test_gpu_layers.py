@@ -13,6 +13,7 @@ import torch
 
 from dianoia_amd import _lib
 from dianoia_amd import device as D
+from dianoia_amd import synth
 from gpu_util import bits, dev, host
 
 pytestmark = pytest.mark.gpu
@@ -242,6 +243,129 @@ def test_layer_steps_through_the_abi(gpu_ready, orc):
         B.close()
 
 
+def _profile(lib):
+    """(ms, counts) per kind since the last call (lab_gpu_profile clears)."""
+    ms = (ctypes.c_double * 21)()
+    counts = (ctypes.c_int64 * 21)()
+    assert lib.lab_gpu_profile(ms, counts, 21) == 21
+    return list(ms), list(counts)
+
+
+def _byte_buffer(B, raw):
+    """A lab_gpu buffer holding `raw` (uint8) through its host view."""
+    h = B.lib.lab_gpu_buffer(raw.nbytes)
+    assert h >= 0
+    B.handles.append(h)
+    p = B.lib.lab_gpu_contents(h)
+    view = np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_uint8)), (raw.nbytes,))
+    view[:] = raw
+    return h
+
+
+def _run_sequence(build, split):
+    """Records the commands build(B, lib) encodes, in one command buffer or
+    one per command (split), with profiling on; returns the host views it
+    names and the profile."""
+    B = Bufs()
+    lib = B.lib
+    try:
+        cmds, views = build(B, lib)
+        _profile(lib)
+        lib.lab_gpu_set_profiling(1)
+        if split:
+            for c in cmds:
+                lib.lab_gpu_begin()
+                c()
+                assert lib.lab_gpu_commit(1) == 1
+        else:
+            lib.lab_gpu_begin()
+            for c in cmds:
+                c()
+            assert lib.lab_gpu_commit(1) == 1
+        lib.lab_gpu_set_profiling(0)
+        prof = _profile(lib)
+        return [B.view(h, n).copy() for h, n in views], prof
+    finally:
+        B.close()
+
+
+RMS_NORM, HEAD_NORM_ROPE = 4, 5
+
+
+def test_norm_fusion_declines_weights_in_the_norm_output_buffer(gpu_ready):
+    """An RMSNorm whose output buffer also holds the weights of the matmul
+    that reads it (disjoint regions): the commit runs the norm on its own
+    (its kind gets time of its own) and leaves what one command per commit
+    leaves, bit for bit."""
+    rng = np.random.default_rng(31)
+    rows, cols = 64, 256
+    qs, sc = synth.q4_weights(rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    qs_off, sc_off = 4096, 4096 + qs.nbytes
+    raw = np.zeros(sc_off + sc.nbytes, np.uint8)
+    raw[qs_off:qs_off + qs.nbytes] = qs.reshape(-1)
+    raw[sc_off:] = sc.reshape(-1).view(np.uint8)
+
+    def build(B, lib):
+        hx, hw, hy = B.new(x), B.new(w), B.new(np.zeros(rows))
+        hp = _byte_buffer(B, raw)
+        cmds = [lambda: lib.lab_gpu_enc_rms_norm(hx, 0, hw, 0, hp, 0, 1, cols, 1e-6, 0),
+                lambda: lib.lab_gpu_enc_matmul_q4(hp, qs_off, sc_off, hp, 0, hy, 0, rows, cols, 1)]
+        return cmds, [(hy, rows), (hp, cols)]
+
+    (y1, n1), (ms1, _) = _run_sequence(build, split=False)
+    (y2, n2), (ms2, _) = _run_sequence(build, split=True)
+    assert np.array_equal(bits(y1), bits(y2)) and np.array_equal(bits(n1), bits(n2))
+    assert ms1[RMS_NORM] > 0 and ms2[RMS_NORM] > 0
+
+
+@pytest.mark.parametrize("shared", ["q_norm_weights", "rope_table"])
+def test_rope_attention_fusion_declines_out_sharing_a_buffer(gpu_ready, shared):
+    """A decode token's q/k head norms + RoPE and its attention, where the
+    attention's out buffer also holds (past out's own bytes) the q norm's
+    weights or the rope table: the commit does not fold the norms into the
+    attention (the head norm kind gets time of its own) and leaves out, q and
+    the key row as one command per commit does, bit for bit. (A gate in out's
+    buffer would overlap out itself: both sit at offset 0.)"""
+    rng = np.random.default_rng(37)
+    heads, kv, hd, pos = 4, 2, 64, 200
+    kvd = kv * hd
+    q = rng.standard_normal(heads * hd).astype(np.float32)
+    keys = rng.standard_normal((pos + 1) * kvd).astype(np.float32)
+    vals = rng.standard_normal((pos + 1) * kvd).astype(np.float32)
+    qw = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kw = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    ang = rng.uniform(0, 6.3, hd // 2)
+    rope = np.concatenate([np.cos(ang), np.sin(ang)]).astype(np.float32)
+    gate = rng.standard_normal(heads).astype(np.float32)
+    tail = {"q_norm_weights": qw, "rope_table": rope}[shared]
+    out_floats = heads * hd
+
+    def build(B, lib):
+        hq, hk, hv = B.new(q), B.new(keys), B.new(vals)
+        hout = B.new(np.concatenate([np.zeros(out_floats, np.float32), tail]))
+        tail_off = out_floats * 4
+        hqw = hout if shared == "q_norm_weights" else B.new(qw)
+        qw_off = tail_off if shared == "q_norm_weights" else 0
+        hkw = B.new(kw)
+        hrope = hout if shared == "rope_table" else B.new(rope)
+        rope_off = tail_off if shared == "rope_table" else 0
+        hg = B.new(gate)
+        cmds = [lambda: lib.lab_gpu_enc_head_norm_rope(hq, 0, heads * hd, hqw, qw_off, hrope,
+                                                       rope_off, hd, heads, hd, 1, 1e-6),
+                lambda: lib.lab_gpu_enc_head_norm_rope(hk, pos * kvd * 4, kvd, hkw, 0, hrope,
+                                                       rope_off, hd, kv, hd, 1, 1e-6),
+                lambda: lib.lab_gpu_enc_attention(hq, hk, hv, hg, hout, pos, 1, heads, kv, hd, 0)]
+        return cmds, [(hout, out_floats), (hq, heads * hd), (hk, (pos + 1) * kvd)]
+
+    (o1, q1, k1), (ms1, _) = _run_sequence(build, split=False)
+    (o2, q2, k2), (ms2, _) = _run_sequence(build, split=True)
+    assert np.array_equal(bits(o1), bits(o2))
+    assert np.array_equal(bits(q1), bits(q2)) and np.array_equal(bits(k1), bits(k2))
+    assert ms1[HEAD_NORM_ROPE] > 0
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 2048), (3, 6144), (256, 1024), (1, 4), (2, 16384)])
 def test_add_rms_norm_fused(gpu_ready, orc, rows, cols):
     """The residual add and the following norm in one launch: x and out bit
@@ -299,12 +423,15 @@ def test_head_norm_rope_pair(gpu_ready, h0, h1, hd, n):
                                                           (32, 8, 128, 700, 0, True),
                                                           (8, 8, 64, 300, 0, False),
                                                           (16, 2, 64, 1000, 256, True),
-                                                          (4, 1, 128, 64, 0, False)])
+                                                          (4, 1, 128, 64, 0, False),
+                                                          (8, 4, 256, 300, 0, False),
+                                                          (16, 8, 32, 500, 0, True)])
 def test_attention_rope_equals_norms_then_attention(gpu_ready, heads, kv, hd, pos, window, gated):
     """dnx_attention_rope (the q and k head norms + RoPE folded into a decode
     token's split-key attention) against dnx_head_norm_rope on q and on the
     token's key row, then dnx_attention: out, q and the key row bit for bit;
-    every other key row untouched."""
+    every other key row untouched. Head sizes 32 to 256 (hd 256: two rotary
+    pairs per lane; hd 32: a 256-key split)."""
     rng = np.random.default_rng(heads * 7 + pos)
     kvd = kv * hd
     q0 = rng.standard_normal(heads * hd).astype(np.float32)

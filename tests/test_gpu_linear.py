@@ -283,6 +283,27 @@ def test_float_inputs_match_the_cpu_kernels(float_inputs, gpu, orc, fmt, rows, c
         assert np.array_equal(bits(on_gpu), bits(cpu))
 
 
+@pytest.mark.parametrize("fmt,n", [("q8", 1), ("q4", 3), ("q8", 9)])
+def test_float_inputs_wider_than_the_gemv(float_inputs, gpu, orc, fmt, n):
+    """x rows of 40960 floats: more than the exact float GEMV's LDS holds
+    (one token's fp32 x fits up to about 35000 columns), so the route falls
+    back to the bf16-MFMA float GEMM, any width; its outputs meet the
+    reference GPU test's bar against CPU mode 0 and the reference kernels'
+    own bar (error / sum|terms| < 1e-5) against the exact products."""
+    from test_gpu_gemm_float import exact_mode0
+    rows, cols = 48, 40960
+    rng = np.random.default_rng(7 + n)
+    m, qs, sc = quantized(orc, fmt, values(rng, rows * cols), rows, cols)
+    gpu.upload("wide", m)
+    xs = values(rng, n * cols)
+    on_gpu = np.zeros(n * rows, np.float32)
+    gpu.apply("wide", xs, on_gpu, n)
+    cpu = cpu_mode0(orc, fmt, qs, sc, xs, n).reshape(-1)
+    assert np.all(np.abs(on_gpu - cpu) <= 1e-4 + 1e-5 * np.abs(cpu))
+    exact, mag = exact_mode0(fmt, qs, sc, xs.reshape(n, cols))
+    assert np.all(np.abs(on_gpu.reshape(n, rows).astype(np.float64) - exact) <= 1e-5 * mag)
+
+
 def test_float_inputs_grow_buffers_and_keep_matrices(float_inputs, gpu, orc):
     rng = np.random.default_rng(6)
     small, sq, ss = quantized(orc, "q4", values(rng, 32 * 32), 32, 32)

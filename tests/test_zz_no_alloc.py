@@ -53,6 +53,42 @@ def test_noalloc_gemm_matches_allocating_entry(gpu_ready, orc):
         assert ok, (worst_rel, worst_abs)
 
 
+def test_noalloc_gemm_allocates_nothing(gpu_ready):
+    """The call's defining property: at a shape whose split partials (18.8 MB,
+    2 K parts x 128 tokens x 18336 rows) are larger than any earlier call's,
+    device free memory is the same before and after (an allocating path
+    would have grown its partials buffer by that much); its bits equal the
+    allocating entry point's."""
+    lib = gpu_ready
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rows, cols, n = 18336, 4096, 128     # 191 workgroup tiles: K splits 2 ways
+    rng = np.random.default_rng(3)
+    qs, sc = synth.q4_weights(rng, rows, cols)
+    xs = synth.activations(rng, n, cols)
+    panel = torch.empty(int(lib.dnx_f6_panel_bytes(n, cols)), dtype=torch.uint8, device="cuda")
+    xd = dev(xs)
+    assert lib.dnx_quantize_q8_f6panel(_p(xd), _p(panel), n, cols, stream) == 0
+    packed = torch.empty(int(lib.dnx_q4_f6pack_bytes(rows, cols)), dtype=torch.uint8,
+                         device="cuda")
+    qd, sd = dev(qs), dev(sc)
+    assert lib.dnx_pack_q4_f6(_p(qd), _p(sd), _p(packed), rows, cols, stream) == 0
+    y_free = torch.full((n, rows), float("nan"), device="cuda")
+    y_alloc = torch.full((n, rows), float("nan"), device="cuda")
+    # warm-up at a small split shape (the per-device scratch address lookup)
+    assert lib.dnx_gemm_q4_f6p_noalloc(_p(packed), _p(panel), _p(y_free), 96, cols, n,
+                                       stream) == 0
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    rc = lib.dnx_gemm_q4_f6p_noalloc(_p(packed), _p(panel), _p(y_free), rows, cols, n, stream)
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    assert rc == 0, rc
+    assert free0 - free1 < (4 << 20), (free0, free1)
+    assert lib.dnx_gemm_q4_f6p(_p(packed), _p(panel), _p(y_alloc), rows, cols, n, stream) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(host(y_free)), bits(host(y_alloc)))
+
+
 def test_noalloc_gemm_rejects_bad_arguments(gpu_ready):
     """Shapes the GEMM does not take are refused before any launch, as by the
     allocating entry point; DNX_ESCRATCH is the code for partials beyond the
