@@ -156,42 +156,122 @@ DNX_DEV void write_f6_entries(uint8_t* rec, int r, const int* xq, float scale) {
 
 // fp32 x [n][cols] -> f6 panel [groups][B][kRec]: lab_quantize_q8 of each
 // (token, block) (the same xq and scale bits as dnx_quantize_q8), then its
-// panel entries. One thread per (token, block); consecutive threads take
-// consecutive tokens of a group, so the record writes are contiguous.
-__global__ void __launch_bounds__(kPanelThreads) quantize_f6_panel_kernel(
+// panel entries, with four lanes per (token, block) (a lane per block spent
+// its time packing 32 values in series). Lane j of a quad quantizes values 8j .. 8j+7 (lab_quantize_q8's
+// steps, the block's amax and sum(xq) over the quad by DPP). In the operand
+// order kFieldK those 8 values occupy 8 fields of one 96-bit half (j & 1)
+// of the 192-bit code field, at the places of pattern j >> 1 below; the two
+// lanes of a half OR their bits together, and each lane then stores one 16
+// bytes of the token's two lane records. The same bytes as write_f6_entries
+// writes for the (token, block).
+template <int F>
+DNX_DEV void put_field(uint32_t* d, uint32_t c) {
+  constexpr int bit = 6 * F, wd = bit >> 5, sh = bit & 31;
+  d[wd] |= c << sh;
+  if constexpr (sh > 26) d[wd + 1] |= c >> (32 - sh);
+}
+
+// Fields (within their 96-bit half) of a lane's values 0..7: pattern 0 for
+// lanes 0, 1 (values 0-7, 8-15), pattern 1 for lanes 2, 3 (16-23, 24-31).
+DNX_DEV void place_pattern0(uint32_t* d, const uint32_t* c) {
+  put_field<0>(d, c[0]); put_field<12>(d, c[1]); put_field<8>(d, c[2]); put_field<4>(d, c[3]);
+  put_field<11>(d, c[4]); put_field<7>(d, c[5]); put_field<3>(d, c[6]); put_field<15>(d, c[7]);
+}
+DNX_DEV void place_pattern1(uint32_t* d, const uint32_t* c) {
+  put_field<6>(d, c[0]); put_field<2>(d, c[1]); put_field<14>(d, c[2]); put_field<10>(d, c[3]);
+  put_field<1>(d, c[4]); put_field<13>(d, c[5]); put_field<9>(d, c[6]); put_field<5>(d, c[7]);
+}
+
+__global__ void __launch_bounds__(kPanelThreads) quantize_f6_panel4_kernel(
     const float* __restrict__ x, uint8_t* __restrict__ panel, int n, int cols, int groups) {
   const int B = cols / kBlock;
-  const int64_t total = (int64_t)groups * B * kTokens;
+  const int64_t total = (int64_t)groups * B * kTokens * 4;  // whole quads
   for (int64_t idx = (int64_t)blockIdx.x * kPanelThreads + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * kPanelThreads) {
-    const int r = (int)(idx & (kTokens - 1));
-    const int64_t gb = idx >> 5;
+    const int j = (int)(idx & 3);
+    const int64_t q = idx >> 2;
+    const int r = (int)(q & (kTokens - 1));
+    const int64_t gb = q >> 5;
     const int b = (int)(gb % B);
     const int g = (int)(gb / B);
     const int m = g * kTokens + r;
-    float4 v[8];
     const bool live = m < n;
-    const float4* src = (const float4*)(x + (int64_t)(live ? m : 0) * cols + b * kBlock);
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = live ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) amax = fmaxf(amax, max4abs(v[i]));
+    const float4* src = (const float4*)(x + (int64_t)(live ? m : 0) * cols + b * kBlock + 8 * j);
+    const float4 v0 = live ? src[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 v1 = live ? src[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float amax = fmaxf(max4abs(v0), max4abs(v1));
+    amax = fmaxf(amax, dppf<kQuadXor1>(amax));
+    amax = fmaxf(amax, dppf<kQuadXor2>(amax));
     const float scale = q8_scale(amax);
     const float inv = q8_inv(scale);
-    int xq[32];
+    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    uint32_t ch[8], cl[8];
+    int sum = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      xq[4 * i] = quant1(v[i].x, inv);
-      xq[4 * i + 1] = quant1(v[i].y, inv);
-      xq[4 * i + 2] = quant1(v[i].z, inv);
-      xq[4 * i + 3] = quant1(v[i].w, inv);
+      const int xq = quant1(vv[i], inv);
+      sum += xq;
+      const uint32_t a = (uint32_t)(xq < 0 ? -xq : xq);
+      const uint32_t sg = xq < 0 ? 0x20u : 0u;
+      ch[i] = sg | (a >> 3);
+      cl[i] = sg | (a & 7u);
     }
-    write_f6_entries(panel + gb * kRec, r, xq, scale);
+    sum += dpp<kQuadXor1>(sum);
+    sum += dpp<kQuadXor2>(sum);
+    uint32_t h0[3] = {0, 0, 0}, h1[3] = {0, 0, 0}, l0[3] = {0, 0, 0}, l1[3] = {0, 0, 0};
+    place_pattern0(h0, ch);
+    place_pattern1(h1, ch);
+    place_pattern0(l0, cl);
+    place_pattern1(l1, cl);
+    const bool p1 = (j >> 1) != 0;
+    uint32_t hw[3], lw[3];
+#pragma unroll
+    for (int d = 0; d < 3; d++) {
+      hw[d] = p1 ? h1[d] : h0[d];
+      lw[d] = p1 ? l1[d] : l0[d];
+      hw[d] |= (uint32_t)dpp<kQuadXor2>((int)hw[d]);   // the other lane of this half
+      lw[d] |= (uint32_t)dpp<kQuadXor2>((int)lw[d]);
+    }
+    // Lanes 0, 2 hold dwords 0-2 of the field, lanes 1, 3 dwords 3-5; the
+    // first 16 bytes of a record also need dword 3 (the other half's first).
+    const uint32_t h3 = (uint32_t)dpp<kQuadXor1>((int)hw[0]);
+    const uint32_t l3 = (uint32_t)dpp<kQuadXor1>((int)lw[0]);
+    // The scale's pieces and E8M0 bytes, as write_f6_entries.
+    const uint32_t bits = __float_as_uint(scale);
+    const int ef = (int)((bits >> 23) & 0xff);
+    int e = ef == 0 ? -126 : ef - 127;
+    float mant = ef == 0 ? scale * 0x1p126f : __uint_as_float((bits & 0x807fffffu) | 0x3f800000u);
+    if (scale == 0.0f) {
+      e = 0;
+      mant = 0.0f;
+    }
+    const _Float16 p0 = (_Float16)mant;
+    const float r1 = mant - (float)p0;
+    const _Float16 pp1 = (_Float16)r1;
+    const _Float16 p2 = (_Float16)(r1 - (float)pp1);
+    const uint32_t sh_h = (uint32_t)(127 + 6 + e), sh_l = (uint32_t)(127 + 3 + e);
+    const uint32_t s0 = (uint32_t)__builtin_bit_cast(uint16_t, p0) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, pp1) << 16);
+    const uint32_t s1 = sh_h | ((uint32_t)__builtin_bit_cast(uint16_t, p2) << 16);
+    uint8_t* rec = panel + gb * kRec;
+    // Lane 0: h codes, first half; 1: h codes, second half + operand; 2, 3
+    // the same for the l codes.
+    uint4 o;
+    if (j == 0) o = make_uint4(hw[0], hw[1], hw[2], h3);
+    else if (j == 1) o = make_uint4(hw[1], hw[2], s0, s1);
+    else if (j == 2) o = make_uint4(lw[0], lw[1], lw[2], l3);
+    else o = make_uint4(lw[1], lw[2], 0u, sh_l);
+    const int lane_rec = (j & 2) ? 32 + r : r;
+    *(uint4*)(rec + kRecF + (j & 1) * kRecHalf + lane_rec * 16) = o;
+    if (j == 0) {
+      const float c = sum == 0 ? 0.0f : ldexpf((float)(-8 * sum), e);
+      *(float*)(rec + kRecC + ((((r >> 2) & 1) * 16 + (r >> 3) * 4 + (r & 3)) * 4)) = c;
+    }
   }
 }
 
-// The same panel from already quantized xq int8 [n][cols] + xsc [n][cols/32].
+// The same panel from already quantized xq int8 [n][cols] + xsc [n][cols/32],
+// one thread per (token, block).
 __global__ void __launch_bounds__(kPanelThreads) pack_f6_panel_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ xsc, uint8_t* __restrict__ panel,
     int n, int cols, int groups) {
@@ -1030,8 +1110,8 @@ int dnx_quantize_q8_f6panel(const float* x, void* panel, int64_t n, int64_t cols
     return DNX_EINVAL;
   }
   const int groups = (int)((n + kTokens - 1) / kTokens);
-  const int64_t total = (int64_t)groups * (cols / kBlock) * kTokens;
-  hipLaunchKernelGGL(quantize_f6_panel_kernel, dim3(panel_grid(total)), dim3(kPanelThreads), 0,
+  const int64_t total = (int64_t)groups * (cols / kBlock) * kTokens * 4;
+  hipLaunchKernelGGL(quantize_f6_panel4_kernel, dim3(panel_grid(total)), dim3(kPanelThreads), 0,
                      (hipStream_t)stream, x, (uint8_t*)panel, (int)n, (int)cols, groups);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
@@ -1099,8 +1179,12 @@ int dnx_gemm_q4_f6s(const void* packed, const void* panel, float* y, int64_t row
   p.rows = (int)rows;
   p.cols = (int)cols;
   p.n = (int)n;
-  const dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((n + 2 * kTokens - 1) / (2 * kTokens)));
-  if (n > kTokens) {
+  // 33+ tokens: two token groups per workgroup (one weight read for both:
+  // 64 tokens of 6144 x 2048 in 6.5 us against 7.9 with a workgroup per 32).
+  const bool two = n > kTokens;
+  const int per = two ? 2 * kTokens : kTokens;
+  const dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((n + per - 1) / per));
+  if (two) {
     hipLaunchKernelGGL(gemm_f6s_kernel<2>, grid, dim3(kThreads), 0, (hipStream_t)stream, p);
   } else {
     hipLaunchKernelGGL(gemm_f6s_kernel<1>, grid, dim3(kThreads), 0, (hipStream_t)stream, p);

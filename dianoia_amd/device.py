@@ -35,8 +35,22 @@ def _check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed with code {rc}")
 
 
+def _need(what: str, **operands) -> None:
+    """Refuses, before any launch, an operand tensor smaller than the bytes
+    the kernel will touch for the given shape (the C ABI takes bare
+    pointers and cannot tell)."""
+    for name, (t, nbytes) in operands.items():
+        if t is not None and nbytes > 0 and t.numel() * t.element_size() < nbytes:
+            raise ValueError(f"{what}: {name} holds {t.numel() * t.element_size()} bytes, "
+                             f"the shape needs {nbytes}")
+
+
 def quantize_q8(x: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, rows: int, cols: int,
                 cols_pad: int, stream=None) -> None:
+    _need("quantize_q8",
+          x=(x, rows * cols * 4),
+          qs=(qs, rows * cols_pad),
+          scales=(scales, rows * (cols_pad // 32) * 4))
     _check(_lib.load().dnx_quantize_q8(_ptr(x), _ptr(qs), _ptr(scales), rows, cols, cols_pad,
                                        _stream(stream)), "dnx_quantize_q8")
 
@@ -83,23 +97,43 @@ def quantize_q4_bf16(w: torch.Tensor, qs: torch.Tensor, scales: torch.Tensor, ro
 
 
 def gemv_q8(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> None:
+    _need("gemv_q8",
+          qs=(qs, rows * cols),
+          scales=(scales, rows * (cols // 32) * 4),
+          x=(x, n * cols * 4),
+          y=(y, n * rows * 4))
     _check(_lib.load().dnx_gemv_q8(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
                                    _stream(stream)), "dnx_gemv_q8")
 
 
 def gemv_q4(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> None:
+    _need("gemv_q4",
+          qs=(qs, rows * cols // 2),
+          scales=(scales, rows * (cols // 32) * 2),
+          x=(x, n * cols * 4),
+          y=(y, n * rows * 4))
     _check(_lib.load().dnx_gemv_q4(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
                                    _stream(stream)), "dnx_gemv_q4")
 
 
 def gemv_q8_float(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> None:
     """Float-input GEMV (lab_gemm_q8 mode 0), any n."""
+    _need("gemv_q8_float",
+          qs=(qs, rows * cols),
+          scales=(scales, rows * (cols // 32) * 4),
+          x=(x, n * cols * 4),
+          y=(y, n * rows * 4))
     _check(_lib.load().dnx_gemv_q8_float(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
                                          _stream(stream)), "dnx_gemv_q8_float")
 
 
 def gemv_q4_float(qs, scales, x, y, rows: int, cols: int, n: int = 1, stream=None) -> None:
     """Float-input GEMV (lab_gemm_q4 mode 0), any n."""
+    _need("gemv_q4_float",
+          qs=(qs, rows * cols // 2),
+          scales=(scales, rows * (cols // 32) * 2),
+          x=(x, n * cols * 4),
+          y=(y, n * rows * 4))
     _check(_lib.load().dnx_gemv_q4_float(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
                                          _stream(stream)), "dnx_gemv_q4_float")
 
@@ -214,21 +248,43 @@ def gemv_multi_norm(fmt: str, mats, x, norm_w, norm_out, eps: float, ys, cols: i
 
 def gemm_q8_float(qs, scales, x, y, rows: int, cols: int, n: int, stream=None) -> None:
     """Float-input (mode 0) GEMM on bf16 MFMA, within fp32 rounding of the CPU."""
+    _need("gemm_q8_float",
+          qs=(qs, rows * cols),
+          scales=(scales, rows * (cols // 32) * 4),
+          x=(x, n * cols * 4),
+          y=(y, n * rows * 4))
     _check(_lib.load().dnx_gemm_q8_float(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
                                          _stream(stream)), "dnx_gemm_q8_float")
 
 
 def gemm_q4_float(qs, scales, x, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _need("gemm_q4_float",
+          qs=(qs, rows * cols // 2),
+          scales=(scales, rows * (cols // 32) * 2),
+          x=(x, n * cols * 4),
+          y=(y, n * rows * 4))
     _check(_lib.load().dnx_gemm_q4_float(_ptr(qs), _ptr(scales), _ptr(x), _ptr(y), rows, cols, n,
                                          _stream(stream)), "dnx_gemm_q4_float")
 
 
 def gemm_q8(qs, scales, xq, xsc, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _need("gemm_q8",
+          qs=(qs, rows * cols),
+          scales=(scales, rows * (cols // 32) * 4),
+          xq=(xq, n * cols),
+          xsc=(xsc, n * (cols // 32) * 4),
+          y=(y, n * rows * 4))
     _check(_lib.load().dnx_gemm_q8(_ptr(qs), _ptr(scales), _ptr(xq), _ptr(xsc), _ptr(y), rows,
                                    cols, n, _stream(stream)), "dnx_gemm_q8")
 
 
 def gemm_q4(qs, scales, xq, xsc, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _need("gemm_q4",
+          qs=(qs, rows * cols // 2),
+          scales=(scales, rows * (cols // 32) * 2),
+          xq=(xq, n * cols),
+          xsc=(xsc, n * (cols // 32) * 4),
+          y=(y, n * rows * 4))
     _check(_lib.load().dnx_gemm_q4(_ptr(qs), _ptr(scales), _ptr(xq), _ptr(xsc), _ptr(y), rows,
                                    cols, n, _stream(stream)), "dnx_gemm_q4")
 
@@ -245,6 +301,7 @@ def pack_panel(xq, xsc, panel, n: int, cols: int, stream=None) -> None:
 
 def quantize_q8_panel(x, panel, n: int, cols: int, stream=None) -> None:
     """fp32 x [n][cols] quantized (lab_quantize_q8) straight into the GEMM's panel."""
+    _need("quantize_q8_panel", x=(x, n * cols * 4), panel=(panel, gemm_panel_bytes(n, cols)))
     _check(_lib.load().dnx_quantize_q8_panel(_ptr(x), _ptr(panel), n, cols, _stream(stream)),
            "dnx_quantize_q8_panel")
 
@@ -265,17 +322,27 @@ def f6_panel_bytes(n: int, cols: int) -> int:
 
 def quantize_q8_f6panel(x, panel, n: int, cols: int, stream=None) -> None:
     """fp32 x [n][cols] quantized (lab_quantize_q8) into the fp6 GEMM's panel."""
+    _need("quantize_q8_f6panel", x=(x, n * cols * 4), panel=(panel, f6_panel_bytes(n, cols)))
     _check(_lib.load().dnx_quantize_q8_f6panel(_ptr(x), _ptr(panel), n, cols, _stream(stream)),
            "dnx_quantize_q8_f6panel")
 
 
 def pack_f6panel(xq, xsc, panel, n: int, cols: int, stream=None) -> None:
     """xq int8 [n][cols] + xsc fp32 [n][cols/32] -> the fp6 GEMM's panel."""
+    _need("pack_f6panel",
+          xq=(xq, n * cols),
+          xsc=(xsc, n * (cols // 32) * 4),
+          panel=(panel, f6_panel_bytes(n, cols)))
     _check(_lib.load().dnx_pack_f6panel(_ptr(xq), _ptr(xsc), _ptr(panel), n, cols,
                                         _stream(stream)), "dnx_pack_f6panel")
 
 
 def gemm_q4_f6(qs, scales, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _need("gemm_q4_f6",
+          qs=(qs, rows * cols // 2),
+          scales=(scales, rows * (cols // 32) * 2),
+          panel=(panel, f6_panel_bytes(n, cols)),
+          y=(y, n * rows * 4))
     _check(_lib.load().dnx_gemm_q4_f6(_ptr(qs), _ptr(scales), _ptr(panel), _ptr(y), rows, cols,
                                       n, _stream(stream)), "dnx_gemm_q4_f6")
 
@@ -286,17 +353,29 @@ def q4_f6pack_bytes(rows: int, cols: int) -> int:
 
 def pack_q4_f6(qs, scales, packed, rows: int, cols: int, stream=None) -> None:
     """Load-time re-encoding of Q4 weights for the fp6 GEMM (dnx_gemm_q4_f6p)."""
+    _need("pack_q4_f6",
+          qs=(qs, rows * cols // 2),
+          scales=(scales, rows * (cols // 32) * 2),
+          packed=(packed, q4_f6pack_bytes(rows, cols)))
     _check(_lib.load().dnx_pack_q4_f6(_ptr(qs), _ptr(scales), _ptr(packed), rows, cols,
                                       _stream(stream)), "dnx_pack_q4_f6")
 
 
 def gemm_q4_f6p(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _need("gemm_q4_f6p",
+          packed=(packed, q4_f6pack_bytes(rows, cols)),
+          panel=(panel, f6_panel_bytes(n, cols)),
+          y=(y, n * rows * 4))
     _check(_lib.load().dnx_gemm_q4_f6p(_ptr(packed), _ptr(panel), _ptr(y), rows, cols, n,
                                        _stream(stream)), "dnx_gemm_q4_f6p")
 
 
 def gemm_q4_f6s(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
     """The prefill chunk GEMM (n <= 64) on prepacked Q4 weights."""
+    _need("gemm_q4_f6s",
+          packed=(packed, q4_f6pack_bytes(rows, cols)),
+          panel=(panel, f6_panel_bytes(n, cols)),
+          y=(y, n * rows * 4))
     _check(_lib.load().dnx_gemm_q4_f6s(_ptr(packed), _ptr(panel), _ptr(y), rows, cols, n,
                                        _stream(stream)), "dnx_gemm_q4_f6s")
 
