@@ -621,6 +621,76 @@ __global__ void __launch_bounds__(kPanelThreads) pack_q4_f6_kernel(
   }
 }
 
+// Q8 weights (int8 w in [-128, 127] + an fp32 scale per block, the engine's
+// layout, lab_native.c:398-405) need two fp6 digits, |w| = 8 wh + wl (wh <=
+// 15, wl <= 8; both E2M3 codes with w's sign): the dot takes two MFMAs per
+// block, the h codes against wh (B scale 2^6) and against wl (2^3), chained
+// through the C input (every partial sum an integer below 2^24: exact). The
+// scale sw = mant * 2^ew puts ew into the B operand's E8M0 scales and mant
+// into two fp16 pieces m0 + m1 (22 of its 24 bits) for the scale MFMA:
+// lanes 0..31 pair (p0, p1, byte, p2) of the activation with (m0, m0, 0, m0),
+// lanes 32..63 pair (p0, p1, byte, 0) with (m1, m1, 0, 0), giving
+// (p0 + p1 + p2) m0 + (p0 + p1) m1 (dropped terms below 2^-22 relative).
+// Per 32-row group and block, 2.5 KB: five [32 rows][16 B] parts: wh codes
+// 0..3; wh codes 4..5 + the low lanes' scale slots; the same + the high
+// lanes' slots; wl codes 0..3; wl codes 4..5 + the two E8M0 bytes.
+constexpr int kChunk8 = 2560;
+
+__global__ void __launch_bounds__(kPanelThreads) pack_q8_f6_kernel(
+    const int8_t* __restrict__ qs, const float* __restrict__ scales, uint8_t* __restrict__ out,
+    int rows, int B, int64_t count) {
+  for (int64_t i = (int64_t)blockIdx.x * kPanelThreads + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * kPanelThreads) {
+    const int r = (int)(i / B), b = (int)(i - (int64_t)r * B);
+    uint32_t h[6] = {0, 0, 0, 0, 0, 0}, l[6] = {0, 0, 0, 0, 0, 0};
+    float sw = 0.0f;
+    if (r < rows) {
+      const uint4 v0 = *(const uint4*)(qs + i * 32), v1 = *(const uint4*)(qs + i * 32 + 16);
+      const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int f = 0; f < 32; f++) {
+        const int k = kFieldKHost[f];
+        const int v = (int)(int8_t)(w[k >> 2] >> (8 * (k & 3)));
+        const uint32_t a = (uint32_t)(v < 0 ? -v : v);
+        const uint32_t wh = a >> 3 > 15 ? 15 : a >> 3, wl = a - 8 * wh;
+        const uint32_t sg = v < 0 ? 0x20u : 0u;
+        const uint32_t ch = sg | wh, cl = sg | wl;
+        const int bit = 6 * f, wd = bit >> 5, sh = bit & 31;
+        h[wd] |= ch << sh;
+        l[wd] |= cl << sh;
+        if (sh > 26) {
+          h[wd + 1] |= ch >> (32 - sh);
+          l[wd + 1] |= cl >> (32 - sh);
+        }
+      }
+      sw = scales[i];
+    }
+    // sw = mant * 2^ew, mant in [1, 2) (a subnormal keeps ew = -126, mant < 1;
+    // beyond 2^120 the rest of the exponent moves into mant).
+    const uint32_t bits = __float_as_uint(sw);
+    const int ef = (int)((bits >> 23) & 0xff);
+    int ew = ef == 0 ? -126 : ef - 127;
+    float mant = ef == 0 ? sw * 0x1p126f : __uint_as_float((bits & 0x807fffffu) | 0x3f800000u);
+    if (ew > 120) {
+      mant = ldexpf(mant, ew - 120);
+      ew = 120;
+    }
+    if (sw == 0.0f) {
+      ew = 0;
+      mant = 0.0f;
+    }
+    const _Float16 m0 = (_Float16)mant;
+    const _Float16 m1 = (_Float16)(mant - (float)m0);
+    const uint32_t b0 = __builtin_bit_cast(uint16_t, m0), b1 = __builtin_bit_cast(uint16_t, m1);
+    uint8_t* d = out + ((int64_t)(r >> 5) * B + b) * kChunk8 + (r & 31) * 16;
+    *(uint4*)d = make_uint4(h[0], h[1], h[2], h[3]);
+    *(uint4*)(d + 512) = make_uint4(h[4], h[5], b0 | (b0 << 16), b0 << 16);
+    *(uint4*)(d + 1024) = make_uint4(h[4], h[5], b1 | (b1 << 16), 0u);
+    *(uint4*)(d + 1536) = make_uint4(l[0], l[1], l[2], l[3]);
+    *(uint4*)(d + 2048) = make_uint4(l[4], l[5], (uint32_t)(127 + 6 + ew), (uint32_t)(127 + 3 + ew));
+  }
+}
+
 constexpr int kPKB = 8;     // blocks per stage of the prepacked GEMM
 static_assert(kKB % kPKB == 0, "a K split holds whole prepacked stages");
 
@@ -635,20 +705,28 @@ struct F6PParams {
   int vec;                 // the output allows 16-byte stores
 };
 
-// Stages of kPKB blocks; a stage's weights (kPKB x SN chunks, 24 KB) move
-// into one of two LDS buffers by DMA, three chunks per wave, issued at the
-// start of the stage before: they arrive while that stage computes. The
-// activation records stay in a register ring one stage (kPKB / 2 own
-// blocks) ahead. The DMA is inline asm (buffer_load16_to_lds), so the
-// compiler's waits ignore it; each stage ends with an explicit vmcnt that
-// covers this wave's DMA (only the stage's ring refills are younger) and a
-// barrier that publishes every wave's DMA and retires the buffer just read.
-template <int SN>
+// Stages of kPKB blocks; a stage's weights (SN row groups x kPKB blocks:
+// 24 KB of Q4, 60 KB of Q8, contiguous per row group in the prepack) move
+// into one of two LDS buffers by DMA in 1 KB pieces, spread over the waves,
+// issued at the start of the stage before: they arrive while that stage
+// computes. The activation records stay in a register ring one stage
+// (kPKB / 2 own blocks) ahead. The DMA is inline asm (buffer_load16_to_lds),
+// so the compiler's waits ignore it; each stage ends with an explicit vmcnt
+// that covers this wave's DMA (only the stage's ring refills are younger)
+// and a barrier that publishes every wave's DMA and retires the buffer just
+// read. Blocks past this split's end and row groups past the matrix read
+// whatever lies there (the next blocks or row group, or zeros past the
+// prepack): finite codes and scales that meet zero activations or are
+// never stored.
+template <int SN, bool kQ8>
 __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   constexpr int BN = SN * 32;
-  constexpr int kStage = kPKB * SN * kChunk;
-  constexpr int kChunks = kPKB * SN;                  // DMA chunks per stage
-  constexpr int kPerWave = (kChunks + kWaves - 1) / kWaves;
+  constexpr int kCh = kQ8 ? kChunk8 : kChunk;         // bytes per (row group, block)
+  constexpr int kGroupBytes = kPKB * kCh;             // a row group's stage, contiguous
+  constexpr int kStage = SN * kGroupBytes;
+  constexpr int kPieces = kStage / 1024;              // DMA instructions per stage
+  constexpr int kPiecesPerGroup = kGroupBytes / 1024;
+  static_assert(kGroupBytes % 1024 == 0, "whole 1 KB pieces per row group");
   constexpr int kRingP = kPKB / 2;                    // own-parity blocks per stage
   constexpr int kLds = 2 * kStage > epilogue_lds_bytes<SN>() ? 2 * kStage : epilogue_lds_bytes<SN>();
   __shared__ __align__(16) uint8_t lds[kLds];
@@ -669,22 +747,19 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   const int b_end = min(B, b_begin + p.split_blocks);
   const int stages = (b_end - b_begin + kPKB - 1) / kPKB;
   const i32x4 rpanel = buffer_rsrc(p.panel, (uint32_t)((size_t)groups * B * kRec));
-  const i32x4 rpk = buffer_rsrc(p.packed, (uint32_t)((size_t)groups_n * B * kChunk));
+  const i32x4 rpk = buffer_rsrc(p.packed, (uint32_t)((size_t)groups_n * B * kCh));
   const uint32_t lds0 = lds_address(lds);
 
-  // Stage s's weights into buffer `buf`, chunk (kb, j) at [kb][j]. Blocks
-  // past this split and groups past the matrix read a valid chunk instead
-  // (clamped): their products meet zero activations or are never stored.
+  // Stage s's weights into buffer `buf`, [row group j][block kb][kCh].
   auto dma_w = [&](int s, int buf) {
     const int b0 = b_begin + s * kPKB;
 #pragma unroll
-    for (int e = 0; e < kPerWave; e++) {
-      const int c = wave * kPerWave + e;
-      if (c < kChunks) {
-        const int kb = c / SN, j = c - kb * SN;
-        const int b = min(b0 + kb, b_end - 1);
-        const int gg = min(g0 + j, groups_n - 1);
-        buffer_load16_to_lds(rpk, lds0 + buf * kStage + c * kChunk, (gg * B + b) * kChunk + lane * 16);
+    for (int e = 0; e < (kPieces + kWaves - 1) / kWaves; e++) {
+      const int c = wave + kWaves * e;
+      if (c < kPieces) {
+        const int j = c / kPiecesPerGroup, q = c - j * kPiecesPerGroup;
+        buffer_load16_to_lds(rpk, lds0 + buf * kStage + j * kGroupBytes + q * 1024,
+                             ((g0 + j) * B + b0) * kCh + q * 1024 + lane * 16);
       }
     }
   };
@@ -715,16 +790,24 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[j][v] = fmaf(pd[v], ps[v], acc[j][v]);
   };
-  // B fragment of one tile: lane l takes row l % 32's record (both lane
-  // halves the same weights: the K slots of the h and the l codes).
+  // B fragment of one tile: lane l takes row l % 32's parts (both lane
+  // halves the same codes: the K slots of the h and the l activation codes).
+  // Q4: codes 0..3, then codes 4..5 + scale slots. Q8: wh 0..3, wh 4..5 +
+  // this lane half's scale slots, wl 0..3, wl 4..5 + the E8M0 bytes.
   struct BFrag {
-    uint4 h0, h1;
+    uint4 c[kQ8 ? 4 : 2];
   };
   auto read_b = [&](const uint8_t* sbase, int kb, int j) {
-    const uint8_t* q = sbase + (kb * SN + j) * kChunk + (lane & 31) * 16;
+    const uint8_t* q = sbase + (j * kPKB + kb) * kCh + (lane & 31) * 16;
     BFrag f;
-    f.h0 = *(const uint4*)q;
-    f.h1 = *(const uint4*)(q + kChunk / 2);
+    f.c[0] = *(const uint4*)q;
+    if constexpr (kQ8) {
+      f.c[1] = *(const uint4*)(q + 512 + (lane >> 5) * 512);
+      f.c[2] = *(const uint4*)(q + 1536);
+      f.c[3] = *(const uint4*)(q + 2048);
+    } else {
+      f.c[1] = *(const uint4*)(q + 512);
+    }
     return f;
   };
   // One block of K for the SN tiles; `nb` holds tile 0 of this block on
@@ -733,16 +816,31 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
     asm volatile("" : "+v"(lo), "+v"(hi));
     const v8i a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     const int sa = hi[3];
-    const h4 as = __builtin_bit_cast(h4, make_uint2((uint32_t)hi[2], (uint32_t)hi[3]));
+    // The scale MFMA's activation slots: (p0, p1, byte, p2) on the h lanes;
+    // for Q8 the l lanes take (p0, p1) of their token's h lane (a
+    // permlane32 swap broadcasts the low half), beside their (byte, 0).
+    uint32_t s01 = (uint32_t)hi[2];
+    if constexpr (kQ8) s01 = (uint32_t)__builtin_amdgcn_permlane32_swap(hi[2], hi[2], false, false)[0];
+    const h4 as = __builtin_bit_cast(h4, make_uint2(s01, (uint32_t)hi[3]));
     BFrag cur = nb;
 #pragma unroll
     for (int j = 0; j < SN; j++) {
-      const v8i bq = {(int)cur.h0.x, (int)cur.h0.y, (int)cur.h0.z, (int)cur.h0.w,
-                      (int)cur.h1.x, (int)cur.h1.y, 0, 0};
-      const h4 bs = __builtin_bit_cast(h4, make_uint2(cur.h1.z, cur.h1.w));
+      const v8i bq = {(int)cur.c[0].x, (int)cur.c[0].y, (int)cur.c[0].z, (int)cur.c[0].w,
+                      (int)cur.c[1].x, (int)cur.c[1].y, 0, 0};
+      const h4 bs = __builtin_bit_cast(h4, make_uint2(cur.c[1].z, cur.c[1].w));
       const v16f z = {};
       const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(as, bs, z, 0, 0, 0);
-      const v16f d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bq, z, 2, 2, 0, sa, 0, 130);
+      v16f d;
+      if constexpr (kQ8) {
+        const v8i bl = {(int)cur.c[2].x, (int)cur.c[2].y, (int)cur.c[2].z, (int)cur.c[2].w,
+                        (int)cur.c[3].x, (int)cur.c[3].y, 0, 0};
+        d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bq, z, 2, 2, 0, sa, 0,
+                                                           (int)cur.c[3].z);
+        d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bl, d, 2, 2, 0, sa, 0,
+                                                           (int)cur.c[3].w);
+      } else {
+        d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bq, z, 2, 2, 0, sa, 0, 130);
+      }
       if (j + 1 < SN) {
         cur = read_b(sbase, kb, j + 1);
       } else {
@@ -751,9 +849,9 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
       fold(j > 0 ? j - 1 : SN - 1);
       pd = d;
       ps = sc;
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // the two MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // next fragment
-      __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // previous fold
+      __builtin_amdgcn_sched_group_barrier(0x008, kQ8 ? 3 : 2, 0);   // the MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, kQ8 ? 4 : 2, 0);   // next fragment
+      __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);            // previous fold
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -987,10 +1085,11 @@ bool f6_shape_ok(int64_t rows, int64_t cols, int64_t n) {
          rows * (cols / kBlock) * 2 < (1ll << 31) && n * rows < (1ll << 31);
 }
 
-// The prepacked operand (whole 32-row groups, 1 KB per group and block)
-// below 2 GB as well.
-bool f6p_shape_ok(int64_t rows, int64_t cols, int64_t n) {
-  return f6_shape_ok(rows, cols, n) && (rows + 31) / 32 * (cols / kBlock) * kChunk < (1ll << 31);
+// The prepacked operand (whole 32-row groups, 1 KB per group and block for
+// Q4, 2.5 KB for Q8) below 2 GB as well.
+bool f6p_shape_ok(int64_t rows, int64_t cols, int64_t n, bool q8 = false) {
+  return f6_shape_ok(rows, cols, n) &&
+         (rows + 31) / 32 * (cols / kBlock) * (q8 ? kChunk8 : kChunk) < (1ll << 31);
 }
 
 template <int SN>
@@ -1038,7 +1137,7 @@ int launch_f6(const uint8_t* qs, const uint16_t* scales, const uint8_t* panel, f
   return DNX_OK;
 }
 
-template <int SN>
+template <int SN, bool kQ8 = false>
 int launch_f6p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t rows,
                int64_t cols, int64_t n, hipStream_t stream, float* fixed_part = nullptr,
                size_t fixed_floats = 0) {
@@ -1077,7 +1176,7 @@ int launch_f6p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t ro
     }
   }
   p.vec = (rows % 4 == 0 && ((uintptr_t)(p.part ? (void*)p.part : (void*)y) & 15) == 0) ? 1 : 0;
-  hipLaunchKernelGGL((gemm_f6p_kernel<SN>), dim3((unsigned)p.tiles, (unsigned)splits),
+  hipLaunchKernelGGL((gemm_f6p_kernel<SN, kQ8>), dim3((unsigned)p.tiles, (unsigned)splits),
                      dim3(kThreads), 0, stream, p);
   if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
   if (splits > 1) {
@@ -1190,6 +1289,34 @@ int dnx_gemm_q4_f6s(const void* packed, const void* panel, float* y, int64_t row
     hipLaunchKernelGGL(gemm_f6s_kernel<1>, grid, dim3(kThreads), 0, (hipStream_t)stream, p);
   }
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int64_t dnx_q8_f6pack_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0 || cols % kBlock != 0) return -1;
+  return (rows + 31) / 32 * (cols / kBlock) * kChunk8;
+}
+
+int dnx_pack_q8_f6(const int8_t* qs, const float* scales, void* packed, int64_t rows,
+                   int64_t cols, dnx_stream_t stream) {
+  if (rows <= 0 || cols <= 0 || cols % kBlock != 0 || rows >= (1ll << 31) || ((uintptr_t)qs & 15) ||
+      ((uintptr_t)scales & 3) || ((uintptr_t)packed & 15)) {
+    return DNX_EINVAL;
+  }
+  const int64_t count = (rows + 31) / 32 * 32 * (cols / kBlock);
+  hipLaunchKernelGGL(pack_q8_f6_kernel, dim3(panel_grid(count)), dim3(kPanelThreads), 0,
+                     (hipStream_t)stream, qs, scales, (uint8_t*)packed, (int)rows,
+                     (int)(cols / kBlock), count);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_gemm_q8_f6p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
+                    int64_t n, dnx_stream_t stream) {
+  if (!f6p_shape_ok(rows, cols, n, true) || ((uintptr_t)panel & 15) ||
+      ((uintptr_t)packed & 15) || ((uintptr_t)y & 3)) {
+    return DNX_EINVAL;
+  }
+  return launch_f6p<3, true>((const uint8_t*)packed, (const uint8_t*)panel, y, rows, cols, n,
+                             (hipStream_t)stream);
 }
 
 int64_t dnx_gemm_q4_f6p_noalloc_max_floats(void) { return (int64_t)kScratchFloats; }

@@ -380,6 +380,29 @@ def gemm_q4_f6s(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> 
                                        _stream(stream)), "dnx_gemm_q4_f6s")
 
 
+def q8_f6pack_bytes(rows: int, cols: int) -> int:
+    return int(_lib.load().dnx_q8_f6pack_bytes(rows, cols))
+
+
+def pack_q8_f6(qs, scales, packed, rows: int, cols: int, stream=None) -> None:
+    """Load-time re-encoding of Q8 weights for the fp6 GEMM (dnx_gemm_q8_f6p)."""
+    _need("pack_q8_f6",
+          qs=(qs, rows * cols),
+          scales=(scales, rows * (cols // 32) * 4),
+          packed=(packed, q8_f6pack_bytes(rows, cols)))
+    _check(_lib.load().dnx_pack_q8_f6(_ptr(qs), _ptr(scales), _ptr(packed), rows, cols,
+                                      _stream(stream)), "dnx_pack_q8_f6")
+
+
+def gemm_q8_f6p(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _need("gemm_q8_f6p",
+          packed=(packed, q8_f6pack_bytes(rows, cols)),
+          panel=(panel, f6_panel_bytes(n, cols)),
+          y=(y, n * rows * 4))
+    _check(_lib.load().dnx_gemm_q8_f6p(_ptr(packed), _ptr(panel), _ptr(y), rows, cols, n,
+                                       _stream(stream)), "dnx_gemm_q8_f6p")
+
+
 def argmax_workspace(n: int, device="cuda") -> torch.Tensor:
     nbytes = int(_lib.load().dnx_argmax_workspace_bytes(n))
     return torch.empty(nbytes, dtype=torch.uint8, device=device)

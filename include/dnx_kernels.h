@@ -276,6 +276,21 @@ int dnx_pack_q4_f6(const uint8_t* qs, const uint16_t* scales, void* packed, int6
 int dnx_gemm_q4_f6p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
                     int64_t n, dnx_stream_t stream);
 
+// The same GEMM for Q8 weights (lab_gemm_q8 mode 1, lab_native.c:553-579):
+// a load-time re-encoding of the engine's Q8 layout (int8 + fp32 scale per
+// block) into two fp6 digit planes, |w| = 8 wh + wl, and the scale split into
+// its E8M0 exponent and two fp16 mantissa pieces, tile-major
+// (dnx_q8_f6pack_bytes(rows, cols) bytes, 2.5 KB per 32-row group and block,
+// written once by dnx_pack_q8_f6). Two dot MFMAs per block, chained exactly;
+// the same activation panel as the Q4 GEMMs (dnx_quantize_q8_f6panel).
+// Exact block dots (int8 weights including -128), fp32 within 1e-4 relative
+// (1e-5 absolute near zero) of the CPU kernel.
+int64_t dnx_q8_f6pack_bytes(int64_t rows, int64_t cols);
+int dnx_pack_q8_f6(const int8_t* qs, const float* scales, void* packed, int64_t rows,
+                   int64_t cols, dnx_stream_t stream);
+int dnx_gemm_q8_f6p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
+                    int64_t n, dnx_stream_t stream);
+
 // The prefill chunk GEMM (lab_gemm_q4 mode 1, lab_native.c:1059-1080, at
 // the reference's prefill chunks of up to 64 tokens, lib/src/model.dart:91)
 // on prepacked weights: one launch over the whole K (no split partials, no

@@ -336,3 +336,94 @@ def test_chunk_gemm_refuses_bad_shapes(gpu_ready):
         D.gemm_q4_f6s(z, z, y, 64, 48, 5)    # cols not a multiple of 32
     with pytest.raises(RuntimeError):
         D.gemm_q4_f6s(z, z, y, 64, 64, 0)    # no tokens
+
+
+# --------------------------------------------- Q8 weights on the fp6 GEMM
+
+def gemm_q8_f6(qs, sc, xq, xsc, rows, cols, n):
+    panel = torch.full((D.f6_panel_bytes(n, cols),), 0x7f, dtype=torch.uint8, device="cuda")
+    D.pack_f6panel(dev(xq), dev(xsc), panel, n, cols)
+    packed = torch.empty(D.q8_f6pack_bytes(rows, cols), dtype=torch.uint8, device="cuda")
+    D.pack_q8_f6(dev(qs), dev(sc), packed, rows, cols)
+    y = torch.full((n, rows), float("nan"), dtype=torch.float32, device="cuda")
+    D.gemm_q8_f6p(packed, panel, y, rows, cols, n)
+    return host(y)
+
+
+@pytest.mark.parametrize("rows,cols,n", [(130, 256, 70), (33, 96, 5), (97, 1024, 131),
+                                         (200, 320, 300)])
+def test_q8_block_dots_are_exact(gpu_ready, orc, rows, cols, n):
+    """Scale 1 on one block and 0 on the others: y is that block's exact dot
+    sum_k xq * w, for every block, against brute force. The weights cover
+    every int8 value including -128 (two fp6 digits: 8 * 15 + 8), the
+    activations every |xq| up to 127."""
+    rng = np.random.default_rng(rows + cols + n + 3)
+    B = cols // 32
+    xq = rng.integers(-127, 128, (n, cols), dtype=np.int8)
+    xq[0, :32] = 127
+    xq[-1, -32:] = -127
+    qs = rng.integers(-128, 128, (rows, cols), dtype=np.int16).astype(np.int8)
+    qs[0, :32] = -128
+    qs[-1, -32:] = 127
+    qs[1 % rows, :256 if cols >= 256 else cols] = np.arange(-128, 128, dtype=np.int16)[:min(cols, 256)].astype(np.int8)
+    want = orc.block_dots_q8(qs, xq)
+    for b in range(B):
+        sw = np.zeros((rows, B), np.float32)
+        sw[:, b] = 1.0
+        xsc = np.zeros((n, B), np.float32)
+        xsc[:, b] = 1.0
+        y = gemm_q8_f6(qs, sw, xq, xsc, rows, cols, n)
+        assert np.array_equal(y, want[:, :, b].astype(np.float32)), f"block {b}"
+
+
+def test_q8_power_of_two_scales_are_exact(gpu_ready, orc):
+    """Scales that are powers of two (both exponents ride in the MFMAs' E8M0
+    scales, the mantissas are 1): every term exact; only the fp32 rounding of
+    the running sum remains."""
+    rows, cols, n = 64, 512, 96
+    rng = np.random.default_rng(12)
+    B = cols // 32
+    xq = rng.integers(-127, 128, (n, cols), dtype=np.int8)
+    qs = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+    ex = rng.integers(-20, 10, (n, B))
+    ew = rng.integers(-30, 30, (rows, B))
+    xsc = np.ldexp(np.ones((n, B)), ex).astype(np.float32)
+    sw = np.ldexp(np.ones((rows, B)), ew).astype(np.float32)
+    d = orc.block_dots_q8(qs, xq).astype(np.float64)
+    terms = d * np.ldexp(1.0, ex)[:, None, :] * np.ldexp(1.0, ew)[None, :, :]
+    y = gemm_q8_f6(qs, sw, xq, xsc, rows, cols, n)
+    assert np.max(np.abs(y - terms.sum(axis=2)) / np.abs(terms).sum(axis=2)) < 2 ** -20
+
+
+@pytest.mark.parametrize("rows,cols,n,fp32_scales", [(4304, 1152, 1024, True),
+                                                     (1152, 4320, 1024, True),
+                                                     (1024, 1024, 1024, False),
+                                                     (70, 96, 13, True), (128, 128, 40, False),
+                                                     (97, 160, 129, True),
+                                                     (2048, 4096, 256, False),
+                                                     (300, 8192, 64, True)])
+def test_q8_gemm_within_tolerance(gpu_ready, orc, rows, cols, n, fp32_scales):
+    """Against the exact products (error / sum|terms| below 1e-5) and the CPU
+    kernel's outputs (relative 1e-4, absolute 1e-5 near zero): GGUF-style
+    fp16-exact scales, and weights quantized by lab_quantize_q8 (the vision
+    encoder's BF16 -> Q8 path), whose fp32 scales use both mantissa pieces."""
+    rng = np.random.default_rng(rows * 7 + cols + n)
+    if fp32_scales:
+        qs, sc = orc.quantize_q8((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
+    else:
+        # GGUF-style fp16 scales at the size of real weights (|w| near 0.02):
+        # the synthetic scales / 16, still fp16 values. At the synthetic
+        # size itself (|w| up to 3.8) outputs reach ~20, where two fp32 sums
+        # in different orders differ by more than the 1e-5 absolute bar.
+        qs, sc = synth.q8_weights(rng, rows, cols)
+        sc = (sc / np.float32(16)).astype(np.float16).astype(np.float32)
+    xs = synth.activations(rng, n, cols)
+    xq, xsc = orc.quantize_q8(xs)
+    ref = orc.gemm_q8(qs, sc, xs, n, threads=8, mode=1)
+    y = gemm_q8_f6(qs, sc, xq, xsc, rows, cols, n)
+    d = orc.block_dots_q8(qs, xq).astype(np.float64)
+    s = (sc[None, :, :].astype(np.float32) * xsc[:, None, :]).astype(np.float32).astype(np.float64)
+    exact, mag = (d * s).sum(axis=2), np.abs(d * s).sum(axis=2)
+    assert np.all(np.abs(y - exact) <= 1e-5 * mag)
+    ok, worst_rel, worst_abs = within_tolerance(y, ref)
+    assert ok, (worst_rel, worst_abs)
