@@ -446,15 +446,42 @@ def bench_c4(torch, D, synth, timer, steps, warmup):
     def fc2f_(i):
         D.gemm_q8_float(q2, s2, h, y, 1152, 4320, M)
 
+    # The scaled-fp6 MFMA route: weights re-encoded once at load (two fp6
+    # digits per int8, the scale's mantissa in two pieces), the activations
+    # quantized straight into the fp6 panel.
+    p1 = torch.empty(D.q8_f6pack_bytes(4320, 1152), dtype=torch.uint8, device="cuda")
+    p2 = torch.empty(D.q8_f6pack_bytes(1152, 4320), dtype=torch.uint8, device="cuda")
+    pan1 = torch.empty(D.f6_panel_bytes(M, 1152), dtype=torch.uint8, device="cuda")
+    pan2 = torch.empty(D.f6_panel_bytes(M, 4320), dtype=torch.uint8, device="cuda")
+
+    def pack_w(i):
+        D.pack_q8_f6(q1, s1, p1, 4320, 1152)
+        D.pack_q8_f6(q2, s2, p2, 1152, 4320)
+
+    def fc1p_(i):
+        D.quantize_q8_f6panel(xd, pan1, M, 1152)
+        D.gemm_q8_f6p(p1, pan1, h, 4320, 1152, M)
+
+    def fc2p_(i):
+        D.quantize_q8_f6panel(h, pan2, M, 4320)
+        D.gemm_q8_f6p(p2, pan2, y, 1152, 4320, M)
+
     n = max(10, steps // 4)
     quant_w(0)
-    means = timer.kernel_means([quant_w, fc1_, gelu_, fc2_, fc1f_, fc2f_], n)
+    pack_w(0)
+    means = timer.kernel_means([quant_w, fc1_, gelu_, fc2_, fc1f_, fc2f_, pack_w, fc1p_, fc2p_], n)
     qbytes = (4304 * 1152 * 2 + 4320 * 1152 + 4320 * 36 * 4) + (1152 * 4304 * 2 + 1152 * 4320 + 1152 * 135 * 4)
     ops = 2 * M * 4304 * 1152
     return {"quantize_weights_ms": means[0], "quantize_weights_gbps": qbytes / means[0] / 1e6,
             "fc1_ms": means[1], "fc1_tops": ops / means[1] / 1e9, "gelu_ms": means[2],
             "fc2_ms": means[3], "fc2_tops": ops / means[3] / 1e9,
             "pair_tops": 2 * ops / (means[1] + means[2] + means[3]) / 1e9,
+            "fp6_route": {"pack_weights_ms": means[6],
+                          "fc1_ms": means[7], "fc1_tops": ops / means[7] / 1e9,
+                          "fc2_ms": means[8], "fc2_tops": ops / means[8] / 1e9,
+                          "pair_tops": 2 * ops / (means[7] + means[2] + means[8]) / 1e9,
+                          "kernels": "quantize_f6_panel4_kernel + gemm_f6p_kernel<3, Q8> "
+                                     "(scaled fp6 MFMA)"},
             "float_inputs": {"fc1_ms": means[4], "fc1_tops": ops / means[4] / 1e9,
                              "fc2_ms": means[5], "fc2_tops": ops / means[5] / 1e9,
                              "kernel": "gemm_float_kernel (x in three exact bf16 pieces, "

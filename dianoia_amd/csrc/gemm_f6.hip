@@ -705,12 +705,13 @@ struct F6PParams {
   int vec;                 // the output allows 16-byte stores
 };
 
-// Stages of kPKB blocks; a stage's weights (SN row groups x kPKB blocks:
-// 24 KB of Q4, 60 KB of Q8, contiguous per row group in the prepack) move
+// Stages of kPKB blocks (Q8: kPKB / 2); a stage's weights (SN row groups x
+// its blocks: 24 KB of Q4, 30 KB of Q8, so that two or three workgroups fit
+// a CU's LDS; contiguous per row group in the prepack) move
 // into one of two LDS buffers by DMA in 1 KB pieces, spread over the waves,
 // issued at the start of the stage before: they arrive while that stage
 // computes. The activation records stay in a register ring one stage
-// (kPKB / 2 own blocks) ahead. The DMA is inline asm (buffer_load16_to_lds),
+// (half the stage's blocks, this wave's parity) ahead. The DMA is inline asm (buffer_load16_to_lds),
 // so the compiler's waits ignore it; each stage ends with an explicit vmcnt
 // that covers this wave's DMA (only the stage's ring refills are younger)
 // and a barrier that publishes every wave's DMA and retires the buffer just
@@ -722,12 +723,13 @@ template <int SN, bool kQ8>
 __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   constexpr int BN = SN * 32;
   constexpr int kCh = kQ8 ? kChunk8 : kChunk;         // bytes per (row group, block)
-  constexpr int kGroupBytes = kPKB * kCh;             // a row group's stage, contiguous
+  constexpr int kPK = kQ8 ? kPKB / 2 : kPKB;          // blocks per stage
+  constexpr int kGroupBytes = kPK * kCh;             // a row group's stage, contiguous
   constexpr int kStage = SN * kGroupBytes;
   constexpr int kPieces = kStage / 1024;              // DMA instructions per stage
   constexpr int kPiecesPerGroup = kGroupBytes / 1024;
   static_assert(kGroupBytes % 1024 == 0, "whole 1 KB pieces per row group");
-  constexpr int kRingP = kPKB / 2;                    // own-parity blocks per stage
+  constexpr int kRingP = kPK / 2;                    // own-parity blocks per stage
   constexpr int kLds = 2 * kStage > epilogue_lds_bytes<SN>() ? 2 * kStage : epilogue_lds_bytes<SN>();
   __shared__ __align__(16) uint8_t lds[kLds];
 
@@ -745,14 +747,14 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   const int g = tm * kTileM + mg;
   const int b_begin = blockIdx.y * p.split_blocks;
   const int b_end = min(B, b_begin + p.split_blocks);
-  const int stages = (b_end - b_begin + kPKB - 1) / kPKB;
+  const int stages = (b_end - b_begin + kPK - 1) / kPK;
   const i32x4 rpanel = buffer_rsrc(p.panel, (uint32_t)((size_t)groups * B * kRec));
   const i32x4 rpk = buffer_rsrc(p.packed, (uint32_t)((size_t)groups_n * B * kCh));
   const uint32_t lds0 = lds_address(lds);
 
   // Stage s's weights into buffer `buf`, [row group j][block kb][kCh].
   auto dma_w = [&](int s, int buf) {
-    const int b0 = b_begin + s * kPKB;
+    const int b0 = b_begin + s * kPK;
 #pragma unroll
     for (int e = 0; e < (kPieces + kWaves - 1) / kWaves; e++) {
       const int c = wave + kWaves * e;
@@ -798,7 +800,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
     uint4 c[kQ8 ? 4 : 2];
   };
   auto read_b = [&](const uint8_t* sbase, int kb, int j) {
-    const uint8_t* q = sbase + (j * kPKB + kb) * kCh + (lane & 31) * 16;
+    const uint8_t* q = sbase + (j * kPK + kb) * kCh + (lane & 31) * 16;
     BFrag f;
     f.c[0] = *(const uint4*)q;
     if constexpr (kQ8) {
@@ -868,12 +870,12 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
     // W(s + 1) into the buffer stage s - 1 read (every wave is past it).
     if (s >= 1 && s + 1 < stages) dma_w(s + 1, buf ^ 1);
     const uint8_t* sbase = lds + buf * kStage;
-    const int b0 = b_begin + s * kPKB;
+    const int b0 = b_begin + s * kPK;
     BFrag nb = read_b(sbase, kp, 0);
 #pragma unroll
     for (int r = 0; r < kRingP; r++) {
       const int kb = kp + 2 * r;
-      compute(sbase, kb, min(kb + 2, kPKB - 1), rlo[r], rhi[r], nb);
+      compute(sbase, kb, min(kb + 2, kPK - 1), rlo[r], rhi[r], nb);
       load_a(b0 + kb + 2 * kRingP, rlo[r], rhi[r]);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1042,16 +1044,33 @@ float* part_workspace(size_t bytes) {
   return gF6Part;
 }
 
+// Blocks per K part of the fp6 GEMMs (both layouts, so that they add the
+// same partials in the same order). A workgroup's registers fill its CU, so
+// a launch runs in rounds of 256 workgroups: K is split only when the tiles
+// leave at least half the CUs idle (from 129 to 255 tiles a split would add
+// a round and gain nothing), into the most parts that still fit one round
+// (tiles x parts <= 256), each of whole kKB-block stages.
+int f6_split_blocks(int tiles, int B) {
+  int splits = 1;
+  if (tiles <= 128) {
+    splits = 256 / tiles;
+    const int max_splits = (B + kKB - 1) / kKB;
+    if (splits > max_splits) splits = max_splits;
+  }
+  const int per = (B + splits - 1) / splits;
+  return (per + kKB - 1) / kKB * kKB;
+}
+
 // Split partials of dnx_gemm_q4_f6p_noalloc: a fixed array in the code
 // object, so that entry point never allocates. Every GPU the library runs on
 // holds its own copy from the module's load until the process ends. In host
 // code `scratch` names only a host-side stand-in: kernels get the address
 // hipGetSymbolAddress returns for the current device (scratch_on_device).
-// Size: K is split only below 192 tiles, into at most ceil(256 / tiles)
-// parts, and n x rows <= (128 x tiles_m) x (96 x tiles_n) = 12288 x tiles,
-// so the partials never exceed 12288 x (256 + 191) floats (21 MiB) for any
-// shape the GEMM accepts; the bound is still checked on every call.
-constexpr size_t kScratchFloats = (size_t)12288 * 447;
+// Size: K is split into at most 256 / tiles parts (f6_split_blocks), and
+// n x rows <= (128 x tiles_m) x (96 x tiles_n) = 12288 x tiles, so the
+// partials never exceed 12288 x 256 floats (12 MiB) for any shape the GEMM
+// accepts; the bound is still checked on every call.
+constexpr size_t kScratchFloats = (size_t)12288 * 256;
 static __device__ __align__(256) float scratch[kScratchFloats];
 
 constexpr int kMaxDevices = 64;
@@ -1107,17 +1126,8 @@ int launch_f6(const uint8_t* qs, const uint16_t* scales, const uint8_t* panel, f
   p.tiles_m = (int)((n + kTileM * kTokens - 1) / (kTileM * kTokens));
   p.tiles = p.tiles_m * (int)((rows + BN - 1) / BN);
   const int B = (int)(cols / kBlock);
-  // Split K when the tiles alone leave CUs idle: about 256 workgroups, each
-  // with at least one stage of blocks.
-  int splits = 1;
-  if (p.tiles < 192) {
-    splits = (256 + p.tiles - 1) / p.tiles;
-    const int max_splits = (B + kKB - 1) / kKB;
-    if (splits > max_splits) splits = max_splits;
-  }
-  p.split_blocks = (B + splits - 1) / splits;
-  p.split_blocks = (p.split_blocks + kKB - 1) / kKB * kKB;  // whole stages per split
-  splits = (B + p.split_blocks - 1) / p.split_blocks;
+  p.split_blocks = f6_split_blocks(p.tiles, B);
+  int splits = (B + p.split_blocks - 1) / p.split_blocks;
   const int64_t count = n * rows;
   p.part = nullptr;
   if (splits > 1) {
@@ -1154,15 +1164,8 @@ int launch_f6p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t ro
   const int B = (int)(cols / kBlock);
   // The same split of K as launch_f6 (whole kKB-block parts, kKB a multiple
   // of kPKB), so that both kernels add the same partials in the same order.
-  int splits = 1;
-  if (p.tiles < 192) {
-    splits = (256 + p.tiles - 1) / p.tiles;
-    const int max_splits = (B + kKB - 1) / kKB;
-    if (splits > max_splits) splits = max_splits;
-  }
-  p.split_blocks = (B + splits - 1) / splits;
-  p.split_blocks = (p.split_blocks + kKB - 1) / kKB * kKB;
-  splits = (B + p.split_blocks - 1) / p.split_blocks;
+  p.split_blocks = f6_split_blocks(p.tiles, B);
+  int splits = (B + p.split_blocks - 1) / p.split_blocks;
   const int64_t count = n * rows;
   p.part = nullptr;
   if (splits > 1) {

@@ -54,14 +54,14 @@ def test_noalloc_gemm_matches_allocating_entry(gpu_ready, orc):
 
 
 def test_noalloc_gemm_allocates_nothing(gpu_ready):
-    """The call's defining property: at a shape whose split partials (18.8 MB,
-    2 K parts x 128 tokens x 18336 rows) are larger than any earlier call's,
-    device free memory is the same before and after (an allocating path
-    would have grown its partials buffer by that much); its bits equal the
-    allocating entry point's."""
+    """The call's defining property: at a shape whose split partials (12.6 MB,
+    2 K parts x 128 tokens x 12288 rows) are larger than any earlier call's
+    in this file, device free memory is the same before and after (an
+    allocating path would have grown its partials buffer by that much); its
+    bits equal the allocating entry point's."""
     lib = gpu_ready
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    rows, cols, n = 18336, 4096, 128     # 191 workgroup tiles: K splits 2 ways
+    rows, cols, n = 12288, 4096, 128     # 128 workgroup tiles: K splits 2 ways
     rng = np.random.default_rng(3)
     qs, sc = synth.q4_weights(rng, rows, cols)
     xs = synth.activations(rng, n, cols)
