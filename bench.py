@@ -849,11 +849,19 @@ PMC_KERNELS = {  # kernel-name fragment -> (workload, algorithmic bytes per laun
     "gemm_f16_kernel<true, 3>": (
         "c3 Q4 panel GEMM M=512, 6144x2048", q4_bytes(6144, 2048) + 512 * 2048 + 512 * 64 * 4
         + 512 * 6144 * 4),
-    # The fp6 GEMM reads the prepacked weights (32 B per block) and the fp6
-    # activation panel (2176 B per 32 tokens and block).
-    "gemm_f6p_kernel<3>": (
-        "c3 Q4 fp6 GEMM (prepacked) M=512, 6144x2048", 6144 * 64 * 32 + 16 * 64 * 2176
+    # The fp6 GEMM reads the prepacked weights (32 B per row and block) and
+    # the codes and scales of the fp6 activation panel (2048 of its 2176 B
+    # per 32 tokens and block).
+    "gemm_f6p_kernel<3, false>": (
+        "c3 Q4 fp6 GEMM (prepacked) M=512, 6144x2048", 6144 * 64 * 32 + 16 * 64 * 2048
         + 512 * 6144 * 4),
+    "gemm_kernel<false, 64, 64, 2, 4>": (
+        "c4 fc1 Q8 GEMM (int8 MFMA) M=1024, 4320x1152", q8_bytes(4320, 1152) + 4320 * 36 * 2
+        + 1024 * 1152 + 1024 * 36 * 4 + 1024 * 4320 * 4),
+    # Q8 prepack: 80 B per row and block.
+    "gemm_f6p_kernel<3, true>": (
+        "c4 fc1 Q8 fp6 GEMM (prepacked) M=1024, 4320x1152", 4320 * 36 * 80 + 32 * 36 * 2048
+        + 1024 * 4320 * 4),
     "gemm_float_kernel<false, 4>": (
         "c4 fc1 float-input Q8 GEMM M=1024, 4320x1152", 4320 * 1152 + 4320 * 36 * 4
         + 1024 * 1152 * 4 + 1024 * 4320 * 4),
@@ -862,18 +870,37 @@ PMC_KERNELS = {  # kernel-name fragment -> (workload, algorithmic bytes per laun
 
 def pmc_workload(torch, D, synth, reps):
     """Eager launches for the rocprofv3 --pmc runs: a plain device copy of
-    PMC_COPY_BYTES (the calibration of FETCH_SIZE / WRITE_SIZE), then the
-    config-1 step, the config-2 LM head and the config-3 GEMM, each over
-    rotating weight copies so that every launch reads its weights from HBM,
-    then the causal prefill attention of 512 tokens."""
+    PMC_COPY_BYTES (the calibration of WRITE_SIZE) and a read-only stream
+    over as many bytes (the calibration of FETCH_SIZE), then the config-1
+    step, the config-2 LM head and the config-3 GEMM, each over rotating
+    weight copies so that every launch reads its weights from HBM, config
+    4's fc1 on its three GEMMs, then the causal prefill attention of 512
+    tokens."""
     src = torch.empty(PMC_COPY_BYTES // 4, device="cuda")
     src.fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(reps):
         dst.copy_(src)
     torch.cuda.synchronize()
-    del src, dst
+    del dst
     print("pmc: copy calibration done", file=sys.stderr, flush=True)
+    # The read-only calibration: the GEMV's 16-byte streaming load over the
+    # same PMC_COPY_BYTES (libdnx_ubench.so, dnx_ubench_stream_read).
+    import ctypes
+    ub = ctypes.CDLL(os.path.join(ROOT, "dianoia_amd", "libdnx_ubench.so"))
+    ub.dnx_ubench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                          ctypes.c_void_p, ctypes.c_void_p]
+    ctas = 2048
+    words = torch.empty(ctas * 256, dtype=torch.int32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for _ in range(reps):
+        rc = ub.dnx_ubench_stream_read(src.data_ptr(), PMC_COPY_BYTES, ctas, words.data_ptr(),
+                                       stream)
+        if rc != 0:
+            raise RuntimeError(f"dnx_ubench_stream_read returned {rc}")
+    torch.cuda.synchronize()
+    del src, words
+    print("pmc: read calibration done", file=sys.stderr, flush=True)
 
     (gq, gs), (uq, us), (dq, ds), x = synth.config1()
     copies = copies_for(2 * q4_bytes(6144, 2048) + q4_bytes(2048, 6144))
@@ -940,6 +967,19 @@ def pmc_workload(torch, D, synth, reps):
         D.gemm_q8_float(q1, s1, x4d, h4, 4320, 1152, 1024)
     torch.cuda.synchronize()
     print("pmc: config 4 float done", file=sys.stderr, flush=True)
+    # Config 4's fc1 on int8 inputs: the int8-MFMA GEMM and the Q8 fp6 GEMM.
+    xq4 = torch.empty((1024, 1152), dtype=torch.int8, device="cuda")
+    xs4 = torch.empty((1024, 36), device="cuda")
+    D.quantize_q8(x4d, xq4, xs4, 1024, 1152, 1152)
+    p1 = torch.empty(D.q8_f6pack_bytes(4320, 1152), dtype=torch.uint8, device="cuda")
+    D.pack_q8_f6(q1, s1, p1, 4320, 1152)
+    pan4 = torch.empty(D.f6_panel_bytes(1024, 1152), dtype=torch.uint8, device="cuda")
+    D.quantize_q8_f6panel(x4d, pan4, 1024, 1152)
+    for i in range(reps):
+        D.gemm_q8(q1, s1, xq4, xs4, h4, 4320, 1152, 1024)
+        D.gemm_q8_f6p(p1, pan4, h4, 4320, 1152, 1024)
+    torch.cuda.synchronize()
+    print("pmc: config 4 int8 inputs done", file=sys.stderr, flush=True)
 
     # Causal prefill attention, 512 tokens (the layer steps' matrix-core kernel).
     gen = torch.Generator(device="cuda").manual_seed(6)
@@ -961,8 +1001,12 @@ MFMA_KERNELS = {
                                          I8_PEAK_TOPS),
     "gemm_f16_kernel<true, 3>": ("c3 Q4 GEMM M=512 (fp16 panel)", 2 * 512 * 6144 * 2048,
                                  I8_PEAK_TOPS),
-    "gemm_f6p_kernel<3>": ("c3 Q4 GEMM M=512 (fp6, prepacked)", 2 * 512 * 6144 * 2048,
-                           I8_PEAK_TOPS),
+    "gemm_f6p_kernel<3, false>": ("c3 Q4 GEMM M=512 (fp6, prepacked)", 2 * 512 * 6144 * 2048,
+                                  I8_PEAK_TOPS),
+    "gemm_kernel<false, 64, 64, 2, 4>": ("c4 fc1 Q8 GEMM M=1024 (int8 MFMA)",
+                                         2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
+    "gemm_f6p_kernel<3, true>": ("c4 fc1 Q8 GEMM M=1024 (fp6, prepacked)",
+                                 2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
     "gemm_float_kernel<false, 4>": ("c4 fc1 float inputs M=1024 (bf16)",
                                     2 * 1024 * 4320 * 1152, 2500.0),
     "attention_prefill_kernel<128, 4>": ("prefill attention 512 tokens, 32/8 heads, hd 128",
@@ -1022,20 +1066,23 @@ def _pmc_means(path, counter):
 
 def pmc_summary(fetch_csv, write_csv):
     """HBM bytes per launch of the kernels in PMC_KERNELS from a FETCH_SIZE
-    run and a WRITE_SIZE run (KiB per dispatch), each scaled by what the same
-    counter reads for the calibration copy of PMC_COPY_BYTES."""
+    run and a WRITE_SIZE run (KiB per dispatch). Reads are scaled by what
+    FETCH_SIZE reads for the read-only streaming kernel over PMC_COPY_BYTES
+    (the GEMV's own load), writes by what WRITE_SIZE reads for the copy of
+    PMC_COPY_BYTES; the copy's FETCH_SIZE factor is reported beside."""
     fetch = _pmc_means(fetch_csv, "FETCH_SIZE")
     write = _pmc_means(write_csv, "WRITE_SIZE")
 
-    def calib(table):
-        cands = [(v[0], k) for k, v in table.items() if "copy" in k.lower()]
+    def calib(table, frag):
+        cands = [(v[0], k) for k, v in table.items() if frag in k.lower()]
         if not cands:
-            raise SystemExit("no copy kernel in the counter run")
+            raise SystemExit(f"no {frag} kernel in the counter run")
         kib, name = max(cands)
         return PMC_COPY_BYTES / (kib * 1024.0), name, kib
 
-    ff, fname, fkib = calib(fetch)
-    wf, wname, wkib = calib(write)
+    ff, fname, fkib = calib(fetch, "stream_read")
+    cf, _, ckib = calib(fetch, "copy")
+    wf, wname, wkib = calib(write, "copy")
     kernels = {}
     for frag, (workload, algo) in PMC_KERNELS.items():
         fk = [(v, k) for k, v in fetch.items() if frag in k]
@@ -1050,10 +1097,12 @@ def pmc_summary(fetch_csv, write_csv):
                              "hbm_write_bytes": round(wr), "hbm_bytes_per_launch": round(rd + wr),
                              "algorithmic_bytes": algo,
                              "traffic_over_algorithmic": round((rd + wr) / algo, 4)}
-    return {"calibration": {"kernel": fname, "bytes_read_and_written": PMC_COPY_BYTES,
-                            "fetch_kib": round(fkib, 1), "write_kib": round(wkib, 1),
-                            "fetch_factor": round(ff, 5), "write_factor": round(wf, 5),
-                            "write_kernel": wname},
+    return {"calibration": {"fetch_kernel": fname, "bytes": PMC_COPY_BYTES,
+                            "fetch_kib": round(fkib, 1), "fetch_factor": round(ff, 5),
+                            "write_kernel": wname, "write_kib": round(wkib, 1),
+                            "write_factor": round(wf, 5),
+                            "copy_fetch_kib": round(ckib, 1),
+                            "copy_fetch_factor": round(cf, 5)},
             "kernels": kernels}
 
 

@@ -222,8 +222,12 @@ __device__ __forceinline__ void gemv_body(const GemvParams p) {
       sc = buffer_rsrc(seg_pick(p.seg_scales, seg), rows_s * srow);
     }
     raw[s0 + i] = buffer_load16_stream(q, (int)(live ? oq : kDead));
+    // fp16 scales with the default cache policy: a Q8 row's 128-byte scale
+    // line is read by two requests (half a row each); with the streaming
+    // policy the second fetched the line from HBM again (the LM head read
+    // 1.05x its bytes; 1.00x this way).
     if (kHalf) {
-      swb[s0 + i] = dnx_raw_buffer_load_i16(sc, (int)(live ? os : kDead), 0, kStream);
+      swb[s0 + i] = dnx_raw_buffer_load_i16(sc, (int)(live ? os : kDead), 0, 0);
     } else {
       swb[s0 + i] = dnx_raw_buffer_load_i32(sc, (int)(live ? os : kDead), 0, kStream);
     }

@@ -59,9 +59,13 @@ DNX_DEV float block_max(float v, float* scratch) {
   return t;
 }
 
-// RMSNorm of one row per workgroup (lab_metal.m:327-347): r = 1 / sqrt(
-// sum(x^2) / cols + eps); y = w * (x * r), x * r rounded first; with
-// `accumulate` y is added into out (a post-norm added to the residual).
+// Row-wise RMS normalisation, semantics of lab_metal.m:327-347. Each
+// workgroup owns one row: its threads stride over the row for the sum of
+// squares, one block-wide reduction gives the inverse root of (mean square +
+// eps), and a second pass writes w[j] * (x[j] * r) with the inner product
+// rounded before the weight multiplies it. The `accumulate` flag turns the
+// store into out += value, which is how a norm applied after a block feeds
+// the residual stream without a separate add launch.
 __global__ void __launch_bounds__(kThreads)
 rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, float* out,
                 int cols, float eps, int accumulate) {
@@ -1103,9 +1107,11 @@ copy_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t coun
   }
 }
 
-// A control vector on rows of `cols` values, one workgroup per row
-// (lab_metal.m:531-557): mode 0 adds v; mode 1 removes scale times the
-// row's component along the unit direction v: x - (scale * (x . v)) v.
+// Activation steering in place, semantics of lab_metal.m:531-557. Each
+// workgroup rewrites one row. Mode 0 shifts the row by the vector. Mode 1
+// projects out the vector's direction, scaled: the block reduces the row's
+// dot product with v (v is expected to have unit length), then every
+// element drops (scale * dot) * v[j].
 __global__ void __launch_bounds__(kThreads)
 steer_kernel(float* x, const float* __restrict__ v, int cols, int mode, float scale) {
   __shared__ float scratch[kWaves];

@@ -8,9 +8,14 @@
 // floor the real kernel cannot go below, and runs each part alone and with
 // other VALU counts to show where the time goes.
 //
+// Also here: a read-only streaming kernel, the calibration of rocprofv3's
+// FETCH_SIZE for kernels that only read (the decode GEMVs).
+//
 // Built into its own library (libdnx_ubench.so), not the product library.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "common.h"
 
 namespace {
 
@@ -85,9 +90,50 @@ void launch(int ctas, int threads, int iters, float* out) {
                      0, iters, out);
 }
 
+// Reads bytes (a multiple of 16 * 256 * 4) once, with the decode GEMV's
+// weight load (buffer_load16_stream: 16 bytes per lane, streaming cache
+// policy, a wave's lanes on one contiguous KiB), four loads in flight per
+// lane; each lane folds what it read into one word so that no load can be
+// dropped, and writes it to out. Its FETCH_SIZE per byte is the read-only
+// calibration (a copy kernel's reads come with its writes' request mix).
+constexpr int kReadThreads = 256;
+
+__global__ void __launch_bounds__(kReadThreads)
+stream_read_kernel(const uint8_t* src, int64_t bytes, uint32_t* out) {
+  const dnx::i32x4 r = dnx::buffer_rsrc(src, (uint32_t)bytes);
+  const int64_t step = (int64_t)gridDim.x * kReadThreads * 16;
+  uint32_t h = 0;
+  for (int64_t o = ((int64_t)blockIdx.x * kReadThreads + threadIdx.x) * 16; o < bytes;
+       o += 4 * step) {
+    uint4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int64_t ou = o + u * step;
+      v[u] = dnx::buffer_load16_stream(r, ou < bytes ? (int)ou : -16);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) h ^= v[u].x + v[u].y + v[u].z + v[u].w;
+  }
+  out[(size_t)blockIdx.x * kReadThreads + threadIdx.x] = h;
+}
+
 }  // namespace
 
 extern "C" {
+
+// The streaming read above over `bytes` of src (below 2 GiB, a multiple of
+// 16 KiB) with `ctas` workgroups of 256 threads; out holds ctas * 256 words.
+// Returns 0, -1 for bad arguments, or the HIP error of the launch.
+int dnx_ubench_stream_read(const void* src, int64_t bytes, int ctas, uint32_t* out,
+                           void* stream) {
+  if (bytes <= 0 || bytes >= (1ll << 31) || bytes % 16384 != 0 || ctas <= 0 ||
+      ((uintptr_t)src & 15)) {
+    return -1;
+  }
+  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)ctas), dim3(kReadThreads), 0,
+                     (hipStream_t)stream, (const uint8_t*)src, bytes, out);
+  return (int)hipGetLastError();
+}
 
 // Runs ctas workgroups of `threads` threads (256: one wave per SIMD, 512:
 // two), each wave doing iters x 3 steps with `mfma_mask` MFMAs and `nvalu`

@@ -219,7 +219,12 @@ void lab_gpu_enc_gelu(int64_t x, int64_t xOffset, int64_t count);
 // gpu.dart:102-109, 545-564): per-kind GPU ms and dispatch counts since the
 // last call, in the reference's 18-kind order, followed here by three kinds
 // of this library's own (18 argmax, 19 weight quantization, 20 gelu). Copies
-// at most `kinds` entries and returns the number of kinds (21).
+// at most `kinds` entries and returns the number of kinds (21). A fused
+// launch (several encoded commands in one kernel) books its time under its
+// main kernel's kind and counts each other command under that command's own
+// kind with no time, so the counts equal those of one launch per command.
+// Q4 prefill routes that run a load-time prepack book it once as weight
+// quantization (19) and the activation panel as quantize (10).
 void lab_gpu_set_profiling(int64_t on);
 int64_t lab_gpu_profile(double* ms, int64_t* counts, int64_t kinds);
 
