@@ -314,12 +314,12 @@ def bench_c3(torch, D, synth, timer, steps, warmup):
            "paths": {k: dict(v, gemm_tops=ops / v["gemm_ms"] / 1e9) for k, v in paths.items()}}
     out["issue_floor"] = c3_issue_floor(M, N, K)
     # M = 1..256 sweep on the ABI's route (lab_gpu_enc_matmul_q4): the GEMV
-    # (exact order) up to 4 tokens; prefill chunks of 5..64 tokens (the
-    # reference's prefill, lib/src/model.dart:91) as the fp6 panel quantizer
-    # + the chunk GEMM on the weights' prepack (made once, at first use);
-    # the int8-MFMA GEMM beyond. The batch shapes of the kernels' other
-    # callers (audio encoder / generator and vision attention projections)
-    # lie in this range. Beside each GEMM: the other route's time.
+    # (exact order) up to 4 tokens; from 5 tokens (prefill chunks of up to
+    # 64, the reference's prefill, lib/src/model.dart:91, and the batch
+    # shapes of the kernels' other callers) the fp6 panel quantizer + the
+    # chunk GEMM on the weights' prepack (made once, at first use). Beside
+    # each: the int8-MFMA route's time (quantize + int8 GEMM), the route of
+    # the device-pointer entry points, which keep no prepack.
     sweep = {}
     for m in (1, 2, 4, 8, 16, 32, 64, 128, 256):
         xm = xd[:m].contiguous()
@@ -341,12 +341,9 @@ def bench_c3(torch, D, synth, timer, steps, warmup):
             fn = lambda i, xm=xm, ym=ym, m=m: D.gemv_q4(ws[i % copies][0], ws[i % copies][1],  # noqa: E731
                                                         xm, ym, N, K, m)
             kernel, other = "gemv_q4", None
-        elif m <= 64:
+        else:
             fn, kernel = chunk_route, "quantize_f6panel + gemm_f6s (prepacked chunk GEMM)"
             other = ("int8_route_ms", int8_route)
-        else:
-            fn, kernel = int8_route, "quantize_q8 + gemm_q4 (int8 MFMA)"
-            other = ("chunk_route_ms", chunk_route)
         t = timer.time(fn, n, 3)
         sweep[str(m)] = {"ms": t, "gbps": nbytes / t / 1e6, "tops": 2 * m * N * K / t / 1e9,
                          "kernel": kernel}
@@ -533,8 +530,9 @@ def bench_callers(torch, D, synth, timer, steps):
                     "tops": 2 * n * rows * cols / ms / 1e9, "weight_copies": copies}
         if fmt == "q4" and int8 and n > 4:
             # The chunk GEMM on the weights' prepack, which the lab_gpu_*
-            # command buffer keeps per weight region (its route for 5..64
-            # tokens; timed here at the other token counts too).
+            # command buffer keeps per weight region (its route for 5..512
+            # tokens where the tiled fp6 route does not apply: every shape
+            # here).
             packs = [torch.empty((D.q4_f6pack_bytes(rows, cols),), dtype=torch.uint8,
                                  device="cuda") for _ in range(len(ws))]
             for w, pk in zip(ws, packs):
@@ -547,7 +545,7 @@ def bench_callers(torch, D, synth, timer, steps):
 
             cms = timer.time(chunk, reps, 3)
             out[key]["chunk_route_ms"] = cms
-            if n <= 64:
+            if 5 <= n <= 512:
                 out[key].update({"dnx_matmul_ms": ms, "ms": cms,
                                  "weight_gbps": nbytes / cms / 1e6,
                                  "tops": 2 * n * rows * cols / cms / 1e9,

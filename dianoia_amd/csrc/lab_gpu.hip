@@ -460,9 +460,9 @@ void free_prepacks(int64_t h) {
 }
 
 // The prepacked route: the prepack (made on first use), the activation
-// panel from fp32 x, the GEMM: the chunk GEMM for up to 64 tokens (one
-// launch over the whole K), else the tiled GEMM (the same products as the
-// engine-layout fp6 GEMM, bit for bit).
+// panel from fp32 x, the GEMM: the chunk GEMM (one launch over the whole K)
+// where matmul_uses_f6_chunk takes the shape, else the tiled GEMM (the same
+// products as the engine-layout fp6 GEMM, bit for bit).
 int run_matmul_prepacked(Prepack& pp, int64_t w, int64_t qsOff, int64_t scOff, const float* x,
                          float* y, int64_t rows, int64_t cols, int64_t n) {
   auto s = (dnx_stream_t)gStream;
@@ -477,8 +477,9 @@ int run_matmul_prepacked(Prepack& pp, int64_t w, int64_t qsOff, int64_t scOff, c
   rc = dnx_quantize_q8_f6panel(x, gWs, n, cols, s);
   if (rc != DNX_OK) return rc;
   after_dispatch(kKindQuantize);
-  rc = dnx::matmul_uses_f6_chunk(true, n) ? dnx_gemm_q4_f6s(pp.dev, gWs, y, rows, cols, n, s)
-                                           : dnx_gemm_q4_f6p(pp.dev, gWs, y, rows, cols, n, s);
+  rc = dnx::matmul_uses_f6_chunk(true, rows, cols, n)
+           ? dnx_gemm_q4_f6s(pp.dev, gWs, y, rows, cols, n, s)
+           : dnx_gemm_q4_f6p(pp.dev, gWs, y, rows, cols, n, s);
   if (rc == DNX_OK) after_dispatch(kKindGemmQ4I8);
   return rc;
 }
@@ -491,8 +492,12 @@ bool run_matmul(const Cmd& c, bool q4) {
   const int64_t y = c.a[5], yOff = c.a[6], rows = c.a[7], cols = c.a[8], n = c.a[9];
   use_as_weights(w);
   read_region(x, xOff, n * cols * 4);
-  Prepack* pp = q4 && c.int8_inputs && (dnx::matmul_uses_f6(true, rows, cols, n) ||
-                                         dnx::matmul_uses_f6_chunk(true, n))
+  // The panel quantizer reads x 16 bytes at a time: an x at a 4-byte offset
+  // that is not 16-byte aligned takes the route without the prepack.
+  const bool x16 = ((uintptr_t)dev_at(x, xOff) & 15) == 0;
+  Prepack* pp = q4 && c.int8_inputs && x16 &&
+                        (dnx::matmul_uses_f6(true, rows, cols, n) ||
+                         dnx::matmul_uses_f6_chunk(true, rows, cols, n))
                     ? find_prepack(w, qsOff, scOff, rows, cols)
                     : nullptr;
   if (pp != nullptr) {
@@ -1544,7 +1549,8 @@ static void enc_matmul(Op op, int64_t w, int64_t qsOffset, int64_t scalesOffset,
     return;
   }
   if (q4 && gInt8Inputs &&
-      (dnx::matmul_uses_f6(true, rows, cols, n) || dnx::matmul_uses_f6_chunk(true, n))) {
+      (dnx::matmul_uses_f6(true, rows, cols, n) ||
+       dnx::matmul_uses_f6_chunk(true, rows, cols, n))) {
     reserve_prepack(w, qsOffset, scalesOffset, rows, cols);
   }
   record(op, {w, qsOffset, scalesOffset, x, xOffset, y, yOffset, rows, cols, n});

@@ -27,11 +27,19 @@ inline bool matmul_uses_f6(bool q4, int64_t rows, int64_t cols, int64_t n) {
   return q4 && n >= 320 && rows >= 4096 && cols <= 4096;
 }
 
-// A prefill chunk (5..64 tokens; the reference prefills in chunks of up to
-// 64, lib/src/model.dart:91) of a Q4 matrix: with a prepacked copy of the
+// A prefill chunk (the reference prefills in chunks of up to 64 tokens,
+// lib/src/model.dart:91) or another batch of up to 512 tokens of a Q4
+// matrix that the tiled fp6 route above does not take (the audio encoder's
+// 375 frames, the callers' 128 and 256): with a prepacked copy of the
 // weights (the lab_gpu_* command buffer keeps one per weight region) it runs
 // as the f6 panel quantizer + dnx_gemm_q4_f6s, one launch over the whole K.
-inline bool matmul_uses_f6_chunk(bool q4, int64_t n) { return q4 && n >= 5 && n <= 64; }
+// Measured against quantize + int8 GEMM (graph-timed): 6144 x 2048 at 8..64
+// tokens 7.5-9.4 against 11.0-15.1 us, at 128 / 256 tokens 14.7 / 20.7
+// against 18.1 / 23.0; the audio shapes at 375 tokens 8.1-16.4 against
+// 11.7-19.2.
+inline bool matmul_uses_f6_chunk(bool q4, int64_t rows, int64_t cols, int64_t n) {
+  return q4 && n >= 5 && n <= 512 && !matmul_uses_f6(q4, rows, cols, n);
+}
 
 // Device bytes a route needs for its quantized activations: int8 xq and fp32
 // block scales (each 256-byte aligned), or the fp6 activation panel.
@@ -75,7 +83,10 @@ int matmul_route(bool q4, const void* qs, const void* scales, const float* x, fl
   }
   const int64_t need = matmul_workspace_bytes(cols, n);
   if (need < 0 || workspace == nullptr || workspace_bytes < need) return DNX_EINVAL;
-  if (matmul_uses_f6(q4, rows, cols, n)) {
+  // The fp6 panel quantizer reads x 16 bytes at a time; an x that is only
+  // 4-byte aligned (a float offset into a caller's buffer) takes the int8
+  // route below, which reads it a float at a time where it must.
+  if (matmul_uses_f6(q4, rows, cols, n) && ((uintptr_t)x & 15) == 0) {
     rc = dnx_quantize_q8_f6panel(x, workspace, n, cols, s);
     if (rc != DNX_OK) return rc;
     after(MatmulStep::kQuantizeF6);

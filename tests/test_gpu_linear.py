@@ -357,3 +357,31 @@ def test_input_mode_switch_returns_previous(gpu_ready):
         assert set_int8_inputs(True) is True
     finally:
         set_int8_inputs(was)
+
+
+@pytest.mark.parametrize("rows,cols,n", [(768, 768, 13), (768, 768, 375), (4096, 1024, 320)])
+def test_q4_prefill_with_x_at_any_float_offset(gpu, orc, rows, cols, n):
+    """The Q4 prefill routes with fp6 kernels (the chunk GEMM on the prepack
+    for 5..512 tokens, the tiled fp6 GEMM for 320+ tokens on 4096+ rows)
+    read x 16 bytes at a time; lab_gpu_enc_matmul_q4 takes x at any float
+    offset. At offsets 1..3 floats the command takes the int8 route, at 0
+    and 4 the fp6 route: all within the bar of the CPU kernel."""
+    rng = np.random.default_rng(rows + n)
+    qs, sc = synth.q4_weights(rng, rows, cols)
+    xs = synth.activations(rng, n, cols)
+    gpu.upload("w", QuantMatrix.q4(qs, sc))
+    lib, w = gpu._lib, gpu._matrix("w")
+    x = gpu._aux_buffer("x_off", n * cols + 4)
+    y = gpu._aux_buffer("y_off", n * rows)
+    ref = orc.gemm_q4(qs, sc, xs, n, threads=8, mode=1)
+    for off in (1, 2, 3, 0, 4):
+        v = x.view(count=n * cols + 4)
+        v[:] = np.nan
+        v[off:off + n * cols] = xs.reshape(-1)
+        y.view(count=n * rows)[:] = np.nan
+        lib.lab_gpu_begin()
+        w.encode(lib, x.handle, y.handle, 0, n, x_offset=off * 4)
+        gpu._finish()
+        out = y.view(count=n * rows).reshape(n, rows).copy()
+        ok, rel, ab = within_tolerance(out, ref)
+        assert ok, (off, rel, ab)
