@@ -889,11 +889,12 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
   store_tile_sums<SN>(lds, acc, wave, lane, tm * kTileM * kTokens, n0, M, N, out, p.vec != 0);
 }
 
-// ------------------------------------------- skinny prefill (5..64 tokens)
+// ------------------------------------------- skinny prefill (5..512 tokens)
 //
-// A prefill chunk of at most 64 tokens (the reference prefills in chunks of
-// up to 64, lib/src/model.dart:91) against a whole weight matrix: the
-// weights dominate the bytes, the MFMA work is small. One workgroup owns 32
+// A prefill chunk (the reference prefills in chunks of up to 64 tokens,
+// lib/src/model.dart:91) or another batch of a few hundred tokens against a
+// whole weight matrix: the weights dominate the bytes, the MFMA work is
+// small. One workgroup owns 32
 // weight rows and 64 tokens (G groups of 32; more tokens take more
 // workgroups along y, which read the same weights) over the whole K, so no
 // K split, no partials and no reduce launch: its 8 waves take blocks b = w,
@@ -937,12 +938,15 @@ __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
     const int wb = ((rg * B + b) * kChunk & ok) | (~ok & -(1 << 30));
     sl.w0 = dnx_raw_buffer_load_v4i32(rpk, wb + (lane & 31) * 16, 0, 0);
     sl.w1 = dnx_raw_buffer_load_v4i32(rpk, wb + kChunk / 2 + (lane & 31) * 16, 0, 0);
+    // A lane whose token lies past n (a chunk of 8 tokens fills a quarter of
+    // its 32-token group) reads zeros without a memory access.
 #pragma unroll
     for (int t = 0; t < G; t++) {
-      const int tok = -(int)(t0 + t < groups);
-      const int ab = ((((t0 + t) * B + b) * kRec + kRecF) & ok & tok) | (~(ok & tok) & -(1 << 30));
-      sl.lo[t] = dnx_raw_buffer_load_v4i32(rpanel, ab + lane * 16, 0, 0);
-      sl.hi[t] = dnx_raw_buffer_load_v4i32(rpanel, ab + kRecHalf + lane * 16, 0, 0);
+      const int tok = -(int)((t0 + t) * kTokens + (lane & 31) < M);
+      const int ab = ((((t0 + t) * B + b) * kRec + kRecF + lane * 16) & ok & tok) |
+                     (~(ok & tok) & -(1 << 30));
+      sl.lo[t] = dnx_raw_buffer_load_v4i32(rpanel, ab, 0, 0);
+      sl.hi[t] = dnx_raw_buffer_load_v4i32(rpanel, ab + kRecHalf, 0, 0);
     }
   };
 

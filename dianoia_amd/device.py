@@ -371,7 +371,7 @@ def gemm_q4_f6p(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> 
 
 
 def gemm_q4_f6s(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
-    """The prefill chunk GEMM (n <= 64) on prepacked Q4 weights."""
+    """The prefill chunk GEMM (5..512 tokens) on prepacked Q4 weights."""
     _need("gemm_q4_f6s",
           packed=(packed, q4_f6pack_bytes(rows, cols)),
           panel=(panel, f6_panel_bytes(n, cols)),

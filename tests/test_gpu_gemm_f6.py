@@ -261,7 +261,7 @@ def test_prepacked_gemm_equals_engine_layout(gpu_ready, orc, rows, cols, n):
     assert ok, (worst_rel, worst_abs)
 
 
-# ------------------------------------------- the prefill chunk GEMM (n <= 64)
+# ------------------------------------------- the prefill chunk GEMM (5..512 tokens)
 
 def gemm_f6s(qs, sc, xq, xsc, rows, cols, n):
     panel = torch.full((D.f6_panel_bytes(n, cols),), 0x7f, dtype=torch.uint8, device="cuda")
