@@ -421,20 +421,29 @@ def test_replaced_segv_handler_turns_tracking_off(gpu_ready):
     assert same(out["logits16"], want)
 
 
-def test_long_context_decode_folds_head_norms(gpu_ready):
-    """Decode steps past 64 positions take the split-key attention, where the
-    commit folds the q and k head norms into it: one command buffer per pass
-    against one per command, bit for bit (logits and KV rows), and the
+# Head sizes of the split-key attention with the head norms folded in: its
+# keys per split are 32 at hd 256, 128 at hd 64, 256 at hd 32, so each plan
+# decodes past one split.
+LONG_CONTEXT = {256: 40, 64: 160, 32: 264}
+
+
+@pytest.mark.parametrize("hd", sorted(LONG_CONTEXT))
+def test_long_context_decode_folds_head_norms(gpu_ready, hd):
+    """Decode steps past one key split take the split-key attention, where
+    the commit folds the q and k head norms into it: one command buffer per
+    pass against one per command, bit for bit (logits and KV rows), and the
     folded step dispatches no standalone head norm (the profile counts the
-    folded norms under their kind with no time)."""
+    folded norms under their kind with no time). Head sizes 256 and 32 run
+    the fold's generic lane layout, 64 its 16-lane one."""
     import ctypes
     from dianoia_amd import _lib
     lib = _lib.load()
-    cfg = qwen3_small()
-    # hd 64 splits the keys in runs of 128: decode at 160 and 161
-    plan = [(8, p) for p in range(0, 160, 8)] + [(1, 160), (1, 161)]
-    fused = F.GpuForward(cfg, max_seq=192, max_chunk=8, seed=5)
-    split = F.GpuForward(cfg, max_seq=192, max_chunk=8, seed=5)
+    cfg = F.ForwardConfig(hidden=256, intermediate=512, heads=4, kv_heads=2, head_dim=hd,
+                          vocab=997, layer_types=[F.FULL, F.FULL], eps=1e-6)
+    start = LONG_CONTEXT[hd]
+    plan = [(8, p) for p in range(0, start, 8)] + [(1, start), (1, start + 1)]
+    fused = F.GpuForward(cfg, max_seq=start + 32, max_chunk=8, seed=5)
+    split = F.GpuForward(cfg, max_seq=start + 32, max_chunk=8, seed=5)
     split.split_commits = True
     try:
         a = run(fused, plan[:-1])
