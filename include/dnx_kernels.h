@@ -365,7 +365,8 @@ int dnx_argmax(const float* v, int64_t n, int64_t* out, void* workspace, dnx_str
 int dnx_swiglu(float* g, const float* u, int64_t count, dnx_stream_t stream);
 
 // Exact-erf GELU in place with the Abramowitz-Stegun erf in double
-// (lib/src/vision_encoder.dart:260-263, :496-509).
+// (lib/src/vision_encoder.dart:260-263, :496-509). x 4-byte aligned; any
+// count and offset.
 int dnx_gelu(float* x, int64_t count, dnx_stream_t stream);
 
 // The decoder's other layer steps (the lab_gpu_enc_* encoders of
