@@ -345,8 +345,14 @@ void use_as_weights(int64_t h) {
   b.weights = true;
 }
 
+void stale_prepacks(int64_t h, int64_t offset, int64_t bytes);
+
+// A command wrote [offset, offset + bytes) of h: recorded for the copy-back
+// and the upload gaps; a prepacked copy of weights it overwrote is re-made
+// at its next use.
 void wrote_region(int64_t h, int64_t offset, int64_t bytes) {
   gWritten.push_back({h, offset, bytes});
+  stale_prepacks(h, offset, bytes);
 }
 
 void after_dispatch(int kind) {
@@ -412,13 +418,15 @@ void record(Op op, std::initializer_list<int64_t> args) {
 
 // Prepacked copies of Q4 weight matrices for the fp6 GEMMs (the routes of
 // prefill chunks, dnx::matmul_uses_f6_chunk, and of large prefill shapes,
-// dnx::matmul_uses_f6). Weights are immutable once used (use_as_weights), so
-// a matrix region is re-encoded once, on its first such matmul, into the
-// GEMMs' tile-major layout (dnx_pack_q4_f6), and every later prefill of it
-// runs on the prepack. The copy's memory is
-// reserved when the command is encoded (no allocation inside a commit); it
-// is freed with the buffer. Not a live buffer: lab_gpu_live_buffers does not
-// count it.
+// dnx::matmul_uses_f6). The host cannot change weights once used
+// (use_as_weights), so a matrix region is re-encoded on its first such
+// matmul into the GEMMs' tile-major layout (dnx_pack_q4_f6), and later
+// prefills of it run on the prepack. A command that writes into the region
+// (a load-time quantizer, a copy, a GGUF split run again into the same
+// buffer) marks the prepack stale, and the next matmul re-makes it. The
+// copy's memory is reserved when the command is encoded (no allocation
+// inside a commit); it is freed with the buffer. Not a live buffer:
+// lab_gpu_live_buffers does not count it.
 struct Prepack {
   int64_t handle, qs_off, sc_off, rows, cols;
   void* dev;
@@ -445,6 +453,18 @@ void reserve_prepack(int64_t h, int64_t qs_off, int64_t sc_off, int64_t rows, in
   void* dev = nullptr;
   if (bytes <= 0 || bytes >= (1ll << 31) || hipMalloc(&dev, (size_t)bytes) != hipSuccess) return;
   gPrepacks.push_back({h, qs_off, sc_off, rows, cols, dev, false});
+}
+
+void stale_prepacks(int64_t h, int64_t offset, int64_t bytes) {
+  for (Prepack& p : gPrepacks) {
+    if (p.handle != h || !p.packed) continue;
+    const int64_t qs_end = p.qs_off + p.rows * (p.cols / 2);
+    const int64_t sc_end = p.sc_off + p.rows * (p.cols / 32) * 2;
+    const int64_t end = offset + bytes;
+    if ((offset < qs_end && p.qs_off < end) || (offset < sc_end && p.sc_off < end)) {
+      p.packed = false;
+    }
+  }
 }
 
 void free_prepacks(int64_t h) {

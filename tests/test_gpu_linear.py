@@ -385,3 +385,33 @@ def test_q4_prefill_with_x_at_any_float_offset(gpu, orc, rows, cols, n):
         out = y.view(count=n * rows).reshape(n, rows).copy()
         ok, rel, ab = within_tolerance(out, ref)
         assert ok, (off, rel, ab)
+
+
+@pytest.mark.parametrize("n", [13, 320])
+def test_q4_prefill_follows_gpu_writes_into_the_weights(gpu, orc, n):
+    """The Q4 prefill routes run on a prepacked copy of the weights made at
+    their first use (13 tokens: the chunk GEMM; 320 on 4096 rows: the tiled
+    fp6 GEMM). A GPU command that writes other weights into the same region
+    (lab_gpu_enc_quantize_q4 again, from other fp32 values) makes the next
+    prefill use them, and writing the first weights back returns to those:
+    each product against the CPU kernel on the weights of the moment."""
+    rows, cols = 4096, 1024
+    rng = np.random.default_rng(17 + n)
+    ws = [(rng.standard_normal((rows, cols)) * 0.02).astype(np.float32) for _ in range(2)]
+    gpu.upload_f32("w", ws[0], rows, cols, fmt="q4")
+    lib, m = gpu._lib, gpu._matrix("w")
+    src = gpu._aux_buffer("w_src", rows * cols)
+    xs = synth.activations(rng, n, cols)
+    for step, k in enumerate((0, 1, 0)):
+        if step > 0:   # weights k into the same region, on the GPU
+            src.view(count=rows * cols)[:] = ws[k].reshape(-1)
+            lib.lab_gpu_begin()
+            lib.lab_gpu_enc_quantize_q4(src.handle, 0, m.buffer, m.qs, m.buffer, m.scales,
+                                        rows, cols)
+            gpu._finish()
+        y = np.zeros(n * rows, np.float32)
+        gpu.apply("w", xs, y, n)
+        qs, sc = orc.quantize_q4(ws[k])
+        ok, rel, ab = within_tolerance(y.reshape(n, rows), orc.gemm_q4(qs, sc, xs, n, threads=8,
+                                                                         mode=1))
+        assert ok, (k, rel, ab)
