@@ -284,7 +284,10 @@ int dnx_gemm_q4_f6p(const void* packed, const void* panel, float* y, int64_t row
 // written once by dnx_pack_q8_f6). Two dot MFMAs per block, chained exactly;
 // the same activation panel as the Q4 GEMMs (dnx_quantize_q8_f6panel).
 // Exact block dots (int8 weights including -128), fp32 within 1e-4 relative
-// (1e-5 absolute near zero) of the CPU kernel.
+// (1e-5 absolute near zero) of the CPU kernel, for finite weight scales
+// (an infinite or NaN scale has no E8M0 + mantissa form; the int8 GEMM,
+// dnx_gemm_q8, propagates them as the CPU does). Not the matmul route's
+// choice for Q8: measured slower than the int8 GEMM at the vision shapes.
 int64_t dnx_q8_f6pack_bytes(int64_t rows, int64_t cols);
 int dnx_pack_q8_f6(const int8_t* qs, const float* scales, void* packed, int64_t rows,
                    int64_t cols, dnx_stream_t stream);
