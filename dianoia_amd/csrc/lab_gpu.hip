@@ -135,6 +135,18 @@ int64_t gUpBytes = 0, gDownBytes = 0;
 // Quantized-activation workspace of the GEMM routes, and argmax partials.
 void* gWs = nullptr;
 int64_t gWsBytes = 0;
+
+// The activation panel the prepacked route last made in the matmul
+// workspace, and from which x: the next prepacked matmul of the same x in
+// the command buffer (a prefill chunk's q, k and v projections, or its gate
+// and up, all read one normed x) runs on it without quantizing again. It is
+// forgotten when a command writes that x, when another route uses the
+// workspace, when the workspace is re-made, and at every commit (the host
+// may have written x since).
+struct PanelKey {
+  int64_t handle = -1, offset = 0, n = 0, cols = 0;
+};
+PanelKey gPanel;
 void* gArgmaxWs = nullptr;
 void* gGemvArgmaxWs = nullptr;  // zeroed once; each fused argmax leaves it zero
 
@@ -346,13 +358,15 @@ void use_as_weights(int64_t h) {
 }
 
 void stale_prepacks(int64_t h, int64_t offset, int64_t bytes);
+void stale_panel(int64_t h, int64_t offset, int64_t bytes);
 
 // A command wrote [offset, offset + bytes) of h: recorded for the copy-back
 // and the upload gaps; a prepacked copy of weights it overwrote is re-made
-// at its next use.
+// at its next use, and an activation panel made from it is not reused.
 void wrote_region(int64_t h, int64_t offset, int64_t bytes) {
   gWritten.push_back({h, offset, bytes});
   stale_prepacks(h, offset, bytes);
+  stale_panel(h, offset, bytes);
 }
 
 void after_dispatch(int kind) {
@@ -378,6 +392,7 @@ bool grow_scratch(int64_t cols, int64_t n) {
   if (need < 0) return false;
   if (need <= gWsBytes) return true;
   const int64_t cap = need > (4 << 20) ? need : (4 << 20);
+  gPanel = PanelKey{};
   if (gWs) (void)hipFree(gWs);
   gWs = nullptr;
   gWsBytes = 0;
@@ -467,6 +482,13 @@ void stale_prepacks(int64_t h, int64_t offset, int64_t bytes) {
   }
 }
 
+void stale_panel(int64_t h, int64_t offset, int64_t bytes) {
+  if (h == gPanel.handle && offset < gPanel.offset + gPanel.n * gPanel.cols * 4 &&
+      gPanel.offset < offset + bytes) {
+    gPanel = PanelKey{};
+  }
+}
+
 void free_prepacks(int64_t h) {
   for (size_t i = 0; i < gPrepacks.size();) {
     if (gPrepacks[i].handle == h) {
@@ -483,8 +505,8 @@ void free_prepacks(int64_t h) {
 // panel from fp32 x, the GEMM: the chunk GEMM (one launch over the whole K)
 // where matmul_uses_f6_chunk takes the shape, else the tiled GEMM (the same
 // products as the engine-layout fp6 GEMM, bit for bit).
-int run_matmul_prepacked(Prepack& pp, int64_t w, int64_t qsOff, int64_t scOff, const float* x,
-                         float* y, int64_t rows, int64_t cols, int64_t n) {
+int run_matmul_prepacked(Prepack& pp, int64_t w, int64_t qsOff, int64_t scOff, int64_t xh,
+                         int64_t xOff, float* y, int64_t rows, int64_t cols, int64_t n) {
   auto s = (dnx_stream_t)gStream;
   int rc;
   if (!pp.packed) {
@@ -494,9 +516,13 @@ int run_matmul_prepacked(Prepack& pp, int64_t w, int64_t qsOff, int64_t scOff, c
     after_dispatch(kKindQuantizeWeights);
     pp.packed = true;
   }
-  rc = dnx_quantize_q8_f6panel(x, gWs, n, cols, s);
-  if (rc != DNX_OK) return rc;
-  after_dispatch(kKindQuantize);
+  if (!(gPanel.handle == xh && gPanel.offset == xOff && gPanel.n == n && gPanel.cols == cols)) {
+    gPanel = PanelKey{};
+    rc = dnx_quantize_q8_f6panel((const float*)dev_at(xh, xOff), gWs, n, cols, s);
+    if (rc != DNX_OK) return rc;
+    after_dispatch(kKindQuantize);
+    gPanel = PanelKey{xh, xOff, n, cols};
+  }
   rc = dnx::matmul_uses_f6_chunk(true, rows, cols, n)
            ? dnx_gemm_q4_f6s(pp.dev, gWs, y, rows, cols, n, s)
            : dnx_gemm_q4_f6p(pp.dev, gWs, y, rows, cols, n, s);
@@ -521,8 +547,8 @@ bool run_matmul(const Cmd& c, bool q4) {
                     ? find_prepack(w, qsOff, scOff, rows, cols)
                     : nullptr;
   if (pp != nullptr) {
-    const int rc = run_matmul_prepacked(*pp, w, qsOff, scOff, (const float*)dev_at(x, xOff),
-                                        (float*)dev_at(y, yOff), rows, cols, n);
+    const int rc = run_matmul_prepacked(*pp, w, qsOff, scOff, x, xOff, (float*)dev_at(y, yOff),
+                                        rows, cols, n);
     wrote_region(y, yOff, n * rows * 4);
     if (rc != DNX_OK) {
       LOG("matmul q4 %ldx%ld n=%ld (prepacked fp6) failed (%d)\n", (long)rows, (long)cols,
@@ -530,6 +556,7 @@ bool run_matmul(const Cmd& c, bool q4) {
     }
     return rc == DNX_OK;
   }
+  gPanel = PanelKey{};  // the route may write the workspace
   const int rc = dnx::matmul_route(
       q4, dev_at(w, qsOff), dev_at(w, scOff), (const float*)dev_at(x, xOff),
       (float*)dev_at(y, yOff), rows, cols, n, c.int8_inputs, gWs, gWsBytes, gStream,
@@ -1397,6 +1424,7 @@ int64_t lab_gpu_commit(int64_t wait) {
   if (!gReady) return 0;
   check_handler();
   gWritten.clear();
+  gPanel = PanelKey{};
   gProfiled = 0;
   bool ok = !gFailed;
   (void)hipEventRecord(gStart, gStream);

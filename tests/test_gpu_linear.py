@@ -415,3 +415,61 @@ def test_q4_prefill_follows_gpu_writes_into_the_weights(gpu, orc, n):
         ok, rel, ab = within_tolerance(y.reshape(n, rows), orc.gemm_q4(qs, sc, xs, n, threads=8,
                                                                          mode=1))
         assert ok, (k, rel, ab)
+
+
+def test_q4_prefill_matmuls_of_one_x_share_its_panel(gpu, orc):
+    """Prepacked Q4 prefill matmuls that read the same x in one command
+    buffer (a chunk's q, k, v or gate, up) quantize x once and share the
+    panel. A command that writes x in between (a copy into it) makes the
+    next matmul quantize the new x, and so does a host write between
+    commits: every product against the CPU kernel on the x of its moment,
+    and the profile counts one activation quantize per distinct x."""
+    import ctypes
+    rng = np.random.default_rng(41)
+    n, cols = 13, 1024
+    shapes = {"a": 768, "b": 1536, "c": 512}
+    mats = {}
+    for name, rows in shapes.items():
+        qs, sc = synth.q4_weights(rng, rows, cols)
+        gpu.upload(name, QuantMatrix.q4(qs, sc))
+        mats[name] = (qs, sc)
+    lib = gpu._lib
+    x = gpu._aux_buffer("x_share", n * cols)
+    x2 = gpu._aux_buffer("x_other", n * cols)
+    ys = {name: gpu._aux_buffer("y_" + name, n * rows) for name, rows in shapes.items()}
+    xa = synth.activations(rng, n, cols)
+    xb = synth.activations(rng, n, cols)
+
+    def check(name, xs):
+        rows = shapes[name]
+        qs, sc = mats[name]
+        out = ys[name].view(count=n * rows).reshape(n, rows)
+        ok, rel, ab = within_tolerance(out, orc.gemm_q4(qs, sc, xs, n, threads=8, mode=1))
+        assert ok, (name, rel, ab)
+
+    ms = (ctypes.c_double * 21)()
+    counts = (ctypes.c_int64 * 21)()
+    quantize = 10
+    for rep in range(2):   # the first pass also makes the prepacks
+        x.view(count=n * cols)[:] = xa.reshape(-1)
+        x2.view(count=n * cols)[:] = xb.reshape(-1)
+        lib.lab_gpu_profile(ms, counts, 21)
+        lib.lab_gpu_set_profiling(1)
+        lib.lab_gpu_begin()
+        gpu._matrix("a").encode(lib, x.handle, ys["a"].handle, 0, n)
+        gpu._matrix("b").encode(lib, x.handle, ys["b"].handle, 0, n)
+        lib.lab_gpu_enc_copy(x2.handle, 0, x.handle, 0, n * cols)
+        gpu._matrix("c").encode(lib, x.handle, ys["c"].handle, 0, n)
+        gpu._finish()
+        lib.lab_gpu_set_profiling(0)
+        lib.lab_gpu_profile(ms, counts, 21)
+        check("a", xa)
+        check("b", xa)
+        check("c", xb)
+        assert counts[quantize] == 2, list(counts)
+    # A host write between commits: the panel is made again.
+    x.view(count=n * cols)[:] = xa.reshape(-1)
+    lib.lab_gpu_begin()
+    gpu._matrix("c").encode(lib, x.handle, ys["c"].handle, 0, n)
+    gpu._finish()
+    check("c", xa)
