@@ -777,6 +777,39 @@ def bench_decode_step(steps=20, position=4095, child=False):
     return out
 
 
+def bench_prefill_chunk(reps=10, n=64, position=256):
+    """Prefill chunks of the same Qwen3-1.7B-shaped decoder through the
+    lab_gpu_* ABI: `n` tokens per forward pass (the reference prefills in
+    chunks of up to 64, lib/src/model.dart:91) after `position` tokens of
+    history; the command buffer's GPU time per chunk (lab_gpu_last_ms,
+    median over `reps` chunks at growing positions), and tokens per second.
+    The chunk's matmuls take the prepacked fp6 chunk GEMM, the q/k/v and
+    gate/up matmuls of one x sharing its activation panel; attention is the
+    matrix-core prefill kernel."""
+    from dianoia_amd import forward as F
+    cfg = F.qwen3_1_7b()
+    fwd = F.GpuForward(cfg, max_seq=position + n * (reps + 2), max_chunk=n, seed=11)
+    rng = np.random.default_rng(13)
+    try:
+        emb = (rng.standard_normal(n * cfg.hidden) * 0.5).astype(np.float32)
+        for k in range(2):   # first uses: the weights' prepacks
+            fwd.residual[:n * cfg.hidden] = emb
+            fwd.forward(n, k * n)
+        gpu, wall = [], []
+        for k in range(reps):
+            fwd.residual[:n * cfg.hidden] = emb
+            t0 = time.perf_counter()
+            fwd.forward(n, position + k * n)
+            wall.append(time.perf_counter() - t0)
+            gpu.append(fwd.last_ms())
+    finally:
+        fwd.dispose()
+    g = float(np.median(gpu))
+    return {"model": "Qwen3-1.7B-shaped (as decode_step_abi)", "tokens_per_chunk": n,
+            "first_position": position, "chunks": reps, "gpu_ms": g,
+            "wall_ms": float(np.median(wall)) * 1e3, "tokens_per_s_gpu": n / g * 1e3}
+
+
 # ------------------------------------------------------------------ CPU
 
 def cpu_baseline(runs):
@@ -1200,6 +1233,7 @@ def main():
                          ("load_time_converters", lambda: bench_loaders(torch, D, timer, args.steps)),
                          ("layer_steps", lambda: bench_layers(torch, D, timer, args.steps)),
                          ("decode_step_abi", bench_decode_step),
+                         ("prefill_chunk_abi", bench_prefill_chunk),
                          ("weight_cache_wrap", bench_cache_wrap)):
             if only is not None and name not in only:
                 continue
