@@ -905,11 +905,19 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
 
 constexpr int kSkRing = 4;      // blocks in flight per wave
 
+// Up to kMaxSegs matrices over the same x in one launch (a prefill chunk's
+// q, k and v, or gate and up): their 32-row groups laid end to end along
+// grid x, seg_end holding the cumulative group ends.
+constexpr int kMaxSegs = 4;
+
 struct F6SParams {
-  const uint8_t* packed;   // tile-major prepack
   const uint8_t* panel;    // f6 panel of the n tokens
-  float* y;                // [n][rows]
-  int rows, cols, n;
+  int cols, n;
+  int segs;
+  int seg_end[kMaxSegs];
+  const uint8_t* packed[kMaxSegs];   // tile-major prepacks
+  float* y[kMaxSegs];                // [n][rows]
+  int rows[kMaxSegs];
 };
 
 template <int G>
@@ -918,13 +926,19 @@ __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
   __shared__ __align__(16) float red[kWaves * kOut];   // each wave's sums, [wave][token][row]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int K = p.cols, B = K / kBlock, M = p.n, N = p.rows;
-  const int rg = blockIdx.x;                           // 32-row group
+  // This workgroup's matrix (uniform: scalar selects over the segments).
+  int seg = 0;
+#pragma unroll
+  for (int k = 1; k < kMaxSegs; k++) seg += (k < p.segs && (int)blockIdx.x >= p.seg_end[k - 1]);
+  const int K = p.cols, B = K / kBlock, M = p.n;
+  const int N = p.rows[seg];
+  float* const yout = p.y[seg];
+  const int rg = blockIdx.x - (seg > 0 ? p.seg_end[seg - 1] : 0);   // 32-row group
   const int t0 = blockIdx.y * G;                       // first token group
   const int groups = (M + kTokens - 1) / kTokens;
   const int groups_n = (N + 31) >> 5;
   const i32x4 rpanel = buffer_rsrc(p.panel, (uint32_t)((size_t)groups * B * kRec));
-  const i32x4 rpk = buffer_rsrc(p.packed, (uint32_t)((size_t)groups_n * B * kChunk));
+  const i32x4 rpk = buffer_rsrc(p.packed[seg], (uint32_t)((size_t)groups_n * B * kChunk));
 
   // Block i of this wave is b = wave + 8 i; blocks past K read zeros (offset
   // past the resources), so their products vanish.
@@ -1004,7 +1018,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
     }
     const int r = rg * 32 + c, mt = t0 * kTokens + m;
     if (mt >= M || r >= N) continue;
-    float* dst = p.y + (size_t)mt * N + r;
+    float* dst = yout + (size_t)mt * N + r;
     if (r + 3 < N && ((uintptr_t)dst & 15) == 0) {
       store_wt4(dst, o);
     } else {
@@ -1274,22 +1288,38 @@ int dnx_gemm_q4_f6p(const void* packed, const void* panel, float* y, int64_t row
 
 int dnx_gemm_q4_f6s(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
                     int64_t n, dnx_stream_t stream) {
-  if (!f6p_shape_ok(rows, cols, n) || n > 65535 * 2 * kTokens || ((uintptr_t)panel & 15) ||
-      ((uintptr_t)packed & 15) || ((uintptr_t)y & 3)) {
+  return dnx_gemm_q4_f6s_multi(&packed, &y, &rows, 1, panel, cols, n, stream);
+}
+
+int dnx_gemm_q4_f6s_multi(const void* const* packed, float* const* y, const int64_t* rows,
+                          int count, const void* panel, int64_t cols, int64_t n,
+                          dnx_stream_t stream) {
+  if (count < 1 || count > kMaxSegs || n > 65535 * 2 * kTokens || ((uintptr_t)panel & 15)) {
     return DNX_EINVAL;
   }
   F6SParams p{};
-  p.packed = (const uint8_t*)packed;
   p.panel = (const uint8_t*)panel;
-  p.y = y;
-  p.rows = (int)rows;
   p.cols = (int)cols;
   p.n = (int)n;
+  p.segs = count;
+  int64_t groups = 0;
+  for (int k = 0; k < count; k++) {
+    if (!f6p_shape_ok(rows[k], cols, n) || ((uintptr_t)packed[k] & 15) ||
+        ((uintptr_t)y[k] & 3)) {
+      return DNX_EINVAL;
+    }
+    groups += (rows[k] + 31) / 32;
+    if (groups > 0x7fffffff) return DNX_EINVAL;
+    p.seg_end[k] = (int)groups;
+    p.packed[k] = (const uint8_t*)packed[k];
+    p.y[k] = y[k];
+    p.rows[k] = (int)rows[k];
+  }
   // 33+ tokens: two token groups per workgroup (one weight read for both:
   // 64 tokens of 6144 x 2048 in 6.5 us against 7.9 with a workgroup per 32).
   const bool two = n > kTokens;
   const int per = two ? 2 * kTokens : kTokens;
-  const dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((n + per - 1) / per));
+  const dim3 grid((unsigned)groups, (unsigned)((n + per - 1) / per));
   if (two) {
     hipLaunchKernelGGL(gemm_f6s_kernel<2>, grid, dim3(kThreads), 0, (hipStream_t)stream, p);
   } else {

@@ -442,6 +442,8 @@ void record(Op op, std::initializer_list<int64_t> args) {
 // copy's memory is reserved when the command is encoded (no allocation
 // inside a commit); it is freed with the buffer. Not a live buffer:
 // lab_gpu_live_buffers does not count it.
+constexpr size_t kMaxChunkSegs = 4;   // matrices per dnx_gemm_q4_f6s_multi launch
+
 struct Prepack {
   int64_t handle, qs_off, sc_off, rows, cols;
   void* dev;
@@ -505,24 +507,40 @@ void free_prepacks(int64_t h) {
 // panel from fp32 x, the GEMM: the chunk GEMM (one launch over the whole K)
 // where matmul_uses_f6_chunk takes the shape, else the tiled GEMM (the same
 // products as the engine-layout fp6 GEMM, bit for bit).
+// The prepack of a matrix made if it is not (first use, or stale).
+int ensure_packed(Prepack& pp, int64_t w, int64_t qsOff, int64_t scOff, int64_t rows,
+                  int64_t cols) {
+  if (pp.packed) return DNX_OK;
+  const int rc = dnx_pack_q4_f6((const uint8_t*)dev_at(w, qsOff),
+                                (const uint16_t*)dev_at(w, scOff), pp.dev, rows, cols,
+                                (dnx_stream_t)gStream);
+  if (rc != DNX_OK) return rc;
+  after_dispatch(kKindQuantizeWeights);
+  pp.packed = true;
+  return DNX_OK;
+}
+
+// The activation panel of x in the workspace, unless it is there already.
+int ensure_panel(int64_t xh, int64_t xOff, int64_t n, int64_t cols) {
+  if (gPanel.handle == xh && gPanel.offset == xOff && gPanel.n == n && gPanel.cols == cols) {
+    return DNX_OK;
+  }
+  gPanel = PanelKey{};
+  const int rc = dnx_quantize_q8_f6panel((const float*)dev_at(xh, xOff), gWs, n, cols,
+                                         (dnx_stream_t)gStream);
+  if (rc != DNX_OK) return rc;
+  after_dispatch(kKindQuantize);
+  gPanel = PanelKey{xh, xOff, n, cols};
+  return DNX_OK;
+}
+
 int run_matmul_prepacked(Prepack& pp, int64_t w, int64_t qsOff, int64_t scOff, int64_t xh,
                          int64_t xOff, float* y, int64_t rows, int64_t cols, int64_t n) {
   auto s = (dnx_stream_t)gStream;
-  int rc;
-  if (!pp.packed) {
-    rc = dnx_pack_q4_f6((const uint8_t*)dev_at(w, qsOff), (const uint16_t*)dev_at(w, scOff),
-                        pp.dev, rows, cols, s);
-    if (rc != DNX_OK) return rc;
-    after_dispatch(kKindQuantizeWeights);
-    pp.packed = true;
-  }
-  if (!(gPanel.handle == xh && gPanel.offset == xOff && gPanel.n == n && gPanel.cols == cols)) {
-    gPanel = PanelKey{};
-    rc = dnx_quantize_q8_f6panel((const float*)dev_at(xh, xOff), gWs, n, cols, s);
-    if (rc != DNX_OK) return rc;
-    after_dispatch(kKindQuantize);
-    gPanel = PanelKey{xh, xOff, n, cols};
-  }
+  int rc = ensure_packed(pp, w, qsOff, scOff, rows, cols);
+  if (rc != DNX_OK) return rc;
+  rc = ensure_panel(xh, xOff, n, cols);
+  if (rc != DNX_OK) return rc;
   rc = dnx::matmul_uses_f6_chunk(true, rows, cols, n)
            ? dnx_gemm_q4_f6s(pp.dev, gWs, y, rows, cols, n, s)
            : dnx_gemm_q4_f6p(pp.dev, gWs, y, rows, cols, n, s);
@@ -698,6 +716,80 @@ int run_multi(const std::vector<Cmd>& cmds, size_t i, size_t len) {
   }
   for (size_t k = 0; k < len; k++) wrote_region(cmds[i + k].a[5], cmds[i + k].a[6], rows[k] * 4);
   if (rc != DNX_OK) LOG("%zu fused matmuls of width %ld failed (%d)\n", len, (long)cols, rc);
+  return rc;
+}
+
+// The prepack a recorded Q4 matmul runs on by the chunk route (int8
+// inputs, a chunk shape, x 16-byte aligned, a prepack reserved), or null.
+Prepack* chunk_prepack(const Cmd& c) {
+  if (c.op != kOpMatmulQ4 || !c.int8_inputs) return nullptr;
+  const int64_t rows = c.a[7], cols = c.a[8], n = c.a[9];
+  if (!dnx::matmul_uses_f6_chunk(true, rows, cols, n)) return nullptr;
+  if (((uintptr_t)dev_at(c.a[3], c.a[4]) & 15) != 0) return nullptr;
+  return find_prepack(c.a[0], c.a[1], c.a[2], rows, cols);
+}
+
+// Consecutive prefill matmuls of one x on the chunk route (a chunk's q, k
+// and v, or gate and up): how many (2..4) one launch runs, 0 for none. As in
+// multi_len, no output may overlap x or another output, and none may land
+// in a buffer that holds a group member's weights.
+size_t chunk_multi_len(const std::vector<Cmd>& cmds, size_t i) {
+  const Cmd& a = cmds[i];
+  if (chunk_prepack(a) == nullptr) return 0;
+  const int64_t x = a.a[3], xOff = a.a[4], cols = a.a[8], n = a.a[9];
+  size_t len = 0;
+  for (size_t j = i; j < cmds.size() && len < kMaxChunkSegs; j++, len++) {
+    const Cmd& b = cmds[j];
+    if (b.a[3] != x || b.a[4] != xOff || b.a[8] != cols || b.a[9] != n ||
+        chunk_prepack(b) == nullptr) {
+      break;
+    }
+    const int64_t yb = n * b.a[7] * 4;
+    if (overlaps(b.a[5], b.a[6], yb, x, xOff, n * cols * 4)) break;
+    bool clash = false;
+    for (size_t k = i; k < j; k++) {
+      clash = clash ||
+              overlaps(b.a[5], b.a[6], yb, cmds[k].a[5], cmds[k].a[6], n * cmds[k].a[7] * 4) ||
+              b.a[5] == cmds[k].a[0] || cmds[k].a[5] == b.a[0];
+    }
+    if (clash || b.a[5] == b.a[0]) break;
+  }
+  return len >= 2 ? len : 0;
+}
+
+// DNX_OK, or the launcher's code; DNX_EINVAL means the GEMM was not
+// launched (the caller then runs the matmuls one by one, which reuse the
+// prepacks and the panel made here).
+int run_chunk_multi(const std::vector<Cmd>& cmds, size_t i, size_t len) {
+  const Cmd& a = cmds[i];
+  const int64_t x = a.a[3], xOff = a.a[4], cols = a.a[8], n = a.a[9];
+  const void* packed[kMaxChunkSegs];
+  float* ys[kMaxChunkSegs];
+  int64_t rows[kMaxChunkSegs];
+  int rc = DNX_OK;
+  for (size_t k = 0; k < len && rc == DNX_OK; k++) {
+    const Cmd& c = cmds[i + k];
+    use_as_weights(c.a[0]);
+    Prepack* pp = chunk_prepack(c);
+    rc = ensure_packed(*pp, c.a[0], c.a[1], c.a[2], c.a[7], cols);
+    packed[k] = pp->dev;
+    ys[k] = (float*)dev_at(c.a[5], c.a[6]);
+    rows[k] = c.a[7];
+  }
+  if (rc != DNX_OK) return rc;
+  read_region(x, xOff, n * cols * 4);
+  rc = ensure_panel(x, xOff, n, cols);
+  if (rc != DNX_OK) return rc;
+  rc = dnx_gemm_q4_f6s_multi(packed, ys, rows, (int)len, gWs, cols, n, (dnx_stream_t)gStream);
+  if (rc == DNX_EINVAL) return rc;
+  if (rc == DNX_OK) {
+    after_dispatch(kKindGemmQ4I8);
+    also_ran(kKindGemmQ4I8, (int)len - 1);
+  }
+  for (size_t k = 0; k < len; k++) {
+    wrote_region(cmds[i + k].a[5], cmds[i + k].a[6], n * rows[k] * 4);
+  }
+  if (rc != DNX_OK) LOG("%zu prefill matmuls of width %ld failed (%d)\n", len, (long)cols, rc);
   return rc;
 }
 
@@ -1497,6 +1589,14 @@ int64_t lab_gpu_commit(int64_t wait) {
       i += 1;
     } else if (const size_t len = fusable_multi(gCmds, i)) {
       const int rc = run_multi(gCmds, i, len);
+      if (rc == DNX_EINVAL) {  // not launched: the matmuls as recorded
+        for (size_t k = 0; k < len; k++) ok = run(gCmds[i + k]) && ok;
+      } else {
+        ok = rc == DNX_OK && ok;
+      }
+      i += len - 1;
+    } else if (const size_t len = chunk_multi_len(gCmds, i)) {
+      const int rc = run_chunk_multi(gCmds, i, len);
       if (rc == DNX_EINVAL) {  // not launched: the matmuls as recorded
         for (size_t k = 0; k < len; k++) ok = run(gCmds[i + k]) && ok;
       } else {

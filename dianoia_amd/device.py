@@ -370,6 +370,24 @@ def gemm_q4_f6p(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> 
                                        _stream(stream)), "dnx_gemm_q4_f6p")
 
 
+def gemm_q4_f6s_multi(packs, ys, rows, panel, cols: int, n: int, stream=None) -> None:
+    """The chunk GEMM over 1..4 prepacked matrices reading one panel, in one
+    launch (each output bit-identical to its own gemm_q4_f6s)."""
+    import ctypes
+    k = len(packs)
+    if not (len(ys) == k == len(rows)):
+        raise ValueError("gemm_q4_f6s_multi: one output and one row count per matrix")
+    _need("gemm_q4_f6s_multi", panel=(panel, f6_panel_bytes(n, cols)))
+    for j in range(k):
+        _need("gemm_q4_f6s_multi", packed=(packs[j], q4_f6pack_bytes(rows[j], cols)),
+              y=(ys[j], n * rows[j] * 4))
+    pp = (ctypes.c_void_p * k)(*[_ptr(t) for t in packs])
+    yp = (ctypes.c_void_p * k)(*[_ptr(t) for t in ys])
+    rp = (ctypes.c_int64 * k)(*rows)
+    _check(_lib.load().dnx_gemm_q4_f6s_multi(pp, yp, rp, k, _ptr(panel), cols, n,
+                                             _stream(stream)), "dnx_gemm_q4_f6s_multi")
+
+
 def gemm_q4_f6s(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
     """The prefill chunk GEMM (5..512 tokens) on prepacked Q4 weights."""
     _need("gemm_q4_f6s",

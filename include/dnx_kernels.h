@@ -304,6 +304,16 @@ int dnx_gemm_q8_f6p(const void* packed, const void* panel, float* y, int64_t row
 int dnx_gemm_q4_f6s(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
                     int64_t n, dnx_stream_t stream);
 
+// The same chunk GEMM over 1..4 prepacked matrices of one width that read
+// the same panel (a prefill chunk's q, k and v projections, or its gate and
+// up), in one launch: y[k] = x W[k]^T, each bit-identical to its own
+// dnx_gemm_q4_f6s. No reference counterpart (the reference encodes one
+// dispatch per matmul); the lab_gpu_* command buffer uses it for
+// consecutive prefill matmuls of one x.
+int dnx_gemm_q4_f6s_multi(const void* const* packed, float* const* y, const int64_t* rows,
+                          int count, const void* panel, int64_t cols, int64_t n,
+                          dnx_stream_t stream);
+
 // dnx_gemm_q4_f6p without any allocation. No counterpart in the reference:
 // for callers that cannot allocate device memory (code under HIP graph
 // capture, serving loops, harnesses that forbid hipMalloc). Same kernels and

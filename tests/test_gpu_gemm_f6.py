@@ -329,6 +329,34 @@ def test_chunk_gemm_within_tolerance(gpu_ready, orc, rows, cols, n):
     assert np.array_equal(bits(y), bits(gemm_f6s(qs, sc, xq, xsc, rows, cols, n)))
 
 
+@pytest.mark.parametrize("rows_list,cols,n", [((2048, 1024, 1024), 2048, 13),
+                                              ((6144, 6144), 2048, 64),
+                                              ((97, 300, 33, 130), 160, 40),
+                                              ((70,), 96, 5)])
+def test_chunk_gemm_segments_equal_separate_launches(gpu_ready, orc, rows_list, cols, n):
+    """dnx_gemm_q4_f6s_multi (one launch over up to four matrices reading one
+    panel: a chunk's q, k, v or gate, up) gives every matrix the bits of its
+    own dnx_gemm_q4_f6s, rows not multiples of 32 included."""
+    rng = np.random.default_rng(sum(rows_list) + cols + n)
+    xs = synth.activations(rng, n, cols)
+    xq, xsc = orc.quantize_q8(xs)
+    panel = torch.full((D.f6_panel_bytes(n, cols),), 0x7f, dtype=torch.uint8, device="cuda")
+    D.pack_f6panel(dev(xq), dev(xsc), panel, n, cols)
+    packs, ys, want = [], [], []
+    for rows in rows_list:
+        qs, sc = synth.q4_weights(rng, rows, cols)
+        pk = torch.empty(D.q4_f6pack_bytes(rows, cols), dtype=torch.uint8, device="cuda")
+        D.pack_q4_f6(dev(qs), dev(sc), pk, rows, cols)
+        y1 = torch.full((n, rows), float("nan"), device="cuda")
+        D.gemm_q4_f6s(pk, panel, y1, rows, cols, n)
+        packs.append(pk)
+        ys.append(torch.full((n, rows), float("nan"), device="cuda"))
+        want.append(host(y1))
+    D.gemm_q4_f6s_multi(packs, ys, list(rows_list), panel, cols, n)
+    for k, rows in enumerate(rows_list):
+        assert np.array_equal(bits(host(ys[k])), bits(want[k])), f"matrix {k} ({rows} rows)"
+
+
 def test_chunk_gemm_refuses_bad_shapes(gpu_ready):
     z = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
     y = torch.zeros(65 * 64, device="cuda")
