@@ -1316,8 +1316,11 @@ int dnx_gemm_q4_f6s_multi(const void* const* packed, float* const* y, const int6
     p.rows[k] = (int)rows[k];
   }
   // 33+ tokens: two token groups per workgroup (one weight read for both:
-  // 64 tokens of 6144 x 2048 in 6.5 us against 7.9 with a workgroup per 32).
-  const bool two = n > kTokens;
+  // 64 tokens of 6144 x 2048 in 6.5 us against 7.9 with a workgroup per 32),
+  // unless that leaves fewer than 192 workgroups (a prefill chunk's 2048-row
+  // o and down projections: 64 of 256 CUs); then one per 32 tokens.
+  const int64_t pairs = (n + 2 * kTokens - 1) / (2 * kTokens);
+  const bool two = n > kTokens && groups * pairs >= 192;
   const int per = two ? 2 * kTokens : kTokens;
   const dim3 grid((unsigned)groups, (unsigned)((n + per - 1) / per));
   if (two) {
