@@ -116,6 +116,9 @@ SIGNATURES = {
     "dnx_gemm_q4_f6p": ([_p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_q4_f6s": ([_p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_gemm_q4_f6s_multi": ([_p, _p, _p, _i32, _p, _i64, _i64, _p], _i32),
+    "dnx_swiglu_f6panel": ([_p, _p, _p, _i64, _i64, _p], _i32),
+    "dnx_rms_norm_f6panel": ([_p, _p, _p, _p, _i64, _i64, _f32, _p], _i32),
+    "dnx_add_rms_norm_f6panel": ([_p, _p, _p, _p, _p, _i64, _i64, _f32, _p], _i32),
     "dnx_q8_f6pack_bytes": ([_i64, _i64], _i64),
     "dnx_pack_q8_f6": ([_p, _p, _p, _i64, _i64, _p], _i32),
     "dnx_gemm_q8_f6p": ([_p, _p, _p, _i64, _i64, _i64, _p], _i32),

@@ -172,6 +172,15 @@ DNX_DEV int q4_value(float x, float id) {
 
 // scale = amax / 127 and inv = 1 / scale, both correctly rounded
 // (lab_native.c:418-419).
+// SiLU(g) * u as the CPU glue rounds it (lib/src/shard.dart:457-461): SiLU
+// in double, stored to float, then one float multiply (the product of two
+// floats is exact in double, so rounding it once to float is that multiply).
+DNX_DEV float silu_mul_exact(float g, float u) {
+  const double a = (double)g;
+  const float s = (float)(a / (1.0 + exp(-a)));
+  return s * u;
+}
+
 DNX_DEV float q8_scale(float amax) { return amax / 127.0f; }
 DNX_DEV float q8_inv(float scale) { return scale > 0.0f ? 1.0f / scale : 0.0f; }
 

@@ -52,6 +52,7 @@
 
 #include "common.h"
 #include "dnx_kernels.h"
+#include "f6_panel.h"
 
 using namespace dnx;
 
@@ -64,11 +65,6 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 constexpr int kPanelThreads = 256;
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kTokens = 32;                 // tokens per panel group (one MFMA tile)
-constexpr int kRecF = 0;                    // [2 halves][64 lanes][16 B]: fp6 codes + operand dwords
-constexpr int kRecHalf = 1024;              // the second 16 bytes of every lane's record
-constexpr int kRecC = 2048;                 // 2 halves x 16 floats: the MFMA's C input
-constexpr int kRec = 2176;                  // panel bytes per (32 tokens, block)
 
 // The weight index held by each of a block's 32 fp6 fields after
 // q4_to_f6 (below) and so the order in which the panel lays out the
@@ -156,32 +152,9 @@ DNX_DEV void write_f6_entries(uint8_t* rec, int r, const int* xq, float scale) {
 
 // fp32 x [n][cols] -> f6 panel [groups][B][kRec]: lab_quantize_q8 of each
 // (token, block) (the same xq and scale bits as dnx_quantize_q8), then its
-// panel entries, with four lanes per (token, block) (a lane per block spent
-// its time packing 32 values in series). Lane j of a quad quantizes values 8j .. 8j+7 (lab_quantize_q8's
-// steps, the block's amax and sum(xq) over the quad by DPP). In the operand
-// order kFieldK those 8 values occupy 8 fields of one 96-bit half (j & 1)
-// of the 192-bit code field, at the places of pattern j >> 1 below; the two
-// lanes of a half OR their bits together, and each lane then stores one 16
-// bytes of the token's two lane records. The same bytes as write_f6_entries
-// writes for the (token, block).
-template <int F>
-DNX_DEV void put_field(uint32_t* d, uint32_t c) {
-  constexpr int bit = 6 * F, wd = bit >> 5, sh = bit & 31;
-  d[wd] |= c << sh;
-  if constexpr (sh > 26) d[wd + 1] |= c >> (32 - sh);
-}
-
-// Fields (within their 96-bit half) of a lane's values 0..7: pattern 0 for
-// lanes 0, 1 (values 0-7, 8-15), pattern 1 for lanes 2, 3 (16-23, 24-31).
-DNX_DEV void place_pattern0(uint32_t* d, const uint32_t* c) {
-  put_field<0>(d, c[0]); put_field<12>(d, c[1]); put_field<8>(d, c[2]); put_field<4>(d, c[3]);
-  put_field<11>(d, c[4]); put_field<7>(d, c[5]); put_field<3>(d, c[6]); put_field<15>(d, c[7]);
-}
-DNX_DEV void place_pattern1(uint32_t* d, const uint32_t* c) {
-  put_field<6>(d, c[0]); put_field<2>(d, c[1]); put_field<14>(d, c[2]); put_field<10>(d, c[3]);
-  put_field<1>(d, c[4]); put_field<13>(d, c[5]); put_field<9>(d, c[6]); put_field<5>(d, c[7]);
-}
-
+// panel entries, with four lanes per (token, block) (panel4_lane; a lane
+// per block spent its time packing 32 values in series). Tokens past n get
+// zero records.
 __global__ void __launch_bounds__(kPanelThreads) quantize_f6_panel4_kernel(
     const float* __restrict__ x, uint8_t* __restrict__ panel, int n, int cols, int groups) {
   const int B = cols / kBlock;
@@ -199,74 +172,40 @@ __global__ void __launch_bounds__(kPanelThreads) quantize_f6_panel4_kernel(
     const float4* src = (const float4*)(x + (int64_t)(live ? m : 0) * cols + b * kBlock + 8 * j);
     const float4 v0 = live ? src[0] : make_float4(0.f, 0.f, 0.f, 0.f);
     const float4 v1 = live ? src[1] : make_float4(0.f, 0.f, 0.f, 0.f);
-    float amax = fmaxf(max4abs(v0), max4abs(v1));
-    amax = fmaxf(amax, dppf<kQuadXor1>(amax));
-    amax = fmaxf(amax, dppf<kQuadXor2>(amax));
-    const float scale = q8_scale(amax);
-    const float inv = q8_inv(scale);
-    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    uint32_t ch[8], cl[8];
-    int sum = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int xq = quant1(vv[i], inv);
-      sum += xq;
-      const uint32_t a = (uint32_t)(xq < 0 ? -xq : xq);
-      const uint32_t sg = xq < 0 ? 0x20u : 0u;
-      ch[i] = sg | (a >> 3);
-      cl[i] = sg | (a & 7u);
+    panel4_lane(v0, v1, j, r, panel + gb * kRec);
+  }
+}
+
+// SiLU(g) * u in place (swiglu_kernel's values) over g, u [n][cols], and
+// the panel of the result for the matmul that reads it (a prefill chunk's
+// down projection): one pass, four lanes per (token, block), each lane 8
+// consecutive values. Tokens past n get zero records.
+__global__ void __launch_bounds__(kPanelThreads) swiglu_f6panel_kernel(
+    float* __restrict__ g, const float* __restrict__ u, uint8_t* __restrict__ panel, int n,
+    int cols, int groups) {
+  const int B = cols / kBlock;
+  const int64_t total = (int64_t)groups * B * kTokens * 4;  // whole quads
+  for (int64_t idx = (int64_t)blockIdx.x * kPanelThreads + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * kPanelThreads) {
+    const int j = (int)(idx & 3);
+    const int64_t q = idx >> 2;
+    const int r = (int)(q & (kTokens - 1));
+    const int64_t gb = q >> 5;
+    const int b = (int)(gb % B);
+    const int m = (int)(gb / B) * kTokens + r;
+    float4 h0 = make_float4(0.f, 0.f, 0.f, 0.f), h1 = h0;
+    if (m < n) {
+      float4* gp = (float4*)(g + (int64_t)m * cols + b * kBlock + 8 * j);
+      const float4* up = (const float4*)(u + (int64_t)m * cols + b * kBlock + 8 * j);
+      const float4 g0 = gp[0], g1 = gp[1], u0 = up[0], u1 = up[1];
+      h0 = make_float4(silu_mul_exact(g0.x, u0.x), silu_mul_exact(g0.y, u0.y),
+                       silu_mul_exact(g0.z, u0.z), silu_mul_exact(g0.w, u0.w));
+      h1 = make_float4(silu_mul_exact(g1.x, u1.x), silu_mul_exact(g1.y, u1.y),
+                       silu_mul_exact(g1.z, u1.z), silu_mul_exact(g1.w, u1.w));
+      gp[0] = h0;
+      gp[1] = h1;
     }
-    sum += dpp<kQuadXor1>(sum);
-    sum += dpp<kQuadXor2>(sum);
-    uint32_t h0[3] = {0, 0, 0}, h1[3] = {0, 0, 0}, l0[3] = {0, 0, 0}, l1[3] = {0, 0, 0};
-    place_pattern0(h0, ch);
-    place_pattern1(h1, ch);
-    place_pattern0(l0, cl);
-    place_pattern1(l1, cl);
-    const bool p1 = (j >> 1) != 0;
-    uint32_t hw[3], lw[3];
-#pragma unroll
-    for (int d = 0; d < 3; d++) {
-      hw[d] = p1 ? h1[d] : h0[d];
-      lw[d] = p1 ? l1[d] : l0[d];
-      hw[d] |= (uint32_t)dpp<kQuadXor2>((int)hw[d]);   // the other lane of this half
-      lw[d] |= (uint32_t)dpp<kQuadXor2>((int)lw[d]);
-    }
-    // Lanes 0, 2 hold dwords 0-2 of the field, lanes 1, 3 dwords 3-5; the
-    // first 16 bytes of a record also need dword 3 (the other half's first).
-    const uint32_t h3 = (uint32_t)dpp<kQuadXor1>((int)hw[0]);
-    const uint32_t l3 = (uint32_t)dpp<kQuadXor1>((int)lw[0]);
-    // The scale's pieces and E8M0 bytes, as write_f6_entries.
-    const uint32_t bits = __float_as_uint(scale);
-    const int ef = (int)((bits >> 23) & 0xff);
-    int e = ef == 0 ? -126 : ef - 127;
-    float mant = ef == 0 ? scale * 0x1p126f : __uint_as_float((bits & 0x807fffffu) | 0x3f800000u);
-    if (scale == 0.0f) {
-      e = 0;
-      mant = 0.0f;
-    }
-    const _Float16 p0 = (_Float16)mant;
-    const float r1 = mant - (float)p0;
-    const _Float16 pp1 = (_Float16)r1;
-    const _Float16 p2 = (_Float16)(r1 - (float)pp1);
-    const uint32_t sh_h = (uint32_t)(127 + 6 + e), sh_l = (uint32_t)(127 + 3 + e);
-    const uint32_t s0 = (uint32_t)__builtin_bit_cast(uint16_t, p0) |
-                        ((uint32_t)__builtin_bit_cast(uint16_t, pp1) << 16);
-    const uint32_t s1 = sh_h | ((uint32_t)__builtin_bit_cast(uint16_t, p2) << 16);
-    uint8_t* rec = panel + gb * kRec;
-    // Lane 0: h codes, first half; 1: h codes, second half + operand; 2, 3
-    // the same for the l codes.
-    uint4 o;
-    if (j == 0) o = make_uint4(hw[0], hw[1], hw[2], h3);
-    else if (j == 1) o = make_uint4(hw[1], hw[2], s0, s1);
-    else if (j == 2) o = make_uint4(lw[0], lw[1], lw[2], l3);
-    else o = make_uint4(lw[1], lw[2], 0u, sh_l);
-    const int lane_rec = (j & 2) ? 32 + r : r;
-    *(uint4*)(rec + kRecF + (j & 1) * kRecHalf + lane_rec * 16) = o;
-    if (j == 0) {
-      const float c = sum == 0 ? 0.0f : ldexpf((float)(-8 * sum), e);
-      *(float*)(rec + kRecC + ((((r >> 2) & 1) * 16 + (r >> 3) * 4 + (r & 3)) * 4)) = c;
-    }
+    panel4_lane(h0, h1, j, r, panel + gb * kRec);
   }
 }
 
@@ -1111,9 +1050,6 @@ float* scratch_on_device() {
   return gScratchPtr[dev];
 }
 
-int64_t f6_panel_bytes(int64_t n, int64_t cols) {
-  return (n + kTokens - 1) / kTokens * (cols / kBlock) * kRec;
-}
 
 bool f6_shape_ok(int64_t rows, int64_t cols, int64_t n) {
   if (rows <= 0 || cols <= 0 || n <= 0 || cols % kBlock != 0) return false;
@@ -1221,6 +1157,19 @@ extern "C" {
 int64_t dnx_f6_panel_bytes(int64_t n, int64_t cols) {
   if (n <= 0 || cols <= 0 || cols % kBlock != 0) return -1;
   return f6_panel_bytes(n, cols);
+}
+
+int dnx_swiglu_f6panel(float* g, const float* u, void* panel, int64_t n, int64_t cols,
+                       dnx_stream_t stream) {
+  if (n <= 0 || cols <= 0 || cols % kBlock != 0 || ((uintptr_t)g & 15) || ((uintptr_t)u & 15) ||
+      ((uintptr_t)panel & 15) || f6_panel_bytes(n, cols) >= (1ll << 31)) {
+    return DNX_EINVAL;
+  }
+  const int groups = (int)((n + kTokens - 1) / kTokens);
+  const int64_t total = (int64_t)groups * (cols / kBlock) * kTokens * 4;
+  hipLaunchKernelGGL(swiglu_f6panel_kernel, dim3(panel_grid(total)), dim3(kPanelThreads), 0,
+                     (hipStream_t)stream, g, u, (uint8_t*)panel, (int)n, (int)cols, groups);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 
 int dnx_quantize_q8_f6panel(const float* x, void* panel, int64_t n, int64_t cols,

@@ -124,13 +124,6 @@ DNX_DEV void wave_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
-// SiLU(g) * u as the CPU glue rounds it: SiLU in double, stored to float,
-// then one float multiply (the exact double product rounded once).
-DNX_DEV float silu_mul(float g, float u) {
-  const double a = (double)g;
-  const float s = (float)(a / (1.0 + exp(-a)));
-  return s * u;
-}
 
 // The kernel body; kNorm: RMSNorm of x fused into the prologue (n = 1,
 // 4 waves, one batch of quads; the launch checks these).
@@ -604,7 +597,7 @@ __device__ __forceinline__ void gemv_body(const GemvParams p) {
         if (kPair) {
           const float up = __shfl(v, lane + R * 4);  // the up row of this gate row
           if (lead && i < R) {
-            val = silu_mul(v, up);
+            val = silu_mul_exact(v, up);
             dst = p.y + (size_t)t * p.ldy + row;
           } else if (lead && p.y2 != nullptr) {
             dst = p.y2 + (size_t)t * p.ldy + row;

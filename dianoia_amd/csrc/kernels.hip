@@ -421,20 +421,12 @@ argmax_final_kernel(const float* __restrict__ v, const uint64_t* __restrict__ pa
 // ------------------------------------------------------------ glue
 
 // SiLU(g) * u in place (lab_gpu_enc_swiglu; CPU glue lib/src/shard.dart:
-// 457-461). The CPU does it in double and stores float32 twice: SiLU is
-// computed in double here too, then rounded; the product of two floats in
-// double is exact, so one float multiply rounds it identically.
-DNX_DEV float silu_mul1(float g, float u) {
-  const double a = (double)g;
-  const float s = (float)(a / (1.0 + exp(-a)));
-  return s * u;
-}
-
+// 457-461), rounded as the CPU rounds it (silu_mul_exact).
 __global__ void __launch_bounds__(kThreads)
 swiglu_kernel(float* __restrict__ g, const float* __restrict__ u, int64_t count) {
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < count;
        i += (int64_t)gridDim.x * kThreads) {
-    g[i] = silu_mul1(g[i], u[i]);
+    g[i] = silu_mul_exact(g[i], u[i]);
   }
 }
 

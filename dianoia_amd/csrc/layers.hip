@@ -15,6 +15,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "f6_panel.h"
 #include "dnx_kernels.h"
 
 #include <math.h>
@@ -91,10 +92,15 @@ rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, float*
 // kAdd: the residual add before the norm in the same pass (x += m, as
 // add_kernel rounds it, stored back to x, then the norm of the new x): the
 // pair dnx_add + dnx_rms_norm in one launch.
-template <int V, bool kAdd = false>
+// kPanel: also the fp6 GEMMs' activation panel of the normed rows (for the
+// prefill matmuls that read them), as dnx_quantize_q8_f6panel would make it
+// from out: the row goes through LDS (cols floats, dynamic) to four lanes
+// per 32-value block (panel4_lane); row blockIdx.x is token blockIdx.x.
+template <int V, bool kAdd = false, bool kPanel = false>
 __global__ void __launch_bounds__(kThreads)
 rms_norm_vec_kernel(const float* x_in, const float* __restrict__ w, float* out, int cols,
-                    float eps, int accumulate, const float* __restrict__ m, float* x_out) {
+                    float eps, int accumulate, const float* __restrict__ m, float* x_out,
+                    uint8_t* __restrict__ panel) {
   __shared__ float scratch[kWaves];
   const int q = cols / 4;
   const float4* xr = (const float4*)(x_in + (size_t)blockIdx.x * cols);
@@ -150,6 +156,24 @@ rms_norm_vec_kernel(const float* x_in, const float* __restrict__ w, float* out, 
       v.w = ov[e].w + v.w;
     }
     yr[i] = v;
+    if constexpr (kPanel) {
+      extern __shared__ float4 row_lds[];
+      row_lds[i] = v;
+    }
+  }
+  if constexpr (kPanel) {
+    extern __shared__ float4 row_lds[];
+    __syncthreads();
+    const int B = cols / kBlock;
+    const int tok = blockIdx.x, r = tok % kTokens;
+    uint8_t* recs = panel + (size_t)(tok / kTokens) * B * kRec;
+    // Whole quads of lanes (kThreads and 4 B are multiples of 4): the quad
+    // reductions inside panel4_lane see their four lanes.
+    for (int idx = threadIdx.x; idx < 4 * B; idx += kThreads) {
+      const int j = idx & 3, b = idx >> 2;
+      const float4 v0 = row_lds[b * 8 + 2 * j], v1 = row_lds[b * 8 + 2 * j + 1];
+      panel4_lane(v0, v1, j, r, recs + (size_t)b * kRec);
+    }
   }
 }
 
@@ -1195,9 +1219,58 @@ int attention_split(const float* q, const float* keys, const float* values, cons
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }
 
+// The vector norm with the activation panel of its output (kPanel), with
+// or without the residual add before it (kAdd): V float4 per thread as the
+// row needs, the row in dynamic LDS.
+template <bool kAdd>
+int launch_norm_panel(const float* x_in, const float* w, float* out, int64_t rows, int64_t cols,
+                      float eps, const float* m, float* x_out, uint8_t* panel, hipStream_t s) {
+  const int64_t per = (cols / 4 + kThreads - 1) / kThreads;  // float4 per thread
+  const size_t lds = (size_t)cols * 4;
+  const dim3 grid((unsigned)rows);
+  if (per <= 1) {
+    hipLaunchKernelGGL((rms_norm_vec_kernel<1, kAdd, true>), grid, dim3(kThreads), lds, s, x_in, w,
+                       out, (int)cols, eps, 0, m, x_out, panel);
+  } else if (per <= 2) {
+    hipLaunchKernelGGL((rms_norm_vec_kernel<2, kAdd, true>), grid, dim3(kThreads), lds, s, x_in, w,
+                       out, (int)cols, eps, 0, m, x_out, panel);
+  } else if (per <= 4) {
+    hipLaunchKernelGGL((rms_norm_vec_kernel<4, kAdd, true>), grid, dim3(kThreads), lds, s, x_in, w,
+                       out, (int)cols, eps, 0, m, x_out, panel);
+  } else {
+    hipLaunchKernelGGL((rms_norm_vec_kernel<8, kAdd, true>), grid, dim3(kThreads), lds, s, x_in, w,
+                       out, (int)cols, eps, 0, m, x_out, panel);
+  }
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+bool norm_panel_ok(int64_t rows, int64_t cols, uintptr_t ptrs) {
+  return rows > 0 && rows <= 256 && cols > 0 && cols % kBlock == 0 && cols <= 8192 &&
+         (ptrs & 15) == 0 && f6_panel_bytes(rows, cols) < (1ll << 31);
+}
+
 }  // namespace
 
 extern "C" {
+
+int dnx_rms_norm_f6panel(const float* x, const float* w, float* out, void* panel, int64_t rows,
+                         int64_t cols, float eps, dnx_stream_t stream) {
+  if (!norm_panel_ok(rows, cols, (uintptr_t)x | (uintptr_t)w | (uintptr_t)out | (uintptr_t)panel)) {
+    return DNX_EINVAL;
+  }
+  return launch_norm_panel<false>(x, w, out, rows, cols, eps, nullptr, nullptr, (uint8_t*)panel,
+                                  (hipStream_t)stream);
+}
+
+int dnx_add_rms_norm_f6panel(const float* m, float* x, const float* w, float* out, void* panel,
+                             int64_t rows, int64_t cols, float eps, dnx_stream_t stream) {
+  if (!norm_panel_ok(rows, cols, (uintptr_t)m | (uintptr_t)x | (uintptr_t)w | (uintptr_t)out |
+                                     (uintptr_t)panel)) {
+    return DNX_EINVAL;
+  }
+  return launch_norm_panel<true>(x, w, out, rows, cols, eps, m, x, (uint8_t*)panel,
+                                 (hipStream_t)stream);
+}
 
 int dnx_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64_t cols,
                  float eps, int accumulate, dnx_stream_t stream) {
@@ -1214,19 +1287,19 @@ int dnx_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64
     const int64_t per = (cols / 4 + kThreads - 1) / kThreads;  // float4 per thread
     if (per <= 1) {
       hipLaunchKernelGGL(rms_norm_vec_kernel<1>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
-                         (int)cols, eps, accumulate, nullptr, nullptr);
+                         (int)cols, eps, accumulate, nullptr, nullptr, nullptr);
     } else if (per <= 2) {
       hipLaunchKernelGGL(rms_norm_vec_kernel<2>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
-                         (int)cols, eps, accumulate, nullptr, nullptr);
+                         (int)cols, eps, accumulate, nullptr, nullptr, nullptr);
     } else if (per <= 4) {
       hipLaunchKernelGGL(rms_norm_vec_kernel<4>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
-                         (int)cols, eps, accumulate, nullptr, nullptr);
+                         (int)cols, eps, accumulate, nullptr, nullptr, nullptr);
     } else if (per <= 8) {
       hipLaunchKernelGGL(rms_norm_vec_kernel<8>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
-                         (int)cols, eps, accumulate, nullptr, nullptr);
+                         (int)cols, eps, accumulate, nullptr, nullptr, nullptr);
     } else {
       hipLaunchKernelGGL(rms_norm_vec_kernel<16>, dim3(grid), dim3(kThreads), 0, s, x, w, out,
-                         (int)cols, eps, accumulate, nullptr, nullptr);
+                         (int)cols, eps, accumulate, nullptr, nullptr, nullptr);
     }
   } else {
     hipLaunchKernelGGL(rms_norm_kernel, dim3(grid), dim3(kThreads), 0, s, x, w, out, (int)cols,
@@ -1247,19 +1320,19 @@ int dnx_add_rms_norm(const float* m, float* x, const float* w, float* out, int64
   const int64_t per = (cols / 4 + kThreads - 1) / kThreads;  // float4 per thread
   if (per <= 1) {
     hipLaunchKernelGGL((rms_norm_vec_kernel<1, true>), dim3(grid), dim3(kThreads), 0, s, x, w,
-                       out, (int)cols, eps, 0, m, x);
+                       out, (int)cols, eps, 0, m, x, nullptr);
   } else if (per <= 2) {
     hipLaunchKernelGGL((rms_norm_vec_kernel<2, true>), dim3(grid), dim3(kThreads), 0, s, x, w,
-                       out, (int)cols, eps, 0, m, x);
+                       out, (int)cols, eps, 0, m, x, nullptr);
   } else if (per <= 4) {
     hipLaunchKernelGGL((rms_norm_vec_kernel<4, true>), dim3(grid), dim3(kThreads), 0, s, x, w,
-                       out, (int)cols, eps, 0, m, x);
+                       out, (int)cols, eps, 0, m, x, nullptr);
   } else if (per <= 8) {
     hipLaunchKernelGGL((rms_norm_vec_kernel<8, true>), dim3(grid), dim3(kThreads), 0, s, x, w,
-                       out, (int)cols, eps, 0, m, x);
+                       out, (int)cols, eps, 0, m, x, nullptr);
   } else {
     hipLaunchKernelGGL((rms_norm_vec_kernel<16, true>), dim3(grid), dim3(kThreads), 0, s, x, w,
-                       out, (int)cols, eps, 0, m, x);
+                       out, (int)cols, eps, 0, m, x, nullptr);
   }
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }

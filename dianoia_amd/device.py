@@ -435,6 +435,32 @@ def swiglu(g: torch.Tensor, u: torch.Tensor, stream=None) -> None:
     _check(_lib.load().dnx_swiglu(_ptr(g), _ptr(u), g.numel(), _stream(stream)), "dnx_swiglu")
 
 
+def swiglu_f6panel(g, u, panel, rows: int, cols: int, stream=None) -> None:
+    """swiglu in place, and the fp6 panel of the result."""
+    _need("swiglu_f6panel", g=(g, rows * cols * 4), u=(u, rows * cols * 4),
+          panel=(panel, f6_panel_bytes(rows, cols)))
+    _check(_lib.load().dnx_swiglu_f6panel(_ptr(g), _ptr(u), _ptr(panel), rows, cols,
+                                          _stream(stream)), "dnx_swiglu_f6panel")
+
+
+def rms_norm_f6panel(x, w, out, panel, rows: int, cols: int, eps: float, stream=None) -> None:
+    """rms_norm (no accumulate), and the fp6 panel of its output."""
+    _need("rms_norm_f6panel", x=(x, rows * cols * 4), w=(w, cols * 4),
+          out=(out, rows * cols * 4), panel=(panel, f6_panel_bytes(rows, cols)))
+    _check(_lib.load().dnx_rms_norm_f6panel(_ptr(x), _ptr(w), _ptr(out), _ptr(panel), rows, cols,
+                                            eps, _stream(stream)), "dnx_rms_norm_f6panel")
+
+
+def add_rms_norm_f6panel(m, x, w, out, panel, rows: int, cols: int, eps: float,
+                         stream=None) -> None:
+    """add_rms_norm, and the fp6 panel of its output."""
+    _need("add_rms_norm_f6panel", m=(m, rows * cols * 4), x=(x, rows * cols * 4),
+          w=(w, cols * 4), out=(out, rows * cols * 4), panel=(panel, f6_panel_bytes(rows, cols)))
+    _check(_lib.load().dnx_add_rms_norm_f6panel(_ptr(m), _ptr(x), _ptr(w), _ptr(out),
+                                                _ptr(panel), rows, cols, eps, _stream(stream)),
+           "dnx_add_rms_norm_f6panel")
+
+
 def gelu(x: torch.Tensor, stream=None) -> None:
     _check(_lib.load().dnx_gelu(_ptr(x), x.numel(), _stream(stream)), "dnx_gelu")
 

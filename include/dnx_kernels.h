@@ -377,6 +377,22 @@ int dnx_argmax(const float* v, int64_t n, int64_t* out, void* workspace, dnx_str
 // lab_gpu_enc_swiglu), SiLU in double as the Dart glue computes it.
 int dnx_swiglu(float* g, const float* u, int64_t count, dnx_stream_t stream);
 
+// Producers that also write the fp6 GEMMs' activation panel of their output
+// (the bytes dnx_quantize_q8_f6panel would make from it: dnx_f6_panel_bytes(
+// rows, cols), records of tokens past `rows` not written), so that the
+// prefill matmuls reading that output skip the quantize launch. No
+// reference counterpart; the lab_gpu_* command buffer uses them when the
+// next commands are such matmuls. Outputs bit-identical to dnx_swiglu,
+// dnx_rms_norm (accumulate 0) and dnx_add_rms_norm. The norms take up to 256
+// rows of up to 8192 columns, a multiple of 32; every pointer 16-byte
+// aligned.
+int dnx_swiglu_f6panel(float* g, const float* u, void* panel, int64_t rows, int64_t cols,
+                       dnx_stream_t stream);
+int dnx_rms_norm_f6panel(const float* x, const float* w, float* out, void* panel, int64_t rows,
+                         int64_t cols, float eps, dnx_stream_t stream);
+int dnx_add_rms_norm_f6panel(const float* m, float* x, const float* w, float* out, void* panel,
+                             int64_t rows, int64_t cols, float eps, dnx_stream_t stream);
+
 // Exact-erf GELU in place with the Abramowitz-Stegun erf in double
 // (lib/src/vision_encoder.dart:260-263, :496-509). x 4-byte aligned; any
 // count and offset.

@@ -455,3 +455,70 @@ def test_q8_gemm_within_tolerance(gpu_ready, orc, rows, cols, n, fp32_scales):
     assert np.all(np.abs(y - exact) <= 1e-5 * mag)
     ok, worst_rel, worst_abs = within_tolerance(y, ref)
     assert ok, (worst_rel, worst_abs)
+
+
+# --------------------------- producers that write the panel of their output
+
+def token_records(panel, n, cols):
+    """The panel bytes of tokens 0..n-1 (their four 16-byte lane-record
+    pieces and their C value per block), as one array per token."""
+    p = host(panel).view(np.uint8)
+    B = cols // 32
+    out = []
+    for t in range(n):
+        g, r = divmod(t, 32)
+        parts = []
+        for b in range(B):
+            rec = (g * B + b) * 2176
+            for off in (r * 16, (32 + r) * 16, 1024 + r * 16, 1024 + (32 + r) * 16):
+                parts.append(p[rec + off:rec + off + 16])
+            c = 2048 + ((((r >> 2) & 1) * 16 + (r >> 3) * 4 + (r & 3)) * 4)
+            parts.append(p[rec + c:rec + c + 4])
+        out.append(np.concatenate(parts))
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("n,cols", [(64, 6144), (13, 2048), (5, 96), (33, 1024)])
+def test_swiglu_panel_equals_swiglu_then_quantizer(gpu_ready, n, cols):
+    """dnx_swiglu_f6panel: h = SiLU(g) * u in place with swiglu's bits, and
+    the panel dnx_quantize_q8_f6panel makes from h (padding tokens too)."""
+    rng = np.random.default_rng(n + cols)
+    g = (rng.standard_normal((n, cols)) * 2).astype(np.float32)
+    u = rng.standard_normal((n, cols)).astype(np.float32)
+    g1, g2, ud = dev(g), dev(g), dev(u)
+    p1 = torch.full((D.f6_panel_bytes(n, cols),), 0x7f, dtype=torch.uint8, device="cuda")
+    p2 = p1.clone()
+    D.swiglu(g1, ud)
+    D.quantize_q8_f6panel(g1, p1, n, cols)
+    D.swiglu_f6panel(g2, ud, p2, n, cols)
+    assert np.array_equal(bits(host(g2)), bits(host(g1)))
+    assert np.array_equal(host(p2), host(p1))
+
+
+@pytest.mark.parametrize("add", [False, True])
+@pytest.mark.parametrize("n,cols", [(64, 2048), (13, 2048), (5, 4096), (33, 96), (256, 1024)])
+def test_norm_panel_equals_norm_then_quantizer(gpu_ready, n, cols, add):
+    """dnx_rms_norm_f6panel / dnx_add_rms_norm_f6panel: the norm's outputs
+    (and the residual sum) with the unfused kernels' bits, and every live
+    token's panel records as dnx_quantize_q8_f6panel makes them from the
+    normed rows."""
+    rng = np.random.default_rng(n * 3 + cols + add)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    m = rng.standard_normal((n, cols)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    eps = 1e-6
+    xa, xb, md, wd = dev(x), dev(x), dev(m), dev(w)
+    o1 = torch.empty((n, cols), device="cuda")
+    o2 = torch.empty((n, cols), device="cuda")
+    p1 = torch.full((D.f6_panel_bytes(n, cols),), 0x7f, dtype=torch.uint8, device="cuda")
+    p2 = p1.clone()
+    if add:
+        D.add_rms_norm(md, xa, wd, o1, n, cols, eps)
+        D.add_rms_norm_f6panel(md, xb, wd, o2, p2, n, cols, eps)
+        assert np.array_equal(bits(host(xb)), bits(host(xa)))
+    else:
+        D.rms_norm(xa, wd, o1, n, cols, eps)
+        D.rms_norm_f6panel(xb, wd, o2, p2, n, cols, eps)
+    D.quantize_q8_f6panel(o1, p1, n, cols)
+    assert np.array_equal(bits(host(o2)), bits(host(o1)))
+    assert np.array_equal(token_records(p2, n, cols), token_records(p1, n, cols))
