@@ -729,6 +729,21 @@ Prepack* chunk_prepack(const Cmd& c) {
   return find_prepack(c.a[0], c.a[1], c.a[2], rows, cols);
 }
 
+// The command after the one the commit runs now (set by the commit loop for
+// the commands that can hand the matmul after them its activation panel).
+const Cmd* gNext = nullptr;
+
+// Whether that next command is a prefill matmul on the chunk route reading
+// [h + off, n x cols floats) as its input: the producer of that input then
+// writes its panel too, and the matmul (or the group that starts with it)
+// finds it made (gPanel).
+bool next_reads_panel(int64_t h, int64_t off, int64_t n, int64_t cols) {
+  if (gNext == nullptr || gWs == nullptr) return false;
+  const Cmd& c = *gNext;
+  return chunk_prepack(c) != nullptr && c.a[3] == h && c.a[4] == off && c.a[9] == n &&
+         c.a[8] == cols;
+}
+
 // Consecutive prefill matmuls of one x on the chunk route (a chunk's q, k
 // and v, or gate and up): how many (2..4) one launch runs, 0 for none. As in
 // multi_len, no output may overlap x or another output, and none may land
@@ -984,16 +999,30 @@ int run_add_norm(const Cmd& a, const Cmd& b) {
   read_region(m, mOff, count * 4);
   read_region(x, xOff, count * 4);
   read_region(w, wOff, cols * 4);
-  const int rc = dnx_add_rms_norm((const float*)dev_at(m, mOff), (float*)dev_at(x, xOff),
-                                  (const float*)dev_at(w, wOff), (float*)dev_at(out, outOff), rows,
-                                  cols, (float)eps, gStream);
+  // With the panel of out when the next command is a prefill matmul of it.
+  bool panel = next_reads_panel(out, outOff, rows, cols);
+  int rc = DNX_EINVAL;
+  if (panel) {
+    gPanel = PanelKey{};
+    rc = dnx_add_rms_norm_f6panel((const float*)dev_at(m, mOff), (float*)dev_at(x, xOff),
+                                  (const float*)dev_at(w, wOff), (float*)dev_at(out, outOff), gWs,
+                                  rows, cols, (float)eps, gStream);
+  }
+  if (rc == DNX_EINVAL) {
+    panel = false;
+    rc = dnx_add_rms_norm((const float*)dev_at(m, mOff), (float*)dev_at(x, xOff),
+                          (const float*)dev_at(w, wOff), (float*)dev_at(out, outOff), rows, cols,
+                          (float)eps, gStream);
+  }
   if (rc == DNX_EINVAL) return rc;
   if (rc == DNX_OK) {
     after_dispatch(kKindRmsNorm);
     also_ran(kKindAdd);
+    if (panel) also_ran(kKindQuantize);
   }
   wrote_region(x, xOff, count * 4);
   wrote_region(out, outOff, count * 4);
+  if (panel && rc == DNX_OK) gPanel = PanelKey{out, outOff, rows, cols};
   if (rc != DNX_OK) LOG("add + rms_norm %ldx%ld failed (%d)\n", (long)rows, (long)cols, rc);
   return rc;
 }
@@ -1151,9 +1180,25 @@ bool run(const Cmd& c) {
       const int64_t g = c.a[0], u = c.a[1], count = c.a[2];
       read_region(g, 0, count * 4);
       read_region(u, 0, count * 4);
-      const int rc = dnx_swiglu((float*)dev_at(g, 0), (const float*)dev_at(u, 0), count, gStream);
+      // With the panel of g when the next command is a prefill matmul of it
+      // (a chunk's down projection).
+      const int64_t pn = gNext != nullptr ? gNext->a[9] : 0;
+      const int64_t pc = gNext != nullptr ? gNext->a[8] : 0;
+      bool panel = pn * pc == count && next_reads_panel(g, 0, pn, pc);
+      int rc = DNX_EINVAL;
+      if (panel) {
+        gPanel = PanelKey{};
+        rc = dnx_swiglu_f6panel((float*)dev_at(g, 0), (const float*)dev_at(u, 0), gWs, pn, pc,
+                                gStream);
+      }
+      if (rc == DNX_EINVAL) {
+        panel = false;
+        rc = dnx_swiglu((float*)dev_at(g, 0), (const float*)dev_at(u, 0), count, gStream);
+      }
       after_dispatch(kKindSwiglu);
+      if (panel && rc == DNX_OK) also_ran(kKindQuantize);
       wrote_region(g, 0, count * 4);
+      if (panel && rc == DNX_OK) gPanel = PanelKey{g, 0, pn, pc};
       return rc == DNX_OK;
     }
     case kOpQuantize:
@@ -1224,11 +1269,25 @@ bool run(const Cmd& c) {
       read_region(x, xOff, rows * cols * 4);
       read_region(w, wOff, cols * 4);
       if (acc) read_region(out, outOff, rows * cols * 4);
-      const int rc = dnx_rms_norm((const float*)dev_at(x, xOff), (const float*)dev_at(w, wOff),
-                                  (float*)dev_at(out, outOff), rows, cols, (float)eps,
-                                  acc != 0, gStream);
+      // With the panel of out when the next command is a prefill matmul of
+      // it (and the norm does not accumulate).
+      bool panel = acc == 0 && next_reads_panel(out, outOff, rows, cols);
+      int rc = DNX_EINVAL;
+      if (panel) {
+        gPanel = PanelKey{};
+        rc = dnx_rms_norm_f6panel((const float*)dev_at(x, xOff), (const float*)dev_at(w, wOff),
+                                  (float*)dev_at(out, outOff), gWs, rows, cols, (float)eps,
+                                  gStream);
+      }
+      if (rc == DNX_EINVAL) {
+        panel = false;
+        rc = dnx_rms_norm((const float*)dev_at(x, xOff), (const float*)dev_at(w, wOff),
+                          (float*)dev_at(out, outOff), rows, cols, (float)eps, acc != 0, gStream);
+      }
       after_dispatch(kKindRmsNorm);
+      if (panel && rc == DNX_OK) also_ran(kKindQuantize);
       wrote_region(out, outOff, rows * cols * 4);
+      if (panel && rc == DNX_OK) gPanel = PanelKey{out, outOff, rows, cols};
       return rc == DNX_OK;
     }
     case kOpHeadNormRope: {
@@ -1552,6 +1611,7 @@ int64_t lab_gpu_commit(int64_t wait) {
         i += 1;
       }
     } else if (i + 1 < gCmds.size() && fusable_add_norm(gCmds[i], gCmds[i + 1])) {
+      gNext = i + 2 < gCmds.size() ? &gCmds[i + 2] : nullptr;
       const int rc = run_add_norm(gCmds[i], gCmds[i + 1]);
       if (rc == DNX_EINVAL) {
         ok = run(gCmds[i]) && ok;
@@ -1604,8 +1664,10 @@ int64_t lab_gpu_commit(int64_t wait) {
       }
       i += len - 1;
     } else {
+      gNext = i + 1 < gCmds.size() ? &gCmds[i + 1] : nullptr;
       ok = run(gCmds[i]) && ok;
     }
+    gNext = nullptr;
   }
   // Results back to the host views, each written byte once (regions of a
   // buffer merged where they overlap or touch). A dirty page a copy covers

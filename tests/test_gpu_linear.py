@@ -473,3 +473,80 @@ def test_q4_prefill_matmuls_of_one_x_share_its_panel(gpu, orc):
     gpu._matrix("c").encode(lib, x.handle, ys["c"].handle, 0, n)
     gpu._finish()
     check("c", xa)
+
+
+def test_q4_prefill_inputs_from_norm_add_norm_and_swiglu_bring_their_panel(gpu, orc):
+    """An RMSNorm, a residual add + RMSNorm or a SwiGLU whose output is the x
+    of the prefill matmul right after it (a chunk's q/k/v, gate/up and down
+    projections) writes x's activation panel too, and the matmul uses it:
+    one command buffer gives the same bits as each command committed on its
+    own, and the profile counts one activation quantize per x. A matmul of
+    another x after the producer quantizes its own."""
+    import ctypes
+    rng = np.random.default_rng(43)
+    n, cols, rows = 13, 1024, 768
+    qs, sc = synth.q4_weights(rng, rows, cols)
+    gpu.upload("a", QuantMatrix.q4(qs, sc))
+    qs2, sc2 = synth.q4_weights(rng, cols, rows)
+    gpu.upload("d", QuantMatrix.q4(qs2, sc2))
+    lib = gpu._lib
+    count = n * cols
+    bufs = {k: gpu._aux_buffer("pp_" + k, count) for k in ("x", "m", "h", "o", "g", "u")}
+    w = gpu._aux_buffer("pp_w", cols)
+    ys = {k: gpu._aux_buffer("pp_y" + k, n * cols) for k in ("1", "2", "3", "4")}
+    inputs = {k: synth.activations(rng, n, cols).reshape(-1) for k in ("x", "m", "o")}
+    gu = (rng.standard_normal((2, n * rows)) * 2).astype(np.float32)
+    w.view(count=cols)[:] = (1 + rng.standard_normal(cols) * 0.1).astype(np.float32)
+
+    def encode():
+        h = bufs
+        yield lambda: lib.lab_gpu_enc_rms_norm(h["x"].handle, 0, w.handle, 0, h["h"].handle, 0,
+                                               n, cols, 1e-6, 0)
+        yield lambda: gpu._matrix("a").encode(lib, h["h"].handle, ys["1"].handle, 0, n)
+        yield lambda: lib.lab_gpu_enc_add(h["m"].handle, 0, h["x"].handle, 0, count)
+        yield lambda: lib.lab_gpu_enc_rms_norm(h["x"].handle, 0, w.handle, 0, h["h"].handle, 0,
+                                               n, cols, 1e-6, 0)
+        yield lambda: gpu._matrix("a").encode(lib, h["h"].handle, ys["2"].handle, 0, n)
+        yield lambda: lib.lab_gpu_enc_swiglu(h["g"].handle, h["u"].handle, n * rows)
+        yield lambda: gpu._matrix("d").encode(lib, h["g"].handle, ys["3"].handle, 0, n)
+        yield lambda: lib.lab_gpu_enc_rms_norm(h["x"].handle, 0, w.handle, 0, h["h"].handle, 0,
+                                               n, cols, 1e-6, 0)
+        yield lambda: gpu._matrix("a").encode(lib, h["o"].handle, ys["4"].handle, 0, n)
+
+    def run(together):
+        for k, v in inputs.items():
+            bufs[k].view(count=count)[:] = v
+        bufs["g"].view(count=n * rows)[:] = gu[0]
+        bufs["u"].view(count=n * rows)[:] = gu[1]
+        for y in ys.values():
+            y.view(count=n * cols)[:] = np.nan
+        if together:
+            lib.lab_gpu_begin()
+            for enc in encode():
+                enc()
+            gpu._finish()
+        else:
+            for enc in encode():
+                lib.lab_gpu_begin()
+                enc()
+                gpu._finish()
+        return {k: y.view(count=n * cols).copy() for k, y in ys.items()}
+
+    ms = (ctypes.c_double * 21)()
+    counts = (ctypes.c_int64 * 21)()
+    quantize = 10
+    run(True)   # makes the prepacks
+    apart = run(False)
+    lib.lab_gpu_profile(ms, counts, 21)
+    lib.lab_gpu_set_profiling(1)
+    together = run(True)
+    lib.lab_gpu_set_profiling(0)
+    lib.lab_gpu_profile(ms, counts, 21)
+    for k in ys:
+        assert np.array_equal(bits(apart[k]), bits(together[k])), k
+    assert counts[quantize] == 4, list(counts)
+    # Against the CPU kernels on the inputs of each matmul.
+    x1 = orc.rms_norm(inputs["x"].reshape(n, cols), w.view(count=cols).copy(), 1e-6)
+    ok, rel, ab = within_tolerance(together["1"][:n * rows].reshape(n, rows),
+                                   orc.gemm_q4(qs, sc, x1, n, threads=8, mode=1))
+    assert ok, (rel, ab)
