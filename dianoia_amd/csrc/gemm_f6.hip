@@ -842,8 +842,6 @@ __global__ void __launch_bounds__(kThreads) gemm_f6p_kernel(F6PParams p) {
 // scale MFMA per (token group, block) and folds; then the 8 waves' sums are
 // added through LDS in wave order (deterministic) and stored write-through.
 
-constexpr int kSkRing = 4;      // blocks in flight per wave
-
 // Up to kMaxSegs matrices over the same x in one launch (a prefill chunk's
 // q, k and v, or gate and up): their 32-row groups laid end to end along
 // grid x, seg_end holding the cumulative group ends.
@@ -859,7 +857,9 @@ struct F6SParams {
   int rows[kMaxSegs];
 };
 
-template <int G>
+// R: blocks in flight per wave (the register ring); kOnce: every wave has
+// at most R blocks, all loaded at the start (no refills).
+template <int G, int R, bool kOnce>
 __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
   constexpr int kOut = G * kTokens * 32;               // outputs of the workgroup
   __shared__ __align__(16) float red[kWaves * kOut];   // each wave's sums, [wave][token][row]
@@ -909,12 +909,12 @@ __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
   const int nb = (B - wave + kWaves - 1) / kWaves;     // this wave's blocks
-  Slot ring[kSkRing];
+  Slot ring[R];
 #pragma unroll
-  for (int r = 0; r < kSkRing; r++) load(r, ring[r]);
-  for (int i0 = 0; i0 < nb; i0 += kSkRing) {
+  for (int r = 0; r < R; r++) load(r, ring[r]);
+  for (int i0 = 0; i0 < nb; i0 += R) {
 #pragma unroll
-    for (int r = 0; r < kSkRing; r++) {
+    for (int r = 0; r < R; r++) {
       Slot& sl = ring[r];
       asm volatile("" : "+v"(sl.w0), "+v"(sl.w1));
       const v8i bq = {sl.w0[0], sl.w0[1], sl.w0[2], sl.w0[3], sl.w1[0], sl.w1[1], 0, 0};
@@ -932,7 +932,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[t][v] = fmaf(d[v], sc[v], acc[t][v]);
       }
-      load(i0 + r + kSkRing, sl);
+      if constexpr (!kOnce) load(i0 + r + R, sl);
     }
   }
 
@@ -1267,15 +1267,35 @@ int dnx_gemm_q4_f6s_multi(const void* const* packed, float* const* y, const int6
   // 33+ tokens: two token groups per workgroup (one weight read for both:
   // 64 tokens of 6144 x 2048 in 6.5 us against 7.9 with a workgroup per 32),
   // unless that leaves fewer than 192 workgroups (a prefill chunk's 2048-row
-  // o and down projections: 64 of 256 CUs); then one per 32 tokens.
+  // o and down projections: 64 of 256 CUs) while one per 32 tokens still
+  // fits one round of 256 (a workgroup fills its CU's registers: more than
+  // 256 workgroups run in two rounds; 375 tokens of 768 x 768 take 144
+  // workgroups in one round, not 288 in two).
   const int64_t pairs = (n + 2 * kTokens - 1) / (2 * kTokens);
-  const bool two = n > kTokens && groups * pairs >= 192;
+  const int64_t singles = (n + kTokens - 1) / kTokens;
+  const bool two = n > kTokens && (groups * pairs >= 192 || groups * singles > 256);
   const int per = two ? 2 * kTokens : kTokens;
   const dim3 grid((unsigned)groups, (unsigned)((n + per - 1) / per));
+  // A wave's blocks all loaded at once where they fit the ring (one round
+  // trip: 8 blocks of one token group, 4 of two), else a ring of 4.
+  const int nb = (int)(cols / kBlock + kWaves - 1) / kWaves;
   if (two) {
-    hipLaunchKernelGGL(gemm_f6s_kernel<2>, grid, dim3(kThreads), 0, (hipStream_t)stream, p);
+    if (nb <= 4) {
+      hipLaunchKernelGGL((gemm_f6s_kernel<2, 4, true>), grid, dim3(kThreads), 0,
+                         (hipStream_t)stream, p);
+    } else {
+      hipLaunchKernelGGL((gemm_f6s_kernel<2, 4, false>), grid, dim3(kThreads), 0,
+                         (hipStream_t)stream, p);
+    }
+  } else if (nb <= 4) {
+    hipLaunchKernelGGL((gemm_f6s_kernel<1, 4, true>), grid, dim3(kThreads), 0,
+                       (hipStream_t)stream, p);
+  } else if (nb <= 8) {
+    hipLaunchKernelGGL((gemm_f6s_kernel<1, 8, true>), grid, dim3(kThreads), 0,
+                       (hipStream_t)stream, p);
   } else {
-    hipLaunchKernelGGL(gemm_f6s_kernel<1>, grid, dim3(kThreads), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((gemm_f6s_kernel<1, 4, false>), grid, dim3(kThreads), 0,
+                       (hipStream_t)stream, p);
   }
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
 }

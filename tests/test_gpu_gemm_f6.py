@@ -274,7 +274,7 @@ def gemm_f6s(qs, sc, xq, xsc, rows, cols, n):
 
 
 @pytest.mark.parametrize("rows,cols,n", [(130, 256, 64), (33, 96, 5), (17, 2048, 16),
-                                         (97, 1024, 33), (64, 512, 32)])
+                                         (97, 1024, 33), (64, 512, 32), (40, 1568, 20)])
 def test_chunk_gemm_block_dots_are_exact(gpu_ready, orc, rows, cols, n):
     """dnx_gemm_q4_f6s: scale 1 on one block and 0 on the others gives that
     block's exact dot, for every block (every |xq| up to 127, every nibble)."""
@@ -311,7 +311,8 @@ def test_chunk_gemm_unit_scales_sum_blocks_exactly(gpu_ready, orc):
 @pytest.mark.parametrize("rows,cols,n", [(6144, 2048, 64), (6144, 2048, 8), (2048, 6144, 33),
                                          (768, 768, 13), (97, 160, 5), (257, 2048, 32),
                                          (1152, 4320, 17), (100, 96, 64), (1792, 768, 48),
-                                         (4304, 1152, 64), (768, 768, 375), (2048, 768, 130)])
+                                         (4304, 1152, 64), (768, 768, 375), (2048, 768, 130),
+                                         (300, 1568, 24), (2048, 2048, 64), (1024, 1536, 7)])
 def test_chunk_gemm_within_tolerance(gpu_ready, orc, rows, cols, n):
     """Against the exact products (error / sum|terms| below 1e-5) and the CPU
     kernel's outputs (relative 1e-4, absolute 1e-5 near zero); the same
