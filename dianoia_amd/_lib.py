@@ -138,6 +138,7 @@ SIGNATURES = {
     "dnx_short_conv": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dnx_attention_max_keys": ([_i64], _i64),
     "dnx_attention": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p], _i32),
+    "dnx_attention_f6panel": ([_p] * 6 + [_i64] * 6 + [_p], _i32),
     "dnx_attention_rope": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _f32, _p], _i32),
     "dnx_add": ([_p, _p, _i64, _p], _i32),
     "dnx_copy": ([_p, _p, _i64, _p], _i32),

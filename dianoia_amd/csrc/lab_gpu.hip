@@ -1331,12 +1331,27 @@ bool run(const Cmd& c) {
       read_region(keys, 0, kvBytes);
       read_region(values, 0, kvBytes);
       if (gate >= 0) read_region(gate, 0, n * heads * 4);
-      const int rc = dnx_attention(
-          (const float*)dev_at(q, 0), (const float*)dev_at(keys, 0),
-          (const float*)dev_at(values, 0), gate >= 0 ? (const float*)dev_at(gate, 0) : nullptr,
-          (float*)dev_at(out, 0), position, n, heads, kvHeads, hd, window, gStream);
+      const float* gp = gate >= 0 ? (const float*)dev_at(gate, 0) : nullptr;
+      // With the panel of out when the next command is a prefill matmul of
+      // it (a chunk's o projection) and the attention's row combine runs.
+      bool panel = next_reads_panel(out, 0, n, heads * hd);
+      int rc = DNX_EINVAL;
+      if (panel) {
+        gPanel = PanelKey{};
+        rc = dnx_attention_f6panel((const float*)dev_at(q, 0), (const float*)dev_at(keys, 0),
+                                   (const float*)dev_at(values, 0), gp, (float*)dev_at(out, 0),
+                                   gWs, position, n, heads, kvHeads, hd, window, gStream);
+      }
+      if (rc == DNX_EINVAL) {
+        panel = false;
+        rc = dnx_attention((const float*)dev_at(q, 0), (const float*)dev_at(keys, 0),
+                           (const float*)dev_at(values, 0), gp, (float*)dev_at(out, 0), position,
+                           n, heads, kvHeads, hd, window, gStream);
+      }
       after_dispatch(kKindAttention);
+      if (panel && rc == DNX_OK) also_ran(kKindQuantize);
       wrote_region(out, 0, n * heads * hd * 4);
+      if (panel && rc == DNX_OK) gPanel = PanelKey{out, 0, n, heads * hd};
       return rc == DNX_OK;
     }
     case kOpCopy:

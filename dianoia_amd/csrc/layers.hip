@@ -1042,10 +1042,18 @@ attention_prefill_kernel(const float* __restrict__ q, const float* __restrict__ 
 // flight (the fewest of 2, 4, 8 covering the splits), dims lane + 64 i. Rows past the splits read zeros (the resource
 // ends with the row's last split), and dims past hd are computed but not
 // stored.
+//
+// With `panel` (hd a multiple of 32, at most 256), each row's values also go
+// into the fp6 activation panel of out ([tokens][heads * hd]) for the matmul
+// that reads it (a prefill chunk's o projection): the row through the wave's
+// LDS, then four lanes per 32-value block (panel4_lane, the panel
+// quantizer's bytes). Records of tokens past the last row are not written.
 template <int C>  // splits per load batch: 2, 4 or 8
 __global__ void __launch_bounds__(kThreads)
 attention_combine_rows_kernel(const float* __restrict__ ws, const float* __restrict__ gate,
-                              float* __restrict__ out, int heads, int hd, int splits, int rows) {
+                              float* __restrict__ out, int heads, int hd, int splits, int rows,
+                              uint8_t* __restrict__ panel) {
+  __shared__ __align__(16) float row_lds[kWaves][256];
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * kWaves + (threadIdx.x >> 6);   // token * heads + head
   if (r >= rows) return;
@@ -1077,10 +1085,29 @@ attention_combine_rows_kernel(const float* __restrict__ ws, const float* __restr
     }
   }
   const float g = gate != nullptr ? 1.0f / (1.0f + expf(-gate[r])) : 1.0f;
+  float* mine = row_lds[threadIdx.x >> 6];
 #pragma unroll
   for (int i = 0; i < kND; i++) {
     const int d = lane + 64 * i;
-    if (i < nd && d < hd) out[(size_t)r * hd + d] = gate != nullptr ? (acc[i] / l) * g : acc[i] / l;
+    const float o = gate != nullptr ? (acc[i] / l) * g : acc[i] / l;
+    if (i < nd && d < hd) {
+      out[(size_t)r * hd + d] = o;
+      mine[d] = o;
+    }
+  }
+  if (panel == nullptr) return;
+  // LDS operations of one wave execute in order; the fence keeps the
+  // compiler from moving the reads above the writes.
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  if (lane < hd / 8) {
+    const int token = r / heads, head = r - token * heads;
+    const int B = heads * hd / kBlock;
+    const int b = head * (hd / kBlock) + (lane >> 2);
+    const float4 v0 = *(const float4*)(mine + lane * 8);
+    const float4 v1 = *(const float4*)(mine + lane * 8 + 4);
+    panel4_lane(v0, v1, lane & 3, token % kTokens,
+                panel + ((size_t)(token / kTokens) * B + b) * kRec);
   }
 }
 
@@ -1405,13 +1432,20 @@ int64_t dnx_attention_max_keys(int64_t hd) {
   return (64 * 1024 / 4) - hd - kThreads - 4 - kWaves;
 }
 
-int dnx_attention(const float* q, const float* keys, const float* values, const float* gate,
-                  float* out, int64_t position, int64_t n, int64_t heads, int64_t kv_heads,
-                  int64_t hd, int64_t window, dnx_stream_t stream) {
+// The attention, and with `panel` the fp6 activation panel of out too (only
+// where the split matrix-core path and its row combine run; else DNX_EINVAL
+// before anything is launched).
+static int attention_impl(const float* q, const float* keys, const float* values,
+                          const float* gate, float* out, uint8_t* panel, int64_t position,
+                          int64_t n, int64_t heads, int64_t kv_heads, int64_t hd, int64_t window,
+                          dnx_stream_t stream) {
   if (n < 0 || position < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 ||
       hd <= 0 || hd % 4 != 0 || hd > 256 || kThreads % hd != 0 || window < 0 ||
       heads > 65535 || n > 65535 || position + n > 0x7fffffff || ((uintptr_t)keys & 15) ||
       ((uintptr_t)q & 15)) {
+    return DNX_EINVAL;
+  }
+  if (panel != nullptr && (hd % kBlock != 0 || ((uintptr_t)panel & 15) || n == 0)) {
     return DNX_EINVAL;
   }
   if (n == 0) return DNX_OK;
@@ -1449,6 +1483,7 @@ int dnx_attention(const float* q, const float* keys, const float* values, const 
       tps = tmax;
       pws = 0;
     }
+    if (panel != nullptr && !(splits > 1 && splits <= 64)) return DNX_EINVAL;
     float* ws = nullptr;
     if (splits > 1 && (ws = attention_workspace(pws)) == nullptr) return DNX_ENOMEM;
     const dim3 grid((unsigned)(heads / gw), (unsigned)by, (unsigned)splits);
@@ -1468,7 +1503,7 @@ int dnx_attention(const float* q, const float* keys, const float* values, const 
       auto k = splits <= 2 ? attention_combine_rows_kernel<2>
              : splits <= 4 ? attention_combine_rows_kernel<4> : attention_combine_rows_kernel<8>;
       hipLaunchKernelGGL(k, dim3((unsigned)((rows + kWaves - 1) / kWaves)), dim3(kThreads), 0, st,
-                         ws, gate, out, (int)heads, (int)hd, (int)splits, (int)rows);
+                         ws, gate, out, (int)heads, (int)hd, (int)splits, (int)rows, panel);
     } else if (splits > 1) {
       hipLaunchKernelGGL(attention_combine_kernel<false>, dim3((unsigned)heads, (unsigned)n),
                          dim3(kThreads), (size_t)splits * 4, st, ws, gate, out, (int)heads,
@@ -1476,6 +1511,7 @@ int dnx_attention(const float* q, const float* keys, const float* values, const 
     }
     return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
   }
+  if (panel != nullptr) return DNX_EINVAL;
   // Few (head, token) workgroups for many keys: split the keys.
   const int rc = attention_split(q, keys, values, gate, out, position, n, heads, kv_heads, hd,
                                  window, scale, stream, nullptr);
@@ -1487,6 +1523,22 @@ int dnx_attention(const float* q, const float* keys, const float* values, const 
                      (int)heads, (int)(kv_heads * hd), (int)(heads / kv_heads), (int)hd,
                      (int)window, scale);
   return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_attention(const float* q, const float* keys, const float* values, const float* gate,
+                  float* out, int64_t position, int64_t n, int64_t heads, int64_t kv_heads,
+                  int64_t hd, int64_t window, dnx_stream_t stream) {
+  return attention_impl(q, keys, values, gate, out, nullptr, position, n, heads, kv_heads, hd,
+                        window, stream);
+}
+
+int dnx_attention_f6panel(const float* q, const float* keys, const float* values,
+                          const float* gate, float* out, void* panel, int64_t position, int64_t n,
+                          int64_t heads, int64_t kv_heads, int64_t hd, int64_t window,
+                          dnx_stream_t stream) {
+  if (panel == nullptr) return DNX_EINVAL;
+  return attention_impl(q, keys, values, gate, out, (uint8_t*)panel, position, n, heads,
+                        kv_heads, hd, window, stream);
 }
 
 int dnx_add(const float* src, float* dst, int64_t count, dnx_stream_t stream) {

@@ -505,6 +505,16 @@ def attention(q, keys, values, gate, out, position: int, n: int, heads: int, kv_
            "dnx_attention")
 
 
+def attention_f6panel(q, keys, values, gate, out, panel, position: int, n: int, heads: int,
+                      kv_heads: int, hd: int, window: int = 0, stream=None) -> int:
+    """attention, and the fp6 panel of out; returns the status (DNX_EINVAL
+    where the call does not take the split path whose combine writes it)."""
+    _need("attention_f6panel", panel=(panel, f6_panel_bytes(n, heads * hd)))
+    return int(_lib.load().dnx_attention_f6panel(
+        _ptr(q), _ptr(keys), _ptr(values), None if gate is None else _ptr(gate), _ptr(out),
+        _ptr(panel), position, n, heads, kv_heads, hd, window, _stream(stream)))
+
+
 def attention_rope(q, keys, values, gate, out, position: int, heads: int, kv_heads: int, hd: int,
                    window: int, q_norm, k_norm, rope_row, eps: float, stream=None) -> None:
     """One decode token: head norm + RoPE of q and of keys[position], folded

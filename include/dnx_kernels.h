@@ -448,6 +448,19 @@ int64_t dnx_attention_max_keys(int64_t hd);
 int dnx_attention(const float* q, const float* keys, const float* values, const float* gate,
                   float* out, int64_t position, int64_t n, int64_t heads, int64_t kv_heads,
                   int64_t hd, int64_t window, dnx_stream_t stream);
+// dnx_attention, and the fp6 activation panel of out ([n][heads * hd], as
+// dnx_quantize_q8_f6panel would write it from out) into `panel` (16-byte
+// aligned, f6_panel_bytes(n, heads * hd) bytes) for the prefill matmul that
+// reads out (the o projection, lab_gpu commit peephole; no counterpart in
+// the reference). Only where the call takes the matrix-core path with its
+// keys split over 2..64 workgroups (the row combine writes the panel) and hd
+// is a multiple of 32; else DNX_EINVAL and nothing launched. Records of the
+// panel's padding tokens (past n in its last group of 32) are left as they
+// are: the chunk GEMM never reads them.
+int dnx_attention_f6panel(const float* q, const float* keys, const float* values,
+                          const float* gate, float* out, void* panel, int64_t position, int64_t n,
+                          int64_t heads, int64_t kv_heads, int64_t hd, int64_t window,
+                          dnx_stream_t stream);
 // One decode token's q and k head norms + RoPE folded into its attention
 // (gpu.dart:1157-1175: dnx_head_norm_rope of q with q_norm, of the token's
 // key row keys[position] with k_norm, both with the table row `rope`

@@ -523,3 +523,50 @@ def test_norm_panel_equals_norm_then_quantizer(gpu_ready, n, cols, add):
     D.quantize_q8_f6panel(o1, p1, n, cols)
     assert np.array_equal(bits(host(o2)), bits(host(o1)))
     assert np.array_equal(token_records(p2, n, cols), token_records(p1, n, cols))
+
+
+@pytest.mark.parametrize("n,position,heads,kv_heads,hd,gated,window",
+                         [(64, 256, 16, 8, 128, False, 0), (13, 600, 8, 2, 64, True, 0),
+                          (37, 300, 8, 8, 128, False, 128), (64, 900, 32, 8, 128, True, 0)])
+def test_attention_panel_equals_attention_then_quantizer(gpu_ready, n, position, heads,
+                                                         kv_heads, hd, gated, window):
+    """dnx_attention_f6panel on the split matrix-core path: out with
+    dnx_attention's bits, and every live token's panel records as
+    dnx_quantize_q8_f6panel makes them from out ([n][heads * hd])."""
+    rng = np.random.default_rng(n + position + hd)
+    cols, kv = heads * hd, kv_heads * hd
+    q = dev(rng.standard_normal((n, cols)).astype(np.float32))
+    keys = dev(rng.standard_normal((position + n, kv)).astype(np.float32))
+    values = dev(rng.standard_normal((position + n, kv)).astype(np.float32))
+    gate = dev(rng.standard_normal((n, heads)).astype(np.float32)) if gated else None
+    o1 = torch.full((n, cols), np.nan, device="cuda")
+    o2 = o1.clone()
+    p1 = torch.full((D.f6_panel_bytes(n, cols),), 0x7f, dtype=torch.uint8, device="cuda")
+    p2 = p1.clone()
+    D.attention(q, keys, values, gate, o1, position, n, heads, kv_heads, hd, window)
+    rc = D.attention_f6panel(q, keys, values, gate, o2, p2, position, n, heads, kv_heads, hd,
+                             window)
+    assert rc == 0
+    D.quantize_q8_f6panel(o1, p1, n, cols)
+    assert np.array_equal(bits(host(o2)), bits(host(o1)))
+    assert np.array_equal(token_records(p2, n, cols), token_records(p1, n, cols))
+
+
+@pytest.mark.parametrize("n,position,hd", [(8, 0, 128), (4, 500, 128), (16, 300, 32)])
+def test_attention_panel_refused_off_the_split_path(gpu_ready, n, position, hd):
+    """Where the attention does not run its split matrix-core path (a short
+    context, fewer than 8 tokens, hd not 64 or 128), dnx_attention_f6panel
+    returns DNX_EINVAL and launches nothing."""
+    heads, kv_heads = 8, 4
+    rng = np.random.default_rng(n + position)
+    cols, kv = heads * hd, kv_heads * hd
+    q = dev(rng.standard_normal((n, cols)).astype(np.float32))
+    keys = dev(rng.standard_normal((position + n, kv)).astype(np.float32))
+    values = dev(rng.standard_normal((position + n, kv)).astype(np.float32))
+    out = torch.full((n, cols), 7.0, device="cuda")
+    panel = torch.full((D.f6_panel_bytes(n, cols),), 0x7f, dtype=torch.uint8, device="cuda")
+    rc = D.attention_f6panel(q, keys, values, None, out, panel, position, n, heads, kv_heads, hd)
+    assert rc == -1
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
+    assert bool((panel == 0x7f).all())
