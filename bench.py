@@ -336,6 +336,12 @@ def bench_c3(torch, D, synth, timer, steps, warmup):
             D.quantize_q8_f6panel(xm, pm, m, K)
             D.gemm_q4_f6s(packed[i % copies], pm, ym, N, K, m)
 
+        # The GEMM alone, on a panel made before: what the route costs in a
+        # prefill chunk through the ABI, where the norm, SwiGLU or attention
+        # that produces x writes its panel (about 1 us more in that kernel).
+        def chunk_gemm(i, ym=ym, m=m, pm=pm):
+            D.gemm_q4_f6s(packed[i % copies], pm, ym, N, K, m)
+
         nbytes = q4_bytes(N, K) + m * K * 4 + m * N * 4
         if m <= 4:
             fn = lambda i, xm=xm, ym=ym, m=m: D.gemv_q4(ws[i % copies][0], ws[i % copies][1],  # noqa: E731
@@ -349,6 +355,7 @@ def bench_c3(torch, D, synth, timer, steps, warmup):
                          "kernel": kernel}
         if other is not None:
             sweep[str(m)][other[0]] = timer.time(other[1], n, 3)
+            sweep[str(m)]["gemm_on_producer_panel_ms"] = timer.time(chunk_gemm, n, 3)
     out["sweep_m"] = sweep
     return out
 
@@ -545,6 +552,13 @@ def bench_callers(torch, D, synth, timer, steps):
 
             cms = timer.time(chunk, reps, 3)
             out[key]["chunk_route_ms"] = cms
+
+            # The GEMM alone on that panel (a producer-written panel in an
+            # ABI prefill).
+            def chunk_gemm(i, packs=packs, pnl=pnl, y=y, rows=rows, cols=cols, n=n):
+                D.gemm_q4_f6s(packs[i % len(packs)], pnl, y, rows, cols, n)
+
+            out[key]["gemm_on_producer_panel_ms"] = timer.time(chunk_gemm, reps, 3)
             if 5 <= n <= 512:
                 out[key].update({"dnx_matmul_ms": ms, "ms": cms,
                                  "weight_gbps": nbytes / cms / 1e6,
