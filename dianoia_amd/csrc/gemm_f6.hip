@@ -1264,22 +1264,30 @@ int dnx_gemm_q4_f6s_multi(const void* const* packed, float* const* y, const int6
     p.y[k] = y[k];
     p.rows[k] = (int)rows[k];
   }
-  // 33+ tokens: two token groups per workgroup (one weight read for both:
-  // 64 tokens of 6144 x 2048 in 6.5 us against 7.9 with a workgroup per 32),
-  // unless that leaves fewer than 192 workgroups (a prefill chunk's 2048-row
-  // o and down projections: 64 of 256 CUs) while one per 32 tokens still
-  // fits one round of 256 (a workgroup fills its CU's registers: more than
-  // 256 workgroups run in two rounds; 375 tokens of 768 x 768 take 144
-  // workgroups in one round, not 288 in two).
-  const int64_t pairs = (n + 2 * kTokens - 1) / (2 * kTokens);
-  const int64_t singles = (n + kTokens - 1) / kTokens;
-  const bool two = n > kTokens && (groups * pairs >= 192 || groups * singles > 256);
-  const int per = two ? 2 * kTokens : kTokens;
+  // Token groups of 32 per workgroup (one weight read for all of them):
+  // the fewest that keep the launch to one round of 256 workgroups (a
+  // workgroup fills its CU's registers, so more run in two rounds: 64
+  // tokens of 6144 x 2048 take 192 workgroups of two groups in 6.5 us
+  // against 7.9 with 384 of one; 375 tokens of 768 x 768, 144 of two in 4.3
+  // us against 6.2 with 288 of one). Three groups fit the registers only
+  // with a wave's blocks all loaded at once (K up to 1024), and are taken
+  // only where they make one round (375 tokens of 1792 x 768: 5.8 us against
+  // 7.4 with two groups; two rounds of three groups were slower than two
+  // of two).
+  const int nb = (int)(cols / kBlock + kWaves - 1) / kWaves;
+  auto workgroups = [&](int64_t g) { return groups * ((n + g * kTokens - 1) / (g * kTokens)); };
+  int G = 1;
+  if (n > kTokens && workgroups(1) > 256) {
+    G = (n > 2 * kTokens && workgroups(2) > 256 && workgroups(3) <= 256 && nb <= 4) ? 3 : 2;
+  }
+  const int per = G * kTokens;
   const dim3 grid((unsigned)groups, (unsigned)((n + per - 1) / per));
   // A wave's blocks all loaded at once where they fit the ring (one round
-  // trip: 8 blocks of one token group, 4 of two), else a ring of 4.
-  const int nb = (int)(cols / kBlock + kWaves - 1) / kWaves;
-  if (two) {
+  // trip: 8 blocks of one token group, 4 of two or three), else a ring of 4.
+  if (G == 3) {
+    hipLaunchKernelGGL((gemm_f6s_kernel<3, 4, true>), grid, dim3(kThreads), 0,
+                       (hipStream_t)stream, p);
+  } else if (G == 2) {
     if (nb <= 4) {
       hipLaunchKernelGGL((gemm_f6s_kernel<2, 4, true>), grid, dim3(kThreads), 0,
                          (hipStream_t)stream, p);

@@ -312,7 +312,8 @@ def test_chunk_gemm_unit_scales_sum_blocks_exactly(gpu_ready, orc):
                                          (768, 768, 13), (97, 160, 5), (257, 2048, 32),
                                          (1152, 4320, 17), (100, 96, 64), (1792, 768, 48),
                                          (4304, 1152, 64), (768, 768, 375), (2048, 768, 130),
-                                         (300, 1568, 24), (2048, 2048, 64), (1024, 1536, 7)])
+                                         (300, 1568, 24), (2048, 2048, 64), (1024, 1536, 7),
+                                         (1792, 768, 375), (2304, 1024, 300)])
 def test_chunk_gemm_within_tolerance(gpu_ready, orc, rows, cols, n):
     """Against the exact products (error / sum|terms| below 1e-5) and the CPU
     kernel's outputs (relative 1e-4, absolute 1e-5 near zero); the same
@@ -332,6 +333,7 @@ def test_chunk_gemm_within_tolerance(gpu_ready, orc, rows, cols, n):
 
 @pytest.mark.parametrize("rows_list,cols,n", [((2048, 1024, 1024), 2048, 13),
                                               ((6144, 6144), 2048, 64),
+                                              ((1792, 256), 768, 375),
                                               ((97, 300, 33, 130), 160, 40),
                                               ((70,), 96, 5)])
 def test_chunk_gemm_segments_equal_separate_launches(gpu_ready, orc, rows_list, cols, n):
