@@ -296,11 +296,12 @@ int dnx_gemm_q8_f6p(const void* packed, const void* panel, float* y, int64_t row
 
 // The prefill chunk GEMM (lab_gemm_q4 mode 1, lab_native.c:1059-1080, at
 // the reference's prefill chunks of up to 64 tokens, lib/src/model.dart:91,
-// and other batches of a few hundred tokens) on prepacked weights: one launch over the whole K (no split partials, no
-// reduce launch), a workgroup per 32 rows and 64 tokens (more tokens, more
+// and other batches of a few hundred tokens) on prepacked weights: one
+// launch over the whole K (no split partials, no reduce launch), a
+// workgroup per 32 rows and 32 to 96 tokens (more tokens, more
 // workgroups); exact block dots, fp32 within 1e-4 relative (1e-5 absolute
 // near zero) of the CPU kernel. Deterministic (a fixed order of the K
-// parts).
+// parts, whatever the workgroup shape).
 int dnx_gemm_q4_f6s(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
                     int64_t n, dnx_stream_t stream);
 
