@@ -550,3 +550,50 @@ def test_q4_prefill_inputs_from_norm_add_norm_and_swiglu_bring_their_panel(gpu, 
     ok, rel, ab = within_tolerance(together["1"][:n * rows].reshape(n, rows),
                                    orc.gemm_q4(qs, sc, x1, n, threads=8, mode=1))
     assert ok, (rel, ab)
+
+
+@pytest.mark.parametrize("n", [200, 300])
+def test_q4_prefill_after_a_norm_with_or_without_its_panel(gpu, orc, n):
+    """An RMSNorm of up to 256 rows writes the next prefill matmul's panel;
+    one of more rows cannot (its kernel holds a row per workgroup only up
+    to 256 rows), so the matmul quantizes its input itself: either way one
+    command buffer gives the bits of one command per commit, within the bar
+    of the CPU kernels."""
+    rng = np.random.default_rng(47 + n)
+    cols, rows = 1024, 768
+    qs, sc = synth.q4_weights(rng, rows, cols)
+    gpu.upload("a", QuantMatrix.q4(qs, sc))
+    lib = gpu._lib
+    x = gpu._aux_buffer("pf_x", n * cols)
+    h = gpu._aux_buffer("pf_h", n * cols)
+    w = gpu._aux_buffer("pf_w", cols)
+    y = gpu._aux_buffer("pf_y", n * rows)
+    xs = synth.activations(rng, n, cols)
+    wv = (1 + rng.standard_normal(cols) * 0.1).astype(np.float32)
+    w.view(count=cols)[:] = wv
+
+    def run(together):
+        x.view(count=n * cols)[:] = xs.reshape(-1)
+        y.view(count=n * rows)[:] = np.nan
+        cmds = [lambda: lib.lab_gpu_enc_rms_norm(x.handle, 0, w.handle, 0, h.handle, 0, n, cols,
+                                                 1e-6, 0),
+                lambda: gpu._matrix("a").encode(lib, h.handle, y.handle, 0, n)]
+        if together:
+            lib.lab_gpu_begin()
+            for c in cmds:
+                c()
+            gpu._finish()
+        else:
+            for c in cmds:
+                lib.lab_gpu_begin()
+                c()
+                gpu._finish()
+        return y.view(count=n * rows).copy()
+
+    run(True)   # makes the prepack
+    apart, together = run(False), run(True)
+    assert np.array_equal(bits(apart), bits(together))
+    hn = orc.rms_norm(xs, wv, 1e-6)
+    ok, rel, ab = within_tolerance(together.reshape(n, rows),
+                                   orc.gemm_q4(qs, sc, hn, n, threads=8, mode=1))
+    assert ok, (rel, ab)
