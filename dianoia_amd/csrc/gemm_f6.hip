@@ -858,11 +858,13 @@ struct F6SParams {
 };
 
 // R: blocks in flight per wave (the register ring); kOnce: every wave has
-// at most R blocks, all loaded at the start (no refills).
-template <int G, int R, bool kOnce>
+// at most R blocks, all loaded at the start (no refills); RG: 32-row groups
+// per workgroup (seg_end counts workgroups).
+template <int G, int R, bool kOnce, int RG = 1>
 __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
-  constexpr int kOut = G * kTokens * 32;               // outputs of the workgroup
-  __shared__ __align__(16) float red[kWaves * kOut];   // each wave's sums, [wave][token][row]
+  constexpr int kTile = G * kTokens * 32;              // outputs of one row group
+  constexpr int kOut = RG * kTile;                     // outputs of the workgroup
+  __shared__ __align__(16) float red[kWaves * kOut];   // each wave's sums, [wave][group][token][row]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // This workgroup's matrix (uniform: scalar selects over the segments).
@@ -872,7 +874,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
   const int K = p.cols, B = K / kBlock, M = p.n;
   const int N = p.rows[seg];
   float* const yout = p.y[seg];
-  const int rg = blockIdx.x - (seg > 0 ? p.seg_end[seg - 1] : 0);   // 32-row group
+  const int rg = (blockIdx.x - (seg > 0 ? p.seg_end[seg - 1] : 0)) * RG;   // first 32-row group
   const int t0 = blockIdx.y * G;                       // first token group
   const int groups = (M + kTokens - 1) / kTokens;
   const int groups_n = (N + 31) >> 5;
@@ -882,15 +884,19 @@ __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
   // Block i of this wave is b = wave + 8 i; blocks past K read zeros (offset
   // past the resources), so their products vanish.
   struct Slot {
-    i32x4 w0, w1;       // B: the record halves of row lane % 32
-    i32x4 lo[G], hi[G]; // A: the token groups' lane records
+    i32x4 w0[RG], w1[RG]; // B: the record halves of row lane % 32 of each row group
+    i32x4 lo[G], hi[G];   // A: the token groups' lane records
   };
   auto load = [&](int i, Slot& sl) {
     const int b = wave + kWaves * i;
     const int ok = -(int)(b < B);
-    const int wb = ((rg * B + b) * kChunk & ok) | (~ok & -(1 << 30));
-    sl.w0 = dnx_raw_buffer_load_v4i32(rpk, wb + (lane & 31) * 16, 0, 0);
-    sl.w1 = dnx_raw_buffer_load_v4i32(rpk, wb + kChunk / 2 + (lane & 31) * 16, 0, 0);
+    // Row groups past the matrix read zeros (offsets past the resource).
+#pragma unroll
+    for (int j = 0; j < RG; j++) {
+      const int wb = (((rg + j) * B + b) * kChunk & ok) | (~ok & -(1 << 30));
+      sl.w0[j] = dnx_raw_buffer_load_v4i32(rpk, wb + (lane & 31) * 16, 0, 0);
+      sl.w1[j] = dnx_raw_buffer_load_v4i32(rpk, wb + kChunk / 2 + (lane & 31) * 16, 0, 0);
+    }
     // A lane whose token lies past n (a chunk of 8 tokens fills a quarter of
     // its 32-token group) reads zeros without a memory access.
 #pragma unroll
@@ -903,11 +909,13 @@ __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
     }
   };
 
-  v16f acc[G];
+  v16f acc[RG][G];
 #pragma unroll
-  for (int t = 0; t < G; t++)
+  for (int j = 0; j < RG; j++)
 #pragma unroll
-    for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
+    for (int t = 0; t < G; t++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[j][t][v] = 0.0f;
   const int nb = (B - wave + kWaves - 1) / kWaves;     // this wave's blocks
   Slot ring[R];
 #pragma unroll
@@ -916,21 +924,27 @@ __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
 #pragma unroll
     for (int r = 0; r < R; r++) {
       Slot& sl = ring[r];
-      asm volatile("" : "+v"(sl.w0), "+v"(sl.w1));
-      const v8i bq = {sl.w0[0], sl.w0[1], sl.w0[2], sl.w0[3], sl.w1[0], sl.w1[1], 0, 0};
-      const h4 bs = __builtin_bit_cast(h4, make_uint2((uint32_t)sl.w1[2], (uint32_t)sl.w1[3]));
 #pragma unroll
-      for (int t = 0; t < G; t++) {
-        i32x4 lo = sl.lo[t], hi = sl.hi[t];
-        asm volatile("" : "+v"(lo), "+v"(hi));
-        const v8i a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        const h4 as = __builtin_bit_cast(h4, make_uint2((uint32_t)hi[2], (uint32_t)hi[3]));
-        const v16f z = {};
-        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(as, bs, z, 0, 0, 0);
-        const v16f d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bq, z, 2, 2, 0, hi[3],
-                                                                       0, 130);
+      for (int j = 0; j < RG; j++) {
+        i32x4 w0 = sl.w0[j], w1 = sl.w1[j];
+        asm volatile("" : "+v"(w0), "+v"(w1));
+        const v8i bq = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], 0, 0};
+        const h4 bs = __builtin_bit_cast(h4, make_uint2((uint32_t)w1[2], (uint32_t)w1[3]));
 #pragma unroll
-        for (int v = 0; v < 16; v++) acc[t][v] = fmaf(d[v], sc[v], acc[t][v]);
+        for (int t = 0; t < G; t++) {
+          i32x4 lo = sl.lo[t], hi = sl.hi[t];
+          asm volatile("" : "+v"(lo), "+v"(hi));
+          const v8i a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          const h4 as = __builtin_bit_cast(h4, make_uint2((uint32_t)hi[2], (uint32_t)hi[3]));
+          const v16f z = {};
+          const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(as, bs, z, 0, 0, 0);
+          const v16f d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bq, z, 2, 2, 0,
+                                                                         hi[3], 0, 130);
+#pragma unroll
+          for (int v = 0; v < 16; v++) acc[j][t][v] = fmaf(d[v], sc[v], acc[j][t][v]);
+        }
+        // Two row groups: one group's MFMA results live at a time.
+        if constexpr (RG > 1) __builtin_amdgcn_sched_barrier(0);
       }
       if constexpr (!kOnce) load(i0 + r + R, sl);
     }
@@ -940,22 +954,25 @@ __global__ void __launch_bounds__(kThreads) gemm_f6s_kernel(F6SParams p) {
   // float4 of rows over the 8 waves in wave order and stores it.
   float* mine = red + wave * kOut;
 #pragma unroll
-  for (int t = 0; t < G; t++)
+  for (int j = 0; j < RG; j++)
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int m = t * kTokens + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      mine[m * 32 + (lane & 31)] = acc[t][v];
-    }
+    for (int t = 0; t < G; t++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int m = t * kTokens + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        mine[j * kTile + m * 32 + (lane & 31)] = acc[j][t][v];
+      }
   __syncthreads();
   for (int q = tid; q < kOut / 4; q += kThreads) {
-    const int m = q >> 3, c = (q & 7) * 4;
-    float4 o = *(const float4*)(red + m * 32 + c);
+    const int j = q / (kTile / 4), qq = q - j * (kTile / 4);
+    const int m = qq >> 3, c = (qq & 7) * 4;
+    float4 o = *(const float4*)(red + j * kTile + m * 32 + c);
 #pragma unroll
     for (int w = 1; w < kWaves; w++) {
-      const float4 e = *(const float4*)(red + w * kOut + m * 32 + c);
+      const float4 e = *(const float4*)(red + w * kOut + j * kTile + m * 32 + c);
       o = make_float4(o.x + e.x, o.y + e.y, o.z + e.z, o.w + e.w);
     }
-    const int r = rg * 32 + c, mt = t0 * kTokens + m;
+    const int r = (rg + j) * 32 + c, mt = t0 * kTokens + m;
     if (mt >= M || r >= N) continue;
     float* dst = yout + (size_t)mt * N + r;
     if (r + 3 < N && ((uintptr_t)dst & 15) == 0) {
@@ -1281,10 +1298,23 @@ int dnx_gemm_q4_f6s_multi(const void* const* packed, float* const* y, const int6
     G = (n > 2 * kTokens && workgroups(2) > 256 && workgroups(3) <= 256 && nb <= 4) ? 3 : 2;
   }
   const int per = G * kTokens;
-  const dim3 grid((unsigned)groups, (unsigned)((n + per - 1) / per));
+  // Two 32-row groups per workgroup where the launch would otherwise need
+  // more than one round (a chunk's gate and up: 384 workgroups of two token
+  // groups -> 192).
+  const int RG = (G == 2 && nb > 4 && workgroups(2) > 256) ? 2 : 1;
+  int64_t wgs = 0;
+  for (int k = 0; k < count; k++) {
+    wgs += ((rows[k] + 31) / 32 + RG - 1) / RG;
+    p.seg_end[k] = (int)wgs;
+  }
+  const dim3 grid((unsigned)wgs, (unsigned)((n + per - 1) / per));
   // A wave's blocks all loaded at once where they fit the ring (one round
   // trip: 8 blocks of one token group, 4 of two or three), else a ring of 4.
-  if (G == 3) {
+  if (RG == 2) {
+    // A ring of 3 (4 spills with two row groups' fragments).
+    hipLaunchKernelGGL((gemm_f6s_kernel<2, 3, false, 2>), grid, dim3(kThreads), 0,
+                       (hipStream_t)stream, p);
+  } else if (G == 3) {
     hipLaunchKernelGGL((gemm_f6s_kernel<3, 4, true>), grid, dim3(kThreads), 0,
                        (hipStream_t)stream, p);
   } else if (G == 2) {

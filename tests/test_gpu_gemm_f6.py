@@ -313,7 +313,7 @@ def test_chunk_gemm_unit_scales_sum_blocks_exactly(gpu_ready, orc):
                                          (1152, 4320, 17), (100, 96, 64), (1792, 768, 48),
                                          (4304, 1152, 64), (768, 768, 375), (2048, 768, 130),
                                          (300, 1568, 24), (2048, 2048, 64), (1024, 1536, 7),
-                                         (1792, 768, 375), (2304, 1024, 300)])
+                                         (1792, 768, 375), (2304, 1024, 300), (10000, 1536, 40)])
 def test_chunk_gemm_within_tolerance(gpu_ready, orc, rows, cols, n):
     """Against the exact products (error / sum|terms| below 1e-5) and the CPU
     kernel's outputs (relative 1e-4, absolute 1e-5 near zero); the same
