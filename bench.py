@@ -470,22 +470,69 @@ def bench_c4(torch, D, synth, timer, steps, warmup):
         D.quantize_q8_f6panel(h, pan2, M, 4320)
         D.gemm_q8_f6p(p2, pan2, y, 1152, 4320, M)
 
+    # The int8-MFMA route on prepacked operands: weights re-encoded once at
+    # load into fragment order, the activations quantized into the int8 panel.
+    i1 = torch.empty(D.q8_i8pack_bytes(4320, 1152), dtype=torch.uint8, device="cuda")
+    i2 = torch.empty(D.q8_i8pack_bytes(1152, 4320), dtype=torch.uint8, device="cuda")
+    ipan1 = torch.empty(D.i8_panel_bytes(M, 1152), dtype=torch.uint8, device="cuda")
+    ipan2 = torch.empty(D.i8_panel_bytes(M, 4320), dtype=torch.uint8, device="cuda")
+
+    def pack_i(i):
+        D.pack_q8_i8(q1, s1, i1, 4320, 1152)
+        D.pack_q8_i8(q2, s2, i2, 1152, 4320)
+
+    def fc1i_(i):
+        D.quantize_q8_i8panel(xd, ipan1, M, 1152)
+        D.gemm_q8_i8p(i1, ipan1, h, 4320, 1152, M)
+
+    def fc2i_(i):
+        D.quantize_q8_i8panel(h, ipan2, M, 4320)
+        D.gemm_q8_i8p(i2, ipan2, y, 1152, 4320, M)
+
+    def fc1i_gemm(i):
+        D.gemm_q8_i8p(i1, ipan1, h, 4320, 1152, M)
+
+    def fc2i_gemm(i):
+        D.gemm_q8_i8p(i2, ipan2, y, 1152, 4320, M)
+
     n = max(10, steps // 4)
     quant_w(0)
     pack_w(0)
-    means = timer.kernel_means([quant_w, fc1_, gelu_, fc2_, fc1f_, fc2f_, pack_w, fc1p_, fc2p_], n)
+    pack_i(0)
+    fc1i_(0)
+    fc2i_(0)
+    means = timer.kernel_means([quant_w, fc1_, gelu_, fc2_, fc1f_, fc2f_, pack_w, fc1p_, fc2p_,
+                                pack_i, fc1i_, fc2i_, fc1i_gemm, fc2i_gemm], n)
     qbytes = (4304 * 1152 * 2 + 4320 * 1152 + 4320 * 36 * 4) + (1152 * 4304 * 2 + 1152 * 4320 + 1152 * 135 * 4)
     ops = 2 * M * 4304 * 1152
+    # fc1_ms / fc2_ms: the route lab_gpu_enc_matmul_q8 takes at these shapes
+    # (dnx::matmul_uses_i8p: the int8 panel quantizer + the int8 GEMM on the
+    # weights' prepack, which the command buffer keeps per weight region).
     return {"quantize_weights_ms": means[0], "quantize_weights_gbps": qbytes / means[0] / 1e6,
-            "fc1_ms": means[1], "fc1_tops": ops / means[1] / 1e9, "gelu_ms": means[2],
-            "fc2_ms": means[3], "fc2_tops": ops / means[3] / 1e9,
-            "pair_tops": 2 * ops / (means[1] + means[2] + means[3]) / 1e9,
+            "fc1_ms": means[10], "fc1_tops": ops / means[10] / 1e9, "gelu_ms": means[2],
+            "fc2_ms": means[11], "fc2_tops": ops / means[11] / 1e9,
+            "pair_tops": 2 * ops / (means[10] + means[2] + means[11]) / 1e9,
+            "route": "lab_gpu_enc_matmul_q8: quantize_i8_panel_kernel + gemm_i8p_kernel "
+                     "(fc1: 160-row tiles, fc2: 128-row tiles in 3 K parts) on the prepack",
+            "int8_route": {"fc1_ms": means[1], "fc1_tops": ops / means[1] / 1e9,
+                           "fc2_ms": means[3], "fc2_tops": ops / means[3] / 1e9,
+                           "kernels": "quantize_kernel + gemm_kernel<Q8, 64, 64> (+ split-K "
+                                      "reduce for fc2): dnx_matmul_q8, no prepack"},
             "fp6_route": {"pack_weights_ms": means[6],
                           "fc1_ms": means[7], "fc1_tops": ops / means[7] / 1e9,
                           "fc2_ms": means[8], "fc2_tops": ops / means[8] / 1e9,
                           "pair_tops": 2 * ops / (means[7] + means[2] + means[8]) / 1e9,
                           "kernels": "quantize_f6_panel4_kernel + gemm_f6p_kernel<3, Q8> "
                                      "(scaled fp6 MFMA)"},
+            "i8_prepacked_route": {"pack_weights_ms": means[9],
+                                   "fc1_ms": means[10], "fc1_tops": ops / means[10] / 1e9,
+                                   "fc2_ms": means[11], "fc2_tops": ops / means[11] / 1e9,
+                                   "fc1_gemm_ms": means[12], "fc2_gemm_ms": means[13],
+                                   "pair_tops": 2 * ops / (means[10] + means[2] + means[11]) / 1e9,
+                                   "tile_rows": [D.gemm_q8_i8p_tile_rows(4320, 1152, M),
+                                                 D.gemm_q8_i8p_tile_rows(1152, 4320, M)],
+                                   "kernels": "quantize_i8_panel_kernel + gemm_i8p_kernel "
+                                              "(int8 MFMA, bf16 scale MFMA, prepacked operands)"},
             "float_inputs": {"fc1_ms": means[4], "fc1_tops": ops / means[4] / 1e9,
                              "fc2_ms": means[5], "fc2_tops": ops / means[5] / 1e9,
                              "kernel": "gemm_float_kernel (x in three exact bf16 pieces, "
@@ -564,6 +611,34 @@ def bench_callers(torch, D, synth, timer, steps):
                                  "weight_gbps": nbytes / cms / 1e6,
                                  "tops": 2 * n * rows * cols / cms / 1e9,
                                  "route": "lab_gpu_enc_matmul_q4: quantize_f6panel + gemm_f6s "
+                                          "(prepack)"})
+            del packs
+        if fmt == "q8" and int8 and n >= 128:
+            # The int8 GEMM on prepacked operands (weights re-encoded once
+            # into fragment order, x quantized into the int8 panel).
+            packs = [torch.empty((D.q8_i8pack_bytes(rows, cols),), dtype=torch.uint8,
+                                 device="cuda") for _ in range(len(ws))]
+            for w, pk in zip(ws, packs):
+                D.pack_q8_i8(w[0], w[1], pk, rows, cols)
+            pnl = torch.empty((D.i8_panel_bytes(n, cols),), dtype=torch.uint8, device="cuda")
+
+            def i8p(i, packs=packs, pnl=pnl, x=x, y=y, rows=rows, cols=cols, n=n):
+                D.quantize_q8_i8panel(x, pnl, n, cols)
+                D.gemm_q8_i8p(packs[i % len(packs)], pnl, y, rows, cols, n)
+
+            def i8p_gemm(i, packs=packs, pnl=pnl, y=y, rows=rows, cols=cols, n=n):
+                D.gemm_q8_i8p(packs[i % len(packs)], pnl, y, rows, cols, n)
+
+            ims = timer.time(i8p, reps, 3)
+            out[key]["i8p_route_ms"] = ims
+            out[key]["i8p_gemm_ms"] = timer.time(i8p_gemm, reps, 3)
+            out[key]["i8p_tile_rows"] = D.gemm_q8_i8p_tile_rows(rows, cols, n)
+            if rows * cols * n >= 1 << 32:
+                # The route lab_gpu_enc_matmul_q8 takes (dnx::matmul_uses_i8p).
+                out[key].update({"dnx_matmul_ms": ms, "ms": ims,
+                                 "weight_gbps": nbytes / ims / 1e6,
+                                 "tops": 2 * n * rows * cols / ims / 1e9,
+                                 "route": "lab_gpu_enc_matmul_q8: quantize_i8panel + gemm_i8p "
                                           "(prepack)"})
             del packs
         del ws

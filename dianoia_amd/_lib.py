@@ -122,6 +122,12 @@ SIGNATURES = {
     "dnx_q8_f6pack_bytes": ([_i64, _i64], _i64),
     "dnx_pack_q8_f6": ([_p, _p, _p, _i64, _i64, _p], _i32),
     "dnx_gemm_q8_f6p": ([_p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dnx_i8_panel_bytes": ([_i64, _i64], _i64),
+    "dnx_quantize_q8_i8panel": ([_p, _p, _i64, _i64, _p], _i32),
+    "dnx_q8_i8pack_bytes": ([_i64, _i64], _i64),
+    "dnx_pack_q8_i8": ([_p, _p, _p, _i64, _i64, _p], _i32),
+    "dnx_gemm_q8_i8p": ([_p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dnx_gemm_q8_i8p_tile_rows": ([_i64, _i64, _i64], _i32),
     "dnx_gemm_q4_f6p_noalloc_max_floats": ([], _i64),
     "dnx_matmul_workspace_bytes": ([_i64, _i64], _i64),
     "dnx_matmul_q8": ([_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p], _i32),

@@ -298,6 +298,65 @@ DNX_DEV void store_tile_sums(uint8_t* lds, const v16f* acc, int wave, int lane, 
   }
 }
 
+// The same sums with half the LDS (wide tiles whose two parities' partials
+// would not fit a CU's 160 KB): the parity-1 waves put their partials into
+// LDS, the parity-0 waves add theirs to them in place (the same sum,
+// parity 0 + parity 1), then every wave stores as above.
+template <int SN>
+constexpr int epilogue_lds_bytes_inplace() {
+  return kTileM * kTokens * (SN * 32 + 4) * 4;
+}
+
+template <int SN>
+DNX_DEV void store_tile_sums_inplace(uint8_t* lds, const v16f* acc, int wave, int lane, int m0,
+                                     int n0, int M, int N, float* out, bool vec) {
+  constexpr int BN = SN * 32;
+  constexpr int RS = BN + 4;
+  constexpr int C4 = BN / 4;
+  constexpr int PER = kTileM * kTokens * C4 / kWaves / 64;
+  static_assert(kTileM * kTokens * C4 % (kWaves * 64) == 0, "whole float4 per lane");
+  const int mg = wave & 3, kp = wave >> 2;
+  float* part = (float*)lds + (size_t)mg * kTokens * RS;
+  if (kp == 1) {
+#pragma unroll
+    for (int j = 0; j < SN; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int m = (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        part[m * RS + j * 32 + (lane & 31)] = acc[j][v];
+      }
+  }
+  __syncthreads();
+  if (kp == 0) {
+#pragma unroll
+    for (int j = 0; j < SN; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int m = (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        float* e = &part[m * RS + j * 32 + (lane & 31)];
+        *e = acc[j][v] + *e;
+      }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < PER; it++) {
+    const int idx = (wave * PER + it) * 64 + lane;
+    const int tok = idx / C4, c4 = idx - tok * C4;
+    const float4 o = *(const float4*)((const float*)lds + (size_t)tok * RS + c4 * 4);
+    const int m = m0 + tok, r = n0 + c4 * 4;
+    if (m >= M || r >= N) continue;
+    float* dst = out + (size_t)m * N + r;
+    if (vec) {
+      store_wt4(dst, o);
+    } else {
+      store_wt(dst, o.x);
+      if (r + 1 < N) store_wt(dst + 1, o.y);
+      if (r + 2 < N) store_wt(dst + 2, o.z);
+      if (r + 3 < N) store_wt(dst + 3, o.w);
+    }
+  }
+}
+
 struct F6Params {
   const uint8_t* qs;       // Q4 nibbles [rows][cols/2]
   const uint16_t* scales;  // fp16 bits [rows][cols/32]
@@ -1162,6 +1221,359 @@ int launch_f6p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t ro
   return DNX_OK;
 }
 
+// ----------------------------------- Q8 weights, prepacked, on int8 MFMA
+//
+// The Q8 GEMM at batch sizes (the vision encoder's fc1 / fc2 at 1024
+// tokens, lib/src/vision_encoder.dart:275-316; the product of lab_gemm_q8
+// mode 1, lab_native.c:1059-1080). One v_mfma_i32_32x32x32_i8 takes a whole
+// Q8 block (K = 32) and gives its exact int32 dot D_b, where the fp6 form
+// above needs two digits of each weight and two MFMAs per block. The scale
+// product s = sx * sw of a 32 x 32 tile comes from the bf16 outer-product
+// MFMA (three exact bf16 pieces of each scale, a_scale_half* /
+// b_scale_half* in common.h), and the fold per output and block is cvt +
+// fma: acc += float(D_b) * s, blocks in order.
+//
+// Both operands sit in HBM in fragment order, so a wave's loads (weights by
+// LDS DMA, activations straight into registers) need no rearranging: per 32
+// rows (or tokens) and block a 1536-byte record, [2 lane halves][32 rows][16
+// B] of int8 values (half 0: k = 0..15, half 1: k = 16..31), then [2 lane
+// halves][32 rows][8 B] of the scale's bf16 pieces. The workgroup, its
+// stages and the split of K follow gemm_f6p_kernel: 128 tokens x SN * 32
+// rows, wave w on the 32 tokens (w % 4) and the blocks of parity w / 4,
+// 8-block stages in two LDS buffers, the fold of one tile under the MFMAs of
+// the next.
+constexpr int kI8Rec = 1536;   // bytes per (32 rows or tokens, block)
+constexpr int kI8Sc = 1024;    // the scale pieces' offset in a record
+constexpr int kI8KB = 8;       // blocks per stage
+
+int64_t i8_panel_bytes(int64_t n, int64_t cols) {
+  return (n + kTokens - 1) / kTokens * (cols / kBlock) * kI8Rec;
+}
+
+// fp32 x [n][cols] -> the int8 panel, lab_quantize_q8 of each (token,
+// block) (the same xq and scale bits as dnx_quantize_q8), four lanes per
+// (token, block): lane j quantizes values 8j .. 8j+7 and stores them as 8
+// bytes of its token's half j / 2; lanes 0 and 1 store the scale's two
+// halves of bf16 pieces. All four lanes of a quad run every iteration
+// together (the block maximum comes by DPP over the quad). Tokens past n
+// get zero records.
+__global__ void __launch_bounds__(kPanelThreads) quantize_i8_panel_kernel(
+    const float* __restrict__ x, uint8_t* __restrict__ panel, int n, int cols, int groups) {
+  const int B = cols / kBlock;
+  const int64_t total = (int64_t)groups * B * kTokens * 4;  // whole quads
+  for (int64_t idx = (int64_t)blockIdx.x * kPanelThreads + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * kPanelThreads) {
+    const int j = (int)(idx & 3);
+    const int64_t q = idx >> 2;
+    const int r = (int)(q & (kTokens - 1));
+    const int64_t gb = q >> 5;
+    const int b = (int)(gb % B);
+    const int m = (int)(gb / B) * kTokens + r;
+    const bool live = m < n;
+    const float4* src = (const float4*)(x + (int64_t)(live ? m : 0) * cols + b * kBlock + 8 * j);
+    const float4 v0 = live ? src[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 v1 = live ? src[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float amax = fmaxf(max4abs(v0), max4abs(v1));
+    amax = fmaxf(amax, dppf<kQuadXor1>(amax));
+    amax = fmaxf(amax, dppf<kQuadXor2>(amax));
+    const float scale = q8_scale(amax);
+    const float inv = q8_inv(scale);
+    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i >> 2] |= ((uint32_t)quant1(vv[i], inv) & 0xffu) << (8 * (i & 3));
+    uint8_t* rec = panel + gb * kI8Rec;
+    *(uint2*)(rec + (j >> 1) * 512 + r * 16 + (j & 1) * 8) = make_uint2(w[0], w[1]);
+    if (j < 2) {
+      uint32_t p0, p1, p2;
+      split3_bf16(scale, p0, p1, p2);
+      *(uint2*)(rec + kI8Sc + j * 256 + r * 8) =
+          j == 0 ? a_scale_half0(p0, p1, p2) : a_scale_half1(p0, p1, p2);
+    }
+  }
+}
+
+// Q8 weights (int8 codes [rows][cols] + fp32 scales [rows][cols/32], the
+// engine's layout, lab_native.c:398-405) -> the int8 prepack, one thread per
+// (row, block) of the matrix padded to whole 32-row groups (rows past the
+// matrix: zero records).
+__global__ void __launch_bounds__(kPanelThreads) pack_q8_i8_kernel(
+    const int8_t* __restrict__ qs, const float* __restrict__ scales, uint8_t* __restrict__ out,
+    int rows, int B, int64_t count) {
+  for (int64_t i = (int64_t)blockIdx.x * kPanelThreads + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * kPanelThreads) {
+    const int r = (int)(i / B), b = (int)(i - (int64_t)r * B);
+    uint4 c0 = make_uint4(0u, 0u, 0u, 0u), c1 = c0;
+    float sw = 0.0f;
+    if (r < rows) {
+      c0 = *(const uint4*)(qs + i * 32);
+      c1 = *(const uint4*)(qs + i * 32 + 16);
+      sw = scales[i];
+    }
+    uint8_t* rec = out + ((int64_t)(r >> 5) * B + b) * kI8Rec;
+    *(uint4*)(rec + (r & 31) * 16) = c0;
+    *(uint4*)(rec + 512 + (r & 31) * 16) = c1;
+    uint32_t p0, p1, p2;
+    split3_bf16(sw, p0, p1, p2);
+    *(uint2*)(rec + kI8Sc + (r & 31) * 8) = b_scale_half0(p0, p1, p2);
+    *(uint2*)(rec + kI8Sc + 256 + (r & 31) * 8) = b_scale_half1(p0, p1, p2);
+  }
+}
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+typedef short s4_t __attribute__((ext_vector_type(4)));
+
+// The GEMM on the int8 prepack and panel. Stage s (kI8KB blocks of the
+// workgroup's SN row groups, 12 KB per group, contiguous in the prepack)
+// moves into one of two LDS buffers by DMA, issued one stage ahead; each
+// wave's activation records (16 + 8 bytes per lane and block) ride a
+// register ring of its parity's blocks one stage ahead. Waits and barriers
+// as in gemm_f6p_kernel. Blocks past this split's end and row groups past
+// the matrix read what lies there (finite codes and scales that meet zero
+// activations or are never stored); tokens past n read zeros.
+template <int SN>
+__global__ void __launch_bounds__(kThreads) gemm_i8p_kernel(F6PParams p) {
+  constexpr int BN = SN * 32;
+  constexpr int kGroupBytes = kI8KB * kI8Rec;
+  constexpr int kStage = SN * kGroupBytes;
+  constexpr int kPieces = kStage / 1024;
+  constexpr int kPiecesPerGroup = kGroupBytes / 1024;
+  static_assert(kGroupBytes % 1024 == 0, "whole 1 KB pieces per row group");
+  constexpr int kRingP = kI8KB / 2;
+  // Up to 4 row groups both parities' partials fit beside nothing else;
+  // wider tiles add them in place.
+  constexpr bool kInplace = epilogue_lds_bytes<SN>() > 160 * 1024;
+  constexpr int kEpi = kInplace ? epilogue_lds_bytes_inplace<SN>() : epilogue_lds_bytes<SN>();
+  constexpr int kLds = 2 * kStage > kEpi ? 2 * kStage : kEpi;
+  static_assert(kLds <= 160 * 1024, "a CU's LDS");
+  __shared__ __align__(16) uint8_t lds[kLds];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int mg = wave & 3, kp = wave >> 2;
+  const int K = p.cols, B = K / kBlock, M = p.n, N = p.rows;
+  const int groups_n = (N + 31) >> 5;
+
+  const int i = blockIdx.x;
+  const int t = (p.tiles % 8 == 0) ? (i % 8) * (p.tiles / 8) + i / 8 : i;
+  const int tm = t % p.tiles_m, tn = t / p.tiles_m;
+  const int n0 = tn * BN, g0 = tn * SN;
+  const int groups = (M + kTokens - 1) / kTokens;
+  const int g = tm * kTileM + mg;
+  const int b_begin = blockIdx.y * p.split_blocks;
+  const int b_end = min(B, b_begin + p.split_blocks);
+  const int stages = (b_end - b_begin + kI8KB - 1) / kI8KB;
+  const i32x4 rpanel = buffer_rsrc(p.panel, (uint32_t)((size_t)groups * B * kI8Rec));
+  const i32x4 rpk = buffer_rsrc(p.packed, (uint32_t)((size_t)groups_n * B * kI8Rec));
+  const uint32_t lds0 = lds_address(lds);
+
+  auto dma_w = [&](int s, int buf) {
+    const int b0 = b_begin + s * kI8KB;
+#pragma unroll
+    for (int e = 0; e < (kPieces + kWaves - 1) / kWaves; e++) {
+      const int c = wave + kWaves * e;
+      if (c < kPieces) {
+        const int j = c / kPiecesPerGroup, q = c - j * kPiecesPerGroup;
+        buffer_load16_to_lds(rpk, lds0 + buf * kStage + j * kGroupBytes + q * 1024,
+                             ((g0 + j) * B + b0) * kI8Rec + q * 1024 + lane * 16);
+      }
+    }
+  };
+
+  // This lane's bytes of a record: row lane % 32's values of its lane half,
+  // and that half's scale pieces.
+  const int off_c = (lane >> 5) * 512 + (lane & 31) * 16;
+  const int off_s = kI8Sc + (lane >> 5) * 256 + (lane & 31) * 8;
+  const bool live = g < groups;
+  auto load_a = [&](int b, i32x4& c, i32x2& s) {
+    const int ok = -(int)(live & (b < b_end));
+    const int base = (((g * B + b) * kI8Rec) & ok) | (~ok & -(1 << 20));
+    c = dnx_raw_buffer_load_v4i32(rpanel, base + off_c, 0, 0);
+    s = dnx_raw_buffer_load_v2i32(rpanel, base + off_s, 0, 0);
+  };
+
+  v16f acc[SN];
+#pragma unroll
+  for (int j = 0; j < SN; j++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[j][v] = 0.0f;
+  v16i_t pd;
+  v16f ps;
+#pragma unroll
+  for (int v = 0; v < 16; v++) {
+    pd[v] = 0;
+    ps[v] = 0.0f;
+  }
+  auto fold = [&](int j) {
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[j][v] = fmaf((float)pd[v], ps[v], acc[j][v]);
+  };
+  struct BFrag {
+    uint4 c;
+    uint2 s;
+  };
+  auto read_b = [&](const uint8_t* sbase, int kb, int j) {
+    const uint8_t* q = sbase + (j * kI8KB + kb) * kI8Rec;
+    BFrag f;
+    f.c = *(const uint4*)(q + off_c);
+    f.s = *(const uint2*)(q + off_s);
+    return f;
+  };
+  // One block of K for the SN tiles; `nb` holds tile 0 of this block on
+  // entry and tile 0 of block kb_next on exit. The order inside a tile is
+  // pinned (MFMAs, the next fragment's LDS reads, the previous tile's fold).
+  auto compute = [&](const uint8_t* sbase, int kb, int kb_next, i32x4 c, i32x2 s, BFrag& nb) {
+    asm volatile("" : "+v"(c), "+v"(s));
+    const v4i_t a = __builtin_bit_cast(v4i_t, c);
+    const s4_t as = __builtin_bit_cast(s4_t, s);
+    BFrag cur = nb;
+#pragma unroll
+    for (int j = 0; j < SN; j++) {
+      const v4i_t bq = __builtin_bit_cast(v4i_t, cur.c);
+      const s4_t bs = __builtin_bit_cast(s4_t, cur.s);
+      const v16f z = {};
+      const v16i_t zi = {};
+      const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(as, bs, z, 0, 0, 0);
+      const v16i_t d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, zi, 0, 0, 0);
+      if (j + 1 < SN) {
+        cur = read_b(sbase, kb, j + 1);
+      } else {
+        nb = read_b(sbase, kb_next, 0);
+      }
+      fold(j > 0 ? j - 1 : SN - 1);
+      pd = d;
+      ps = sc;
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);    // the MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);    // next fragment
+      __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);   // previous fold
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  i32x4 rc[kRingP];
+  i32x2 rs[kRingP];
+  dma_w(0, 0);
+#pragma unroll
+  for (int r = 0; r < kRingP; r++) load_a(b_begin + kp + 2 * r, rc[r], rs[r]);
+  if (stages > 1) dma_w(1, 1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int s = 0; s < stages; s++) {
+    const int buf = s & 1;
+    if (s >= 1 && s + 1 < stages) dma_w(s + 1, buf ^ 1);
+    const uint8_t* sbase = lds + buf * kStage;
+    const int b0 = b_begin + s * kI8KB;
+    BFrag nb = read_b(sbase, kp, 0);
+#pragma unroll
+    for (int r = 0; r < kRingP; r++) {
+      const int kb = kp + 2 * r;
+      compute(sbase, kb, min(kb + 2, kI8KB - 1), rc[r], rs[r], nb);
+      load_a(b0 + kb + 2 * kRingP, rc[r], rs[r]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // This wave's W(s + 1) has landed: only the 2 * kRingP ring refills of
+    // this stage were issued after it.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2 * kRingP));
+    __syncthreads();
+  }
+  fold(SN - 1);
+  float* out = p.part ? p.part + (size_t)blockIdx.y * M * N : p.y;
+  if constexpr (kInplace) {
+    store_tile_sums_inplace<SN>(lds, acc, wave, lane, tm * kTileM * kTokens, n0, M, N, out,
+                                p.vec != 0);
+  } else {
+    store_tile_sums<SN>(lds, acc, wave, lane, tm * kTileM * kTokens, n0, M, N, out, p.vec != 0);
+  }
+}
+
+// Blocks per K part of the int8 prepacked GEMM: as f6_split_blocks (a split
+// only at 128 tiles or fewer, the most parts that fit one round of 256
+// workgroups), in whole kI8KB-block stages.
+int i8_split_blocks(int tiles, int B) {
+  int splits = 1;
+  if (tiles <= 128) {
+    splits = 256 / tiles;
+    const int max_splits = (B + kI8KB - 1) / kI8KB;
+    if (splits > max_splits) splits = max_splits;
+  }
+  const int per = (B + splits - 1) / splits;
+  return (per + kI8KB - 1) / kI8KB * kI8KB;
+}
+
+bool i8p_shape_ok(int64_t rows, int64_t cols, int64_t n) {
+  if (rows <= 0 || cols <= 0 || n <= 0 || cols % kBlock != 0) return false;
+  return (rows + 31) / 32 * (cols / kBlock) * kI8Rec < (1ll << 31) &&
+         i8_panel_bytes(n, cols) < (1ll << 31) && n * rows < (1ll << 31);
+}
+
+// Row groups per workgroup tile (3, 4 or 5: 96 to 160 rows) of the int8
+// prepacked GEMM: the tile width whose launch takes the least time by a
+// model of its measured costs. A workgroup fills its CU, so a launch runs
+// in rounds of 256 workgroups; per round the slowest CU runs SN tiles of
+// its split's blocks (about 100 ns per tile and block pair per SIMD, two
+// waves of opposite block parity), plus about 2 us of prologue and
+// epilogue; a K split adds the reduce launch (about 1 us plus its partials
+// read at 4 TB/s). The vision encoder's fc1 (4320 x 1152 at 1024 tokens)
+// takes 160-row tiles (216 workgroups, one round, against 360 in two);
+// fc2 (1152 x 4320) 128-row tiles (72 tiles in three K parts).
+int i8p_groups(int64_t rows, int64_t cols, int64_t n) {
+  const int64_t tm = (n + kTileM * kTokens - 1) / (kTileM * kTokens);
+  const int64_t gn = (rows + 31) / 32;
+  const int B = (int)(cols / kBlock);
+  int best = 3;
+  double best_ns = 0.0;
+  for (int sn = 3; sn <= 5; sn++) {
+    const int64_t tiles = tm * ((gn + sn - 1) / sn);
+    if (tiles > 0x7fffffff) continue;
+    const int per = i8_split_blocks((int)tiles, B);
+    const int64_t splits = (B + per - 1) / per;
+    const int64_t rounds = (tiles * splits + 255) / 256;
+    double ns = (double)rounds * ((double)sn * ((per + 1) / 2) * 200.0 + 2000.0);
+    if (splits > 1) ns += 1000.0 + (double)splits * (double)n * (double)rows / 1000.0;
+    if (sn == 3 || ns < best_ns) {
+      best = sn;
+      best_ns = ns;
+    }
+  }
+  return best;
+}
+
+template <int SN>
+int launch_i8p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t rows, int64_t cols,
+               int64_t n, hipStream_t stream) {
+  constexpr int BN = SN * 32;
+  F6PParams p{};
+  p.packed = packed;
+  p.panel = panel;
+  p.y = y;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.n = (int)n;
+  p.tiles_m = (int)((n + kTileM * kTokens - 1) / (kTileM * kTokens));
+  p.tiles = p.tiles_m * (int)((rows + BN - 1) / BN);
+  const int B = (int)(cols / kBlock);
+  p.split_blocks = i8_split_blocks(p.tiles, B);
+  const int splits = (B + p.split_blocks - 1) / p.split_blocks;
+  const int64_t count = n * rows;
+  p.part = nullptr;
+  if (splits > 1) {
+    p.part = part_workspace((size_t)splits * count * 4);
+    if (p.part == nullptr) return DNX_ENOMEM;
+  }
+  p.vec = (rows % 4 == 0 && ((uintptr_t)(p.part ? (void*)p.part : (void*)y) & 15) == 0) ? 1 : 0;
+  hipLaunchKernelGGL((gemm_i8p_kernel<SN>), dim3((unsigned)p.tiles, (unsigned)splits),
+                     dim3(kThreads), 0, stream, p);
+  if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+  if (splits > 1) {
+    const int64_t blocks = (count + 255) / 256;
+    hipLaunchKernelGGL(f6_splitk_reduce_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)),
+                       dim3(256), 0, stream, p.part, y, count, splits);
+    if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
+  }
+  return DNX_OK;
+}
+
 int panel_grid(int64_t total) {
   const int64_t blocks = (total + kPanelThreads - 1) / kPanelThreads;
   return (int)(blocks < 16384 ? blocks : 16384);
@@ -1364,6 +1776,62 @@ int dnx_gemm_q8_f6p(const void* packed, const void* panel, float* y, int64_t row
   }
   return launch_f6p<3, true>((const uint8_t*)packed, (const uint8_t*)panel, y, rows, cols, n,
                              (hipStream_t)stream);
+}
+
+int64_t dnx_i8_panel_bytes(int64_t n, int64_t cols) {
+  if (n <= 0 || cols <= 0 || cols % kBlock != 0) return -1;
+  return i8_panel_bytes(n, cols);
+}
+
+int dnx_quantize_q8_i8panel(const float* x, void* panel, int64_t n, int64_t cols,
+                            dnx_stream_t stream) {
+  if (n <= 0 || cols <= 0 || cols % kBlock != 0 || ((uintptr_t)x & 15) ||
+      ((uintptr_t)panel & 15) || i8_panel_bytes(n, cols) >= (1ll << 31)) {
+    return DNX_EINVAL;
+  }
+  const int groups = (int)((n + kTokens - 1) / kTokens);
+  const int64_t total = (int64_t)groups * (cols / kBlock) * kTokens * 4;
+  hipLaunchKernelGGL(quantize_i8_panel_kernel, dim3(panel_grid(total)), dim3(kPanelThreads), 0,
+                     (hipStream_t)stream, x, (uint8_t*)panel, (int)n, (int)cols, groups);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int64_t dnx_q8_i8pack_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0 || cols % kBlock != 0) return -1;
+  return (rows + 31) / 32 * (cols / kBlock) * kI8Rec;
+}
+
+int dnx_pack_q8_i8(const int8_t* qs, const float* scales, void* packed, int64_t rows,
+                   int64_t cols, dnx_stream_t stream) {
+  if (rows <= 0 || cols <= 0 || cols % kBlock != 0 || rows >= (1ll << 31) ||
+      ((uintptr_t)qs & 15) || ((uintptr_t)scales & 3) || ((uintptr_t)packed & 15)) {
+    return DNX_EINVAL;
+  }
+  const int64_t count = (rows + 31) / 32 * 32 * (cols / kBlock);
+  hipLaunchKernelGGL(pack_q8_i8_kernel, dim3(panel_grid(count)), dim3(kPanelThreads), 0,
+                     (hipStream_t)stream, qs, scales, (uint8_t*)packed, (int)rows,
+                     (int)(cols / kBlock), count);
+  return hipGetLastError() == hipSuccess ? DNX_OK : DNX_ELAUNCH;
+}
+
+int dnx_gemm_q8_i8p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
+                    int64_t n, dnx_stream_t stream) {
+  if (!i8p_shape_ok(rows, cols, n) || ((uintptr_t)panel & 15) || ((uintptr_t)packed & 15) ||
+      ((uintptr_t)y & 3)) {
+    return DNX_EINVAL;
+  }
+  const uint8_t* pk = (const uint8_t*)packed;
+  const uint8_t* pn = (const uint8_t*)panel;
+  switch (i8p_groups(rows, cols, n)) {
+    case 5: return launch_i8p<5>(pk, pn, y, rows, cols, n, (hipStream_t)stream);
+    case 4: return launch_i8p<4>(pk, pn, y, rows, cols, n, (hipStream_t)stream);
+    default: return launch_i8p<3>(pk, pn, y, rows, cols, n, (hipStream_t)stream);
+  }
+}
+
+int dnx_gemm_q8_i8p_tile_rows(int64_t rows, int64_t cols, int64_t n) {
+  if (!i8p_shape_ok(rows, cols, n)) return -1;
+  return 32 * i8p_groups(rows, cols, n);
 }
 
 int64_t dnx_gemm_q4_f6p_noalloc_max_floats(void) { return (int64_t)kScratchFloats; }

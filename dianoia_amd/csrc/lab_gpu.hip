@@ -145,6 +145,7 @@ int64_t gWsBytes = 0;
 // may have written x since).
 struct PanelKey {
   int64_t handle = -1, offset = 0, n = 0, cols = 0;
+  bool i8 = false;  // the int8 GEMM's panel (dnx_quantize_q8_i8panel), else the fp6 one
 };
 PanelKey gPanel;
 void* gArgmaxWs = nullptr;
@@ -431,12 +432,13 @@ void record(Op op, std::initializer_list<int64_t> args) {
   gCmds.push_back(c);
 }
 
-// Prepacked copies of Q4 weight matrices for the fp6 GEMMs (the routes of
+// Prepacked copies of weight matrices: Q4 for the fp6 GEMMs (the routes of
 // prefill chunks, dnx::matmul_uses_f6_chunk, and of large prefill shapes,
-// dnx::matmul_uses_f6). The host cannot change weights once used
+// dnx::matmul_uses_f6), Q8 for the int8 GEMM on prepacked operands (large
+// batches, dnx::matmul_uses_i8p). The host cannot change weights once used
 // (use_as_weights), so a matrix region is re-encoded on its first such
-// matmul into the GEMMs' tile-major layout (dnx_pack_q4_f6), and later
-// prefills of it run on the prepack. A command that writes into the region
+// matmul into the GEMM's layout (dnx_pack_q4_f6, dnx_pack_q8_i8), and later
+// products of it run on the prepack. A command that writes into the region
 // (a load-time quantizer, a copy, a GGUF split run again into the same
 // buffer) marks the prepack stale, and the next matmul re-makes it. The
 // copy's memory is reserved when the command is encoded (no allocation
@@ -448,35 +450,39 @@ struct Prepack {
   int64_t handle, qs_off, sc_off, rows, cols;
   void* dev;
   bool packed;
+  bool q8;
 };
 std::vector<Prepack> gPrepacks;
 
-Prepack* find_prepack(int64_t h, int64_t qs_off, int64_t sc_off, int64_t rows, int64_t cols) {
+Prepack* find_prepack(int64_t h, int64_t qs_off, int64_t sc_off, int64_t rows, int64_t cols,
+                      bool q8 = false) {
   for (Prepack& p : gPrepacks) {
     if (p.handle == h && p.qs_off == qs_off && p.sc_off == sc_off && p.rows == rows &&
-        p.cols == cols) {
+        p.cols == cols && p.q8 == q8) {
       return &p;
     }
   }
   return nullptr;
 }
 
-// At encode time: the prepack a Q4 int8-input matmul of this shape will use,
-// reserved now. Where the device has no memory for it (or the copy would
-// pass the GEMM's 2 GB operand limit) the command runs on the engine layout.
-void reserve_prepack(int64_t h, int64_t qs_off, int64_t sc_off, int64_t rows, int64_t cols) {
-  if (find_prepack(h, qs_off, sc_off, rows, cols) != nullptr) return;
-  const int64_t bytes = dnx_q4_f6pack_bytes(rows, cols);
+// At encode time: the prepack an int8-input matmul of this shape will use
+// (Q4, or Q8 with q8), reserved now. Where the device has no memory for it
+// (or the copy would pass the GEMM's 2 GB operand limit) the command runs on
+// the engine layout.
+void reserve_prepack(int64_t h, int64_t qs_off, int64_t sc_off, int64_t rows, int64_t cols,
+                     bool q8 = false) {
+  if (find_prepack(h, qs_off, sc_off, rows, cols, q8) != nullptr) return;
+  const int64_t bytes = q8 ? dnx_q8_i8pack_bytes(rows, cols) : dnx_q4_f6pack_bytes(rows, cols);
   void* dev = nullptr;
   if (bytes <= 0 || bytes >= (1ll << 31) || hipMalloc(&dev, (size_t)bytes) != hipSuccess) return;
-  gPrepacks.push_back({h, qs_off, sc_off, rows, cols, dev, false});
+  gPrepacks.push_back({h, qs_off, sc_off, rows, cols, dev, false, q8});
 }
 
 void stale_prepacks(int64_t h, int64_t offset, int64_t bytes) {
   for (Prepack& p : gPrepacks) {
     if (p.handle != h || !p.packed) continue;
-    const int64_t qs_end = p.qs_off + p.rows * (p.cols / 2);
-    const int64_t sc_end = p.sc_off + p.rows * (p.cols / 32) * 2;
+    const int64_t qs_end = p.qs_off + p.rows * (p.q8 ? p.cols : p.cols / 2);
+    const int64_t sc_end = p.sc_off + p.rows * (p.cols / 32) * (p.q8 ? 4 : 2);
     const int64_t end = offset + bytes;
     if ((offset < qs_end && p.qs_off < end) || (offset < sc_end && p.sc_off < end)) {
       p.packed = false;
@@ -511,26 +517,32 @@ void free_prepacks(int64_t h) {
 int ensure_packed(Prepack& pp, int64_t w, int64_t qsOff, int64_t scOff, int64_t rows,
                   int64_t cols) {
   if (pp.packed) return DNX_OK;
-  const int rc = dnx_pack_q4_f6((const uint8_t*)dev_at(w, qsOff),
-                                (const uint16_t*)dev_at(w, scOff), pp.dev, rows, cols,
-                                (dnx_stream_t)gStream);
+  const int rc = pp.q8 ? dnx_pack_q8_i8((const int8_t*)dev_at(w, qsOff),
+                                        (const float*)dev_at(w, scOff), pp.dev, rows, cols,
+                                        (dnx_stream_t)gStream)
+                       : dnx_pack_q4_f6((const uint8_t*)dev_at(w, qsOff),
+                                        (const uint16_t*)dev_at(w, scOff), pp.dev, rows, cols,
+                                        (dnx_stream_t)gStream);
   if (rc != DNX_OK) return rc;
   after_dispatch(kKindQuantizeWeights);
   pp.packed = true;
   return DNX_OK;
 }
 
-// The activation panel of x in the workspace, unless it is there already.
-int ensure_panel(int64_t xh, int64_t xOff, int64_t n, int64_t cols) {
-  if (gPanel.handle == xh && gPanel.offset == xOff && gPanel.n == n && gPanel.cols == cols) {
+// The activation panel of x in the workspace (the fp6 GEMMs', or with i8
+// the int8 GEMM's), unless it is there already.
+int ensure_panel(int64_t xh, int64_t xOff, int64_t n, int64_t cols, bool i8 = false) {
+  if (gPanel.handle == xh && gPanel.offset == xOff && gPanel.n == n && gPanel.cols == cols &&
+      gPanel.i8 == i8) {
     return DNX_OK;
   }
   gPanel = PanelKey{};
-  const int rc = dnx_quantize_q8_f6panel((const float*)dev_at(xh, xOff), gWs, n, cols,
-                                         (dnx_stream_t)gStream);
+  const float* x = (const float*)dev_at(xh, xOff);
+  const int rc = i8 ? dnx_quantize_q8_i8panel(x, gWs, n, cols, (dnx_stream_t)gStream)
+                    : dnx_quantize_q8_f6panel(x, gWs, n, cols, (dnx_stream_t)gStream);
   if (rc != DNX_OK) return rc;
   after_dispatch(kKindQuantize);
-  gPanel = PanelKey{xh, xOff, n, cols};
+  gPanel = PanelKey{xh, xOff, n, cols, i8};
   return DNX_OK;
 }
 
@@ -539,8 +551,13 @@ int run_matmul_prepacked(Prepack& pp, int64_t w, int64_t qsOff, int64_t scOff, i
   auto s = (dnx_stream_t)gStream;
   int rc = ensure_packed(pp, w, qsOff, scOff, rows, cols);
   if (rc != DNX_OK) return rc;
-  rc = ensure_panel(xh, xOff, n, cols);
+  rc = ensure_panel(xh, xOff, n, cols, pp.q8);
   if (rc != DNX_OK) return rc;
+  if (pp.q8) {
+    rc = dnx_gemm_q8_i8p(pp.dev, gWs, y, rows, cols, n, s);
+    if (rc == DNX_OK) after_dispatch(kKindGemmQ8I8);
+    return rc;
+  }
   rc = dnx::matmul_uses_f6_chunk(true, rows, cols, n)
            ? dnx_gemm_q4_f6s(pp.dev, gWs, y, rows, cols, n, s)
            : dnx_gemm_q4_f6p(pp.dev, gWs, y, rows, cols, n, s);
@@ -549,8 +566,9 @@ int run_matmul_prepacked(Prepack& pp, int64_t w, int64_t qsOff, int64_t scOff, i
 }
 
 // The matmul of one recorded command, on the product route of
-// matmul_route.h (the same as dnx_matmul_q8 / _q4), with the fp6 GEMM on a
-// prepacked copy of the weights where one is reserved.
+// matmul_route.h (the same as dnx_matmul_q8 / _q4), with the fp6 GEMMs (Q4)
+// or the int8 GEMM on prepacked operands (Q8) on a prepacked copy of the
+// weights where one is reserved.
 bool run_matmul(const Cmd& c, bool q4) {
   const int64_t w = c.a[0], qsOff = c.a[1], scOff = c.a[2], x = c.a[3], xOff = c.a[4];
   const int64_t y = c.a[5], yOff = c.a[6], rows = c.a[7], cols = c.a[8], n = c.a[9];
@@ -559,18 +577,22 @@ bool run_matmul(const Cmd& c, bool q4) {
   // The panel quantizer reads x 16 bytes at a time: an x at a 4-byte offset
   // that is not 16-byte aligned takes the route without the prepack.
   const bool x16 = ((uintptr_t)dev_at(x, xOff) & 15) == 0;
-  Prepack* pp = q4 && c.int8_inputs && x16 &&
-                        (dnx::matmul_uses_f6(true, rows, cols, n) ||
-                         dnx::matmul_uses_f6_chunk(true, rows, cols, n))
-                    ? find_prepack(w, qsOff, scOff, rows, cols)
-                    : nullptr;
+  Prepack* pp = nullptr;
+  if (c.int8_inputs && x16) {
+    if (q4 && (dnx::matmul_uses_f6(true, rows, cols, n) ||
+               dnx::matmul_uses_f6_chunk(true, rows, cols, n))) {
+      pp = find_prepack(w, qsOff, scOff, rows, cols);
+    } else if (!q4 && dnx::matmul_uses_i8p(false, rows, cols, n)) {
+      pp = find_prepack(w, qsOff, scOff, rows, cols, true);
+    }
+  }
   if (pp != nullptr) {
     const int rc = run_matmul_prepacked(*pp, w, qsOff, scOff, x, xOff, (float*)dev_at(y, yOff),
                                         rows, cols, n);
     wrote_region(y, yOff, n * rows * 4);
     if (rc != DNX_OK) {
-      LOG("matmul q4 %ldx%ld n=%ld (prepacked fp6) failed (%d)\n", (long)rows, (long)cols,
-          (long)n, rc);
+      LOG("matmul %s %ldx%ld n=%ld (prepacked) failed (%d)\n", q4 ? "q4" : "q8", (long)rows,
+          (long)cols, (long)n, rc);
     }
     return rc == DNX_OK;
   }
@@ -1777,6 +1799,9 @@ static void enc_matmul(Op op, int64_t w, int64_t qsOffset, int64_t scalesOffset,
       (dnx::matmul_uses_f6(true, rows, cols, n) ||
        dnx::matmul_uses_f6_chunk(true, rows, cols, n))) {
     reserve_prepack(w, qsOffset, scalesOffset, rows, cols);
+  }
+  if (!q4 && gInt8Inputs && dnx::matmul_uses_i8p(false, rows, cols, n)) {
+    reserve_prepack(w, qsOffset, scalesOffset, rows, cols, true);
   }
   record(op, {w, qsOffset, scalesOffset, x, xOffset, y, yOffset, rows, cols, n});
 }

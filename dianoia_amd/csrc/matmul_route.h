@@ -41,6 +41,20 @@ inline bool matmul_uses_f6_chunk(bool q4, int64_t rows, int64_t cols, int64_t n)
   return q4 && n >= 5 && n <= 512 && !matmul_uses_f6(q4, rows, cols, n);
 }
 
+// Q8 batches of large products (the vision encoder's fc1 / fc2 and
+// projector at its 1024 patches, lib/src/vision_encoder.dart:275-316) with a
+// prepacked copy of the weights (the lab_gpu_* command buffer keeps one per
+// weight region): the int8 panel quantizer + dnx_gemm_q8_i8p. Measured
+// against quantize + int8 GEMM (graph-timed, weights rotated past the
+// MALL): 1152 x 4320 and 4320 x 1152 at 1024 tokens 32.8 / 27.1 against
+// 42.6 / 30.1 us, 4096 x 4096 at 1024 tokens 57.2 against 80.9, 1024 x 1024
+// at 4096 tokens 26.5 against 30.7; below 2^32 multiply-adds the int8
+// GEMM's smaller tiles win or tie (1024 x 1024 at 1024 tokens: 20.6 against
+// 14.7; 2048 x 4096 at 256 tokens: 22.4 against 22.2).
+inline bool matmul_uses_i8p(bool q4, int64_t rows, int64_t cols, int64_t n) {
+  return !q4 && n >= 128 && rows * cols * n >= (1ll << 32);
+}
+
 // Device bytes a route needs for its quantized activations: int8 xq and fp32
 // block scales (each 256-byte aligned), or the fp6 activation panel.
 inline int64_t matmul_workspace_bytes(int64_t cols, int64_t n) {

@@ -421,6 +421,45 @@ def gemm_q8_f6p(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> 
                                        _stream(stream)), "dnx_gemm_q8_f6p")
 
 
+def i8_panel_bytes(n: int, cols: int) -> int:
+    return int(_lib.load().dnx_i8_panel_bytes(n, cols))
+
+
+def quantize_q8_i8panel(x, panel, n: int, cols: int, stream=None) -> None:
+    """fp32 x -> the int8 GEMM's activation panel (lab_quantize_q8's bits)."""
+    _need("quantize_q8_i8panel", x=(x, n * cols * 4), panel=(panel, i8_panel_bytes(n, cols)))
+    _check(_lib.load().dnx_quantize_q8_i8panel(_ptr(x), _ptr(panel), n, cols, _stream(stream)),
+           "dnx_quantize_q8_i8panel")
+
+
+def q8_i8pack_bytes(rows: int, cols: int) -> int:
+    return int(_lib.load().dnx_q8_i8pack_bytes(rows, cols))
+
+
+def pack_q8_i8(qs, scales, packed, rows: int, cols: int, stream=None) -> None:
+    """Load-time re-encoding of Q8 weights for the int8 GEMM (dnx_gemm_q8_i8p)."""
+    _need("pack_q8_i8",
+          qs=(qs, rows * cols),
+          scales=(scales, rows * (cols // 32) * 4),
+          packed=(packed, q8_i8pack_bytes(rows, cols)))
+    _check(_lib.load().dnx_pack_q8_i8(_ptr(qs), _ptr(scales), _ptr(packed), rows, cols,
+                                      _stream(stream)), "dnx_pack_q8_i8")
+
+
+def gemm_q8_i8p(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> None:
+    _need("gemm_q8_i8p",
+          packed=(packed, q8_i8pack_bytes(rows, cols)),
+          panel=(panel, i8_panel_bytes(n, cols)),
+          y=(y, n * rows * 4))
+    _check(_lib.load().dnx_gemm_q8_i8p(_ptr(packed), _ptr(panel), _ptr(y), rows, cols, n,
+                                       _stream(stream)), "dnx_gemm_q8_i8p")
+
+
+def gemm_q8_i8p_tile_rows(rows: int, cols: int, n: int) -> int:
+    """Weight rows per workgroup tile dnx_gemm_q8_i8p takes for a shape."""
+    return int(_lib.load().dnx_gemm_q8_i8p_tile_rows(rows, cols, n))
+
+
 def argmax_workspace(n: int, device="cuda") -> torch.Tensor:
     nbytes = int(_lib.load().dnx_argmax_workspace_bytes(n))
     return torch.empty(nbytes, dtype=torch.uint8, device=device)

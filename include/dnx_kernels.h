@@ -294,6 +294,30 @@ int dnx_pack_q8_f6(const int8_t* qs, const float* scales, void* packed, int64_t 
 int dnx_gemm_q8_f6p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
                     int64_t n, dnx_stream_t stream);
 
+// The Q8 GEMM (lab_gemm_q8 mode 1, lab_native.c:553-579, :1059-1080; the
+// vision encoder's fc1 / fc2, lib/src/vision_encoder.dart:275-316) on the
+// int8 matrix cores, one v_mfma_i32_32x32x32_i8 per block (exact int32 block
+// dots), the scale products from a bf16 outer-product MFMA, cvt + fma per
+// output and block. Both operands in fragment order, 1536 bytes per 32 rows
+// (or tokens) and block: the weights re-encoded once at load
+// (dnx_q8_i8pack_bytes, dnx_pack_q8_i8), the activations quantized from fp32
+// x with lab_quantize_q8's xq and scale bits (dnx_i8_panel_bytes,
+// dnx_quantize_q8_i8panel; x and the panel 16-byte aligned). fp32 within
+// 1e-4 relative (1e-5 absolute near zero) of the CPU kernel; the scales are
+// applied as by dnx_gemm_q8. Tiles of 128 tokens x 96, 128 or 160 rows
+// (dnx_gemm_q8_i8p_tile_rows: the choice for a shape, -1 for a shape the
+// GEMM refuses); at 128 tiles or fewer K is split, the partials added in a
+// fixed order in a second launch.
+int64_t dnx_i8_panel_bytes(int64_t n, int64_t cols);
+int dnx_quantize_q8_i8panel(const float* x, void* panel, int64_t n, int64_t cols,
+                            dnx_stream_t stream);
+int64_t dnx_q8_i8pack_bytes(int64_t rows, int64_t cols);
+int dnx_pack_q8_i8(const int8_t* qs, const float* scales, void* packed, int64_t rows,
+                   int64_t cols, dnx_stream_t stream);
+int dnx_gemm_q8_i8p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
+                    int64_t n, dnx_stream_t stream);
+int dnx_gemm_q8_i8p_tile_rows(int64_t rows, int64_t cols, int64_t n);
+
 // The prefill chunk GEMM (lab_gemm_q4 mode 1, lab_native.c:1059-1080, at
 // the reference's prefill chunks of up to 64 tokens, lib/src/model.dart:91,
 // and other batches of a few hundred tokens) on prepacked weights: one

@@ -417,6 +417,71 @@ def test_q4_prefill_follows_gpu_writes_into_the_weights(gpu, orc, n):
         assert ok, (k, rel, ab)
 
 
+def test_q8_batch_follows_gpu_writes_into_the_weights(gpu, orc):
+    """A Q8 batch of 2^32+ multiply-adds (1024 x 1024 at 4096 tokens) runs on
+    a prepacked copy of the weights made at its first use (the int8 GEMM on
+    prepacked operands). A GPU command that writes other weights into the
+    same region (lab_gpu_enc_quantize_q8 again) makes the next product use
+    them, and writing the first weights back returns to those: each product
+    against the CPU kernel on the weights of the moment."""
+    from dianoia_amd import _lib
+    rows, cols, n = 1024, 1024, 4096
+    assert _lib.load().dnx_gemm_q8_i8p_tile_rows(rows, cols, n) > 0
+    rng = np.random.default_rng(23)
+    ws = [(rng.standard_normal((rows, cols)) * 0.02).astype(np.float32) for _ in range(2)]
+    gpu.upload_f32("w", ws[0], rows, cols, fmt="q8")
+    lib, m = gpu._lib, gpu._matrix("w")
+    src = gpu._aux_buffer("w_src", rows * cols)
+    xs = synth.activations(rng, n, cols)
+    for step, k in enumerate((0, 1, 0)):
+        if step > 0:   # weights k into the same region, on the GPU
+            src.view(count=rows * cols)[:] = ws[k].reshape(-1)
+            lib.lab_gpu_begin()
+            lib.lab_gpu_enc_quantize_q8(src.handle, 0, m.buffer, m.qs, m.buffer, m.scales,
+                                        rows, cols, cols)
+            gpu._finish()
+        y = np.zeros(n * rows, np.float32)
+        gpu.apply("w", xs, y, n)
+        qs, sc = orc.quantize_q8(ws[k])
+        ok, rel, ab = within_tolerance(y.reshape(n, rows), orc.gemm_q8(qs, sc, xs, n, threads=8,
+                                                                         mode=1))
+        assert ok, (k, rel, ab)
+
+
+def test_q8_batch_and_q4_chunk_of_one_x_keep_their_own_panels(gpu, orc):
+    """One x read in one command buffer by a Q8 batch (the int8 panel) and
+    then by Q4 prefill matmuls (the fp6 panel), then Q8 again: each route
+    quantizes x into its own panel format (the workspace's panel is keyed
+    by format as well as by x), every product against the CPU kernel."""
+    rng = np.random.default_rng(29)
+    n, cols = 256, 4096
+    q8r, q4r = 4096, 1024
+    q8qs, q8sc = synth.q8_weights(rng, q8r, cols)
+    q8sc = (q8sc / np.float32(16)).astype(np.float16).astype(np.float32)
+    q4qs, q4sc = synth.q4_weights(rng, q4r, cols)
+    gpu.upload("a", QuantMatrix.q8(q8qs, q8sc))
+    gpu.upload("b", QuantMatrix.q4(q4qs, q4sc))
+    lib = gpu._lib
+    x = gpu._aux_buffer("x_fmt", n * cols)
+    ya = gpu._aux_buffer("y_a", n * q8r)
+    yb = gpu._aux_buffer("y_b", n * q4r)
+    ya2 = gpu._aux_buffer("y_a2", n * q8r)
+    xs = synth.activations(rng, n, cols)
+    x.view(count=n * cols)[:] = xs.reshape(-1)
+    ref8 = orc.gemm_q8(q8qs, q8sc, xs, n, threads=8, mode=1)
+    ref4 = orc.gemm_q4(q4qs, q4sc, xs, n, threads=8, mode=1)
+    for rep in range(2):   # the first pass also makes the prepacks
+        lib.lab_gpu_begin()
+        gpu._matrix("a").encode(lib, x.handle, ya.handle, 0, n)
+        gpu._matrix("b").encode(lib, x.handle, yb.handle, 0, n)
+        gpu._matrix("a").encode(lib, x.handle, ya2.handle, 0, n)
+        gpu._finish()
+        for name, y, ref, rows in (("a", ya, ref8, q8r), ("b", yb, ref4, q4r),
+                                   ("a2", ya2, ref8, q8r)):
+            ok, rel, ab = within_tolerance(y.view(count=n * rows).reshape(n, rows), ref)
+            assert ok, (rep, name, rel, ab)
+
+
 def test_q4_prefill_matmuls_of_one_x_share_its_panel(gpu, orc):
     """Prepacked Q4 prefill matmuls that read the same x in one command
     buffer (a chunk's q, k, v or gate, up) quantize x once and share the
