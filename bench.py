@@ -1100,6 +1100,27 @@ def pmc_workload(torch, D, synth, reps):
         D.gemm_q8_f6p(p1, pan4, h4, 4320, 1152, 1024)
     torch.cuda.synchronize()
     print("pmc: config 4 int8 inputs done", file=sys.stderr, flush=True)
+    # The ABI's route for both projections: the int8 GEMM on prepacked
+    # operands (fc1 on 160-row tiles, fc2 on 128-row tiles in three K parts).
+    _, fc2, _ = synth.config4()
+    w2 = dev(torch, fc2)
+    q2 = torch.empty((1152, 4320), dtype=torch.int8, device="cuda")
+    s2 = torch.empty((1152, 135), device="cuda")
+    D.quantize_q8_bf16(w2, q2, s2, 1152, 4304, 4320)
+    i1 = torch.empty(D.q8_i8pack_bytes(4320, 1152), dtype=torch.uint8, device="cuda")
+    i2 = torch.empty(D.q8_i8pack_bytes(1152, 4320), dtype=torch.uint8, device="cuda")
+    D.pack_q8_i8(q1, s1, i1, 4320, 1152)
+    D.pack_q8_i8(q2, s2, i2, 1152, 4320)
+    ip1 = torch.empty(D.i8_panel_bytes(1024, 1152), dtype=torch.uint8, device="cuda")
+    ip2 = torch.empty(D.i8_panel_bytes(1024, 4320), dtype=torch.uint8, device="cuda")
+    D.quantize_q8_i8panel(x4d, ip1, 1024, 1152)
+    D.quantize_q8_i8panel(h4, ip2, 1024, 4320)
+    y4 = torch.empty((1024, 1152), device="cuda")
+    for i in range(reps):
+        D.gemm_q8_i8p(i1, ip1, h4, 4320, 1152, 1024)
+        D.gemm_q8_i8p(i2, ip2, y4, 1152, 4320, 1024)
+    torch.cuda.synchronize()
+    print("pmc: config 4 int8 prepacked route done", file=sys.stderr, flush=True)
 
     # Causal prefill attention, 512 tokens (the layer steps' matrix-core kernel).
     gen = torch.Generator(device="cuda").manual_seed(6)
@@ -1127,6 +1148,10 @@ MFMA_KERNELS = {
                                          2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
     "gemm_f6p_kernel<3, true>": ("c4 fc1 Q8 GEMM M=1024 (fp6, prepacked)",
                                  2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
+    "gemm_i8p_kernel<5>": ("c4 fc1 Q8 GEMM M=1024 (int8 MFMA, prepacked: the ABI's route)",
+                           2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
+    "gemm_i8p_kernel<4>": ("c4 fc2 Q8 GEMM M=1024 (int8 MFMA, prepacked, 3 K parts)",
+                           2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
     "gemm_float_kernel<false, 4>": ("c4 fc1 float inputs M=1024 (bf16)",
                                     2 * 1024 * 4320 * 1152, 2500.0),
     "attention_prefill_kernel<128, 4>": ("prefill attention 512 tokens, 32/8 heads, hd 128",
