@@ -307,7 +307,10 @@ int dnx_gemm_q8_f6p(const void* packed, const void* panel, float* y, int64_t row
 // applied as by dnx_gemm_q8. Tiles of 128 tokens x 96, 128 or 160 rows
 // (dnx_gemm_q8_i8p_tile_rows: the choice for a shape, -1 for a shape the
 // GEMM refuses); at 128 tiles or fewer K is split, the partials added in a
-// fixed order in a second launch.
+// fixed order in a second launch, from the fp6 GEMMs' library-owned
+// workspace, grown on demand (the first call at a larger split shape
+// allocates, so it must not be captured into a graph; calls share it:
+// serialize them on one GPU).
 int64_t dnx_i8_panel_bytes(int64_t n, int64_t cols);
 int dnx_quantize_q8_i8panel(const float* x, void* panel, int64_t n, int64_t cols,
                             dnx_stream_t stream);
