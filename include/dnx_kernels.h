@@ -248,8 +248,8 @@ int dnx_gemm_q4_panel(const uint8_t* qs, const uint16_t* scales, const void* pan
 // writes it from fp32 x [n][cols] (lab_quantize_q8's values, bit-exact with
 // dnx_quantize_q8; x 16-byte aligned), dnx_pack_f6panel from xq int8
 // [n][cols] + xsc fp32 [n][cols/32]. The products are within 1e-4 relative
-// of the CPU kernels; the same inputs always give the same bits. With fewer
-// than 192 workgroup tiles (128 tokens x 96 rows) K is split across
+// of the CPU kernels; the same inputs always give the same bits. With 128
+// workgroup tiles (128 tokens x 96 rows) or fewer K is split across
 // workgroups and summed in a fixed order in a library-owned workspace,
 // allocated on the first such call at a larger shape (so that call must not
 // be captured into a graph).
