@@ -513,7 +513,8 @@ def bench_c4(torch, D, synth, timer, steps, warmup):
             "fc2_ms": means[11], "fc2_tops": ops / means[11] / 1e9,
             "pair_tops": 2 * ops / (means[10] + means[2] + means[11]) / 1e9,
             "route": "lab_gpu_enc_matmul_q8: quantize_i8_panel_kernel + gemm_i8p_kernel "
-                     "(fc1: 160-row tiles, fc2: 128-row tiles in 3 K parts) on the prepack",
+                     "(fc1: 128 x 160 tiles, fc2: 128 x 128 tiles in 3 K parts) on the "
+                     "prepack",
             "int8_route": {"fc1_ms": means[1], "fc1_tops": ops / means[1] / 1e9,
                            "fc2_ms": means[3], "fc2_tops": ops / means[3] / 1e9,
                            "kernels": "quantize_kernel + gemm_kernel<Q8, 64, 64> (+ split-K "
@@ -529,8 +530,8 @@ def bench_c4(torch, D, synth, timer, steps, warmup):
                                    "fc2_ms": means[11], "fc2_tops": ops / means[11] / 1e9,
                                    "fc1_gemm_ms": means[12], "fc2_gemm_ms": means[13],
                                    "pair_tops": 2 * ops / (means[10] + means[2] + means[11]) / 1e9,
-                                   "tile_rows": [D.gemm_q8_i8p_tile_rows(4320, 1152, M),
-                                                 D.gemm_q8_i8p_tile_rows(1152, 4320, M)],
+                                   "tiles_rows_tokens": [D.gemm_q8_i8p_tile(4320, 1152, M),
+                                                         D.gemm_q8_i8p_tile(1152, 4320, M)],
                                    "kernels": "quantize_i8_panel_kernel + gemm_i8p_kernel "
                                               "(int8 MFMA, bf16 scale MFMA, prepacked operands)"},
             "float_inputs": {"fc1_ms": means[4], "fc1_tops": ops / means[4] / 1e9,
@@ -632,8 +633,8 @@ def bench_callers(torch, D, synth, timer, steps):
             ims = timer.time(i8p, reps, 3)
             out[key]["i8p_route_ms"] = ims
             out[key]["i8p_gemm_ms"] = timer.time(i8p_gemm, reps, 3)
-            out[key]["i8p_tile_rows"] = D.gemm_q8_i8p_tile_rows(rows, cols, n)
-            if rows * cols * n >= 1 << 32:
+            out[key]["i8p_tile_rows_tokens"] = D.gemm_q8_i8p_tile(rows, cols, n)
+            if n >= 256 and rows * cols * n >= 1 << 28:
                 # The route lab_gpu_enc_matmul_q8 takes (dnx::matmul_uses_i8p).
                 out[key].update({"dnx_matmul_ms": ms, "ms": ims,
                                  "weight_gbps": nbytes / ims / 1e6,
@@ -1148,10 +1149,10 @@ MFMA_KERNELS = {
                                          2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
     "gemm_f6p_kernel<3, true>": ("c4 fc1 Q8 GEMM M=1024 (fp6, prepacked)",
                                  2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
-    "gemm_i8p_kernel<5>": ("c4 fc1 Q8 GEMM M=1024 (int8 MFMA, prepacked: the ABI's route)",
-                           2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
-    "gemm_i8p_kernel<4>": ("c4 fc2 Q8 GEMM M=1024 (int8 MFMA, prepacked, 3 K parts)",
-                           2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
+    "gemm_i8p_kernel<5, 4>": ("c4 fc1 Q8 GEMM M=1024 (int8 MFMA, prepacked: the ABI's route)",
+                              2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
+    "gemm_i8p_kernel<4, 4>": ("c4 fc2 Q8 GEMM M=1024 (int8 MFMA, prepacked, 3 K parts)",
+                              2 * 1024 * 4304 * 1152, I8_PEAK_TOPS),
     "gemm_float_kernel<false, 4>": ("c4 fc1 float inputs M=1024 (bf16)",
                                     2 * 1024 * 4320 * 1152, 2500.0),
     "attention_prefill_kernel<128, 4>": ("prefill attention 512 tokens, 32/8 heads, hd 128",

@@ -127,7 +127,7 @@ SIGNATURES = {
     "dnx_q8_i8pack_bytes": ([_i64, _i64], _i64),
     "dnx_pack_q8_i8": ([_p, _p, _p, _i64, _i64, _p], _i32),
     "dnx_gemm_q8_i8p": ([_p, _p, _p, _i64, _i64, _i64, _p], _i32),
-    "dnx_gemm_q8_i8p_tile_rows": ([_i64, _i64, _i64], _i32),
+    "dnx_gemm_q8_i8p_tile": ([_i64, _i64, _i64, _p, _p], _i32),
     "dnx_gemm_q4_f6p_noalloc_max_floats": ([], _i64),
     "dnx_matmul_workspace_bytes": ([_i64, _i64], _i64),
     "dnx_matmul_q8": ([_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p], _i32),

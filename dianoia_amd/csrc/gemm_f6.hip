@@ -357,6 +357,58 @@ DNX_DEV void store_tile_sums_inplace(uint8_t* lds, const v16f* acc, int wave, in
   }
 }
 
+// The sums of a 64-token tile whose 8 waves are 2 token groups x 4 block
+// parities: every wave puts its partials into LDS, then every wave adds the
+// four parities (in parity order) for 1/8 of the outputs and stores them as
+// store_tile_sums does.
+template <int SN>
+constexpr int epilogue_lds_bytes_par4() {
+  return 2 * 4 * kTokens * (SN * 32 + 4) * 4;
+}
+
+template <int SN>
+DNX_DEV void store_tile_sums_par4(uint8_t* lds, const v16f* acc, int wave, int lane, int m0,
+                                  int n0, int M, int N, float* out, bool vec) {
+  constexpr int BN = SN * 32;
+  constexpr int RS = BN + 4;
+  constexpr int C4 = BN / 4;
+  constexpr int PER = 2 * kTokens * C4 / kWaves / 64;
+  static_assert(2 * kTokens * C4 % (kWaves * 64) == 0, "whole float4 per lane");
+  const int mg = wave & 1, kp = wave >> 1;
+  float* part = (float*)lds + (size_t)(mg * 4 + kp) * kTokens * RS;
+#pragma unroll
+  for (int j = 0; j < SN; j++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int m = (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+      part[m * RS + j * 32 + (lane & 31)] = acc[j][v];
+    }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < PER; it++) {
+    const int idx = (wave * PER + it) * 64 + lane;
+    const int tok = idx / C4, c4 = idx - tok * C4;
+    const float* e = (const float*)lds + ((size_t)((tok >> 5) * 4) * kTokens + (tok & 31)) * RS + c4 * 4;
+    float4 o = *(const float4*)e;
+#pragma unroll
+    for (int q = 1; q < 4; q++) {
+      const float4 b = *(const float4*)(e + q * kTokens * RS);
+      o = make_float4(o.x + b.x, o.y + b.y, o.z + b.z, o.w + b.w);
+    }
+    const int m = m0 + tok, r = n0 + c4 * 4;
+    if (m >= M || r >= N) continue;
+    float* dst = out + (size_t)m * N + r;
+    if (vec) {
+      store_wt4(dst, o);
+    } else {
+      store_wt(dst, o.x);
+      if (r + 1 < N) store_wt(dst + 1, o.y);
+      if (r + 2 < N) store_wt(dst + 2, o.z);
+      if (r + 3 < N) store_wt(dst + 3, o.w);
+    }
+  }
+}
+
 struct F6Params {
   const uint8_t* qs;       // Q4 nibbles [rows][cols/2]
   const uint16_t* scales;  // fp16 bits [rows][cols/32]
@@ -1332,26 +1384,30 @@ typedef short s4_t __attribute__((ext_vector_type(4)));
 // as in gemm_f6p_kernel. Blocks past this split's end and row groups past
 // the matrix read what lies there (finite codes and scales that meet zero
 // activations or are never stored); tokens past n read zeros.
-template <int SN>
+template <int SN, int kTM>
 __global__ void __launch_bounds__(kThreads) gemm_i8p_kernel(F6PParams p) {
+  static_assert(kTM == 4 || kTM == 2, "128- or 64-token tiles");
+  constexpr int kPar = kWaves / kTM;                 // block parities
   constexpr int BN = SN * 32;
   constexpr int kGroupBytes = kI8KB * kI8Rec;
   constexpr int kStage = SN * kGroupBytes;
   constexpr int kPieces = kStage / 1024;
   constexpr int kPiecesPerGroup = kGroupBytes / 1024;
   static_assert(kGroupBytes % 1024 == 0, "whole 1 KB pieces per row group");
-  constexpr int kRingP = kI8KB / 2;
-  // Up to 4 row groups both parities' partials fit beside nothing else;
-  // wider tiles add them in place.
-  constexpr bool kInplace = epilogue_lds_bytes<SN>() > 160 * 1024;
-  constexpr int kEpi = kInplace ? epilogue_lds_bytes_inplace<SN>() : epilogue_lds_bytes<SN>();
+  constexpr int kRingP = kI8KB / kPar;
+  // 128-token tiles: up to 4 row groups both parities' partials fit beside
+  // nothing else, wider tiles add them in place; 64-token tiles keep their
+  // four parities' partials.
+  constexpr bool kInplace = kTM == 4 && epilogue_lds_bytes<SN>() > 160 * 1024;
+  constexpr int kEpi = kTM == 2 ? epilogue_lds_bytes_par4<SN>()
+                       : kInplace ? epilogue_lds_bytes_inplace<SN>() : epilogue_lds_bytes<SN>();
   constexpr int kLds = 2 * kStage > kEpi ? 2 * kStage : kEpi;
   static_assert(kLds <= 160 * 1024, "a CU's LDS");
   __shared__ __align__(16) uint8_t lds[kLds];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int mg = wave & 3, kp = wave >> 2;
+  const int mg = wave % kTM, kp = wave / kTM;
   const int K = p.cols, B = K / kBlock, M = p.n, N = p.rows;
   const int groups_n = (N + 31) >> 5;
 
@@ -1360,7 +1416,7 @@ __global__ void __launch_bounds__(kThreads) gemm_i8p_kernel(F6PParams p) {
   const int tm = t % p.tiles_m, tn = t / p.tiles_m;
   const int n0 = tn * BN, g0 = tn * SN;
   const int groups = (M + kTokens - 1) / kTokens;
-  const int g = tm * kTileM + mg;
+  const int g = tm * kTM + mg;
   const int b_begin = blockIdx.y * p.split_blocks;
   const int b_end = min(B, b_begin + p.split_blocks);
   const int stages = (b_end - b_begin + kI8KB - 1) / kI8KB;
@@ -1455,7 +1511,7 @@ __global__ void __launch_bounds__(kThreads) gemm_i8p_kernel(F6PParams p) {
   i32x2 rs[kRingP];
   dma_w(0, 0);
 #pragma unroll
-  for (int r = 0; r < kRingP; r++) load_a(b_begin + kp + 2 * r, rc[r], rs[r]);
+  for (int r = 0; r < kRingP; r++) load_a(b_begin + kp + kPar * r, rc[r], rs[r]);
   if (stages > 1) dma_w(1, 1);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -1467,9 +1523,9 @@ __global__ void __launch_bounds__(kThreads) gemm_i8p_kernel(F6PParams p) {
     BFrag nb = read_b(sbase, kp, 0);
 #pragma unroll
     for (int r = 0; r < kRingP; r++) {
-      const int kb = kp + 2 * r;
-      compute(sbase, kb, min(kb + 2, kI8KB - 1), rc[r], rs[r], nb);
-      load_a(b0 + kb + 2 * kRingP, rc[r], rs[r]);
+      const int kb = kp + kPar * r;
+      compute(sbase, kb, min(kb + kPar, kI8KB - 1), rc[r], rs[r], nb);
+      load_a(b0 + kb + kI8KB, rc[r], rs[r]);
       __builtin_amdgcn_sched_barrier(0);
     }
     // This wave's W(s + 1) has landed: only the 2 * kRingP ring refills of
@@ -1479,11 +1535,14 @@ __global__ void __launch_bounds__(kThreads) gemm_i8p_kernel(F6PParams p) {
   }
   fold(SN - 1);
   float* out = p.part ? p.part + (size_t)blockIdx.y * M * N : p.y;
-  if constexpr (kInplace) {
-    store_tile_sums_inplace<SN>(lds, acc, wave, lane, tm * kTileM * kTokens, n0, M, N, out,
+  if constexpr (kTM == 2) {
+    store_tile_sums_par4<SN>(lds, acc, wave, lane, tm * kTM * kTokens, n0, M, N, out,
+                             p.vec != 0);
+  } else if constexpr (kInplace) {
+    store_tile_sums_inplace<SN>(lds, acc, wave, lane, tm * kTM * kTokens, n0, M, N, out,
                                 p.vec != 0);
   } else {
-    store_tile_sums<SN>(lds, acc, wave, lane, tm * kTileM * kTokens, n0, M, N, out, p.vec != 0);
+    store_tile_sums<SN>(lds, acc, wave, lane, tm * kTM * kTokens, n0, M, N, out, p.vec != 0);
   }
 }
 
@@ -1507,39 +1566,51 @@ bool i8p_shape_ok(int64_t rows, int64_t cols, int64_t n) {
          i8_panel_bytes(n, cols) < (1ll << 31) && n * rows < (1ll << 31);
 }
 
-// Row groups per workgroup tile (3, 4 or 5: 96 to 160 rows) of the int8
-// prepacked GEMM: the tile width whose launch takes the least time by a
-// model of its measured costs. A workgroup fills its CU, so a launch runs
-// in rounds of 256 workgroups; per round the slowest CU runs SN tiles of
-// its split's blocks (about 100 ns per tile and block pair per SIMD, two
-// waves of opposite block parity), plus about 2 us of prologue and
+// The tile of the int8 prepacked GEMM: row groups per workgroup SN (3, 4 or
+// 5: 96 to 160 rows) and token groups TM (4: 128 tokens, the waves in two
+// block parities; 2: 64 tokens in four parities), the one whose launch
+// takes the least time by a model of its measured costs. A workgroup fills
+// its CU, so a launch runs in rounds of 256 workgroups; per round the
+// slowest SIMD runs its two waves' tiles of their parities' blocks (about
+// 100 ns per tile and block each, 120 on 64-token tiles), plus about 2 us of prologue and
 // epilogue; a K split adds the reduce launch (about 1 us plus its partials
 // read at 4 TB/s). The vision encoder's fc1 (4320 x 1152 at 1024 tokens)
-// takes 160-row tiles (216 workgroups, one round, against 360 in two);
-// fc2 (1152 x 4320) 128-row tiles (72 tiles in three K parts).
-int i8p_groups(int64_t rows, int64_t cols, int64_t n) {
-  const int64_t tm = (n + kTileM * kTokens - 1) / (kTileM * kTokens);
+// takes 128 x 160 tiles (216 workgroups, one round, against 360 in two);
+// 1024 x 1024 at 1024 tokens 64 x 96 tiles (176 workgroups with no K split:
+// 9.8 against 16.2 us for 128 x 96 tiles in two K parts).
+struct I8PTile {
+  int sn, tm;
+};
+
+I8PTile i8p_tile(int64_t rows, int64_t cols, int64_t n) {
   const int64_t gn = (rows + 31) / 32;
   const int B = (int)(cols / kBlock);
-  int best = 3;
-  double best_ns = 0.0;
-  for (int sn = 3; sn <= 5; sn++) {
-    const int64_t tiles = tm * ((gn + sn - 1) / sn);
-    if (tiles > 0x7fffffff) continue;
-    const int per = i8_split_blocks((int)tiles, B);
-    const int64_t splits = (B + per - 1) / per;
-    const int64_t rounds = (tiles * splits + 255) / 256;
-    double ns = (double)rounds * ((double)sn * ((per + 1) / 2) * 200.0 + 2000.0);
-    if (splits > 1) ns += 1000.0 + (double)splits * (double)n * (double)rows / 1000.0;
-    if (sn == 3 || ns < best_ns) {
-      best = sn;
-      best_ns = ns;
+  I8PTile best{3, 4};
+  double best_ns = -1.0;
+  for (int tmg = 4; tmg >= 2; tmg -= 2) {
+    const int par = kWaves / tmg;
+    const int64_t tm = (n + tmg * kTokens - 1) / (tmg * kTokens);
+    for (int sn = 3; sn <= (tmg == 4 ? 5 : 4); sn++) {
+      const int64_t tiles = tm * ((gn + sn - 1) / sn);
+      if (tiles > 0x7fffffff) continue;
+      const int per = i8_split_blocks((int)tiles, B);
+      const int64_t splits = (B + per - 1) / per;
+      const int64_t rounds = (tiles * splits + 255) / 256;
+      // 64-token tiles: each staged weight serves half the tokens, about
+      // 1.2x the time per tile and block (measured).
+      const double step_ns = tmg == 4 ? 100.0 : 120.0;
+      double ns = (double)rounds * (2.0 * sn * ((per + par - 1) / par) * step_ns + 2000.0);
+      if (splits > 1) ns += 1000.0 + (double)splits * (double)n * (double)rows / 1000.0;
+      if (best_ns < 0.0 || ns < best_ns) {
+        best = {sn, tmg};
+        best_ns = ns;
+      }
     }
   }
   return best;
 }
 
-template <int SN>
+template <int SN, int kTM>
 int launch_i8p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t rows, int64_t cols,
                int64_t n, hipStream_t stream) {
   constexpr int BN = SN * 32;
@@ -1550,7 +1621,7 @@ int launch_i8p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t ro
   p.rows = (int)rows;
   p.cols = (int)cols;
   p.n = (int)n;
-  p.tiles_m = (int)((n + kTileM * kTokens - 1) / (kTileM * kTokens));
+  p.tiles_m = (int)((n + kTM * kTokens - 1) / (kTM * kTokens));
   p.tiles = p.tiles_m * (int)((rows + BN - 1) / BN);
   const int B = (int)(cols / kBlock);
   p.split_blocks = i8_split_blocks(p.tiles, B);
@@ -1562,7 +1633,7 @@ int launch_i8p(const uint8_t* packed, const uint8_t* panel, float* y, int64_t ro
     if (p.part == nullptr) return DNX_ENOMEM;
   }
   p.vec = (rows % 4 == 0 && ((uintptr_t)(p.part ? (void*)p.part : (void*)y) & 15) == 0) ? 1 : 0;
-  hipLaunchKernelGGL((gemm_i8p_kernel<SN>), dim3((unsigned)p.tiles, (unsigned)splits),
+  hipLaunchKernelGGL((gemm_i8p_kernel<SN, kTM>), dim3((unsigned)p.tiles, (unsigned)splits),
                      dim3(kThreads), 0, stream, p);
   if (hipGetLastError() != hipSuccess) return DNX_ELAUNCH;
   if (splits > 1) {
@@ -1822,16 +1893,28 @@ int dnx_gemm_q8_i8p(const void* packed, const void* panel, float* y, int64_t row
   }
   const uint8_t* pk = (const uint8_t*)packed;
   const uint8_t* pn = (const uint8_t*)panel;
-  switch (i8p_groups(rows, cols, n)) {
-    case 5: return launch_i8p<5>(pk, pn, y, rows, cols, n, (hipStream_t)stream);
-    case 4: return launch_i8p<4>(pk, pn, y, rows, cols, n, (hipStream_t)stream);
-    default: return launch_i8p<3>(pk, pn, y, rows, cols, n, (hipStream_t)stream);
+  const I8PTile tile = i8p_tile(rows, cols, n);
+  const hipStream_t st = (hipStream_t)stream;
+  if (tile.tm == 2) {
+    return tile.sn == 4 ? launch_i8p<4, 2>(pk, pn, y, rows, cols, n, st)
+                        : launch_i8p<3, 2>(pk, pn, y, rows, cols, n, st);
+  }
+  switch (tile.sn) {
+    case 5: return launch_i8p<5, 4>(pk, pn, y, rows, cols, n, st);
+    case 4: return launch_i8p<4, 4>(pk, pn, y, rows, cols, n, st);
+    default: return launch_i8p<3, 4>(pk, pn, y, rows, cols, n, st);
   }
 }
 
-int dnx_gemm_q8_i8p_tile_rows(int64_t rows, int64_t cols, int64_t n) {
-  if (!i8p_shape_ok(rows, cols, n)) return -1;
-  return 32 * i8p_groups(rows, cols, n);
+int dnx_gemm_q8_i8p_tile(int64_t rows, int64_t cols, int64_t n, int* tile_rows,
+                         int* tile_tokens) {
+  if (!i8p_shape_ok(rows, cols, n) || tile_rows == nullptr || tile_tokens == nullptr) {
+    return DNX_EINVAL;
+  }
+  const I8PTile tile = i8p_tile(rows, cols, n);
+  *tile_rows = 32 * tile.sn;
+  *tile_tokens = kTokens * tile.tm;
+  return DNX_OK;
 }
 
 int64_t dnx_gemm_q4_f6p_noalloc_max_floats(void) { return (int64_t)kScratchFloats; }

@@ -41,18 +41,22 @@ inline bool matmul_uses_f6_chunk(bool q4, int64_t rows, int64_t cols, int64_t n)
   return q4 && n >= 5 && n <= 512 && !matmul_uses_f6(q4, rows, cols, n);
 }
 
-// Q8 batches of large products (the vision encoder's fc1 / fc2 and
-// projector at its 1024 patches, lib/src/vision_encoder.dart:275-316) with a
-// prepacked copy of the weights (the lab_gpu_* command buffer keeps one per
-// weight region): the int8 panel quantizer + dnx_gemm_q8_i8p. Measured
-// against quantize + int8 GEMM (graph-timed, weights rotated past the
-// MALL): 1152 x 4320 and 4320 x 1152 at 1024 tokens 32.8 / 27.1 against
-// 42.6 / 30.1 us, 4096 x 4096 at 1024 tokens 57.2 against 80.9, 1024 x 1024
-// at 4096 tokens 26.5 against 30.7; below 2^32 multiply-adds the int8
-// GEMM's smaller tiles win or tie (1024 x 1024 at 1024 tokens: 20.6 against
-// 14.7; 2048 x 4096 at 256 tokens: 22.4 against 22.2).
+// Q8 batches (the vision encoder's attention projections, fc1 / fc2 and
+// projector at its 1024 patches, lib/src/vision_encoder.dart:252-316) with
+// a prepacked copy of the weights (the lab_gpu_* command buffer keeps one
+// per weight region): the int8 panel quantizer + dnx_gemm_q8_i8p.
+// Measured against quantize + int8 GEMM (graph-timed, weights rotated past
+// the MALL): 1152 x 4320 and 4320 x 1152 at 1024 tokens 32.0-33.1 /
+// 26.3-27.1 against 41.9-42.6 / 29.3-30.1 us, 4096 x 4096 at 1024 tokens
+// 53.1-53.7 against 78.3-84.7, 1152 x 1152 at 1024 tokens 14.5 against
+// 17.3, 1024 x 1024 at 256 / 512 / 1024 tokens 11.6 / 13.9 / 13.0-13.9
+// against 12.5 / 14.6 / 14.4-14.9, 768 x 768 at 512 tokens 12.3 against
+// 13.6. Below 256 tokens or 2^28 multiply-adds the int8 GEMM's smaller
+// tiles win or tie (1024 x 1024 and 2048 x 2048 at 128 tokens: 10.2 / 14.0
+// against 10.0 / 13.4); one shape inside the bounds measured slower (4096
+// x 1024 at 256 tokens, K of 32 blocks: 13.8 against 12.8).
 inline bool matmul_uses_i8p(bool q4, int64_t rows, int64_t cols, int64_t n) {
-  return !q4 && n >= 128 && rows * cols * n >= (1ll << 32);
+  return !q4 && n >= 256 && rows * cols * n >= (1ll << 28);
 }
 
 // Device bytes a route needs for its quantized activations: int8 xq and fp32

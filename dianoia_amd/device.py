@@ -455,9 +455,13 @@ def gemm_q8_i8p(packed, panel, y, rows: int, cols: int, n: int, stream=None) -> 
                                        _stream(stream)), "dnx_gemm_q8_i8p")
 
 
-def gemm_q8_i8p_tile_rows(rows: int, cols: int, n: int) -> int:
-    """Weight rows per workgroup tile dnx_gemm_q8_i8p takes for a shape."""
-    return int(_lib.load().dnx_gemm_q8_i8p_tile_rows(rows, cols, n))
+def gemm_q8_i8p_tile(rows: int, cols: int, n: int):
+    """(weight rows, tokens) of the workgroup tile dnx_gemm_q8_i8p takes for
+    a shape, or None for a shape it refuses."""
+    import ctypes
+    r, t = ctypes.c_int(0), ctypes.c_int(0)
+    rc = _lib.load().dnx_gemm_q8_i8p_tile(rows, cols, n, ctypes.byref(r), ctypes.byref(t))
+    return None if rc != 0 else (r.value, t.value)
 
 
 def argmax_workspace(n: int, device="cuda") -> torch.Tensor:

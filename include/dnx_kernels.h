@@ -304,9 +304,9 @@ int dnx_gemm_q8_f6p(const void* packed, const void* panel, float* y, int64_t row
 // x with lab_quantize_q8's xq and scale bits (dnx_i8_panel_bytes,
 // dnx_quantize_q8_i8panel; x and the panel 16-byte aligned). fp32 within
 // 1e-4 relative (1e-5 absolute near zero) of the CPU kernel; the scales are
-// applied as by dnx_gemm_q8. Tiles of 128 tokens x 96, 128 or 160 rows
-// (dnx_gemm_q8_i8p_tile_rows: the choice for a shape, -1 for a shape the
-// GEMM refuses); at 128 tiles or fewer K is split, the partials added in a
+// applied as by dnx_gemm_q8. Tiles of 128 tokens x 96, 128 or 160 rows or
+// 64 tokens x 96 or 128 rows (dnx_gemm_q8_i8p_tile: the choice for a shape,
+// DNX_EINVAL for a shape the GEMM refuses); at 128 tiles or fewer K is split, the partials added in a
 // fixed order in a second launch, from the fp6 GEMMs' library-owned
 // workspace, grown on demand (the first call at a larger split shape
 // allocates, so it must not be captured into a graph; calls share it:
@@ -319,7 +319,8 @@ int dnx_pack_q8_i8(const int8_t* qs, const float* scales, void* packed, int64_t 
                    int64_t cols, dnx_stream_t stream);
 int dnx_gemm_q8_i8p(const void* packed, const void* panel, float* y, int64_t rows, int64_t cols,
                     int64_t n, dnx_stream_t stream);
-int dnx_gemm_q8_i8p_tile_rows(int64_t rows, int64_t cols, int64_t n);
+int dnx_gemm_q8_i8p_tile(int64_t rows, int64_t cols, int64_t n, int* tile_rows,
+                         int* tile_tokens);
 
 // The prefill chunk GEMM (lab_gemm_q4 mode 1, lab_native.c:1059-1080, at
 // the reference's prefill chunks of up to 64 tokens, lib/src/model.dart:91,

@@ -156,14 +156,20 @@ def test_gemm_within_tolerance(gpu_ready, orc, rows, cols, n, fp32_scales):
     assert ok, (worst_rel, worst_abs)
 
 
-@pytest.mark.parametrize("rows,cols,n,tile", [(4303, 1152, 1000, 160), (4318, 1152, 1001, 160),
-                                               (999, 4096, 300, 128), (771, 1024, 333, 96)])
-def test_every_tile_width(gpu_ready, orc, rows, cols, n, tile):
-    """The 96-, 128- and 160-row tiles (the last adds the two block parities
-    in place, in half the LDS) at ragged shapes: rows not a multiple of the
-    tile or of 4 (no 16-byte stores), tokens not a multiple of 128, against
-    the exact products and the CPU kernel."""
-    assert D.gemm_q8_i8p_tile_rows(rows, cols, n) == tile
+@pytest.mark.parametrize("rows,cols,n,tile", [(4303, 1152, 1000, (160, 128)),
+                                               (2001, 256, 2100, (160, 128)),
+                                               (2900, 256, 1100, (128, 128)),
+                                               (999, 256, 2100, (96, 128)),
+                                               (333, 1024, 1100, (128, 64)),
+                                               (771, 1024, 333, (96, 64)),
+                                               (333, 256, 130, (96, 64))])
+def test_every_tile(gpu_ready, orc, rows, cols, n, tile):
+    """Every tile: 128 tokens x 96, 128 or 160 rows (160 adds the two block
+    parities in place, in half the LDS) and 64 tokens x 96 or 128 rows (four
+    block parities), at ragged shapes: rows not a multiple of the tile or
+    of 4 (no 16-byte stores), tokens not a multiple of the tile, against the
+    exact products and the CPU kernel."""
+    assert D.gemm_q8_i8p_tile(rows, cols, n) == tile
     rng = np.random.default_rng(rows + cols * 3 + n)
     qs, sc = orc.quantize_q8((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
     xs = synth.activations(rng, n, cols)
@@ -179,11 +185,14 @@ def test_every_tile_width(gpu_ready, orc, rows, cols, n, tile):
 
 
 def test_tile_choice_of_the_vision_pair(gpu_ready):
-    """fc1 (4320 x 1152 at 1024 tokens) takes 160-row tiles, one round of 216
-    workgroups; fc2 (1152 x 4320) 128-row tiles; refused shapes give -1."""
-    assert D.gemm_q8_i8p_tile_rows(4320, 1152, 1024) == 160
-    assert D.gemm_q8_i8p_tile_rows(1152, 4320, 1024) == 128
-    assert D.gemm_q8_i8p_tile_rows(64, 48, 5) == -1
+    """fc1 (4320 x 1152 at 1024 tokens) takes 128 x 160 tiles, one round of
+    216 workgroups; fc2 (1152 x 4320) 128 x 128 tiles in three K parts; the
+    1024 x 1024 projections at 1024 tokens 64 x 96 tiles with no K split;
+    refused shapes give None."""
+    assert D.gemm_q8_i8p_tile(4320, 1152, 1024) == (160, 128)
+    assert D.gemm_q8_i8p_tile(1152, 4320, 1024) == (128, 128)
+    assert D.gemm_q8_i8p_tile(1024, 1024, 1024) == (96, 64)
+    assert D.gemm_q8_i8p_tile(64, 48, 5) is None
 
 
 def test_gemm_is_deterministic(gpu_ready, orc):

@@ -418,15 +418,15 @@ def test_q4_prefill_follows_gpu_writes_into_the_weights(gpu, orc, n):
 
 
 def test_q8_batch_follows_gpu_writes_into_the_weights(gpu, orc):
-    """A Q8 batch of 2^32+ multiply-adds (1024 x 1024 at 4096 tokens) runs on
+    """A Q8 batch of 256+ tokens (1024 x 1024 at 4096 tokens) runs on
     a prepacked copy of the weights made at its first use (the int8 GEMM on
     prepacked operands). A GPU command that writes other weights into the
     same region (lab_gpu_enc_quantize_q8 again) makes the next product use
     them, and writing the first weights back returns to those: each product
     against the CPU kernel on the weights of the moment."""
-    from dianoia_amd import _lib
+    from dianoia_amd import device as D
     rows, cols, n = 1024, 1024, 4096
-    assert _lib.load().dnx_gemm_q8_i8p_tile_rows(rows, cols, n) > 0
+    assert D.gemm_q8_i8p_tile(rows, cols, n) is not None
     rng = np.random.default_rng(23)
     ws = [(rng.standard_normal((rows, cols)) * 0.02).astype(np.float32) for _ in range(2)]
     gpu.upload_f32("w", ws[0], rows, cols, fmt="q8")
