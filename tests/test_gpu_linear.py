@@ -359,6 +359,33 @@ def test_input_mode_switch_returns_previous(gpu_ready):
         set_int8_inputs(was)
 
 
+def test_q8_batch_with_x_at_any_float_offset(gpu, orc):
+    """The Q8 batch route on prepacked operands (1152 x 1152 at 1024 tokens)
+    reads x 16 bytes at a time; lab_gpu_enc_matmul_q8 takes x at any float
+    offset. At offsets 1..3 floats the command takes the int8 route, at 0
+    and 4 the prepacked one: all within the bar of the CPU kernel."""
+    rows, cols, n = 1152, 1152, 1024
+    rng = np.random.default_rng(31)
+    qs, sc = orc.quantize_q8((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
+    xs = synth.activations(rng, n, cols)
+    gpu.upload("w", QuantMatrix.q8(qs, sc))
+    lib, w = gpu._lib, gpu._matrix("w")
+    x = gpu._aux_buffer("x_off8", n * cols + 4)
+    y = gpu._aux_buffer("y_off8", n * rows)
+    ref = orc.gemm_q8(qs, sc, xs, n, threads=8, mode=1)
+    for off in (1, 2, 3, 0, 4):
+        v = x.view(count=n * cols + 4)
+        v[:] = np.nan
+        v[off:off + n * cols] = xs.reshape(-1)
+        y.view(count=n * rows)[:] = np.nan
+        lib.lab_gpu_begin()
+        w.encode(lib, x.handle, y.handle, 0, n, x_offset=off * 4)
+        gpu._finish()
+        out = y.view(count=n * rows).reshape(n, rows).copy()
+        ok, rel, ab = within_tolerance(out, ref)
+        assert ok, (off, rel, ab)
+
+
 @pytest.mark.parametrize("rows,cols,n", [(768, 768, 13), (768, 768, 375), (4096, 1024, 320)])
 def test_q4_prefill_with_x_at_any_float_offset(gpu, orc, rows, cols, n):
     """The Q4 prefill routes with fp6 kernels (the chunk GEMM on the prepack
