@@ -1310,7 +1310,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the quantized linear layer runs on one MI355X; see DESIGN.md for sharding)",
+              "(the quantized linear layer runs on one MI355X; sharding is design-only)",
               file=sys.stderr)
         sys.exit(2)
 

@@ -16,6 +16,7 @@ command as the reference's GpuForward.forward does (lib/src/gpu.dart:
 
 import os
 import subprocess
+import tempfile
 import sys
 
 import numpy as np
@@ -389,10 +390,11 @@ def test_tracking_off_uploads_the_history_and_agrees(gpu_ready):
     finally:
         fwd.dispose()
     env = dict(os.environ, DIANOIA_GPU_TRACK_WRITES="0")
-    r = subprocess.run([sys.executable, script], env=env, capture_output=True, text=True,
-                       timeout=300)
-    assert r.returncode == 0, r.stderr[-2000:]
-    out = np.load(os.path.join(ROOT, "gpurun_out", "forward_child.npz"))
+    with tempfile.TemporaryDirectory() as out_dir:
+        r = subprocess.run([sys.executable, script, "plain", out_dir], env=env,
+                           capture_output=True, text=True, timeout=300)
+        assert r.returncode == 0, r.stderr[-2000:]
+        out = dict(np.load(os.path.join(out_dir, "forward_child.npz")))
     assert int(out["tracking"]) == 0
     assert same(out["logits16"], want) and same(out["logits17"], want17)
     assert int(out["up17"]) >= up_tracked + 2 * 17 * cfg.kv_dim * 4 * cfg.layers
@@ -413,10 +415,11 @@ def test_replaced_segv_handler_turns_tracking_off(gpu_ready):
         want = fwd.logits.copy()
     finally:
         fwd.dispose()
-    r = subprocess.run([sys.executable, script, "replace-handler"], capture_output=True,
-                       text=True, timeout=120)
-    assert r.returncode == 0, (r.returncode, r.stderr[-2000:])
-    out = np.load(os.path.join(ROOT, "gpurun_out", "forward_child_handler.npz"))
+    with tempfile.TemporaryDirectory() as out_dir:
+        r = subprocess.run([sys.executable, script, "replace-handler", out_dir],
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, (r.returncode, r.stderr[-2000:])
+        out = dict(np.load(os.path.join(out_dir, "forward_child_handler.npz")))
     assert int(out["before"]) == 1 and int(out["after"]) == 0
     assert same(out["logits16"], want)
 
